@@ -1,0 +1,79 @@
+// Shared device helpers for the acorninfer_amd HIP kernels (gfx950 / CDNA4).
+//
+// Conventions used by every kernel in this library:
+//  * activations are one of fp32 / fp16 / bf16, selected by an integer dtype
+//    code (ACORN_F32=0, ACORN_F16=1, ACORN_BF16=2) at the C-ABI;
+//  * every entry point launches only on the stream it is given, never
+//    allocates, never synchronises, and returns 0 or a negative error code;
+//  * a wavefront is 64 lanes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/acorn_hip.h"
+
+namespace acorn {
+
+constexpr int kWave = 64;
+
+// ---- scalar conversions -------------------------------------------------
+// __bf16 <-> float conversions lower to v_cvt_pk_bf16_f32 (RNE) on gfx950;
+// _Float16 conversions are IEEE RNE as well.
+template <typename T> __device__ __forceinline__ float to_f32(T v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }
+
+// Round a float to the grid of T and widen it back (identity for float).
+template <typename T> __device__ __forceinline__ float round_to(float v) {
+  return (float)(T)v;
+}
+template <> __device__ __forceinline__ float round_to<float>(float v) { return v; }
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  __bf16 a = (__bf16)lo, b = (__bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// ---- wavefront reductions -----------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Block-wide sum for blockDim.x == NT (multiple of 64); every thread gets the
+// total. `red` must hold NT/64 floats of LDS.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  if (NT == kWave) return v;
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NT / kWave; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+}  // namespace acorn
+
+// Launch-error mapping shared by every entry point.
+#define ACORN_LAUNCH_CHECK()                                    \
+  do {                                                          \
+    hipError_t _e = hipGetLastError();                          \
+    if (_e != hipSuccess) return ACORN_ERR_HIP - (int)_e;       \
+  } while (0)

@@ -1,0 +1,162 @@
+// K1: fused residual add + RMSNorm, one workgroup per row.
+//
+// Numerics follow acorninfer/ops/rmsnorm.py:74-82 (the reference oracle):
+//   r      = round_T(residual + x)            (fp32 add, one rounding)
+//   normed = round_T((r * rsqrt(mean(r*r) + eps)) * w)   (fp32 throughout)
+// with rsqrt computed as a correctly rounded 1/sqrt, and no FMA contraction so
+// each product is rounded as torch rounds it.
+#include "common.h"
+
+using namespace acorn;
+
+namespace {
+
+constexpr int kNT = 256;     // threads per row
+constexpr int kCache = 16;   // elements per thread kept in registers (4096 cols)
+
+template <typename T, typename TW, bool HAS_RES, bool FROM_PART>
+__global__ __launch_bounds__(kNT) void fused_add_rmsnorm_kernel(
+    const T* __restrict__ x, const float* __restrict__ part, int nsplit,
+    const T* __restrict__ res, T* __restrict__ res_out, const TW* __restrict__ w,
+    T* __restrict__ normed, T* __restrict__ x_out, int rows, int cols, float eps) {
+#pragma clang fp contract(off)
+  __shared__ float red[kNT / kWave];
+  const int row = blockIdx.x;
+  const size_t base = (size_t)row * cols;
+  const size_t plane = (size_t)rows * cols;
+
+  auto load_x = [&](int i) -> float {
+    if constexpr (FROM_PART) {
+      float a = part[base + i];
+      for (int s = 1; s < nsplit; ++s) a += part[s * plane + base + i];
+      float xr = round_to<T>(a);
+      if (x_out) x_out[base + i] = from_f32<T>(xr);
+      return xr;
+    } else {
+      return to_f32(x[base + i]);
+    }
+  };
+
+  float v[kCache];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kCache; ++j) {
+    const int i = threadIdx.x + j * kNT;
+    v[j] = 0.f;
+    if (i < cols) {
+      float a = load_x(i);
+      if constexpr (HAS_RES) a = to_f32(res[base + i]) + a;
+      const float r = round_to<T>(a);
+      res_out[base + i] = from_f32<T>(r);
+      v[j] = r;
+      ss += r * r;
+    }
+  }
+  for (int i = threadIdx.x + kCache * kNT; i < cols; i += kNT) {
+    float a = load_x(i);
+    if constexpr (HAS_RES) a = to_f32(res[base + i]) + a;
+    const float r = round_to<T>(a);
+    res_out[base + i] = from_f32<T>(r);
+    ss += r * r;
+  }
+  ss = block_sum<kNT>(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+#pragma unroll
+  for (int j = 0; j < kCache; ++j) {
+    const int i = threadIdx.x + j * kNT;
+    if (i < cols) normed[base + i] = from_f32<T>((v[j] * inv) * to_f32(w[i]));
+  }
+  for (int i = threadIdx.x + kCache * kNT; i < cols; i += kNT) {
+    // Re-read this thread's own store: program order makes it visible.
+    const float r = to_f32(res_out[base + i]);
+    normed[base + i] = from_f32<T>((r * inv) * to_f32(w[i]));
+  }
+}
+
+template <typename T, typename TW>
+int launch_k1(const void* x, const float* part, int nsplit, const void* res, void* res_out,
+              const void* w, void* normed, void* x_out, int64_t rows, int64_t cols, float eps,
+              hipStream_t st) {
+  dim3 grid((unsigned)rows), block(kNT);
+  const T* xp = (const T*)x;
+  const T* rp = (const T*)res;
+  T* rop = (T*)res_out;
+  const TW* wp = (const TW*)w;
+  T* np = (T*)normed;
+  T* xo = (T*)x_out;
+  if (part) {
+    if (res)
+      fused_add_rmsnorm_kernel<T, TW, true, true><<<grid, block, 0, st>>>(
+          xp, part, nsplit, rp, rop, wp, np, xo, (int)rows, (int)cols, eps);
+    else
+      fused_add_rmsnorm_kernel<T, TW, false, true><<<grid, block, 0, st>>>(
+          xp, part, nsplit, rp, rop, wp, np, xo, (int)rows, (int)cols, eps);
+  } else {
+    if (res)
+      fused_add_rmsnorm_kernel<T, TW, true, false><<<grid, block, 0, st>>>(
+          xp, part, nsplit, rp, rop, wp, np, xo, (int)rows, (int)cols, eps);
+    else
+      fused_add_rmsnorm_kernel<T, TW, false, false><<<grid, block, 0, st>>>(
+          xp, part, nsplit, rp, rop, wp, np, xo, (int)rows, (int)cols, eps);
+  }
+  ACORN_LAUNCH_CHECK();
+  return ACORN_OK;
+}
+
+template <typename T>
+int dispatch_w(int wdtype, const void* x, const float* part, int nsplit, const void* res,
+               void* res_out, const void* w, void* normed, void* x_out, int64_t rows,
+               int64_t cols, float eps, hipStream_t st) {
+  switch (wdtype) {
+    case ACORN_F32:
+      return launch_k1<T, float>(x, part, nsplit, res, res_out, w, normed, x_out, rows, cols, eps, st);
+    case ACORN_F16:
+      return launch_k1<T, _Float16>(x, part, nsplit, res, res_out, w, normed, x_out, rows, cols, eps, st);
+    case ACORN_BF16:
+      return launch_k1<T, __bf16>(x, part, nsplit, res, res_out, w, normed, x_out, rows, cols, eps, st);
+  }
+  return ACORN_ERR_DTYPE;
+}
+
+int k1_entry(const void* x, const float* part, int64_t nsplit, const void* res, void* res_out,
+             const void* w, void* normed, void* x_out, int64_t rows, int64_t cols, float eps,
+             int dtype, int wdtype, void* stream) {
+  if (rows < 0 || cols <= 0 || nsplit < 0) return ACORN_ERR_SHAPE;
+  if (rows == 0) return ACORN_OK;
+  if (rows > 0x7fffffff || cols > 0x7fffffff || rows * cols > ((int64_t)1 << 40))
+    return ACORN_ERR_SHAPE;
+  if (!res_out || !w || !normed || (!x && !part)) return ACORN_ERR_VALUE;
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case ACORN_F32:
+      return dispatch_w<float>(wdtype, x, part, (int)nsplit, res, res_out, w, normed, x_out, rows, cols, eps, st);
+    case ACORN_F16:
+      return dispatch_w<_Float16>(wdtype, x, part, (int)nsplit, res, res_out, w, normed, x_out, rows, cols, eps, st);
+    case ACORN_BF16:
+      return dispatch_w<__bf16>(wdtype, x, part, (int)nsplit, res, res_out, w, normed, x_out, rows, cols, eps, st);
+  }
+  return ACORN_ERR_DTYPE;
+}
+
+}  // namespace
+
+extern "C" int acorn_fused_add_rmsnorm(const void* x, const void* residual, void* residual_out,
+                                       const void* weight, void* normed, int64_t rows,
+                                       int64_t cols, float eps, int dtype, int wdtype,
+                                       void* stream) {
+  if (!x) return ACORN_ERR_VALUE;
+  return k1_entry(x, nullptr, 0, residual, residual_out, weight, normed, nullptr, rows, cols,
+                  eps, dtype, wdtype, stream);
+}
+
+extern "C" int acorn_fused_add_rmsnorm_partials(const float* part, int64_t nsplit,
+                                                const void* residual, void* residual_out,
+                                                const void* weight, void* normed, void* x_out,
+                                                int64_t rows, int64_t cols, float eps, int dtype,
+                                                int wdtype, void* stream) {
+  if (!part || nsplit < 1) return ACORN_ERR_VALUE;
+  return k1_entry(nullptr, part, nsplit, residual, residual_out, weight, normed, x_out, rows,
+                  cols, eps, dtype, wdtype, stream);
+}
+
+extern "C" int acorn_version(void) { return 1; }

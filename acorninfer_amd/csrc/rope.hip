@@ -1,0 +1,265 @@
+// K2: half-rotate RoPE, optionally preceded by the per-head q/k RMSNorm and
+// followed by the paged-KV scatter of the decode step.
+//
+// Rounding mirrors the reference torch path (acorninfer/ops/rope.py:1-13,
+// 116-125): cos/sin are computed in fp32 and rounded to the activation dtype;
+// each product is rounded; the sum/difference is rounded again:
+//   y1 = r(r(x1*c) - r(x2*s)),  y2 = r(r(x2*c) + r(x1*s))
+// The per-head norm is models/qwen3.py:50-60: r((x * rsqrt(mean(x^2)+eps)) * w).
+// FMA contraction is disabled so every product is rounded as torch does.
+#include "common.h"
+
+using namespace acorn;
+
+namespace {
+
+constexpr int kMaxPairs = 2;  // head_dim <= 256 -> half <= 128 -> 2 pairs per lane
+
+template <typename T>
+__device__ __forceinline__ void rope_pair(float& x1, float& x2, float pos, float inv_freq) {
+#pragma clang fp contract(off)
+  const float f = pos * inv_freq;
+  const float c = round_to<T>(cosf(f));
+  const float s = round_to<T>(sinf(f));
+  const float t1 = round_to<T>(x1 * c), t2 = round_to<T>(x2 * s);
+  const float t3 = round_to<T>(x2 * c), t4 = round_to<T>(x1 * s);
+  x1 = round_to<T>(t1 - t2);
+  x2 = round_to<T>(t3 + t4);
+}
+
+// One wavefront per row of head_dim values.
+template <typename T, bool POS64>
+__global__ __launch_bounds__(kWave) void rope_kernel(T* __restrict__ x, int heads, int D,
+                                                     const void* __restrict__ pos,
+                                                     const float* __restrict__ inv_freq) {
+  const int row = blockIdx.x;
+  const int b = row / heads;
+  const float p = POS64 ? (float)((const int64_t*)pos)[b] : (float)((const int32_t*)pos)[b];
+  T* base = x + (size_t)row * D;
+  const int half = D / 2;
+  for (int i = threadIdx.x; i < half; i += kWave) {
+    float x1 = to_f32(base[i]), x2 = to_f32(base[i + half]);
+    rope_pair<T>(x1, x2, p, inv_freq[i]);
+    base[i] = from_f32<T>(x1);
+    base[i + half] = from_f32<T>(x2);
+  }
+}
+
+// Per-head RMSNorm over the lane's pairs (x1[j], x2[j]) followed by RoPE.
+template <typename T, typename TW>
+__device__ __forceinline__ void norm_rope_row(float (&x1)[kMaxPairs], float (&x2)[kMaxPairs],
+                                              int half, const TW* __restrict__ w, float eps,
+                                              float pos, const float* __restrict__ inv_freq) {
+#pragma clang fp contract(off)
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxPairs; ++j) {
+    const int i = threadIdx.x + j * kWave;
+    if (i < half) ss += x1[j] * x1[j] + x2[j] * x2[j];
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)(2 * half) + eps);
+#pragma unroll
+  for (int j = 0; j < kMaxPairs; ++j) {
+    const int i = threadIdx.x + j * kWave;
+    if (i < half) {
+      x1[j] = round_to<T>((x1[j] * inv) * to_f32(w[i]));
+      x2[j] = round_to<T>((x2[j] * inv) * to_f32(w[i + half]));
+      rope_pair<T>(x1[j], x2[j], pos, inv_freq[i]);
+    }
+  }
+}
+
+template <typename T, typename TW, bool POS64>
+__global__ __launch_bounds__(kWave) void qknorm_rope_kernel(
+    T* __restrict__ q, T* __restrict__ k, int q_heads, int kv_heads, int D,
+    const TW* __restrict__ q_w, const TW* __restrict__ k_w, float eps,
+    const void* __restrict__ pos, const float* __restrict__ inv_freq) {
+  const int rows_per_b = q_heads + kv_heads;
+  const int b = blockIdx.x / rows_per_b;
+  const int h = blockIdx.x % rows_per_b;
+  const bool is_q = h < q_heads;
+  T* base = is_q ? q + ((size_t)b * q_heads + h) * D
+                 : k + ((size_t)b * kv_heads + (h - q_heads)) * D;
+  const TW* w = is_q ? q_w : k_w;
+  const float p = POS64 ? (float)((const int64_t*)pos)[b] : (float)((const int32_t*)pos)[b];
+  const int half = D / 2;
+  float x1[kMaxPairs], x2[kMaxPairs];
+#pragma unroll
+  for (int j = 0; j < kMaxPairs; ++j) {
+    const int i = threadIdx.x + j * kWave;
+    x1[j] = i < half ? to_f32(base[i]) : 0.f;
+    x2[j] = i < half ? to_f32(base[i + half]) : 0.f;
+  }
+  norm_rope_row<T, TW>(x1, x2, half, w, eps, p, inv_freq);
+#pragma unroll
+  for (int j = 0; j < kMaxPairs; ++j) {
+    const int i = threadIdx.x + j * kWave;
+    if (i < half) {
+      base[i] = from_f32<T>(x1[j]);
+      base[i + half] = from_f32<T>(x2[j]);
+    }
+  }
+}
+
+// Decode-step epilogue of the fused qkv projection. Rows per batch entry:
+// [0, H) q heads, [H, H+KV) k heads, [H+KV, H+2KV) v heads.
+template <typename T, typename TW>
+__global__ __launch_bounds__(kWave) void qkv_epilogue_kernel(
+    const float* __restrict__ part, int nsplit, T* __restrict__ q_out,
+    T* __restrict__ k_pages, T* __restrict__ v_pages, const int64_t* __restrict__ pages,
+    const int64_t* __restrict__ slots, int batch, int H, int KV, int D, int P,
+    const TW* __restrict__ q_w, const TW* __restrict__ k_w, float eps,
+    const int64_t* __restrict__ pos, const float* __restrict__ inv_freq) {
+  const int rows_per_b = H + 2 * KV;
+  const int b = blockIdx.x / rows_per_b;
+  const int h = blockIdx.x % rows_per_b;
+  const int half = D / 2;
+  const size_t width = (size_t)rows_per_b * D;
+  const size_t plane = (size_t)batch * width;
+  const float* src = part + (size_t)b * width + (size_t)h * D;
+  float x1[kMaxPairs], x2[kMaxPairs];
+#pragma unroll
+  for (int j = 0; j < kMaxPairs; ++j) {
+    const int i = threadIdx.x + j * kWave;
+    float a = 0.f, c = 0.f;
+    if (i < half) {
+      a = src[i];
+      c = src[i + half];
+      for (int s = 1; s < nsplit; ++s) {
+        a += src[s * plane + i];
+        c += src[s * plane + i + half];
+      }
+    }
+    x1[j] = round_to<T>(a);  // the projection's bf16 output
+    x2[j] = round_to<T>(c);
+  }
+  T* dst;
+  if (h < H) {
+    norm_rope_row<T, TW>(x1, x2, half, q_w, eps, (float)pos[b], inv_freq);
+    dst = q_out + ((size_t)b * H + h) * D;
+  } else {
+    const int kvh = h < H + KV ? h - H : h - H - KV;
+    const size_t off = (((size_t)pages[b] * P + (size_t)slots[b]) * KV + kvh) * D;
+    if (h < H + KV) {
+      norm_rope_row<T, TW>(x1, x2, half, k_w, eps, (float)pos[b], inv_freq);
+      dst = k_pages + off;
+    } else {
+      dst = v_pages + off;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxPairs; ++j) {
+    const int i = threadIdx.x + j * kWave;
+    if (i < half) {
+      dst[i] = from_f32<T>(x1[j]);
+      dst[i + half] = from_f32<T>(x2[j]);
+    }
+  }
+}
+
+bool head_dim_ok(int64_t D) { return D >= 2 && D <= 2 * kMaxPairs * kWave && (D & (D - 1)) == 0; }
+
+template <typename T>
+int launch_rope(void* x, int64_t batch, int64_t heads, int64_t D, const void* pos, int pos64,
+                const float* inv_freq, hipStream_t st) {
+  dim3 grid((unsigned)(batch * heads)), block(kWave);
+  if (pos64)
+    rope_kernel<T, true><<<grid, block, 0, st>>>((T*)x, (int)heads, (int)D, pos, inv_freq);
+  else
+    rope_kernel<T, false><<<grid, block, 0, st>>>((T*)x, (int)heads, (int)D, pos, inv_freq);
+  ACORN_LAUNCH_CHECK();
+  return ACORN_OK;
+}
+
+template <typename T, typename TW>
+int launch_qknorm(void* q, void* k, int64_t batch, int64_t H, int64_t KV, int64_t D,
+                  const void* qw, const void* kw, float eps, const void* pos, int pos64,
+                  const float* inv_freq, hipStream_t st) {
+  dim3 grid((unsigned)(batch * (H + KV))), block(kWave);
+  if (pos64)
+    qknorm_rope_kernel<T, TW, true><<<grid, block, 0, st>>>(
+        (T*)q, (T*)k, (int)H, (int)KV, (int)D, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
+  else
+    qknorm_rope_kernel<T, TW, false><<<grid, block, 0, st>>>(
+        (T*)q, (T*)k, (int)H, (int)KV, (int)D, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
+  ACORN_LAUNCH_CHECK();
+  return ACORN_OK;
+}
+
+template <typename T, typename TW>
+int launch_qkv(const float* part, int64_t nsplit, void* q_out, void* kp, void* vp,
+               const int64_t* pages, const int64_t* slots, int64_t batch, int64_t H, int64_t KV,
+               int64_t D, int64_t P, const void* qw, const void* kw, float eps,
+               const int64_t* pos, const float* inv_freq, hipStream_t st) {
+  dim3 grid((unsigned)(batch * (H + 2 * KV))), block(kWave);
+  qkv_epilogue_kernel<T, TW><<<grid, block, 0, st>>>(
+      part, (int)nsplit, (T*)q_out, (T*)kp, (T*)vp, pages, slots, (int)batch, (int)H, (int)KV,
+      (int)D, (int)P, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
+  ACORN_LAUNCH_CHECK();
+  return ACORN_OK;
+}
+
+#define ACORN_DISPATCH_T(dtype, FN, ...)                 \
+  switch (dtype) {                                       \
+    case ACORN_F32: return FN<float>(__VA_ARGS__);       \
+    case ACORN_F16: return FN<_Float16>(__VA_ARGS__);    \
+    case ACORN_BF16: return FN<__bf16>(__VA_ARGS__);     \
+  }                                                      \
+  return ACORN_ERR_DTYPE;
+
+#define ACORN_DISPATCH_TW(dtype, wdtype, FN, ...)                                   \
+  switch (dtype * 3 + wdtype) {                                                     \
+    case ACORN_F32 * 3 + ACORN_F32: return FN<float, float>(__VA_ARGS__);           \
+    case ACORN_F32 * 3 + ACORN_F16: return FN<float, _Float16>(__VA_ARGS__);        \
+    case ACORN_F32 * 3 + ACORN_BF16: return FN<float, __bf16>(__VA_ARGS__);         \
+    case ACORN_F16 * 3 + ACORN_F32: return FN<_Float16, float>(__VA_ARGS__);        \
+    case ACORN_F16 * 3 + ACORN_F16: return FN<_Float16, _Float16>(__VA_ARGS__);     \
+    case ACORN_F16 * 3 + ACORN_BF16: return FN<_Float16, __bf16>(__VA_ARGS__);      \
+    case ACORN_BF16 * 3 + ACORN_F32: return FN<__bf16, float>(__VA_ARGS__);         \
+    case ACORN_BF16 * 3 + ACORN_F16: return FN<__bf16, _Float16>(__VA_ARGS__);      \
+    case ACORN_BF16 * 3 + ACORN_BF16: return FN<__bf16, __bf16>(__VA_ARGS__);       \
+  }                                                                                 \
+  return ACORN_ERR_DTYPE;
+
+}  // namespace
+
+extern "C" int acorn_rope_inplace(void* x, int64_t batch, int64_t heads, int64_t head_dim,
+                                  const void* positions, int pos_is_i64, const float* inv_freq,
+                                  int dtype, void* stream) {
+  if (batch < 0 || heads < 0 || !head_dim_ok(head_dim)) return ACORN_ERR_SHAPE;
+  if (batch * heads == 0) return ACORN_OK;
+  if (!x || !positions || !inv_freq) return ACORN_ERR_VALUE;
+  ACORN_DISPATCH_T(dtype, launch_rope, x, batch, heads, head_dim, positions, pos_is_i64,
+                   inv_freq, (hipStream_t)stream)
+}
+
+extern "C" int acorn_qknorm_rope_inplace(void* q, void* k, int64_t batch, int64_t q_heads,
+                                         int64_t kv_heads, int64_t head_dim, const void* q_w,
+                                         const void* k_w, float eps, const void* positions,
+                                         int pos_is_i64, const float* inv_freq, int dtype,
+                                         int wdtype, void* stream) {
+  if (batch < 0 || q_heads < 0 || kv_heads < 0 || !head_dim_ok(head_dim)) return ACORN_ERR_SHAPE;
+  if (batch * (q_heads + kv_heads) == 0) return ACORN_OK;
+  if (!q || !k || !q_w || !k_w || !positions || !inv_freq) return ACORN_ERR_VALUE;
+  ACORN_DISPATCH_TW(dtype, wdtype, launch_qknorm, q, k, batch, q_heads, kv_heads, head_dim, q_w,
+                    k_w, eps, positions, pos_is_i64, inv_freq, (hipStream_t)stream)
+}
+
+extern "C" int acorn_qkv_epilogue(const float* part, int64_t nsplit, void* q_out, void* k_pages,
+                                  void* v_pages, const int64_t* pages, const int64_t* slots,
+                                  int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                  int64_t head_dim, int64_t page_size, const void* q_w,
+                                  const void* k_w, float eps, const int64_t* positions,
+                                  const float* inv_freq, int dtype, int wdtype, void* stream) {
+  if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || page_size <= 0 || nsplit < 1 ||
+      !head_dim_ok(head_dim))
+    return ACORN_ERR_SHAPE;
+  if (batch == 0) return ACORN_OK;
+  if (!part || !q_out || !k_pages || !v_pages || !pages || !slots || !q_w || !k_w ||
+      !positions || !inv_freq)
+    return ACORN_ERR_VALUE;
+  ACORN_DISPATCH_TW(dtype, wdtype, launch_qkv, part, nsplit, q_out, k_pages, v_pages, pages,
+                    slots, batch, q_heads, kv_heads, head_dim, page_size, q_w, k_w, eps,
+                    positions, inv_freq, (hipStream_t)stream)
+}

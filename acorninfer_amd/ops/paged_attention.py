@@ -1,0 +1,113 @@
+"""K3: paged flash-decoding attention on the GPU, plus block-table helpers.
+
+Drop-in for acorninfer/ops/paged_attention.py: `paged_decode_attention`
+(:125-152), `num_splits_for` (:155-158) and `build_tables` (:161-189). The
+kernel is csrc/paged_attention.hip (acorn_paged_attention): one wavefront per
+(split, kv head, sequence) serving every query head of the kv head.
+
+`plan_splits` is this build's split heuristic for MI355X (256 CUs); the
+reference's `num_splits_for` is kept with its exact semantics for callers that
+use it.
+"""
+from __future__ import annotations
+
+import torch
+
+from acorninfer_amd._lib import check, dtype_code, lib, ptr, require_gpu, stream_ptr
+
+_SM_COUNT = 128          # the reference's fixed heuristic constant (num_splits_for)
+MI355X_CUS = 256
+
+
+def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                           tables: torch.Tensor, seq_lens: torch.Tensor,
+                           num_splits: int, *, out: torch.Tensor | None = None,
+                           workspace: tuple[torch.Tensor, torch.Tensor] | None = None
+                           ) -> torch.Tensor:
+    """q [B,H,D] (normed + roped); k/v_pages [NB,P,KV,D]; tables [B,MP] int32;
+    seq_lens [B] int32 (including the current token, >= 1). Returns [B,H,D] in
+    q.dtype. q head j reads kv head j // (H//KV). `num_splits` page-aligned
+    splits per sequence; empty splits contribute nothing.
+
+    `out` / `workspace` (fp32 acc [B*H*S*D], fp32 m|l [2*B*H*S]) let a caller
+    pass address-stable buffers (graph capture); by default they are
+    allocated per call like the reference's.
+    """
+    require_gpu(q, k_pages, v_pages, tables, seq_lens)
+    B, H, D = q.shape
+    NB, P, KV, _ = k_pages.shape
+    S = int(num_splits)
+    assert D & (D - 1) == 0 and P & (P - 1) == 0, "D and P must be power-of-2"
+    assert H % KV == 0, "GQA requires H divisible by KV"
+    assert S >= 1
+    assert v_pages.shape == k_pages.shape and k_pages.shape[3] == D
+    assert tables.shape[0] == B and seq_lens.shape[0] == B
+    assert k_pages.is_contiguous() and v_pages.is_contiguous()
+    assert tables.is_contiguous() and seq_lens.is_contiguous()
+    assert tables.dtype == torch.int32 and seq_lens.dtype == torch.int32
+    assert k_pages.dtype == q.dtype == v_pages.dtype
+    q2 = q.contiguous()
+    if out is None:
+        out = torch.empty((B, H, D), dtype=q.dtype, device=q.device)
+    if workspace is None and S > 1:
+        workspace = (torch.empty(B * H * S * D, dtype=torch.float32, device=q.device),
+                     torch.empty(2 * B * H * S, dtype=torch.float32, device=q.device))
+    acc, ml = workspace if workspace is not None else (None, None)
+    rc = lib().acorn_paged_attention(
+        ptr(q2), ptr(k_pages), ptr(v_pages), ptr(tables), ptr(seq_lens), ptr(out), ptr(acc),
+        ptr(ml), B, H, KV, D, P, NB, max(1, tables.shape[1]), S, float(D ** -0.5),
+        dtype_code(q2), stream_ptr(q.device))
+    check(rc, "paged_decode_attention")
+    return out
+
+
+def num_splits_for(B: int, num_heads: int, *, sm_count: int = _SM_COUNT,
+                   max_splits: int = 8) -> int:
+    """The reference's split heuristic (paged_attention.py:155-158), unchanged:
+    enough (b, q-head, split) programs to cover `sm_count` SMs, capped."""
+    return max(1, min(max_splits, -(-sm_count // (B * num_heads))))
+
+
+def plan_splits(B: int, kv_heads: int, max_pages: int, *, cu_count: int = MI355X_CUS,
+                waves_per_cu: int = 4, min_pages_per_split: int = 4,
+                max_splits: int = 64) -> int:
+    """Split count for the MI355X kernel, whose grid is (S, KV, B) single-wave
+    workgroups. Aim for `waves_per_cu` waves per CU, but never fewer than
+    `min_pages_per_split` pages per split (the fixed per-split cost of loading
+    q and writing the partial)."""
+    target = -(-cu_count * waves_per_cu // max(1, B * kv_heads))
+    by_len = max(1, max_pages // min_pages_per_split)
+    return max(1, min(max_splits, target, by_len))
+
+
+def build_tables(views, page_size: int, device, *, lens_override=None,
+                 out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Block tables -> ([B, max_pages] int32 zero-padded, [B] int32 lengths).
+
+    Same contract as the reference (paged_attention.py:161-189): lengths come
+    from `lens_override` or each view's `seq_len`; row i holds the first
+    ceil(L_i / page_size) entries of `views[i].table`. With `out` (a CPU
+    buffer, e.g. a pinned mirror) the first B rows are zeroed and filled in
+    place and (out[:B], CPU lens) is returned with no device transfer.
+    """
+    if lens_override is not None:
+        lens = [int(L) for L in lens_override]
+    else:
+        lens = [int(v.seq_len) for v in views]
+    npages = [-(-L // page_size) for L in lens]
+    max_pages = max([1, *npages])
+    if out is not None:
+        assert out.shape[0] >= len(views) and out.shape[1] >= max_pages, \
+            "out buffer must be at least [B, max_pages]"
+        t = out[: len(views)]
+        t.zero_()
+    else:
+        t = torch.zeros((len(views), max_pages), dtype=torch.int32)
+    for i, v in enumerate(views):
+        n = npages[i]
+        if n:
+            t[i, :n] = torch.tensor(list(v.table[:n]), dtype=torch.int32)
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    if out is not None:
+        return t, lens_t
+    return t.to(device), lens_t.to(device)

@@ -1,0 +1,296 @@
+"""Weight-only quantised GEMM on the GPU (W8A16, W4A16 g128, and bf16).
+
+Drop-in for acorninfer/ops/quant_gemm.py: `quant_gemm` (:257-294), `CLASSES`
+(:67-73), `_CLS_BY_SHAPE` (:99), `M_BUCKETS_LARGE` (:82), `bucket_for`
+(:86-94), `_state` (:101-107), `configure` (:449-492) and `reset` (:495-499).
+New next to them (no reference counterpart in production): `quant_gemm_w4`
+for packed int4 group-128 weights, and `gemm_partials`, the decode-step form
+that leaves fp32 split-K partials for the consumer kernel to reduce.
+
+All formats run on one MFMA kernel (csrc/quant_gemm.hip). A tiling is
+(rt, nw, ksplit): 16*rt weight rows per wavefront, nw wavefronts per
+workgroup along K, ksplit workgroups along K. The reference's 5-tuple configs
+are accepted for compatibility; only their SPLIT_K field carries over.
+"""
+from __future__ import annotations
+
+import ctypes
+import time
+
+import torch
+
+from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W8, check, lib, ptr,
+                                 require_gpu, stream_ptr)
+
+CLASSES = {
+    "qo": (4096, 4096),
+    "kv": (1024, 4096),
+    "gate_up": (12288, 4096),
+    "down": (4096, 12288),
+    "lm_head": (151936, 4096),
+}
+# Fused projection shapes used by this build's decode step (qkv and gate|up
+# concatenated along N).
+FUSED_CLASSES = {
+    "qkv": (6144, 4096),
+    "gate_up2": (24576, 4096),
+}
+_CLS_BY_SHAPE = {v: k for k, v in CLASSES.items()}
+
+DECODE_M_MAX = 16
+M_BUCKETS_LARGE = ("s", "m", "l")
+_M_REP_M = {"s": 64, "m": 256, "l": 1024}
+
+_state: dict = {
+    "configs": {},     # cls -> (rt, nw, ksplit)   decode bucket (M <= 16)
+    "m_configs": {},   # cls -> {bucket: (rt, nw, ksplit)}
+    "shapes": {},      # cls -> (N, K)
+    "workspaces": {},  # (rows, N, ksplit) -> fp32 [ksplit, rows, N]
+    "device": None,
+    "report": None,
+}
+
+
+def bucket_for(M: int) -> str:
+    """M -> bucket name: d (M <= 16, decode) / s (<= 64) / m (<= 256) / l."""
+    if M <= DECODE_M_MAX:
+        return "d"
+    if M <= 64:
+        return "s"
+    if M <= 256:
+        return "m"
+    return "l"
+
+
+def plan(M: int, N: int, K: int, wfmt: int, *, partials: bool) -> tuple[int, int, int]:
+    """Default (rt, nw, ksplit) from the library's planner."""
+    rt, nw, ks = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    rc = lib().acorn_gemm_plan(M, N, K, wfmt, int(partials), ctypes.byref(rt),
+                               ctypes.byref(nw), ctypes.byref(ks))
+    check(rc, "gemm_plan")
+    return rt.value, nw.value, ks.value
+
+
+def _native_cfg(cfg, M: int) -> tuple[int, int, int] | None:
+    """(rt, nw, ksplit) from an explicit cfg. 0 means "planner default".
+
+    A reference 5-tuple is read by M regime as the reference does: for
+    M <= 16 it is (BN, BK, warps, stages, SPLIT_K) and SPLIT_K carries over;
+    for M > 16 it is (BM, BN, BK, warps, stages) and nothing carries over
+    (this kernel picks its own M tiling).
+    """
+    if cfg is None:
+        return None
+    cfg = tuple(int(c) for c in cfg)
+    if len(cfg) == 3:
+        return cfg
+    if len(cfg) == 5:
+        return (0, 0, cfg[4]) if M <= DECODE_M_MAX else (0, 0, 1)
+    raise ValueError(f"quant_gemm cfg must be (rt, nw, ksplit) or a reference 5-tuple: {cfg}")
+
+
+def _workspace(rows: int, N: int, ksplit: int, device) -> torch.Tensor:
+    key = (rows, N, ksplit, str(device))
+    ws = _state["workspaces"].get(key)
+    if ws is None:
+        ws = torch.empty(ksplit, rows, N, dtype=torch.float32, device=device)
+        _state["workspaces"][key] = ws
+    return ws
+
+
+def _launch(x2: torch.Tensor, w: torch.Tensor, scale, zero, wfmt: int, N: int,
+            cfg: tuple[int, int, int] | None, out: torch.Tensor | None) -> torch.Tensor:
+    M, K = x2.shape
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=x2.device)
+    assert out.shape == (M, N) and out.dtype == torch.bfloat16 and out.is_contiguous()
+    rt, nw, ks = cfg if cfg is not None else (0, 0, 1)
+    st = stream_ptr(x2.device)
+    if ks <= 1:
+        rc = lib().acorn_quant_gemm(ptr(x2), ptr(w), ptr(scale), ptr(zero), ptr(out), None,
+                                    M, N, K, wfmt, rt, nw, 1, st)
+        check(rc, "quant_gemm")
+        return out
+    part = _workspace(M, N, ks, x2.device)
+    rc = lib().acorn_quant_gemm(ptr(x2), ptr(w), ptr(scale), ptr(zero), None, ptr(part),
+                                M, N, K, wfmt, rt, nw, ks, st)
+    check(rc, "quant_gemm")
+    rc = lib().acorn_splitk_reduce(ptr(part), ks, M * N, ptr(out), BF16, st)
+    check(rc, "splitk_reduce")
+    return out
+
+
+def _prep_x(x: torch.Tensor) -> torch.Tensor:
+    K = x.shape[-1]
+    x2 = x.reshape(x.numel() // K, K)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    assert x2.dtype == torch.bfloat16, "activations must be bf16"
+    return x2
+
+
+def _pick_cfg(cls, M: int, cfg) -> tuple[int, int, int] | None:
+    native = _native_cfg(cfg, M)
+    if native is not None:
+        return native
+    if M <= DECODE_M_MAX:
+        return _state["configs"].get(cls)
+    table = _state["m_configs"].get(cls)
+    if not table:
+        raise RuntimeError(
+            f"quant_gemm large-M bucket not configured: cls={cls} (M={M}); call "
+            f"configure() at load time (tests may pass an explicit cfg)")
+    bucket = bucket_for(M)
+    if bucket not in table:
+        raise RuntimeError(f"quant_gemm large-M bucket missing: cls={cls} bucket={bucket} (M={M})")
+    return table[bucket]
+
+
+def quant_gemm(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor, cls, cfg=None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """W8A16: x [..., K] bf16, q int8 [N, K], scale fp16 [N] -> [M, N] bf16.
+
+    y = x @ (q * scale)^T accumulated in fp32 (the products x*q are exact;
+    the per-channel scale is applied once per output). M > 16 needs a
+    configure()d large-M table or an explicit cfg, as in the reference.
+    """
+    require_gpu(x, q, scale)
+    x2 = _prep_x(x)
+    N, K = q.shape
+    assert q.dtype == torch.int8 and q.is_contiguous(), "q must be contiguous int8 [N,K]"
+    assert scale.dtype == torch.float16 and scale.numel() == N
+    assert x2.shape[1] == K
+    c = _pick_cfg(cls, x2.shape[0], cfg)
+    return _launch(x2, q, scale.contiguous(), None, WFMT_W8, N, c, out)
+
+
+def quant_gemm_w4(x: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor,
+                  zero: torch.Tensor | None = None, cls=None, cfg=None,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """W4A16 group-128: x [..., K] bf16, packed uint8 [N, K/2] (low nibble =
+    even k, quantize.pack_w4), scale fp16 [N, K/128], zero fp16 [N, K/128] or
+    None -> [M, N] bf16.
+
+    zero None means the symmetric format: stored u = v + 8, w = v * scale.
+    With a zero (the reference's asymmetric quantize_w4), w = u*scale + zero.
+    """
+    require_gpu(x, packed, scale, zero)
+    x2 = _prep_x(x)
+    N, Kh = packed.shape
+    K = 2 * Kh
+    assert packed.dtype == torch.uint8 and packed.is_contiguous()
+    assert K % 128 == 0, "K must be a multiple of the 128 group"
+    assert scale.dtype == torch.float16 and scale.shape == (N, K // 128)
+    if zero is not None:
+        assert zero.dtype == torch.float16 and zero.shape == (N, K // 128)
+        zero = zero.contiguous()
+    assert x2.shape[1] == K
+    M = x2.shape[0]
+    c = _native_cfg(cfg, M) if cfg is not None else (
+        _state["configs"].get(cls) if M <= DECODE_M_MAX else
+        _state["m_configs"].get(cls, {}).get(bucket_for(M)))
+    return _launch(x2, packed, scale.contiguous(), zero, WFMT_W4, N, c, out)
+
+
+def bf16_gemm(x: torch.Tensor, w: torch.Tensor, cls=None, cfg=None,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """Dense bf16 x [..., K] @ w[N, K]^T -> [M, N] bf16 (fp32 accumulate)."""
+    require_gpu(x, w)
+    x2 = _prep_x(x)
+    N, K = w.shape
+    assert w.dtype == torch.bfloat16 and w.is_contiguous() and x2.shape[1] == K
+    c = _native_cfg(cfg, x2.shape[0]) if cfg is not None else _state["configs"].get(cls)
+    return _launch(x2, w, None, None, WFMT_BF16, N, c, out)
+
+
+def gemm_partials(x2: torch.Tensor, w: torch.Tensor, scale, zero, wfmt: int,
+                  part: torch.Tensor, cfg: tuple[int, int, int]) -> None:
+    """Decode-step form: write fp32 split-K partials part[ksplit, M, N]; the
+    consumer kernel sums them (in split order) and applies the output cast."""
+    M, K = x2.shape
+    ks, Mp, N = part.shape
+    assert Mp == M and part.dtype == torch.float32 and part.is_contiguous()
+    rt, nw, ks_cfg = cfg
+    assert ks_cfg == ks
+    rc = lib().acorn_quant_gemm(ptr(x2), ptr(w), ptr(scale), ptr(zero), None, ptr(part),
+                                M, N, K, wfmt, rt, nw, ks, stream_ptr(x2.device))
+    check(rc, "quant_gemm(partials)")
+
+
+# ---------------------------------------------------------------- load time --
+
+def _time_cfg(fn, reps: int = 20) -> float:
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / reps
+
+
+def configure(classes=None, *, device="cuda:0", verbose=True, wfmt: int = WFMT_W8) -> dict:
+    """Load-time tiling choice per class (before any graph capture).
+
+    For each class: the planner's default plus a small split-K neighbourhood
+    timed on random weights rotated over 4 sets (to defeat the 256 MB MALL);
+    the fastest becomes the decode (M <= 16) entry. Large-M buckets take the
+    planner default for their representative M.
+    """
+    reset()
+    classes = CLASSES if classes is None else dict(classes)
+    _state["device"] = device
+    _state["shapes"] = classes
+    report = {"classes": {}}
+    t0 = time.perf_counter()
+    for cls, (n, k) in classes.items():
+        t1 = time.perf_counter()
+        if wfmt == WFMT_W8:
+            sets = [(torch.randint(-127, 128, (n, k), dtype=torch.int8, device=device),
+                     torch.rand(n, device=device).half() * 0.02, None) for _ in range(4)]
+        elif wfmt == WFMT_W4:
+            sets = [(torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=device),
+                     torch.rand(n, k // 128, device=device).half() * 0.02, None)
+                    for _ in range(4)]
+        else:
+            sets = [(torch.randn(n, k, device=device).bfloat16(), None, None) for _ in range(4)]
+        x = torch.randn(8, k, device=device).bfloat16()
+        base = plan(8, n, k, wfmt, partials=False)
+        cands = {base}
+        for ks in (2, 3, 4):
+            cands.add((base[0], 0, ks))
+        best = None
+        for c in sorted(cands):
+            def run(c=c):
+                for w, s, z in sets:
+                    _launch(x, w, s, z, wfmt, n, c, None)
+            try:
+                us = _time_cfg(run) / len(sets)
+            except (AssertionError, ValueError, NotImplementedError):
+                continue
+            if verbose:
+                print(f"GEMM AUTOTUNE {cls} cfg={c} us={us:.2f}", flush=True)
+            if best is None or us < best[0]:
+                best = (us, c)
+        _state["configs"][cls] = best[1]
+        _state["m_configs"][cls] = {
+            b: plan(_M_REP_M[b], n, k, wfmt, partials=False) for b in M_BUCKETS_LARGE}
+        report["classes"][cls] = {"config": best[1], "us": best[0],
+                                  "autotune_s": time.perf_counter() - t1}
+        del sets
+    report["total_s"] = time.perf_counter() - t0
+    _state["report"] = report
+    if verbose:
+        print(f"GEMM CONFIGURE total_s={report['total_s']:.2f} "
+              f"cfgs={ {c: r['config'] for c, r in report['classes'].items()} }", flush=True)
+    return report
+
+
+def reset() -> None:
+    """Clear all load-time state (test isolation)."""
+    _state.clear()
+    _state.update({"configs": {}, "m_configs": {}, "shapes": {}, "workspaces": {},
+                   "device": None, "report": None})

@@ -1,0 +1,159 @@
+/*
+ * acorn_hip.h — C-ABI of libacorn_hip.so, the MI355X (gfx950) kernels behind
+ * the acorninfer_amd Python operators.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, int64 sizes and a hipStream_t (passed as
+ *     void* so this header needs no HIP include);
+ *   - launches only on that stream, never allocates, never synchronises, so
+ *     it can be recorded into a hipGraph;
+ *   - returns ACORN_OK (0) or a negative error code (below). Launch failures
+ *     come back as ACORN_ERR_HIP - hipError_t.
+ *
+ * The Python layer (acorninfer_amd/_lib.py) maps the codes onto the
+ * exceptions the reference raises at the same boundary.
+ */
+#ifndef ACORN_HIP_H_
+#define ACORN_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* activation / weight dtype codes */
+#define ACORN_F32 0
+#define ACORN_F16 1
+#define ACORN_BF16 2
+
+/* weight formats of the quantised GEMM */
+#define ACORN_WFMT_BF16 0 /* dense bf16 [N,K] (nn.Linear layout) */
+#define ACORN_WFMT_W8 1   /* int8 [N,K], fp16 per-channel scale [N] */
+#define ACORN_WFMT_W4 2   /* packed uint4 [N,K/2] (low nibble = even k),
+                             fp16 scale [N,K/128], optional fp16 zero [N,K/128];
+                             no zero pointer = symmetric (w = (u-8)*s) */
+
+/* error codes */
+#define ACORN_OK 0
+#define ACORN_ERR_SHAPE (-1)       /* shape/contiguity contract (reference: AssertionError) */
+#define ACORN_ERR_DTYPE (-2)       /* unsupported dtype combination */
+#define ACORN_ERR_VALUE (-3)       /* bad argument value (reference: ValueError) */
+#define ACORN_ERR_UNSUPPORTED (-4) /* configuration not built (reference: NotImplementedError) */
+#define ACORN_ERR_HIP (-1000)      /* ACORN_ERR_HIP - hipError_t */
+
+/* Library version, bumped when an entry point changes meaning. */
+int acorn_version(void);
+
+/*
+ * K1 fused residual add + RMSNorm.
+ * Replaces acorninfer/ops/rmsnorm.py:39-71 (fused_add_rmsnorm).
+ *   residual == NULL : residual_out = x,                   normed = rmsnorm(x)
+ *   otherwise        : residual_out = round_T(residual+x), normed = rmsnorm(residual_out)
+ * rmsnorm(r) = round_T(r * rsqrt(mean(r^2) + eps) * w) computed in fp32.
+ * x, residual, residual_out, normed: [rows, cols] contiguous, dtype `dtype`;
+ * weight: [cols], dtype `wdtype`. x and residual are never written.
+ */
+int acorn_fused_add_rmsnorm(const void* x, const void* residual, void* residual_out,
+                            const void* weight, void* normed, int64_t rows, int64_t cols,
+                            float eps, int dtype, int wdtype, void* stream);
+
+/*
+ * K1 variant that first reduces `nsplit` fp32 split-K partials of the
+ * previous projection: x = round_T(sum_s part[s, rows, cols]) (summed in
+ * order s = 0..nsplit-1), then behaves as acorn_fused_add_rmsnorm. x_out (may
+ * be NULL) receives the rounded x. No counterpart in the reference: it fuses
+ * the projection's output cast (qwen3.py:232-233, 392-396) into K1.
+ */
+int acorn_fused_add_rmsnorm_partials(const float* part, int64_t nsplit, const void* residual,
+                                     void* residual_out, const void* weight, void* normed,
+                                     void* x_out, int64_t rows, int64_t cols, float eps,
+                                     int dtype, int wdtype, void* stream);
+
+/*
+ * K2 in-place half-rotate RoPE on rows of `head_dim` values.
+ * Replaces acorninfer/ops/rope.py:91-113 (fused_rope_inplace), one call per
+ * tensor. x: [batch, heads, head_dim] contiguous; positions: [batch] int32 or
+ * int64 (pos_is_i64); inv_freq: [head_dim/2] fp32. Rounding mirrors the
+ * reference's three-step torch path (rope.py:1-13).
+ */
+int acorn_rope_inplace(void* x, int64_t batch, int64_t heads, int64_t head_dim,
+                       const void* positions, int pos_is_i64, const float* inv_freq,
+                       int dtype, void* stream);
+
+/*
+ * K2 fused per-head q/k RMSNorm + RoPE, in place on q [batch, q_heads, D] and
+ * k [batch, kv_heads, D]. The norm is models/qwen3.py:50-60 (RMSNorm over D)
+ * applied as q_norm/k_norm (qwen3.py:184-185), followed by rope.py's rotation.
+ * q_w, k_w: [D] dtype `wdtype`.
+ */
+int acorn_qknorm_rope_inplace(void* q, void* k, int64_t batch, int64_t q_heads,
+                              int64_t kv_heads, int64_t head_dim, const void* q_w,
+                              const void* k_w, float eps, const void* positions,
+                              int pos_is_i64, const float* inv_freq, int dtype, int wdtype,
+                              void* stream);
+
+/*
+ * Decode-step fusion of the qkv projection's epilogue with K2 and the KV
+ * scatter: reduces `nsplit` fp32 partials of the fused qkv projection
+ * part[s, batch, (H + 2*KV)*D], rounds to T, applies q/k RMSNorm + RoPE,
+ * writes q_out [batch, H, D] and scatters k, v into
+ * k_pages/v_pages [num_blocks, page, KV, D] at (pages[b], slots[b]) (int64).
+ * Semantics = qwen3.py:180-192 followed by cache/pager.py:87-113
+ * (scatter_decode). No single reference function.
+ */
+int acorn_qkv_epilogue(const float* part, int64_t nsplit, void* q_out, void* k_pages,
+                       void* v_pages, const int64_t* pages, const int64_t* slots,
+                       int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                       int64_t page_size, const void* q_w, const void* k_w, float eps,
+                       const int64_t* positions, const float* inv_freq, int dtype,
+                       int wdtype, void* stream);
+
+/*
+ * K3 flash-decoding paged attention (phase 1 + phase 2).
+ * Replaces acorninfer/ops/paged_attention.py:125-152 (paged_decode_attention).
+ * q: [B, H, D]; k_pages, v_pages: [NB, P, KV, D]; tables: [B, table_stride]
+ * int32; seq_lens: [B] int32 (>= 1, includes the current token);
+ * out: [B, H, D]. Token t of sequence b lives at (tables[b, t/P], t%P);
+ * q head h reads kv head h / (H/KV). One workgroup serves all H/KV q heads of
+ * a kv head (GQA reuse). Workspace: ws_acc [B*H*num_splits*D] fp32 and
+ * ws_ml [2*B*H*num_splits] fp32, caller-owned.
+ */
+int acorn_paged_attention(const void* q, const void* k_pages, const void* v_pages,
+                          const int32_t* tables, const int32_t* seq_lens, void* out,
+                          float* ws_acc, float* ws_ml, int64_t B, int64_t H, int64_t KV,
+                          int64_t D, int64_t P, int64_t num_blocks, int64_t table_stride,
+                          int64_t num_splits, float scale, int dtype, void* stream);
+
+/*
+ * Weight-only quantised GEMM y[M,N] = x[M,K] @ dequant(W)[N,K]^T, bf16 in,
+ * fp32 accumulate.
+ * Replaces acorninfer/ops/quant_gemm.py:257-294 (quant_gemm, W8) and the W4
+ * spike scripts/m7_spike.py:152-231, plus the bf16 decode GEMM
+ * acorninfer/ops/decode_gemm.py:236-257.
+ *   wfmt ACORN_WFMT_BF16: w bf16 [N,K]
+ *   wfmt ACORN_WFMT_W8  : w int8 [N,K], scale fp16 [N]
+ *   wfmt ACORN_WFMT_W4  : w uint8 [N,K/2], scale fp16 [N,K/128], zero fp16
+ *                         [N,K/128] or NULL (symmetric, zero = -8*scale)
+ * out_bf16 != NULL: writes bf16 [M,N] (requires ksplit == 1).
+ * out_part != NULL: writes fp32 partials [ksplit, M, N] (out_bf16 ignored).
+ * Tiling: rows_per_wave = 16*rt, waves (along K) = nw, K per workgroup =
+ * K / ksplit. See acorn_gemm_plan for a default choice.
+ */
+int acorn_quant_gemm(const void* x, const void* w, const void* scale, const void* zero,
+                     void* out_bf16, float* out_part, int64_t M, int64_t N, int64_t K,
+                     int wfmt, int rt, int nw, int ksplit, void* stream);
+
+/* Deterministic split-K reduction: out[M*N] = round_T(sum_s part[s, M*N]). */
+int acorn_splitk_reduce(const float* part, int64_t nsplit, int64_t count, void* out,
+                        int dtype, void* stream);
+
+/* Default tiling for acorn_quant_gemm on this device: writes rt, nw, ksplit. */
+int acorn_gemm_plan(int64_t M, int64_t N, int64_t K, int wfmt, int want_partials, int* rt,
+                    int* nw, int* ksplit);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ACORN_HIP_H_ */

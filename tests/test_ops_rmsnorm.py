@@ -1,0 +1,108 @@
+"""K1 fused_add_rmsnorm (HIP) vs the oracle restatement of
+acorninfer/ops/rmsnorm.py:74-82 (cases as the reference's
+tests/test_ops_rmsnorm.py:19: 4096 rows, tiny hidden 64, non-power-of-2 100)."""
+import pytest
+import torch
+
+from oracle.ops_ref import fused_add_rmsnorm_ref
+from tolerances import TOL_BF16, TOL_F32, max_abs_diff
+from gpu_utils import graph_replays_match
+
+CASES = [(1, 4096), (4, 4096), (8, 4096), (3, 1024), (2, 64), (5, 100), (2, 5000)]
+
+
+def _gen(dtype, wdtype=None):
+    g = torch.Generator().manual_seed(7)
+    for rows, cols in CASES:
+        x = torch.randn(rows, cols, generator=g).to(dtype)
+        r = torch.randn(rows, cols, generator=g).to(dtype)
+        w = torch.randn(cols, generator=g).to(wdtype or dtype)
+        yield x, r, w
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, TOL_F32), (torch.bfloat16, TOL_BF16),
+                                       (torch.float16, TOL_BF16)])
+def test_matches_oracle(dtype, tol):
+    from acorninfer_amd.ops.rmsnorm import fused_add_rmsnorm
+    worst = 0.0
+    for x, r, w in _gen(dtype):
+        xd, rd, wd = x.cuda(), r.cuda(), w.cuda()
+        x_before = xd.clone()
+        for residual in (None, r):
+            n_ref, r_ref = fused_add_rmsnorm_ref(x, residual, w, 1e-6)
+            n_k, r_k = fused_add_rmsnorm(xd, None if residual is None else rd, wd, 1e-6)
+            torch.testing.assert_close(n_k.cpu(), n_ref, **tol)
+            torch.testing.assert_close(r_k.cpu(), r_ref, **tol)
+            worst = max(worst, max_abs_diff(n_k, n_ref))
+        assert torch.equal(xd, x_before)  # x is never written
+    print(f"\n[rmsnorm {dtype} max|diff| = {worst:.3g}]")
+
+
+@pytest.mark.gpu
+def test_residual_is_bit_exact_bf16():
+    """The residual path is one fp32 add + one RNE rounding: bit-exact."""
+    from acorninfer_amd.ops.rmsnorm import fused_add_rmsnorm
+    for x, r, w in _gen(torch.bfloat16):
+        _, r_ref = fused_add_rmsnorm_ref(x, r, w, 1e-6)
+        _, r_k = fused_add_rmsnorm(x.cuda(), r.cuda(), w.cuda(), 1e-6)
+        assert torch.equal(r_k.cpu(), r_ref)
+
+
+@pytest.mark.gpu
+def test_bf16_weight_f32_activation_mix():
+    from acorninfer_amd.ops.rmsnorm import fused_add_rmsnorm
+    for x, r, w in _gen(torch.float32, torch.bfloat16):
+        n_ref, _ = fused_add_rmsnorm_ref(x, r, w, 1e-6)
+        n_k, _ = fused_add_rmsnorm(x.cuda(), r.cuda(), w.cuda(), 1e-6)
+        torch.testing.assert_close(n_k.cpu(), n_ref, **TOL_F32)
+
+
+@pytest.mark.gpu
+def test_leading_dims_and_noncontiguous():
+    from acorninfer_amd.ops.rmsnorm import fused_add_rmsnorm
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(4, 1, 256, generator=g).bfloat16()
+    r = torch.randn(4, 1, 256, generator=g).bfloat16()
+    w = torch.randn(256, generator=g).bfloat16()
+    n_ref, r_ref = fused_add_rmsnorm_ref(x, r, w, 1e-6)
+    n_k, r_k = fused_add_rmsnorm(x.cuda(), r.cuda(), w.cuda(), 1e-6)
+    assert n_k.shape == (4, 1, 256)
+    torch.testing.assert_close(n_k.cpu(), n_ref, **TOL_BF16)
+    xt = torch.randn(256, 6, generator=g).bfloat16().t()  # non-contiguous [6, 256]
+    n_ref, _ = fused_add_rmsnorm_ref(xt, None, w, 1e-6)
+    n_k, _ = fused_add_rmsnorm(xt.cuda(), None, w.cuda(), 1e-6)
+    torch.testing.assert_close(n_k.cpu(), n_ref, **TOL_BF16)
+
+
+@pytest.mark.gpu
+def test_partials_variant_matches_sum_then_k1():
+    from acorninfer_amd.ops.rmsnorm import fused_add_rmsnorm_partials
+    g = torch.Generator().manual_seed(5)
+    part = torch.randn(3, 8, 4096, generator=g)
+    res = torch.randn(8, 4096, generator=g).bfloat16()
+    w = torch.randn(4096, generator=g).bfloat16()
+    x = (part[0] + part[1] + part[2]).bfloat16()  # same order as the kernel
+    n_ref, r_ref = fused_add_rmsnorm_ref(x, res, w, 1e-6)
+    normed = torch.empty(8, 4096, dtype=torch.bfloat16, device="cuda")
+    rout = torch.empty_like(normed)
+    xout = torch.empty_like(normed)
+    fused_add_rmsnorm_partials(part.cuda(), res.cuda(), w.cuda(), 1e-6, normed=normed,
+                               residual_out=rout, x_out=xout)
+    assert torch.equal(xout.cpu(), x)
+    assert torch.equal(rout.cpu(), r_ref)
+    torch.testing.assert_close(normed.cpu(), n_ref, **TOL_BF16)
+
+
+@pytest.mark.gpu
+def test_graph_replay_bitwise():
+    from acorninfer_amd.ops.rmsnorm import fused_add_rmsnorm_partials
+    g = torch.Generator().manual_seed(9)
+    part = torch.randn(2, 8, 4096, generator=g).cuda()
+    res = torch.randn(8, 4096, generator=g).bfloat16().cuda()
+    w = torch.randn(4096, generator=g).bfloat16().cuda()
+    normed = torch.empty(8, 4096, dtype=torch.bfloat16, device="cuda")
+    rout = torch.empty_like(normed)
+    assert graph_replays_match(
+        lambda: fused_add_rmsnorm_partials(part, res, w, 1e-6, normed=normed, residual_out=rout),
+        lambda: normed)

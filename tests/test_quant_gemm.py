@@ -1,0 +1,202 @@
+"""Weight-only GEMM (HIP MFMA) vs the dequantised-matmul oracle.
+
+Anchor as in the reference (tests/test_quant_gemm.py:93-96): y_ref = x.float()
+@ dequant(W).T, dequant from oracle/quant_ref.py. Bar: norm-wise relative
+error <= 1e-2 (north star) and, for W8, the reference's per-class elementwise
+tolerances TOL_W8 (test_quant_gemm.py:56-62).
+
+Shapes: BASELINE config 3 — qkv 4096->6144, o 4096->4096, gate_up
+4096->24576, down 12288->4096, M in {1, 8, 64, 256}; int4 symmetric g128
+(v ~U{-8..7}, fp16 scale ~U(0.005, 0.02)), the same shapes in int8
+per-channel (randn -> quantize_w8, the reference's distribution) and dense
+bf16; plus the reference's asymmetric int4 (quantize_w4) format.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.quant_ref import (dequant_w4_ref, dequant_w4_sym_ref, dequant_w8_ref,
+                              pack_w4_ref, quantize_w4_ref, quantize_w8_ref)
+from tolerances import GEMM_REL, rel_err
+from gpu_utils import graph_replays_match
+
+SHAPES = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (24576, 4096), "down": (4096, 12288)}
+MS = [1, 8, 64, 256]
+TOL_W8 = {"qkv": dict(rtol=2e-2, atol=1.5), "o": dict(rtol=2e-2, atol=1.5),
+          "gate_up": dict(rtol=2e-2, atol=1.5), "down": dict(rtol=2e-2, atol=2.0)}
+
+_W: dict = {}
+
+
+def _w4(cls):
+    key = ("w4", cls)
+    if key not in _W:
+        n, k = SHAPES[cls]
+        g = torch.Generator().manual_seed(101)
+        v = torch.randint(-8, 8, (n, k), generator=g, dtype=torch.int16).numpy()
+        s = (0.005 + 0.015 * torch.rand(n, k // 128, generator=g)).half().numpy()
+        u = (v + 8).astype(np.uint8)
+        wref = torch.from_numpy(dequant_w4_sym_ref(u, s))
+        _W[key] = (torch.from_numpy(pack_w4_ref(u)).cuda(), torch.from_numpy(s).cuda(), wref.cuda())
+    return _W[key]
+
+
+def _w8(cls):
+    key = ("w8", cls)
+    if key not in _W:
+        n, k = SHAPES[cls]
+        g = torch.Generator().manual_seed(11)
+        w = torch.randn(n, k, generator=g).bfloat16().float().numpy()
+        q, s = quantize_w8_ref(w)
+        wref = torch.from_numpy(dequant_w8_ref(q, s))
+        _W[key] = (torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), wref.cuda())
+    return _W[key]
+
+
+def _bf(cls):
+    key = ("bf16", cls)
+    if key not in _W:
+        n, k = SHAPES[cls]
+        g = torch.Generator().manual_seed(7)
+        w = (0.02 * torch.randn(n, k, generator=g)).bfloat16()
+        _W[key] = (w.cuda(), w.float().cuda())
+    return _W[key]
+
+
+def _x(m, k, seed):
+    g = torch.Generator().manual_seed(23 + m + seed)
+    return torch.randn(m, k, generator=g).bfloat16().cuda()
+
+
+def _ref(x, wref):
+    return x.float() @ wref.T  # fp32 anchor on the GPU (torch matmul)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cls", list(SHAPES))
+@pytest.mark.parametrize("m", MS)
+def test_w4_sym_matches_dequant_matmul(cls, m):
+    from acorninfer_amd.ops.quant_gemm import quant_gemm_w4
+    p, s, wref = _w4(cls)
+    x = _x(m, SHAPES[cls][1], 0)
+    out = quant_gemm_w4(x, p, s, cfg=(0, 0, 1))
+    assert out.dtype == torch.bfloat16 and out.shape == (m, SHAPES[cls][0])
+    r = rel_err(out, _ref(x, wref))
+    assert r <= GEMM_REL, f"rel err {r:.3g}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cls", list(SHAPES))
+@pytest.mark.parametrize("m", MS)
+def test_w8_matches_dequant_matmul(cls, m):
+    from acorninfer_amd.ops.quant_gemm import quant_gemm
+    q, s, wref = _w8(cls)
+    x = _x(m, SHAPES[cls][1], 1)
+    out = quant_gemm(x, q, s, cls, cfg=(0, 0, 1))
+    ref = _ref(x, wref)
+    assert rel_err(out, ref) <= GEMM_REL
+    torch.testing.assert_close(out.float(), ref, **TOL_W8[cls])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cls", list(SHAPES))
+@pytest.mark.parametrize("m", [1, 8, 64])
+def test_bf16_matches_matmul(cls, m):
+    from acorninfer_amd.ops.quant_gemm import bf16_gemm
+    w, wref = _bf(cls)
+    x = _x(m, SHAPES[cls][1], 2)
+    out = bf16_gemm(x, w, cfg=(0, 0, 1))
+    assert rel_err(out, _ref(x, wref)) <= GEMM_REL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 8, 16, 33])
+def test_w4_asymmetric_reference_format(m):
+    """The reference's own int4 format (quantize_w4: u in [0,15], fp16 scale
+    and zero per group) through the same kernel with a zero pointer."""
+    from acorninfer_amd.ops.quant_gemm import quant_gemm_w4
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(1024, 4096, generator=g).bfloat16().float().numpy()
+    u, s, z = quantize_w4_ref(w)
+    wref = torch.from_numpy(dequant_w4_ref(u, s, z)).cuda()
+    x = _x(m, 4096, 3)
+    out = quant_gemm_w4(x, torch.from_numpy(pack_w4_ref(u)).cuda(), torch.from_numpy(s).cuda(),
+                        torch.from_numpy(z).cuda(), cfg=(0, 0, 1))
+    assert rel_err(out, _ref(x, wref)) <= GEMM_REL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ks", [2, 3])
+def test_split_k_partials_and_reduce(ks):
+    """ksplit > 1 writes fp32 partials; summing them in order equals the
+    reduce kernel's output; ksplit=1 and ksplit>1 agree to fp32 rounding."""
+    from acorninfer_amd._lib import WFMT_W4
+    from acorninfer_amd.ops.quant_gemm import gemm_partials, quant_gemm_w4
+    p, s, wref = _w4("down")
+    x = _x(8, 12288, 4)
+    part = torch.empty(ks, 8, 4096, device="cuda")
+    gemm_partials(x, p, s, None, WFMT_W4, part, (1, 0, ks))
+    full = part.sum(0)
+    one = quant_gemm_w4(x, p, s, cfg=(0, 0, 1))
+    via = quant_gemm_w4(x, p, s, cfg=(0, 0, ks))
+    torch.testing.assert_close(full, _ref(x, wref), rtol=1e-2, atol=5e-2)
+    acc = part[0].clone()
+    for i in range(1, ks):
+        acc += part[i]
+    assert torch.equal(via, acc.bfloat16())
+    assert rel_err(one, via) < 5e-3
+
+
+@pytest.mark.gpu
+def test_deterministic_and_graph_replay():
+    from acorninfer_amd.ops.quant_gemm import quant_gemm_w4
+    p, s, _ = _w4("down")
+    x = _x(8, 12288, 5)
+    a = quant_gemm_w4(x, p, s, cfg=(0, 0, 3))
+    b = quant_gemm_w4(x, p, s, cfg=(0, 0, 3))
+    assert torch.equal(a, b)
+    out = torch.empty(8, 4096, dtype=torch.bfloat16, device="cuda")
+    assert graph_replays_match(lambda: quant_gemm_w4(x, p, s, cfg=(0, 0, 3), out=out),
+                               lambda: out)
+
+
+@pytest.mark.gpu
+def test_no_host_sync_on_launch():
+    from acorninfer_amd.ops import quant_gemm as qg
+    q, s, _ = _w8("o")
+    x = _x(8, 4096, 6)
+    qg.reset()
+    qg._state["configs"]["qo"] = (0, 0, 2)
+    qg.quant_gemm(x, q, s, "qo")  # allocates the split workspace before the check
+    torch.cuda.synchronize()
+    prev = torch.cuda.get_sync_debug_mode()
+    try:
+        torch.cuda.set_sync_debug_mode(2)
+        out = qg.quant_gemm(x, q, s, "qo")
+    finally:
+        torch.cuda.set_sync_debug_mode(prev)
+    assert torch.equal(out, qg.quant_gemm(x, q, s, "qo", cfg=(0, 0, 2)))
+    qg.reset()
+
+
+@pytest.mark.gpu
+def test_large_m_routing_contract():
+    """As the reference (test_quant_gemm.py:208-221): M > 16 without
+    configure() raises RuntimeError naming configure; an explicit cfg works."""
+    from acorninfer_amd.ops import quant_gemm as qg
+    q, s, _ = _w8("o")
+    x = _x(17, 4096, 7)
+    qg.reset()
+    with pytest.raises(RuntimeError, match="configure"):
+        qg.quant_gemm(x, q, s, "qo")
+    assert qg.quant_gemm(x, q, s, "qo", cfg=(32, 64, 128, 4, 3)).shape == (17, 4096)
+
+
+def test_bucket_boundaries_and_classes():
+    from acorninfer_amd.ops import quant_gemm as qg
+    assert qg.bucket_for(16) == "d" and qg.bucket_for(17) == "s"
+    assert qg.bucket_for(66) == "m" and qg.bucket_for(256) == "m"
+    assert qg.bucket_for(257) == "l" and qg.bucket_for(1024) == "l"
+    assert qg.CLASSES == {"qo": (4096, 4096), "kv": (1024, 4096), "gate_up": (12288, 4096),
+                          "down": (4096, 12288), "lm_head": (151936, 4096)}
+    assert qg._CLS_BY_SHAPE[(4096, 12288)] == "down"
