@@ -44,7 +44,7 @@ __global__ __launch_bounds__(kWave) void paged_attn_split_kernel(
     const T* __restrict__ q, const T* __restrict__ k_pages, const T* __restrict__ v_pages,
     const int32_t* __restrict__ tables, const int32_t* __restrict__ lens, T* __restrict__ out,
     float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l, int H,
-    int KV, int P, int table_stride, int S, float scale_log2) {
+    int KV, int P, int num_blocks, int table_stride, int S, float scale_log2) {
   constexpr int DQ = D / kLPT;                 // q.k dims per lane
   constexpr int DPO = D >= kWave ? D / kWave : 1;  // p.V dims per lane
   constexpr bool kPVAll = D >= kWave;
@@ -56,7 +56,10 @@ __global__ __launch_bounds__(kWave) void paged_attn_split_kernel(
   const bool pv_active = kPVAll || lane < D;
   const int d0 = kPVAll ? lane * DPO : lane;
 
-  const int L = lens[b];
+  // Bounds guards: a length beyond the table row or a block id outside the
+  // pool is clamped so that a malformed table can never read outside the
+  // caller's buffers (valid inputs are unaffected).
+  const int L = min(max(lens[b], 0), table_stride * P);
   const int npages = (L + P - 1) / P;
   const int pps = (npages + S - 1) / S;
   const int start = sp * pps * P;
@@ -83,12 +86,16 @@ __global__ __launch_bounds__(kWave) void paged_attn_split_kernel(
     for (int i = 0; i < DPO; ++i) acc[h][i] = 0.f;
   }
 
+  auto block_of = [&](int t) -> size_t {
+    const unsigned page = (unsigned)trow[t / P];
+    return page < (unsigned)num_blocks ? page : 0u;
+  };
   auto k_addr = [&](int t) -> const T* {
-    const int page = trow[t / P];
+    const size_t page = block_of(t);
     return k_pages + ((size_t)page * P + (t % P)) * tok_stride + (size_t)kvh * D + c * DQ;
   };
   auto v_addr = [&](int t) -> const T* {
-    const int page = trow[t / P];
+    const size_t page = block_of(t);
     return v_pages + ((size_t)page * P + (t % P)) * tok_stride + (size_t)kvh * D + d0;
   };
 
@@ -214,14 +221,14 @@ __global__ __launch_bounds__(kWave) void paged_attn_combine_kernel(
 template <typename T, int D, int REP>
 int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* tables,
                 const int32_t* lens, void* out, float* ws_acc, float* ws_ml, int64_t B,
-                int64_t H, int64_t KV, int64_t P, int64_t table_stride, int64_t S, float scale,
+                int64_t H, int64_t KV, int64_t P, int64_t num_blocks, int64_t table_stride, int64_t S, float scale,
                 hipStream_t st) {
   dim3 grid((unsigned)S, (unsigned)KV, (unsigned)B), block(kWave);
   float* ws_m = ws_ml;
   float* ws_l = ws_ml ? ws_ml + B * H * S : nullptr;
   paged_attn_split_kernel<T, D, REP><<<grid, block, 0, st>>>(
       (const T*)q, (const T*)kp, (const T*)vp, tables, lens, (T*)out, ws_acc, ws_m, ws_l,
-      (int)H, (int)KV, (int)P, (int)table_stride, (int)S, scale * kLog2e);
+      (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e);
   ACORN_LAUNCH_CHECK();
   if (S > 1) {
     paged_attn_combine_kernel<T, D><<<dim3((unsigned)(B * H)), dim3(kWave), 0, st>>>(
@@ -234,13 +241,13 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
 template <typename T, int D>
 int dispatch_rep(int64_t rep, const void* q, const void* kp, const void* vp,
                  const int32_t* tables, const int32_t* lens, void* out, float* ws_acc,
-                 float* ws_ml, int64_t B, int64_t H, int64_t KV, int64_t P, int64_t ts,
+                 float* ws_ml, int64_t B, int64_t H, int64_t KV, int64_t P, int64_t num_blocks, int64_t ts,
                  int64_t S, float scale, hipStream_t st) {
   switch (rep) {
-    case 1: return launch_attn<T, D, 1>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, ts, S, scale, st);
-    case 2: return launch_attn<T, D, 2>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, ts, S, scale, st);
-    case 4: return launch_attn<T, D, 4>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, ts, S, scale, st);
-    case 8: return launch_attn<T, D, 8>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, ts, S, scale, st);
+    case 1: return launch_attn<T, D, 1>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
+    case 2: return launch_attn<T, D, 2>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
+    case 4: return launch_attn<T, D, 4>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
+    case 8: return launch_attn<T, D, 8>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
   }
   return ACORN_ERR_UNSUPPORTED;
 }
@@ -248,13 +255,13 @@ int dispatch_rep(int64_t rep, const void* q, const void* kp, const void* vp,
 template <typename T>
 int dispatch_d(int64_t D, int64_t rep, const void* q, const void* kp, const void* vp,
                const int32_t* tables, const int32_t* lens, void* out, float* ws_acc,
-               float* ws_ml, int64_t B, int64_t H, int64_t KV, int64_t P, int64_t ts,
+               float* ws_ml, int64_t B, int64_t H, int64_t KV, int64_t P, int64_t num_blocks, int64_t ts,
                int64_t S, float scale, hipStream_t st) {
   switch (D) {
-    case 16: return dispatch_rep<T, 16>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, ts, S, scale, st);
-    case 32: return dispatch_rep<T, 32>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, ts, S, scale, st);
-    case 64: return dispatch_rep<T, 64>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, ts, S, scale, st);
-    case 128: return dispatch_rep<T, 128>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, ts, S, scale, st);
+    case 16: return dispatch_rep<T, 16>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
+    case 32: return dispatch_rep<T, 32>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
+    case 64: return dispatch_rep<T, 64>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
+    case 128: return dispatch_rep<T, 128>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
   }
   return ACORN_ERR_UNSUPPORTED;
 }
@@ -278,9 +285,9 @@ extern "C" int acorn_paged_attention(const void* q, const void* k_pages, const v
   const int64_t rep = H / KV;
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
-    case ACORN_F32: return dispatch_d<float>(D, rep, q, k_pages, v_pages, tables, seq_lens, out, ws_acc, ws_ml, B, H, KV, P, table_stride, num_splits, scale, st);
-    case ACORN_F16: return dispatch_d<_Float16>(D, rep, q, k_pages, v_pages, tables, seq_lens, out, ws_acc, ws_ml, B, H, KV, P, table_stride, num_splits, scale, st);
-    case ACORN_BF16: return dispatch_d<__bf16>(D, rep, q, k_pages, v_pages, tables, seq_lens, out, ws_acc, ws_ml, B, H, KV, P, table_stride, num_splits, scale, st);
+    case ACORN_F32: return dispatch_d<float>(D, rep, q, k_pages, v_pages, tables, seq_lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, table_stride, num_splits, scale, st);
+    case ACORN_F16: return dispatch_d<_Float16>(D, rep, q, k_pages, v_pages, tables, seq_lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, table_stride, num_splits, scale, st);
+    case ACORN_BF16: return dispatch_d<__bf16>(D, rep, q, k_pages, v_pages, tables, seq_lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, table_stride, num_splits, scale, st);
   }
   return ACORN_ERR_DTYPE;
 }
