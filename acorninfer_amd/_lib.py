@@ -21,7 +21,7 @@ LIB_PATH = Path(os.environ.get(
 
 # dtype / format codes (acorn_hip.h)
 F32, F16, BF16 = 0, 1, 2
-WFMT_BF16, WFMT_W8, WFMT_W4 = 0, 1, 2
+WFMT_BF16, WFMT_W8, WFMT_W4, WFMT_F32 = 0, 1, 2, 3
 
 OK = 0
 ERR_SHAPE, ERR_DTYPE, ERR_VALUE, ERR_UNSUPPORTED, ERR_HIP = -1, -2, -3, -4, -1000
@@ -44,13 +44,18 @@ _SIGNATURES = {
     "acorn_qknorm_rope_inplace": [_vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _f32, _vp, _i32,
                                   _vp, _i32, _i32, _vp],
     "acorn_qkv_epilogue": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
-                           _vp, _vp, _f32, _vp, _vp, _i32, _i32, _vp],
+                           _i64, _vp, _vp, _f32, _vp, _vp, _i32, _i32, _vp],
     "acorn_paged_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                               _i64, _i64, _i64, _i64, _f32, _i32, _vp],
     "acorn_quant_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _i32, _i32,
                          _i32, _vp],
     "acorn_splitk_reduce": [_vp, _i64, _i64, _vp, _i32, _vp],
     "acorn_gemm_plan": [_i64, _i64, _i64, _i32, _i32, _pi, _pi, _pi],
+    "acorn_embedding": [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
+    "acorn_silu_mul": [_vp, _i64, _vp, _vp, _i64, _i64, _i32, _vp],
+    "acorn_argmax": [_vp, _i64, _i64, _vp, _i32, _vp],
+    "acorn_kv_scatter": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32,
+                         _vp],
 }
 
 _lib = None

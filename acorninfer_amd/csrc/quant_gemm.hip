@@ -273,6 +273,28 @@ __global__ __launch_bounds__(256) void wgemm_kernel(
   }
 }
 
+// fp32 weights and activations (the fp32 parity path; not a performance
+// path). One wavefront per weight row; lanes stride K by 4-float vectors and
+// the M dot products are finished with a wavefront reduction. Writes fp32
+// y[m, n] into part[blockIdx.y, m, n] for the K range of split blockIdx.y.
+__global__ __launch_bounds__(256) void f32_gemv_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ w,
+                                                       float* __restrict__ part, int M, int N,
+                                                       int K, int kper) {
+  const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int n = blockIdx.x * (blockDim.x / kWave) + wid;
+  if (n >= N) return;
+  const int k0 = blockIdx.y * kper, k1 = min(K, k0 + kper);
+  const float* wr = w + (size_t)n * K;
+  for (int m = 0; m < M; ++m) {
+    const float* xr = x + (size_t)m * K;
+    float a = 0.f;
+    for (int k = k0 + lane; k < k1; k += kWave) a += xr[k] * wr[k];
+    a = wave_sum(a);
+    if (lane == 0) part[(size_t)blockIdx.y * M * N + (size_t)m * N + n] = a;
+  }
+}
+
 // Split-K reduction (fixed order) with the output cast.
 template <typename T>
 __global__ void splitk_reduce_kernel(const float* __restrict__ part, int nsplit, size_t count,
@@ -332,6 +354,7 @@ int ilog2_ceil(int v) {
 }
 
 int ku_of(int wfmt) {
+  if (wfmt == ACORN_WFMT_F32) return 4;
   return wfmt == ACORN_WFMT_BF16 ? 32 : wfmt == ACORN_WFMT_W8 ? 64 : 128;
 }
 
@@ -341,6 +364,15 @@ int plan(int64_t M, int64_t N, int64_t K, int wfmt, int want_partials, Cfg* cfg,
          int* ksplit, int* nchunk) {
   const int ku = ku_of(wfmt);
   if (M <= 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
+  if (wfmt == ACORN_WFMT_F32) {
+    cfg->rt = 1;
+    cfg->mt = 1;
+    cfg->upw = 1;
+    *nw = 4;
+    *ksplit = 1;
+    *nchunk = 1;
+    return ACORN_OK;
+  }
   cfg->mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
   cfg->rt = 1;
   const int R = cfg->mt == 1 ? (1 << ilog2_ceil((int)M)) : 16;
@@ -388,10 +420,23 @@ extern "C" int acorn_quant_gemm(const void* x, const void* w, const void* scale,
                                 const void* zero, void* out_bf16, float* out_part, int64_t M,
                                 int64_t N, int64_t K, int wfmt, int rt, int nw, int ksplit,
                                 void* stream) {
-  if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4)
+  if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
+      wfmt != ACORN_WFMT_F32)
     return ACORN_ERR_DTYPE;
   if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   if (M == 0) return ACORN_OK;
+  if (wfmt == ACORN_WFMT_F32) {
+    // fp32 output always goes through out_part ([ksplit, M, N]).
+    if (!x || !w || !out_part) return ACORN_ERR_VALUE;
+    if (M > 65535 || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return ACORN_ERR_SHAPE;
+    const int ks = ksplit > 0 ? ksplit : 1;
+    const int64_t kper = (K + ks - 1) / ks;
+    dim3 grid((unsigned)((N + 3) / 4), (unsigned)ks), block(256);
+    f32_gemv_kernel<<<grid, block, 0, (hipStream_t)stream>>>(
+        (const float*)x, (const float*)w, out_part, (int)M, (int)N, (int)K, (int)kper);
+    ACORN_LAUNCH_CHECK();
+    return ACORN_OK;
+  }
   if (!x || !w || (wfmt != ACORN_WFMT_BF16 && !scale)) return ACORN_ERR_VALUE;
   if (!out_bf16 && !out_part) return ACORN_ERR_VALUE;
   if (M > 65535 * 64 || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return ACORN_ERR_SHAPE;

@@ -109,7 +109,7 @@ __global__ __launch_bounds__(kWave) void qkv_epilogue_kernel(
     const float* __restrict__ part, int nsplit, T* __restrict__ q_out,
     T* __restrict__ k_pages, T* __restrict__ v_pages, const int64_t* __restrict__ pages,
     const int64_t* __restrict__ slots, int batch, int H, int KV, int D, int P,
-    const TW* __restrict__ q_w, const TW* __restrict__ k_w, float eps,
+    int64_t num_blocks, const TW* __restrict__ q_w, const TW* __restrict__ k_w, float eps,
     const int64_t* __restrict__ pos, const float* __restrict__ inv_freq) {
   const int rows_per_b = H + 2 * KV;
   const int b = blockIdx.x / rows_per_b;
@@ -134,24 +134,27 @@ __global__ __launch_bounds__(kWave) void qkv_epilogue_kernel(
     x1[j] = round_to<T>(a);  // the projection's bf16 output
     x2[j] = round_to<T>(c);
   }
-  T* dst;
+  T* dst = nullptr;
   if (h < H) {
     norm_rope_row<T, TW>(x1, x2, half, q_w, eps, (float)pos[b], inv_freq);
     dst = q_out + ((size_t)b * H + h) * D;
   } else {
     const int kvh = h < H + KV ? h - H : h - H - KV;
-    const size_t off = (((size_t)pages[b] * P + (size_t)slots[b]) * KV + kvh) * D;
+    // A (page, slot) outside the pool is dropped rather than written.
+    const uint64_t page = (uint64_t)pages[b], slot = (uint64_t)slots[b];
+    const bool in_pool = page < (uint64_t)num_blocks && slot < (uint64_t)P;
+    const size_t off = in_pool ? ((page * P + slot) * KV + kvh) * D : 0;
     if (h < H + KV) {
       norm_rope_row<T, TW>(x1, x2, half, k_w, eps, (float)pos[b], inv_freq);
-      dst = k_pages + off;
+      if (in_pool) dst = k_pages + off;
     } else {
-      dst = v_pages + off;
+      if (in_pool) dst = v_pages + off;
     }
   }
 #pragma unroll
   for (int j = 0; j < kMaxPairs; ++j) {
     const int i = threadIdx.x + j * kWave;
-    if (i < half) {
+    if (dst && i < half) {
       dst[i] = from_f32<T>(x1[j]);
       dst[i + half] = from_f32<T>(x2[j]);
     }
@@ -190,12 +193,12 @@ int launch_qknorm(void* q, void* k, int64_t batch, int64_t H, int64_t KV, int64_
 template <typename T, typename TW>
 int launch_qkv(const float* part, int64_t nsplit, void* q_out, void* kp, void* vp,
                const int64_t* pages, const int64_t* slots, int64_t batch, int64_t H, int64_t KV,
-               int64_t D, int64_t P, const void* qw, const void* kw, float eps,
+               int64_t D, int64_t P, int64_t NB, const void* qw, const void* kw, float eps,
                const int64_t* pos, const float* inv_freq, hipStream_t st) {
   dim3 grid((unsigned)(batch * (H + 2 * KV))), block(kWave);
   qkv_epilogue_kernel<T, TW><<<grid, block, 0, st>>>(
       part, (int)nsplit, (T*)q_out, (T*)kp, (T*)vp, pages, slots, (int)batch, (int)H, (int)KV,
-      (int)D, (int)P, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
+      (int)D, (int)P, NB, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
   ACORN_LAUNCH_CHECK();
   return ACORN_OK;
 }
@@ -249,17 +252,18 @@ extern "C" int acorn_qknorm_rope_inplace(void* q, void* k, int64_t batch, int64_
 extern "C" int acorn_qkv_epilogue(const float* part, int64_t nsplit, void* q_out, void* k_pages,
                                   void* v_pages, const int64_t* pages, const int64_t* slots,
                                   int64_t batch, int64_t q_heads, int64_t kv_heads,
-                                  int64_t head_dim, int64_t page_size, const void* q_w,
+                                  int64_t head_dim, int64_t page_size, int64_t num_blocks,
+                                  const void* q_w,
                                   const void* k_w, float eps, const int64_t* positions,
                                   const float* inv_freq, int dtype, int wdtype, void* stream) {
-  if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || page_size <= 0 || nsplit < 1 ||
-      !head_dim_ok(head_dim))
+  if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || page_size <= 0 || num_blocks <= 0 ||
+      nsplit < 1 || !head_dim_ok(head_dim))
     return ACORN_ERR_SHAPE;
   if (batch == 0) return ACORN_OK;
   if (!part || !q_out || !k_pages || !v_pages || !pages || !slots || !q_w || !k_w ||
       !positions || !inv_freq)
     return ACORN_ERR_VALUE;
   ACORN_DISPATCH_TW(dtype, wdtype, launch_qkv, part, nsplit, q_out, k_pages, v_pages, pages,
-                    slots, batch, q_heads, kv_heads, head_dim, page_size, q_w, k_w, eps,
+                    slots, batch, q_heads, kv_heads, head_dim, page_size, num_blocks, q_w, k_w, eps,
                     positions, inv_freq, (hipStream_t)stream)
 }

@@ -1,0 +1,267 @@
+"""Decode throughput of the Qwen3-8B-shaped hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--format bf16|w4a16|w8a16]
+                    [--batch C] [--prompt-len L] [--extra] [--no-cpu-baseline]
+
+A step is one hipGraph-replayed decode step of C sequences (BASELINE
+configuration 4: Qwen3-8B shape, 36 layers, random-init weights N(0, 0.02),
+greedy, page 16, prompts of L=512 tokens). The prompts' KV is synthetic
+(random bf16 written straight into the paged pool; prefill is not part of
+the measured path), the first ids are random, every later id is the greedy
+choice of the previous step (fed back on the device). `value` is decode
+tokens per second over the K timed steps: C*K / elapsed.
+
+The JSON line also carries:
+- roofline: the dominant kernel (the weight-streaming GEMM) timed with HIP
+  events on its own stream: a hipGraph of one step's GEMM launches (36 x
+  {qkv, o, gate|up, down} + lm_head, the step's own weights and buffers) is
+  replayed and timed; achieved = algorithmic bytes of those launches / time.
+- cpu_baseline: the CPU oracle of the reference's path (oracle/qwen3_ref.py,
+  fp32 torch on the host cores) on a bounded sample of the same workload
+  (C sequences at context L, a few decode steps of a few layers plus the
+  lm_head), scaled to the 36-layer step.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _gemm_bytes(lin, M: int) -> int:
+    """Algorithmic bytes of one projection launch: weights (+ scales) once,
+    activations in and bf16 results out."""
+    return lin.nbytes() + 2 * M * lin.K + 2 * M * lin.N
+
+
+def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int, seed: int):
+    import torch
+
+    from acorninfer_amd.cache.pager import BlockAllocator, PagedCacheView, PagedKVCache
+    from acorninfer_amd.engine.graph_runner import DecodeGraphRunner
+    from acorninfer_amd.models.qwen3 import Qwen3DecodeModel
+
+    t0 = time.perf_counter()
+    model = Qwen3DecodeModel.random_init(cfg, weight_format=fmt, seed=seed, device="cuda")
+    torch.cuda.synchronize()
+    _log(f"model {fmt}: {model.weight_bytes() / 1e9:.3f} GB weights in "
+         f"{time.perf_counter() - t0:.1f} s")
+    P = 16
+    max_len = prompt_len + total_steps + 1
+    per_seq = -(-max_len // P)
+    alloc = BlockAllocator(batch * per_seq + 2)
+    cache = PagedKVCache(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim, P, alloc,
+                         "cuda", torch.bfloat16)
+    g = torch.Generator(device="cuda").manual_seed(seed + 1)
+    cache.k_pool.normal_(generator=g)
+    cache.v_pool.normal_(generator=g)
+    views = []
+    for _ in range(batch):
+        v = PagedCacheView(cache)
+        for _t in range(-(-prompt_len // P)):
+            v.table.append(alloc.allocate())
+        for li in range(cfg.num_hidden_layers):
+            v._lens[li] = prompt_len
+        views.append(v)
+    runner = DecodeGraphRunner(model, cache, alloc, max_model_len=max_len, buckets=(batch,))
+    first = torch.randint(0, cfg.vocab_size, (batch,), generator=torch.Generator().manual_seed(
+        seed + 2)).tolist()
+    return model, cache, runner, views, first
+
+
+def time_decode(runner, views, first, steps: int, warmup: int):
+    import torch
+    log = runner.decode_loop(views, first, warmup) if warmup else None
+    nxt = log[-1].tolist() if warmup else first
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    log = runner.decode_loop(views, nxt, steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return dt, log
+
+
+def gemm_roofline(model, runner, batch: int, reps: int = 5):
+    """Time one step's GEMM launches (hipGraph on a private stream, HIP events
+    on that stream). Returns (achieved GB/s, per-step bytes, per-step µs,
+    launches per step)."""
+    import torch
+    st = runner._state(batch)
+    buf = st.buf
+    s = torch.cuda.Stream()
+    launches = []
+    for lw in model.layers:
+        launches += [(lw.qkv, buf.normed, buf.cfgs["qkv"], None, buf.part_qkv),
+                     (lw.o, buf.attn, buf.cfgs["o"], None, buf.part_o),
+                     (lw.gate_up, buf.normed, buf.cfgs["gate_up"], None, buf.part_gu),
+                     (lw.down, buf.act, buf.cfgs["down"], None, buf.part_down)]
+    launches.append((model.lm_head, buf.normed, buf.cfgs["lm_head"], buf.logits, None))
+    nbytes = sum(_gemm_bytes(lin, batch) for lin, *_ in launches)
+
+    def body():
+        sp = s.cuda_stream
+        for lin, x, cfg, out, part in launches:
+            lin.launch(x, batch, cfg, out=out, part=part, stream=sp)
+
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            body()
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            g.replay()
+        e1.record(s)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    return nbytes / (us * 1e-6) / 1e9, nbytes, us, len(launches)
+
+
+def cpu_baseline(cfg, batch: int, prompt_len: int, layers: int = 2, steps: int = 2):
+    """The CPU oracle (fp32 torch) on a bounded sample of the same step:
+    `layers` of the 36 layers plus the lm_head, `steps` decode steps of
+    `batch` sequences at context `prompt_len`; the per-step time is scaled to
+    36 layers."""
+    import torch
+
+    from acorninfer_amd.models.qwen3 import random_state_dict
+    from oracle.qwen3_ref import Qwen3Ref
+
+    threads = torch.get_num_threads()
+    sub = cfg.with_layers(layers)
+    sd = random_state_dict(sub, seed=5, std=0.02, dtype=torch.float32)
+    ref = Qwen3Ref(sub, sd, torch.float32)
+    del sd
+    g = torch.Generator().manual_seed(6)
+    shape = (batch, cfg.num_key_value_heads, prompt_len, cfg.head_dim)
+    cache = [[torch.randn(*shape, generator=g), torch.randn(*shape, generator=g)]
+             for _ in range(layers)]
+    ids = torch.randint(0, cfg.vocab_size, (batch, 1), generator=g)
+    # split the step into the layer part and the lm_head part
+    t_total = 0.0
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        ref.forward(ids, cache)
+        t_total += time.perf_counter() - t0
+    per_step_sample = t_total / steps
+    h = torch.randn(batch, 1, cfg.hidden_size, generator=g)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ref._linear(h, "lm_head")
+    t_head = (time.perf_counter() - t0) / steps
+    t_layers = max(per_step_sample - t_head, 0.0)
+    t_step = t_layers * cfg.num_hidden_layers / layers + t_head
+    return {
+        "value": round(batch / t_step, 4),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle/qwen3_ref.py fp32 on {threads} host threads: {steps} decode steps "
+                   f"of {batch} sequences at context {prompt_len}, {layers} of "
+                   f"{cfg.num_hidden_layers} layers + lm_head, scaled to "
+                   f"{cfg.num_hidden_layers} layers ({t_step:.2f} s/step)"),
+    }
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--format", default="bf16", choices=["bf16", "w8a16", "w4a16"])
+    ap.add_argument("--batch", type=int, default=8)
+    ap.add_argument("--prompt-len", type=int, default=512)
+    ap.add_argument("--layers", type=int, default=0, help="override layer count (debug only)")
+    ap.add_argument("--extra", action="store_true",
+                    help="also measure C=1 and the W4A16 model (reported under 'extra')")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=20261027)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the decode step is sized for one MI355X; see the sharding notes).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from acorninfer_amd.config import Qwen3Config
+
+    cfg = Qwen3Config.qwen3_8b()
+    if args.layers:
+        cfg = cfg.with_layers(args.layers)
+    total = args.warmup + args.steps
+    model, cache, runner, views, first = build_workload(cfg, args.format, args.batch,
+                                                        args.prompt_len, total, args.seed)
+    _log(f"graph captured for C={args.batch}; warmup {args.warmup}, timed {args.steps}")
+    dt, log = time_decode(runner, views, first, args.steps, args.warmup)
+    tok_s = args.batch * args.steps / dt
+    ms = dt * 1e3 / args.steps
+    _log(f"decode: {tok_s:.1f} tok/s, {ms:.3f} ms/step; last tokens {log[-1].tolist()}")
+    gbs, nbytes, us, nl = gemm_roofline(model, runner, args.batch)
+    _log(f"GEMM: {nl} launches/step, {nbytes / 1e9:.3f} GB, {us:.1f} us -> {gbs:.0f} GB/s")
+    step_bytes = model.weight_bytes() + sum(
+        v.seq_len for v in views) * cfg.num_hidden_layers * cfg.num_key_value_heads * \
+        cfg.head_dim * 2 * 2
+    extra = {"step_hbm_bound_ms": round(step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3, 4),
+             "step_roofline_frac": round(step_bytes / (HBM_PEAK_GBS * 1e9) / (dt / args.steps), 4),
+             "gemm_us_per_step": round(us, 2), "gemm_launches_per_step": nl}
+    if args.extra:
+        del model, cache, runner
+        torch.cuda.empty_cache()
+        for fmt, c in (("bf16", 1), ("w4a16", 8), ("w4a16", 1)):
+            m2, c2, r2, v2, f2 = build_workload(cfg, fmt, c, args.prompt_len, total, args.seed)
+            dt2, _ = time_decode(r2, v2, f2, args.steps, args.warmup)
+            extra[f"{fmt}_C{c}_tok_s"] = round(c * args.steps / dt2, 2)
+            extra[f"{fmt}_C{c}_ms_per_step"] = round(dt2 * 1e3 / args.steps, 4)
+            _log(f"{fmt} C={c}: {c * args.steps / dt2:.1f} tok/s")
+            del m2, c2, r2
+            torch.cuda.empty_cache()
+    cpu = None
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(cfg, args.batch, args.prompt_len)
+        _log(f"cpu baseline {cpu['value']} tok/s in {time.perf_counter() - t0:.1f} s")
+    line = {
+        "metric": "decode tok/s Qwen3-8B C=1/8 (bf16, W4A16); kernel HBM GB/s vs 8 TB/s peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if args.format == "bf16" else f"bf16 activations, {args.format} weights",
+        "data": "synthetic: random-init weights N(0,0.02), random prompt KV, greedy ids",
+        "config": {"workload": f"Qwen3-8B-shaped decode, C={args.batch}, prompt "
+                               f"{args.prompt_len}, {args.format}, hipGraph step, page 16",
+                   "batch": args.batch, "prompt_len": args.prompt_len,
+                   "layers": cfg.num_hidden_layers, "weights": args.format},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "wgemm_kernel (all projections of one step)",
+                     "bytes_per_step": nbytes, "us_per_step": round(us, 2)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

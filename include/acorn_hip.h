@@ -33,6 +33,8 @@ extern "C" {
 #define ACORN_WFMT_W4 2   /* packed uint4 [N,K/2] (low nibble = even k),
                              fp16 scale [N,K/128], optional fp16 zero [N,K/128];
                              no zero pointer = symmetric (w = (u-8)*s) */
+#define ACORN_WFMT_F32 3  /* dense fp32 [N,K] with fp32 activations; output
+                             only through out_part (the fp32 parity path) */
 
 /* error codes */
 #define ACORN_OK 0
@@ -98,14 +100,16 @@ int acorn_qknorm_rope_inplace(void* q, void* k, int64_t batch, int64_t q_heads,
  * scatter: reduces `nsplit` fp32 partials of the fused qkv projection
  * part[s, batch, (H + 2*KV)*D], rounds to T, applies q/k RMSNorm + RoPE,
  * writes q_out [batch, H, D] and scatters k, v into
- * k_pages/v_pages [num_blocks, page, KV, D] at (pages[b], slots[b]) (int64).
+ * k_pages/v_pages [num_blocks, page, KV, D] at (pages[b], slots[b]) (int64);
+ * a (page, slot) outside [0, num_blocks) x [0, page_size) is not written.
  * Semantics = qwen3.py:180-192 followed by cache/pager.py:87-113
  * (scatter_decode). No single reference function.
  */
 int acorn_qkv_epilogue(const float* part, int64_t nsplit, void* q_out, void* k_pages,
                        void* v_pages, const int64_t* pages, const int64_t* slots,
                        int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                       int64_t page_size, const void* q_w, const void* k_w, float eps,
+                       int64_t page_size, int64_t num_blocks, const void* q_w,
+                       const void* k_w, float eps,
                        const int64_t* positions, const float* inv_freq, int dtype,
                        int wdtype, void* stream);
 
@@ -135,6 +139,7 @@ int acorn_paged_attention(const void* q, const void* k_pages, const void* v_page
  *   wfmt ACORN_WFMT_W8  : w int8 [N,K], scale fp16 [N]
  *   wfmt ACORN_WFMT_W4  : w uint8 [N,K/2], scale fp16 [N,K/128], zero fp16
  *                         [N,K/128] or NULL (symmetric, zero = -8*scale)
+ *   wfmt ACORN_WFMT_F32 : w fp32 [N,K], x fp32 [M,K]; fp32 result in out_part
  * out_bf16 != NULL: writes bf16 [M,N] (requires ksplit == 1).
  * out_part != NULL: writes fp32 partials [ksplit, M, N] (out_bf16 ignored).
  * Tiling: rows_per_wave = 16*rt, waves (along K) = nw, K per workgroup =
@@ -151,6 +156,46 @@ int acorn_splitk_reduce(const float* part, int64_t nsplit, int64_t count, void* 
 /* Default tiling for acorn_quant_gemm on this device: writes rt, nw, ksplit. */
 int acorn_gemm_plan(int64_t M, int64_t N, int64_t K, int wfmt, int want_partials, int* rt,
                     int* nw, int* ksplit);
+
+/*
+ * Embedding row gather: out[b, :] = table[ids[b], :].
+ * Replaces nn.Embedding in acorninfer/models/qwen3.py:585 (embed_tokens).
+ * table: [vocab, cols]; ids: [rows] int64 (an id outside [0, vocab) reads
+ * row 0); out: [rows, cols].
+ */
+int acorn_embedding(const void* table, const int64_t* ids, void* out, int64_t rows,
+                    int64_t vocab, int64_t cols, int dtype, void* stream);
+
+/*
+ * SwiGLU activation of the fused gate|up projection:
+ *   act[r, i] = round(round(silu(g)) * u),  g = gate_up[r, i], u = gate_up[r, inter + i]
+ * Replaces F.silu(gate_proj(x)) * up_proj(x) in acorninfer/models/qwen3.py:392-396.
+ * part != NULL: g, u = round(sum_s part[s, r, .]) over `nsplit` fp32 split-K
+ * partials [nsplit, rows, 2*inter] (summed in split order); otherwise
+ * gate_up [rows, 2*inter] of dtype `dtype` is read. act: [rows, inter].
+ */
+int acorn_silu_mul(const float* part, int64_t nsplit, const void* gate_up, void* act,
+                   int64_t rows, int64_t inter, int dtype, void* stream);
+
+/*
+ * Greedy token choice: out[r] = first index of the row maximum of x[rows, cols]
+ * (NaN ranks above every number). Replaces logits.argmax(dim=1) in
+ * acorninfer/engine/graph_runner.py:177 and engine/executor.py:105-107.
+ */
+int acorn_argmax(const void* x, int64_t rows, int64_t cols, int64_t* out, int dtype,
+                 void* stream);
+
+/*
+ * Decode-step KV write: k_pages[pages[b], slots[b], h, :] = k[b, h, :] (same
+ * for v). Replaces PagedKVCache.scatter_decode in
+ * acorninfer/cache/pager.py:87-113 (torch index_put). k, v: [batch, kv_heads,
+ * head_dim]; k_pages, v_pages: [num_blocks, page_size, kv_heads, head_dim];
+ * pages, slots: [batch] int64. A (page, slot) outside the pool is skipped.
+ */
+int acorn_kv_scatter(const void* k, const void* v, void* k_pages, void* v_pages,
+                     const int64_t* pages, const int64_t* slots, int64_t batch,
+                     int64_t kv_heads, int64_t head_dim, int64_t page_size,
+                     int64_t num_blocks, int dtype, void* stream);
 
 #ifdef __cplusplus
 }
