@@ -5,27 +5,36 @@
 // group-128 (fp16 scale [N,K/128], optional fp16 zero [N,K/128]; byte =
 // u_even | u_odd << 4 as in quantize.py:122-131; symmetric int4 v in [-8,7]
 // is stored as u = v + 8 with zero = -8*scale, which dequantises exactly).
+// A fourth format, dense fp32 with fp32 activations, is a plain VALU kernel
+// for the fp32 parity path.
 //
-// Design (decode is HBM-bound on the weight stream, so the goal is to keep
-// the VALU cost of dequantisation below the HBM rate and to have every weight
-// byte in flight early):
+// Decode (M <= 16) is a weight stream, so the kernel is built to keep HBM
+// busy:
 //  * v_mfma_f32_16x16x32_bf16 with the WEIGHTS as the 16-row A operand and x
-//    (M <= 16 rows, zero/duplicate padded) as the B operand. A 16-byte load
-//    per lane feeds 1 (bf16), 2 (int8) or 4 (int4) MFMAs.
+//    (M rows, padded) as the B operand. One 16-byte load per lane feeds 1
+//    (bf16), 2 (int8) or 4 (int4) MFMAs.
 //  * int4 -> bf16 in two VALU ops per dword: (w >> 4p) & 0x000F000F | 0x43004300
-//    gives the bf16 pair (128+u_p, 128+u_{p+4}); the (p, p+4) pairing is a
-//    k permutation that is applied once to x when it is staged into LDS.
-//  * int8 -> bf16 via (q ^ 0x80) -> v_cvt_f32_ubyteN -> v_cvt_pk_bf16_f32,
-//    i.e. 128+q, exact.
-//  * The +128 offset is removed with sum_k x = ones-MFMA on the same B
-//    operand: y = s * (C - 128 X) (+ zero X for int4), applied per 128-group
-//    (int4) or once at the end (int8).
-//  * x for the workgroup's K chunk is staged in LDS in MFMA-B order
-//    ([k/8][row][8]), so every B fetch is one conflict-free ds_read_b128.
-//  * A workgroup = NW waves splitting the chunk's K; waves are reduced through
-//    LDS in fixed order; split-K across workgroups writes fp32 partials that
-//    the consumer (or acorn_splitk_reduce) sums in fixed order: results are
-//    bitwise deterministic and graph-replay stable.
+//    is the bf16 pair (128+u_p, 128+u_{p+4}); the (p, p+4) pairing is a k
+//    permutation applied once to x when it is staged into LDS.
+//    int8 -> bf16 via (q ^ 0x80) -> v_cvt_f32_ubyteN -> v_cvt_pk_bf16_f32
+//    (= 128+q, exact). The +128 offset is removed with X = sum_k x (an MFMA
+//    against ones, computed once per workgroup because x does not change
+//    from tile to tile): y = s*(C - 128 X) (+ zero*X for int4), per 128-group
+//    for int4, once per row for int8.
+//  * A workgroup owns a run of 16*RT-row tiles and one K range (split
+//    blockIdx.y). x for the whole K range is staged in LDS once, in MFMA-B
+//    order ([k/8][row][8], one conflict-free ds_read_b128 per B fetch).
+//    The NW waves split the K range; the next (tile, k-chunk) step's weights
+//    and scales are loaded into the second register set while the current
+//    step is on the MFMAs, so every wave keeps a step of loads in flight.
+//  * At the end of a tile the waves' partials are summed through
+//    double-buffered LDS in fixed wave order (one barrier per tile).
+//  * Split-K (ksplit > 1): each split writes fp32 partials, which the
+//    consumer (the decode step's K1 / SwiGLU / qkv epilogue, or
+//    splitk_reduce_kernel for a bf16 output) sums in split order, so results
+//    are bitwise deterministic. There is no cross-workgroup reduction inside
+//    the kernel: on CDNA an agent-scope fence writes back and invalidates the
+//    XCD's whole L2.
 #include <algorithm>
 
 #include "common.h"
@@ -37,13 +46,12 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <int WFMT> struct Fmt;
 template <> struct Fmt<ACORN_WFMT_BF16> {
-  static constexpr int KU = 32;     // k covered by one 16-byte lane load across the wave
-  static constexpr int MPU = 1;     // MFMAs per unit
-  static constexpr int BPK_NUM = 2, BPK_DEN = 1;  // bytes per k = NUM/DEN
+  static constexpr int KU = 32;                   // k of one 16-byte lane load across the wave
+  static constexpr int MPU = 1;                   // MFMAs per unit
+  static constexpr int BPK_NUM = 2, BPK_DEN = 1;  // bytes per k
 };
 template <> struct Fmt<ACORN_WFMT_W8> {
   static constexpr int KU = 64, MPU = 2, BPK_NUM = 1, BPK_DEN = 1;
@@ -85,198 +93,271 @@ __device__ __forceinline__ u32x4 unpack_w8(uint32_t lo, uint32_t hi) {
   return r;
 }
 
-__device__ __forceinline__ float h2f(const _Float16* p, size_t i) { return (float)p[i]; }
+// UPW consecutive fp16 values; the caller guarantees 2*UPW-byte alignment.
+template <int UPW> struct HalfVec {
+  _Float16 v[UPW];
+};
+template <int UPW>
+__device__ __forceinline__ void load_halves(const _Float16* p, _Float16 (&dst)[UPW]) {
+  typedef _Float16 hv __attribute__((ext_vector_type(UPW)));
+  const hv t = *(const hv*)p;
+#pragma unroll
+  for (int u = 0; u < UPW; ++u) dst[u] = t[u];
+}
 
-// Grid: x = N / (16*RT) row blocks, y = ksplit, z = ceil(M / (16*MT)) m blocks.
-// Each workgroup covers K range [y*Kwg, (y+1)*Kwg), Kwg = nchunk * NW*UPW*KU.
-template <int WFMT, int RT, int MT, int UPW>
-__global__ __launch_bounds__(256) void wgemm_kernel(
-    const __bf16* __restrict__ x, const uint8_t* __restrict__ w,
-    const _Float16* __restrict__ scale, const _Float16* __restrict__ zero,
-    __bf16* __restrict__ out, float* __restrict__ part, int M, int N, int K, int nchunk,
-    int log2R) {
+// Registers of one pipeline step: this lane's weight units plus the scales
+// of the output rows it holds (rows 4*(lane/16)+i of each 16-row group).
+template <int WFMT, int RT, int UPW>
+struct StepRegs {
+  static constexpr int NS = WFMT == ACORN_WFMT_W4 ? UPW : 1;
+  u32x4 w[RT][UPW];
+  _Float16 s[RT][4][NS];
+  _Float16 z[RT][4][NS];
+};
+
+struct KArgs {
+  const __bf16* x;
+  const uint8_t* w;
+  const _Float16* scale;
+  const _Float16* zero;
+  __bf16* out;
+  float* part;
+  int M, N, K;
+  int nk;          // k-chunks per tile (K range = nk * KC)
+  int tpw;         // tiles per workgroup
+  int ksplit;
+  int log2R;       // LDS rows per m tile = 1 << log2R
+};
+
+// Grid: x = tile groups, y = ksplit, z = m blocks of 16*MT rows.
+template <int WFMT, int RT, int MT, int UPW, int NW>
+__global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
   using F = Fmt<WFMT>;
-  constexpr int KU = F::KU, MPU = F::MPU;
-  constexpr int ROWS = 16 * RT;
+  constexpr int KU = F::KU, MPU = F::MPU, ROWS = 16 * RT;
+  constexpr int KC = NW * UPW * KU;               // k per chunk (all waves)
+  constexpr int TILE = RT * MT * 4 * kWave;       // floats of one wave's tile partial
+  constexpr int NT = NW * kWave;
   extern __shared__ __align__(16) unsigned char smem[];
 
-  const int NW = blockDim.x / kWave;
   const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int lg = lane / 16, lr = lane % 16;
-  const int R = 1 << log2R;                 // LDS rows per m tile
-  const int n0 = blockIdx.x * ROWS;
+  const int lg = lane >> 4, lr = lane & 15;
+  const int R = 1 << a.log2R;
+  const int nk = a.nk;
+  const int KR = nk * KC;                         // K range of this workgroup
+  const int kr0 = blockIdx.y * KR;
+  const int CPR = KR / 8;                         // 16-byte x pieces per row
+  const int GR = KR / 128;                        // int4 groups in the K range
+  const int ntiles = a.N / ROWS;
+  const int t_begin = blockIdx.x * a.tpw;
+  const int t_end = min(t_begin + a.tpw, ntiles);
+  if (t_begin >= t_end) return;                   // uniform for the workgroup
   const int mblk = blockIdx.z * 16 * MT;
-  const int kc = NW * UPW * KU;             // k per chunk
-  const int k_wg0 = blockIdx.y * nchunk * kc;
-  const int groups_c = kc / 128;            // int4 groups per chunk
-  const size_t wrow_bytes = (size_t)K * F::BPK_NUM / F::BPK_DEN;
+  const size_t wrow = (size_t)a.K * F::BPK_NUM / F::BPK_DEN;
+  const int G = a.K / 128;
+  const bool has_zero = a.zero != nullptr;
 
-  // LDS carve-up: x chunk [MT][kc/8][R][16B] | int4 scale [groups_c][ROWS] | zero
+  // LDS: x [MT][CPR][R] u32x4 | int4 group sums [MT][GR][16] f32 | red [2][NW][TILE]
   u32x4* xs = (u32x4*)smem;
-  const int xs_vecs = MT * (kc / 8) * R;
-  _Float16* s_lds = (_Float16*)(smem + (size_t)xs_vecs * 16);
-  _Float16* z_lds = s_lds + groups_c * ROWS;
+  float* xgs = (float*)(smem + (size_t)MT * CPR * R * 16);
+  float* red = xgs + (WFMT == ACORN_WFMT_W4 ? MT * GR * 16 : 0);
 
-  f32x4 acc[RT][MT];
-  f32x4 xtot[MT];  // int8: running sum_k x per column
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) xtot[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
-
-  for (int ch = 0; ch < nchunk; ++ch) {
-    const int kchunk0 = k_wg0 + ch * kc;
-    const int kw0 = kchunk0 + wid * UPW * KU;  // this wave's first k
-    // ---- issue this wave's weight loads (16 B per lane per unit) ---------
-    u32x4 wreg[RT][UPW];
+  auto load_step = [&](int s, StepRegs<WFMT, RT, UPW>& r) {
+    const int t = t_begin + s / nk, c = s % nk;
+    const int kw = kr0 + c * KC + wid * UPW * KU;  // this wave's first k of the step
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const uint8_t* rowp = w + (size_t)(n0 + rt * 16 + lr) * wrow_bytes;
+      const uint8_t* rowp = a.w + (size_t)(t * ROWS + rt * 16 + lr) * wrow;
 #pragma unroll
       for (int u = 0; u < UPW; ++u) {
-        const int k = kw0 + u * KU + (KU / 4) * lg;
-        wreg[rt][u] = *(const u32x4*)(rowp + (size_t)k * F::BPK_NUM / F::BPK_DEN);
+        const int k = kw + u * KU + (KU / 4) * lg;
+        r.w[rt][u] = *(const u32x4*)(rowp + (size_t)k * F::BPK_NUM / F::BPK_DEN);
       }
-    }
-    // ---- stage x chunk into LDS (MFMA-B order; int4 k-permutation) -------
-    const int cpr = kc / 8;  // 16-byte pieces per row
-    for (int p = threadIdx.x; p < MT * R * cpr; p += blockDim.x) {
-      const int c = p % cpr, rr = p / cpr;  // rr = mt * R + row
-      const int mt = rr / R, row = rr % R;
-      const int m = mblk + mt * 16 + row;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (m < M) {
-        v = *(const u32x4*)(x + (size_t)m * K + kchunk0 + c * 8);
-        if constexpr (WFMT == ACORN_WFMT_W4) {
-          // items [x0,x4,x1,x5,x2,x6,x3,x7] to match unpack_w4's pairing
-          u32x4 t;
-          t[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
-          t[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
-          t[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
-          t[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
-          v = t;
-        }
-      }
-      xs[((size_t)mt * cpr + c) * R + row] = v;
     }
     if constexpr (WFMT == ACORN_WFMT_W4) {
-      const int G = K / 128, g0 = kchunk0 / 128;
-      for (int p = threadIdx.x; p < ROWS * groups_c; p += blockDim.x) {
-        const int g = p % groups_c, row = p / groups_c;
-        const size_t gi = (size_t)(n0 + row) * G + g0 + g;
-        s_lds[g * ROWS + row] = scale[gi];
-        if (zero) z_lds[g * ROWS + row] = zero[gi];
+      const int g0 = kw / 128;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const size_t row = (size_t)t * ROWS + rt * 16 + 4 * lg + i;
+          load_halves<UPW>(a.scale + row * G + g0, r.s[rt][i]);
+          if (has_zero) load_halves<UPW>(a.zero + row * G + g0, r.z[rt][i]);
+        }
+    } else if constexpr (WFMT == ACORN_WFMT_W8) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        _Float16 sv[4];
+        load_halves<4>(a.scale + (size_t)t * ROWS + rt * 16 + 4 * lg, sv);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.s[rt][i][0] = sv[i];
       }
     }
-    __syncthreads();
+  };
 
-    // ---- MFMA over this wave's units --------------------------------------
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  f32x4 x8[MT];  // int8: sum of x over this wave's k (all chunks), per column
+
+  auto compute = [&](const StepRegs<WFMT, RT, UPW>& r, int c, f32x4 (&acc)[RT][MT]) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
-      const int c0 = (wid * UPW * KU + u * KU) / 8 + (KU / 32) * lg;  // chunk-local
+      const int kl = c * KC + wid * UPW * KU + u * KU;  // workgroup-local k of unit u
+      const int c0 = kl / 8 + (KU / 32) * lg;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         u32x4 bop[MPU];
 #pragma unroll
-        for (int j = 0; j < MPU; ++j)
-          bop[j] = xs[((size_t)mt * cpr + c0 + j) * R + (lr & (R - 1))];
+        for (int j = 0; j < MPU; ++j) bop[j] = xs[((size_t)mt * CPR + c0 + j) * R + (lr & (R - 1))];
         if constexpr (WFMT == ACORN_WFMT_BF16) {
 #pragma unroll
-          for (int rt = 0; rt < RT; ++rt) acc[rt][mt] = mfma(wreg[rt][u], bop[0], acc[rt][mt]);
+          for (int rt = 0; rt < RT; ++rt) acc[rt][mt] = mfma(r.w[rt][u], bop[0], acc[rt][mt]);
         } else if constexpr (WFMT == ACORN_WFMT_W8) {
 #pragma unroll
-          for (int j = 0; j < MPU; ++j) xtot[mt] = mfma(ones, bop[j], xtot[mt]);
-#pragma unroll
           for (int rt = 0; rt < RT; ++rt) {
-            const u32x4 q = wreg[rt][u];
+            const u32x4 q = r.w[rt][u];
             acc[rt][mt] = mfma(unpack_w8(q[0], q[1]), bop[0], acc[rt][mt]);
             acc[rt][mt] = mfma(unpack_w8(q[2], q[3]), bop[1], acc[rt][mt]);
           }
-        } else {  // int4: one 128-group per unit
-          f32x4 xg = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int j = 0; j < MPU; ++j) xg = mfma(ones, bop[j], xg);
-          const int g = (wid * UPW * KU + u * KU) / 128;  // chunk-local group
+        } else {
+          const float xg = xgs[((size_t)mt * GR + kl / 128) * 16 + lr];
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt) {
-            const u32x4 q = wreg[rt][u];
-            f32x4 c = {0.f, 0.f, 0.f, 0.f};
+            const u32x4 q = r.w[rt][u];
+            f32x4 cc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < MPU; ++j) c = mfma(unpack_w4(q[j]), bop[j], c);
-            const int rbase = g * ROWS + rt * 16 + 4 * lg;
+            for (int j = 0; j < MPU; ++j) cc = mfma(unpack_w4(q[j]), bop[j], cc);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const float s = (float)s_lds[rbase + i];
-              const float zc = zero ? (float)z_lds[rbase + i] - 128.f * s : -136.f * s;
-              acc[rt][mt][i] += s * c[i] + zc * xg[i];
+              const float s = (float)r.s[rt][i][u];
+              const float zc = has_zero ? (float)r.z[rt][i][u] - 128.f * s : -136.f * s;
+              acc[rt][mt][i] += s * cc[i] + zc * xg;
             }
           }
         }
       }
     }
-    __syncthreads();
-  }
-
-  // ---- int8 per-channel epilogue: y = s * (C - 128 X) ---------------------
-  if constexpr (WFMT == ACORN_WFMT_W8) {
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float s = h2f(scale, (size_t)n0 + rt * 16 + 4 * lg + i);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          acc[rt][mt][i] = s * (acc[rt][mt][i] - 128.f * xtot[mt][i]);
-      }
-    }
-  }
-
-  // ---- reduce the NW waves (fixed order) and store ------------------------
-  const size_t plane = (size_t)M * N;
-  auto store = [&](int rt, int mt, int i, int ln, float v) {
-    const int n = n0 + rt * 16 + 4 * (ln / 16) + i;
-    const int m = mblk + mt * 16 + (ln % 16);
-    if (m >= M) return;
-    if (part)
-      part[(size_t)blockIdx.y * plane + (size_t)m * N + n] = v;
-    else
-      out[(size_t)m * N + n] = (__bf16)v;
   };
-  if (NW == 1) {
+
+  const size_t plane = (size_t)a.M * a.N;
+  auto out_index = [&](int t, int e, int& m, int& n) {
+    const int ln = e % kWave, i = (e / kWave) % 4, rm = e / (4 * kWave);
+    const int rt = rm / MT, mt = rm % MT;
+    n = t * ROWS + rt * 16 + 4 * (ln / 16) + i;
+    m = mblk + mt * 16 + (ln % 16);
+  };
+
+  int rbuf = 0;
+  auto finish_tile = [&](int t, const StepRegs<WFMT, RT, UPW>& r, f32x4 (&acc)[RT][MT]) {
+    if constexpr (WFMT == ACORN_WFMT_W8) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float s = (float)r.s[rt][i][0];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[rt][mt][i] = s * (acc[rt][mt][i] - 128.f * x8[mt][i]);
+        }
+    }
+    float* rb = red + (size_t)rbuf * NW * TILE;
+    rbuf ^= 1;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) store(rt, mt, i, lane, acc[rt][mt][i]);
-    return;
+        for (int i = 0; i < 4; ++i) {
+          rb[(size_t)wid * TILE + ((rt * MT + mt) * 4 + i) * kWave + lane] = acc[rt][mt][i];
+          acc[rt][mt][i] = 0.f;
+        }
+    __syncthreads();
+    const bool direct = a.ksplit == 1 && a.out != nullptr;
+    for (int e = threadIdx.x; e < TILE; e += NT) {
+      float v = rb[e];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) v += rb[(size_t)ww * TILE + e];
+      int m, n;
+      out_index(t, e, m, n);
+      if (m >= a.M) continue;
+      if (direct)
+        a.out[(size_t)m * a.N + n] = (__bf16)v;
+      else
+        a.part[(size_t)blockIdx.y * plane + (size_t)m * a.N + n] = v;
+    }
+  };
+
+  const int nsteps = (t_end - t_begin) * nk;
+  StepRegs<WFMT, RT, UPW> ra, rb;
+  load_step(0, ra);
+
+  // ---- stage x for the whole K range (MFMA-B order; int4 k-permutation) ----
+  for (int p = threadIdx.x; p < MT * R * CPR; p += NT) {
+    const int c = p % CPR, rr = p / CPR;  // rr = mt * R + row
+    const int mt = rr / R, row = rr % R;
+    const int m = mblk + mt * 16 + row;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (m < a.M) {
+      v = *(const u32x4*)(a.x + (size_t)m * a.K + kr0 + c * 8);
+      if constexpr (WFMT == ACORN_WFMT_W4) {
+        // items [x0,x4,x1,x5,x2,x6,x3,x7] to match unpack_w4's pairing
+        u32x4 t;
+        t[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+        t[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+        t[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+        t[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+        v = t;
+      }
+    }
+    xs[((size_t)mt * CPR + c) * R + row] = v;
   }
-  float* red = (float*)smem;  // [NW][RT][MT][4][64]
-  constexpr int TILE = RT * MT * 4 * kWave;
+  __syncthreads();
+  // ---- per-workgroup x sums (tile independent) -----------------------------
+  if constexpr (WFMT == ACORN_WFMT_W4) {
+    for (int g = wid; g < GR; g += NW) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        f32x4 xg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < MPU; ++j)
+          xg = mfma(ones, xs[((size_t)mt * CPR + g * 16 + 4 * lg + j) * R + (lr & (R - 1))], xg);
+        if (lg == 0) xgs[((size_t)mt * GR + g) * 16 + lr] = xg[0];
+      }
+    }
+    __syncthreads();
+  } else if constexpr (WFMT == ACORN_WFMT_W8) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) x8[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nk; ++c)
+#pragma unroll
+      for (int u = 0; u < UPW; ++u) {
+        const int c0 = (c * KC + wid * UPW * KU + u * KU) / 8 + 2 * lg;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            x8[mt] = mfma(ones, xs[((size_t)mt * CPR + c0 + j) * R + (lr & (R - 1))], x8[mt]);
+      }
+  }
+
+  // ---- main pipeline: load step s+1 while step s is on the MFMAs ----------
+  f32x4 acc[RT][MT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        red[(size_t)wid * TILE + ((rt * MT + mt) * 4 + i) * kWave + lane] = acc[rt][mt][i];
-  __syncthreads();
-  for (int e = threadIdx.x; e < TILE; e += blockDim.x) {
-    float v = red[e];
-    for (int ww = 1; ww < NW; ++ww) v += red[(size_t)ww * TILE + e];
-    const int ln = e % kWave, i = (e / kWave) % 4, rm = e / (4 * kWave);
-    store(rm / MT, rm % MT, i, ln, v);
+    for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < nsteps; s += 2) {
+    if (s + 1 < nsteps) load_step(s + 1, rb);
+    compute(ra, s % nk, acc);
+    if (s % nk == nk - 1) finish_tile(t_begin + s / nk, ra, acc);
+    if (s + 1 >= nsteps) break;
+    if (s + 2 < nsteps) load_step(s + 2, ra);
+    compute(rb, (s + 1) % nk, acc);
+    if ((s + 1) % nk == nk - 1) finish_tile(t_begin + (s + 1) / nk, rb, acc);
   }
 }
 
 // fp32 weights and activations (the fp32 parity path; not a performance
-// path). One wavefront per weight row; lanes stride K by 4-float vectors and
-// the M dot products are finished with a wavefront reduction. Writes fp32
-// y[m, n] into part[blockIdx.y, m, n] for the K range of split blockIdx.y.
+// path). One wavefront per weight row; lanes stride K and the M dot products
+// are finished with a wavefront reduction. Writes fp32 y[m, n] into
+// part[blockIdx.y, m, n] for the K range of split blockIdx.y.
 __global__ __launch_bounds__(256) void f32_gemv_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ w,
                                                        float* __restrict__ part, int M, int N,
@@ -288,10 +369,10 @@ __global__ __launch_bounds__(256) void f32_gemv_kernel(const float* __restrict__
   const float* wr = w + (size_t)n * K;
   for (int m = 0; m < M; ++m) {
     const float* xr = x + (size_t)m * K;
-    float a = 0.f;
-    for (int k = k0 + lane; k < k1; k += kWave) a += xr[k] * wr[k];
-    a = wave_sum(a);
-    if (lane == 0) part[(size_t)blockIdx.y * M * N + (size_t)m * N + n] = a;
+    float acc = 0.f;
+    for (int k = k0 + lane; k < k1; k += kWave) acc += xr[k] * wr[k];
+    acc = wave_sum(acc);
+    if (lane == 0) part[(size_t)blockIdx.y * M * N + (size_t)m * N + n] = acc;
   }
 }
 
@@ -301,51 +382,18 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, int nsplit,
                                      T* __restrict__ out) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= count) return;
-  float a = part[i];
-  for (int s = 1; s < nsplit; ++s) a += part[(size_t)s * count + i];
-  out[i] = (T)a;
+  float acc = part[i];
+  for (int s = 1; s < nsplit; ++s) acc += part[(size_t)s * count + i];
+  out[i] = (T)acc;
 }
 
-struct Cfg {
-  int rt, mt, upw;
+// ----------------------------------------------------------------- planning --
+
+struct Tiling {
+  int rt, upw, nw, ksplit, tpw;  // the tunable knobs (acorn_gemm_plan's cfg[0..4])
+  int mt, R, nk, ntiles, mblocks, groups;
+  size_t lds;
 };
-
-template <int WFMT, int RT, int MT, int UPW>
-void launch_one(dim3 grid, dim3 block, size_t lds, hipStream_t st, const void* x, const void* w,
-                const void* s, const void* z, void* out, float* part, int M, int N, int K,
-                int nchunk, int log2R) {
-  auto kfn = wgemm_kernel<WFMT, RT, MT, UPW>;
-  kfn<<<grid, block, lds, st>>>((const __bf16*)x, (const uint8_t*)w, (const _Float16*)s,
-                                (const _Float16*)z, (__bf16*)out, part, M, N, K, nchunk, log2R);
-}
-
-template <int WFMT, int RT, int MT>
-int dispatch_upw(int upw, dim3 grid, dim3 block, size_t lds, hipStream_t st, const void* x,
-                 const void* w, const void* s, const void* z, void* out, float* part, int M,
-                 int N, int K, int nchunk, int log2R) {
-  switch (upw) {
-    case 2: launch_one<WFMT, RT, MT, 2>(grid, block, lds, st, x, w, s, z, out, part, M, N, K, nchunk, log2R); return 0;
-    case 4: launch_one<WFMT, RT, MT, 4>(grid, block, lds, st, x, w, s, z, out, part, M, N, K, nchunk, log2R); return 0;
-    case 8: launch_one<WFMT, RT, MT, 8>(grid, block, lds, st, x, w, s, z, out, part, M, N, K, nchunk, log2R); return 0;
-  }
-  return ACORN_ERR_UNSUPPORTED;
-}
-
-template <int WFMT>
-int dispatch_cfg(const Cfg& c, dim3 grid, dim3 block, size_t lds, hipStream_t st, const void* x,
-                 const void* w, const void* s, const void* z, void* out, float* part, int M,
-                 int N, int K, int nchunk, int log2R) {
-#define ACORN_CASE(RT_, MT_)                                                                 \
-  if (c.rt == RT_ && c.mt == MT_)                                                            \
-    return dispatch_upw<WFMT, RT_, MT_>(c.upw, grid, block, lds, st, x, w, s, z, out, part, M, \
-                                        N, K, nchunk, log2R);
-  ACORN_CASE(1, 1)
-  ACORN_CASE(2, 1)
-  ACORN_CASE(1, 2)
-  ACORN_CASE(1, 4)
-#undef ACORN_CASE
-  return ACORN_ERR_UNSUPPORTED;
-}
 
 int ilog2_ceil(int v) {
   int r = 0;
@@ -354,136 +402,235 @@ int ilog2_ceil(int v) {
 }
 
 int ku_of(int wfmt) {
-  if (wfmt == ACORN_WFMT_F32) return 4;
   return wfmt == ACORN_WFMT_BF16 ? 32 : wfmt == ACORN_WFMT_W8 ? 64 : 128;
 }
 
-// Plan: M-tiles, units per wave, waves, k-split. Keeps the LDS x chunk
-// <= 64 KiB and every weight byte in a register load issued up front.
-int plan(int64_t M, int64_t N, int64_t K, int wfmt, int want_partials, Cfg* cfg, int* nw,
-         int* ksplit, int* nchunk) {
-  const int ku = ku_of(wfmt);
+bool supported(int rt, int mt, int upw, int nw) {
+  const bool shape = (mt == 1 && (rt == 1 || rt == 2 || rt == 4)) || (rt == 1 && (mt == 2 || mt == 4));
+  const bool u = upw == 2 || upw == 4 || upw == 8 || upw == 16;
+  const bool w = nw == 1 || nw == 2 || nw == 4 || nw == 8;
+  return shape && u && w && rt * upw <= 16 && (mt == 1 || upw <= 8) && (mt == 1 || nw <= 4);
+}
+
+constexpr int kCUs = 256;
+constexpr int64_t kTargetWG = 4 * kCUs;  // default workgroups per launch
+
+size_t lds_bytes(int wfmt, int mt, int R, int rt, int nw, int KR) {
+  size_t b = (size_t)mt * R * KR * 2;
+  if (wfmt == ACORN_WFMT_W4) b += (size_t)mt * (KR / 128) * 16 * 4;
+  b += (size_t)2 * nw * rt * mt * 4 * kWave * 4;
+  return b;
+}
+
+// cfg: {rt, upw, nw, ksplit, tpw}; 0 = choose.
+int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling* t) {
   if (M <= 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
-  if (wfmt == ACORN_WFMT_F32) {
-    cfg->rt = 1;
-    cfg->mt = 1;
-    cfg->upw = 1;
-    *nw = 4;
-    *ksplit = 1;
-    *nchunk = 1;
-    return ACORN_OK;
+  const int ku = ku_of(wfmt);
+  if (N % 16 || K % ku) return ACORN_ERR_SHAPE;
+  if (wfmt == ACORN_WFMT_W4 && K % 128) return ACORN_ERR_SHAPE;
+  const int req_rt = cfg ? cfg[0] : 0, req_upw = cfg ? cfg[1] : 0, req_nw = cfg ? cfg[2] : 0;
+  const int req_ks = cfg ? cfg[3] : 0, req_tpw = cfg ? cfg[4] : 0;
+  t->mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  t->R = t->mt == 1 ? (1 << ilog2_ceil((int)M)) : 16;
+  t->rt = req_rt > 0 ? req_rt : 1;
+  if (t->mt > 1) t->rt = 1;
+  while (t->rt > 1 && N % (16 * t->rt)) t->rt /= 2;
+  t->upw = req_upw > 0 ? req_upw : (wfmt == ACORN_WFMT_W4 ? 4 : 8);
+  t->nw = req_nw > 0 ? req_nw : 4;
+  if (t->mt > 1) {
+    t->upw = std::min(t->upw, 8);
+    t->nw = std::min(t->nw, 4);
   }
-  cfg->mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-  cfg->rt = 1;
-  const int R = cfg->mt == 1 ? (1 << ilog2_ceil((int)M)) : 16;
-  if (N % 16) return ACORN_ERR_SHAPE;
-  if (K % ku) return ACORN_ERR_SHAPE;
-  // units per wave (8 -> every lane holds 128 B of weights per row tile)
-  int upw = 8;
-  while (upw > 2 && K % (ku * upw)) upw /= 2;
-  if (K % (ku * upw)) return ACORN_ERR_SHAPE;
-  // waves per workgroup along K: as many as divide K, <= 4
-  int w = 4;
-  while (w > 1 && (K % ((int64_t)ku * upw * w))) --w;
-  // LDS budget for the x chunk
-  while (w > 1 && (int64_t)cfg->mt * R * ku * upw * w * 2 > 64 * 1024) --w;
-  while (K % ((int64_t)ku * upw * w)) --w;
-  const int64_t kc = (int64_t)ku * upw * w;
-  const int64_t chunks = K / kc;
-  cfg->upw = upw;
-  *nw = w;
-  if (want_partials) {
-    *ksplit = (int)chunks;
-    *nchunk = 1;
+  while (t->rt * t->upw > 16) t->upw /= 2;
+  const int64_t G = K / 128;
+  auto kc = [&]() { return (int64_t)t->nw * t->upw * ku; };
+  auto fits = [&]() {
+    return K % kc() == 0 && (wfmt != ACORN_WFMT_W4 || G % t->upw == 0);
+  };
+  while (!fits() && t->upw > 2) t->upw /= 2;
+  while (!fits() && t->nw > 1) t->nw /= 2;
+  if (!fits()) return ACORN_ERR_SHAPE;
+  if (!supported(t->rt, t->mt, t->upw, t->nw)) return ACORN_ERR_UNSUPPORTED;
+  // LDS budget per workgroup: two workgroups per CU for decode sizes, one
+  // for larger M (which is MFMA-bound anyway).
+  const size_t limit = t->mt == 1 ? 80 * 1024 : 160 * 1024;
+  auto lds_for = [&](int64_t kr) { return lds_bytes(wfmt, t->mt, t->R, t->rt, t->nw, (int)kr); };
+  while (lds_for(kc()) > limit && t->nw > 1) t->nw /= 2;
+  while (lds_for(kc()) > limit && t->upw > 2) t->upw /= 2;
+  if (!fits() || lds_for(kc()) > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
+  const int64_t chunks = K / kc();
+  if (req_ks > 0) {
+    // a requested split is raised to the next divisor of the chunk count
+    // whose K range fits the LDS of one workgroup
+    t->ksplit = req_ks;
+    while (t->ksplit <= chunks && (chunks % t->ksplit || lds_for(K / t->ksplit) > 160 * 1024))
+      ++t->ksplit;
+    if (t->ksplit > chunks) return ACORN_ERR_UNSUPPORTED;
   } else {
-    *ksplit = 1;
-    *nchunk = (int)chunks;
+    // default: about kTargetWG workgroups of one tile each, splitting K as
+    // far as needed to reach that count (and to fit the LDS budget)
+    t->ksplit = 1;
+    while (chunks % t->ksplit || lds_for(K / t->ksplit) > limit) ++t->ksplit;
+    const int64_t ntl = N / (16 * t->rt);
+    while (ntl * t->ksplit < kTargetWG) {
+      int64_t nx = t->ksplit + 1;
+      while (nx <= chunks && chunks % nx) ++nx;
+      if (nx > chunks) break;
+      t->ksplit = (int)nx;
+    }
   }
+  t->nk = (int)(chunks / t->ksplit);
+  t->ntiles = (int)(N / (16 * t->rt));
+  t->mblocks = (int)((M + 16 * t->mt - 1) / (16 * t->mt));
+  if (req_tpw > 0) {
+    t->tpw = req_tpw;
+  } else {
+    const int64_t groups = std::max<int64_t>(1, kTargetWG / ((int64_t)t->ksplit * t->mblocks));
+    t->tpw = (int)std::max<int64_t>(1, (t->ntiles + groups - 1) / groups);
+  }
+  t->groups = (t->ntiles + t->tpw - 1) / t->tpw;
+  t->lds = lds_bytes(wfmt, t->mt, t->R, t->rt, t->nw, (int)(K / t->ksplit));
+  if (t->lds > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
+  if (t->groups > 0x7fffffff || t->ksplit > 65535 || t->mblocks > 65535) return ACORN_ERR_SHAPE;
   return ACORN_OK;
+}
+
+template <int WFMT, int RT, int MT, int UPW, int NW>
+void launch_one(const Tiling& t, const KArgs& a, hipStream_t st) {
+  auto kfn = wgemm_kernel<WFMT, RT, MT, UPW, NW>;
+  static bool lds_raised = false;  // once per instantiation, before any capture
+  if (!lds_raised && t.lds > 64 * 1024) {
+    (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    lds_raised = true;
+  }
+  dim3 grid((unsigned)t.groups, (unsigned)t.ksplit, (unsigned)t.mblocks), block(NW * kWave);
+  kfn<<<grid, block, t.lds, st>>>(a);
+}
+
+template <int WFMT, int RT, int MT, int UPW>
+int dispatch_nw(const Tiling& t, const KArgs& a, hipStream_t st) {
+  switch (t.nw) {
+    case 1: launch_one<WFMT, RT, MT, UPW, 1>(t, a, st); return ACORN_OK;
+    case 2: launch_one<WFMT, RT, MT, UPW, 2>(t, a, st); return ACORN_OK;
+    case 4: launch_one<WFMT, RT, MT, UPW, 4>(t, a, st); return ACORN_OK;
+    case 8:
+      if constexpr (MT == 1) {
+        launch_one<WFMT, RT, MT, UPW, 8>(t, a, st);
+        return ACORN_OK;
+      }
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+template <int WFMT, int RT, int MT>
+int dispatch_upw(const Tiling& t, const KArgs& a, hipStream_t st) {
+  switch (t.upw) {
+    case 2: return dispatch_nw<WFMT, RT, MT, 2>(t, a, st);
+    case 4: return dispatch_nw<WFMT, RT, MT, 4>(t, a, st);
+    case 8:
+      if constexpr (RT <= 2) return dispatch_nw<WFMT, RT, MT, 8>(t, a, st);
+      break;
+    case 16:
+      if constexpr (RT == 1 && MT == 1) return dispatch_nw<WFMT, RT, MT, 16>(t, a, st);
+      break;
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+template <int WFMT>
+int dispatch_tile(const Tiling& t, const KArgs& a, hipStream_t st) {
+  if (t.mt == 1) {
+    switch (t.rt) {
+      case 1: return dispatch_upw<WFMT, 1, 1>(t, a, st);
+      case 2: return dispatch_upw<WFMT, 2, 1>(t, a, st);
+      case 4: return dispatch_upw<WFMT, 4, 1>(t, a, st);
+    }
+  } else if (t.rt == 1) {
+    if (t.mt == 2) return dispatch_upw<WFMT, 1, 2>(t, a, st);
+    if (t.mt == 4) return dispatch_upw<WFMT, 1, 4>(t, a, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
 }
 
 }  // namespace
 
-extern "C" int acorn_gemm_plan(int64_t M, int64_t N, int64_t K, int wfmt, int want_partials,
-                               int* rt, int* nw, int* ksplit) {
-  Cfg c;
-  int w, ks, nch;
-  int rc = plan(M, N, K, wfmt, want_partials, &c, &w, &ks, &nch);
+extern "C" int acorn_gemm_plan(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg) {
+  if (!cfg) return ACORN_ERR_VALUE;
+  if (wfmt == ACORN_WFMT_F32) {
+    cfg[0] = 1; cfg[1] = 1; cfg[2] = 4; cfg[3] = cfg[3] > 0 ? cfg[3] : 1; cfg[4] = 1; cfg[5] = 0;
+    return ACORN_OK;
+  }
+  if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4)
+    return ACORN_ERR_DTYPE;
+  Tiling t;
+  const int rc = make_plan(M, N, K, wfmt, cfg, &t);
   if (rc) return rc;
-  if (rt) *rt = c.rt;
-  if (nw) *nw = w;
-  if (ksplit) *ksplit = ks;
+  cfg[0] = t.rt;
+  cfg[1] = t.upw;
+  cfg[2] = t.nw;
+  cfg[3] = t.ksplit;
+  cfg[4] = t.tpw;
+  cfg[5] = t.ntiles * t.mblocks;  // output tiles of the launch
   return ACORN_OK;
 }
 
 extern "C" int acorn_quant_gemm(const void* x, const void* w, const void* scale,
-                                const void* zero, void* out_bf16, float* out_part, int64_t M,
-                                int64_t N, int64_t K, int wfmt, int rt, int nw, int ksplit,
-                                void* stream) {
+                                const void* zero, void* out_bf16, float* part, int64_t M,
+                                int64_t N, int64_t K, int wfmt, const int* cfg, void* stream) {
   if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
       wfmt != ACORN_WFMT_F32)
     return ACORN_ERR_DTYPE;
   if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   if (M == 0) return ACORN_OK;
+  hipStream_t st = (hipStream_t)stream;
   if (wfmt == ACORN_WFMT_F32) {
-    // fp32 output always goes through out_part ([ksplit, M, N]).
-    if (!x || !w || !out_part) return ACORN_ERR_VALUE;
+    // fp32 output always goes through part ([ksplit, M, N]).
+    if (!x || !w || !part) return ACORN_ERR_VALUE;
     if (M > 65535 || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return ACORN_ERR_SHAPE;
-    const int ks = ksplit > 0 ? ksplit : 1;
+    const int ks = cfg && cfg[3] > 0 ? cfg[3] : 1;
     const int64_t kper = (K + ks - 1) / ks;
     dim3 grid((unsigned)((N + 3) / 4), (unsigned)ks), block(256);
-    f32_gemv_kernel<<<grid, block, 0, (hipStream_t)stream>>>(
-        (const float*)x, (const float*)w, out_part, (int)M, (int)N, (int)K, (int)kper);
+    f32_gemv_kernel<<<grid, block, 0, st>>>((const float*)x, (const float*)w, part, (int)M,
+                                            (int)N, (int)K, (int)kper);
     ACORN_LAUNCH_CHECK();
     return ACORN_OK;
   }
   if (!x || !w || (wfmt != ACORN_WFMT_BF16 && !scale)) return ACORN_ERR_VALUE;
-  if (!out_bf16 && !out_part) return ACORN_ERR_VALUE;
+  if (!out_bf16 && !part) return ACORN_ERR_VALUE;
   if (M > 65535 * 64 || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return ACORN_ERR_SHAPE;
-  Cfg c;
-  int pw, pks, pnch;
-  int rc = plan(M, N, K, wfmt, out_part != nullptr, &c, &pw, &pks, &pnch);
+  Tiling t;
+  int rc = make_plan(M, N, K, wfmt, cfg, &t);
   if (rc) return rc;
-  if (rt > 0) c.rt = rt;
-  if (nw > 0) pw = nw;
-  if (ksplit > 0) pks = ksplit;
-  if (!out_part && pks != 1) return ACORN_ERR_VALUE;
-  const int ku = ku_of(wfmt);
-  const int64_t rows = 16 * (int64_t)c.rt;
-  if (N % rows) return ACORN_ERR_SHAPE;
-  if (pw < 1 || pw > 4 || pks < 1) return ACORN_ERR_SHAPE;
-  // Fit (waves, units per wave) so that ksplit workgroups tile K exactly.
-  if (K % ((int64_t)ku * c.upw * pw * pks)) {
-    bool found = false;
-    for (int ww = pw; ww >= 1 && !found; --ww)
-      for (int u = c.upw; u >= 2 && !found; u /= 2)
-        if (K % ((int64_t)ku * u * ww * pks) == 0) {
-          pw = ww;
-          c.upw = u;
-          found = true;
-        }
-    if (!found) return ACORN_ERR_SHAPE;
-  }
-  const int64_t kc = (int64_t)ku * c.upw * pw;
-  const int64_t nchunk = K / (kc * pks);
-  const int R = c.mt == 1 ? (1 << ilog2_ceil((int)std::min<int64_t>(M, 16))) : 16;
-  const int log2R = ilog2_ceil(R);
-  const int groups_c = (int)(kc / 128);
-  size_t lds = (size_t)c.mt * (kc / 8) * R * 16;
-  if (wfmt == ACORN_WFMT_W4) lds += (size_t)groups_c * rows * 2 * 2;
-  const size_t red = (size_t)pw * c.rt * c.mt * 4 * kWave * 4;
-  lds = std::max(lds, red);
-  if (lds > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
-  const int64_t mblocks = (M + 16 * c.mt - 1) / (16 * c.mt);
-  dim3 grid((unsigned)(N / rows), (unsigned)pks, (unsigned)mblocks), block(kWave * pw);
-  hipStream_t st = (hipStream_t)stream;
+  // ksplit > 1 with a bf16 output needs the partials workspace
+  if (out_bf16 && t.ksplit > 1 && !part) return ACORN_ERR_VALUE;
+  KArgs a;
+  a.x = (const __bf16*)x;
+  a.w = (const uint8_t*)w;
+  a.scale = (const _Float16*)scale;
+  a.zero = (const _Float16*)zero;
+  a.out = t.ksplit == 1 ? (__bf16*)out_bf16 : nullptr;
+  a.part = part;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.nk = t.nk;
+  a.tpw = t.tpw;
+  a.ksplit = t.ksplit;
+  a.log2R = ilog2_ceil(t.R);
   switch (wfmt) {
-    case ACORN_WFMT_BF16: rc = dispatch_cfg<ACORN_WFMT_BF16>(c, grid, block, lds, st, x, w, scale, zero, out_bf16, out_part, (int)M, (int)N, (int)K, (int)nchunk, log2R); break;
-    case ACORN_WFMT_W8: rc = dispatch_cfg<ACORN_WFMT_W8>(c, grid, block, lds, st, x, w, scale, zero, out_bf16, out_part, (int)M, (int)N, (int)K, (int)nchunk, log2R); break;
-    case ACORN_WFMT_W4: rc = dispatch_cfg<ACORN_WFMT_W4>(c, grid, block, lds, st, x, w, scale, zero, out_bf16, out_part, (int)M, (int)N, (int)K, (int)nchunk, log2R); break;
+    case ACORN_WFMT_BF16: rc = dispatch_tile<ACORN_WFMT_BF16>(t, a, st); break;
+    case ACORN_WFMT_W8: rc = dispatch_tile<ACORN_WFMT_W8>(t, a, st); break;
+    case ACORN_WFMT_W4: rc = dispatch_tile<ACORN_WFMT_W4>(t, a, st); break;
   }
   if (rc) return rc;
   ACORN_LAUNCH_CHECK();
+  if (out_bf16 && t.ksplit > 1) {
+    const int64_t count = M * N;
+    splitk_reduce_kernel<__bf16><<<(unsigned)((count + 255) / 256), 256, 0, st>>>(
+        part, t.ksplit, (size_t)count, (__bf16*)out_bf16);
+    ACORN_LAUNCH_CHECK();
+  }
   return ACORN_OK;
 }
 

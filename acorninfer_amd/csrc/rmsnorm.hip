@@ -73,6 +73,86 @@ __global__ __launch_bounds__(kNT) void fused_add_rmsnorm_kernel(
   }
 }
 
+// Vectorised form for cols % 8 == 0 and cols <= 8 * kNT * kVMax: each thread
+// owns up to kVMax 8-element vectors of the row (16-byte loads for bf16),
+// issues every load of its vectors before using any, and keeps the rounded
+// residual in registers for the second pass.
+constexpr int kVMax = 4;
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
+  T t[8];
+  __builtin_memcpy(t, p, sizeof(t));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = to_f32(t[i]);
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
+  T t[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) t[i] = from_f32<T>(v[i]);
+  __builtin_memcpy(p, t, sizeof(t));
+}
+
+template <typename T, typename TW, bool HAS_RES, bool FROM_PART>
+__global__ __launch_bounds__(kNT) void fused_add_rmsnorm_vec_kernel(
+    const T* __restrict__ x, const float* __restrict__ part, int nsplit,
+    const T* __restrict__ res, T* __restrict__ res_out, const TW* __restrict__ w,
+    T* __restrict__ normed, T* __restrict__ x_out, int rows, int cols, float eps) {
+#pragma clang fp contract(off)
+  __shared__ float red[kNT / kWave];
+  const size_t base = (size_t)blockIdx.x * cols;
+  const size_t plane = (size_t)rows * cols;
+  const int nvec = cols / 8;
+  float v[kVMax][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kVMax; ++j) {
+    const int vi = threadIdx.x + j * kNT;
+    if (vi >= nvec) break;
+    const size_t off = base + (size_t)vi * 8;
+    float a[8];
+    if constexpr (FROM_PART) {
+      load8<float>(part + off, a);
+      for (int s = 1; s < nsplit; ++s) {
+        float b[8];
+        load8<float>(part + s * plane + off, b);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] += b[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = round_to<T>(a[i]);
+      if (x_out) store8<T>(x_out + off, a);
+    } else {
+      load8<T>(x + off, a);
+    }
+    if constexpr (HAS_RES) {
+      float r[8];
+      load8<T>(res + off, r);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = r[i] + a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[j][i] = round_to<T>(a[i]);
+      ss += v[j][i] * v[j][i];
+    }
+    store8<T>(res_out + off, v[j]);
+  }
+  ss = block_sum<kNT>(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
+#pragma unroll
+  for (int j = 0; j < kVMax; ++j) {
+    const int vi = threadIdx.x + j * kNT;
+    if (vi >= nvec) break;
+    float wv[8], o[8];
+    load8<TW>(w + (size_t)vi * 8, wv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (v[j][i] * inv) * wv[i];
+    store8<T>(normed + base + (size_t)vi * 8, o);
+  }
+}
+
 template <typename T, typename TW>
 int launch_k1(const void* x, const float* part, int nsplit, const void* res, void* res_out,
               const void* w, void* normed, void* x_out, int64_t rows, int64_t cols, float eps,
@@ -84,21 +164,28 @@ int launch_k1(const void* x, const float* part, int nsplit, const void* res, voi
   const TW* wp = (const TW*)w;
   T* np = (T*)normed;
   T* xo = (T*)x_out;
-  if (part) {
-    if (res)
-      fused_add_rmsnorm_kernel<T, TW, true, true><<<grid, block, 0, st>>>(
-          xp, part, nsplit, rp, rop, wp, np, xo, (int)rows, (int)cols, eps);
-    else
-      fused_add_rmsnorm_kernel<T, TW, false, true><<<grid, block, 0, st>>>(
-          xp, part, nsplit, rp, rop, wp, np, xo, (int)rows, (int)cols, eps);
+  const bool vec = cols % 8 == 0 && cols <= 8 * kNT * kVMax;
+#define ACORN_K1(KERNEL, RES, PART)                                                        \
+  KERNEL<T, TW, RES, PART><<<grid, block, 0, st>>>(xp, part, nsplit, rp, rop, wp, np, xo, \
+                                                   (int)rows, (int)cols, eps)
+  if (vec) {
+    if (part) {
+      if (res) ACORN_K1(fused_add_rmsnorm_vec_kernel, true, true);
+      else ACORN_K1(fused_add_rmsnorm_vec_kernel, false, true);
+    } else {
+      if (res) ACORN_K1(fused_add_rmsnorm_vec_kernel, true, false);
+      else ACORN_K1(fused_add_rmsnorm_vec_kernel, false, false);
+    }
   } else {
-    if (res)
-      fused_add_rmsnorm_kernel<T, TW, true, false><<<grid, block, 0, st>>>(
-          xp, part, nsplit, rp, rop, wp, np, xo, (int)rows, (int)cols, eps);
-    else
-      fused_add_rmsnorm_kernel<T, TW, false, false><<<grid, block, 0, st>>>(
-          xp, part, nsplit, rp, rop, wp, np, xo, (int)rows, (int)cols, eps);
+    if (part) {
+      if (res) ACORN_K1(fused_add_rmsnorm_kernel, true, true);
+      else ACORN_K1(fused_add_rmsnorm_kernel, false, true);
+    } else {
+      if (res) ACORN_K1(fused_add_rmsnorm_kernel, true, false);
+      else ACORN_K1(fused_add_rmsnorm_kernel, false, false);
+    }
   }
+#undef ACORN_K1
   ACORN_LAUNCH_CHECK();
   return ACORN_OK;
 }

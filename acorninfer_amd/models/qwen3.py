@@ -92,22 +92,22 @@ class QLinear:
                 n += t.numel() * t.element_size()
         return n
 
-    def plan(self, M: int, partials: bool) -> tuple[int, int, int]:
-        rt, nw, ks = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-        rc = lib().acorn_gemm_plan(M, self.N, self.K, self.fmt, int(partials),
-                                   ctypes.byref(rt), ctypes.byref(nw), ctypes.byref(ks))
-        check(rc, "gemm_plan")
-        return rt.value, nw.value, ks.value
+    def plan(self, M: int, tiling=None):
+        """(Tiling, output tiles) from the library planner."""
+        from acorninfer_amd.ops.quant_gemm import plan
+        return plan(M, self.N, self.K, self.fmt, tiling)
 
-    def launch(self, x: torch.Tensor, M: int, cfg: tuple[int, int, int], *,
-               out: torch.Tensor | None = None, part: torch.Tensor | None = None,
-               stream: int) -> None:
-        rt, nw, ks = cfg
-        if self.fmt == _lib.WFMT_F32 and part is None:
-            part = out      # fp32 results come back through the partials pointer
+    def launch(self, x: torch.Tensor, M: int, tiling, *, out: torch.Tensor | None = None,
+               part: torch.Tensor | None = None, stream: int) -> None:
+        """out given: bf16 [M, N] (part is the split-K workspace when
+        tiling.ksplit > 1); out None: fp32 partials [ksplit, M, N] into part.
+        fp32 weights always write fp32 through part."""
+        if self.fmt == _lib.WFMT_F32:
+            part, out = (out if part is None else part), None
+        arr = (ctypes.c_int * 6)(*tiling, 0)
         rc = lib().acorn_quant_gemm(ptr(x), ptr(self.w), ptr(self.scale), ptr(self.zero),
-                                    None if part is not None else ptr(out), ptr(part),
-                                    M, self.N, self.K, self.fmt, rt, nw, ks, stream)
+                                    ptr(out), ptr(part), M, self.N, self.K, self.fmt, arr,
+                                    stream)
         check(rc, "quant_gemm")
 
 
@@ -189,6 +189,8 @@ class Qwen3DecodeModel:
         # Switches with the reference's names (qwen3.py:487-489).
         self.attention_backend = "hip"
         self.fused_ops = True
+        # batch -> {projection name -> Tiling}, filled by tune()
+        self.tilings: dict[int, dict] = {}
 
     # ---------------------------------------------------------------- building --
     @classmethod
@@ -259,9 +261,10 @@ class Qwen3DecodeModel:
         return n
 
     # ------------------------------------------------------------------ decode --
-    def buffers(self, batch: int, max_pages: int, num_splits: int | None = None
-                ) -> "StepBuffers":
-        return StepBuffers(self, batch, max_pages, num_splits)
+    def buffers(self, batch: int, max_pages: int, num_splits: int | None = None,
+                tilings: dict | None = None) -> "StepBuffers":
+        return StepBuffers(self, batch, max_pages, num_splits,
+                           tilings if tilings is not None else self.tilings.get(batch))
 
     def step(self, buf: "StepBuffers", k_pool: torch.Tensor, v_pool: torch.Tensor,
              num_blocks: int, page_size: int) -> None:
@@ -287,26 +290,24 @@ class Qwen3DecodeModel:
 
         check(L.acorn_embedding(ptr(self.embed), ptr(buf.ids), ptr(buf.x), B, cfg.vocab_size, H,
                                 dt, st), "embedding")
-        res_in = None           # residual stream; None before layer 0's K1
-        prev_part, prev_ks = None, 0
+        prev_ks = 0             # splits of the previous layer's down-projection partials
         for li, lw in enumerate(self.layers):
-            # K1: input norm (layer 0 from the embedding, later layers fuse
-            # the previous down projection's split-K reduce + residual add).
-            if prev_part is None:
+            # K1: input norm (layer 0 from the embedding; later layers reduce
+            # the previous down projection's partials and add the residual)
+            if prev_ks == 0:
                 check(L.acorn_fused_add_rmsnorm(ptr(buf.x), None, ptr(buf.res), ptr(lw.input_norm),
                                                 ptr(buf.normed), B, H, eps, dt, wdt, st), "K1")
             else:
                 check(L.acorn_fused_add_rmsnorm_partials(
-                    ptr(prev_part), prev_ks, ptr(res_in), ptr(buf.res), ptr(lw.input_norm),
+                    ptr(buf.part_down), prev_ks, ptr(buf.res), ptr(buf.res), ptr(lw.input_norm),
                     ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
-            res_in = buf.res
-            # qkv projection -> partials -> K2 epilogue (+ KV scatter)
+            # qkv projection -> fp32 partials -> K2 epilogue (+ KV scatter)
             cq = buf.cfgs["qkv"]
             lw.qkv.launch(buf.normed, B, cq, part=buf.part_qkv, stream=st)
             kp = kbase + li * layer_elems * esz
             vp = vbase + li * layer_elems * esz
             check(L.acorn_qkv_epilogue(
-                ptr(buf.part_qkv), cq[2], ptr(buf.q), kp, vp, ptr(buf.pages), ptr(buf.slots),
+                ptr(buf.part_qkv), cq.ksplit, ptr(buf.q), kp, vp, ptr(buf.pages), ptr(buf.slots),
                 B, nq, nkv, D, page_size, num_blocks, ptr(lw.q_norm), ptr(lw.k_norm), eps,
                 ptr(buf.positions), ptr(self.inv_freq), dt, wdt, st), "qkv_epilogue")
             # K3
@@ -314,27 +315,89 @@ class Qwen3DecodeModel:
                 ptr(buf.q), kp, vp, ptr(buf.tables), ptr(buf.lens), ptr(buf.attn),
                 ptr(buf.ws_acc), ptr(buf.ws_ml), B, nq, nkv, D, page_size, num_blocks,
                 buf.max_pages, buf.num_splits, float(self.scale), dt, st), "K3")
-            # o projection -> K1 (reduce + residual + post-attention norm)
+            # o projection -> K1 (reduce + residual add + post-attention norm)
             co = buf.cfgs["o"]
             lw.o.launch(buf.attn, B, co, part=buf.part_o, stream=st)
             check(L.acorn_fused_add_rmsnorm_partials(
-                ptr(buf.part_o), co[2], ptr(buf.res), ptr(buf.res), ptr(lw.post_norm),
+                ptr(buf.part_o), co.ksplit, ptr(buf.res), ptr(buf.res), ptr(lw.post_norm),
                 ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
-            # MLP
+            # MLP: gate|up partials -> SwiGLU -> down partials
             cg = buf.cfgs["gate_up"]
             lw.gate_up.launch(buf.normed, B, cg, part=buf.part_gu, stream=st)
-            check(L.acorn_silu_mul(ptr(buf.part_gu), cg[2], None, ptr(buf.act), B, inter, dt, st),
-                  "silu_mul")
+            check(L.acorn_silu_mul(ptr(buf.part_gu), cg.ksplit, None, ptr(buf.act), B, inter, dt,
+                                   st), "silu_mul")
             cd = buf.cfgs["down"]
             lw.down.launch(buf.act, B, cd, part=buf.part_down, stream=st)
-            prev_part, prev_ks = buf.part_down, cd[2]
-        # final norm (reduce + residual) -> lm_head -> greedy
+            prev_ks = cd.ksplit
+        # final norm (reduce + residual add) -> lm_head -> greedy
         check(L.acorn_fused_add_rmsnorm_partials(
-            ptr(prev_part), prev_ks, ptr(res_in), ptr(buf.res), ptr(self.norm), ptr(buf.normed),
-            None, B, H, eps, dt, wdt, st), "K1")
-        self.lm_head.launch(buf.normed, B, buf.cfgs["lm_head"], out=buf.logits, stream=st)
+            ptr(buf.part_down), prev_ks, ptr(buf.res), ptr(buf.res), ptr(self.norm),
+            ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
+        self.lm_head.launch(buf.normed, B, buf.cfgs["lm_head"], out=buf.logits,
+                            part=buf.ws_lm, stream=st)
         check(L.acorn_argmax(ptr(buf.logits), B, cfg.vocab_size, ptr(buf.next_ids),
                              dtype_code(buf.logits), st), "argmax")
+
+    def projections(self) -> dict[str, list[QLinear]]:
+        """Each projection of the step with its per-layer weights."""
+        return {"qkv": [L.qkv for L in self.layers], "o": [L.o for L in self.layers],
+                "gate_up": [L.gate_up for L in self.layers],
+                "down": [L.down for L in self.layers], "lm_head": [self.lm_head]}
+
+    def time_projection(self, lins: list[QLinear], M: int, tiling, reps: int = 3) -> float:
+        """Average µs of one launch of `tiling`, measured as a hipGraph of one
+        launch per weight in `lins` (distinct weights, so the 256 MB MALL does
+        not hold them between launches) on a private stream with HIP events."""
+        from acorninfer_amd.ops.quant_gemm import _native_cfg
+        t = lins[0].plan(M, _native_cfg(tiling, M))[0]
+        lin0 = lins[0]
+        x = torch.randn(M, lin0.K, device=self.device).to(self.dtype)
+        part = torch.empty(t.ksplit, M, lin0.N, dtype=torch.float32, device=self.device)
+        s = torch.cuda.Stream(self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            def body():
+                for lin in lins:
+                    lin.launch(x, M, t, part=part, stream=s.cuda_stream)
+            body()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                body()
+            g.replay()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(reps):
+                g.replay()
+            e1.record(s)
+        e1.synchronize()
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        return e0.elapsed_time(e1) * 1e3 / (reps * len(lins))
+
+    def tune(self, batch: int, *, names=None, verbose: bool = False) -> dict:
+        """Load-time tiling choice for a decode bucket (the reference's
+        quant_gemm.configure, acorninfer/ops/quant_gemm.py:449-492): every
+        candidate tiling of each projection is timed in place and the fastest
+        is kept in self.tilings[batch]; run before any graph capture."""
+        from acorninfer_amd.ops.quant_gemm import candidates
+        if self.lm_head.fmt == _lib.WFMT_F32:
+            return {}
+        report = {}
+        chosen = self.tilings.setdefault(batch, {})
+        for name, lins in self.projections().items():
+            if names is not None and name not in names:
+                continue
+            best = None
+            for c in candidates(batch, lins[0].N, lins[0].K, lins[0].fmt):
+                us = self.time_projection(lins, batch, c)
+                if verbose:
+                    print(f"TUNE {name} M={batch} {tuple(c)} {us:.2f} us", flush=True)
+                if best is None or us < best[0]:
+                    best = (us, c)
+            chosen[name] = best[1]
+            report[name] = {"tiling": tuple(best[1]), "us": round(best[0], 3),
+                            "bytes": lins[0].nbytes()}
+        return report
 
     # Reference-shaped entry point (qwen3.py:520-595).
     def forward_decode(self, input_ids: torch.Tensor, views, *, prepared=None) -> torch.Tensor:
@@ -396,6 +459,7 @@ class StepBuffers:
     batch: int
     max_pages: int
     num_splits: int | None = None
+    tilings: dict | None = None       # name -> requested Tiling (0 fields = planner)
     cfgs: dict = field(default_factory=dict)
 
     def __post_init__(self):
@@ -407,10 +471,10 @@ class StepBuffers:
         if self.num_splits is None:
             self.num_splits = attention_splits(B, nkv)
         lw = m.layers[0]
+        tilings = self.tilings or {}
         for name, lin in (("qkv", lw.qkv), ("o", lw.o), ("gate_up", lw.gate_up),
-                          ("down", lw.down)):
-            self.cfgs[name] = lin.plan(B, partials=True)
-        self.cfgs["lm_head"] = m.lm_head.plan(B, partials=False)
+                          ("down", lw.down), ("lm_head", m.lm_head)):
+            self.cfgs[name] = lin.plan(B, tilings.get(name))[0]
         # int64 block: ids | positions | pages | slots | next_ids ; int32 block: lens | tables
         self.flat_i64 = torch.zeros(5 * B, dtype=torch.int64, device=dev)
         self.flat_i32 = torch.zeros(B * (1 + self.max_pages), dtype=torch.int32, device=dev)
@@ -434,10 +498,12 @@ class StepBuffers:
         self.q = z(B, nq, D)
         self.attn = z(B, nq * D)
         self.act = z(B, inter)
-        self.part_qkv = z(self.cfgs["qkv"][2], B, (nq + 2 * nkv) * D, dtype=f32)
-        self.part_o = z(self.cfgs["o"][2], B, H, dtype=f32)
-        self.part_gu = z(self.cfgs["gate_up"][2], B, 2 * inter, dtype=f32)
-        self.part_down = z(self.cfgs["down"][2], B, H, dtype=f32)
+        self.part_qkv = z(self.cfgs["qkv"].ksplit, B, (nq + 2 * nkv) * D, dtype=f32)
+        self.part_o = z(self.cfgs["o"].ksplit, B, H, dtype=f32)
+        self.part_gu = z(self.cfgs["gate_up"].ksplit, B, 2 * inter, dtype=f32)
+        self.part_down = z(self.cfgs["down"].ksplit, B, H, dtype=f32)
+        ks_lm = self.cfgs["lm_head"].ksplit
+        self.ws_lm = z(ks_lm, B, cfg.vocab_size, dtype=f32) if ks_lm > 1 else None
         S = self.num_splits
         self.ws_acc = z(B * nq * S * D, dtype=f32)
         self.ws_ml = z(2 * B * nq * S, dtype=f32)

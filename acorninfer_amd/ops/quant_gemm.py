@@ -7,15 +7,17 @@ New next to them (no reference counterpart in production): `quant_gemm_w4`
 for packed int4 group-128 weights, and `gemm_partials`, the decode-step form
 that leaves fp32 split-K partials for the consumer kernel to reduce.
 
-All formats run on one MFMA kernel (csrc/quant_gemm.hip). A tiling is
-(rt, nw, ksplit): 16*rt weight rows per wavefront, nw wavefronts per
-workgroup along K, ksplit workgroups along K. The reference's 5-tuple configs
-are accepted for compatibility; only their SPLIT_K field carries over.
+All formats run on one MFMA kernel (csrc/quant_gemm.hip); a tiling is a
+`Tiling` (rt, upw, nw, ksplit, tpw). The reference's 5-tuple configs are
+accepted for compatibility; only their SPLIT_K field carries over. With
+ksplit > 1 and a bf16 output the partials go through an address-stable
+workspace (`_workspace`) and are summed in split order by a second launch.
 """
 from __future__ import annotations
 
 import ctypes
 import time
+from typing import NamedTuple
 
 import torch
 
@@ -42,8 +44,8 @@ M_BUCKETS_LARGE = ("s", "m", "l")
 _M_REP_M = {"s": 64, "m": 256, "l": 1024}
 
 _state: dict = {
-    "configs": {},     # cls -> (rt, nw, ksplit)   decode bucket (M <= 16)
-    "m_configs": {},   # cls -> {bucket: (rt, nw, ksplit)}
+    "configs": {},     # cls -> Tiling   decode bucket (M <= 16)
+    "m_configs": {},   # cls -> {bucket: Tiling}
     "shapes": {},      # cls -> (N, K)
     "workspaces": {},  # (rows, N, ksplit) -> fp32 [ksplit, rows, N]
     "device": None,
@@ -62,34 +64,53 @@ def bucket_for(M: int) -> str:
     return "l"
 
 
-def plan(M: int, N: int, K: int, wfmt: int, *, partials: bool) -> tuple[int, int, int]:
-    """Default (rt, nw, ksplit) from the library's planner."""
-    rt, nw, ks = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    rc = lib().acorn_gemm_plan(M, N, K, wfmt, int(partials), ctypes.byref(rt),
-                               ctypes.byref(nw), ctypes.byref(ks))
-    check(rc, "gemm_plan")
-    return rt.value, nw.value, ks.value
+class Tiling(NamedTuple):
+    """Native tiling of acorn_quant_gemm; 0 = planner's choice.
+
+    rt: 16-row weight tiles per wavefront row block; upw: 16-byte weight
+    loads per lane per pipeline step; nw: wavefronts per workgroup (they
+    split K); ksplit: workgroups along K; tpw: row tiles per workgroup.
+    """
+    rt: int = 0
+    upw: int = 0
+    nw: int = 0
+    ksplit: int = 0
+    tpw: int = 0
 
 
-def _native_cfg(cfg, M: int) -> tuple[int, int, int] | None:
-    """(rt, nw, ksplit) from an explicit cfg. 0 means "planner default".
+def plan(M: int, N: int, K: int, wfmt: int, cfg: Tiling | None = None
+         ) -> tuple[Tiling, int]:
+    """The library planner's full choice for (M, N, K, format), honouring the
+    non-zero fields of `cfg`. Returns (tiling, output tiles of the launch)."""
+    arr = (ctypes.c_int * 6)(*(tuple(cfg) if cfg is not None else (0,) * 5), 0)
+    check(lib().acorn_gemm_plan(M, N, K, wfmt, arr), "gemm_plan")
+    return Tiling(*arr[:5]), arr[5]
 
-    A reference 5-tuple is read by M regime as the reference does: for
-    M <= 16 it is (BN, BK, warps, stages, SPLIT_K) and SPLIT_K carries over;
-    for M > 16 it is (BM, BN, BK, warps, stages) and nothing carries over
-    (this kernel picks its own M tiling).
+
+def _native_cfg(cfg, M: int) -> Tiling | None:
+    """A native Tiling from an explicit cfg.
+
+    Accepted: a Tiling; a 3-tuple (rt, nw, ksplit); or the reference's
+    5-tuple, read by M regime as the reference does: for M <= 16 it is
+    (BN, BK, warps, stages, SPLIT_K) and SPLIT_K carries over; for M > 16 it
+    is (BM, BN, BK, warps, stages) and nothing carries over (this kernel picks
+    its own M tiling).
     """
     if cfg is None:
         return None
+    if isinstance(cfg, Tiling):
+        return cfg
     cfg = tuple(int(c) for c in cfg)
     if len(cfg) == 3:
-        return cfg
+        return Tiling(rt=cfg[0], nw=cfg[1], ksplit=cfg[2])
     if len(cfg) == 5:
-        return (0, 0, cfg[4]) if M <= DECODE_M_MAX else (0, 0, 1)
-    raise ValueError(f"quant_gemm cfg must be (rt, nw, ksplit) or a reference 5-tuple: {cfg}")
+        return Tiling(ksplit=cfg[4]) if M <= DECODE_M_MAX else Tiling()
+    raise ValueError(f"quant_gemm cfg must be a Tiling, (rt, nw, ksplit) or a reference "
+                     f"5-tuple: {cfg}")
 
 
 def _workspace(rows: int, N: int, ksplit: int, device) -> torch.Tensor:
+    """Address-stable fp32 split-K workspace [ksplit, rows, N]."""
     key = (rows, N, ksplit, str(device))
     ws = _state["workspaces"].get(key)
     if ws is None:
@@ -99,24 +120,17 @@ def _workspace(rows: int, N: int, ksplit: int, device) -> torch.Tensor:
 
 
 def _launch(x2: torch.Tensor, w: torch.Tensor, scale, zero, wfmt: int, N: int,
-            cfg: tuple[int, int, int] | None, out: torch.Tensor | None) -> torch.Tensor:
+            cfg: Tiling | None, out: torch.Tensor | None) -> torch.Tensor:
     M, K = x2.shape
     if out is None:
         out = torch.empty(M, N, dtype=torch.bfloat16, device=x2.device)
     assert out.shape == (M, N) and out.dtype == torch.bfloat16 and out.is_contiguous()
-    rt, nw, ks = cfg if cfg is not None else (0, 0, 1)
-    st = stream_ptr(x2.device)
-    if ks <= 1:
-        rc = lib().acorn_quant_gemm(ptr(x2), ptr(w), ptr(scale), ptr(zero), ptr(out), None,
-                                    M, N, K, wfmt, rt, nw, 1, st)
-        check(rc, "quant_gemm")
-        return out
-    part = _workspace(M, N, ks, x2.device)
-    rc = lib().acorn_quant_gemm(ptr(x2), ptr(w), ptr(scale), ptr(zero), None, ptr(part),
-                                M, N, K, wfmt, rt, nw, ks, st)
+    tiling, _ = plan(M, N, K, wfmt, _native_cfg(cfg, M))
+    part = _workspace(M, N, tiling.ksplit, x2.device) if tiling.ksplit > 1 else None
+    arr = (ctypes.c_int * 6)(*tiling, 0)
+    rc = lib().acorn_quant_gemm(ptr(x2), ptr(w), ptr(scale), ptr(zero), ptr(out), ptr(part),
+                                M, N, K, wfmt, arr, stream_ptr(x2.device))
     check(rc, "quant_gemm")
-    rc = lib().acorn_splitk_reduce(ptr(part), ks, M * N, ptr(out), BF16, st)
-    check(rc, "splitk_reduce")
     return out
 
 
@@ -204,16 +218,17 @@ def bf16_gemm(x: torch.Tensor, w: torch.Tensor, cls=None, cfg=None,
 
 
 def gemm_partials(x2: torch.Tensor, w: torch.Tensor, scale, zero, wfmt: int,
-                  part: torch.Tensor, cfg: tuple[int, int, int]) -> None:
+                  part: torch.Tensor, cfg) -> None:
     """Decode-step form: write fp32 split-K partials part[ksplit, M, N]; the
     consumer kernel sums them (in split order) and applies the output cast."""
     M, K = x2.shape
     ks, Mp, N = part.shape
     assert Mp == M and part.dtype == torch.float32 and part.is_contiguous()
-    rt, nw, ks_cfg = cfg
-    assert ks_cfg == ks
+    tiling, _ = plan(M, N, K, wfmt, _native_cfg(cfg, M))
+    assert tiling.ksplit == ks, f"partials buffer has {ks} splits, tiling wants {tiling.ksplit}"
+    arr = (ctypes.c_int * 6)(*tiling, 0)
     rc = lib().acorn_quant_gemm(ptr(x2), ptr(w), ptr(scale), ptr(zero), None, ptr(part),
-                                M, N, K, wfmt, rt, nw, ks, stream_ptr(x2.device))
+                                M, N, K, wfmt, arr, stream_ptr(x2.device))
     check(rc, "quant_gemm(partials)")
 
 
@@ -232,13 +247,36 @@ def _time_cfg(fn, reps: int = 20) -> float:
     return start.elapsed_time(end) * 1e3 / reps
 
 
+def candidates(M: int, N: int, K: int, wfmt: int) -> list[Tiling]:
+    """The planner's default plus a neighbourhood of valid tilings (distinct
+    full choices only) for a load-time sweep."""
+    seen, out = set(), []
+    base, _ = plan(M, N, K, wfmt)
+    reqs = [Tiling()]
+    for rt in (1, 2, 4):
+        for upw in (2, 4, 8, 16):
+            for nw in (2, 4, 8):
+                for ks in (0, 1, 2, 3, 4):
+                    reqs.append(Tiling(rt, upw, nw, ks, 0))
+    for r in reqs:
+        try:
+            t, _ = plan(M, N, K, wfmt, r)
+        except (AssertionError, ValueError, NotImplementedError):
+            continue
+        if t not in seen:
+            seen.add(t)
+            out.append(t)
+    out.sort(key=lambda t: t != base)
+    return out
+
+
 def configure(classes=None, *, device="cuda:0", verbose=True, wfmt: int = WFMT_W8) -> dict:
     """Load-time tiling choice per class (before any graph capture).
 
-    For each class: the planner's default plus a small split-K neighbourhood
-    timed on random weights rotated over 4 sets (to defeat the 256 MB MALL);
-    the fastest becomes the decode (M <= 16) entry. Large-M buckets take the
-    planner default for their representative M.
+    For each class: the planner's default and its neighbourhood
+    (`candidates`), timed at M=8 on random weights rotated over 4 sets (to
+    defeat the 256 MB MALL); the fastest becomes the decode (M <= 16) entry.
+    Large-M buckets take the planner default for their representative M.
     """
     reset()
     classes = CLASSES if classes is None else dict(classes)
@@ -258,26 +296,22 @@ def configure(classes=None, *, device="cuda:0", verbose=True, wfmt: int = WFMT_W
         else:
             sets = [(torch.randn(n, k, device=device).bfloat16(), None, None) for _ in range(4)]
         x = torch.randn(8, k, device=device).bfloat16()
-        base = plan(8, n, k, wfmt, partials=False)
-        cands = {base}
-        for ks in (2, 3, 4):
-            cands.add((base[0], 0, ks))
         best = None
-        for c in sorted(cands):
+        for c in candidates(8, n, k, wfmt):
             def run(c=c):
-                for w, s, z in sets:
-                    _launch(x, w, s, z, wfmt, n, c, None)
+                for w, sc, z in sets:
+                    _launch(x, w, sc, z, wfmt, n, c, None)
             try:
                 us = _time_cfg(run) / len(sets)
             except (AssertionError, ValueError, NotImplementedError):
                 continue
             if verbose:
-                print(f"GEMM AUTOTUNE {cls} cfg={c} us={us:.2f}", flush=True)
+                print(f"GEMM AUTOTUNE {cls} cfg={tuple(c)} us={us:.2f}", flush=True)
             if best is None or us < best[0]:
                 best = (us, c)
         _state["configs"][cls] = best[1]
         _state["m_configs"][cls] = {
-            b: plan(_M_REP_M[b], n, k, wfmt, partials=False) for b in M_BUCKETS_LARGE}
+            b: plan(_M_REP_M[b], n, k, wfmt)[0] for b in M_BUCKETS_LARGE}
         report["classes"][cls] = {"config": best[1], "us": best[0],
                                   "autotune_s": time.perf_counter() - t1}
         del sets

@@ -45,7 +45,8 @@ def _gemm_bytes(lin, M: int) -> int:
     return lin.nbytes() + 2 * M * lin.K + 2 * M * lin.N
 
 
-def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int, seed: int):
+def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int, seed: int,
+                   tune: bool = True):
     import torch
 
     from acorninfer_amd.cache.pager import BlockAllocator, PagedCacheView, PagedKVCache
@@ -57,6 +58,12 @@ def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int,
     torch.cuda.synchronize()
     _log(f"model {fmt}: {model.weight_bytes() / 1e9:.3f} GB weights in "
          f"{time.perf_counter() - t0:.1f} s")
+    if tune:
+        t0 = time.perf_counter()
+        report = model.tune(batch)
+        _log(f"tuned C={batch} in {time.perf_counter() - t0:.1f} s: " + ", ".join(
+            f"{k} {v['tiling']} {v['us']:.1f}us {v['bytes'] / v['us'] / 1e3:.0f}GB/s"
+            for k, v in report.items()))
     P = 16
     max_len = prompt_len + total_steps + 1
     per_seq = -(-max_len // P)
@@ -102,17 +109,19 @@ def gemm_roofline(model, runner, batch: int, reps: int = 5):
     s = torch.cuda.Stream()
     launches = []
     for lw in model.layers:
-        launches += [(lw.qkv, buf.normed, buf.cfgs["qkv"], None, buf.part_qkv),
-                     (lw.o, buf.attn, buf.cfgs["o"], None, buf.part_o),
-                     (lw.gate_up, buf.normed, buf.cfgs["gate_up"], None, buf.part_gu),
-                     (lw.down, buf.act, buf.cfgs["down"], None, buf.part_down)]
-    launches.append((model.lm_head, buf.normed, buf.cfgs["lm_head"], buf.logits, None))
-    nbytes = sum(_gemm_bytes(lin, batch) for lin, *_ in launches)
+        launches += [("qkv", lw.qkv, buf.normed, buf.part_qkv), ("o", lw.o, buf.attn, buf.part_o),
+                     ("gate_up", lw.gate_up, buf.normed, buf.part_gu),
+                     ("down", lw.down, buf.act, buf.part_down)]
+    launches.append(("lm_head", model.lm_head, buf.normed, None))
+    nbytes = sum(_gemm_bytes(lin, batch) for _, lin, *_ in launches)
 
     def body():
         sp = s.cuda_stream
-        for lin, x, cfg, out, part in launches:
-            lin.launch(x, batch, cfg, out=out, part=part, stream=sp)
+        for name, lin, x, part in launches:
+            if part is None:
+                lin.launch(x, batch, buf.cfgs[name], out=buf.logits, part=buf.ws_lm, stream=sp)
+            else:
+                lin.launch(x, batch, buf.cfgs[name], part=part, stream=sp)
 
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -189,6 +198,7 @@ def main() -> None:
     ap.add_argument("--extra", action="store_true",
                     help="also measure C=1 and the W4A16 model (reported under 'extra')")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-tune", action="store_true", help="use the planner's default tilings")
     ap.add_argument("--seed", type=int, default=20261027)
     args = ap.parse_args()
 
@@ -206,7 +216,8 @@ def main() -> None:
         cfg = cfg.with_layers(args.layers)
     total = args.warmup + args.steps
     model, cache, runner, views, first = build_workload(cfg, args.format, args.batch,
-                                                        args.prompt_len, total, args.seed)
+                                                        args.prompt_len, total, args.seed,
+                                                        tune=not args.no_tune)
     _log(f"graph captured for C={args.batch}; warmup {args.warmup}, timed {args.steps}")
     dt, log = time_decode(runner, views, first, args.steps, args.warmup)
     tok_s = args.batch * args.steps / dt
@@ -224,7 +235,8 @@ def main() -> None:
         del model, cache, runner
         torch.cuda.empty_cache()
         for fmt, c in (("bf16", 1), ("w4a16", 8), ("w4a16", 1)):
-            m2, c2, r2, v2, f2 = build_workload(cfg, fmt, c, args.prompt_len, total, args.seed)
+            m2, c2, r2, v2, f2 = build_workload(cfg, fmt, c, args.prompt_len, total, args.seed,
+                                                tune=not args.no_tune)
             dt2, _ = time_decode(r2, v2, f2, args.steps, args.warmup)
             extra[f"{fmt}_C{c}_tok_s"] = round(c * args.steps / dt2, 2)
             extra[f"{fmt}_C{c}_ms_per_step"] = round(dt2 * 1e3 / args.steps, 4)

@@ -139,23 +139,31 @@ int acorn_paged_attention(const void* q, const void* k_pages, const void* v_page
  *   wfmt ACORN_WFMT_W8  : w int8 [N,K], scale fp16 [N]
  *   wfmt ACORN_WFMT_W4  : w uint8 [N,K/2], scale fp16 [N,K/128], zero fp16
  *                         [N,K/128] or NULL (symmetric, zero = -8*scale)
- *   wfmt ACORN_WFMT_F32 : w fp32 [N,K], x fp32 [M,K]; fp32 result in out_part
- * out_bf16 != NULL: writes bf16 [M,N] (requires ksplit == 1).
- * out_part != NULL: writes fp32 partials [ksplit, M, N] (out_bf16 ignored).
- * Tiling: rows_per_wave = 16*rt, waves (along K) = nw, K per workgroup =
- * K / ksplit. See acorn_gemm_plan for a default choice.
+ *   wfmt ACORN_WFMT_F32 : w fp32 [N,K], x fp32 [M,K]; fp32 result in part
+ * cfg: NULL or int[6] {rt, upw, nw, ksplit, tpw, -}; 0 entries are chosen by
+ * the planner (acorn_gemm_plan). With the chosen ksplit:
+ *   out_bf16 != NULL, ksplit == 1: writes bf16 [M,N];
+ *   out_bf16 != NULL, ksplit > 1 : part is an fp32 workspace [ksplit,M,N]; a
+ *       second launch sums the partials in split order into out_bf16
+ *       (bitwise deterministic);
+ *   out_bf16 == NULL             : writes fp32 partials part[ksplit,M,N].
  */
 int acorn_quant_gemm(const void* x, const void* w, const void* scale, const void* zero,
-                     void* out_bf16, float* out_part, int64_t M, int64_t N, int64_t K,
-                     int wfmt, int rt, int nw, int ksplit, void* stream);
+                     void* out_bf16, float* part, int64_t M, int64_t N, int64_t K, int wfmt,
+                     const int* cfg, void* stream);
 
 /* Deterministic split-K reduction: out[M*N] = round_T(sum_s part[s, M*N]). */
 int acorn_splitk_reduce(const float* part, int64_t nsplit, int64_t count, void* out,
                         int dtype, void* stream);
 
-/* Default tiling for acorn_quant_gemm on this device: writes rt, nw, ksplit. */
-int acorn_gemm_plan(int64_t M, int64_t N, int64_t K, int wfmt, int want_partials, int* rt,
-                    int* nw, int* ksplit);
+/*
+ * Tiling for acorn_quant_gemm: cfg[0..4] hold requests (0 = choose) and are
+ * overwritten with the full choice {rt: 16-row tiles per wavefront row block,
+ * upw: 16-byte weight loads per lane per step, nw: wavefronts per workgroup,
+ * ksplit: K splits, tpw: tiles per workgroup}; cfg[5] receives the number of
+ * output tiles. No GPU access.
+ */
+int acorn_gemm_plan(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg);
 
 /*
  * Embedding row gather: out[b, :] = table[ids[b], :].

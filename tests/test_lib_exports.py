@@ -38,12 +38,10 @@ def test_binding_table_matches_header():
 def test_version_and_plan_need_no_gpu():
     lib = _lib.lib()
     assert lib.acorn_version() >= 1
-    rt, nw, ks = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    rc = lib.acorn_gemm_plan(8, 4096, 12288, _lib.WFMT_W4, 1, ctypes.byref(rt),
-                             ctypes.byref(nw), ctypes.byref(ks))
-    assert rc == 0 and rt.value >= 1 and nw.value >= 1 and ks.value >= 1
+    cfg = (ctypes.c_int * 6)()
+    rc = lib.acorn_gemm_plan(8, 4096, 12288, _lib.WFMT_W4, cfg)
+    assert rc == 0 and all(v >= 1 for v in cfg[:5]) and cfg[5] >= 1
     # an invalid shape maps to the reference's AssertionError
-    rc = lib.acorn_gemm_plan(8, 4095, 4096, _lib.WFMT_W4, 1, ctypes.byref(rt),
-                             ctypes.byref(nw), ctypes.byref(ks))
+    rc = lib.acorn_gemm_plan(8, 4095, 4096, _lib.WFMT_W4, (ctypes.c_int * 6)())
     with pytest.raises(AssertionError):
         _lib.check(rc, "plan")

@@ -200,3 +200,37 @@ def test_bucket_boundaries_and_classes():
     assert qg.CLASSES == {"qo": (4096, 4096), "kv": (1024, 4096), "gate_up": (12288, 4096),
                           "down": (4096, 12288), "lm_head": (151936, 4096)}
     assert qg._CLS_BY_SHAPE[(4096, 12288)] == "down"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["bf16", "w8", "w4"])
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_every_candidate_tiling_matches(fmt, m):
+    """Every tiling the load-time sweep may pick (row tiles per wave, loads per
+    lane, waves, K splits with the in-kernel reduction, tiles per workgroup)
+    gives the oracle's result on the o shape (K=4096) and the down shape
+    (K=12288); tilings differ only in fp32 summation order."""
+    from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, WFMT_W8
+    from acorninfer_amd.ops.quant_gemm import _launch, candidates
+    for cls in ("o", "down"):
+        n, k = SHAPES[cls]
+        if fmt == "bf16":
+            w, wref = _bf(cls)
+            args, wf = (w, None, None), WFMT_BF16
+        elif fmt == "w8":
+            q, s, wref = _w8(cls)
+            args, wf = (q, s, None), WFMT_W8
+        else:
+            p, s, wref = _w4(cls)
+            args, wf = (p, s, None), WFMT_W4
+        x = _x(m, k, 9)
+        ref = _ref(x, wref)
+        cands = candidates(m, n, k, wf)
+        assert len(cands) >= 8
+        outs = []
+        for c in cands:
+            out = _launch(x, *args, wf, n, c, None)
+            r = rel_err(out, ref)
+            assert r <= GEMM_REL, f"{cls} {tuple(c)}: rel err {r:.3g}"
+            outs.append(out)
+        print(f"\n[{fmt} M={m} {cls}: {len(cands)} tilings ok]")
