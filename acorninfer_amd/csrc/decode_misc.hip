@@ -46,20 +46,22 @@ __device__ __forceinline__ float silu_r(float g) {
   return round_to<T>(g / (1.0f + expf(-g)));
 }
 
-// part: [nsplit, rows, 2*inter] fp32 (gate columns first) or NULL;
-// gu: [rows, 2*inter] T when part is NULL. act: [rows, inter].
+// part: [nsplit, rows, 2*inter] fp32 or NULL; gu: [rows, 2*inter] T when
+// part is NULL. Columns are gate-first ([gate | up]) or, with il16, in
+// 16-column blocks alternating gate and up. act: [rows, inter].
 template <typename T>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ part,
                                                        int nsplit, const T* __restrict__ gu,
                                                        T* __restrict__ act, int rows,
-                                                       int inter) {
+                                                       int inter, int il16) {
 #pragma clang fp contract(off)
   const size_t n = (size_t)rows * inter;
   const size_t plane = (size_t)rows * 2 * inter;
   for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
        e += (size_t)gridDim.x * blockDim.x) {
     const size_t r = e / inter, i = e % inter;
-    const size_t gi = r * 2 * inter + i, ui = gi + inter;
+    const size_t gi = r * 2 * inter + (il16 ? (i / 16) * 32 + i % 16 : i);
+    const size_t ui = gi + (il16 ? 16 : inter);
     float g, u;
     if (part) {
       g = part[gi];
@@ -178,8 +180,10 @@ extern "C" int acorn_embedding(const void* table, const int64_t* ids, void* out,
 }
 
 extern "C" int acorn_silu_mul(const float* part, int64_t nsplit, const void* gate_up, void* act,
-                              int64_t rows, int64_t inter, int dtype, void* stream) {
+                              int64_t rows, int64_t inter, int interleaved16, int dtype,
+                              void* stream) {
   if (rows < 0 || inter <= 0 || (part && nsplit < 1)) return ACORN_ERR_SHAPE;
+  if (interleaved16 && inter % 16) return ACORN_ERR_SHAPE;
   if (rows * inter > ((int64_t)1 << 40)) return ACORN_ERR_SHAPE;
   if (rows == 0) return ACORN_OK;
   if (!act || (!part && !gate_up)) return ACORN_ERR_VALUE;
@@ -188,13 +192,13 @@ extern "C" int acorn_silu_mul(const float* part, int64_t nsplit, const void* gat
   const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
   switch (dtype) {
     case ACORN_F32:
-      silu_mul_kernel<float><<<blocks, 256, 0, st>>>(part, (int)nsplit, (const float*)gate_up, (float*)act, (int)rows, (int)inter);
+      silu_mul_kernel<float><<<blocks, 256, 0, st>>>(part, (int)nsplit, (const float*)gate_up, (float*)act, (int)rows, (int)inter, interleaved16);
       break;
     case ACORN_F16:
-      silu_mul_kernel<_Float16><<<blocks, 256, 0, st>>>(part, (int)nsplit, (const _Float16*)gate_up, (_Float16*)act, (int)rows, (int)inter);
+      silu_mul_kernel<_Float16><<<blocks, 256, 0, st>>>(part, (int)nsplit, (const _Float16*)gate_up, (_Float16*)act, (int)rows, (int)inter, interleaved16);
       break;
     case ACORN_BF16:
-      silu_mul_kernel<__bf16><<<blocks, 256, 0, st>>>(part, (int)nsplit, (const __bf16*)gate_up, (__bf16*)act, (int)rows, (int)inter);
+      silu_mul_kernel<__bf16><<<blocks, 256, 0, st>>>(part, (int)nsplit, (const __bf16*)gate_up, (__bf16*)act, (int)rows, (int)inter, interleaved16);
       break;
     default:
       return ACORN_ERR_DTYPE;

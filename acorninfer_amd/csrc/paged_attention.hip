@@ -26,6 +26,7 @@ namespace {
 constexpr int kChunk = 16;  // tokens per step
 constexpr int kLPT = 4;     // lanes per token in the q.k phase
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kAttnWaves = 8;  // waves per workgroup of the single-kernel form
 
 template <typename T, int N>
 struct Vec {
@@ -197,6 +198,230 @@ __global__ __launch_bounds__(kWave) void paged_attn_split_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Single-kernel form for D in {64, 128} (the Qwen3 head size): one
+// workgroup of NWV waves per (split, kv head, sequence). The waves divide the
+// workgroup's pages; inside a wave a token's D values are spread over D/8
+// lanes (8 values, one 16-byte load for bf16, per lane), so a 16-token chunk
+// costs each lane D/32 loads of K and of V. The next chunk's K/V are loaded
+// into the second register set while the current chunk is processed. The
+// workgroup's block-table entries are staged in LDS first. At the end the
+// waves' (m, l, acc) are merged in LDS and the output (or, with S > 1
+// workgroup splits, this split's partial for the combine kernel) is written.
+template <typename T>
+struct V8 {
+  T v[8];
+};
+
+// DPP lane permutations within a row of 16 lanes (gfx9 encodings).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over groups of N lanes (N in {2, 4, 8, 16}, aligned within a row of
+// 16); every lane of the group receives the sum.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp<0xB1>(v);                      // quad_perm [1,0,3,2]: lane ^ 1
+  if constexpr (N >= 4) v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (N >= 8) v += dpp<0x141>(v);  // row_half_mirror: lane i <- 7-i
+  if constexpr (N >= 16) v += dpp<0x140>(v); // row_mirror: lane i <- 15-i
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ void load8f(const T* p, float (&f)[8]) {
+  V8<T> r;
+  __builtin_memcpy(&r, p, sizeof(r));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = to_f32(r.v[i]);
+}
+
+template <typename T, int D, int REP, int NWV>
+__global__ __launch_bounds__(NWV * kWave) void paged_attn_wg_kernel(
+    const T* __restrict__ q, const T* __restrict__ k_pages, const T* __restrict__ v_pages,
+    const int32_t* __restrict__ tables, const int32_t* __restrict__ lens, T* __restrict__ out,
+    float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l, int H,
+    int KV, int P, int num_blocks, int table_stride, int S, float scale_log2) {
+  constexpr int LPT = D / 8;                   // lanes per token
+  constexpr int TR = kWave / LPT;              // tokens per wave-wide load
+  constexpr int CH = 16;                       // tokens per chunk
+  constexpr int NL = CH / TR;                  // loads per lane per chunk
+  static_assert(NL >= 1, "D too small for this kernel");
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* sacc = (float*)smem;                  // [NWV][REP][D]
+  float* sm = sacc + NWV * REP * D;            // [NWV][REP]
+  float* sl = sm + NWV * REP;                  // [NWV][REP]
+  int* tbl = (int*)(sl + NWV * REP);           // this workgroup's block ids
+
+  const int sp = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int g = lane / LPT, c = lane % LPT;
+
+  const int L = min(max(lens[b], 0), table_stride * P);
+  const int npages = (L + P - 1) / P;
+  const int ppw = (npages + S - 1) / S;        // pages per workgroup split
+  const int wp0 = min(sp * ppw, npages), wp1 = min(wp0 + ppw, npages);
+  const int32_t* trow = tables + (size_t)b * table_stride;
+  for (int i = threadIdx.x; i < wp1 - wp0; i += NWV * kWave) {
+    const unsigned pg = (unsigned)trow[wp0 + i];
+    tbl[i] = pg < (unsigned)num_blocks ? (int)pg : 0;
+  }
+  // this wave's pages and tokens
+  const int ppv = (wp1 - wp0 + NWV - 1) / NWV;
+  const int vp0 = min(wp0 + wid * ppv, wp1), vp1 = min(vp0 + ppv, wp1);
+  const int tstart = vp0 * P, tend = min(vp1 * P, L);
+
+  float qf[REP][8];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    load8f<T>(q + ((size_t)b * H + kvh * REP + h) * D + c * 8, qf[h]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qf[h][i] *= scale_log2;
+  }
+  float m[REP], l[REP], acc[REP][8];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
+  }
+  __syncthreads();  // tbl ready
+
+  const size_t tok_stride = (size_t)KV * D;
+  // Raw (unconverted) chunk registers; tokens past the end are zero so that
+  // p = 0 multiplies a finite value.
+  auto load_chunk = [&](int t0, V8<T> (&kr)[NL], V8<T> (&vr)[NL]) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int t = t0 + g + TR * i;
+      if (t < tend) {
+        const size_t off =
+            ((size_t)tbl[t / P - wp0] * P + (t % P)) * tok_stride + (size_t)kvh * D + c * 8;
+        __builtin_memcpy(&kr[i], k_pages + off, sizeof(V8<T>));
+        __builtin_memcpy(&vr[i], v_pages + off, sizeof(V8<T>));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          kr[i].v[j] = from_f32<T>(0.f);
+          vr[i].v[j] = from_f32<T>(0.f);
+        }
+      }
+    }
+  };
+  // Each group of LPT lanes keeps its own online-softmax state over its
+  // tokens (t0 + g + TR*i); the groups are merged once, after the loop.
+  auto consume = [&](int t0, const V8<T> (&kr)[NL], const V8<T> (&vr)[NL]) {
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+      float sc[NL];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) d += qf[h][j] * to_f32(kr[i].v[j]);
+        d = group_sum<LPT>(d);
+        sc[i] = (t0 + g + TR * i < tend) ? d : -INFINITY;
+        mx = fmaxf(mx, sc[i]);
+      }
+      if (mx == -INFINITY) continue;       // no token of this group in the chunk
+      const float mn = fmaxf(m[h], mx);
+      const float alpha = exp2f(m[h] - mn);
+      m[h] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[h][j] *= alpha;
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        const float p = exp2f(sc[i] - mn);
+        ps += p;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[h][j] += p * to_f32(vr[i].v[j]);
+      }
+      l[h] = l[h] * alpha + ps;
+    }
+  };
+
+  {
+    // three chunks in flight per wave: consume chunk c while c+1, c+2 load
+    V8<T> ka[NL], va[NL], kb[NL], vb[NL], kc[NL], vc[NL];
+    if (tstart < tend) load_chunk(tstart, ka, va);
+    if (tstart + CH < tend) load_chunk(tstart + CH, kb, vb);
+    if (tstart + 2 * CH < tend) load_chunk(tstart + 2 * CH, kc, vc);
+    for (int t0 = tstart; t0 < tend; t0 += 3 * CH) {
+      consume(t0, ka, va);
+      if (t0 + 3 * CH < tend) load_chunk(t0 + 3 * CH, ka, va);
+      if (t0 + CH >= tend) break;
+      consume(t0 + CH, kb, vb);
+      if (t0 + 4 * CH < tend) load_chunk(t0 + 4 * CH, kb, vb);
+      if (t0 + 2 * CH >= tend) break;
+      consume(t0 + 2 * CH, kc, vc);
+      if (t0 + 5 * CH < tend) load_chunk(t0 + 5 * CH, kc, vc);
+    }
+  }
+  // merge the wave's token groups (a group's lanes hold equal m and l)
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    float M = m[h];
+#pragma unroll
+    for (int o = LPT; o < kWave; o <<= 1) M = fmaxf(M, __shfl_xor(M, o));
+    const float f = M == -INFINITY ? 0.f : exp2f(m[h] - M);
+    m[h] = M;
+    l[h] *= f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[h][j] *= f;
+#pragma unroll
+    for (int o = LPT; o < kWave; o <<= 1) {
+      l[h] += __shfl_xor(l[h], o);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[h][j] += __shfl_xor(acc[h][j], o);
+    }
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int h = 0; h < REP; ++h)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sacc[(wid * REP + h) * D + c * 8 + j] = acc[h][j];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+      sm[wid * REP + h] = m[h];
+      sl[wid * REP + h] = l[h];
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < REP * D; e += NWV * kWave) {
+    const int h = e / D, d = e % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) M = fmaxf(M, sm[w * REP + h]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < NWV; ++w) {
+        const float f = exp2f(sm[w * REP + h] - M);
+        num += f * sacc[(w * REP + h) * D + d];
+        den += f * sl[w * REP + h];
+      }
+    }
+    const size_t row = (size_t)b * H + kvh * REP + h;
+    if (S == 1) {
+      out[row * D + d] = from_f32<T>(num / den);
+    } else {
+      const size_t slot = row * S + sp;
+      ws_acc[slot * D + d] = num;
+      if (d == 0) {
+        ws_m[slot] = M;
+        ws_l[slot] = den;
+      }
+    }
+  }
+}
+
 // Phase 2: merge S partials of one (b, h) with the common max.
 template <typename T, int D>
 __global__ __launch_bounds__(kWave) void paged_attn_combine_kernel(
@@ -223,12 +448,29 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
                 const int32_t* lens, void* out, float* ws_acc, float* ws_ml, int64_t B,
                 int64_t H, int64_t KV, int64_t P, int64_t num_blocks, int64_t table_stride, int64_t S, float scale,
                 hipStream_t st) {
-  dim3 grid((unsigned)S, (unsigned)KV, (unsigned)B), block(kWave);
+  dim3 grid((unsigned)S, (unsigned)KV, (unsigned)B);
   float* ws_m = ws_ml;
   float* ws_l = ws_ml ? ws_ml + B * H * S : nullptr;
-  paged_attn_split_kernel<T, D, REP><<<grid, block, 0, st>>>(
-      (const T*)q, (const T*)kp, (const T*)vp, tables, lens, (T*)out, ws_acc, ws_m, ws_l,
-      (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e);
+  if constexpr (D >= 64) {
+    constexpr int NWV = kAttnWaves;
+    const int64_t ppw = (table_stride + S - 1) / S;  // most pages one workgroup can get
+    const size_t lds = (size_t)(NWV * REP * D + 2 * NWV * REP) * 4 + (size_t)ppw * 4;
+    if (lds > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
+    auto kfn = paged_attn_wg_kernel<T, D, REP, NWV>;
+    static bool lds_raised = false;
+    if (!lds_raised && lds > 64 * 1024) {
+      (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                160 * 1024);
+      lds_raised = true;
+    }
+    kfn<<<grid, dim3(NWV * kWave), lds, st>>>(
+        (const T*)q, (const T*)kp, (const T*)vp, tables, lens, (T*)out, ws_acc, ws_m, ws_l,
+        (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e);
+  } else {
+    paged_attn_split_kernel<T, D, REP><<<grid, dim3(kWave), 0, st>>>(
+        (const T*)q, (const T*)kp, (const T*)vp, tables, lens, (T*)out, ws_acc, ws_m, ws_l,
+        (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e);
+  }
   ACORN_LAUNCH_CHECK();
   if (S > 1) {
     paged_attn_combine_kernel<T, D><<<dim3((unsigned)(B * H)), dim3(kWave), 0, st>>>(

@@ -129,8 +129,21 @@ struct KArgs {
   int log2R;       // LDS rows per m tile = 1 << log2R
 };
 
+// SwiGLU epilogue of the fused gate|up projection: g, u rounded to bf16,
+// act = round(round(silu(g)) * u), silu(g) = g / (1 + exp(-g)) in fp32
+// (models/qwen3.py:392-396, each torch bf16 op rounded).
+__device__ __forceinline__ float swiglu_bf16(float g, float u) {
+#pragma clang fp contract(off)
+  g = (float)(__bf16)g;
+  u = (float)(__bf16)u;
+  const float sg = (float)(__bf16)(g / (1.0f + expf(-g)));
+  return sg * u;
+}
+
 // Grid: x = tile groups, y = ksplit, z = m blocks of 16*MT rows.
-template <int WFMT, int RT, int MT, int UPW, int NW>
+// SWIGLU: RT == 2, the tile's first 16 weight rows are gate rows and the next
+// 16 the up rows of the same 16 outputs; out is act [M, N/2] (ksplit == 1).
+template <int WFMT, int RT, int MT, int UPW, int NW, bool SWIGLU>
 __global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
   using F = Fmt<WFMT>;
   constexpr int KU = F::KU, MPU = F::MPU, ROWS = 16 * RT;
@@ -269,6 +282,23 @@ __global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
           acc[rt][mt][i] = 0.f;
         }
     __syncthreads();
+    if constexpr (SWIGLU) {
+      constexpr int HALF = TILE / 2;  // rt = 0 (gate) entries; rt = 1 (up) follow
+      const int NA = a.N / 2;
+      for (int e = threadIdx.x; e < HALF; e += NT) {
+        float gv = rb[e], uv = rb[e + HALF];
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) {
+          gv += rb[(size_t)ww * TILE + e];
+          uv += rb[(size_t)ww * TILE + e + HALF];
+        }
+        const int ln = e % kWave, i = (e / kWave) % 4, mt = e / (4 * kWave);
+        const int m = mblk + mt * 16 + (ln % 16);
+        const int n = t * 16 + 4 * (ln / 16) + i;
+        if (m < a.M) a.out[(size_t)m * NA + n] = (__bf16)swiglu_bf16(gv, uv);
+      }
+      return;
+    }
     const bool direct = a.ksplit == 1 && a.out != nullptr;
     for (int e = threadIdx.x; e < TILE; e += NT) {
       float v = rb[e];
@@ -393,6 +423,7 @@ struct Tiling {
   int rt, upw, nw, ksplit, tpw;  // the tunable knobs (acorn_gemm_plan's cfg[0..4])
   int mt, R, nk, ntiles, mblocks, groups;
   size_t lds;
+  int swiglu;                    // fused SwiGLU epilogue (rt == 2, ksplit == 1)
 };
 
 int ilog2_ceil(int v) {
@@ -422,9 +453,13 @@ size_t lds_bytes(int wfmt, int mt, int R, int rt, int nw, int KR) {
   return b;
 }
 
-// cfg: {rt, upw, nw, ksplit, tpw}; 0 = choose.
-int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling* t) {
+// cfg: {rt, upw, nw, ksplit, tpw}; 0 = choose. swiglu: fused SwiGLU epilogue,
+// which fixes rt = 2 and ksplit = 1.
+int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling* t,
+              bool swiglu = false) {
   if (M <= 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
+  t->swiglu = swiglu;
+  if (swiglu && (M > 16 || N % 32)) return ACORN_ERR_UNSUPPORTED;
   const int ku = ku_of(wfmt);
   if (N % 16 || K % ku) return ACORN_ERR_SHAPE;
   if (wfmt == ACORN_WFMT_W4 && K % 128) return ACORN_ERR_SHAPE;
@@ -432,7 +467,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   const int req_ks = cfg ? cfg[3] : 0, req_tpw = cfg ? cfg[4] : 0;
   t->mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
   t->R = t->mt == 1 ? (1 << ilog2_ceil((int)M)) : 16;
-  t->rt = req_rt > 0 ? req_rt : 1;
+  t->rt = swiglu ? 2 : req_rt > 0 ? req_rt : 1;
   if (t->mt > 1) t->rt = 1;
   while (t->rt > 1 && N % (16 * t->rt)) t->rt /= 2;
   t->upw = req_upw > 0 ? req_upw : (wfmt == ACORN_WFMT_W4 ? 4 : 8);
@@ -459,7 +494,10 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   while (lds_for(kc()) > limit && t->upw > 2) t->upw /= 2;
   if (!fits() || lds_for(kc()) > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
   const int64_t chunks = K / kc();
-  if (req_ks > 0) {
+  if (swiglu) {
+    t->ksplit = 1;
+    if (lds_for(K) > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
+  } else if (req_ks > 0) {
     // a requested split is raised to the next divisor of the chunk count
     // whose K range fits the LDS of one workgroup
     t->ksplit = req_ks;
@@ -497,12 +535,15 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
 
 template <int WFMT, int RT, int MT, int UPW, int NW>
 void launch_one(const Tiling& t, const KArgs& a, hipStream_t st) {
-  auto kfn = wgemm_kernel<WFMT, RT, MT, UPW, NW>;
-  static bool lds_raised = false;  // once per instantiation, before any capture
-  if (!lds_raised && t.lds > 64 * 1024) {
+  auto kfn = wgemm_kernel<WFMT, RT, MT, UPW, NW, false>;
+  if constexpr (RT == 2) {
+    if (t.swiglu) kfn = wgemm_kernel<WFMT, RT, MT, UPW, NW, true>;
+  }
+  static bool lds_raised[2] = {false, false};  // once per instantiation, before any capture
+  if (!lds_raised[t.swiglu] && t.lds > 64 * 1024) {
     (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
                               160 * 1024);
-    lds_raised = true;
+    lds_raised[t.swiglu] = true;
   }
   dim3 grid((unsigned)t.groups, (unsigned)t.ksplit, (unsigned)t.mblocks), block(NW * kWave);
   kfn<<<grid, block, t.lds, st>>>(a);
@@ -553,18 +594,12 @@ int dispatch_tile(const Tiling& t, const KArgs& a, hipStream_t st) {
   return ACORN_ERR_UNSUPPORTED;
 }
 
-}  // namespace
-
-extern "C" int acorn_gemm_plan(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg) {
+int plan_entry(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg, bool swiglu) {
   if (!cfg) return ACORN_ERR_VALUE;
-  if (wfmt == ACORN_WFMT_F32) {
-    cfg[0] = 1; cfg[1] = 1; cfg[2] = 4; cfg[3] = cfg[3] > 0 ? cfg[3] : 1; cfg[4] = 1; cfg[5] = 0;
-    return ACORN_OK;
-  }
   if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4)
     return ACORN_ERR_DTYPE;
   Tiling t;
-  const int rc = make_plan(M, N, K, wfmt, cfg, &t);
+  const int rc = make_plan(M, N, K, wfmt, cfg, &t, swiglu);
   if (rc) return rc;
   cfg[0] = t.rt;
   cfg[1] = t.upw;
@@ -575,32 +610,14 @@ extern "C" int acorn_gemm_plan(int64_t M, int64_t N, int64_t K, int wfmt, int* c
   return ACORN_OK;
 }
 
-extern "C" int acorn_quant_gemm(const void* x, const void* w, const void* scale,
-                                const void* zero, void* out_bf16, float* part, int64_t M,
-                                int64_t N, int64_t K, int wfmt, const int* cfg, void* stream) {
-  if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
-      wfmt != ACORN_WFMT_F32)
-    return ACORN_ERR_DTYPE;
-  if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
-  if (M == 0) return ACORN_OK;
-  hipStream_t st = (hipStream_t)stream;
-  if (wfmt == ACORN_WFMT_F32) {
-    // fp32 output always goes through part ([ksplit, M, N]).
-    if (!x || !w || !part) return ACORN_ERR_VALUE;
-    if (M > 65535 || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return ACORN_ERR_SHAPE;
-    const int ks = cfg && cfg[3] > 0 ? cfg[3] : 1;
-    const int64_t kper = (K + ks - 1) / ks;
-    dim3 grid((unsigned)((N + 3) / 4), (unsigned)ks), block(256);
-    f32_gemv_kernel<<<grid, block, 0, st>>>((const float*)x, (const float*)w, part, (int)M,
-                                            (int)N, (int)K, (int)kper);
-    ACORN_LAUNCH_CHECK();
-    return ACORN_OK;
-  }
+int gemm_entry(const void* x, const void* w, const void* scale, const void* zero,
+               void* out_bf16, float* part, int64_t M, int64_t N, int64_t K, int wfmt,
+               const int* cfg, bool swiglu, hipStream_t st) {
   if (!x || !w || (wfmt != ACORN_WFMT_BF16 && !scale)) return ACORN_ERR_VALUE;
   if (!out_bf16 && !part) return ACORN_ERR_VALUE;
   if (M > 65535 * 64 || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return ACORN_ERR_SHAPE;
   Tiling t;
-  int rc = make_plan(M, N, K, wfmt, cfg, &t);
+  int rc = make_plan(M, N, K, wfmt, cfg, &t, swiglu);
   if (rc) return rc;
   // ksplit > 1 with a bf16 output needs the partials workspace
   if (out_bf16 && t.ksplit > 1 && !part) return ACORN_ERR_VALUE;
@@ -632,6 +649,57 @@ extern "C" int acorn_quant_gemm(const void* x, const void* w, const void* scale,
     ACORN_LAUNCH_CHECK();
   }
   return ACORN_OK;
+}
+
+}  // namespace
+
+extern "C" int acorn_gemm_plan(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg) {
+  if (!cfg) return ACORN_ERR_VALUE;
+  if (wfmt == ACORN_WFMT_F32) {
+    cfg[0] = 1; cfg[1] = 1; cfg[2] = 4; cfg[3] = cfg[3] > 0 ? cfg[3] : 1; cfg[4] = 1; cfg[5] = 0;
+    return ACORN_OK;
+  }
+  return plan_entry(M, N, K, wfmt, cfg, false);
+}
+
+extern "C" int acorn_gemm_swiglu_plan(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg) {
+  return plan_entry(M, N, K, wfmt, cfg, true);
+}
+
+extern "C" int acorn_quant_gemm(const void* x, const void* w, const void* scale,
+                                const void* zero, void* out_bf16, float* part, int64_t M,
+                                int64_t N, int64_t K, int wfmt, const int* cfg, void* stream) {
+  if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
+      wfmt != ACORN_WFMT_F32)
+    return ACORN_ERR_DTYPE;
+  if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
+  if (M == 0) return ACORN_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (wfmt == ACORN_WFMT_F32) {
+    // fp32 output always goes through part ([ksplit, M, N]).
+    if (!x || !w || !part) return ACORN_ERR_VALUE;
+    if (M > 65535 || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return ACORN_ERR_SHAPE;
+    const int ks = cfg && cfg[3] > 0 ? cfg[3] : 1;
+    const int64_t kper = (K + ks - 1) / ks;
+    dim3 grid((unsigned)((N + 3) / 4), (unsigned)ks), block(256);
+    f32_gemv_kernel<<<grid, block, 0, st>>>((const float*)x, (const float*)w, part, (int)M,
+                                            (int)N, (int)K, (int)kper);
+    ACORN_LAUNCH_CHECK();
+    return ACORN_OK;
+  }
+  return gemm_entry(x, w, scale, zero, out_bf16, part, M, N, K, wfmt, cfg, false, st);
+}
+
+extern "C" int acorn_quant_gemm_swiglu(const void* x, const void* w, const void* scale,
+                                       const void* zero, void* act, int64_t M, int64_t N,
+                                       int64_t K, int wfmt, const int* cfg, void* stream) {
+  if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4)
+    return ACORN_ERR_DTYPE;
+  if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
+  if (M == 0) return ACORN_OK;
+  if (!act) return ACORN_ERR_VALUE;
+  return gemm_entry(x, w, scale, zero, act, nullptr, M, N, K, wfmt, cfg, true,
+                    (hipStream_t)stream);
 }
 
 extern "C" int acorn_splitk_reduce(const float* part, int64_t nsplit, int64_t count, void* out,

@@ -61,6 +61,7 @@ class QLinear:
     K: int
     scale: torch.Tensor | None = None
     zero: torch.Tensor | None = None
+    il16: bool = False          # gate|up rows interleaved in 16-row blocks (fused SwiGLU)
 
     @classmethod
     def from_dense(cls, w: torch.Tensor, fmt: int) -> "QLinear":
@@ -75,15 +76,28 @@ class QLinear:
             return cls(fmt, Q.pack_w4(u).contiguous(), N, K, s.contiguous())
         raise ValueError(f"unknown weight format {fmt}")
 
+    def interleaved(self) -> "QLinear":
+        """The same [gate; up] weight with rows (and scales, zeros) in the
+        16-row gate/up blocks of the fused SwiGLU launch."""
+        from acorninfer_amd.ops.quant_gemm import interleave16
+        il = lambda t: None if t is None else interleave16(t)  # noqa: E731
+        return QLinear(self.fmt, il(self.w), self.N, self.K, il(self.scale), il(self.zero),
+                       il16=True)
+
     def dense(self) -> torch.Tensor:
-        """fp32 dequantised weight [N, K] (test/inspection helper)."""
+        """fp32 dequantised weight [N, K] in [gate; up] row order (test helper)."""
         if self.fmt in (WFMT_BF16, _lib.WFMT_F32):
-            return self.w.float()
-        if self.fmt == WFMT_W8:
-            return Q.dequant_w8(self.w, self.scale)
-        u = Q.unpack_w4(self.w)
-        zero = self.zero if self.zero is not None else Q.sym_zero(self.scale)
-        return Q.dequant_w4(u, self.scale, zero)
+            d = self.w.float()
+        elif self.fmt == WFMT_W8:
+            d = Q.dequant_w8(self.w, self.scale)
+        else:
+            u = Q.unpack_w4(self.w)
+            zero = self.zero if self.zero is not None else Q.sym_zero(self.scale)
+            d = Q.dequant_w4(u, self.scale, zero)
+        if self.il16:
+            from acorninfer_amd.ops.quant_gemm import deinterleave16
+            d = deinterleave16(d)
+        return d
 
     def nbytes(self) -> int:
         n = self.w.numel() * self.w.element_size()
@@ -109,6 +123,19 @@ class QLinear:
                                     ptr(out), ptr(part), M, self.N, self.K, self.fmt, arr,
                                     stream)
         check(rc, "quant_gemm")
+
+    def swiglu_plan(self, M: int, tiling=None):
+        from acorninfer_amd.ops.quant_gemm import swiglu_plan
+        return swiglu_plan(M, self.N, self.K, self.fmt, tiling)
+
+    def launch_swiglu(self, x: torch.Tensor, M: int, tiling, act: torch.Tensor,
+                      stream: int) -> None:
+        """Fused gate|up + SwiGLU (il16 weights): act [M, N/2] bf16."""
+        arr = (ctypes.c_int * 6)(*tiling, 0)
+        rc = lib().acorn_quant_gemm_swiglu(ptr(x), ptr(self.w), ptr(self.scale),
+                                           ptr(self.zero), ptr(act), M, self.N, self.K,
+                                           self.fmt, arr, stream)
+        check(rc, "quant_gemm_swiglu")
 
 
 @dataclass
@@ -191,6 +218,7 @@ class Qwen3DecodeModel:
         self.fused_ops = True
         # batch -> {projection name -> Tiling}, filled by tune()
         self.tilings: dict[int, dict] = {}
+        self.swiglu_choice: dict[int, bool] = {}
 
     # ---------------------------------------------------------------- building --
     @classmethod
@@ -221,6 +249,9 @@ class Qwen3DecodeModel:
         qkv = torch.cat([get("self_attn.q_proj"), get("self_attn.k_proj"),
                          get("self_attn.v_proj")], 0)
         gate_up = torch.cat([get("mlp.gate_proj"), get("mlp.up_proj")], 0)
+        gu = lin(gate_up)
+        if gu.fmt != _lib.WFMT_F32 and gu.N % 32 == 0:
+            gu = gu.interleaved()
         return LayerWeights(
             input_norm=get("input_layernorm").to(dtype).contiguous(),
             qkv=lin(qkv),
@@ -228,7 +259,7 @@ class Qwen3DecodeModel:
             k_norm=get("self_attn.k_norm").to(dtype).contiguous(),
             o=lin(get("self_attn.o_proj")),
             post_norm=get("post_attention_layernorm").to(dtype).contiguous(),
-            gate_up=lin(gate_up),
+            gate_up=gu,
             down=lin(get("mlp.down_proj")),
         )
 
@@ -321,11 +352,14 @@ class Qwen3DecodeModel:
             check(L.acorn_fused_add_rmsnorm_partials(
                 ptr(buf.part_o), co.ksplit, ptr(buf.res), ptr(buf.res), ptr(lw.post_norm),
                 ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
-            # MLP: gate|up partials -> SwiGLU -> down partials
+            # MLP: gate|up (+ fused SwiGLU) -> act -> down partials
             cg = buf.cfgs["gate_up"]
-            lw.gate_up.launch(buf.normed, B, cg, part=buf.part_gu, stream=st)
-            check(L.acorn_silu_mul(ptr(buf.part_gu), cg.ksplit, None, ptr(buf.act), B, inter, dt,
-                                   st), "silu_mul")
+            if buf.swiglu:
+                lw.gate_up.launch_swiglu(buf.normed, B, cg, buf.act, st)
+            else:
+                lw.gate_up.launch(buf.normed, B, cg, part=buf.part_gu, stream=st)
+                check(L.acorn_silu_mul(ptr(buf.part_gu), cg.ksplit, None, ptr(buf.act), B, inter,
+                                       int(lw.gate_up.il16), dt, st), "silu_mul")
             cd = buf.cfgs["down"]
             lw.down.launch(buf.act, B, cd, part=buf.part_down, stream=st)
             prev_ks = cd.ksplit
@@ -338,27 +372,44 @@ class Qwen3DecodeModel:
         check(L.acorn_argmax(ptr(buf.logits), B, cfg.vocab_size, ptr(buf.next_ids),
                              dtype_code(buf.logits), st), "argmax")
 
+    def fused_swiglu(self, batch: int) -> bool:
+        """The gate|up launch carries the SwiGLU epilogue (decode sizes, and
+        unless tune() found the split-K launch + silu_mul faster)."""
+        ok = batch <= 16 and self.layers[0].gate_up.il16
+        return ok and self.swiglu_choice.get(batch, True)
+
     def projections(self) -> dict[str, list[QLinear]]:
         """Each projection of the step with its per-layer weights."""
         return {"qkv": [L.qkv for L in self.layers], "o": [L.o for L in self.layers],
                 "gate_up": [L.gate_up for L in self.layers],
                 "down": [L.down for L in self.layers], "lm_head": [self.lm_head]}
 
-    def time_projection(self, lins: list[QLinear], M: int, tiling, reps: int = 3) -> float:
+    def time_projection(self, lins: list[QLinear], M: int, tiling, reps: int = 3,
+                        swiglu: bool = False, with_act: bool = False) -> float:
         """Average µs of one launch of `tiling`, measured as a hipGraph of one
         launch per weight in `lins` (distinct weights, so the 256 MB MALL does
         not hold them between launches) on a private stream with HIP events."""
         from acorninfer_amd.ops.quant_gemm import _native_cfg
-        t = lins[0].plan(M, _native_cfg(tiling, M))[0]
         lin0 = lins[0]
+        planner = lin0.swiglu_plan if swiglu else lin0.plan
+        t = planner(M, _native_cfg(tiling, M))[0]
         x = torch.randn(M, lin0.K, device=self.device).to(self.dtype)
         part = torch.empty(t.ksplit, M, lin0.N, dtype=torch.float32, device=self.device)
+        act = torch.empty(M, lin0.N // 2, dtype=self.dtype, device=self.device)
         s = torch.cuda.Stream(self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(s):
             def body():
                 for lin in lins:
-                    lin.launch(x, M, t, part=part, stream=s.cuda_stream)
+                    if swiglu:
+                        lin.launch_swiglu(x, M, t, act, s.cuda_stream)
+                    else:
+                        lin.launch(x, M, t, part=part, stream=s.cuda_stream)
+                        if with_act:   # the separate activation the fused form saves
+                            check(lib().acorn_silu_mul(ptr(part), t.ksplit, None, ptr(act), M,
+                                                       lin.N // 2, int(lin.il16),
+                                                       dtype_code(act), s.cuda_stream),
+                                  "silu_mul")
             body()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=s):
@@ -388,15 +439,26 @@ class Qwen3DecodeModel:
             if names is not None and name not in names:
                 continue
             best = None
-            for c in candidates(batch, lins[0].N, lins[0].K, lins[0].fmt):
-                us = self.time_projection(lins, batch, c)
-                if verbose:
-                    print(f"TUNE {name} M={batch} {tuple(c)} {us:.2f} us", flush=True)
-                if best is None or us < best[0]:
-                    best = (us, c)
+            modes = [False]
+            if name == "gate_up":
+                self.swiglu_choice.pop(batch, None)
+                modes = [True, False] if self.fused_swiglu(batch) else [False]
+            for sw in modes:
+                act = name == "gate_up" and not sw
+                for c in candidates(batch, lins[0].N, lins[0].K, lins[0].fmt, swiglu=sw):
+                    us = self.time_projection(lins, batch, c, swiglu=sw, with_act=act)
+                    if verbose:
+                        print(f"TUNE {name} M={batch} swiglu={sw} {tuple(c)} {us:.2f} us",
+                              flush=True)
+                    if best is None or us < best[0]:
+                        best = (us, c, sw)
+            if name == "gate_up" and len(modes) == 2:
+                self.swiglu_choice[batch] = best[2]
             chosen[name] = best[1]
             report[name] = {"tiling": tuple(best[1]), "us": round(best[0], 3),
                             "bytes": lins[0].nbytes()}
+            if name == "gate_up":
+                report[name]["fused_swiglu"] = best[2]
         return report
 
     # Reference-shaped entry point (qwen3.py:520-595).
@@ -444,12 +506,21 @@ def _dense_linear(w: torch.Tensor, dtype: torch.dtype) -> QLinear:
     raise ValueError(f"no dense weight format for activations of dtype {dtype}")
 
 
-def attention_splits(batch: int, kv_heads: int, *, cu_count: int = MI355X_CUS,
-                     waves_per_cu: int = 4, max_splits: int = 64) -> int:
-    """K3 split count for a captured bucket: enough (split, kv head, sequence)
-    wavefronts to give every CU `waves_per_cu` of them. Fixed per bucket (the
-    kernel skips splits beyond a sequence's pages)."""
-    return max(1, min(max_splits, -(-cu_count * waves_per_cu // max(1, batch * kv_heads))))
+ATTN_WAVES = 8   # waves per K3 workgroup (csrc/paged_attention.hip kAttnWaves)
+
+
+def attention_splits(batch: int, kv_heads: int, max_pages: int, *,
+                     pages_per_wave: int = 8, max_workgroups: int = 1024) -> int:
+    """K3 workgroup splits per (sequence, kv head) for a captured bucket.
+
+    One workgroup's ATTN_WAVES waves already divide a sequence's pages, so
+    the sequence is split across workgroups (merged by the combine launch)
+    only when every wave would otherwise get more than `pages_per_wave`
+    pages, and never beyond `max_workgroups` workgroups in total. Fixed per
+    bucket: splits past a sequence's last page are empty."""
+    want = -(-max_pages // (ATTN_WAVES * pages_per_wave))
+    cap = max(1, max_workgroups // max(1, batch * kv_heads))
+    return max(1, min(want, cap))
 
 
 @dataclass
@@ -469,12 +540,16 @@ class StepBuffers:
         H, D = cfg.hidden_size, cfg.head_dim
         nq, nkv, inter = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.intermediate_size
         if self.num_splits is None:
-            self.num_splits = attention_splits(B, nkv)
+            self.num_splits = attention_splits(B, nkv, self.max_pages)
         lw = m.layers[0]
         tilings = self.tilings or {}
+        self.swiglu = m.fused_swiglu(B)
         for name, lin in (("qkv", lw.qkv), ("o", lw.o), ("gate_up", lw.gate_up),
                           ("down", lw.down), ("lm_head", m.lm_head)):
-            self.cfgs[name] = lin.plan(B, tilings.get(name))[0]
+            if name == "gate_up" and self.swiglu:
+                self.cfgs[name] = lin.swiglu_plan(B, tilings.get(name))[0]
+            else:
+                self.cfgs[name] = lin.plan(B, tilings.get(name))[0]
         # int64 block: ids | positions | pages | slots | next_ids ; int32 block: lens | tables
         self.flat_i64 = torch.zeros(5 * B, dtype=torch.int64, device=dev)
         self.flat_i32 = torch.zeros(B * (1 + self.max_pages), dtype=torch.int32, device=dev)

@@ -2,8 +2,9 @@
 
 Drop-in for acorninfer/ops/paged_attention.py: `paged_decode_attention`
 (:125-152), `num_splits_for` (:155-158) and `build_tables` (:161-189). The
-kernel is csrc/paged_attention.hip (acorn_paged_attention): one wavefront per
-(split, kv head, sequence) serving every query head of the kv head.
+kernel is csrc/paged_attention.hip (acorn_paged_attention): one workgroup per
+(split, kv head, sequence) whose waves divide the split's pages and serve
+every query head of the kv head.
 
 `plan_splits` is this build's split heuristic for MI355X (256 CUs); the
 reference's `num_splits_for` is kept with its exact semantics for callers that
@@ -68,16 +69,12 @@ def num_splits_for(B: int, num_heads: int, *, sm_count: int = _SM_COUNT,
     return max(1, min(max_splits, -(-sm_count // (B * num_heads))))
 
 
-def plan_splits(B: int, kv_heads: int, max_pages: int, *, cu_count: int = MI355X_CUS,
-                waves_per_cu: int = 4, min_pages_per_split: int = 4,
-                max_splits: int = 64) -> int:
-    """Split count for the MI355X kernel, whose grid is (S, KV, B) single-wave
-    workgroups. Aim for `waves_per_cu` waves per CU, but never fewer than
-    `min_pages_per_split` pages per split (the fixed per-split cost of loading
-    q and writing the partial)."""
-    target = -(-cu_count * waves_per_cu // max(1, B * kv_heads))
-    by_len = max(1, max_pages // min_pages_per_split)
-    return max(1, min(max_splits, target, by_len))
+def plan_splits(B: int, kv_heads: int, max_pages: int, **kw) -> int:
+    """Workgroup split count for the MI355X kernel (see
+    models.qwen3.attention_splits): split a sequence across workgroups only
+    when each of a workgroup's waves would otherwise hold many pages."""
+    from acorninfer_amd.models.qwen3 import attention_splits
+    return attention_splits(B, kv_heads, max_pages, **kw)
 
 
 def build_tables(views, page_size: int, device, *, lens_override=None,

@@ -87,6 +87,31 @@ def plan(M: int, N: int, K: int, wfmt: int, cfg: Tiling | None = None
     return Tiling(*arr[:5]), arr[5]
 
 
+def swiglu_plan(M: int, N: int, K: int, wfmt: int, cfg: Tiling | None = None
+                ) -> tuple[Tiling, int]:
+    """Tiling of the fused gate|up + SwiGLU launch (rt = 2, ksplit = 1)."""
+    arr = (ctypes.c_int * 6)(*(tuple(cfg) if cfg is not None else (0,) * 5), 0)
+    check(lib().acorn_gemm_swiglu_plan(M, N, K, wfmt, arr), "gemm_swiglu_plan")
+    return Tiling(*arr[:5]), arr[5]
+
+
+def interleave16(t: torch.Tensor) -> torch.Tensor:
+    """[gate (I rows); up (I rows)] -> 16-row blocks alternating gate and up
+    (the weight layout of acorn_quant_gemm_swiglu). Works on weights, packed
+    weights and per-row scales alike."""
+    n2 = t.shape[0]
+    assert n2 % 32 == 0, "gate|up rows must be a multiple of 32"
+    rest = t.shape[1:]
+    return t.reshape(2, n2 // 32, 16, *rest).transpose(0, 1).reshape(n2, *rest).contiguous()
+
+
+def deinterleave16(t: torch.Tensor) -> torch.Tensor:
+    """Inverse of interleave16."""
+    n2 = t.shape[0]
+    rest = t.shape[1:]
+    return t.reshape(n2 // 32, 2, 16, *rest).transpose(0, 1).reshape(n2, *rest).contiguous()
+
+
 def _native_cfg(cfg, M: int) -> Tiling | None:
     """A native Tiling from an explicit cfg.
 
@@ -247,20 +272,25 @@ def _time_cfg(fn, reps: int = 20) -> float:
     return start.elapsed_time(end) * 1e3 / reps
 
 
-def candidates(M: int, N: int, K: int, wfmt: int) -> list[Tiling]:
+def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[Tiling]:
     """The planner's default plus a neighbourhood of valid tilings (distinct
     full choices only) for a load-time sweep."""
     seen, out = set(), []
-    base, _ = plan(M, N, K, wfmt)
+    planner = swiglu_plan if swiglu else plan
+    base, _ = planner(M, N, K, wfmt)
     reqs = [Tiling()]
     for rt in (1, 2, 4):
         for upw in (2, 4, 8, 16):
             for nw in (2, 4, 8):
                 for ks in (0, 1, 2, 3, 4):
                     reqs.append(Tiling(rt, upw, nw, ks, 0))
+    for tpw in (1, 2, 4, 8):
+        for upw in (2, 4, 8):
+            for nw in (2, 4, 8):
+                reqs.append(Tiling(0, upw, nw, 0, tpw))
     for r in reqs:
         try:
-            t, _ = plan(M, N, K, wfmt, r)
+            t, _ = planner(M, N, K, wfmt, r)
         except (AssertionError, ValueError, NotImplementedError):
             continue
         if t not in seen:

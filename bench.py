@@ -58,6 +58,7 @@ def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int,
     torch.cuda.synchronize()
     _log(f"model {fmt}: {model.weight_bytes() / 1e9:.3f} GB weights in "
          f"{time.perf_counter() - t0:.1f} s")
+    report = {}
     if tune:
         t0 = time.perf_counter()
         report = model.tune(batch)
@@ -84,6 +85,7 @@ def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int,
     runner = DecodeGraphRunner(model, cache, alloc, max_model_len=max_len, buckets=(batch,))
     first = torch.randint(0, cfg.vocab_size, (batch,), generator=torch.Generator().manual_seed(
         seed + 2)).tolist()
+    model.tune_report = report
     return model, cache, runner, views, first
 
 
@@ -110,7 +112,7 @@ def gemm_roofline(model, runner, batch: int, reps: int = 5):
     launches = []
     for lw in model.layers:
         launches += [("qkv", lw.qkv, buf.normed, buf.part_qkv), ("o", lw.o, buf.attn, buf.part_o),
-                     ("gate_up", lw.gate_up, buf.normed, buf.part_gu),
+                     ("gate_up", lw.gate_up, buf.normed, "swiglu" if buf.swiglu else buf.part_gu),
                      ("down", lw.down, buf.act, buf.part_down)]
     launches.append(("lm_head", model.lm_head, buf.normed, None))
     nbytes = sum(_gemm_bytes(lin, batch) for _, lin, *_ in launches)
@@ -120,6 +122,8 @@ def gemm_roofline(model, runner, batch: int, reps: int = 5):
         for name, lin, x, part in launches:
             if part is None:
                 lin.launch(x, batch, buf.cfgs[name], out=buf.logits, part=buf.ws_lm, stream=sp)
+            elif isinstance(part, str):
+                lin.launch_swiglu(x, batch, buf.cfgs[name], buf.act, sp)
             else:
                 lin.launch(x, batch, buf.cfgs[name], part=part, stream=sp)
 
@@ -138,6 +142,149 @@ def gemm_roofline(model, runner, batch: int, reps: int = 5):
     e1.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / reps
     return nbytes / (us * 1e-6) / 1e9, nbytes, us, len(launches)
+
+
+def _time_graph(body, reps: int = 10) -> float:
+    """µs per replay of a hipGraph of `body`, HIP events on its stream. Bodies
+    hold many launches so the graph's own launch cost is amortised."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            body(s)
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            g.replay()
+        e1.record(s)
+    e1.synchronize()
+    torch.cuda.current_stream().wait_stream(s)
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def kernel_benchmarks(seed: int = 23, only_attention: bool = False) -> dict:
+    """Isolated kernels at BASELINE configurations 2 and 3 (algorithmic bytes
+    / time, HIP events around hipGraph replays)."""
+    import torch
+
+    from acorninfer_amd import _lib
+    from acorninfer_amd._lib import lib, ptr
+    from acorninfer_amd.models.qwen3 import QLinear, attention_splits
+    from acorninfer_amd.ops.quant_gemm import candidates
+
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    # ---- K3, configuration 2 --------------------------------------------
+    B, H, KV, D, P, NB = 8, 32, 8, 128, 16, 4096
+    lens = torch.randint(512, 4097, (B,), generator=torch.Generator().manual_seed(seed))
+    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(seed + 1))
+    mp = -(-int(lens.max()) // P)
+    tables = torch.zeros(B, 256, dtype=torch.int32)
+    o = 0
+    for b in range(B):
+        n = -(-int(lens[b]) // P)
+        tables[b, :n] = perm[o:o + n].to(torch.int32)
+        o += n
+    # rotate 4 pools so the 256 MB MALL cannot hold the one being read
+    pools = [(torch.randn(NB, P, KV, D, device="cuda", generator=g).bfloat16(),
+              torch.randn(NB, P, KV, D, device="cuda", generator=g).bfloat16()) for _ in range(4)]
+    q = torch.randn(B, H, D, device="cuda", generator=g).bfloat16()
+    attn_out = torch.empty_like(q)
+    tb, ln = tables.cuda(), lens.to(torch.int32).cuda()
+    S = attention_splits(B, KV, 256)
+    ws_acc = torch.empty(B * H * S * D, device="cuda")
+    ws_ml = torch.empty(2 * B * H * S, device="cuda")
+    st_code = _lib.BF16
+
+    def k3(st):
+        for kp, vp in pools * 16:
+            _lib.check(lib().acorn_paged_attention(
+                ptr(q), ptr(kp), ptr(vp), ptr(tb), ptr(ln), ptr(attn_out), ptr(ws_acc),
+                ptr(ws_ml), B, H, KV, D, P, NB, 256, S, D ** -0.5, st_code, st.cuda_stream), "K3")
+    us = _time_graph(k3) / (16 * len(pools))
+    nbytes = int(lens.sum()) * KV * D * 2 * 2 + 2 * B * H * D * 2 + 4 * sum(
+        -(-int(L) // P) for L in lens) + 4 * B
+    out["K3_config2"] = {"us": round(us, 2), "bytes": nbytes,
+                         "GBps": round(nbytes / us / 1e3, 1),
+                         "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "splits": S,
+                         "mean_ctx": round(float(lens.float().mean()), 1)}
+    del pools
+    if only_attention:
+        return out
+    # ---- K1 / K2 at configuration-2 sizes (latency-bound: µs) ----------
+    x = torch.randn(8, 4096, device="cuda", generator=g).bfloat16()
+    res = torch.randn(8, 4096, device="cuda", generator=g).bfloat16()
+    w = torch.ones(4096, device="cuda").bfloat16()
+    normed, res_out = torch.empty_like(x), torch.empty_like(x)
+
+    def k1(st):
+        for _ in range(100):
+            _lib.check(lib().acorn_fused_add_rmsnorm(ptr(x), ptr(res), ptr(res_out), ptr(w),
+                                                     ptr(normed), 8, 4096, 1e-6, _lib.BF16,
+                                                     _lib.BF16, st.cuda_stream), "K1")
+    out["K1_8x4096_us"] = round(_time_graph(k1, 5) / 100, 2)
+    qq = torch.randn(8, 32, 128, device="cuda", generator=g).bfloat16()
+    kk = torch.randn(8, 8, 128, device="cuda", generator=g).bfloat16()
+    wq = torch.ones(128, device="cuda").bfloat16()
+    pos = (lens - 1).cuda()
+    invf = (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).cuda()
+
+    def k2(st):
+        for _ in range(100):
+            _lib.check(lib().acorn_qknorm_rope_inplace(
+                ptr(qq), ptr(kk), 8, 32, 8, 128, ptr(wq), ptr(wq), 1e-6, ptr(pos), 1,
+                ptr(invf), _lib.BF16, _lib.BF16, st.cuda_stream), "K2")
+    out["K2_qknorm_rope_us"] = round(_time_graph(k2, 5) / 100, 2)
+    # ---- quant GEMM, configuration 3 -------------------------------------
+    shapes = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (24576, 4096),
+              "down": (4096, 12288)}
+    for fmt_name, wf in (("w4", _lib.WFMT_W4), ("w8", _lib.WFMT_W8)):
+        for name, (n, k) in shapes.items():
+            nsets = max(2, -(-1_200_000_000 // (n * k // (2 if wf == _lib.WFMT_W4 else 1))))
+            lins = []
+            for _ in range(nsets):
+                if wf == _lib.WFMT_W4:
+                    wq4 = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device="cuda",
+                                        generator=g)
+                    sc = (0.005 + 0.015 * torch.rand(n, k // 128, device="cuda",
+                                                     generator=g)).half()
+                    lins.append(QLinear(wf, wq4, n, k, sc))
+                else:
+                    wq8 = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda",
+                                        generator=g)
+                    sc = (0.005 + 0.015 * torch.rand(n, device="cuda", generator=g)).half()
+                    lins.append(QLinear(wf, wq8, n, k, sc))
+            for M in (1, 8, 64, 256):
+                xm = torch.randn(M, k, device="cuda", generator=g).bfloat16()
+                best = None
+                cands = candidates(M, n, k, wf) if M <= 16 else [None]
+                for c in cands:
+                    t = lins[0].plan(M, c)[0]
+                    part = torch.empty(t.ksplit, M, n, device="cuda")
+                    ob = torch.empty(M, n, device="cuda").bfloat16()
+
+                    nl = max(64, len(lins))
+
+                    def gemm(st, t=t, part=part, ob=ob, nl=nl):
+                        for i in range(nl):
+                            lins[i % len(lins)].launch(xm, M, t, out=ob, part=part,
+                                                       stream=st.cuda_stream)
+                    us = _time_graph(gemm, 3) / nl
+                    if best is None or us < best[0]:
+                        best = (us, t)
+                nb = lins[0].nbytes() + 2 * M * k + 2 * M * n
+                flops = 2 * M * n * k
+                out[f"gemm_{fmt_name}_{name}_M{M}"] = {
+                    "us": round(best[0], 2), "GBps": round(nb / best[0] / 1e3, 1),
+                    "frac_hbm": round(nb / best[0] / 1e3 / HBM_PEAK_GBS, 4),
+                    "TFLOPs": round(flops / best[0] / 1e6, 2), "tiling": tuple(best[1])}
+            del lins
+            torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(cfg, batch: int, prompt_len: int, layers: int = 2, steps: int = 2):
@@ -199,6 +346,8 @@ def main() -> None:
                     help="also measure C=1 and the W4A16 model (reported under 'extra')")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-tune", action="store_true", help="use the planner's default tilings")
+    ap.add_argument("--kernels", action="store_true",
+                    help="also time the isolated kernels at configurations 2 and 3")
     ap.add_argument("--seed", type=int, default=20261027)
     args = ap.parse_args()
 
@@ -230,7 +379,10 @@ def main() -> None:
         cfg.head_dim * 2 * 2
     extra = {"step_hbm_bound_ms": round(step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3, 4),
              "step_roofline_frac": round(step_bytes / (HBM_PEAK_GBS * 1e9) / (dt / args.steps), 4),
-             "gemm_us_per_step": round(us, 2), "gemm_launches_per_step": nl}
+             "gemm_us_per_step": round(us, 2), "gemm_launches_per_step": nl,
+             "tuned": {k: {"tiling": v["tiling"], "us": v["us"],
+                           "GBps": round(v["bytes"] / v["us"] / 1e3, 1)}
+                       for k, v in model.tune_report.items()}}
     if args.extra:
         del model, cache, runner
         torch.cuda.empty_cache()
@@ -243,6 +395,10 @@ def main() -> None:
             _log(f"{fmt} C={c}: {c * args.steps / dt2:.1f} tok/s")
             del m2, c2, r2
             torch.cuda.empty_cache()
+    if args.kernels:
+        t0 = time.perf_counter()
+        extra["kernels"] = kernel_benchmarks()
+        _log(f"kernel benchmarks in {time.perf_counter() - t0:.1f} s: {extra['kernels']}")
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()

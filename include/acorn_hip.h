@@ -152,6 +152,26 @@ int acorn_quant_gemm(const void* x, const void* w, const void* scale, const void
                      void* out_bf16, float* part, int64_t M, int64_t N, int64_t K, int wfmt,
                      const int* cfg, void* stream);
 
+/*
+ * gate|up projection with the SwiGLU activation fused into its epilogue:
+ *   act[m, j] = round(round(silu(g)) * u),  g = round(x[m] . Wg[j]), u = round(x[m] . Wu[j])
+ * (acorninfer/models/qwen3.py:392-396: F.silu(gate_proj(x)) * up_proj(x), each
+ * bf16 op rounded; silu(g) = g / (1 + exp(-g)) in fp32). No single reference
+ * function: it fuses gate_proj, up_proj and the activation of Qwen3MLP.
+ * w holds the gate and up weights interleaved in 16-row blocks: rows
+ * [32i, 32i+16) are gate rows 16i..16i+15 and rows [32i+16, 32i+32) the up
+ * rows of the same outputs (scales / zeros interleaved the same way); N is
+ * the interleaved row count (2 * intermediate), act is [M, N/2] bf16.
+ * Decode sizes only (M <= 16); cfg as for acorn_quant_gemm (rt is 2 and
+ * ksplit 1 by construction).
+ */
+int acorn_quant_gemm_swiglu(const void* x, const void* w, const void* scale, const void* zero,
+                            void* act, int64_t M, int64_t N, int64_t K, int wfmt,
+                            const int* cfg, void* stream);
+
+/* Tiling of acorn_quant_gemm_swiglu, as acorn_gemm_plan. */
+int acorn_gemm_swiglu_plan(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg);
+
 /* Deterministic split-K reduction: out[M*N] = round_T(sum_s part[s, M*N]). */
 int acorn_splitk_reduce(const float* part, int64_t nsplit, int64_t count, void* out,
                         int dtype, void* stream);
@@ -180,10 +200,12 @@ int acorn_embedding(const void* table, const int64_t* ids, void* out, int64_t ro
  * Replaces F.silu(gate_proj(x)) * up_proj(x) in acorninfer/models/qwen3.py:392-396.
  * part != NULL: g, u = round(sum_s part[s, r, .]) over `nsplit` fp32 split-K
  * partials [nsplit, rows, 2*inter] (summed in split order); otherwise
- * gate_up [rows, 2*inter] of dtype `dtype` is read. act: [rows, inter].
+ * gate_up [rows, 2*inter] of dtype `dtype` is read. Columns are [gate | up],
+ * or with interleaved16 the 16-column blocks of acorn_quant_gemm_swiglu's
+ * weight layout (gate block i at 32i, up block i at 32i+16). act: [rows, inter].
  */
 int acorn_silu_mul(const float* part, int64_t nsplit, const void* gate_up, void* act,
-                   int64_t rows, int64_t inter, int dtype, void* stream);
+                   int64_t rows, int64_t inter, int interleaved16, int dtype, void* stream);
 
 /*
  * Greedy token choice: out[r] = first index of the row maximum of x[rows, cols]

@@ -234,3 +234,50 @@ def test_every_candidate_tiling_matches(fmt, m):
             assert r <= GEMM_REL, f"{cls} {tuple(c)}: rel err {r:.3g}"
             outs.append(out)
         print(f"\n[{fmt} M={m} {cls}: {len(cands)} tilings ok]")
+
+
+def _swiglu_ref(x, wg, wu):
+    """models/qwen3.py:392-396 in bf16 torch semantics on fp32-dequantised
+    weights: each projection rounded to bf16, silu rounded, product rounded."""
+    g = (x.float() @ wg.T).bfloat16()
+    u = (x.float() @ wu.T).bfloat16()
+    return (torch.nn.functional.silu(g.float()).bfloat16().float() * u.float()).bfloat16()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["bf16", "w8", "w4"])
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_fused_swiglu_every_tiling(fmt, m):
+    """gate|up with the SwiGLU epilogue (interleaved 16-row gate/up blocks) vs
+    the oracle's separate projections + activation; every candidate tiling;
+    and the unfused path (partials + silu_mul on the interleaved layout)."""
+    import ctypes
+    from acorninfer_amd import _lib
+    from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, WFMT_W8, lib, ptr, stream_ptr
+    from acorninfer_amd.models.qwen3 import QLinear
+    from acorninfer_amd.ops.quant_gemm import candidates
+    inter, k = 1024, 4096
+    g = torch.Generator().manual_seed(31)
+    w = (0.02 * torch.randn(2 * inter, k, generator=g)).bfloat16().cuda()
+    wf = {"bf16": WFMT_BF16, "w8": WFMT_W8, "w4": WFMT_W4}[fmt]
+    lin = QLinear.from_dense(w, wf).interleaved()
+    deq = lin.dense()
+    x = (torch.randn(m, k, generator=g)).bfloat16().cuda()
+    ref = _swiglu_ref(x, deq[:inter], deq[inter:])
+    st = stream_ptr()
+    cands = candidates(m, 2 * inter, k, wf, swiglu=True)
+    assert len(cands) >= 4
+    for c in cands:
+        act = torch.full((m, inter), float("nan"), dtype=torch.bfloat16, device="cuda")
+        lin.launch_swiglu(x, m, c, act, st)
+        r = rel_err(act, ref)
+        assert r <= 1e-2, f"{tuple(c)}: rel err {r:.3g}"
+    # unfused: partials in interleaved column order -> silu_mul(il16)
+    t, _ = lin.plan(m)
+    part = torch.empty(t.ksplit, m, 2 * inter, device="cuda")
+    lin.launch(x, m, t, part=part, stream=st)
+    act2 = torch.empty(m, inter, dtype=torch.bfloat16, device="cuda")
+    _lib.check(lib().acorn_silu_mul(ptr(part), t.ksplit, None, ptr(act2), m, inter, 1,
+                                    _lib.BF16, st), "silu_mul")
+    assert rel_err(act2, ref) <= 1e-2
+    print(f"\n[swiglu {fmt} M={m}: {len(cands)} tilings ok]")
