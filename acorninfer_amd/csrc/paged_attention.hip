@@ -17,6 +17,8 @@
 //    needed;
 //  * the next chunk's K/V are loaded before the current chunk is consumed;
 //  * scores live in the log2 domain (exp2), the workspace m is log2-domain.
+#include <type_traits>
+
 #include "common.h"
 
 using namespace acorn;
@@ -422,6 +424,253 @@ __global__ __launch_bounds__(NWV * kWave) void paged_attn_wg_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA form (bf16 / fp16, D in {64, 128}): the main decode kernel.
+//
+// Per 16-token chunk of a wave:
+//  * S = q K^T on v_mfma_f32_16x16x32: A = q (the REP heads padded to 16
+//    rows; lane row = lane % 16, k = 8 * (lane / 16)), B = K^T loaded straight
+//    from the page (lane column = token lane % 16, 8 dims per k-block), D/32
+//    MFMAs. The result puts head 4*(lane/16)+i of token lane%16 in register i.
+//  * online softmax on that layout: row max / row sum over the 16 tokens with
+//    DPP; each lane row tracks (m, l) of its four heads.
+//  * P V on VALU in the row layout (lane = 8 dims of one token, 16-byte V
+//    loads); p and the rescale factors reach those lanes through a per-wave
+//    LDS slot (same-wave LDS traffic needs no barrier).
+//  * chunks are page aligned when P % 16 == 0, so a chunk costs one block-table
+//    lookup; three chunks are in flight per wave.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  if constexpr (std::is_same<T, __bf16>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return v;
+}
+
+template <typename T, int D, int REP, int NWV, bool PAGE16>
+__global__ __launch_bounds__(NWV * kWave) void paged_attn_mfma_kernel(
+    const T* __restrict__ q, const T* __restrict__ k_pages, const T* __restrict__ v_pages,
+    const int32_t* __restrict__ tables, const int32_t* __restrict__ lens, T* __restrict__ out,
+    float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l, int H,
+    int KV, int P, int num_blocks, int table_stride, int S, float scale_log2) {
+  constexpr int KB = D / 32;                   // MFMA k-blocks
+  constexpr int LPT = D / 8;                   // P V layout: lanes per token
+  constexpr int TR = kWave / LPT;              // tokens per wave-wide V load
+  constexpr int CH = 16;                       // tokens per chunk
+  constexpr int NL = CH / TR;                  // V loads per lane per chunk
+  constexpr int HG = (REP + 3) / 4;            // lane rows that hold scores
+  static_assert(REP <= 16 && NL >= 1, "unsupported shape");
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* sacc = (float*)smem;                  // [NWV][REP][D]
+  float* sm = sacc + NWV * REP * D;            // [NWV][REP]
+  float* sl = sm + NWV * REP;                  // [NWV][REP]
+  float* pl = sl + NWV * REP;                  // [NWV][CH][4*HG]  p per token and head
+  float* al = pl + NWV * CH * 4 * HG;          // [NWV][4*HG]      rescale per head
+  int* tbl = (int*)(al + NWV * 4 * HG);
+
+  const int sp = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int row = lane >> 4, col = lane & 15;  // MFMA layout
+  const int g = lane / LPT, c = lane % LPT;    // P V layout
+  float* mypl = pl + wid * CH * 4 * HG;
+  float* myal = al + wid * 4 * HG;
+
+  const int L = min(max(lens[b], 0), table_stride * P);
+  const int npages = (L + P - 1) / P;
+  const int ppw = (npages + S - 1) / S;
+  const int wp0 = min(sp * ppw, npages), wp1 = min(wp0 + ppw, npages);
+  const int32_t* trow = tables + (size_t)b * table_stride;
+  for (int i = threadIdx.x; i < wp1 - wp0; i += NWV * kWave) {
+    const unsigned pg = (unsigned)trow[wp0 + i];
+    tbl[i] = pg < (unsigned)num_blocks ? (int)pg : 0;
+  }
+  const int ppv = (wp1 - wp0 + NWV - 1) / NWV;
+  const int vp0 = min(wp0 + wid * ppv, wp1), vp1 = min(vp0 + ppv, wp1);
+  const int tstart = vp0 * P, tend = min(vp1 * P, L);
+
+  // q as the MFMA A operand (raw; the softmax scale is applied to S)
+  u32x4_t qa[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    qa[j] = u32x4_t{0u, 0u, 0u, 0u};
+    if (col < REP)
+      qa[j] = *(const u32x4_t*)(q + ((size_t)b * H + kvh * REP + col) * D + 32 * j + 8 * row);
+  }
+  float m4[4], l4[4], acc[REP][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m4[i] = -INFINITY;
+    l4[i] = 0.f;
+  }
+#pragma unroll
+  for (int h = 0; h < REP; ++h)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
+  __syncthreads();  // tbl ready
+
+  const size_t tok_stride = (size_t)KV * D;
+  struct Chunk {
+    u32x4_t k[KB];
+    u32x4_t v[NL];
+  };
+  auto token_base = [&](int t) -> size_t {
+    return ((size_t)tbl[t / P - wp0] * P + (t % P)) * tok_stride + (size_t)kvh * D;
+  };
+  auto load_chunk = [&](int t0, Chunk& ch) {
+    // K in B layout: token t0 + col, dims 32j + 8*row
+    {
+      const int t = t0 + col;
+      size_t base;
+      if constexpr (PAGE16)
+        base = ((size_t)tbl[t0 / P - wp0] * P + (t0 % P) + col) * tok_stride + (size_t)kvh * D;
+      else
+        base = t < tend ? token_base(t) : 0;
+#pragma unroll
+      for (int j = 0; j < KB; ++j) {
+        ch.k[j] = u32x4_t{0u, 0u, 0u, 0u};
+        if (t < tend) ch.k[j] = *(const u32x4_t*)(k_pages + base + 32 * j + 8 * row);
+      }
+    }
+    // V in row layout: tokens t0 + g + TR*i, dims 8c..8c+7
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int t = t0 + g + TR * i;
+      ch.v[i] = u32x4_t{0u, 0u, 0u, 0u};
+      if (t < tend) {
+        size_t base;
+        if constexpr (PAGE16)
+          base = ((size_t)tbl[t0 / P - wp0] * P + (t0 % P) + g + TR * i) * tok_stride +
+                 (size_t)kvh * D;
+        else
+          base = token_base(t);
+        ch.v[i] = *(const u32x4_t*)(v_pages + base + 8 * c);
+      }
+    }
+  };
+  auto consume = [&](int t0, const Chunk& ch) {
+    f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KB; ++j) sc = mfma16x16x32<T>(qa[j], ch.k[j], sc);
+    const bool valid = t0 + col < tend;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (4 * row + i >= 4 * HG) continue;
+      const float s = valid ? sc[i] * scale_log2 : -INFINITY;
+      const float mx = row16_max(s);           // finite: the chunk holds >= 1 token
+      const float mn = fmaxf(m4[i], mx);
+      const float alpha = exp2f(m4[i] - mn);
+      const float p = exp2f(s - mn);
+      l4[i] = l4[i] * alpha + group_sum<16>(p);
+      m4[i] = mn;
+      if (row < HG) {
+        mypl[col * 4 * HG + 4 * row + i] = p;
+        if (col == 0) myal[4 * row + i] = alpha;
+      }
+    }
+    // P V on the row layout
+    float pv[NL][REP], alph[REP];
+#pragma unroll
+    for (int h = 0; h < REP; ++h) alph[h] = myal[h];
+#pragma unroll
+    for (int i = 0; i < NL; ++i)
+#pragma unroll
+      for (int h = 0; h < REP; ++h) pv[i][h] = mypl[(g + TR * i) * 4 * HG + h];
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[h][j] *= alph[h];
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        const V8<T> vv = __builtin_bit_cast(V8<T>, ch.v[i]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[h][j] += pv[i][h] * to_f32(vv.v[j]);
+      }
+    }
+  };
+
+  {
+    Chunk ca, cb, cc;
+    if (tstart < tend) load_chunk(tstart, ca);
+    if (tstart + CH < tend) load_chunk(tstart + CH, cb);
+    if (tstart + 2 * CH < tend) load_chunk(tstart + 2 * CH, cc);
+    for (int t0 = tstart; t0 < tend; t0 += 3 * CH) {
+      consume(t0, ca);
+      if (t0 + 3 * CH < tend) load_chunk(t0 + 3 * CH, ca);
+      if (t0 + CH >= tend) break;
+      consume(t0 + CH, cb);
+      if (t0 + 4 * CH < tend) load_chunk(t0 + 4 * CH, cb);
+      if (t0 + 2 * CH >= tend) break;
+      consume(t0 + 2 * CH, cc);
+      if (t0 + 5 * CH < tend) load_chunk(t0 + 5 * CH, cc);
+    }
+  }
+  // sum the token groups' P V (all groups used the same running max)
+#pragma unroll
+  for (int h = 0; h < REP; ++h)
+#pragma unroll
+    for (int o = LPT; o < kWave; o <<= 1)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[h][j] += __shfl_xor(acc[h][j], o);
+  if (g == 0) {
+#pragma unroll
+    for (int h = 0; h < REP; ++h)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sacc[(wid * REP + h) * D + c * 8 + j] = acc[h][j];
+  }
+  if (col == 0 && row < HG) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * row + i;
+      if (h < REP) {
+        sm[wid * REP + h] = m4[i];
+        sl[wid * REP + h] = l4[i];
+      }
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < REP * D; e += NWV * kWave) {
+    const int h = e / D, d = e % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) M = fmaxf(M, sm[w * REP + h]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < NWV; ++w) {
+        const float f = exp2f(sm[w * REP + h] - M);
+        num += f * sacc[(w * REP + h) * D + d];
+        den += f * sl[w * REP + h];
+      }
+    }
+    const size_t orow = (size_t)b * H + kvh * REP + h;
+    if (S == 1) {
+      out[orow * D + d] = from_f32<T>(num / den);
+    } else {
+      const size_t slot = orow * S + sp;
+      ws_acc[slot * D + d] = num;
+      if (d == 0) {
+        ws_m[slot] = M;
+        ws_l[slot] = den;
+      }
+    }
+  }
+}
+
 // Phase 2: merge S partials of one (b, h) with the common max.
 template <typename T, int D>
 __global__ __launch_bounds__(kWave) void paged_attn_combine_kernel(
@@ -451,7 +700,26 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
   dim3 grid((unsigned)S, (unsigned)KV, (unsigned)B);
   float* ws_m = ws_ml;
   float* ws_l = ws_ml ? ws_ml + B * H * S : nullptr;
-  if constexpr (D >= 64) {
+  if constexpr (D >= 64 && !std::is_same<T, float>::value) {
+    constexpr int NWV = kAttnWaves;
+    constexpr int HG = (REP + 3) / 4;
+    const int64_t ppw = (table_stride + S - 1) / S;
+    const size_t lds = (size_t)(NWV * REP * D + 2 * NWV * REP + NWV * 16 * 4 * HG +
+                                NWV * 4 * HG) * 4 + (size_t)ppw * 4;
+    if (lds > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
+    const bool page16 = P % 16 == 0;
+    auto kfn = page16 ? paged_attn_mfma_kernel<T, D, REP, NWV, true>
+                      : paged_attn_mfma_kernel<T, D, REP, NWV, false>;
+    static bool lds_raised[2] = {false, false};
+    if (!lds_raised[page16] && lds > 64 * 1024) {
+      (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                160 * 1024);
+      lds_raised[page16] = true;
+    }
+    kfn<<<grid, dim3(NWV * kWave), lds, st>>>(
+        (const T*)q, (const T*)kp, (const T*)vp, tables, lens, (T*)out, ws_acc, ws_m, ws_l,
+        (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e);
+  } else if constexpr (D >= 64) {
     constexpr int NWV = kAttnWaves;
     const int64_t ppw = (table_stride + S - 1) / S;  // most pages one workgroup can get
     const size_t lds = (size_t)(NWV * REP * D + 2 * NWV * REP) * 4 + (size_t)ppw * 4;

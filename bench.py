@@ -45,6 +45,21 @@ def _gemm_bytes(lin, M: int) -> int:
     return lin.nbytes() + 2 * M * lin.K + 2 * M * lin.N
 
 
+def measured_traffic(fmt: str, batch: int):
+    """HBM bytes per step of the GEMM launches from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary for this workload (scaled by the copy
+    calibration), or None when no such summary exists."""
+    path = os.path.join(ROOT, "profiles", f"gemm_traffic_{fmt}_C{batch}.txt")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_step:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int, seed: int,
                    tune: bool = True):
     import torch
@@ -348,6 +363,10 @@ def main() -> None:
     ap.add_argument("--no-tune", action="store_true", help="use the planner's default tilings")
     ap.add_argument("--kernels", action="store_true",
                     help="also time the isolated kernels at configurations 2 and 3")
+    ap.add_argument("--mode", default="full", choices=["full", "step", "attention", "copy"],
+                    help="profiling workloads: 'step' = decode steps only (no JSON line), "
+                         "'attention' = K3 at configuration 2 only, 'copy' = the 1 GiB "
+                         "copy that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--seed", type=int, default=20261027)
     args = ap.parse_args()
 
@@ -360,6 +379,17 @@ def main() -> None:
     import torch
     from acorninfer_amd.config import Qwen3Config
 
+    if args.mode == "copy":
+        a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        _log("copied 1 GiB x 5")
+        return
+    if args.mode == "attention":
+        _log(f"K3 configuration 2: {kernel_benchmarks(only_attention=True)}")
+        return
     cfg = Qwen3Config.qwen3_8b()
     if args.layers:
         cfg = cfg.with_layers(args.layers)
@@ -372,6 +402,8 @@ def main() -> None:
     tok_s = args.batch * args.steps / dt
     ms = dt * 1e3 / args.steps
     _log(f"decode: {tok_s:.1f} tok/s, {ms:.3f} ms/step; last tokens {log[-1].tolist()}")
+    if args.mode == "step":
+        return
     gbs, nbytes, us, nl = gemm_roofline(model, runner, args.batch)
     _log(f"GEMM: {nl} launches/step, {nbytes / 1e9:.3f} GB, {us:.1f} us -> {gbs:.0f} GB/s")
     step_bytes = model.weight_bytes() + sum(
@@ -423,7 +455,8 @@ def main() -> None:
                    "layers": cfg.num_hidden_layers, "weights": args.format},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "wgemm_kernel (all projections of one step)",
+                     "traffic": measured_traffic(args.format, args.batch),
+                     "kernel": "wgemm_kernel (all projections of one step)",
                      "bytes_per_step": nbytes, "us_per_step": round(us, 2)},
         "cpu_baseline": cpu,
         "extra": extra,
