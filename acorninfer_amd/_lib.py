@@ -55,6 +55,7 @@ _SIGNATURES = {
     "acorn_embedding": [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "acorn_silu_mul": [_vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _vp],
     "acorn_argmax": [_vp, _i64, _i64, _vp, _i32, _vp],
+    "acorn_sample": [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "acorn_kv_scatter": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32,
                          _vp],
 }

@@ -227,6 +227,22 @@ int acorn_kv_scatter(const void* k, const void* v, void* k_pages, void* v_pages,
                      int64_t kv_heads, int64_t head_dim, int64_t page_size,
                      int64_t num_blocks, int dtype, void* stream);
 
+/*
+ * Token sampling, one row per sequence: temperature -> top-k -> top-p -> draw.
+ * Replaces acorninfer/sampler.py:38-68 (Sampler.process / Sampler.sample) and
+ * the greedy branch of engine/executor.py:128-138.
+ * logits [rows, vocab] (dtype); per row: temperature (0 = greedy argmax, logprob
+ * 0), top_k (0 = off), top_p (1 = off), uniform u in [0, 1). The token is the
+ * inverse-CDF draw of u over the kept tokens in vocabulary order; logprob is
+ * log_softmax(processed)[token]. processed (NULL or fp32 [rows, vocab]) receives
+ * x = logits / T where kept and -inf elsewhere. status[r] = 1 when the row holds
+ * NaN or +-inf (the reference raises ValueError), else 0. Deterministic.
+ */
+int acorn_sample(const void* logits, int64_t rows, int64_t vocab, int dtype,
+                 const float* temperature, const int32_t* top_k, const float* top_p,
+                 const float* uniform, int64_t* token, float* logprob, float* processed,
+                 int32_t* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
