@@ -41,13 +41,15 @@ class _Bucket:
     graph: torch.cuda.CUDAGraph | None
     pin_i64: list[torch.Tensor]       # ring of [4*bucket] int64: ids|positions|pages|slots
     pin_i32: list[torch.Tensor]       # ring of [bucket*(1+W)] int32: lens|tables
+    pin_f32: list[torch.Tensor]       # ring of [4*bucket] f32: temperature|top_p|uniform|top_k
     done: list[torch.cuda.Event | None]
     turn: int = 0
+    sampled: bool = False             # the device block holds sampling rows
 
 
 class DecodeGraphRunner:
     def __init__(self, model: Qwen3DecodeModel, cache, allocator, *, max_model_len: int,
-                 buckets: tuple[int, ...] = BUCKETS, capture: bool = True):
+                 buckets: tuple[int, ...] = BUCKETS, capture: bool = True, seed: int = 0):
         self.model = model
         self.cache = cache
         self.allocator = allocator
@@ -60,6 +62,8 @@ class DecodeGraphRunner:
         self.states: dict[int, _Bucket] = {}
         self.capture = capture
         self.last_logits: torch.Tensor | None = None
+        self.last_logprobs: torch.Tensor | None = None
+        self.rng = torch.Generator().manual_seed(seed)   # uniforms of sampled rows
 
     # ------------------------------------------------------------- construction --
     def _state(self, B: int) -> _Bucket:
@@ -73,8 +77,11 @@ class DecodeGraphRunner:
     def _build(self, bk: int) -> _Bucket:
         buf = self.model.buffers(bk, self.max_pages)
         W = self.max_pages
-        pin_i64, pin_i32 = [], []
+        pin_i64, pin_i32, pin_f32 = [], [], []
         for _ in range(MIRRORS):
+            f = torch.zeros(4 * bk, dtype=torch.float32, pin_memory=True)
+            f[bk:2 * bk] = 1.0                       # top_p off
+            pin_f32.append(f)
             a = torch.zeros(4 * bk, dtype=torch.int64, pin_memory=True)
             b = torch.zeros(bk * (1 + W), dtype=torch.int32, pin_memory=True)
             a[2 * bk:3 * bk] = self.scratch          # pages of padding rows
@@ -85,7 +92,7 @@ class DecodeGraphRunner:
         # device side starts from the same "all padding" state
         buf.flat_i64[:4 * bk].copy_(pin_i64[0].to(self.device))
         buf.flat_i32.copy_(pin_i32[0].to(self.device))
-        st = _Bucket(bk, buf, None, pin_i64, pin_i32, [None] * MIRRORS)
+        st = _Bucket(bk, buf, None, pin_i64, pin_i32, pin_f32, [None] * MIRRORS)
         if self.capture:
             self._capture(st)
         return st
@@ -114,9 +121,11 @@ class DecodeGraphRunner:
             self._body(st)
 
     # -------------------------------------------------------------- per step --
-    def _prepare(self, st: _Bucket, views, ids: list[int] | None) -> list[int]:
+    def _prepare(self, st: _Bucket, views, ids: list[int] | None, sampling=None) -> list[int]:
         """Fill the next pinned mirror and copy it to the step's buffers.
-        Returns the new lengths (pre-write + 1)."""
+        `sampling`: None (all greedy) or one SamplingParams-like (temperature,
+        top_k, top_p) per row; each sampled row draws a fresh uniform from the
+        runner's generator. Returns the new lengths (pre-write + 1)."""
         from acorninfer_amd.ops.paged_attention import build_tables
         B, bk = len(views), st.bucket
         j = st.turn % MIRRORS
@@ -146,6 +155,22 @@ class DecodeGraphRunner:
         else:
             buf.meta_i64.copy_(a[bk:4 * bk], non_blocking=True)
         buf.flat_i32.copy_(b, non_blocking=True)
+        f = st.pin_f32[j]
+        if sampling is not None or st.sampled:
+            f.zero_()
+            f[bk:2 * bk] = 1.0
+            st.sampled = False
+            if sampling is not None:
+                u = torch.rand(B, generator=self.rng)
+                for i, sp in enumerate(sampling):
+                    if sp is None or sp.temperature == 0:
+                        continue
+                    f[i] = sp.temperature
+                    f[bk + i] = sp.top_p
+                    f[2 * bk + i] = u[i]
+                    f[3 * bk:4 * bk].view(torch.int32)[i] = sp.top_k
+                    st.sampled = True
+            buf.flat_f32.copy_(f, non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(self.device))
         st.done[j] = ev
@@ -158,25 +183,36 @@ class DecodeGraphRunner:
                 v._lens[li] = n
 
     def decode_batch(self, seqs, views) -> list[int]:
-        """Greedy decode step for `views` (ids = each seq's last generated id).
-        Same arguments and result as the reference's runner."""
+        """One decode step for `views` (ids = each seq's last generated id).
+        Same arguments and result as the reference's runner; rows whose
+        `seq.sampling` has temperature > 0 are sampled inside the graph (the
+        reference routes them to eager decoding)."""
         B = len(views)
         assert 1 <= B <= self.buckets[-1], f"batch {B} exceeds the largest bucket"
         assert len(seqs) == B, "seqs and views must correspond"
         st = self._state(B)
-        self._prepare(st, views, [int(s.generated_ids[-1]) for s in seqs])
+        sampling = [getattr(s, "sampling", None) for s in seqs]
+        if all(sp is None or sp.temperature == 0 for sp in sampling):
+            sampling = None
+        self._prepare(st, views, [int(s.generated_ids[-1]) for s in seqs], sampling)
         self._run(st)
         self.last_logits = st.buf.logits
-        return st.buf.next_ids[:B].tolist()
+        self.last_logprobs = st.buf.logprob
+        toks = st.buf.next_ids[:B].tolist()
+        if sampling is not None and int(st.buf.status[:B].max()) != 0:
+            raise ValueError("logits contain NaN/inf; model forward is broken")
+        return toks
 
-    def decode_loop(self, views, first_ids: list[int], steps: int) -> torch.Tensor:
-        """`steps` greedy steps starting from `first_ids`, tokens fed back on
-        the device. Returns the int64 token log [steps, B] (one D2H copy)."""
+    def decode_loop(self, views, first_ids: list[int], steps: int, sampling=None
+                    ) -> torch.Tensor:
+        """`steps` decode steps starting from `first_ids` (greedy, or per-row
+        `sampling` params), tokens fed back on the device. Returns the int64
+        token log [steps, B] (one D2H copy)."""
         B = len(views)
         st = self._state(B)
         log = torch.empty(steps, st.bucket, dtype=torch.int64, device=self.device)
         for t in range(steps):
-            self._prepare(st, views, first_ids if t == 0 else None)
+            self._prepare(st, views, first_ids if t == 0 else None, sampling)
             self._run(st)
             log[t].copy_(st.buf.ids)               # = this step's greedy tokens
         self.last_logits = st.buf.logits

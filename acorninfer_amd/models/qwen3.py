@@ -16,7 +16,8 @@ buffers (`StepBuffers`), so it can be recorded once into a hipGraph:
       K3  paged attention (split-K over pages, GQA reuse)
       GEMM o ─► partials ─► K1 (reduce + residual add + RMSNorm)
       GEMM gate|up ─► partials ─► silu_mul ─► GEMM down ─► partials
-    final K1 (reduce + residual + norm) ─► lm_head GEMM (bf16 logits) ─► argmax
+    final K1 (reduce + residual + norm) ─► lm_head GEMM (bf16 logits) ─► sampler
+    (argmax for temperature-0 rows)
 
 Numerics are the reference's: every bf16 op of the torch path is rounded at
 the same place (projection outputs, residual adds, norm outputs, RoPE steps,
@@ -301,8 +302,9 @@ class Qwen3DecodeModel:
              num_blocks: int, page_size: int) -> None:
         """Launch one decode step on the current stream.
 
-        Reads buf.ids/positions/pages/slots/lens/tables; writes buf.logits
-        (bf16 [B, vocab]) and buf.next_ids (int64 [B], greedy). k_pool/v_pool
+        Reads buf.ids/positions/pages/slots/lens/tables and the sampling
+        block (temperature 0 = greedy); writes buf.logits (bf16 [B, vocab]),
+        buf.next_ids (int64 [B]), buf.logprob and buf.status. k_pool/v_pool
         are [layers, NB, P, KV, D]; layer l's new k/v go to
         (pages[b], slots[b]) before attention reads lens[b] tokens.
         """
@@ -369,8 +371,12 @@ class Qwen3DecodeModel:
             ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
         self.lm_head.launch(buf.normed, B, buf.cfgs["lm_head"], out=buf.logits,
                             part=buf.ws_lm, stream=st)
-        check(L.acorn_argmax(ptr(buf.logits), B, cfg.vocab_size, ptr(buf.next_ids),
-                             dtype_code(buf.logits), st), "argmax")
+        # next token: greedy rows (temperature 0) take the argmax, the others
+        # temperature -> top-k -> top-p -> inverse-CDF draw of their uniform
+        check(L.acorn_sample(ptr(buf.logits), B, cfg.vocab_size, dtype_code(buf.logits),
+                             ptr(buf.temperature), ptr(buf.top_k), ptr(buf.top_p),
+                             ptr(buf.uniform), ptr(buf.next_ids), ptr(buf.logprob), None,
+                             ptr(buf.status), st), "sample")
 
     def fused_swiglu(self, batch: int) -> bool:
         """The gate|up launch carries the SwiGLU epilogue (decode sizes, and
@@ -562,6 +568,16 @@ class StepBuffers:
         self.lens = self.flat_i32[0:B]
         self.tables = self.flat_i32[B:].view(B, self.max_pages)
         self.lens.fill_(1)
+        # sampling block: temperature | top_p | uniform | top_k (int32 bits);
+        # temperature 0 = greedy
+        self.flat_f32 = torch.zeros(4 * B, dtype=torch.float32, device=dev)
+        self.temperature = self.flat_f32[0:B]
+        self.top_p = self.flat_f32[B:2 * B]
+        self.uniform = self.flat_f32[2 * B:3 * B]
+        self.top_k = self.flat_f32[3 * B:4 * B].view(torch.int32)
+        self.top_p.fill_(1.0)
+        self.logprob = torch.zeros(B, dtype=torch.float32, device=dev)
+        self.status = torch.zeros(B, dtype=torch.int32, device=dev)
 
         def z(*shape, dtype=dt):
             return torch.zeros(*shape, dtype=dtype, device=dev)

@@ -61,7 +61,7 @@ def measured_traffic(fmt: str, batch: int):
 
 
 def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int, seed: int,
-                   tune: bool = True):
+                   tune: bool = True, prompt_lens: list[int] | None = None):
     import torch
 
     from acorninfer_amd.cache.pager import BlockAllocator, PagedCacheView, PagedKVCache
@@ -81,21 +81,22 @@ def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int,
             f"{k} {v['tiling']} {v['us']:.1f}us {v['bytes'] / v['us'] / 1e3:.0f}GB/s"
             for k, v in report.items()))
     P = 16
-    max_len = prompt_len + total_steps + 1
+    lens = prompt_lens if prompt_lens is not None else [prompt_len] * batch
+    max_len = max(lens) + total_steps + 1
     per_seq = -(-max_len // P)
-    alloc = BlockAllocator(batch * per_seq + 2)
+    alloc = BlockAllocator(sum(-(-(n + total_steps + 1) // P) for n in lens) + 2)
     cache = PagedKVCache(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim, P, alloc,
                          "cuda", torch.bfloat16)
     g = torch.Generator(device="cuda").manual_seed(seed + 1)
     cache.k_pool.normal_(generator=g)
     cache.v_pool.normal_(generator=g)
     views = []
-    for _ in range(batch):
+    for n in lens:
         v = PagedCacheView(cache)
-        for _t in range(-(-prompt_len // P)):
+        for _t in range(-(-n // P)):
             v.table.append(alloc.allocate())
         for li in range(cfg.num_hidden_layers):
-            v._lens[li] = prompt_len
+            v._lens[li] = n
         views.append(v)
     runner = DecodeGraphRunner(model, cache, alloc, max_model_len=max_len, buckets=(batch,))
     first = torch.randint(0, cfg.vocab_size, (batch,), generator=torch.Generator().manual_seed(
@@ -104,13 +105,13 @@ def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int,
     return model, cache, runner, views, first
 
 
-def time_decode(runner, views, first, steps: int, warmup: int):
+def time_decode(runner, views, first, steps: int, warmup: int, sampling=None):
     import torch
-    log = runner.decode_loop(views, first, warmup) if warmup else None
+    log = runner.decode_loop(views, first, warmup, sampling) if warmup else None
     nxt = log[-1].tolist() if warmup else first
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    log = runner.decode_loop(views, nxt, steps)
+    log = runner.decode_loop(views, nxt, steps, sampling)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     return dt, log
@@ -427,6 +428,21 @@ def main() -> None:
             _log(f"{fmt} C={c}: {c * args.steps / dt2:.1f} tok/s")
             del m2, c2, r2
             torch.cuda.empty_cache()
+        # configuration 5 at C=8: W4A16, prompts U[1024, 8192], sampled
+        from acorninfer_amd.sampler import SamplingParams
+        plens = torch.randint(1024, 8193, (8,), generator=torch.Generator().manual_seed(
+            args.seed + 5)).tolist()
+        m2, c2, r2, v2, f2 = build_workload(cfg, "w4a16", 8, 0, total, args.seed,
+                                            tune=not args.no_tune, prompt_lens=plens)
+        sp = [SamplingParams(temperature=0.6, top_p=0.95, top_k=20)] * 8
+        dt2, _ = time_decode(r2, v2, f2, args.steps, args.warmup, sampling=sp)
+        extra["w4a16_C8_long_sampled_tok_s"] = round(8 * args.steps / dt2, 2)
+        extra["w4a16_C8_long_sampled_ms_per_step"] = round(dt2 * 1e3 / args.steps, 4)
+        extra["w4a16_C8_long_sampled_mean_ctx"] = round(sum(plens) / 8, 1)
+        _log(f"w4a16 C=8 long sampled (mean ctx {sum(plens) / 8:.0f}): "
+             f"{8 * args.steps / dt2:.1f} tok/s")
+        del m2, c2, r2
+        torch.cuda.empty_cache()
     if args.kernels:
         t0 = time.perf_counter()
         extra["kernels"] = kernel_benchmarks()

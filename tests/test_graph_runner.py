@@ -125,3 +125,37 @@ def test_decode_loop_matches_decode_batch(model):
         cur = runner2.decode_batch([SimpleNamespace(generated_ids=[i]) for i in cur], views2)
         assert log[t].tolist() == cur
     assert [v.seq_len for v in views] == [v.seq_len for v in views2]
+
+
+@pytest.mark.gpu
+def test_sampled_rows_inside_the_graph(model):
+    """Rows with temperature > 0 are sampled inside the captured step (the
+    reference falls back to eager for them): greedy rows take the argmax of
+    the step's logits; sampled rows take the oracle's processed distribution
+    and inverse-CDF draw for the runner's seeded uniform."""
+    from acorninfer_amd.sampler import SamplingParams
+    from oracle.sampler_ref import draw_ref, process_ref
+    prompts = _prompts()[:3]
+    alloc, cache = new_cache(model, 64)
+    views = [PagedCacheView(cache) for _ in prompts]
+    ids = [int(feed_prompt(model, v, p).argmax()) for v, p in zip(views, prompts)]
+    runner = DecodeGraphRunner(model, cache, alloc, max_model_len=256, seed=5)
+    rng = torch.Generator().manual_seed(5)
+    sps = [SamplingParams(temperature=0.7, top_p=0.95, top_k=20), None,
+           SamplingParams(temperature=1.0, top_p=0.9, top_k=50)]
+    for step in range(4):
+        seqs = [SimpleNamespace(generated_ids=[ids[i]], sampling=sps[i]) for i in range(3)]
+        toks = runner.decode_batch(seqs, views)
+        u = torch.rand(3, generator=rng)
+        logits = runner.last_logits[:3].float().cpu()
+        for i, sp in enumerate(sps):
+            if sp is None:
+                assert toks[i] == int(logits[i].argmax())
+            else:
+                want = process_ref(logits[i], sp.temperature, sp.top_k, sp.top_p)
+                assert toks[i] == draw_ref(want, float(u[i]))[0]
+        ids = toks
+    # a greedy-only step after sampled ones resets the device sampling block
+    seqs = [SimpleNamespace(generated_ids=[i]) for i in ids]
+    toks = runner.decode_batch(seqs, views)
+    assert toks == runner.last_logits[:3].float().argmax(1).tolist()
