@@ -3,9 +3,13 @@
 // Semantics follow acorninfer/ops/paged_attention.py:125-152 (kernel
 // :33-122, oracle :192-216): for each (b, h) out = softmax(q . K^T * scale) V
 // over tokens 0..L_b-1, token t stored at (tables[b, t/P], t%P), kv head
-// h / (H/KV). Splits are page aligned: split sp covers pages
-// [sp*pps, (sp+1)*pps) with pps = ceil(ceil(L/P)/S); an empty split writes
-// (m=-inf, l=0, acc=0) and contributes nothing to the merge.
+// h / (H/KV). Splits are page aligned and of one size per launch: split sp
+// covers pages [sp*pps, (sp+1)*pps) with pps = ceil(table_stride / S), so a
+// sequence uses nsb = ceil(ceil(L/P) / pps) splits and every workgroup has at
+// most the same pps pages of work. Splits past nsb exit at once; a sequence
+// with nsb = 1 gets its output written directly, the others' partials
+// (log2-domain max m, sum l, unnormalised acc) are merged by the combine
+// kernel.
 //
 // MI355X design (not the reference's per-q-head grid):
 //  * one wavefront per (split, kv head, sequence) serves all REP = H/KV query
@@ -29,6 +33,11 @@ constexpr int kChunk = 16;  // tokens per step
 constexpr int kLPT = 4;     // lanes per token in the q.k phase
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kAttnWaves = 8;  // waves per workgroup of the single-kernel form
+constexpr int kOneWavePages = 16;  // MFMA form: splits of at most this many pages use one wave
+#ifndef ACORN_K3_ONE_WAVE_DEPTH
+#define ACORN_K3_ONE_WAVE_DEPTH 3
+#endif
+constexpr int kOneWaveDepth = ACORN_K3_ONE_WAVE_DEPTH;  // chunks in flight per one-wave split
 
 template <typename T, int N>
 struct Vec {
@@ -64,7 +73,9 @@ __global__ __launch_bounds__(kWave) void paged_attn_split_kernel(
   // caller's buffers (valid inputs are unaffected).
   const int L = min(max(lens[b], 0), table_stride * P);
   const int npages = (L + P - 1) / P;
-  const int pps = (npages + S - 1) / S;
+  const int pps = (table_stride + S - 1) / S;            // pages per split
+  const int nsb = max(1, (npages + pps - 1) / pps);      // splits this sequence uses
+  if (sp >= nsb) return;
   const int start = sp * pps * P;
   const int end = min(start + pps * P, L);
   const int32_t* trow = tables + (size_t)b * table_stride;
@@ -172,15 +183,14 @@ __global__ __launch_bounds__(kWave) void paged_attn_split_kernel(
     }
   }
 
-  // ---- write this split's partial (or the final output when S == 1) ------
+  // ---- write this split's partial (or the final output for one split) ----
 #pragma unroll
   for (int h = 0; h < REP; ++h) l_run[h] = wave_sum(l_run[h]);
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
     const int hq = kvh * REP + h;
     const size_t row = (size_t)b * H + hq;
-    if (S == 1) {
-      // start < end always holds for S == 1 (L >= 1).
+    if (nsb == 1) {
       const float inv = 1.0f / l_run[h];
       if (pv_active) {
 #pragma unroll
@@ -263,8 +273,10 @@ __global__ __launch_bounds__(NWV * kWave) void paged_attn_wg_kernel(
 
   const int L = min(max(lens[b], 0), table_stride * P);
   const int npages = (L + P - 1) / P;
-  const int ppw = (npages + S - 1) / S;        // pages per workgroup split
-  const int wp0 = min(sp * ppw, npages), wp1 = min(wp0 + ppw, npages);
+  const int pps = (table_stride + S - 1) / S;            // pages per split
+  const int nsb = max(1, (npages + pps - 1) / pps);      // splits this sequence uses
+  if (sp >= nsb) return;                                 // uniform over the workgroup
+  const int wp0 = sp * pps, wp1 = min(wp0 + pps, npages);
   const int32_t* trow = tables + (size_t)b * table_stride;
   for (int i = threadIdx.x; i < wp1 - wp0; i += NWV * kWave) {
     const unsigned pg = (unsigned)trow[wp0 + i];
@@ -411,7 +423,7 @@ __global__ __launch_bounds__(NWV * kWave) void paged_attn_wg_kernel(
       }
     }
     const size_t row = (size_t)b * H + kvh * REP + h;
-    if (S == 1) {
+    if (nsb == 1) {
       out[row * D + d] = from_f32<T>(num / den);
     } else {
       const size_t slot = row * S + sp;
@@ -427,22 +439,39 @@ __global__ __launch_bounds__(NWV * kWave) void paged_attn_wg_kernel(
 // ---------------------------------------------------------------------------
 // MFMA form (bf16 / fp16, D in {64, 128}): the main decode kernel.
 //
-// Per 16-token chunk of a wave:
-//  * S = q K^T on v_mfma_f32_16x16x32: A = q (the REP heads padded to 16
-//    rows; lane row = lane % 16, k = 8 * (lane / 16)), B = K^T loaded straight
-//    from the page (lane column = token lane % 16, 8 dims per k-block), D/32
-//    MFMAs. The result puts head 4*(lane/16)+i of token lane%16 in register i.
-//  * online softmax on that layout: row max / row sum over the 16 tokens with
-//    DPP; each lane row tracks (m, l) of its four heads.
-//  * P V on VALU in the row layout (lane = 8 dims of one token, 16-byte V
-//    loads); p and the rescale factors reach those lanes through a per-wave
-//    LDS slot (same-wave LDS traffic needs no barrier).
-//  * chunks are page aligned when P % 16 == 0, so a chunk costs one block-table
-//    lookup; three chunks are in flight per wave.
+// A workgroup of NWV waves serves one (split, kv head, sequence); the waves
+// divide the split's pages. Per 16-token chunk of a wave, with lane = 16 r + c:
+//  * S^T = K q^T on v_mfma_f32_16x16x32: A = K straight from the page (row =
+//    token c, 8 dims per k-block), B = q^T (column = head c; the REP heads are
+//    padded to 16 with zero rows of q), D/32 MFMAs. Register i of lane (r, c)
+//    then holds the score of head c for token 4 r + i.
+//  * online softmax in that layout. A head's running max m moves only when a
+//    score exceeds it by more than kMaxSlack (log2 units): most chunks then
+//    need no cross-lane max and no rescale, and p = 2^(s - m) stays below
+//    2^kMaxSlack. p is rounded to T and l sums the rounded values, so the
+//    output is the p-weighted mean of V up to fp32 accumulation.
+//  * O^T += V^T P^T on v_mfma_f32_16x16x16: B = the p of lane (r, c) as it
+//    stands (head c, tokens 4 r .. 4 r + 3); A = V^T, for which lane (r, c)
+//    loads dims [c D/16, (c + 1) D/16) of tokens 4 r .. 4 r + 3 and
+//    transposes them in registers with v_perm (output row c of MFMA b is dim
+//    c D/16 + b). Register i of accumulator b of lane (r, c) holds dim
+//    D/16 (4 r + i) + b of head c.
+//  * chunks are page aligned when P % 16 == 0: one block-table lookup per
+//    chunk (wave-uniform), and a chunk's loads stay inside its page, so only a
+//    sequence's last chunk can be partial; there the rows past the end are
+//    masked (scores to -inf, V rows to zero, so stale cache contents cannot
+//    reach the sum). Three chunks are in flight per wave.
+// At the end the waves' (m, l, acc) are merged in LDS and the output (or this
+// split's partial for the combine kernel) is written.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kMaxSlack = 8.0f;
 
 template <typename T>
 __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
@@ -454,192 +483,251 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
                                                    __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp<0xB1>(v));
-  v = fmaxf(v, dpp<0x4E>(v));
-  v = fmaxf(v, dpp<0x141>(v));
-  v = fmaxf(v, dpp<0x140>(v));
-  return v;
+template <typename T>
+__device__ __forceinline__ f32x4_t mfma16x16x16(u32x2_t a, u32x2_t b, f32x4_t c) {
+  if constexpr (std::is_same<T, __bf16>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a),
+                                                      __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
+                                                  __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
 }
 
-template <typename T, int D, int REP, int NWV, bool PAGE16>
-__global__ __launch_bounds__(NWV * kWave) void paged_attn_mfma_kernel(
+// Two values already on T's grid, packed lo | hi << 16.
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const T a = (T)lo, b = (T)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+template <typename T, int D, int REP, int NWV, bool PAGE16, int DEPTH = 3>
+__global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) void paged_attn_mfma_kernel(
     const T* __restrict__ q, const T* __restrict__ k_pages, const T* __restrict__ v_pages,
     const int32_t* __restrict__ tables, const int32_t* __restrict__ lens, T* __restrict__ out,
     float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l, int H,
     int KV, int P, int num_blocks, int table_stride, int S, float scale_log2) {
-  constexpr int KB = D / 32;                   // MFMA k-blocks
-  constexpr int LPT = D / 8;                   // P V layout: lanes per token
-  constexpr int TR = kWave / LPT;              // tokens per wave-wide V load
+  constexpr int KB = D / 32;                   // q.k MFMA k-blocks
+  constexpr int DPL = D / 16;                  // P V: dims per lane per token = MFMAs per chunk
+  constexpr int VW = DPL / 2;                  // ... in 32-bit words
   constexpr int CH = 16;                       // tokens per chunk
-  constexpr int NL = CH / TR;                  // V loads per lane per chunk
-  constexpr int HG = (REP + 3) / 4;            // lane rows that hold scores
-  static_assert(REP <= 16 && NL >= 1, "unsupported shape");
+  static_assert(REP <= 16 && (D == 64 || D == 128), "unsupported shape");
   extern __shared__ __align__(16) unsigned char smem[];
   float* sacc = (float*)smem;                  // [NWV][REP][D]
   float* sm = sacc + NWV * REP * D;            // [NWV][REP]
   float* sl = sm + NWV * REP;                  // [NWV][REP]
-  float* pl = sl + NWV * REP;                  // [NWV][CH][4*HG]  p per token and head
-  float* al = pl + NWV * CH * 4 * HG;          // [NWV][4*HG]      rescale per head
-  int* tbl = (int*)(al + NWV * 4 * HG);
+  int* tbl = (int*)(sl + NWV * REP);
 
-  const int sp = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int row = lane >> 4, col = lane & 15;  // MFMA layout
-  const int g = lane / LPT, c = lane % LPT;    // P V layout
-  float* mypl = pl + wid * CH * 4 * HG;
-  float* myal = al + wid * 4 * HG;
+  // kv head fastest in the grid: the KV workgroups of one split read the same
+  // pages (the heads of a token are adjacent in a page) at about the same time
+  const int kvh = blockIdx.x, sp = blockIdx.y, b = blockIdx.z;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int r = lane >> 4, c = lane & 15;
+  const int pshift = __builtin_ctz(P);
 
-  const int L = min(max(lens[b], 0), table_stride * P);
-  const int npages = (L + P - 1) / P;
-  const int ppw = (npages + S - 1) / S;
-  const int wp0 = min(sp * ppw, npages), wp1 = min(wp0 + ppw, npages);
+  // The partition is fixed per launch (pps pages per split, ppv per wave),
+  // so a wave's block ids are requested together with the length.
+  const int pps = (table_stride + S - 1) / S;
+  const int ppv = (pps + NWV - 1) / NWV;
+  const int wp0 = sp * pps;
+  const int vn0 = wp0 + wid * ppv;                   // the wave's first page, if any
+  const bool reg_pages = ppv <= kWave;               // one block id per lane
   const int32_t* trow = tables + (size_t)b * table_stride;
-  for (int i = threadIdx.x; i < wp1 - wp0; i += NWV * kWave) {
-    const unsigned pg = (unsigned)trow[wp0 + i];
-    tbl[i] = pg < (unsigned)num_blocks ? (int)pg : 0;
+  int pgr = 0;
+  if (reg_pages && lane < ppv && vn0 + lane < min(wp0 + pps, table_stride))
+    pgr = trow[vn0 + lane];
+  const int L = min(max(lens[b], 0), table_stride * P);
+  const int npages = (L + P - 1) >> pshift;
+  const int nsb = max(1, (npages + pps - 1) / pps);  // splits this sequence uses
+  if (sp >= nsb) return;                             // uniform over the workgroup
+  const int wp1 = min(wp0 + pps, npages);
+  pgr = (unsigned)pgr < (unsigned)num_blocks ? pgr : 0;
+  if (!reg_pages) {
+    for (int i = threadIdx.x; i < wp1 - wp0; i += NWV * kWave) {
+      const unsigned pg = (unsigned)trow[wp0 + i];
+      tbl[i] = pg < (unsigned)num_blocks ? (int)pg : 0;
+    }
   }
-  const int ppv = (wp1 - wp0 + NWV - 1) / NWV;
-  const int vp0 = min(wp0 + wid * ppv, wp1), vp1 = min(vp0 + ppv, wp1);
-  const int tstart = vp0 * P, tend = min(vp1 * P, L);
+  const int vp0 = min(vn0, wp1), vp1 = min(vp0 + ppv, wp1);
+  const int tstart = vp0 << pshift, tend = min(vp1 << pshift, L);
 
-  // q as the MFMA A operand (raw; the softmax scale is applied to S)
-  u32x4_t qa[KB];
+  // q^T as the B operand (raw; the softmax scale is applied to S)
+  u32x4_t qb[KB];
 #pragma unroll
   for (int j = 0; j < KB; ++j) {
-    qa[j] = u32x4_t{0u, 0u, 0u, 0u};
-    if (col < REP)
-      qa[j] = *(const u32x4_t*)(q + ((size_t)b * H + kvh * REP + col) * D + 32 * j + 8 * row);
+    qb[j] = u32x4_t{0u, 0u, 0u, 0u};
+    if (c < REP)
+      qb[j] = *(const u32x4_t*)(q + ((size_t)b * H + kvh * REP + c) * D + 32 * j + 8 * r);
   }
-  float m4[4], l4[4], acc[REP][8];
+  float m = -INFINITY, l = 0.f;
+  f32x4_t acc[DPL];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m4[i] = -INFINITY;
-    l4[i] = 0.f;
-  }
-#pragma unroll
-  for (int h = 0; h < REP; ++h)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
-  __syncthreads();  // tbl ready
+  for (int j = 0; j < DPL; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  if (!reg_pages) __syncthreads();  // tbl ready
+  // Prefetches past the wave's last chunk are still issued (an unconditional
+  // load count keeps the wait counts static): they read one line of the last
+  // chunk with every lane.
+  const int tlast = tstart + max(tend - tstart - 1, 0) / CH * CH;
 
-  const size_t tok_stride = (size_t)KV * D;
+  const int tok_stride = KV * D;
+  const int k_off = c * tok_stride + 8 * r;          // this lane's K row / dims
+  const int v_off = 4 * r * tok_stride + DPL * c;    // this lane's V rows / dims
   struct Chunk {
     u32x4_t k[KB];
-    u32x4_t v[NL];
+    uint32_t v[4][VW];
   };
-  auto token_base = [&](int t) -> size_t {
-    return ((size_t)tbl[t / P - wp0] * P + (t % P)) * tok_stride + (size_t)kvh * D;
+  auto page_base = [&](int t) -> size_t {            // element offset of token t's row
+    // every lane calls this (the shuffle reads other lanes' registers)
+    const int pg = reg_pages ? __shfl(pgr, (t >> pshift) - vp0) : tbl[(t >> pshift) - wp0];
+    return ((size_t)pg * P + (t & (P - 1))) * tok_stride + (size_t)kvh * D;
   };
   auto load_chunk = [&](int t0, Chunk& ch) {
-    // K in B layout: token t0 + col, dims 32j + 8*row
-    {
-      const int t = t0 + col;
-      size_t base;
-      if constexpr (PAGE16)
-        base = ((size_t)tbl[t0 / P - wp0] * P + (t0 % P) + col) * tok_stride + (size_t)kvh * D;
-      else
-        base = t < tend ? token_base(t) : 0;
+    const bool spare = t0 > tlast;
+    t0 = min(t0, tlast);
+    if constexpr (PAGE16) {
+      // the whole chunk lies in one page: a uniform base, per-lane offsets
+      const int pi = (t0 >> pshift) - vp0;
+      const int pg = reg_pages ? __builtin_amdgcn_readlane(pgr, pi)
+                               : __builtin_amdgcn_readfirstlane(tbl[pi + vp0 - wp0]);
+      const size_t base = ((size_t)pg * P + (t0 & (P - 1))) * tok_stride + (size_t)kvh * D;
+      const T* kb = k_pages + base + (spare ? 0 : k_off);
+      const T* vb = v_pages + base + (spare ? 0 : v_off);
+      const int vstep = spare ? 0 : tok_stride;
 #pragma unroll
-      for (int j = 0; j < KB; ++j) {
-        ch.k[j] = u32x4_t{0u, 0u, 0u, 0u};
-        if (t < tend) ch.k[j] = *(const u32x4_t*)(k_pages + base + 32 * j + 8 * row);
+      for (int j = 0; j < KB; ++j) ch.k[j] = *(const u32x4_t*)(kb + (spare ? 0 : 32 * j));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) __builtin_memcpy(ch.v[j], vb + j * vstep, sizeof(ch.v[j]));
+    } else {
+      // pages smaller than a chunk: one lookup per token, rows past the end
+      // read as zero
+      const int tk = t0 + c;
+      const size_t kbase = page_base(min(tk, tend - 1));
+#pragma unroll
+      for (int j = 0; j < KB; ++j) ch.k[j] = u32x4_t{0u, 0u, 0u, 0u};
+      if (tk < tend) {
+        const T* kb = k_pages + kbase + 8 * r;
+#pragma unroll
+        for (int j = 0; j < KB; ++j) ch.k[j] = *(const u32x4_t*)(kb + 32 * j);
       }
-    }
-    // V in row layout: tokens t0 + g + TR*i, dims 8c..8c+7
 #pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int t = t0 + g + TR * i;
-      ch.v[i] = u32x4_t{0u, 0u, 0u, 0u};
-      if (t < tend) {
-        size_t base;
-        if constexpr (PAGE16)
-          base = ((size_t)tbl[t0 / P - wp0] * P + (t0 % P) + g + TR * i) * tok_stride +
-                 (size_t)kvh * D;
-        else
-          base = token_base(t);
-        ch.v[i] = *(const u32x4_t*)(v_pages + base + 8 * c);
+      for (int j = 0; j < 4; ++j) {
+        const int tv = t0 + 4 * r + j;
+        const size_t vbase = page_base(min(tv, tend - 1));
+#pragma unroll
+        for (int w = 0; w < VW; ++w) ch.v[j][w] = 0u;
+        if (tv < tend)
+          __builtin_memcpy(ch.v[j], v_pages + vbase + DPL * c, sizeof(ch.v[j]));
       }
     }
   };
-  auto consume = [&](int t0, const Chunk& ch) {
+  auto consume = [&](int t0, Chunk& ch) {
     f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < KB; ++j) sc = mfma16x16x32<T>(qa[j], ch.k[j], sc);
-    const bool valid = t0 + col < tend;
+    for (int j = 0; j < KB; ++j) sc = mfma16x16x32<T>(ch.k[j], qb[j], sc);
+    float s[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (4 * row + i >= 4 * HG) continue;
-      const float s = valid ? sc[i] * scale_log2 : -INFINITY;
-      const float mx = row16_max(s);           // finite: the chunk holds >= 1 token
-      const float mn = fmaxf(m4[i], mx);
-      const float alpha = exp2f(m4[i] - mn);
-      const float p = exp2f(s - mn);
-      l4[i] = l4[i] * alpha + group_sum<16>(p);
-      m4[i] = mn;
-      if (row < HG) {
-        mypl[col * 4 * HG + 4 * row + i] = p;
-        if (col == 0) myal[4 * row + i] = alpha;
+    for (int i = 0; i < 4; ++i) s[i] = sc[i] * scale_log2;
+    if (t0 + CH > tend) {                      // the sequence's last chunk
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (t0 + 4 * r + i >= tend) {
+          s[i] = -INFINITY;
+#pragma unroll
+          for (int w = 0; w < VW; ++w) ch.v[i][w] = 0u;
+        }
       }
     }
-    // P V on the row layout
-    float pv[NL][REP], alph[REP];
+    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    // row 0 holds token t0 < tend, so the head max below is finite
+    if (__builtin_amdgcn_ballot_w64(mx > m + kMaxSlack) != 0) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);
+      m = mn;
+      l *= alpha;
 #pragma unroll
-    for (int h = 0; h < REP; ++h) alph[h] = myal[h];
+      for (int j = 0; j < DPL; ++j) acc[j] *= alpha;
+    }
+    float p[4];
 #pragma unroll
-    for (int i = 0; i < NL; ++i)
+    for (int i = 0; i < 4; ++i) {
+      p[i] = round_to<T>(__builtin_amdgcn_exp2f(s[i] - m));
+      l += p[i];
+    }
+    const u32x2_t pb = {pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3])};
 #pragma unroll
-      for (int h = 0; h < REP; ++h) pv[i][h] = mypl[(g + TR * i) * 4 * HG + h];
-#pragma unroll
-    for (int h = 0; h < REP; ++h) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[h][j] *= alph[h];
-#pragma unroll
-      for (int i = 0; i < NL; ++i) {
-        const V8<T> vv = __builtin_bit_cast(V8<T>, ch.v[i]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[h][j] += pv[i][h] * to_f32(vv.v[j]);
-      }
+    for (int j = 0; j < DPL; ++j) {
+      // element j of each of the lane's four V rows: word j/2, half j%2
+      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+      const u32x2_t va = {__builtin_amdgcn_perm(ch.v[1][j / 2], ch.v[0][j / 2], sel),
+                          __builtin_amdgcn_perm(ch.v[3][j / 2], ch.v[2][j / 2], sel)};
+      acc[j] = mfma16x16x16<T>(va, pb, acc[j]);
     }
   };
 
-  {
-    Chunk ca, cb, cc;
-    if (tstart < tend) load_chunk(tstart, ca);
-    if (tstart + CH < tend) load_chunk(tstart + CH, cb);
-    if (tstart + 2 * CH < tend) load_chunk(tstart + 2 * CH, cc);
-    for (int t0 = tstart; t0 < tend; t0 += 3 * CH) {
-      consume(t0, ca);
-      if (t0 + 3 * CH < tend) load_chunk(t0 + 3 * CH, ca);
-      if (t0 + CH >= tend) break;
-      consume(t0 + CH, cb);
-      if (t0 + 4 * CH < tend) load_chunk(t0 + 4 * CH, cb);
-      if (t0 + 2 * CH >= tend) break;
-      consume(t0 + 2 * CH, cc);
-      if (t0 + 5 * CH < tend) load_chunk(t0 + 5 * CH, cc);
+  if (tstart < tend) {
+    // DEPTH chunks in flight: chunk slot i is refilled right after use
+    Chunk cs[DEPTH];
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i) load_chunk(tstart + i * CH, cs[i]);
+    bool more = true;
+    for (int t0 = tstart; more; t0 += DEPTH * CH) {
+#pragma unroll
+      for (int i = 0; i < DEPTH; ++i) {
+        if (more) {
+          consume(t0 + i * CH, cs[i]);
+          load_chunk(t0 + (i + DEPTH) * CH, cs[i]);
+          more = t0 + (i + 1) * CH < tend;
+        }
+      }
     }
   }
-  // sum the token groups' P V (all groups used the same running max)
+  // l: each lane summed its own tokens; add the four lane rows of a head
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if constexpr (NWV == 1) {
+    // a one-wave split writes its result straight from the accumulators:
+    // lane (r, c < REP) holds dims DPL (4 r + i) + j of head c
+    if (c < REP) {
+      const size_t orow = (size_t)b * H + kvh * REP + c;
+      if (nsb == 1) {
+        const float inv = 1.0f / l;
 #pragma unroll
-  for (int h = 0; h < REP; ++h)
+        for (int i = 0; i < 4; ++i) {
+          uint32_t w[VW];
 #pragma unroll
-    for (int o = LPT; o < kWave; o <<= 1)
+          for (int j = 0; j < VW; ++j)
+            w[j] = pack2<T>(acc[2 * j][i] * inv, acc[2 * j + 1][i] * inv);
+          __builtin_memcpy(out + orow * D + DPL * (4 * r + i), w, sizeof(w));
+        }
+      } else {
+        const size_t slot = orow * S + sp;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[h][j] += __shfl_xor(acc[h][j], o);
-  if (g == 0) {
+        for (int i = 0; i < 4; ++i) {
+          float f[DPL];
 #pragma unroll
-    for (int h = 0; h < REP; ++h)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sacc[(wid * REP + h) * D + c * 8 + j] = acc[h][j];
-  }
-  if (col == 0 && row < HG) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * row + i;
-      if (h < REP) {
-        sm[wid * REP + h] = m4[i];
-        sl[wid * REP + h] = l4[i];
+          for (int j = 0; j < DPL; ++j) f[j] = acc[j][i];
+          __builtin_memcpy(ws_acc + slot * D + DPL * (4 * r + i), f, sizeof(f));
+        }
+        if (r == 0) {
+          ws_m[slot] = m;
+          ws_l[slot] = l;
+        }
       }
+    }
+    return;
+  }
+  if (c < REP) {
+    float* dst = sacc + (wid * REP + c) * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) dst[DPL * (4 * r + i) + j] = acc[j][i];
+    if (r == 0) {
+      sm[wid * REP + c] = m;
+      sl[wid * REP + c] = l;
     }
   }
   __syncthreads();
@@ -658,7 +746,7 @@ __global__ __launch_bounds__(NWV * kWave) void paged_attn_mfma_kernel(
       }
     }
     const size_t orow = (size_t)b * H + kvh * REP + h;
-    if (S == 1) {
+    if (nsb == 1) {
       out[orow * D + d] = from_f32<T>(num / den);
     } else {
       const size_t slot = orow * S + sp;
@@ -671,24 +759,87 @@ __global__ __launch_bounds__(NWV * kWave) void paged_attn_mfma_kernel(
   }
 }
 
-// Phase 2: merge S partials of one (b, h) with the common max.
+// Phase 2: merge the partials of one (b, h) with the common max.
+// Only sequences that used more than one split have partials; the kernels
+// above wrote the others' output directly.
+//
+// One workgroup of kCombineWaves waves per (b, h), built so that one round
+// trip to memory suffices for up to kWave splits: the length, every split's
+// (m, l) (lane s) and each wave's share of the partial rows (s = wave,
+// wave + kCombineWaves, ...) are all requested before any of them is used;
+// slots past the sequence's split count are masked by selection, so stale
+// workspace contents never reach the sums. The waves' sums are added in LDS
+// in a fixed order.
+constexpr int kCombineWaves = 4;
+
 template <typename T, int D>
-__global__ __launch_bounds__(kWave) void paged_attn_combine_kernel(
+__global__ __launch_bounds__(kCombineWaves * kWave) void paged_attn_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
-    const float* __restrict__ ws_l, T* __restrict__ out, int S) {
+    const float* __restrict__ ws_l, T* __restrict__ out, const int32_t* __restrict__ lens,
+    int H, int P, int table_stride, int S) {
+  constexpr int DL = (D + kWave - 1) / kWave;        // dims per lane
+  constexpr int SPW = kWave / kCombineWaves;         // slots per wave per round
+  __shared__ float part[kCombineWaves][D];
   const size_t row = blockIdx.x;
-  const int lane = threadIdx.x;
-  float mx = -INFINITY;
-  for (int s = lane; s < S; s += kWave) mx = fmaxf(mx, ws_m[row * S + s]);
-  mx = wave_max(mx);  // finite: split 0 is never empty (L >= 1)
-  float lsum = 0.f;
-  for (int s = lane; s < S; s += kWave) lsum += exp2f(ws_m[row * S + s] - mx) * ws_l[row * S + s];
-  lsum = wave_sum(lsum);
+  const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int d0 = lane * DL;
+  const float* m = ws_m + row * S;
+  const float* l = ws_l + row * S;
+  const float* src = ws_acc + row * S * D;
+  const int pps = (table_stride + S - 1) / S;
+  float a[DL];
+#pragma unroll
+  for (int i = 0; i < DL; ++i) a[i] = 0.f;
+  float M = -INFINITY, lsum = 0.f;
+  int nsb = 0;
+  for (int s0 = 0; s0 < S; s0 += kWave) {
+    // ---- requests: length, (m, l) of slots s0 + lane, this wave's rows ----
+    const int L = min(max(lens[row / H], 0), table_stride * P);
+    const bool have = s0 + lane < S;
+    const float ml = have ? m[s0 + lane] : -INFINITY;
+    const float ll = have ? l[s0 + lane] : 0.f;
+    float x[SPW][DL];
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {
+      const int s = s0 + wid + kCombineWaves * k;
+#pragma unroll
+      for (int i = 0; i < DL; ++i)
+        x[k][i] = (s < S && d0 + i < D) ? src[(size_t)s * D + d0 + i] : 0.f;
+    }
+    // ---- use ----
+    nsb = ((L + P - 1) / P + pps - 1) / pps;
+    if (nsb <= 1) return;                            // uniform over the workgroup
+    const bool used = s0 + lane < nsb;
+    const float mv = used ? ml : -INFINITY;
+    const float Mr = wave_max(mv);                   // finite when s0 < nsb
+    if (s0 >= nsb) break;
+    const float Mn = fmaxf(M, Mr);
+    const float scale_old = exp2f(M - Mn);           // 0 on the first round
+    const float wl = used ? exp2f(ml - Mn) : 0.f;
+    lsum = lsum * scale_old + wave_sum(used ? wl * ll : 0.f);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) a[i] *= scale_old;
+    M = Mn;
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {
+      const int s = s0 + wid + kCombineWaves * k;
+      const float w = __shfl(wl, wid + kCombineWaves * k);
+      if (s < nsb) {
+#pragma unroll
+        for (int i = 0; i < DL; ++i) a[i] += w * x[k][i];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < DL; ++i)
+    if (d0 + i < D) part[wid][d0 + i] = a[i];
+  __syncthreads();
   const float inv = 1.0f / lsum;
-  for (int d = lane; d < D; d += kWave) {
-    float a = 0.f;
-    for (int s = 0; s < S; ++s) a += exp2f(ws_m[row * S + s] - mx) * ws_acc[(row * S + s) * D + d];
-    out[row * D + d] = from_f32<T>(a * inv);
+  for (int d = threadIdx.x; d < D; d += kCombineWaves * kWave) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kCombineWaves; ++w) t += part[w][d];
+    out[row * D + d] = from_f32<T>(t * inv);
   }
 }
 
@@ -701,22 +852,30 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
   float* ws_m = ws_ml;
   float* ws_l = ws_ml ? ws_ml + B * H * S : nullptr;
   if constexpr (D >= 64 && !std::is_same<T, float>::value) {
-    constexpr int NWV = kAttnWaves;
-    constexpr int HG = (REP + 3) / 4;
-    const int64_t ppw = (table_stride + S - 1) / S;
-    const size_t lds = (size_t)(NWV * REP * D + 2 * NWV * REP + NWV * 16 * 4 * HG +
-                                NWV * 4 * HG) * 4 + (size_t)ppw * 4;
+    // small splits run as one-wave workgroups (many independent work units
+    // that the dispatcher spreads over the CUs); large ones as NWV waves
+    // merged in LDS
+    const int64_t pps = (table_stride + S - 1) / S;
+    const bool one = pps <= kOneWavePages;
+    const int nwv = one ? 1 : kAttnWaves;
+    const size_t lds = (size_t)(nwv * REP * D + 2 * nwv * REP) * 4 + (size_t)pps * 4;
     if (lds > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
     const bool page16 = P % 16 == 0;
-    auto kfn = page16 ? paged_attn_mfma_kernel<T, D, REP, NWV, true>
-                      : paged_attn_mfma_kernel<T, D, REP, NWV, false>;
-    static bool lds_raised[2] = {false, false};
-    if (!lds_raised[page16] && lds > 64 * 1024) {
+    const int which = (one ? 2 : 0) + (page16 ? 1 : 0);
+    using KFn = void (*)(const T*, const T*, const T*, const int32_t*, const int32_t*, T*, float*,
+                         float*, float*, int, int, int, int, int, int, float);
+    const KFn fns[4] = {paged_attn_mfma_kernel<T, D, REP, kAttnWaves, false>,
+                        paged_attn_mfma_kernel<T, D, REP, kAttnWaves, true>,
+                        paged_attn_mfma_kernel<T, D, REP, 1, false, kOneWaveDepth>,
+                        paged_attn_mfma_kernel<T, D, REP, 1, true, kOneWaveDepth>};
+    const KFn kfn = fns[which];
+    static bool lds_raised[4] = {false, false, false, false};
+    if (!lds_raised[which] && lds > 64 * 1024) {
       (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 160 * 1024);
-      lds_raised[page16] = true;
+      lds_raised[which] = true;
     }
-    kfn<<<grid, dim3(NWV * kWave), lds, st>>>(
+    kfn<<<dim3((unsigned)KV, (unsigned)S, (unsigned)B), dim3(nwv * kWave), lds, st>>>(
         (const T*)q, (const T*)kp, (const T*)vp, tables, lens, (T*)out, ws_acc, ws_m, ws_l,
         (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e);
   } else if constexpr (D >= 64) {
@@ -741,8 +900,8 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
   }
   ACORN_LAUNCH_CHECK();
   if (S > 1) {
-    paged_attn_combine_kernel<T, D><<<dim3((unsigned)(B * H)), dim3(kWave), 0, st>>>(
-        ws_acc, ws_m, ws_l, (T*)out, (int)S);
+    paged_attn_combine_kernel<T, D><<<dim3((unsigned)(B * H)), dim3(kCombineWaves * kWave), 0, st>>>(
+        ws_acc, ws_m, ws_l, (T*)out, lens, (int)H, (int)P, (int)table_stride, (int)S);
     ACORN_LAUNCH_CHECK();
   }
   return ACORN_OK;

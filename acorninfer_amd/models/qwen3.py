@@ -512,21 +512,23 @@ def _dense_linear(w: torch.Tensor, dtype: torch.dtype) -> QLinear:
     raise ValueError(f"no dense weight format for activations of dtype {dtype}")
 
 
-ATTN_WAVES = 8   # waves per K3 workgroup (csrc/paged_attention.hip kAttnWaves)
+UNIT_PAGES = 4      # K3 split size the heuristic aims for (pages)
+MAX_SPLITS = 64     # bound on K3 splits per (sequence, kv head)
 
 
 def attention_splits(batch: int, kv_heads: int, max_pages: int, *,
-                     pages_per_wave: int = 8, max_workgroups: int = 1024) -> int:
-    """K3 workgroup splits per (sequence, kv head) for a captured bucket.
+                     unit_pages: int = UNIT_PAGES, max_splits: int = MAX_SPLITS) -> int:
+    """K3 split count S for block tables `max_pages` wide.
 
-    One workgroup's ATTN_WAVES waves already divide a sequence's pages, so
-    the sequence is split across workgroups (merged by the combine launch)
-    only when every wave would otherwise get more than `pages_per_wave`
-    pages, and never beyond `max_workgroups` workgroups in total. Fixed per
-    bucket: splits past a sequence's last page are empty."""
-    want = -(-max_pages // (ATTN_WAVES * pages_per_wave))
-    cap = max(1, max_workgroups // max(1, batch * kv_heads))
-    return max(1, min(want, cap))
+    K3 gives every split the same pps = ceil(max_pages / S) pages, so a
+    sequence of n pages uses ceil(n / pps) splits and the rest exit at once.
+    Small splits (here `unit_pages`, 64 tokens at P = 16) run as one-wave
+    workgroups: many equal work units that the dispatcher spreads evenly over
+    the CUs, whatever the mix of context lengths. S is capped at `max_splits`
+    (workspace B*H*S*(D+2) floats; the combine reads one partial per used
+    split), so very wide tables get proportionally larger splits."""
+    del batch, kv_heads  # the unit size, not the grid, sets the balance
+    return max(1, min(-(-max_pages // unit_pages), max_splits))
 
 
 @dataclass

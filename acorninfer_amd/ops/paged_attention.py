@@ -70,9 +70,8 @@ def num_splits_for(B: int, num_heads: int, *, sm_count: int = _SM_COUNT,
 
 
 def plan_splits(B: int, kv_heads: int, max_pages: int, **kw) -> int:
-    """Workgroup split count for the MI355X kernel (see
-    models.qwen3.attention_splits): split a sequence across workgroups only
-    when each of a workgroup's waves would otherwise hold many pages."""
+    """Split count for the MI355X kernel (models.qwen3.attention_splits):
+    splits of a few pages each, up to a bound on the workspace."""
     from acorninfer_amd.models.qwen3 import attention_splits
     return attention_splits(B, kv_heads, max_pages, **kw)
 

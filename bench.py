@@ -182,7 +182,8 @@ def _time_graph(body, reps: int = 10) -> float:
     return e0.elapsed_time(e1) * 1e3 / reps
 
 
-def kernel_benchmarks(seed: int = 23, only_attention: bool = False) -> dict:
+def kernel_benchmarks(seed: int = 23, only_attention: bool = False,
+                      attn_splits: list[int] | None = None) -> dict:
     """Isolated kernels at BASELINE configurations 2 and 3 (algorithmic bytes
     / time, HIP events around hipGraph replays)."""
     import torch
@@ -212,18 +213,25 @@ def kernel_benchmarks(seed: int = 23, only_attention: bool = False) -> dict:
     attn_out = torch.empty_like(q)
     tb, ln = tables.cuda(), lens.to(torch.int32).cuda()
     S = attention_splits(B, KV, 256)
-    ws_acc = torch.empty(B * H * S * D, device="cuda")
-    ws_ml = torch.empty(2 * B * H * S, device="cuda")
+    smax = max([S] + list(attn_splits or []))
+    ws_acc = torch.empty(B * H * smax * D, device="cuda")
+    ws_ml = torch.empty(2 * B * H * smax, device="cuda")
     st_code = _lib.BF16
 
-    def k3(st):
-        for kp, vp in pools * 16:
-            _lib.check(lib().acorn_paged_attention(
-                ptr(q), ptr(kp), ptr(vp), ptr(tb), ptr(ln), ptr(attn_out), ptr(ws_acc),
-                ptr(ws_ml), B, H, KV, D, P, NB, 256, S, D ** -0.5, st_code, st.cuda_stream), "K3")
-    us = _time_graph(k3) / (16 * len(pools))
+    def k3_us(nsplit):
+        def k3(st):
+            for kp, vp in pools * 16:
+                _lib.check(lib().acorn_paged_attention(
+                    ptr(q), ptr(kp), ptr(vp), ptr(tb), ptr(ln), ptr(attn_out), ptr(ws_acc),
+                    ptr(ws_ml), B, H, KV, D, P, NB, 256, nsplit, D ** -0.5, st_code,
+                    st.cuda_stream), "K3")
+        return _time_graph(k3) / (16 * len(pools))
+
+    us = k3_us(S)
     nbytes = int(lens.sum()) * KV * D * 2 * 2 + 2 * B * H * D * 2 + 4 * sum(
         -(-int(L) // P) for L in lens) + 4 * B
+    if attn_splits:
+        out["K3_config2_split_sweep_us"] = {n: round(k3_us(n), 2) for n in attn_splits}
     out["K3_config2"] = {"us": round(us, 2), "bytes": nbytes,
                          "GBps": round(nbytes / us / 1e3, 1),
                          "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "splits": S,
@@ -364,6 +372,8 @@ def main() -> None:
     ap.add_argument("--no-tune", action="store_true", help="use the planner's default tilings")
     ap.add_argument("--kernels", action="store_true",
                     help="also time the isolated kernels at configurations 2 and 3")
+    ap.add_argument("--splits", default="",
+                    help="with --mode attention: comma-separated K3 split counts to time")
     ap.add_argument("--mode", default="full", choices=["full", "step", "attention", "copy"],
                     help="profiling workloads: 'step' = decode steps only (no JSON line), "
                          "'attention' = K3 at configuration 2 only, 'copy' = the 1 GiB "
@@ -389,7 +399,8 @@ def main() -> None:
         _log("copied 1 GiB x 5")
         return
     if args.mode == "attention":
-        _log(f"K3 configuration 2: {kernel_benchmarks(only_attention=True)}")
+        sweep = [int(x) for x in args.splits.split(",")] if args.splits else None
+        _log(f"K3 configuration 2: {kernel_benchmarks(only_attention=True, attn_splits=sweep)}")
         return
     cfg = Qwen3Config.qwen3_8b()
     if args.layers:

@@ -28,6 +28,9 @@ CONFIGS = [
     (2, 16, 8, 128, 16, [129, 260], 5),
     (2, 8, 8, 64, 16, [50, 3], 3),
     (2, 64, 8, 128, 16, [100, 31], 2),
+    (2, 32, 8, 128, 4, [37, 70], 3),
+    (2, 16, 8, 64, 8, [45, 19], 2),
+    (1, 8, 1, 128, 32, [95], 1),
 ]
 
 
@@ -71,6 +74,39 @@ def test_matches_oracle_half(dtype):
         worst = max(worst, max_abs_diff(out, ref))
         torch.testing.assert_close(out, ref, **TOL_BF16)
     print(f"\n[paged_attn {dtype} max|diff| = {worst:.3g}]")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("direction", [1.0, -1.0])
+def test_score_ramps(dtype, direction):
+    """Scores that climb (or fall) by ~100 nats along the context: the
+    running max moves in many chunks of every wave, so the rescale path is
+    exercised throughout, with scores far outside any fixed window."""
+    g = torch.Generator().manual_seed(5)
+    B, H, KV, D, P, lens = 2, 32, 8, 128, 16, [700, 1000]
+    nb = 2 * 63 + 2
+    u = torch.ones(D) / D ** 0.5
+    q = torch.randn(B, H, D, generator=g) + 2.0 * D ** 0.5 * u
+    k_pages = torch.randn(nb, P, KV, D, generator=g)
+    v_pages = torch.randn(nb, P, KV, D, generator=g)
+    perm = torch.randperm(nb, generator=g)
+    tables = torch.zeros(B, 63, dtype=torch.int32)
+    off = 0
+    for b, L in enumerate(lens):
+        n = -(-L // P)
+        tables[b, :n] = perm[off:off + n].to(torch.int32)
+        for t in range(L):
+            ramp = (t / L) if direction > 0 else (1.0 - t / L)
+            k_pages[int(tables[b, t // P]), t % P] += 40.0 * ramp * u
+        off += n
+    args = (q.to(dtype), k_pages.to(dtype), v_pages.to(dtype), tables,
+            torch.tensor(lens, dtype=torch.int32))
+    ref = paged_attention_ref(*args)
+    for S in (1, 3):
+        out = _run(*args, S)
+        assert torch.isfinite(out).all()
+        torch.testing.assert_close(out, ref, **TOL_BF16)
 
 
 @pytest.mark.gpu
