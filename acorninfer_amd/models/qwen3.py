@@ -46,6 +46,41 @@ MI355X_CUS = 256
 FORMATS = {"bf16": WFMT_BF16, "w8a16": WFMT_W8, "w4a16": WFMT_W4}
 
 
+def dispatch_linear(mod, x: torch.Tensor) -> torch.Tensor:
+    """The reference model's single entry for every projection and lm_head
+    (acorninfer/models/qwen3.py:21-47), for callers that keep the reference's
+    nn.Module model and quantise it with quant.apply_quant:
+
+    - no `_m7_quant` marker: `mod(x)` (the module's own forward, unchanged);
+    - "w8a16": quant_gemm(x, int8 weight, `_q_scale`, cls), cls looked up by
+      the weight's (N, K) in `_CLS_BY_SHAPE` (an unknown shape is a
+      ValueError, as in the reference);
+    - "w4a16": quant_gemm_w4 on the packed weight (the reference rejects this
+      mode; this build supports it, apply_quant sets it);
+    - any other marker: ValueError.
+    The result takes x's leading shape."""
+    mode = getattr(mod, "_m7_quant", None)
+    if mode is None:
+        return mod(x)
+    from acorninfer_amd.ops.quant_gemm import _CLS_BY_SHAPE, quant_gemm, quant_gemm_w4
+    w = mod.weight.data
+    if mode == "w8a16":
+        N, K = w.shape
+    elif mode == "w4a16":
+        N, K = w.shape[0], 2 * w.shape[1]
+    else:
+        raise ValueError(f"dispatch_linear: unsupported _m7_quant={mode!r}")
+    cls = _CLS_BY_SHAPE.get((N, K))
+    if cls is None:
+        raise ValueError(f"dispatch_linear: quantized linear shape {(N, K)} is not one of "
+                         f"the CLASSES (apply_quant targets the production 8B shapes)")
+    if mode == "w8a16":
+        out = quant_gemm(x, w, mod._q_scale, cls)
+    else:
+        out = quant_gemm_w4(x, w, mod._q_scale, None, cls)
+    return out.view(*x.shape[:-1], N)
+
+
 # --------------------------------------------------------------------------- weights --
 
 @dataclass

@@ -107,3 +107,28 @@ def build_tables(views, page_size: int, device, *, lens_override=None,
     if out is not None:
         return t, lens_t
     return t.to(device), lens_t.to(device)
+
+
+def paged_decode_attention_ref(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                               tables: torch.Tensor, seq_lens: torch.Tensor) -> torch.Tensor:
+    """Plain torch statement of K3's contract, exported because the reference
+    module exports one (acorninfer/ops/paged_attention.py:192-216): for each
+    sequence, gather tokens 0..L-1 from (tables[b, t // P], t % P), map q head
+    h to kv head h // (H / KV), softmax(q.K^T * D^-0.5) V in fp32, cast to
+    q.dtype. Device-agnostic; the GPU op above never calls it."""
+    B, H, D = q.shape
+    P, KV = k_pages.shape[1], k_pages.shape[2]
+    group = H // KV
+    out = torch.empty_like(q)
+    for b in range(B):
+        L = int(seq_lens[b])
+        t = torch.arange(L, device=k_pages.device)
+        blocks = tables[b].to(k_pages.device).long()[t // P]
+        k = k_pages[blocks, t % P].float()                     # [L, KV, D]
+        v = v_pages[blocks, t % P].float()
+        k = k.permute(1, 0, 2).repeat_interleave(group, dim=0)  # [H, L, D]
+        v = v.permute(1, 0, 2).repeat_interleave(group, dim=0)
+        scores = torch.bmm(k, q[b].float().unsqueeze(-1)).squeeze(-1) * D ** -0.5   # [H, L]
+        p = torch.softmax(scores, dim=-1)
+        out[b] = torch.bmm(p.unsqueeze(1), v).squeeze(1).to(q.dtype)
+    return out

@@ -56,3 +56,15 @@ def fused_add_rmsnorm_partials(part: torch.Tensor, residual: torch.Tensor | None
         ptr(part), S, ptr(residual), ptr(residual_out), ptr(weight), ptr(normed), ptr(x_out),
         rows, H, float(eps), dtype_code(normed), dtype_code(weight), stream_ptr(part.device))
     check(rc, "fused_add_rmsnorm_partials")
+
+
+def fused_add_rmsnorm_ref(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor,
+                          eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """Plain torch statement of the K1 contract, exported because the
+    reference module exports one (acorninfer/ops/rmsnorm.py:74-82) and its
+    callers' tests import it from here. Device-agnostic; the GPU op above never
+    calls it. The residual add is in x's dtype; the norm is fp32 then cast."""
+    res = x if residual is None else residual + x
+    f = res.float()
+    scale = torch.rsqrt(f.square().mean(dim=-1, keepdim=True) + eps)
+    return (f * scale * weight.float()).to(x.dtype), res.to(x.dtype)

@@ -60,3 +60,20 @@ def qknorm_rope_inplace(q: torch.Tensor, k: torch.Tensor, q_w: torch.Tensor,
         float(eps), ptr(pos), int(pos.dtype == torch.int64), ptr(inv), dtype_code(q),
         dtype_code(q_w), stream_ptr(q.device))
     check(rc, "qknorm_rope_inplace")
+
+
+def fused_rope_ref(x: torch.Tensor, positions: torch.Tensor,
+                   inv_freq: torch.Tensor) -> torch.Tensor:
+    """Plain torch statement of the RoPE contract on x [B, H, 1, D], exported
+    because the reference module exports one (acorninfer/ops/rope.py:116-125).
+    Angles pos * inv_freq in fp32; cos and sin are rounded to x.dtype; the
+    rotate-half products and their sum are in x.dtype. The GPU op above never
+    calls it."""
+    ang = positions.to(device=x.device, dtype=torch.float32)[:, None] * \
+        inv_freq.to(device=x.device, dtype=torch.float32)[None, :]
+    ang = torch.cat([ang, ang], dim=-1)                        # [B, D]
+    cos = ang.cos().to(x.dtype).view(x.shape[0], 1, 1, -1)
+    sin = ang.sin().to(x.dtype).view(x.shape[0], 1, 1, -1)
+    half = x.shape[-1] // 2
+    rotated = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+    return x * cos + rotated * sin
