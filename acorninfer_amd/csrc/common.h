@@ -35,10 +35,13 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
 __device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
 
+// Two floats -> a bf16 pair (round to nearest even), lo in the low half; the
+// vector conversion selects one v_cvt_pk_bf16_f32.
+typedef __bf16 acorn_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float acorn_f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  __bf16 a = (__bf16)lo, b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) |
-         ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  const acorn_f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, acorn_bf16x2));
 }
 
 // ---- wavefront reductions -----------------------------------------------

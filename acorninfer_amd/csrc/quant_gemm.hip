@@ -406,6 +406,225 @@ __global__ __launch_bounds__(256) void f32_gemv_kernel(const float* __restrict__
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tiled form for M > 16, where the product is a dense contraction rather
+// than a weight stream:
+//  * a workgroup of 4 waves owns a BN (N) x BM (M) output tile and one K
+//    range (split blockIdx.y); each wave a BN/2 x BM/2 quarter (2 x 2
+//    waves). A K step is BK = 8192 / BN wide (BN 128: 64, BN 64: 128), so a
+//    thread always loads 32 consecutive k of one weight row per step;
+//  * per K step the weights are dequantised once into LDS as bf16
+//    and x is staged beside them, both double-buffered with one barrier per
+//    step; the global loads of the next DP steps are in flight (a ring of DP
+//    register stages) while the MFMAs run. DP divides the step count, so
+//    the loop has no data-dependent branch and the wait counts are static;
+//    prefetches past the last step re-read it.
+//    LDS rows are padded by 8 bf16 so the 16 rows of an MFMA operand fetch
+//    spread over the banks;
+//  * dequantisation: int8 -> bf16(q) exactly, the channel scale applied to
+//    the fp32 result; int4 -> bf16(u * s + z) per 128-group (z = -8 s for
+//    the symmetric form), one rounding per weight, as a dequantise-then-dot
+//    kernel does; bf16 as is;
+//  * v_mfma_f32_16x16x32_bf16 with W as A (rows n) and x as B (columns m);
+//  * output as in the streaming form: bf16 when ksplit == 1, else fp32
+//    partials [ksplit, M, N].
+constexpr int kTileKN = 8192;                          // BN * BK
+
+template <int WFMT, int BM, int BN, int DP>
+__global__ __launch_bounds__(256) void wgemm_tile_kernel(KArgs a) {
+  constexpr int BK = kTileKN / BN, KP = BK + 8;       // K step, LDS row pitch (bf16)
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int MB = WM / 16, NB = WN / 16;          // 16x16 blocks per wave
+  constexpr int CPR = BK / 8;                         // 16-byte x chunks per row per step
+  constexpr int XR = BM * CPR / 256;                  // 16-byte x loads per thread per step
+  constexpr int TPR = 256 / BN;                       // threads per weight row
+  constexpr int WR = WFMT == ACORN_WFMT_W4 ? 1 : WFMT == ACORN_WFMT_W8 ? 2 : 4;
+  static_assert(XR >= 1 && MB >= 1 && NB >= 1 && BK / TPR == 32, "unsupported tile");
+  extern __shared__ __align__(16) unsigned char smem[];
+  __bf16* xs = (__bf16*)smem;                         // [2][BM][KP]
+  __bf16* wsm = xs + 2 * BM * KP;                     // [2][BN][KP]
+  _Float16* gsl = (_Float16*)(wsm + 2 * BN * KP);     // int4: [BN][G] scales, then zeros
+
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  const int r = lane >> 4, c = lane & 15;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.z * BM;
+  const int K = a.K;
+  const int kper = K / a.ksplit, kb = blockIdx.y * kper, nsteps = kper / BK;
+  const int wn = (wid & 1) * WN, wm = (wid >> 1) * WM;
+  const int wrow = tid / TPR, wpart = tid % TPR;      // this thread's weight row / 32-k part
+
+  struct Stage {
+    u32x4 x[XR], w[WR];
+  };
+  // int4: the tile's group scales (and zeros) for this K range, loaded once
+  const int G = kper / 128;
+  if constexpr (WFMT == ACORN_WFMT_W4) {
+    // eight independent loads in flight per thread per round
+    for (int i0 = 0; i0 < BN * G; i0 += 256 * 8) {
+      _Float16 sv[8], zv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = min(i0 + tid + 256 * u, BN * G - 1);
+        const size_t gi = (size_t)(n0 + i / G) * (K / 128) + kb / 128 + i % G;
+        sv[u] = a.scale[gi];
+        zv[u] = a.zero ? a.zero[gi] : (_Float16)0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + tid + 256 * u;
+        if (i < BN * G) {
+          gsl[i] = sv[u];
+          gsl[BN * G + i] = zv[u];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  auto gload = [&](int s, Stage& st) {
+    const int k0 = kb + min(s, nsteps - 1) * BK;
+    u32x4 (&xr)[XR] = st.x;
+    u32x4 (&wr)[WR] = st.w;
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+      // rows past M re-read row M-1 (no branch, so the wait counts stay
+      // static); their outputs are never stored
+      const int q = tid + 256 * j, row = q / CPR, ch = q % CPR, m = min(m0 + row, a.M - 1);
+      xr[j] = *(const u32x4*)(a.x + (size_t)m * K + k0 + 8 * ch);
+    }
+    const size_t wk = (size_t)(n0 + wrow) * K + k0 + 32 * wpart;   // weight element index
+    if constexpr (WFMT == ACORN_WFMT_W4) {
+      wr[0] = *(const u32x4*)(a.w + wk / 2);
+    } else if constexpr (WFMT == ACORN_WFMT_W8) {
+#pragma unroll
+      for (int j = 0; j < WR; ++j) wr[j] = *(const u32x4*)(a.w + wk + 16 * j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < WR; ++j) wr[j] = *(const u32x4*)(a.w + 2 * (wk + 8 * j));
+    }
+  };
+  auto lstore = [&](int s, const Stage& st) {
+    const u32x4 (&xr)[XR] = st.x;
+    const u32x4 (&wr)[WR] = st.w;
+    __bf16* xd = xs + (s & 1) * BM * KP;
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+      const int q = tid + 256 * j, row = q / CPR, ch = q % CPR;
+      *(u32x4*)(xd + row * KP + 8 * ch) = xr[j];
+    }
+    __bf16* wd = wsm + (s & 1) * BN * KP + wrow * KP + 32 * wpart;
+    if constexpr (WFMT == ACORN_WFMT_W4) {
+      const int g = (min(s, nsteps - 1) * BK + 32 * wpart) / 128;
+      const float gs = (float)gsl[wrow * G + g];
+      const float gz = a.zero ? (float)gsl[BN * G + wrow * G + g] : -8.f * gs;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        // nibbles k = 8d .. 8d+7 (low nibble = even k) -> bf16(u * s + z)
+        const uint32_t w = wr[0][d];
+        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        u32x4 o;
+        o[0] = pack_bf16x2(ubyte_f32<0>(lo) * gs + gz, ubyte_f32<0>(hi) * gs + gz);
+        o[1] = pack_bf16x2(ubyte_f32<1>(lo) * gs + gz, ubyte_f32<1>(hi) * gs + gz);
+        o[2] = pack_bf16x2(ubyte_f32<2>(lo) * gs + gz, ubyte_f32<2>(hi) * gs + gz);
+        o[3] = pack_bf16x2(ubyte_f32<3>(lo) * gs + gz, ubyte_f32<3>(hi) * gs + gz);
+        *(u32x4*)(wd + 8 * d) = o;
+      }
+    } else if constexpr (WFMT == ACORN_WFMT_W8) {
+#pragma unroll
+      for (int j = 0; j < WR; ++j) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          // 8 signed bytes -> bf16(q), exact; ^0x80 then -128 keeps the
+          // conversion on v_cvt_f32_ubyteN
+          const uint32_t lo = wr[j][2 * h] ^ 0x80808080u, hi = wr[j][2 * h + 1] ^ 0x80808080u;
+          u32x4 o;
+          o[0] = pack_bf16x2(ubyte_f32<0>(lo) - 128.f, ubyte_f32<1>(lo) - 128.f);
+          o[1] = pack_bf16x2(ubyte_f32<2>(lo) - 128.f, ubyte_f32<3>(lo) - 128.f);
+          o[2] = pack_bf16x2(ubyte_f32<0>(hi) - 128.f, ubyte_f32<1>(hi) - 128.f);
+          o[3] = pack_bf16x2(ubyte_f32<2>(hi) - 128.f, ubyte_f32<3>(hi) - 128.f);
+          *(u32x4*)(wd + 16 * j + 8 * h) = o;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < WR; ++j) *(u32x4*)(wd + 8 * j) = wr[j];
+    }
+  };
+
+  f32x4 acc[NB][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int s) {
+    const __bf16* xd = xs + (s & 1) * BM * KP;
+    const __bf16* wd = wsm + (s & 1) * BN * KP;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 32) {
+      u32x4 af[NB], bfr[MB];
+#pragma unroll
+      for (int i = 0; i < NB; ++i) af[i] = *(const u32x4*)(wd + (wn + 16 * i + c) * KP + kk + 8 * r);
+#pragma unroll
+      for (int j = 0; j < MB; ++j) bfr[j] = *(const u32x4*)(xd + (wm + 16 * j + c) * KP + kk + 8 * r);
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j) acc[i][j] = mfma(af[i], bfr[j], acc[i][j]);
+    }
+  };
+
+  // step t's registers live in ring[t % DP]
+  Stage ring[DP];
+#pragma unroll
+  for (int d = 0; d < DP; ++d) gload(d, ring[d]);
+  lstore(0, ring[0]);
+  __syncthreads();
+  for (int s0 = 0; s0 < nsteps; s0 += DP) {
+#pragma unroll
+    for (int d = 0; d < DP; ++d) {
+      const int s = s0 + d;
+      if constexpr (DP > 1) gload(s + DP, ring[d]);   // ring[d] went to LDS last step
+      compute(s);
+      if constexpr (DP == 1) gload(s + 1, ring[0]);
+      lstore(s + 1, ring[(d + 1) % DP]);              // harmless past the end
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue ----
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int n = n0 + wn + 16 * i + 4 * r;
+    float sc[4] = {1.f, 1.f, 1.f, 1.f};
+    if constexpr (WFMT == ACORN_WFMT_W8) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[e] = (float)a.scale[n + e];
+    }
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int m = m0 + wm + 16 * j + c;
+      if (m >= a.M) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = sc[e] * acc[i][j][e];
+      if (a.out) {
+        uint32_t p[2] = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        __builtin_memcpy(a.out + (size_t)m * a.N + n, p, sizeof(p));
+      } else {
+        float* dst = a.part + ((size_t)blockIdx.y * a.M + m) * a.N + n;
+        *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
+      }
+    }
+  }
+}
+
+size_t tile_lds_bytes(int wfmt, int bm, int bn, int64_t kper) {
+  const int kp = kTileKN / bn + 8;
+  size_t b = (size_t)2 * (bm + bn) * kp * 2;
+  if (wfmt == ACORN_WFMT_W4) b += (size_t)2 * bn * (kper / 128) * 2;  // scales + zeros
+  return b;
+}
+
 // Split-K reduction (fixed order) with the output cast.
 template <typename T>
 __global__ void splitk_reduce_kernel(const float* __restrict__ part, int nsplit, size_t count,
@@ -424,6 +643,7 @@ struct Tiling {
   int mt, R, nk, ntiles, mblocks, groups;
   size_t lds;
   int swiglu;                    // fused SwiGLU epilogue (rt == 2, ksplit == 1)
+  int kind;                      // 0 = streaming kernel, 1 = tiled kernel (rt == 0, upw = BM)
 };
 
 int ilog2_ceil(int v) {
@@ -453,12 +673,69 @@ size_t lds_bytes(int wfmt, int mt, int R, int rt, int nw, int KR) {
   return b;
 }
 
+// Tiled kernel plan (M > 16). Request: BM in upw (32 / 64 / 128), BN in nw
+// (64 / 128), 0 = choose (BN 64 for M <= 64, else 128; BM from M). The K
+// split keeps every split on whole K steps (int4: whole 128-k groups). By
+// default it grows until about two workgroups per CU are launched, while each
+// split keeps at least 256 k and, for M <= 64 (weight-bound), the fp32
+// partials (written and read again, 8*ksplit*M*N bytes) stay below half the
+// weight bytes.
+int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int req_bn,
+                   int req_ks, Tiling* t) {
+  const int bn = (req_bn == 64 || req_bn == 128) ? req_bn : M <= 64 ? 64 : 128;
+  if (N % bn) return ACORN_ERR_UNSUPPORTED;
+  const int bk = kTileKN / bn;
+  const int align = wfmt == ACORN_WFMT_W4 ? std::max(128, bk) : bk;
+  if (K % align) return ACORN_ERR_SHAPE;
+  const int bm = (req_bm == 32 || req_bm == 64 || req_bm == 128) ? req_bm
+                 : M <= 32 ? 32 : M <= 64 ? 64 : 128;
+  const int64_t units = K / align;
+  t->kind = 1;
+  t->rt = 0;
+  t->upw = bm;
+  t->nw = bn;
+  t->tpw = 1;
+  t->mt = 0;
+  t->R = 0;
+  t->swiglu = 0;
+  t->ntiles = (int)(N / bn);
+  t->mblocks = (int)((M + bm - 1) / bm);
+  t->groups = t->ntiles;
+  int64_t ks;
+  if (req_ks > 0) {
+    ks = req_ks;
+    while (ks <= units && units % ks) ++ks;
+    if (ks > units) return ACORN_ERR_UNSUPPORTED;
+  } else {
+    ks = 1;
+    const int64_t tiles = (int64_t)t->ntiles * t->mblocks;
+    const double wbytes = (double)N * K * (wfmt == ACORN_WFMT_W4 ? 0.5 : wfmt == ACORN_WFMT_W8 ? 1 : 2);
+    while (tiles * ks < 2 * kCUs) {
+      int64_t nx = ks + 1;
+      while (nx <= units && units % nx) ++nx;
+      if (nx > units || K / nx < 256) break;
+      if (M <= 64 && 8.0 * nx * M * N > 0.5 * wbytes) break;  // weight-bound: keep partials small
+      ks = nx;
+    }
+  }
+  t->ksplit = (int)ks;
+  t->nk = (int)(K / ks / bk);
+  t->lds = tile_lds_bytes(wfmt, bm, bn, K / ks);
+  if (t->lds > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
+  if (t->ksplit > 65535 || t->mblocks > 65535 || t->ntiles > 0x7fffffff) return ACORN_ERR_SHAPE;
+  return ACORN_OK;
+}
+
 // cfg: {rt, upw, nw, ksplit, tpw}; 0 = choose. swiglu: fused SwiGLU epilogue,
-// which fixes rt = 2 and ksplit = 1.
+// which fixes rt = 2 and ksplit = 1. For M > 16 an rt of 0 selects the tiled
+// kernel (upw = its BM), rt >= 1 the streaming kernel.
 int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling* t,
               bool swiglu = false) {
   if (M <= 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   t->swiglu = swiglu;
+  t->kind = 0;
+  if (M > 16 && !swiglu && (!cfg || cfg[0] <= 0))
+    return make_tile_plan(M, N, K, wfmt, cfg ? cfg[1] : 0, cfg ? cfg[2] : 0, cfg ? cfg[3] : 0, t);
   if (swiglu && (M > 16 || N % 32)) return ACORN_ERR_UNSUPPORTED;
   const int ku = ku_of(wfmt);
   if (N % 16 || K % ku) return ACORN_ERR_SHAPE;
@@ -594,6 +871,48 @@ int dispatch_tile(const Tiling& t, const KArgs& a, hipStream_t st) {
   return ACORN_ERR_UNSUPPORTED;
 }
 
+template <int WFMT, int BM, int BN, int DP>
+void launch_tiled(const Tiling& t, const KArgs& a, hipStream_t st) {
+  auto kfn = wgemm_tile_kernel<WFMT, BM, BN, DP>;
+  static bool lds_raised = false;  // once per instantiation, before any capture
+  if (!lds_raised && t.lds > 64 * 1024) {
+    (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    lds_raised = true;
+  }
+  dim3 grid((unsigned)t.ntiles, (unsigned)t.ksplit, (unsigned)t.mblocks), block(256);
+  kfn<<<grid, block, t.lds, st>>>(a);
+}
+
+// Prefetch depth: as deep as the registers allow for the tile (4 steps for
+// BM <= 64, 2 for BM = 128), reduced until it divides the step count.
+template <int WFMT, int BM, int BN>
+void launch_tiled_dp(const Tiling& t, const KArgs& a, hipStream_t st) {
+  const int steps = t.nk;
+  if (BM <= 64 && steps % 4 == 0) launch_tiled<WFMT, BM, BN, 4>(t, a, st);
+  else if (steps % 2 == 0) launch_tiled<WFMT, BM, BN, 2>(t, a, st);
+  else launch_tiled<WFMT, BM, BN, 1>(t, a, st);
+}
+
+template <int WFMT, int BN>
+int dispatch_tiled_bm(const Tiling& t, const KArgs& a, hipStream_t st) {
+  switch (t.upw) {
+    case 32: launch_tiled_dp<WFMT, 32, BN>(t, a, st); return ACORN_OK;
+    case 64: launch_tiled_dp<WFMT, 64, BN>(t, a, st); return ACORN_OK;
+    case 128: launch_tiled_dp<WFMT, 128, BN>(t, a, st); return ACORN_OK;
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+template <int WFMT>
+int dispatch_tiled(const Tiling& t, const KArgs& a, hipStream_t st) {
+  switch (t.nw) {
+    case 64: return dispatch_tiled_bm<WFMT, 64>(t, a, st);
+    case 128: return dispatch_tiled_bm<WFMT, 128>(t, a, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
 int plan_entry(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg, bool swiglu) {
   if (!cfg) return ACORN_ERR_VALUE;
   if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4)
@@ -635,10 +954,18 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
   a.tpw = t.tpw;
   a.ksplit = t.ksplit;
   a.log2R = ilog2_ceil(t.R);
-  switch (wfmt) {
-    case ACORN_WFMT_BF16: rc = dispatch_tile<ACORN_WFMT_BF16>(t, a, st); break;
-    case ACORN_WFMT_W8: rc = dispatch_tile<ACORN_WFMT_W8>(t, a, st); break;
-    case ACORN_WFMT_W4: rc = dispatch_tile<ACORN_WFMT_W4>(t, a, st); break;
+  if (t.kind == 1) {
+    switch (wfmt) {
+      case ACORN_WFMT_BF16: rc = dispatch_tiled<ACORN_WFMT_BF16>(t, a, st); break;
+      case ACORN_WFMT_W8: rc = dispatch_tiled<ACORN_WFMT_W8>(t, a, st); break;
+      case ACORN_WFMT_W4: rc = dispatch_tiled<ACORN_WFMT_W4>(t, a, st); break;
+    }
+  } else {
+    switch (wfmt) {
+      case ACORN_WFMT_BF16: rc = dispatch_tile<ACORN_WFMT_BF16>(t, a, st); break;
+      case ACORN_WFMT_W8: rc = dispatch_tile<ACORN_WFMT_W8>(t, a, st); break;
+      case ACORN_WFMT_W4: rc = dispatch_tile<ACORN_WFMT_W4>(t, a, st); break;
+    }
   }
   if (rc) return rc;
   ACORN_LAUNCH_CHECK();

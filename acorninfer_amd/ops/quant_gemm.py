@@ -67,9 +67,13 @@ def bucket_for(M: int) -> str:
 class Tiling(NamedTuple):
     """Native tiling of acorn_quant_gemm; 0 = planner's choice.
 
+    Streaming kernel (the weight-stream form; M <= 16, or any M with rt >= 1):
     rt: 16-row weight tiles per wavefront row block; upw: 16-byte weight
     loads per lane per pipeline step; nw: wavefronts per workgroup (they
     split K); ksplit: workgroups along K; tpw: row tiles per workgroup.
+    Tiled kernel (M > 16 with rt == 0, the default there): upw is the M tile
+    BM (32 / 64 / 128), nw the N tile BN (64 / 128), ksplit the K split; the
+    planner reports (0, BM, BN, ksplit, 1).
     """
     rt: int = 0
     upw: int = 0
@@ -288,6 +292,12 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
         for upw in (2, 4, 8):
             for nw in (2, 4, 8):
                 reqs.append(Tiling(0, upw, nw, 0, tpw))
+    if M > DECODE_M_MAX and not swiglu:
+        reqs = [r for r in reqs if r.rt > 0]      # rt 0 means the tiled kernel here
+        for bm in (32, 64, 128):
+            for bn in (64, 128):
+                for ks in (0, 1, 2, 4, 8):
+                    reqs.append(Tiling(0, bm, bn, ks, 0))
     for r in reqs:
         try:
             t, _ = planner(M, N, K, wfmt, r)

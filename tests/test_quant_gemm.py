@@ -204,12 +204,14 @@ def test_bucket_boundaries_and_classes():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("fmt", ["bf16", "w8", "w4"])
-@pytest.mark.parametrize("m", [1, 8, 16])
+@pytest.mark.parametrize("m", [1, 8, 16, 40, 256])
 def test_every_candidate_tiling_matches(fmt, m):
-    """Every tiling the load-time sweep may pick (row tiles per wave, loads per
-    lane, waves, K splits with the in-kernel reduction, tiles per workgroup)
-    gives the oracle's result on the o shape (K=4096) and the down shape
-    (K=12288); tilings differ only in fp32 summation order."""
+    """Every tiling the load-time sweep may pick (streaming kernel: row tiles
+    per wave, loads per lane, waves, K splits, tiles per workgroup; for
+    M > 16 also the tiled kernel at every M tile and K split, including a
+    partial last M tile at M = 40) gives the oracle's result on the o shape
+    (K=4096) and the down shape (K=12288); tilings differ only in fp32
+    summation order."""
     from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, WFMT_W8
     from acorninfer_amd.ops.quant_gemm import _launch, candidates
     for cls in ("o", "down"):
