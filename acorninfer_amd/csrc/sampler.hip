@@ -90,16 +90,43 @@ __global__ __launch_bounds__(kNT) void sample_kernel(
   __syncthreads();
 
   // ---- pass 1: max (first index on ties), finiteness --------------------
+  // 16-byte vectors, kUnroll of them in flight per thread; a scalar tail
   float bv = -INFINITY;
   int64_t bi = INT64_MAX;
   bool bad = false;
-  for (int64_t i = tid; i < V; i += kNT) {
-    const float l = to_f32(row[i]);
+  auto visit = [&](float l, int64_t i) {
     if (!(l == l) || l == INFINITY || l == -INFINITY) bad = true;
     if (l > bv || (l == bv && i < bi)) {
       bv = l;
       bi = i;
     }
+  };
+  {
+    constexpr int E = 16 / sizeof(T);                 // elements per vector
+    constexpr int kUnroll = 4;
+    struct Vec16 {
+      T v[E];
+    };
+    const bool aligned = ((uintptr_t)row % 16) == 0;
+    const int64_t nvec = aligned ? V / E : 0;
+    const Vec16* rv = (const Vec16*)row;
+    for (int64_t j0 = tid; j0 < nvec; j0 += (int64_t)kNT * kUnroll) {
+      Vec16 buf[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t j = j0 + (int64_t)u * kNT;
+        if (j < nvec) buf[u] = rv[j];
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t j = j0 + (int64_t)u * kNT;
+        if (j < nvec) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) visit(to_f32(buf[u].v[e]), j * E + e);
+        }
+      }
+    }
+    for (int64_t i = nvec * E + tid; i < V; i += kNT) visit(to_f32(row[i]), i);
   }
   if (bad) sh_bad = 1;  // benign race: every writer stores 1
 #pragma unroll

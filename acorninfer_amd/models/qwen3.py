@@ -426,10 +426,15 @@ class Qwen3DecodeModel:
                 "down": [L.down for L in self.layers], "lm_head": [self.lm_head]}
 
     def time_projection(self, lins: list[QLinear], M: int, tiling, reps: int = 3,
-                        swiglu: bool = False, with_act: bool = False) -> float:
+                        swiglu: bool = False, with_act: bool = False,
+                        with_reduce: bool = False) -> float:
         """Average µs of one launch of `tiling`, measured as a hipGraph of one
         launch per weight in `lins` (distinct weights, so the 256 MB MALL does
-        not hold them between launches) on a private stream with HIP events."""
+        not hold them between launches) on a private stream with HIP events.
+        with_act adds the separate SwiGLU kernel the fused form saves;
+        with_reduce adds a split-order reduction of the partials, standing in
+        for the step's consumer kernel (qkv epilogue, K1), whose cost grows with
+        the split count."""
         from acorninfer_amd.ops.quant_gemm import _native_cfg
         lin0 = lins[0]
         planner = lin0.swiglu_plan if swiglu else lin0.plan
@@ -437,6 +442,7 @@ class Qwen3DecodeModel:
         x = torch.randn(M, lin0.K, device=self.device).to(self.dtype)
         part = torch.empty(t.ksplit, M, lin0.N, dtype=torch.float32, device=self.device)
         act = torch.empty(M, lin0.N // 2, dtype=self.dtype, device=self.device)
+        red = torch.empty(M, lin0.N, dtype=self.dtype, device=self.device) if with_reduce else None
         s = torch.cuda.Stream(self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(s):
@@ -451,6 +457,10 @@ class Qwen3DecodeModel:
                                                        lin.N // 2, int(lin.il16),
                                                        dtype_code(act), s.cuda_stream),
                                   "silu_mul")
+                        if with_reduce:
+                            check(lib().acorn_splitk_reduce(ptr(part), t.ksplit, M * lin.N,
+                                                            ptr(red), dtype_code(red),
+                                                            s.cuda_stream), "splitk_reduce")
             body()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=s):
@@ -469,8 +479,9 @@ class Qwen3DecodeModel:
     def tune(self, batch: int, *, names=None, verbose: bool = False) -> dict:
         """Load-time tiling choice for a decode bucket (the reference's
         quant_gemm.configure, acorninfer/ops/quant_gemm.py:449-492): every
-        candidate tiling of each projection is timed in place and the fastest
-        is kept in self.tilings[batch]; run before any graph capture."""
+        candidate tiling of each projection is timed in place, together with
+        the work its split count puts on the consumer, and the fastest is kept
+        in self.tilings[batch]; run before any graph capture."""
         from acorninfer_amd.ops.quant_gemm import candidates
         if self.lm_head.fmt == _lib.WFMT_F32:
             return {}
@@ -486,8 +497,10 @@ class Qwen3DecodeModel:
                 modes = [True, False] if self.fused_swiglu(batch) else [False]
             for sw in modes:
                 act = name == "gate_up" and not sw
+                red = name in ("qkv", "o", "down")    # consumers that read the partials
                 for c in candidates(batch, lins[0].N, lins[0].K, lins[0].fmt, swiglu=sw):
-                    us = self.time_projection(lins, batch, c, swiglu=sw, with_act=act)
+                    us = self.time_projection(lins, batch, c, swiglu=sw, with_act=act,
+                                              with_reduce=red)
                     if verbose:
                         print(f"TUNE {name} M={batch} swiglu={sw} {tuple(c)} {us:.2f} us",
                               flush=True)
