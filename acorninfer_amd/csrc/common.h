@@ -44,6 +44,43 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, acorn_bf16x2));
 }
 
+// ---- split-K partial sums -------------------------------------------------
+// sum_s p[s * plane] for s < nsplit, added in split order (so results do not
+// depend on the launch). The loads of a batch of splits are issued before the
+// first add: indices past the split count are clamped (in bounds, no branch)
+// and their values discarded by a uniform test, which keeps the wait counts
+// static.
+constexpr int kSplitBatch = 8;
+__device__ __forceinline__ float sum_splits(const float* p, size_t plane, int nsplit) {
+  float a = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += kSplitBatch) {
+    float v[kSplitBatch];
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) v[u] = p[(size_t)min(s0 + u, nsplit - 1) * plane];
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u)
+      if (s0 + u < nsplit) a = s0 + u == 0 ? v[u] : a + v[u];
+  }
+  return a;
+}
+// The same over 8 consecutive floats (16-byte aligned), 4 splits per batch.
+__device__ __forceinline__ void sum_splits8(const float* p, size_t plane, int nsplit,
+                                            float (&a)[8]) {
+  typedef float f8 __attribute__((ext_vector_type(8)));
+  for (int s0 = 0; s0 < nsplit; s0 += 4) {
+    f8 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = *(const f8*)(p + (size_t)min(s0 + u, nsplit - 1) * plane);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (s0 + u < nsplit) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[i] = s0 + u == 0 ? v[u][i] : a[i] + v[u][i];
+      }
+    }
+  }
+}
+
 // ---- wavefront reductions -----------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -64,12 +64,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
     const size_t ui = gi + (il16 ? 16 : inter);
     float g, u;
     if (part) {
-      g = part[gi];
-      u = part[ui];
-      for (int s = 1; s < nsplit; ++s) {
-        g += part[s * plane + gi];
-        u += part[s * plane + ui];
-      }
+      g = sum_splits(part + gi, plane, nsplit);
+      u = sum_splits(part + ui, plane, nsplit);
       g = round_to<T>(g);
       u = round_to<T>(u);
     } else {

@@ -27,9 +27,7 @@ __global__ __launch_bounds__(kNT) void fused_add_rmsnorm_kernel(
 
   auto load_x = [&](int i) -> float {
     if constexpr (FROM_PART) {
-      float a = part[base + i];
-      for (int s = 1; s < nsplit; ++s) a += part[s * plane + base + i];
-      float xr = round_to<T>(a);
+      float xr = round_to<T>(sum_splits(part + base + i, plane, nsplit));
       if (x_out) x_out[base + i] = from_f32<T>(xr);
       return xr;
     } else {
@@ -113,13 +111,7 @@ __global__ __launch_bounds__(kNT) void fused_add_rmsnorm_vec_kernel(
     const size_t off = base + (size_t)vi * 8;
     float a[8];
     if constexpr (FROM_PART) {
-      load8<float>(part + off, a);
-      for (int s = 1; s < nsplit; ++s) {
-        float b[8];
-        load8<float>(part + s * plane + off, b);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) a[i] += b[i];
-      }
+      sum_splits8(part + off, plane, nsplit, a);
 #pragma unroll
       for (int i = 0; i < 8; ++i) a[i] = round_to<T>(a[i]);
       if (x_out) store8<T>(x_out + off, a);

@@ -124,12 +124,8 @@ __global__ __launch_bounds__(kWave) void qkv_epilogue_kernel(
     const int i = threadIdx.x + j * kWave;
     float a = 0.f, c = 0.f;
     if (i < half) {
-      a = src[i];
-      c = src[i + half];
-      for (int s = 1; s < nsplit; ++s) {
-        a += src[s * plane + i];
-        c += src[s * plane + i + half];
-      }
+      a = sum_splits(src + i, plane, nsplit);
+      c = sum_splits(src + i + half, plane, nsplit);
     }
     x1[j] = round_to<T>(a);  // the projection's bf16 output
     x2[j] = round_to<T>(c);
