@@ -319,24 +319,42 @@ __global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
   load_step(0, ra);
 
   // ---- stage x for the whole K range (MFMA-B order; int4 k-permutation) ----
-  for (int p = threadIdx.x; p < MT * R * CPR; p += NT) {
-    const int c = p % CPR, rr = p / CPR;  // rr = mt * R + row
-    const int mt = rr / R, row = rr % R;
-    const int m = mblk + mt * 16 + row;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (m < a.M) {
-      v = *(const u32x4*)(a.x + (size_t)m * a.K + kr0 + c * 8);
-      if constexpr (WFMT == ACORN_WFMT_W4) {
-        // items [x0,x4,x1,x5,x2,x6,x3,x7] to match unpack_w4's pairing
-        u32x4 t;
-        t[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
-        t[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
-        t[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
-        t[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
-        v = t;
+  // Eight loads per thread are issued before the first store, so staging
+  // costs about one memory round trip. Rows past M (padding up to R or the
+  // m tile) re-read row M-1 rather than branch: their outputs are never
+  // written, and the loads stay unconditional (static wait counts).
+  {
+    constexpr int XB = 8;
+    const int total = MT * R * CPR;
+    for (int p0 = threadIdx.x; p0 < total; p0 += NT * XB) {
+      u32x4 v[XB];
+#pragma unroll
+      for (int u = 0; u < XB; ++u) {
+        const int p = min(p0 + u * NT, total - 1);
+        const int c = p % CPR, rr = p / CPR;  // rr = mt * R + row
+        const int m = min(mblk + (rr / R) * 16 + rr % R, a.M - 1);
+        v[u] = *(const u32x4*)(a.x + (size_t)m * a.K + kr0 + c * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < XB; ++u) {
+        const int p = p0 + u * NT;
+        if (p < total) {
+          const int c = p % CPR, rr = p / CPR;
+          const int mt = rr / R, row = rr % R;
+          u32x4 w = v[u];
+          if constexpr (WFMT == ACORN_WFMT_W4) {
+            // items [x0,x4,x1,x5,x2,x6,x3,x7] to match unpack_w4's pairing
+            u32x4 t;
+            t[0] = __builtin_amdgcn_perm(w[2], w[0], 0x05040100u);
+            t[1] = __builtin_amdgcn_perm(w[2], w[0], 0x07060302u);
+            t[2] = __builtin_amdgcn_perm(w[3], w[1], 0x05040100u);
+            t[3] = __builtin_amdgcn_perm(w[3], w[1], 0x07060302u);
+            w = t;
+          }
+          xs[((size_t)mt * CPR + c) * R + row] = w;
+        }
       }
     }
-    xs[((size_t)mt * CPR + c) * R + row] = v;
   }
   __syncthreads();
   // ---- per-workgroup x sums (tile independent) -----------------------------
@@ -734,7 +752,9 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   if (M <= 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   t->swiglu = swiglu;
   t->kind = 0;
-  if (M > 16 && !swiglu && (!cfg || cfg[0] <= 0))
+  // the tiled kernel: the default for M > 16; for M <= 16 on request (rt 0
+  // with an M tile of 32 or more in upw)
+  if (!swiglu && ((M > 16 && (!cfg || cfg[0] <= 0)) || (cfg && cfg[0] == 0 && cfg[1] >= 32)))
     return make_tile_plan(M, N, K, wfmt, cfg ? cfg[1] : 0, cfg ? cfg[2] : 0, cfg ? cfg[3] : 0, t);
   if (swiglu && (M > 16 || N % 32)) return ACORN_ERR_UNSUPPORTED;
   const int ku = ku_of(wfmt);

@@ -292,12 +292,25 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
         for upw in (2, 4, 8):
             for nw in (2, 4, 8):
                 reqs.append(Tiling(0, upw, nw, 0, tpw))
+    # more rows per workgroup over a shorter K range: the staged x (shared by
+    # all workgroups) then costs less per weight byte, at the price of more
+    # split partials
+    for ks in (4, 6, 8, 12, 16):
+        for tpw in (2, 4, 8, 12, 16, 24):
+            for nw in (1, 2, 4):
+                for upw in (2, 4):
+                    reqs.append(Tiling(0, upw, nw, ks, tpw))
     if M > DECODE_M_MAX and not swiglu:
         reqs = [r for r in reqs if r.rt > 0]      # rt 0 means the tiled kernel here
         for bm in (32, 64, 128):
             for bn in (64, 128):
                 for ks in (0, 1, 2, 4, 8):
                     reqs.append(Tiling(0, bm, bn, ks, 0))
+    elif not swiglu:
+        # the tiled kernel at its smallest M tile competes for decode sizes too
+        for bn in (64, 128):
+            for ks in (1, 2, 4, 8, 16):
+                reqs.append(Tiling(0, 32, bn, ks, 0))
     for r in reqs:
         try:
             t, _ = planner(M, N, K, wfmt, r)
