@@ -24,9 +24,13 @@
 //  * A workgroup owns a run of 16*RT-row tiles and one K range (split
 //    blockIdx.y). x for the whole K range is staged in LDS once, in MFMA-B
 //    order ([k/8][row][8], one conflict-free ds_read_b128 per B fetch).
-//    The NW waves split the K range; the next (tile, k-chunk) step's weights
-//    and scales are loaded into the second register set while the current
-//    step is on the MFMAs, so every wave keeps a step of loads in flight.
+//    The NW waves split the K range and walk (tile, k-chunk) steps through
+//    a ring of D register sets (D = 4, 2 or 1 by the step's size). The
+//    first x loads, then the first D steps' weights and scales, are issued
+//    before anything waits, so a decode-sized workgroup (nsteps <= D) has
+//    all of its HBM reads in flight at once. Every load is unconditional
+//    (clamped indices): a load under a branch makes the compiler wait for
+//    all outstanding loads before the next use.
 //  * At the end of a tile the waves' partials are summed through
 //    double-buffered LDS in fixed wave order (one barrier per tile).
 //  * Split-K (ksplit > 1): each split writes fp32 partials, which the
@@ -93,26 +97,47 @@ __device__ __forceinline__ u32x4 unpack_w8(uint32_t lo, uint32_t hi) {
   return r;
 }
 
-// UPW consecutive fp16 values; the caller guarantees 2*UPW-byte alignment.
-template <int UPW> struct HalfVec {
-  _Float16 v[UPW];
-};
-template <int UPW>
-__device__ __forceinline__ void load_halves(const _Float16* p, _Float16 (&dst)[UPW]) {
-  typedef _Float16 hv __attribute__((ext_vector_type(UPW)));
-  const hv t = *(const hv*)p;
+// NDW consecutive dwords from a 4*NDW-byte aligned address (one vector load
+// per 16 bytes).
+template <int NDW>
+__device__ __forceinline__ void load_dwords(const void* p, uint32_t (&d)[NDW]) {
+  if constexpr (NDW == 1) {
+    d[0] = *(const uint32_t*)p;
+  } else if constexpr (NDW == 2) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 t = *(const u32x2*)p;
+    d[0] = t[0];
+    d[1] = t[1];
+  } else {
+    static_assert(NDW % 4 == 0, "whole 16-byte pieces");
 #pragma unroll
-  for (int u = 0; u < UPW; ++u) dst[u] = t[u];
+    for (int c = 0; c < NDW / 4; ++c) {
+      const u32x4 t = *(const u32x4*)((const uint32_t*)p + 4 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[4 * c + j] = t[j];
+    }
+  }
+}
+
+// fp16 number u of a run of packed halves (even u in the low half).
+template <int NDW>
+__device__ __forceinline__ float half_at(const uint32_t (&d)[NDW], int u) {
+  const uint32_t v = d[u / 2];
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)((u & 1) ? v >> 16 : v & 0xffffu));
 }
 
 // Registers of one pipeline step: this lane's weight units plus the scales
-// of the output rows it holds (rows 4*(lane/16)+i of each 16-row group).
-template <int WFMT, int RT, int UPW>
+// of the output rows it holds (rows 4*(lane/16)+i of each 16-row group), as
+// packed fp16 pairs. int4 keeps UPW group scales (and, with ZERO, zero
+// points) per row; int8 keeps the 4 channel scales.
+template <int WFMT, int RT, int UPW, bool ZERO>
 struct StepRegs {
-  static constexpr int NS = WFMT == ACORN_WFMT_W4 ? UPW : 1;
+  static constexpr bool W4 = WFMT == ACORN_WFMT_W4;
+  static constexpr int NR = W4 ? 4 : 1;
+  static constexpr int NDW = W4 ? (UPW + 1) / 2 : 2;
   u32x4 w[RT][UPW];
-  _Float16 s[RT][4][NS];
-  _Float16 z[RT][4][NS];
+  uint32_t s[RT][NR][NDW];
+  uint32_t z[RT][ZERO ? 4 : 1][ZERO ? NDW : 1];
 };
 
 struct KArgs {
@@ -143,8 +168,9 @@ __device__ __forceinline__ float swiglu_bf16(float g, float u) {
 // Grid: x = tile groups, y = ksplit, z = m blocks of 16*MT rows.
 // SWIGLU: RT == 2, the tile's first 16 weight rows are gate rows and the next
 // 16 the up rows of the same 16 outputs; out is act [M, N/2] (ksplit == 1).
-template <int WFMT, int RT, int MT, int UPW, int NW, bool SWIGLU>
-__global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
+// ZERO: int4 with zero points (a.zero != nullptr).
+template <int WFMT, int RT, int MT, int UPW, int NW, bool SWIGLU, bool ZERO>
+__global__ __launch_bounds__(NW * kWave, NW == 8 ? 2 : 3) void wgemm_kernel(KArgs a) {
   using F = Fmt<WFMT>;
   constexpr int KU = F::KU, MPU = F::MPU, ROWS = 16 * RT;
   constexpr int KC = NW * UPW * KU;               // k per chunk (all waves)
@@ -167,14 +193,13 @@ __global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
   const int mblk = blockIdx.z * 16 * MT;
   const size_t wrow = (size_t)a.K * F::BPK_NUM / F::BPK_DEN;
   const int G = a.K / 128;
-  const bool has_zero = a.zero != nullptr;
 
   // LDS: x [MT][CPR][R] u32x4 | int4 group sums [MT][GR][16] f32 | red [2][NW][TILE]
   u32x4* xs = (u32x4*)smem;
   float* xgs = (float*)(smem + (size_t)MT * CPR * R * 16);
   float* red = xgs + (WFMT == ACORN_WFMT_W4 ? MT * GR * 16 : 0);
 
-  auto load_step = [&](int s, StepRegs<WFMT, RT, UPW>& r) {
+  auto load_step = [&](int s, StepRegs<WFMT, RT, UPW, ZERO>& r) {
     const int t = t_begin + s / nk, c = s % nk;
     const int kw = kr0 + c * KC + wid * UPW * KU;  // this wave's first k of the step
 #pragma unroll
@@ -193,24 +218,20 @@ __global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const size_t row = (size_t)t * ROWS + rt * 16 + 4 * lg + i;
-          load_halves<UPW>(a.scale + row * G + g0, r.s[rt][i]);
-          if (has_zero) load_halves<UPW>(a.zero + row * G + g0, r.z[rt][i]);
+          load_dwords(a.scale + row * G + g0, r.s[rt][i]);
+          if constexpr (ZERO) load_dwords(a.zero + row * G + g0, r.z[rt][i]);
         }
     } else if constexpr (WFMT == ACORN_WFMT_W8) {
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        _Float16 sv[4];
-        load_halves<4>(a.scale + (size_t)t * ROWS + rt * 16 + 4 * lg, sv);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r.s[rt][i][0] = sv[i];
-      }
+      for (int rt = 0; rt < RT; ++rt)
+        load_dwords(a.scale + (size_t)t * ROWS + rt * 16 + 4 * lg, r.s[rt][0]);
     }
   };
 
   const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
   f32x4 x8[MT];  // int8: sum of x over this wave's k (all chunks), per column
 
-  auto compute = [&](const StepRegs<WFMT, RT, UPW>& r, int c, f32x4 (&acc)[RT][MT]) {
+  auto compute = [&](const StepRegs<WFMT, RT, UPW, ZERO>& r, int c, f32x4 (&acc)[RT][MT]) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
       const int kl = c * KC + wid * UPW * KU + u * KU;  // workgroup-local k of unit u
@@ -240,8 +261,10 @@ __global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
             for (int j = 0; j < MPU; ++j) cc = mfma(unpack_w4(q[j]), bop[j], cc);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const float s = (float)r.s[rt][i][u];
-              const float zc = has_zero ? (float)r.z[rt][i][u] - 128.f * s : -136.f * s;
+              const float s = half_at(r.s[rt][i], u);
+              float zc;
+              if constexpr (ZERO) zc = half_at(r.z[rt][i], u) - 128.f * s;
+              else zc = -136.f * s;
               acc[rt][mt][i] += s * cc[i] + zc * xg;
             }
           }
@@ -259,13 +282,13 @@ __global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
   };
 
   int rbuf = 0;
-  auto finish_tile = [&](int t, const StepRegs<WFMT, RT, UPW>& r, f32x4 (&acc)[RT][MT]) {
+  auto finish_tile = [&](int t, const StepRegs<WFMT, RT, UPW, ZERO>& r, f32x4 (&acc)[RT][MT]) {
     if constexpr (WFMT == ACORN_WFMT_W8) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float s = (float)r.s[rt][i][0];
+          const float s = half_at(r.s[rt][0], i);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) acc[rt][mt][i] = s * (acc[rt][mt][i] - 128.f * x8[mt][i]);
         }
@@ -315,46 +338,60 @@ __global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
   };
 
   const int nsteps = (t_end - t_begin) * nk;
-  StepRegs<WFMT, RT, UPW> ra, rb;
-  load_step(0, ra);
 
-  // ---- stage x for the whole K range (MFMA-B order; int4 k-permutation) ----
-  // Eight loads per thread are issued before the first store, so staging
-  // costs about one memory round trip. Rows past M (padding up to R or the
-  // m tile) re-read row M-1 rather than branch: their outputs are never
-  // written, and the loads stay unconditional (static wait counts).
-  {
-    constexpr int XB = 8;
-    const int total = MT * R * CPR;
-    for (int p0 = threadIdx.x; p0 < total; p0 += NT * XB) {
-      u32x4 v[XB];
-#pragma unroll
-      for (int u = 0; u < XB; ++u) {
-        const int p = min(p0 + u * NT, total - 1);
-        const int c = p % CPR, rr = p / CPR;  // rr = mt * R + row
-        const int m = min(mblk + (rr / R) * 16 + rr % R, a.M - 1);
-        v[u] = *(const u32x4*)(a.x + (size_t)m * a.K + kr0 + c * 8);
-      }
-#pragma unroll
-      for (int u = 0; u < XB; ++u) {
-        const int p = p0 + u * NT;
-        if (p < total) {
-          const int c = p % CPR, rr = p / CPR;
-          const int mt = rr / R, row = rr % R;
-          u32x4 w = v[u];
-          if constexpr (WFMT == ACORN_WFMT_W4) {
-            // items [x0,x4,x1,x5,x2,x6,x3,x7] to match unpack_w4's pairing
-            u32x4 t;
-            t[0] = __builtin_amdgcn_perm(w[2], w[0], 0x05040100u);
-            t[1] = __builtin_amdgcn_perm(w[2], w[0], 0x07060302u);
-            t[2] = __builtin_amdgcn_perm(w[3], w[1], 0x05040100u);
-            t[3] = __builtin_amdgcn_perm(w[3], w[1], 0x07060302u);
-            w = t;
-          }
-          xs[((size_t)mt * CPR + c) * R + row] = w;
-        }
-      }
+  // ---- loads: the first x batch, then the first D steps' weights ----------
+  // x for the whole K range is staged into LDS in MFMA-B order (int4: the
+  // unpack_w4 k-permutation). The first XB pieces per thread are loaded
+  // before any weight so that waiting for them leaves the weights in flight;
+  // indices past the end are clamped (loads stay unconditional, the stores
+  // are skipped). Rows past M (padding up to R or the m tile) re-read row
+  // M-1: their outputs are never written.
+  constexpr int XB = 4;
+  const int xtotal = MT * R * CPR;
+  auto x_load = [&](int p) -> u32x4 {
+    const int c = p % CPR, rr = p / CPR;  // rr = mt * R + row
+    const int m = min(mblk + (rr / R) * 16 + rr % R, a.M - 1);
+    return *(const u32x4*)(a.x + (size_t)m * a.K + kr0 + c * 8);
+  };
+  auto x_store = [&](int p, u32x4 w) {
+    const int c = p % CPR, rr = p / CPR;
+    const int mt = rr / R, row = rr % R;
+    if constexpr (WFMT == ACORN_WFMT_W4) {
+      // items [x0,x4,x1,x5,x2,x6,x3,x7] to match unpack_w4's pairing
+      u32x4 t;
+      t[0] = __builtin_amdgcn_perm(w[2], w[0], 0x05040100u);
+      t[1] = __builtin_amdgcn_perm(w[2], w[0], 0x07060302u);
+      t[2] = __builtin_amdgcn_perm(w[3], w[1], 0x05040100u);
+      t[3] = __builtin_amdgcn_perm(w[3], w[1], 0x07060302u);
+      w = t;
     }
+    xs[((size_t)mt * CPR + c) * R + row] = w;
+  };
+  u32x4 xv[XB];
+#pragma unroll
+  for (int u = 0; u < XB; ++u) xv[u] = x_load(min((int)threadIdx.x + u * NT, xtotal - 1));
+
+  // D steps in flight per wave (as many as the registers allow): a
+  // workgroup with nsteps <= D has every weight of its work requested here,
+  // before x is stored.
+  constexpr int D = RT * UPW <= 2 ? 4 : RT * UPW <= 8 ? 2 : 1;
+  StepRegs<WFMT, RT, UPW, ZERO> ring[D];
+  load_step(0, ring[0]);
+#pragma unroll
+  for (int d = 1; d < D; ++d)
+    if (d < nsteps) load_step(d, ring[d]);
+
+#pragma unroll
+  for (int u = 0; u < XB; ++u) {
+    const int p = (int)threadIdx.x + u * NT;
+    if (p < xtotal) x_store(p, xv[u]);
+  }
+  for (int p0 = (int)threadIdx.x + NT * XB; p0 < xtotal; p0 += NT * XB) {
+#pragma unroll
+    for (int u = 0; u < XB; ++u) xv[u] = x_load(min(p0 + u * NT, xtotal - 1));
+#pragma unroll
+    for (int u = 0; u < XB; ++u)
+      if (p0 + u * NT < xtotal) x_store(p0 + u * NT, xv[u]);
   }
   __syncthreads();
   // ---- per-workgroup x sums (tile independent) -----------------------------
@@ -385,20 +422,31 @@ __global__ __launch_bounds__(NW * kWave) void wgemm_kernel(KArgs a) {
       }
   }
 
-  // ---- main pipeline: load step s+1 while step s is on the MFMAs ----------
+  // ---- main pipeline --------------------------------------------------------
   f32x4 acc[RT][MT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < nsteps; s += 2) {
-    if (s + 1 < nsteps) load_step(s + 1, rb);
-    compute(ra, s % nk, acc);
-    if (s % nk == nk - 1) finish_tile(t_begin + s / nk, ra, acc);
-    if (s + 1 >= nsteps) break;
-    if (s + 2 < nsteps) load_step(s + 2, ra);
-    compute(rb, (s + 1) % nk, acc);
-    if ((s + 1) % nk == nk - 1) finish_tile(t_begin + (s + 1) / nk, rb, acc);
+  auto step = [&](int s, const StepRegs<WFMT, RT, UPW, ZERO>& r) {
+    compute(r, s % nk, acc);
+    if (s % nk == nk - 1) finish_tile(t_begin + s / nk, r, acc);
+  };
+  if (nsteps <= D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d < nsteps) step(d, ring[d]);
+  } else {
+    // ring refill: step s + D goes into the slot step s leaves; refills past
+    // the end re-request the last step (unconditional loads keep the wait
+    // counts static)
+    for (int s0 = 0; s0 < nsteps; s0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        if (s0 + d < nsteps) step(s0 + d, ring[d]);
+        load_step(min(s0 + d + D, nsteps - 1), ring[d]);
+      }
+    }
   }
 }
 
@@ -832,15 +880,31 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
 
 template <int WFMT, int RT, int MT, int UPW, int NW>
 void launch_one(const Tiling& t, const KArgs& a, hipStream_t st) {
-  auto kfn = wgemm_kernel<WFMT, RT, MT, UPW, NW, false>;
+  auto kfn = wgemm_kernel<WFMT, RT, MT, UPW, NW, false, false>;
+  int variant = 0;
   if constexpr (RT == 2) {
-    if (t.swiglu) kfn = wgemm_kernel<WFMT, RT, MT, UPW, NW, true>;
+    if (t.swiglu) {
+      kfn = wgemm_kernel<WFMT, RT, MT, UPW, NW, true, false>;
+      variant = 1;
+    }
   }
-  static bool lds_raised[2] = {false, false};  // once per instantiation, before any capture
-  if (!lds_raised[t.swiglu] && t.lds > 64 * 1024) {
+  if constexpr (WFMT == ACORN_WFMT_W4) {
+    if (a.zero) {
+      kfn = wgemm_kernel<WFMT, RT, MT, UPW, NW, false, true>;
+      variant = 2;
+      if constexpr (RT == 2) {
+        if (t.swiglu) {
+          kfn = wgemm_kernel<WFMT, RT, MT, UPW, NW, true, true>;
+          variant = 3;
+        }
+      }
+    }
+  }
+  static bool lds_raised[4] = {false, false, false, false};  // once per kernel, before any capture
+  if (!lds_raised[variant] && t.lds > 64 * 1024) {
     (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
                               160 * 1024);
-    lds_raised[t.swiglu] = true;
+    lds_raised[variant] = true;
   }
   dim3 grid((unsigned)t.groups, (unsigned)t.ksplit, (unsigned)t.mblocks), block(NW * kWave);
   kfn<<<grid, block, t.lds, st>>>(a);
