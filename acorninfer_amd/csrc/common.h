@@ -44,6 +44,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, acorn_bf16x2));
 }
 
+// ---- streamed loads --------------------------------------------------------
+// Weights that a decode step reads exactly once may be loaded with the
+// non-temporal cache policy (global_load ... nt) where every load
+// instruction consumes whole 128-byte lines: on gfx950 such streams reach a
+// higher HBM read rate (about 6.7 vs 5.9 TB/s for a 2 GiB linear read). Where
+// an instruction reads half lines (16 rows x 64 bytes, the MFMA A layout) the
+// policy is slower (the other half is fetched again), so those loads keep the
+// default policy.
+template <typename V>
+__device__ __forceinline__ V load_nt(const V* p) {
+  return __builtin_nontemporal_load(p);
+}
+
 // ---- split-K partial sums -------------------------------------------------
 // sum_s p[s * plane] for s < nsplit, added in split order (so results do not
 // depend on the launch). The loads of a batch of splits are issued before the

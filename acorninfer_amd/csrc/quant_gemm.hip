@@ -518,6 +518,8 @@ __global__ __launch_bounds__(256) void wgemm_tile_kernel(KArgs a) {
   const int kper = K / a.ksplit, kb = blockIdx.y * kper, nsteps = kper / BK;
   const int wn = (wid & 1) * WN, wm = (wid >> 1) * WM;
   const int wrow = tid / TPR, wpart = tid % TPR;      // this thread's weight row / 32-k part
+  constexpr int PPR = BK / 8, BROWS = 256 / PPR;      // bf16: 16-byte pieces per row, rows per load
+  const int brow = tid / PPR, bpiece = tid % PPR;
 
   struct Stage {
     u32x4 x[XR], w[WR];
@@ -564,8 +566,12 @@ __global__ __launch_bounds__(256) void wgemm_tile_kernel(KArgs a) {
 #pragma unroll
       for (int j = 0; j < WR; ++j) wr[j] = *(const u32x4*)(a.w + wk + 16 * j);
     } else {
+      // bf16: instruction j reads whole 16-byte pieces of rows BROWS*j + t/PPR,
+      // consecutive threads consecutive pieces, so each instruction consumes
+      // whole cache lines and can use the non-temporal policy
 #pragma unroll
-      for (int j = 0; j < WR; ++j) wr[j] = *(const u32x4*)(a.w + 2 * (wk + 8 * j));
+      for (int j = 0; j < WR; ++j)
+        wr[j] = load_nt((const u32x4*)(a.w + 2 * ((size_t)(n0 + brow + BROWS * j) * K + k0 + 8 * bpiece)));
     }
   };
   auto lstore = [&](int s, const Stage& st) {
@@ -611,8 +617,9 @@ __global__ __launch_bounds__(256) void wgemm_tile_kernel(KArgs a) {
         }
       }
     } else {
+      __bf16* wb = wsm + (s & 1) * BN * KP + brow * KP + 8 * bpiece;
 #pragma unroll
-      for (int j = 0; j < WR; ++j) *(u32x4*)(wd + 8 * j) = wr[j];
+      for (int j = 0; j < WR; ++j) *(u32x4*)(wb + BROWS * j * KP) = wr[j];
     }
   };
 
