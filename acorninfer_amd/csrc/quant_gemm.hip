@@ -12,7 +12,9 @@
 // busy:
 //  * v_mfma_f32_16x16x32_bf16 with the WEIGHTS as the 16-row A operand and x
 //    (M rows, padded) as the B operand. One 16-byte load per lane feeds 1
-//    (bf16), 2 (int8) or 4 (int4) MFMAs.
+//    (bf16), 2 (int8) or 4 (int4) MFMAs. Weights are loaded in whole cache
+//    lines with the non-temporal policy and moved into the A layout through
+//    a per-wave LDS slab.
 //  * int4 -> bf16 in two VALU ops per dword: (w >> 4p) & 0x000F000F | 0x43004300
 //    is the bf16 pair (128+u_p, 128+u_{p+4}); the (p, p+4) pairing is a k
 //    permutation applied once to x when it is staged into LDS.
@@ -195,22 +197,28 @@ __global__ __launch_bounds__(NW * kWave, NW == 8 ? 2 : 3) void wgemm_kernel(KArg
   const int G = a.K / 128;
 
   // LDS: x [MT][CPR][R] u32x4 | int4 group sums [MT][GR][16] f32 | red [2][NW][TILE]
+  //      | per-wave slabs [NW][ROWS][SBW + 16] bytes
   u32x4* xs = (u32x4*)smem;
   float* xgs = (float*)(smem + (size_t)MT * CPR * R * 16);
   float* red = xgs + (WFMT == ACORN_WFMT_W4 ? MT * GR * 16 : 0);
+  // Weights are read in whole cache lines: a wave's step covers ROWS rows x
+  // SBW contiguous bytes per row, and load instruction q reads rows
+  // RPI*q .. RPI*q+RPI-1 (LPR lanes per row, 16 bytes each) with the
+  // non-temporal policy. The MFMA A layout (16 rows x 64 bytes per
+  // instruction) would read half lines, which streams slower. The wave turns
+  // a step into the A layout through its own LDS slab (one write and one
+  // read per 16 bytes; no barrier, LDS operations of a wave run in order).
+  constexpr int SBW = UPW * 64, LPR = SBW / 16, RPI = kWave / LPR, SPITCH = SBW + 16;
+  uint8_t* slab = (uint8_t*)(red + 2 * NW * TILE) + (size_t)wid * ROWS * SPITCH;
+  const int fl_row = lane / LPR, fl_byte = 16 * (lane % LPR);
 
   auto load_step = [&](int s, StepRegs<WFMT, RT, UPW, ZERO>& r) {
     const int t = t_begin + s / nk, c = s % nk;
     const int kw = kr0 + c * KC + wid * UPW * KU;  // this wave's first k of the step
+    const uint8_t* stp = a.w + (size_t)t * ROWS * wrow + (size_t)kw * F::BPK_NUM / F::BPK_DEN + fl_byte;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const uint8_t* rowp = a.w + (size_t)(t * ROWS + rt * 16 + lr) * wrow;
-#pragma unroll
-      for (int u = 0; u < UPW; ++u) {
-        const int k = kw + u * KU + (KU / 4) * lg;
-        r.w[rt][u] = *(const u32x4*)(rowp + (size_t)k * F::BPK_NUM / F::BPK_DEN);
-      }
-    }
+    for (int q = 0; q < RT * UPW; ++q)
+      r.w[q / UPW][q % UPW] = load_nt((const u32x4*)(stp + (size_t)(RPI * q + fl_row) * wrow));
     if constexpr (WFMT == ACORN_WFMT_W4) {
       const int g0 = kw / 128;
 #pragma unroll
@@ -231,7 +239,19 @@ __global__ __launch_bounds__(NW * kWave, NW == 8 ? 2 : 3) void wgemm_kernel(KArg
   const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
   f32x4 x8[MT];  // int8: sum of x over this wave's k (all chunks), per column
 
-  auto compute = [&](const StepRegs<WFMT, RT, UPW, ZERO>& r, int c, f32x4 (&acc)[RT][MT]) {
+  auto compute = [&](const StepRegs<WFMT, RT, UPW, ZERO>& r0, int c, f32x4 (&acc)[RT][MT]) {
+    // line layout -> A layout: unit u of row tile rt is 16 rows x 64 bytes
+    StepRegs<WFMT, RT, UPW, ZERO> r = r0;
+#pragma unroll
+    for (int q = 0; q < RT * UPW; ++q)
+      *(u32x4*)(slab + (RPI * q + fl_row) * SPITCH + fl_byte) = r0.w[q / UPW][q % UPW];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int u = 0; u < UPW; ++u)
+        r.w[rt][u] = *(const u32x4*)(slab + (rt * 16 + lr) * SPITCH + 64 * u + 16 * lg);
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
       const int kl = c * KC + wid * UPW * KU + u * KU;  // workgroup-local k of unit u
@@ -739,10 +759,11 @@ bool supported(int rt, int mt, int upw, int nw) {
 constexpr int kCUs = 256;
 constexpr int64_t kTargetWG = 4 * kCUs;  // default workgroups per launch
 
-size_t lds_bytes(int wfmt, int mt, int R, int rt, int nw, int KR) {
+size_t lds_bytes(int wfmt, int mt, int R, int rt, int nw, int KR, int upw) {
   size_t b = (size_t)mt * R * KR * 2;
   if (wfmt == ACORN_WFMT_W4) b += (size_t)mt * (KR / 128) * 16 * 4;
   b += (size_t)2 * nw * rt * mt * 4 * kWave * 4;
+  b += (size_t)nw * 16 * rt * (upw * 64 + 16);  // per-wave line-to-A-layout slabs
   return b;
 }
 
@@ -841,14 +862,20 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   // LDS budget per workgroup: two workgroups per CU for decode sizes, one
   // for larger M (which is MFMA-bound anyway).
   const size_t limit = t->mt == 1 ? 80 * 1024 : 160 * 1024;
-  auto lds_for = [&](int64_t kr) { return lds_bytes(wfmt, t->mt, t->R, t->rt, t->nw, (int)kr); };
+  auto lds_for = [&](int64_t kr) { return lds_bytes(wfmt, t->mt, t->R, t->rt, t->nw, (int)kr, t->upw); };
   while (lds_for(kc()) > limit && t->nw > 1) t->nw /= 2;
   while (lds_for(kc()) > limit && t->upw > 2) t->upw /= 2;
   if (!fits() || lds_for(kc()) > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
-  const int64_t chunks = K / kc();
+  int64_t chunks = K / kc();
   if (swiglu) {
+    // the whole K range is staged: narrow the workgroup (fewer waves, then
+    // shorter steps) until x, the reduction buffers and the slabs fit
     t->ksplit = 1;
-    if (lds_for(K) > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
+    while (lds_for(K) > 160 * 1024 && t->nw > 1) t->nw /= 2;
+    while (lds_for(K) > 160 * 1024 && t->upw > 2) t->upw /= 2;
+    if (lds_for(K) > 160 * 1024 || !supported(t->rt, t->mt, t->upw, t->nw))
+      return ACORN_ERR_UNSUPPORTED;
+    chunks = K / kc();
   } else if (req_ks > 0) {
     // a requested split is raised to the next divisor of the chunk count
     // whose K range fits the LDS of one workgroup
@@ -879,7 +906,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
     t->tpw = (int)std::max<int64_t>(1, (t->ntiles + groups - 1) / groups);
   }
   t->groups = (t->ntiles + t->tpw - 1) / t->tpw;
-  t->lds = lds_bytes(wfmt, t->mt, t->R, t->rt, t->nw, (int)(K / t->ksplit));
+  t->lds = lds_bytes(wfmt, t->mt, t->R, t->rt, t->nw, (int)(K / t->ksplit), t->upw);
   if (t->lds > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
   if (t->groups > 0x7fffffff || t->ksplit > 65535 || t->mblocks > 65535) return ACORN_ERR_SHAPE;
   return ACORN_OK;
