@@ -27,7 +27,7 @@
 //    blockIdx.y). x for the whole K range is staged in LDS once, in MFMA-B
 //    order ([k/8][row][8], one conflict-free ds_read_b128 per B fetch).
 //    The NW waves split the K range and walk (tile, k-chunk) steps through
-//    a ring of D register sets (D = 4, 2 or 1 by the step's size). The
+//    a ring of D register sets (D = 8, 4, 2 or 1 by the step's size). The
 //    first x loads, then the first D steps' weights and scales, are issued
 //    before anything waits, so a decode-sized workgroup (nsteps <= D) has
 //    all of its HBM reads in flight at once. Every load is unconditional
@@ -391,10 +391,15 @@ __global__ __launch_bounds__(NW * kWave, NW == 8 ? 2 : 3) void wgemm_kernel(KArg
 #pragma unroll
   for (int u = 0; u < XB; ++u) xv[u] = x_load(min((int)threadIdx.x + u * NT, xtotal - 1));
 
-  // D steps in flight per wave (as many as the registers allow): a
-  // workgroup with nsteps <= D has every weight of its work requested here,
-  // before x is stored.
-  constexpr int D = RT * UPW <= 2 ? 4 : RT * UPW <= 8 ? 2 : 1;
+  // D steps in flight per wave, as many as the registers allow without
+  // spilling: bf16 steps are weights only (4 VGPRs per unit), so about 64
+  // VGPRs of ring; int4/int8 steps also carry scales and the dequantised
+  // operands, so they keep a shallower ring. A workgroup with nsteps <= D
+  // has every weight of its work requested here, before x is stored.
+  constexpr int kUnits = RT * UPW * MT;
+  constexpr int D = WFMT == ACORN_WFMT_BF16
+                        ? (kUnits <= 2 ? 8 : kUnits <= 4 ? 4 : kUnits <= 8 ? 2 : 1)
+                        : (RT * UPW <= 2 ? 4 : RT * UPW <= 8 ? 2 : 1);
   StepRegs<WFMT, RT, UPW, ZERO> ring[D];
   load_step(0, ring[0]);
 #pragma unroll
