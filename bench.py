@@ -367,7 +367,9 @@ def main() -> None:
     ap.add_argument("--prompt-len", type=int, default=512)
     ap.add_argument("--layers", type=int, default=0, help="override layer count (debug only)")
     ap.add_argument("--extra", action="store_true",
-                    help="also measure C=1 and the W4A16 model (reported under 'extra')")
+                    help="(default) also measure C=1, C=32, W4A16 at C=1/8 and configuration 5 "
+                         "(reported under 'extra')")
+    ap.add_argument("--no-extra", action="store_true", help="only the C=8 bf16 headline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-tune", action="store_true", help="use the planner's default tilings")
     ap.add_argument("--kernels", action="store_true",
@@ -427,7 +429,7 @@ def main() -> None:
              "tuned": {k: {"tiling": v["tiling"], "us": v["us"],
                            "GBps": round(v["bytes"] / v["us"] / 1e3, 1)}
                        for k, v in model.tune_report.items()}}
-    if args.extra:
+    if not args.no_extra:
         del model, cache, runner
         torch.cuda.empty_cache()
         for fmt, c in (("bf16", 1), ("w4a16", 8), ("w4a16", 1)):
@@ -439,21 +441,31 @@ def main() -> None:
             _log(f"{fmt} C={c}: {c * args.steps / dt2:.1f} tok/s")
             del m2, c2, r2
             torch.cuda.empty_cache()
-        # configuration 5 at C=8: W4A16, prompts U[1024, 8192], sampled
-        from acorninfer_amd.sampler import SamplingParams
-        plens = torch.randint(1024, 8193, (8,), generator=torch.Generator().manual_seed(
-            args.seed + 5)).tolist()
-        m2, c2, r2, v2, f2 = build_workload(cfg, "w4a16", 8, 0, total, args.seed,
-                                            tune=not args.no_tune, prompt_lens=plens)
-        sp = [SamplingParams(temperature=0.6, top_p=0.95, top_k=20)] * 8
-        dt2, _ = time_decode(r2, v2, f2, args.steps, args.warmup, sampling=sp)
-        extra["w4a16_C8_long_sampled_tok_s"] = round(8 * args.steps / dt2, 2)
-        extra["w4a16_C8_long_sampled_ms_per_step"] = round(dt2 * 1e3 / args.steps, 4)
-        extra["w4a16_C8_long_sampled_mean_ctx"] = round(sum(plens) / 8, 1)
-        _log(f"w4a16 C=8 long sampled (mean ctx {sum(plens) / 8:.0f}): "
-             f"{8 * args.steps / dt2:.1f} tok/s")
+        # configuration 4's largest concurrency: C=32, bf16, prompts of 512
+        m2, c2, r2, v2, f2 = build_workload(cfg, "bf16", 32, args.prompt_len, total, args.seed,
+                                            tune=not args.no_tune)
+        dt2, _ = time_decode(r2, v2, f2, args.steps, args.warmup)
+        extra["bf16_C32_tok_s"] = round(32 * args.steps / dt2, 2)
+        extra["bf16_C32_ms_per_step"] = round(dt2 * 1e3 / args.steps, 4)
+        _log(f"bf16 C=32: {32 * args.steps / dt2:.1f} tok/s")
         del m2, c2, r2
         torch.cuda.empty_cache()
+        # configuration 5: W4A16, prompts U[1024, 8192], sampled, C=8 and C=64
+        from acorninfer_amd.sampler import SamplingParams
+        for c in (8, 64):
+            plens = torch.randint(1024, 8193, (c,), generator=torch.Generator().manual_seed(
+                args.seed + 5)).tolist()
+            m2, c2, r2, v2, f2 = build_workload(cfg, "w4a16", c, 0, total, args.seed,
+                                                tune=not args.no_tune, prompt_lens=plens)
+            sp = [SamplingParams(temperature=0.6, top_p=0.95, top_k=20)] * c
+            dt2, _ = time_decode(r2, v2, f2, args.steps, args.warmup, sampling=sp)
+            extra[f"w4a16_C{c}_long_sampled_tok_s"] = round(c * args.steps / dt2, 2)
+            extra[f"w4a16_C{c}_long_sampled_ms_per_step"] = round(dt2 * 1e3 / args.steps, 4)
+            extra[f"w4a16_C{c}_long_sampled_mean_ctx"] = round(sum(plens) / c, 1)
+            _log(f"w4a16 C={c} long sampled (mean ctx {sum(plens) / c:.0f}): "
+                 f"{c * args.steps / dt2:.1f} tok/s")
+            del m2, c2, r2
+            torch.cuda.empty_cache()
     if args.kernels:
         t0 = time.perf_counter()
         extra["kernels"] = kernel_benchmarks()
