@@ -776,9 +776,8 @@ size_t lds_bytes(int wfmt, int mt, int R, int rt, int nw, int KR, int upw) {
 // (64 / 128), 0 = choose (BN 64 for M <= 64, else 128; BM from M). The K
 // split keeps every split on whole K steps (int4: whole 128-k groups). By
 // default it grows until about two workgroups per CU are launched, while each
-// split keeps at least 256 k and, for M <= 64 (weight-bound), the fp32
-// partials (written and read again, 8*ksplit*M*N bytes) stay below half the
-// weight bytes.
+// split keeps at least 256 k and the fp32 partials (written and read again,
+// 8*ksplit*M*N bytes) stay below half the weight bytes.
 int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int req_bn,
                    int req_ks, Tiling* t) {
   const int bn = (req_bn == 64 || req_bn == 128) ? req_bn : M <= 64 ? 64 : 128;
@@ -813,7 +812,10 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
       int64_t nx = ks + 1;
       while (nx <= units && units % nx) ++nx;
       if (nx > units || K / nx < 256) break;
-      if (M <= 64 && 8.0 * nx * M * N > 0.5 * wbytes) break;  // weight-bound: keep partials small
+      // the fp32 partials (written, then read by the reduction) stay below
+      // half the weight bytes: beyond that they cost more than the extra
+      // workgroups gain, whether the size is weight- or MFMA-bound
+      if (8.0 * nx * M * N > 0.5 * wbytes) break;
       ks = nx;
     }
   }

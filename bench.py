@@ -285,7 +285,7 @@ def kernel_benchmarks(seed: int = 23, only_attention: bool = False,
             for M in (1, 8, 64, 256):
                 xm = torch.randn(M, k, device="cuda", generator=g).bfloat16()
                 best = None
-                cands = candidates(M, n, k, wf) if M <= 16 else [None]
+                cands = candidates(M, n, k, wf)
                 for c in cands:
                     t = lins[0].plan(M, c)[0]
                     part = torch.empty(t.ksplit, M, n, device="cuda")
