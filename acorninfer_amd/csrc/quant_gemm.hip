@@ -521,8 +521,11 @@ __global__ __launch_bounds__(256) void f32_gemv_kernel(const float* __restrict__
 //    partials [ksplit, M, N].
 constexpr int kTileKN = 8192;                          // BN * BK
 
+// Occupancy: the LDS tiles allow two or three workgroups per CU, so the
+// register budget is that of two waves per SIMD (without the bound the
+// compiler assumes more and spills the accumulators' neighbours into AGPRs).
 template <int WFMT, int BM, int BN, int DP>
-__global__ __launch_bounds__(256) void wgemm_tile_kernel(KArgs a) {
+__global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
   constexpr int BK = kTileKN / BN, KP = BK + 8;       // K step, LDS row pitch (bf16)
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int MB = WM / 16, NB = WN / 16;          // 16x16 blocks per wave
@@ -617,7 +620,10 @@ __global__ __launch_bounds__(256) void wgemm_tile_kernel(KArgs a) {
       for (int d = 0; d < 4; ++d) {
         // nibbles k = 8d .. 8d+7 (low nibble = even k) -> bf16(u * s + z)
         const uint32_t w = wr[0][d];
-        const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        // opaque to the optimiser: otherwise it folds the masks into a
+        // bit-field extract per nibble ahead of each v_cvt_f32_ubyteN
+        asm volatile("" : "+v"(lo), "+v"(hi));
         u32x4 o;
         o[0] = pack_bf16x2(ubyte_f32<0>(lo) * gs + gz, ubyte_f32<0>(hi) * gs + gz);
         o[1] = pack_bf16x2(ubyte_f32<1>(lo) * gs + gz, ubyte_f32<1>(hi) * gs + gz);
@@ -776,8 +782,9 @@ size_t lds_bytes(int wfmt, int mt, int R, int rt, int nw, int KR, int upw) {
 // (64 / 128), 0 = choose (BN 64 for M <= 64, else 128; BM from M). The K
 // split keeps every split on whole K steps (int4: whole 128-k groups). By
 // default it grows until about two workgroups per CU are launched, while each
-// split keeps at least 256 k and the fp32 partials (written and read again,
-// 8*ksplit*M*N bytes) stay below half the weight bytes.
+// split keeps at least 256 k and, for M <= 64 (weight-bound), the fp32
+// partials (written and read again, 8*ksplit*M*N bytes) stay below half the
+// weight bytes.
 int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int req_bn,
                    int req_ks, Tiling* t) {
   const int bn = (req_bn == 64 || req_bn == 128) ? req_bn : M <= 64 ? 64 : 128;
@@ -812,10 +819,11 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
       int64_t nx = ks + 1;
       while (nx <= units && units % nx) ++nx;
       if (nx > units || K / nx < 256) break;
-      // the fp32 partials (written, then read by the reduction) stay below
-      // half the weight bytes: beyond that they cost more than the extra
-      // workgroups gain, whether the size is weight- or MFMA-bound
-      if (8.0 * nx * M * N > 0.5 * wbytes) break;
+      // weight-bound sizes: the fp32 partials (written, then read by the
+      // reduction) stay below half the weight bytes (beyond that they cost
+      // more than the extra workgroups gain); MFMA-bound sizes need the
+      // workgroups more than they mind the partials
+      if (M <= 64 && 8.0 * nx * M * N > 0.5 * wbytes) break;
       ks = nx;
     }
   }
