@@ -541,9 +541,30 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
 
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
   const int r = lane >> 4, c = lane & 15;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.z * BM;
+  // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by
+  // linear id, and each XCD has its own L2. The M blocks of one (N tile,
+  // split) read the same weights, so they go to the same XCD at about the
+  // same time: the first read comes from HBM, the others from that L2.
+  int tile_n, split, mblk;
+  {
+    const int ntl = gridDim.x, nks = gridDim.y, nmb = gridDim.z;
+    const int lin = blockIdx.x + ntl * (blockIdx.y + nks * blockIdx.z);
+    const int units = ntl * nks;
+    int unit;
+    if (nmb > 1 && units % 8 == 0) {
+      const int xcd = lin % 8, j = lin / 8;
+      unit = xcd * (units / 8) + j / nmb;
+      mblk = j % nmb;
+    } else {
+      unit = lin % units;
+      mblk = lin / units;
+    }
+    tile_n = unit % ntl;
+    split = unit / ntl;
+  }
+  const int n0 = tile_n * BN, m0 = mblk * BM;
   const int K = a.K;
-  const int kper = K / a.ksplit, kb = blockIdx.y * kper, nsteps = kper / BK;
+  const int kper = K / a.ksplit, kb = split * kper, nsteps = kper / BK;
   const int wn = (wid & 1) * WN, wm = (wid >> 1) * WM;
   const int wrow = tid / TPR, wpart = tid % TPR;      // this thread's weight row / 32-k part
   constexpr int PPR = BK / 8, BROWS = 256 / PPR;      // bf16: 16-byte pieces per row, rows per load
@@ -715,7 +736,7 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
         uint32_t p[2] = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         __builtin_memcpy(a.out + (size_t)m * a.N + n, p, sizeof(p));
       } else {
-        float* dst = a.part + ((size_t)blockIdx.y * a.M + m) * a.N + n;
+        float* dst = a.part + ((size_t)split * a.M + m) * a.N + n;
         *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
       }
     }
