@@ -501,7 +501,8 @@ __global__ __launch_bounds__(256) void f32_gemv_kernel(const float* __restrict__
 // Tiled form for M > 16, where the product is a dense contraction rather
 // than a weight stream:
 //  * a workgroup of 4 waves owns a BN (N) x BM (M) output tile and one K
-//    range (split blockIdx.y); each wave a BN/2 x BM/2 quarter (2 x 2
+//    range (a split; the block id is remapped so that the M blocks of one
+//    weight tile run on one XCD); each wave a BN/2 x BM/2 quarter (2 x 2
 //    waves). A K step is BK = 8192 / BN wide (BN 128: 64, BN 64: 128), so a
 //    thread always loads 32 consecutive k of one weight row per step;
 //  * per K step the weights are dequantised once into LDS as bf16
