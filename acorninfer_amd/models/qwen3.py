@@ -427,14 +427,15 @@ class Qwen3DecodeModel:
 
     def time_projection(self, lins: list[QLinear], M: int, tiling, reps: int = 3,
                         swiglu: bool = False, with_act: bool = False,
-                        with_reduce: bool = False) -> float:
+                        with_reduce: bool = False, with_norm: bool = False) -> float:
         """Average µs of one launch of `tiling`, measured as a hipGraph of one
         launch per weight in `lins` (distinct weights, so the 256 MB MALL does
         not hold them between launches) on a private stream with HIP events.
-        with_act adds the separate SwiGLU kernel the fused form saves;
-        with_reduce adds a split-order reduction of the partials, standing in
-        for the step's consumer kernel (qkv epilogue, K1), whose cost grows with
-        the split count."""
+        The step's consumer of the partials is timed with it, because its cost
+        grows with the split count: with_act adds the separate SwiGLU kernel
+        the fused form saves; with_reduce a split-order reduction (the qkv
+        epilogue's, spread over many workgroups); with_norm the step's own K1
+        (one workgroup per row), which reads the o and down partials."""
         from acorninfer_amd.ops.quant_gemm import _native_cfg
         lin0 = lins[0]
         planner = lin0.swiglu_plan if swiglu else lin0.plan
@@ -443,6 +444,10 @@ class Qwen3DecodeModel:
         part = torch.empty(t.ksplit, M, lin0.N, dtype=torch.float32, device=self.device)
         act = torch.empty(M, lin0.N // 2, dtype=self.dtype, device=self.device)
         red = torch.empty(M, lin0.N, dtype=self.dtype, device=self.device) if with_reduce else None
+        if with_norm:
+            res = torch.zeros(M, lin0.N, dtype=self.dtype, device=self.device)
+            nrm = torch.empty(M, lin0.N, dtype=self.dtype, device=self.device)
+            nw = torch.ones(lin0.N, dtype=self.norm.dtype, device=self.device)
         s = torch.cuda.Stream(self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(s):
@@ -461,6 +466,11 @@ class Qwen3DecodeModel:
                             check(lib().acorn_splitk_reduce(ptr(part), t.ksplit, M * lin.N,
                                                             ptr(red), dtype_code(red),
                                                             s.cuda_stream), "splitk_reduce")
+                        if with_norm:
+                            check(lib().acorn_fused_add_rmsnorm_partials(
+                                ptr(part), t.ksplit, ptr(res), ptr(res), ptr(nw), ptr(nrm), None,
+                                M, lin.N, float(self.cfg.rms_norm_eps), dtype_code(nrm),
+                                dtype_code(nw), s.cuda_stream), "K1")
             body()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=s):
@@ -497,10 +507,11 @@ class Qwen3DecodeModel:
                 modes = [True, False] if self.fused_swiglu(batch) else [False]
             for sw in modes:
                 act = name == "gate_up" and not sw
-                red = name in ("qkv", "o", "down")    # consumers that read the partials
+                red = name == "qkv"                   # the qkv epilogue reads its partials
+                nrm = name in ("o", "down")           # ... K1 those of o and down
                 for c in candidates(batch, lins[0].N, lins[0].K, lins[0].fmt, swiglu=sw):
                     us = self.time_projection(lins, batch, c, swiglu=sw, with_act=act,
-                                              with_reduce=red)
+                                              with_reduce=red, with_norm=nrm)
                     if verbose:
                         print(f"TUNE {name} M={batch} swiglu={sw} {tuple(c)} {us:.2f} us",
                               flush=True)
