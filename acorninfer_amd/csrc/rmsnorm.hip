@@ -71,11 +71,16 @@ __global__ __launch_bounds__(kNT) void fused_add_rmsnorm_kernel(
   }
 }
 
-// Vectorised form for cols % 8 == 0 and cols <= 8 * kNT * kVMax: each thread
-// owns up to kVMax 8-element vectors of the row (16-byte loads for bf16),
-// issues every load of its vectors before using any, and keeps the rounded
-// residual in registers for the second pass.
-constexpr int kVMax = 4;
+// Vectorised form for cols % 8 == 0 and cols <= 8 * kVecNT * kVMax: each
+// thread owns up to VM 8-element vectors of the row and requests every
+// load it needs (weights, residual, and the first kPartBatch split partials,
+// or x) before using any, so the row costs one memory round trip before the
+// reduction. Vector indices past the row re-read its last vector (loads stay
+// unconditional, which keeps the wait counts static); their results are not
+// stored. Split partials are added in split order, as acorn::sum_splits does.
+constexpr int kVecNT = 512;    // threads per row
+constexpr int kVMax = 2;       // largest VM: cols <= 8192
+constexpr int kPartBatch = 8;  // split partials requested per vector up front
 
 template <typename T>
 __device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
@@ -92,56 +97,83 @@ __device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
   __builtin_memcpy(p, t, sizeof(t));
 }
 
-template <typename T, typename TW, bool HAS_RES, bool FROM_PART>
-__global__ __launch_bounds__(kNT) void fused_add_rmsnorm_vec_kernel(
+template <typename T, typename TW, bool HAS_RES, bool FROM_PART, int VM>
+__global__ __launch_bounds__(kVecNT) void fused_add_rmsnorm_vec_kernel(
     const T* __restrict__ x, const float* __restrict__ part, int nsplit,
     const T* __restrict__ res, T* __restrict__ res_out, const TW* __restrict__ w,
     T* __restrict__ normed, T* __restrict__ x_out, int rows, int cols, float eps) {
 #pragma clang fp contract(off)
-  __shared__ float red[kNT / kWave];
+  typedef float f8 __attribute__((ext_vector_type(8)));
+  __shared__ float red[kVecNT / kWave];
   const size_t base = (size_t)blockIdx.x * cols;
   const size_t plane = (size_t)rows * cols;
   const int nvec = cols / 8;
-  float v[kVMax][8];
+  int vi[VM];
+  size_t col[VM];
+#pragma unroll
+  for (int j = 0; j < VM; ++j) {
+    vi[j] = threadIdx.x + j * kVecNT;
+    col[j] = (size_t)min(vi[j], nvec - 1) * 8;
+  }
+  // ---- requests ----
+  float wv[VM][8], rv[VM][8], a[VM][8];
+  f8 pv[VM][kPartBatch];
+#pragma unroll
+  for (int j = 0; j < VM; ++j) {
+    load8<TW>(w + col[j], wv[j]);
+    if constexpr (HAS_RES) load8<T>(res + base + col[j], rv[j]);
+    if constexpr (FROM_PART) {
+#pragma unroll
+      for (int u = 0; u < kPartBatch; ++u)
+        pv[j][u] = *(const f8*)(part + (size_t)min(u, nsplit - 1) * plane + base + col[j]);
+    } else {
+      load8<T>(x + base + col[j], a[j]);
+    }
+  }
+  // ---- use ----
+  float v[VM][8];
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kVMax; ++j) {
-    const int vi = threadIdx.x + j * kNT;
-    if (vi >= nvec) break;
-    const size_t off = base + (size_t)vi * 8;
-    float a[8];
+  for (int j = 0; j < VM; ++j) {
+    const bool own = vi[j] < nvec;
     if constexpr (FROM_PART) {
-      sum_splits8(part + off, plane, nsplit, a);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] = round_to<T>(a[i]);
-      if (x_out) store8<T>(x_out + off, a);
-    } else {
-      load8<T>(x + off, a);
-    }
-    if constexpr (HAS_RES) {
-      float r[8];
-      load8<T>(res + off, r);
+      for (int i = 0; i < 8; ++i) a[j][i] = pv[j][0][i];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a[i] = r[i] + a[i];
+      for (int u = 1; u < kPartBatch; ++u) {
+        if (u < nsplit) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) a[j][i] = a[j][i] + pv[j][u][i];
+        }
+      }
+      for (int sp = kPartBatch; sp < nsplit; ++sp) {
+        const f8 q = *(const f8*)(part + (size_t)sp * plane + base + col[j]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a[j][i] = a[j][i] + q[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[j][i] = round_to<T>(a[j][i]);
+      if (x_out && own) store8<T>(x_out + base + col[j], a[j]);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      v[j][i] = round_to<T>(a[i]);
-      ss += v[j][i] * v[j][i];
+      float t = a[j][i];
+      if constexpr (HAS_RES) t = rv[j][i] + t;
+      v[j][i] = round_to<T>(t);
+      if (own) ss += v[j][i] * v[j][i];
     }
-    store8<T>(res_out + off, v[j]);
+    if (own) store8<T>(res_out + base + col[j], v[j]);
   }
-  ss = block_sum<kNT>(ss, red);
+  ss = block_sum<kVecNT>(ss, red);
   const float inv = 1.0f / sqrtf(ss / (float)cols + eps);
 #pragma unroll
-  for (int j = 0; j < kVMax; ++j) {
-    const int vi = threadIdx.x + j * kNT;
-    if (vi >= nvec) break;
-    float wv[8], o[8];
-    load8<TW>(w + (size_t)vi * 8, wv);
+  for (int j = 0; j < VM; ++j) {
+    if (vi[j] < nvec) {
+      float o[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (v[j][i] * inv) * wv[i];
-    store8<T>(normed + base + (size_t)vi * 8, o);
+      for (int i = 0; i < 8; ++i) o[i] = (v[j][i] * inv) * wv[j][i];
+      store8<T>(normed + base + col[j], o);
+    }
   }
 }
 
@@ -149,34 +181,34 @@ template <typename T, typename TW>
 int launch_k1(const void* x, const float* part, int nsplit, const void* res, void* res_out,
               const void* w, void* normed, void* x_out, int64_t rows, int64_t cols, float eps,
               hipStream_t st) {
-  dim3 grid((unsigned)rows), block(kNT);
+  dim3 grid((unsigned)rows);
   const T* xp = (const T*)x;
   const T* rp = (const T*)res;
   T* rop = (T*)res_out;
   const TW* wp = (const TW*)w;
   T* np = (T*)normed;
   T* xo = (T*)x_out;
-  const bool vec = cols % 8 == 0 && cols <= 8 * kNT * kVMax;
-#define ACORN_K1(KERNEL, RES, PART)                                                        \
-  KERNEL<T, TW, RES, PART><<<grid, block, 0, st>>>(xp, part, nsplit, rp, rop, wp, np, xo, \
-                                                   (int)rows, (int)cols, eps)
-  if (vec) {
-    if (part) {
-      if (res) ACORN_K1(fused_add_rmsnorm_vec_kernel, true, true);
-      else ACORN_K1(fused_add_rmsnorm_vec_kernel, false, true);
-    } else {
-      if (res) ACORN_K1(fused_add_rmsnorm_vec_kernel, true, false);
-      else ACORN_K1(fused_add_rmsnorm_vec_kernel, false, false);
-    }
+#define ACORN_K1(NT, ...)                                                                \
+  __VA_ARGS__<<<grid, dim3(NT), 0, st>>>(xp, part, nsplit, rp, rop, wp, np, xo, (int)rows, \
+                                        (int)cols, eps)
+#define ACORN_K1_RP(NT, KERNEL, ...)                                  \
+  do {                                                                \
+    if (part) {                                                       \
+      if (res) ACORN_K1(NT, KERNEL<T, TW, true, true __VA_ARGS__>);   \
+      else ACORN_K1(NT, KERNEL<T, TW, false, true __VA_ARGS__>);      \
+    } else {                                                          \
+      if (res) ACORN_K1(NT, KERNEL<T, TW, true, false __VA_ARGS__>);  \
+      else ACORN_K1(NT, KERNEL<T, TW, false, false __VA_ARGS__>);     \
+    }                                                                 \
+  } while (0)
+  if (cols % 8 == 0 && cols <= 8 * kVecNT) {
+    ACORN_K1_RP(kVecNT, fused_add_rmsnorm_vec_kernel, , 1);
+  } else if (cols % 8 == 0 && cols <= 8 * kVecNT * kVMax) {
+    ACORN_K1_RP(kVecNT, fused_add_rmsnorm_vec_kernel, , kVMax);
   } else {
-    if (part) {
-      if (res) ACORN_K1(fused_add_rmsnorm_kernel, true, true);
-      else ACORN_K1(fused_add_rmsnorm_kernel, false, true);
-    } else {
-      if (res) ACORN_K1(fused_add_rmsnorm_kernel, true, false);
-      else ACORN_K1(fused_add_rmsnorm_kernel, false, false);
-    }
+    ACORN_K1_RP(kNT, fused_add_rmsnorm_kernel);
   }
+#undef ACORN_K1_RP
 #undef ACORN_K1
   ACORN_LAUNCH_CHECK();
   return ACORN_OK;
