@@ -501,6 +501,16 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
          ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
+// Byte offset of the per-wave K slabs in the MFMA kernel's dynamic LDS:
+// after the wave partials [NWV][REP][D], their (m, l) and the split's pps
+// block ids, rounded up to 16 bytes.
+__host__ __device__ constexpr size_t k3_slab_offset(int nwv, int rep, int d, int pps) {
+  return ((size_t)(nwv * rep * d + 2 * nwv * rep) * 4 + (size_t)pps * 4 + 15) / 16 * 16;
+}
+__host__ __device__ constexpr size_t k3_slab_bytes(int nwv, int d) {
+  return (size_t)nwv * kChunk * (2 * d + 16);
+}
+
 template <typename T, int D, int REP, int NWV, bool PAGE16, int DEPTH = 3>
 __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) void paged_attn_mfma_kernel(
     const T* __restrict__ q, const T* __restrict__ k_pages, const T* __restrict__ v_pages,
@@ -551,6 +561,13 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   }
   const int vp0 = min(vn0, wp1), vp1 = min(vp0 + ppv, wp1);
   const int tstart = vp0 << pshift, tend = min(vp1 << pshift, L);
+  // PAGE16: K rows are loaded like V rows (each load instruction reads four
+  // tokens' whole 2D-byte rows, so every cache line is fetched by one
+  // instruction) and turned into the MFMA A layout through this wave's slab.
+  // Loading the A layout directly would read 16 tokens' 64-byte pieces per
+  // instruction, each line split over two instructions.
+  constexpr int KPITCH = 2 * D + 16;           // bytes per slab row
+  uint8_t* kslab = (uint8_t*)smem + k3_slab_offset(NWV, REP, D, pps) + (size_t)wid * CH * KPITCH;
 
   // q^T as the B operand (raw; the softmax scale is applied to S)
   u32x4_t qb[KB];
@@ -571,10 +588,10 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   const int tlast = tstart + max(tend - tstart - 1, 0) / CH * CH;
 
   const int tok_stride = KV * D;
-  const int k_off = c * tok_stride + 8 * r;          // this lane's K row / dims
   const int v_off = 4 * r * tok_stride + DPL * c;    // this lane's V rows / dims
   struct Chunk {
-    u32x4_t k[KB];
+    u32x4_t k[PAGE16 ? 1 : KB];                // A layout (pages of < 16 tokens)
+    uint32_t kr[PAGE16 ? 4 : 1][VW];           // V layout (PAGE16)
     uint32_t v[4][VW];
   };
   auto page_base = [&](int t) -> size_t {            // element offset of token t's row
@@ -591,11 +608,11 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
       const int pg = reg_pages ? __builtin_amdgcn_readlane(pgr, pi)
                                : __builtin_amdgcn_readfirstlane(tbl[pi + vp0 - wp0]);
       const size_t base = ((size_t)pg * P + (t0 & (P - 1))) * tok_stride + (size_t)kvh * D;
-      const T* kb = k_pages + base + (spare ? 0 : k_off);
+      const T* kb = k_pages + base + (spare ? 0 : v_off);
       const T* vb = v_pages + base + (spare ? 0 : v_off);
       const int vstep = spare ? 0 : tok_stride;
 #pragma unroll
-      for (int j = 0; j < KB; ++j) ch.k[j] = *(const u32x4_t*)(kb + (spare ? 0 : 32 * j));
+      for (int j = 0; j < 4; ++j) __builtin_memcpy(ch.kr[j], kb + j * vstep, sizeof(ch.kr[j]));
 #pragma unroll
       for (int j = 0; j < 4; ++j) __builtin_memcpy(ch.v[j], vb + j * vstep, sizeof(ch.v[j]));
     } else {
@@ -623,8 +640,27 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   };
   auto consume = [&](int t0, Chunk& ch) {
     f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (PAGE16) {
+      // slab row = token, lane (r, c) wrote tokens 4 r + j, dims DPL c ...;
+      // it reads token c, dims 32 j + 8 r ... (the A operand of k-block j)
 #pragma unroll
-    for (int j = 0; j < KB; ++j) sc = mfma16x16x32<T>(ch.k[j], qb[j], sc);
+      for (int j = 0; j < 4; ++j) {
+        uint8_t* dst = kslab + (4 * r + j) * KPITCH + 2 * DPL * c;
+        if constexpr (VW == 4)
+          *(u32x4_t*)dst = u32x4_t{ch.kr[j][0], ch.kr[j][1], ch.kr[j][2], ch.kr[j][3]};
+        else
+#pragma unroll
+          for (int w = 0; w < VW; ++w) ((uint32_t*)dst)[w] = ch.kr[j][w];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+        sc = mfma16x16x32<T>(*(const u32x4_t*)(kslab + c * KPITCH + 2 * (32 * j + 8 * r)), qb[j], sc);
+    } else {
+#pragma unroll
+      for (int j = 0; j < KB; ++j) sc = mfma16x16x32<T>(ch.k[j], qb[j], sc);
+    }
     float s[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[i] = sc[i] * scale_log2;
@@ -856,11 +892,11 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
     // that the dispatcher spreads over the CUs); large ones as NWV waves
     // merged in LDS
     const int64_t pps = (table_stride + S - 1) / S;
+    const bool page16 = P % 16 == 0;
     const bool one = pps <= kOneWavePages;
     const int nwv = one ? 1 : kAttnWaves;
-    const size_t lds = (size_t)(nwv * REP * D + 2 * nwv * REP) * 4 + (size_t)pps * 4;
+    const size_t lds = k3_slab_offset(nwv, REP, D, (int)pps) + (page16 ? k3_slab_bytes(nwv, D) : 0);
     if (lds > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
-    const bool page16 = P % 16 == 0;
     const int which = (one ? 2 : 0) + (page16 ? 1 : 0);
     using KFn = void (*)(const T*, const T*, const T*, const int32_t*, const int32_t*, T*, float*,
                          float*, float*, int, int, int, int, int, int, float);

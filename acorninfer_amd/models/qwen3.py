@@ -584,8 +584,9 @@ def attention_splits(batch: int, kv_heads: int, max_pages: int, *,
     Small splits (here `unit_pages`, 64 tokens at P = 16) run as one-wave
     workgroups: many equal work units that the dispatcher spreads evenly over
     the CUs, whatever the mix of context lengths. S is capped at `max_splits`
-    (workspace B*H*S*(D+2) floats; the combine reads one partial per used
-    split), so very wide tables get proportionally larger splits."""
+    (workspace B*H*S*(D+2) floats; K3 writes and the combine reads one
+    partial per used split), so very wide tables get proportionally larger
+    splits."""
     del batch, kv_heads  # the unit size, not the grid, sets the balance
     return max(1, min(-(-max_pages // unit_pages), max_splits))
 
