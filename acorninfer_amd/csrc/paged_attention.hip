@@ -548,6 +548,18 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   if (reg_pages && lane < ppv && vn0 + lane < min(wp0 + pps, table_stride))
     pgr = trow[vn0 + lane];
   const int L = min(max(lens[b], 0), table_stride * P);
+  // q^T as the B operand (raw; the softmax scale is applied to S), requested
+  // together with the block ids and the length: one round trip before K/V.
+  // Columns c >= REP repeat head REP-1 (unconditional loads keep the wait
+  // counts static); MFMA columns are independent and those are never stored.
+  // (The empty asm pins the loads here; otherwise they sink below the early
+  // exit and cost a second round trip.)
+  u32x4_t qb[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j)
+    qb[j] = *(const u32x4_t*)(q + ((size_t)b * H + kvh * REP + min(c, REP - 1)) * D + 32 * j + 8 * r);
+#pragma unroll
+  for (int j = 0; j < KB; ++j) asm volatile("" ::"v"(qb[j]));
   const int npages = (L + P - 1) >> pshift;
   const int nsb = max(1, (npages + pps - 1) / pps);  // splits this sequence uses
   if (sp >= nsb) return;                             // uniform over the workgroup
@@ -569,14 +581,6 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   constexpr int KPITCH = 2 * D + 16;           // bytes per slab row
   uint8_t* kslab = (uint8_t*)smem + k3_slab_offset(NWV, REP, D, pps) + (size_t)wid * CH * KPITCH;
 
-  // q^T as the B operand (raw; the softmax scale is applied to S)
-  u32x4_t qb[KB];
-#pragma unroll
-  for (int j = 0; j < KB; ++j) {
-    qb[j] = u32x4_t{0u, 0u, 0u, 0u};
-    if (c < REP)
-      qb[j] = *(const u32x4_t*)(q + ((size_t)b * H + kvh * REP + c) * D + 32 * j + 8 * r);
-  }
   float m = -INFINITY, l = 0.f;
   f32x4_t acc[DPL];
 #pragma unroll
