@@ -831,23 +831,36 @@ __global__ __launch_bounds__(kCombineWaves * kWave) void paged_attn_combine_kern
 #pragma unroll
   for (int i = 0; i < DL; ++i) a[i] = 0.f;
   float M = -INFINITY, lsum = 0.f;
+  // the length as a vector load (a VGPR index), so that it is in flight with
+  // the partial rows instead of a scalar round trip ahead of them
+  int bi = (int)(row / H);
+  asm volatile("" : "+v"(bi));
+  const int lraw = lens[bi];
   int nsb = 0;
   for (int s0 = 0; s0 < S; s0 += kWave) {
-    // ---- requests: length, (m, l) of slots s0 + lane, this wave's rows ----
-    const int L = min(max(lens[row / H], 0), table_stride * P);
-    const bool have = s0 + lane < S;
-    const float ml = have ? m[s0 + lane] : -INFINITY;
-    const float ll = have ? l[s0 + lane] : 0.f;
+    // ---- requests: (m, l) of slots s0 + lane, this wave's rows ----
+    // Slots past S re-read slot S-1 and dims past D re-read dim D-1
+    // (unconditional loads keep the wait counts static); every use below is
+    // masked by s < nsb <= S.
+    const float ml = m[min(s0 + lane, S - 1)];
+    const float ll = l[min(s0 + lane, S - 1)];
     float x[SPW][DL];
 #pragma unroll
     for (int k = 0; k < SPW; ++k) {
-      const int s = s0 + wid + kCombineWaves * k;
+      const int s = min(s0 + wid + kCombineWaves * k, S - 1);
 #pragma unroll
-      for (int i = 0; i < DL; ++i)
-        x[k][i] = (s < S && d0 + i < D) ? src[(size_t)s * D + d0 + i] : 0.f;
+      for (int i = 0; i < DL; ++i) x[k][i] = src[(size_t)s * D + min(d0 + i, D - 1)];
     }
+    // The empty asm pins the requests (with the length above) ahead of the
+    // early exit; otherwise they sink below it and cost a second round trip.
+    asm volatile("" ::"v"(ml), "v"(ll), "v"(lraw));
+#pragma unroll
+    for (int k = 0; k < SPW; ++k)
+#pragma unroll
+      for (int i = 0; i < DL; ++i) asm volatile("" ::"v"(x[k][i]));
     // ---- use ----
-    nsb = ((L + P - 1) / P + pps - 1) / pps;
+    const int L = min(max(__builtin_amdgcn_readfirstlane(lraw), 0), table_stride * P);
+    nsb = ((L + P - 1) / P + pps - 1) / pps;         // <= S
     if (nsb <= 1) return;                            // uniform over the workgroup
     const bool used = s0 + lane < nsb;
     const float mv = used ? ml : -INFINITY;
