@@ -45,29 +45,47 @@ __global__ __launch_bounds__(kWave) void rope_kernel(T* __restrict__ x, int head
   }
 }
 
-// Per-head RMSNorm over the lane's pairs (x1[j], x2[j]) followed by RoPE.
-template <typename T, typename TW>
-__device__ __forceinline__ void norm_rope_row(float (&x1)[kMaxPairs], float (&x2)[kMaxPairs],
-                                              int half, const TW* __restrict__ w, float eps,
-                                              float pos, const float* __restrict__ inv_freq) {
+// Per-head RMSNorm over the lane's NP pairs (x1[j], x2[j]) followed by RoPE,
+// with the norm weights (w1 = w[i], w2 = w[i + half]) and the frequencies
+// already in registers.
+template <typename T, int NP>
+__device__ __forceinline__ void norm_rope_pre(float (&x1)[NP], float (&x2)[NP], int half,
+                                              const float (&w1)[NP], const float (&w2)[NP],
+                                              float eps, float pos, const float (&fr)[NP]) {
 #pragma clang fp contract(off)
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kMaxPairs; ++j) {
+  for (int j = 0; j < NP; ++j) {
     const int i = threadIdx.x + j * kWave;
     if (i < half) ss += x1[j] * x1[j] + x2[j] * x2[j];
   }
   ss = wave_sum(ss);
   const float inv = 1.0f / sqrtf(ss / (float)(2 * half) + eps);
 #pragma unroll
-  for (int j = 0; j < kMaxPairs; ++j) {
+  for (int j = 0; j < NP; ++j) {
     const int i = threadIdx.x + j * kWave;
     if (i < half) {
-      x1[j] = round_to<T>((x1[j] * inv) * to_f32(w[i]));
-      x2[j] = round_to<T>((x2[j] * inv) * to_f32(w[i + half]));
-      rope_pair<T>(x1[j], x2[j], pos, inv_freq[i]);
+      x1[j] = round_to<T>((x1[j] * inv) * w1[j]);
+      x2[j] = round_to<T>((x2[j] * inv) * w2[j]);
+      rope_pair<T>(x1[j], x2[j], pos, fr[j]);
     }
   }
+}
+
+// The same, loading the weights and frequencies of the lane's pairs.
+template <typename T, typename TW>
+__device__ __forceinline__ void norm_rope_row(float (&x1)[kMaxPairs], float (&x2)[kMaxPairs],
+                                              int half, const TW* __restrict__ w, float eps,
+                                              float pos, const float* __restrict__ inv_freq) {
+  float w1[kMaxPairs], w2[kMaxPairs], fr[kMaxPairs];
+#pragma unroll
+  for (int j = 0; j < kMaxPairs; ++j) {
+    const int i = min(threadIdx.x + j * kWave, half - 1);
+    w1[j] = to_f32(w[i]);
+    w2[j] = to_f32(w[i + half]);
+    fr[j] = inv_freq[i];
+  }
+  norm_rope_pre<T, kMaxPairs>(x1, x2, half, w1, w2, eps, pos, fr);
 }
 
 template <typename T, typename TW, bool POS64>
@@ -103,14 +121,21 @@ __global__ __launch_bounds__(kWave) void qknorm_rope_kernel(
 }
 
 // Decode-step epilogue of the fused qkv projection. Rows per batch entry:
-// [0, H) q heads, [H, H+KV) k heads, [H+KV, H+2KV) v heads.
-template <typename T, typename TW>
+// [0, H) q heads, [H, H+KV) k heads, [H+KV, H+2KV) v heads. One wavefront per
+// row; lane pairs (i, i + half), NP per lane. Everything the row needs (the
+// first kSplitBatch split partials of each element, the norm weights, the
+// frequencies, the position and the page slot) is requested before any of it
+// is used: one memory round trip. Indices past the row re-read its last pair
+// (unconditional loads keep the wait counts static); those lanes store
+// nothing. Partials are added in split order, as acorn::sum_splits does.
+template <typename T, typename TW, int NP>
 __global__ __launch_bounds__(kWave) void qkv_epilogue_kernel(
     const float* __restrict__ part, int nsplit, T* __restrict__ q_out,
     T* __restrict__ k_pages, T* __restrict__ v_pages, const int64_t* __restrict__ pages,
     const int64_t* __restrict__ slots, int batch, int H, int KV, int D, int P,
     int64_t num_blocks, const TW* __restrict__ q_w, const TW* __restrict__ k_w, float eps,
     const int64_t* __restrict__ pos, const float* __restrict__ inv_freq) {
+#pragma clang fp contract(off)
   const int rows_per_b = H + 2 * KV;
   const int b = blockIdx.x / rows_per_b;
   const int h = blockIdx.x % rows_per_b;
@@ -118,37 +143,63 @@ __global__ __launch_bounds__(kWave) void qkv_epilogue_kernel(
   const size_t width = (size_t)rows_per_b * D;
   const size_t plane = (size_t)batch * width;
   const float* src = part + (size_t)b * width + (size_t)h * D;
-  float x1[kMaxPairs], x2[kMaxPairs];
+  const TW* w = h < H ? q_w : k_w;  // v rows load them too, unused
+  // ---- requests ----
+  float pa[NP][kSplitBatch], pc[NP][kSplitBatch], w1[NP], w2[NP], fr[NP];
 #pragma unroll
-  for (int j = 0; j < kMaxPairs; ++j) {
-    const int i = threadIdx.x + j * kWave;
-    float a = 0.f, c = 0.f;
-    if (i < half) {
-      a = sum_splits(src + i, plane, nsplit);
-      c = sum_splits(src + i + half, plane, nsplit);
+  for (int j = 0; j < NP; ++j) {
+    const int ic = min(threadIdx.x + j * kWave, half - 1);
+#pragma unroll
+    for (int u = 0; u < kSplitBatch; ++u) {
+      const float* p = src + (size_t)min(u, nsplit - 1) * plane + ic;
+      pa[j][u] = p[0];
+      pc[j][u] = p[half];
+    }
+    w1[j] = to_f32(w[ic]);
+    w2[j] = to_f32(w[ic + half]);
+    fr[j] = inv_freq[ic];
+  }
+  const float p = (float)pos[b];
+  const uint64_t page = (uint64_t)pages[b], slot = (uint64_t)slots[b];
+  // ---- use ----
+  float x1[NP], x2[NP];
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    float a = pa[j][0], c = pc[j][0];
+#pragma unroll
+    for (int u = 1; u < kSplitBatch; ++u) {
+      if (u < nsplit) {
+        a = a + pa[j][u];
+        c = c + pc[j][u];
+      }
+    }
+    const int ic = min(threadIdx.x + j * kWave, half - 1);
+    for (int sp = kSplitBatch; sp < nsplit; ++sp) {
+      const float* q = src + (size_t)sp * plane + ic;
+      a = a + q[0];
+      c = c + q[half];
     }
     x1[j] = round_to<T>(a);  // the projection's bf16 output
     x2[j] = round_to<T>(c);
   }
   T* dst = nullptr;
   if (h < H) {
-    norm_rope_row<T, TW>(x1, x2, half, q_w, eps, (float)pos[b], inv_freq);
+    norm_rope_pre<T, NP>(x1, x2, half, w1, w2, eps, p, fr);
     dst = q_out + ((size_t)b * H + h) * D;
   } else {
     const int kvh = h < H + KV ? h - H : h - H - KV;
     // A (page, slot) outside the pool is dropped rather than written.
-    const uint64_t page = (uint64_t)pages[b], slot = (uint64_t)slots[b];
     const bool in_pool = page < (uint64_t)num_blocks && slot < (uint64_t)P;
     const size_t off = in_pool ? ((page * P + slot) * KV + kvh) * D : 0;
     if (h < H + KV) {
-      norm_rope_row<T, TW>(x1, x2, half, k_w, eps, (float)pos[b], inv_freq);
+      norm_rope_pre<T, NP>(x1, x2, half, w1, w2, eps, p, fr);
       if (in_pool) dst = k_pages + off;
     } else {
       if (in_pool) dst = v_pages + off;
     }
   }
 #pragma unroll
-  for (int j = 0; j < kMaxPairs; ++j) {
+  for (int j = 0; j < NP; ++j) {
     const int i = threadIdx.x + j * kWave;
     if (dst && i < half) {
       dst[i] = from_f32<T>(x1[j]);
@@ -192,7 +243,8 @@ int launch_qkv(const float* part, int64_t nsplit, void* q_out, void* kp, void* v
                int64_t D, int64_t P, int64_t NB, const void* qw, const void* kw, float eps,
                const int64_t* pos, const float* inv_freq, hipStream_t st) {
   dim3 grid((unsigned)(batch * (H + 2 * KV))), block(kWave);
-  qkv_epilogue_kernel<T, TW><<<grid, block, 0, st>>>(
+  auto kfn = D <= 2 * kWave ? qkv_epilogue_kernel<T, TW, 1> : qkv_epilogue_kernel<T, TW, kMaxPairs>;
+  kfn<<<grid, block, 0, st>>>(
       part, (int)nsplit, (T*)q_out, (T*)kp, (T*)vp, pages, slots, (int)batch, (int)H, (int)KV,
       (int)D, (int)P, NB, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
   ACORN_LAUNCH_CHECK();
