@@ -90,7 +90,10 @@ __global__ __launch_bounds__(kNT) void sample_kernel(
   __syncthreads();
 
   // ---- pass 1: max (first index on ties), finiteness --------------------
-  // 16-byte vectors, kUnroll of them in flight per thread; a scalar tail
+  // 16-byte vectors, kUnroll of them in flight per thread (a 151936-entry
+  // bf16 row is two rounds of requests); a scalar tail. Vector indices past
+  // the row re-read its last vector (unconditional loads keep the wait
+  // counts static) and are not visited.
   float bv = -INFINITY;
   int64_t bi = INT64_MAX;
   bool bad = false;
@@ -103,7 +106,7 @@ __global__ __launch_bounds__(kNT) void sample_kernel(
   };
   {
     constexpr int E = 16 / sizeof(T);                 // elements per vector
-    constexpr int kUnroll = 4;
+    constexpr int kUnroll = 10;
     struct Vec16 {
       T v[E];
     };
@@ -113,10 +116,7 @@ __global__ __launch_bounds__(kNT) void sample_kernel(
     for (int64_t j0 = tid; j0 < nvec; j0 += (int64_t)kNT * kUnroll) {
       Vec16 buf[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int64_t j = j0 + (int64_t)u * kNT;
-        if (j < nvec) buf[u] = rv[j];
-      }
+      for (int u = 0; u < kUnroll; ++u) buf[u] = rv[min(j0 + (int64_t)u * kNT, nvec - 1)];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int64_t j = j0 + (int64_t)u * kNT;
