@@ -47,6 +47,10 @@ _SIGNATURES = {
                            _i64, _vp, _vp, _f32, _vp, _vp, _i32, _i32, _vp],
     "acorn_paged_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                               _i64, _i64, _i64, _i64, _f32, _i32, _vp],
+    "acorn_paged_attention_qkv": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+                                  _vp, _vp, _f32, _vp, _vp, _i32, _i32, _vp],
+    "acorn_paged_attention_qkv_supported": [_i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32],
     "acorn_quant_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp],
     "acorn_splitk_reduce": [_vp, _i64, _i64, _vp, _i32, _vp],
     "acorn_gemm_plan": [_i64, _i64, _i64, _i32, _vp],

@@ -24,6 +24,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "qkv_math.h"
 
 using namespace acorn;
 
@@ -511,12 +512,36 @@ __host__ __device__ constexpr size_t k3_slab_bytes(int nwv, int d) {
   return (size_t)nwv * kChunk * (2 * d + 16);
 }
 
-template <typename T, int D, int REP, int NWV, bool PAGE16, int DEPTH = 3>
+// The qkv epilogue run by the attention kernel itself (EPI): instead of q,
+// the kernel reads the qkv projection's split-K partials and the epilogue's
+// inputs, exactly as qkv_epilogue_kernel (rope.hip) does.
+struct EpiArgs {
+  const float* part;      // [nsplit][batch][(H + 2 KV) * D] fp32 partials
+  int nsplit, batch;
+  const void* q_w;        // [D] q/k RMSNorm weights, activation dtype
+  const void* k_w;
+  float eps;
+  const int64_t* pos;     // [batch] positions of the new tokens
+  const float* inv_freq;  // [D / 2]
+  const int64_t* pages;   // [batch] (page, slot) the new k/v go to
+  const int64_t* slots;
+  void* k_dst;            // the pools again, written through these
+  void* v_dst;
+};
+constexpr int kQB = 4;    // EPI: split partials requested per element up front
+
+// EPI LDS after the slabs: q of the REP heads [REP][D], then the new k and v rows.
+__host__ __device__ constexpr size_t k3_epi_bytes(int rep, int d) {
+  return (size_t)(rep + 2) * d * 2;
+}
+
+template <typename T, int D, int REP, int NWV, bool PAGE16, int DEPTH = 3, bool EPI = false>
 __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) void paged_attn_mfma_kernel(
     const T* __restrict__ q, const T* __restrict__ k_pages, const T* __restrict__ v_pages,
     const int32_t* __restrict__ tables, const int32_t* __restrict__ lens, T* __restrict__ out,
     float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l, int H,
-    int KV, int P, int num_blocks, int table_stride, int S, float scale_log2) {
+    int KV, int P, int num_blocks, int table_stride, int S, float scale_log2, EpiArgs e) {
+  static_assert(!EPI || (NWV == 1 && PAGE16), "EPI is the one-wave, 16-token-page form");
   constexpr int KB = D / 32;                   // q.k MFMA k-blocks
   constexpr int DPL = D / 16;                  // P V: dims per lane per token = MFMAs per chunk
   constexpr int VW = DPL / 2;                  // ... in 32-bit words
@@ -554,12 +579,42 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   // counts static); MFMA columns are independent and those are never stored.
   // (The empty asm pins the loads here; otherwise they sink below the early
   // exit and cost a second round trip.)
+  // EPI: instead of q, the first kQB split partials of the REP q heads' lane
+  // pairs (i, i + D/2), their norm weights and frequency, and the position.
+  constexpr int HALF = D / 2;
+  const int ic = min(lane, HALF - 1);                // this lane's pair
+  const size_t width = (size_t)(H + 2 * KV) * D;
+  const size_t qplane = (size_t)e.batch * width;
+  const float* qsrc = EPI ? e.part + (size_t)b * width + (size_t)kvh * REP * D + ic : nullptr;
+  float qpa[EPI ? REP : 1][kQB], qpc[EPI ? REP : 1][kQB], qw1 = 0.f, qw2 = 0.f, qfr = 0.f;
+  float epos = 0.f;
   u32x4_t qb[KB];
+  if constexpr (EPI) {
 #pragma unroll
-  for (int j = 0; j < KB; ++j)
-    qb[j] = *(const u32x4_t*)(q + ((size_t)b * H + kvh * REP + min(c, REP - 1)) * D + 32 * j + 8 * r);
+    for (int h = 0; h < REP; ++h) {
 #pragma unroll
-  for (int j = 0; j < KB; ++j) asm volatile("" ::"v"(qb[j]));
+      for (int u = 0; u < kQB; ++u) {
+        const float* pp = qsrc + (size_t)min(u, e.nsplit - 1) * qplane + h * D;
+        qpa[h][u] = pp[0];
+        qpc[h][u] = pp[HALF];
+      }
+    }
+    qw1 = to_f32(((const T*)e.q_w)[ic]);
+    qw2 = to_f32(((const T*)e.q_w)[ic + HALF]);
+    qfr = e.inv_freq[ic];
+    epos = (float)e.pos[b];
+#pragma unroll
+    for (int h = 0; h < REP; ++h)
+#pragma unroll
+      for (int u = 0; u < kQB; ++u) asm volatile("" ::"v"(qpa[h][u]), "v"(qpc[h][u]));
+    asm volatile("" ::"v"(qw1), "v"(qw2), "v"(qfr), "v"(epos));
+  } else {
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      qb[j] = *(const u32x4_t*)(q + ((size_t)b * H + kvh * REP + min(c, REP - 1)) * D + 32 * j + 8 * r);
+#pragma unroll
+    for (int j = 0; j < KB; ++j) asm volatile("" ::"v"(qb[j]));
+  }
   const int npages = (L + P - 1) >> pshift;
   const int nsb = max(1, (npages + pps - 1) / pps);  // splits this sequence uses
   if (sp >= nsb) return;                             // uniform over the workgroup
@@ -580,6 +635,104 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   // instruction, each line split over two instructions.
   constexpr int KPITCH = 2 * D + 16;           // bytes per slab row
   uint8_t* kslab = (uint8_t*)smem + k3_slab_offset(NWV, REP, D, pps) + (size_t)wid * CH * KPITCH;
+  // EPI: q of the REP heads, then the new token's k and v rows (activation dtype)
+  T* qs = (T*)((uint8_t*)smem + k3_slab_offset(NWV, REP, D, pps) + k3_slab_bytes(NWV, D));
+  T* kn = qs + REP * D;
+  T* vn = kn + D;
+  // EPI: the epilogue's arithmetic for each q head (split partials added in
+  // split order, rounded, per-head RMSNorm, RoPE; one pair per lane), run
+  // while the first chunks' loads are in flight
+  auto epi_q = [&]() {
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+      float a = qpa[h][0], cc = qpc[h][0];
+#pragma unroll
+      for (int u = 1; u < kQB; ++u) {
+        if (u < e.nsplit) {
+          a = a + qpa[h][u];
+          cc = cc + qpc[h][u];
+        }
+      }
+      for (int s2 = kQB; s2 < e.nsplit; ++s2) {
+        const float* pp = qsrc + (size_t)s2 * qplane + h * D;
+        a = a + pp[0];
+        cc = cc + pp[HALF];
+      }
+      float x1[1] = {round_to<T>(a)}, x2[1] = {round_to<T>(cc)};
+      const float w1[1] = {qw1}, w2[1] = {qw2}, fr[1] = {qfr};
+      norm_rope_pre<T, 1>(x1, x2, HALF, w1, w2, e.eps, epos, fr);
+      if (lane < HALF) {
+        qs[h * D + lane] = from_f32<T>(x1[0]);
+        qs[h * D + lane + HALF] = from_f32<T>(x2[0]);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the B operand: head min(c, REP-1), dims 32 j + 8 r ...
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      qb[j] = *(const u32x4_t*)(qs + min(c, REP - 1) * D + 32 * j + 8 * r);
+  };
+  // EPI: the wave whose split holds the new token (the sequence's last split)
+  // computes its k and v from the partials, stores them at (page, slot) as
+  // the epilogue does, and keeps them in LDS: the chunk loaded from the pool
+  // holds that row's old contents, so consume() patches it from there.
+  const bool owner = EPI && sp == nsb - 1;
+  auto epi_kv = [&]() {
+    const float* ksrc = e.part + (size_t)b * width + (size_t)(H + kvh) * D + ic;
+    const float* vsrc = e.part + (size_t)b * width + (size_t)(H + KV + kvh) * D + ic;
+    float kpa[kQB], kpc[kQB], vpa[kQB], vpc[kQB];
+#pragma unroll
+    for (int u = 0; u < kQB; ++u) {
+      const size_t o = (size_t)min(u, e.nsplit - 1) * qplane;
+      kpa[u] = ksrc[o];
+      kpc[u] = ksrc[o + HALF];
+      vpa[u] = vsrc[o];
+      vpc[u] = vsrc[o + HALF];
+    }
+    const float kw1 = to_f32(((const T*)e.k_w)[ic]), kw2 = to_f32(((const T*)e.k_w)[ic + HALF]);
+    const uint64_t page = (uint64_t)e.pages[b], slot = (uint64_t)e.slots[b];
+    float ka = kpa[0], kc = kpc[0], va = vpa[0], vc = vpc[0];
+#pragma unroll
+    for (int u = 1; u < kQB; ++u) {
+      if (u < e.nsplit) {
+        ka = ka + kpa[u];
+        kc = kc + kpc[u];
+        va = va + vpa[u];
+        vc = vc + vpc[u];
+      }
+    }
+    for (int s2 = kQB; s2 < e.nsplit; ++s2) {
+      const size_t o = (size_t)s2 * qplane;
+      ka = ka + ksrc[o];
+      kc = kc + ksrc[o + HALF];
+      va = va + vsrc[o];
+      vc = vc + vsrc[o + HALF];
+    }
+    float k1[1] = {round_to<T>(ka)}, k2[1] = {round_to<T>(kc)};
+    const float w1[1] = {kw1}, w2[1] = {kw2}, fr[1] = {qfr};
+    norm_rope_pre<T, 1>(k1, k2, HALF, w1, w2, e.eps, epos, fr);
+    const float v1 = round_to<T>(va), v2 = round_to<T>(vc);
+    // a (page, slot) outside the pool is dropped rather than written
+    const bool in_pool = page < (uint64_t)num_blocks && slot < (uint64_t)P;
+    if (lane < HALF) {
+      kn[lane] = from_f32<T>(k1[0]);
+      kn[lane + HALF] = from_f32<T>(k2[0]);
+      vn[lane] = from_f32<T>(v1);
+      vn[lane + HALF] = from_f32<T>(v2);
+      if (in_pool) {
+        const size_t off = ((page * P + slot) * KV + kvh) * D;
+        T* kd = (T*)e.k_dst + off;
+        T* vd = (T*)e.v_dst + off;
+        kd[lane] = from_f32<T>(k1[0]);
+        kd[lane + HALF] = from_f32<T>(k2[0]);
+        vd[lane] = from_f32<T>(v1);
+        vd[lane + HALF] = from_f32<T>(v2);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
 
   float m = -INFINITY, l = 0.f;
   f32x4_t acc[DPL];
@@ -656,6 +809,26 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
 #pragma unroll
           for (int w = 0; w < VW; ++w) ((uint32_t*)dst)[w] = ch.kr[j][w];
       }
+      if constexpr (EPI) {
+        const int rho = L - 1 - t0;                // the new token's row, if in this chunk
+        if (owner && rho >= 0 && rho < CH) {
+          uint32_t w[VW];
+          __builtin_memcpy(w, kn + DPL * c, sizeof(w));
+          if (r == 0) {
+#pragma unroll
+            for (int i = 0; i < VW; ++i) ((uint32_t*)(kslab + rho * KPITCH + 2 * DPL * c))[i] = w[i];
+          }
+          __builtin_memcpy(w, vn + DPL * c, sizeof(w));
+          // lane (r, c) holds V rows 4 r + jj: a select per row (a branch or
+          // an indexed store would put the chunk in scratch)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const bool hit = 4 * r + jj == rho;
+#pragma unroll
+            for (int i = 0; i < VW; ++i) ch.v[jj][i] = hit ? w[i] : ch.v[jj][i];
+          }
+        }
+      }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
@@ -712,6 +885,10 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
     Chunk cs[DEPTH];
 #pragma unroll
     for (int i = 0; i < DEPTH; ++i) load_chunk(tstart + i * CH, cs[i]);
+    if constexpr (EPI) {
+      epi_q();
+      if (owner) epi_kv();
+    }
     bool more = true;
     for (int t0 = tstart; more; t0 += DEPTH * CH) {
 #pragma unroll
@@ -722,6 +899,10 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
           more = t0 + (i + 1) * CH < tend;
         }
       }
+    }
+  } else {
+    if constexpr (EPI) {
+      if (owner) epi_kv();                             // an empty sequence still stores k/v
     }
   }
   // l: each lane summed its own tokens; add the four lane rows of a head
@@ -900,7 +1081,7 @@ template <typename T, int D, int REP>
 int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* tables,
                 const int32_t* lens, void* out, float* ws_acc, float* ws_ml, int64_t B,
                 int64_t H, int64_t KV, int64_t P, int64_t num_blocks, int64_t table_stride, int64_t S, float scale,
-                hipStream_t st) {
+                hipStream_t st, const EpiArgs* epi) {
   dim3 grid((unsigned)S, (unsigned)KV, (unsigned)B);
   float* ws_m = ws_ml;
   float* ws_l = ws_ml ? ws_ml + B * H * S : nullptr;
@@ -911,18 +1092,21 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
     const int64_t pps = (table_stride + S - 1) / S;
     const bool page16 = P % 16 == 0;
     const bool one = pps <= kOneWavePages;
+    if (epi && !(one && page16)) return ACORN_ERR_UNSUPPORTED;
     const int nwv = one ? 1 : kAttnWaves;
-    const size_t lds = k3_slab_offset(nwv, REP, D, (int)pps) + (page16 ? k3_slab_bytes(nwv, D) : 0);
+    const size_t lds = k3_slab_offset(nwv, REP, D, (int)pps) +
+                       (page16 ? k3_slab_bytes(nwv, D) : 0) + (epi ? k3_epi_bytes(REP, D) : 0);
     if (lds > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
-    const int which = (one ? 2 : 0) + (page16 ? 1 : 0);
+    const int which = epi ? 4 : (one ? 2 : 0) + (page16 ? 1 : 0);
     using KFn = void (*)(const T*, const T*, const T*, const int32_t*, const int32_t*, T*, float*,
-                         float*, float*, int, int, int, int, int, int, float);
-    const KFn fns[4] = {paged_attn_mfma_kernel<T, D, REP, kAttnWaves, false>,
+                         float*, float*, int, int, int, int, int, int, float, EpiArgs);
+    const KFn fns[5] = {paged_attn_mfma_kernel<T, D, REP, kAttnWaves, false>,
                         paged_attn_mfma_kernel<T, D, REP, kAttnWaves, true>,
                         paged_attn_mfma_kernel<T, D, REP, 1, false, kOneWaveDepth>,
-                        paged_attn_mfma_kernel<T, D, REP, 1, true, kOneWaveDepth>};
+                        paged_attn_mfma_kernel<T, D, REP, 1, true, kOneWaveDepth>,
+                        paged_attn_mfma_kernel<T, D, REP, 1, true, kOneWaveDepth, true>};
     const KFn kfn = fns[which];
-    static bool lds_raised[4] = {false, false, false, false};
+    static bool lds_raised[5] = {false, false, false, false, false};
     if (!lds_raised[which] && lds > 64 * 1024) {
       (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 160 * 1024);
@@ -930,8 +1114,10 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
     }
     kfn<<<dim3((unsigned)KV, (unsigned)S, (unsigned)B), dim3(nwv * kWave), lds, st>>>(
         (const T*)q, (const T*)kp, (const T*)vp, tables, lens, (T*)out, ws_acc, ws_m, ws_l,
-        (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e);
+        (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e,
+        epi ? *epi : EpiArgs{});
   } else if constexpr (D >= 64) {
+    if (epi) return ACORN_ERR_UNSUPPORTED;
     constexpr int NWV = kAttnWaves;
     const int64_t ppw = (table_stride + S - 1) / S;  // most pages one workgroup can get
     const size_t lds = (size_t)(NWV * REP * D + 2 * NWV * REP) * 4 + (size_t)ppw * 4;
@@ -947,6 +1133,7 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
         (const T*)q, (const T*)kp, (const T*)vp, tables, lens, (T*)out, ws_acc, ws_m, ws_l,
         (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e);
   } else {
+    if (epi) return ACORN_ERR_UNSUPPORTED;
     paged_attn_split_kernel<T, D, REP><<<grid, dim3(kWave), 0, st>>>(
         (const T*)q, (const T*)kp, (const T*)vp, tables, lens, (T*)out, ws_acc, ws_m, ws_l,
         (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e);
@@ -964,12 +1151,12 @@ template <typename T, int D>
 int dispatch_rep(int64_t rep, const void* q, const void* kp, const void* vp,
                  const int32_t* tables, const int32_t* lens, void* out, float* ws_acc,
                  float* ws_ml, int64_t B, int64_t H, int64_t KV, int64_t P, int64_t num_blocks, int64_t ts,
-                 int64_t S, float scale, hipStream_t st) {
+                 int64_t S, float scale, hipStream_t st, const EpiArgs* epi) {
   switch (rep) {
-    case 1: return launch_attn<T, D, 1>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
-    case 2: return launch_attn<T, D, 2>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
-    case 4: return launch_attn<T, D, 4>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
-    case 8: return launch_attn<T, D, 8>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
+    case 1: return launch_attn<T, D, 1>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
+    case 2: return launch_attn<T, D, 2>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
+    case 4: return launch_attn<T, D, 4>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
+    case 8: return launch_attn<T, D, 8>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
   }
   return ACORN_ERR_UNSUPPORTED;
 }
@@ -978,12 +1165,12 @@ template <typename T>
 int dispatch_d(int64_t D, int64_t rep, const void* q, const void* kp, const void* vp,
                const int32_t* tables, const int32_t* lens, void* out, float* ws_acc,
                float* ws_ml, int64_t B, int64_t H, int64_t KV, int64_t P, int64_t num_blocks, int64_t ts,
-               int64_t S, float scale, hipStream_t st) {
+               int64_t S, float scale, hipStream_t st, const EpiArgs* epi = nullptr) {
   switch (D) {
-    case 16: return dispatch_rep<T, 16>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
-    case 32: return dispatch_rep<T, 32>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
-    case 64: return dispatch_rep<T, 64>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
-    case 128: return dispatch_rep<T, 128>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st);
+    case 16: return dispatch_rep<T, 16>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
+    case 32: return dispatch_rep<T, 32>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
+    case 64: return dispatch_rep<T, 64>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
+    case 128: return dispatch_rep<T, 128>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
   }
   return ACORN_ERR_UNSUPPORTED;
 }
@@ -1012,4 +1199,52 @@ extern "C" int acorn_paged_attention(const void* q, const void* k_pages, const v
     case ACORN_BF16: return dispatch_d<__bf16>(D, rep, q, k_pages, v_pages, tables, seq_lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, table_stride, num_splits, scale, st);
   }
   return ACORN_ERR_DTYPE;
+}
+
+extern "C" int acorn_paged_attention_qkv_supported(int64_t H, int64_t KV, int64_t D, int64_t P,
+                                                   int64_t table_stride, int64_t num_splits,
+                                                   int dtype, int wdtype) {
+  if (H <= 0 || KV <= 0 || H % KV != 0 || num_splits < 1 || table_stride < 1 || P <= 0) return 0;
+  const int64_t rep = H / KV;
+  if (!(dtype == ACORN_BF16 || dtype == ACORN_F16) || wdtype != dtype) return 0;
+  if (!(D == 64 || D == 128) || P % 16 != 0 || (P & (P - 1)) != 0) return 0;
+  if (!(rep == 1 || rep == 2 || rep == 4 || rep == 8)) return 0;
+  const int64_t pps = (table_stride + num_splits - 1) / num_splits;
+  return pps <= kOneWavePages ? 1 : 0;
+}
+
+extern "C" int acorn_paged_attention_qkv(const float* part, int64_t nsplit, void* k_pages,
+                                         void* v_pages, const int64_t* pages, const int64_t* slots,
+                                         const int32_t* tables, const int32_t* seq_lens, void* out,
+                                         float* ws_acc, float* ws_ml, int64_t B, int64_t H,
+                                         int64_t KV, int64_t D, int64_t P, int64_t num_blocks,
+                                         int64_t table_stride, int64_t num_splits, float scale,
+                                         const void* q_w, const void* k_w, float eps,
+                                         const int64_t* positions, const float* inv_freq,
+                                         int dtype, int wdtype, void* stream) {
+  if (B < 0 || H <= 0 || KV <= 0 || D <= 0 || P <= 0 || num_blocks <= 0 || num_splits < 1 ||
+      table_stride < 1 || nsplit < 1)
+    return ACORN_ERR_SHAPE;
+  if ((D & (D - 1)) != 0 || (P & (P - 1)) != 0 || H % KV != 0) return ACORN_ERR_SHAPE;
+  if (num_splits > 65535 || KV > 65535 || B > 65535 || nsplit > 0x7fffffff ||
+      num_blocks > 0x7fffffff)
+    return ACORN_ERR_SHAPE;
+  if (!acorn_paged_attention_qkv_supported(H, KV, D, P, table_stride, num_splits, dtype, wdtype))
+    return ACORN_ERR_UNSUPPORTED;
+  if (B == 0) return ACORN_OK;
+  if (!part || !k_pages || !v_pages || !pages || !slots || !tables || !seq_lens || !out || !q_w ||
+      !k_w || !positions || !inv_freq)
+    return ACORN_ERR_VALUE;
+  if (num_splits > 1 && (!ws_acc || !ws_ml)) return ACORN_ERR_VALUE;
+  const EpiArgs e{part, (int)nsplit, (int)B, q_w, k_w, eps, positions, inv_freq,
+                  pages, slots, k_pages, v_pages};
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t rep = H / KV;
+  if (dtype == ACORN_BF16)
+    return dispatch_d<__bf16>(D, rep, nullptr, k_pages, v_pages, tables, seq_lens, out, ws_acc,
+                              ws_ml, B, H, KV, P, num_blocks, table_stride, num_splits, scale, st,
+                              &e);
+  return dispatch_d<_Float16>(D, rep, nullptr, k_pages, v_pages, tables, seq_lens, out, ws_acc,
+                              ws_ml, B, H, KV, P, num_blocks, table_stride, num_splits, scale, st,
+                              &e);
 }

@@ -8,24 +8,13 @@
 // The per-head norm is models/qwen3.py:50-60: r((x * rsqrt(mean(x^2)+eps)) * w).
 // FMA contraction is disabled so every product is rounded as torch does.
 #include "common.h"
+#include "qkv_math.h"
 
 using namespace acorn;
 
 namespace {
 
 constexpr int kMaxPairs = 2;  // head_dim <= 256 -> half <= 128 -> 2 pairs per lane
-
-template <typename T>
-__device__ __forceinline__ void rope_pair(float& x1, float& x2, float pos, float inv_freq) {
-#pragma clang fp contract(off)
-  const float f = pos * inv_freq;
-  const float c = round_to<T>(cosf(f));
-  const float s = round_to<T>(sinf(f));
-  const float t1 = round_to<T>(x1 * c), t2 = round_to<T>(x2 * s);
-  const float t3 = round_to<T>(x2 * c), t4 = round_to<T>(x1 * s);
-  x1 = round_to<T>(t1 - t2);
-  x2 = round_to<T>(t3 + t4);
-}
 
 // One wavefront per row of head_dim values.
 template <typename T, bool POS64>
@@ -42,33 +31,6 @@ __global__ __launch_bounds__(kWave) void rope_kernel(T* __restrict__ x, int head
     rope_pair<T>(x1, x2, p, inv_freq[i]);
     base[i] = from_f32<T>(x1);
     base[i + half] = from_f32<T>(x2);
-  }
-}
-
-// Per-head RMSNorm over the lane's NP pairs (x1[j], x2[j]) followed by RoPE,
-// with the norm weights (w1 = w[i], w2 = w[i + half]) and the frequencies
-// already in registers.
-template <typename T, int NP>
-__device__ __forceinline__ void norm_rope_pre(float (&x1)[NP], float (&x2)[NP], int half,
-                                              const float (&w1)[NP], const float (&w2)[NP],
-                                              float eps, float pos, const float (&fr)[NP]) {
-#pragma clang fp contract(off)
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < NP; ++j) {
-    const int i = threadIdx.x + j * kWave;
-    if (i < half) ss += x1[j] * x1[j] + x2[j] * x2[j];
-  }
-  ss = wave_sum(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)(2 * half) + eps);
-#pragma unroll
-  for (int j = 0; j < NP; ++j) {
-    const int i = threadIdx.x + j * kWave;
-    if (i < half) {
-      x1[j] = round_to<T>((x1[j] * inv) * w1[j]);
-      x2[j] = round_to<T>((x2[j] * inv) * w2[j]);
-      rope_pair<T>(x1[j], x2[j], pos, fr[j]);
-    }
   }
 }
 

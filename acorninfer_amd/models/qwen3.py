@@ -358,6 +358,10 @@ class Qwen3DecodeModel:
 
         check(L.acorn_embedding(ptr(self.embed), ptr(buf.ids), ptr(buf.x), B, cfg.vocab_size, H,
                                 dt, st), "embedding")
+        # K3 runs the qkv epilogue itself where it supports the shape (one
+        # launch fewer per layer, the same bits)
+        fused_attn = bool(L.acorn_paged_attention_qkv_supported(
+            nq, nkv, D, page_size, buf.max_pages, buf.num_splits, dt, wdt))
         prev_ks = 0             # splits of the previous layer's down-projection partials
         for li, lw in enumerate(self.layers):
             # K1: input norm (layer 0 from the embedding; later layers reduce
@@ -374,15 +378,24 @@ class Qwen3DecodeModel:
             lw.qkv.launch(buf.normed, B, cq, part=buf.part_qkv, stream=st)
             kp = kbase + li * layer_elems * esz
             vp = vbase + li * layer_elems * esz
-            check(L.acorn_qkv_epilogue(
-                ptr(buf.part_qkv), cq.ksplit, ptr(buf.q), kp, vp, ptr(buf.pages), ptr(buf.slots),
-                B, nq, nkv, D, page_size, num_blocks, ptr(lw.q_norm), ptr(lw.k_norm), eps,
-                ptr(buf.positions), ptr(self.inv_freq), dt, wdt, st), "qkv_epilogue")
-            # K3
-            check(L.acorn_paged_attention(
-                ptr(buf.q), kp, vp, ptr(buf.tables), ptr(buf.lens), ptr(buf.attn),
-                ptr(buf.ws_acc), ptr(buf.ws_ml), B, nq, nkv, D, page_size, num_blocks,
-                buf.max_pages, buf.num_splits, float(self.scale), dt, st), "K3")
+            if fused_attn:
+                check(L.acorn_paged_attention_qkv(
+                    ptr(buf.part_qkv), cq.ksplit, kp, vp, ptr(buf.pages), ptr(buf.slots),
+                    ptr(buf.tables), ptr(buf.lens), ptr(buf.attn), ptr(buf.ws_acc),
+                    ptr(buf.ws_ml), B, nq, nkv, D, page_size, num_blocks, buf.max_pages,
+                    buf.num_splits, float(self.scale), ptr(lw.q_norm), ptr(lw.k_norm), eps,
+                    ptr(buf.positions), ptr(self.inv_freq), dt, wdt, st), "K3+epilogue")
+            else:
+                check(L.acorn_qkv_epilogue(
+                    ptr(buf.part_qkv), cq.ksplit, ptr(buf.q), kp, vp, ptr(buf.pages),
+                    ptr(buf.slots), B, nq, nkv, D, page_size, num_blocks, ptr(lw.q_norm),
+                    ptr(lw.k_norm), eps, ptr(buf.positions), ptr(self.inv_freq), dt, wdt, st),
+                    "qkv_epilogue")
+                # K3
+                check(L.acorn_paged_attention(
+                    ptr(buf.q), kp, vp, ptr(buf.tables), ptr(buf.lens), ptr(buf.attn),
+                    ptr(buf.ws_acc), ptr(buf.ws_ml), B, nq, nkv, D, page_size, num_blocks,
+                    buf.max_pages, buf.num_splits, float(self.scale), dt, st), "K3")
             # o projection -> K1 (reduce + residual add + post-attention norm)
             co = buf.cfgs["o"]
             lw.o.launch(buf.attn, B, co, part=buf.part_o, stream=st)

@@ -130,6 +130,38 @@ int acorn_paged_attention(const void* q, const void* k_pages, const void* v_page
                           int64_t num_splits, float scale, int dtype, void* stream);
 
 /*
+ * Decode-step fusion of acorn_qkv_epilogue with K3: the attention kernel
+ * reduces the qkv projection's partials for its own q heads (q is never
+ * written), and the workgroup holding each sequence's last split also
+ * computes that kv head's new k, v, stores them at (pages[b], slots[b]) as
+ * acorn_qkv_epilogue does, and attends to them. Arguments are those of the
+ * two entry points (tables/seq_lens/out/ws as in acorn_paged_attention,
+ * part..inv_freq as in acorn_qkv_epilogue, positions int64); the results are
+ * the same bits. No single reference function: qwen3.py:180-192, then
+ * cache/pager.py:87-113 (scatter_decode), then paged_attention.py:125-152.
+ * Returns ACORN_ERR_UNSUPPORTED, launching nothing, unless
+ * acorn_paged_attention_qkv_supported() holds for the shape.
+ */
+int acorn_paged_attention_qkv(const float* part, int64_t nsplit, void* k_pages, void* v_pages,
+                              const int64_t* pages, const int64_t* slots, const int32_t* tables,
+                              const int32_t* seq_lens, void* out, float* ws_acc, float* ws_ml,
+                              int64_t B, int64_t H, int64_t KV, int64_t D, int64_t P,
+                              int64_t num_blocks, int64_t table_stride, int64_t num_splits,
+                              float scale, const void* q_w, const void* k_w, float eps,
+                              const int64_t* positions, const float* inv_freq, int dtype,
+                              int wdtype, void* stream);
+
+/*
+ * 1 when acorn_paged_attention_qkv supports the shape: bf16 or fp16
+ * activations with norm weights of the same dtype, D in {64, 128}, H/KV in
+ * {1, 2, 4, 8}, pages of a multiple of 16 tokens and splits of at most 16
+ * pages (ceil(table_stride / num_splits)); else 0. No reference counterpart.
+ */
+int acorn_paged_attention_qkv_supported(int64_t H, int64_t KV, int64_t D, int64_t P,
+                                        int64_t table_stride, int64_t num_splits, int dtype,
+                                        int wdtype);
+
+/*
  * Weight-only quantised GEMM y[M,N] = x[M,K] @ dequant(W)[N,K]^T, bf16 in,
  * fp32 accumulate.
  * Replaces acorninfer/ops/quant_gemm.py:257-294 (quant_gemm, W8) and the W4
