@@ -588,6 +588,12 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   const float* qsrc = EPI ? e.part + (size_t)b * width + (size_t)kvh * REP * D + ic : nullptr;
   float qpa[EPI ? REP : 1][kQB], qpc[EPI ? REP : 1][kQB], qw1 = 0.f, qw2 = 0.f, qfr = 0.f;
   float epos = 0.f;
+  // ... and this kv head's k and v partials and k norm weights, for the wave
+  // that turns out to hold the new token (known only with the length)
+  float kpa[kQB], kpc[kQB], vpa[kQB], vpc[kQB], kw1 = 0.f, kw2 = 0.f;
+  int64_t epage = 0, eslot = 0;
+  const float* ksrc = EPI ? e.part + (size_t)b * width + (size_t)(H + kvh) * D + ic : nullptr;
+  const float* vsrc = EPI ? e.part + (size_t)b * width + (size_t)(H + KV + kvh) * D + ic : nullptr;
   u32x4_t qb[KB];
   if constexpr (EPI) {
 #pragma unroll
@@ -604,10 +610,25 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
     qfr = e.inv_freq[ic];
     epos = (float)e.pos[b];
 #pragma unroll
+    for (int u = 0; u < kQB; ++u) {
+      const size_t o = (size_t)min(u, e.nsplit - 1) * qplane;
+      kpa[u] = ksrc[o];
+      kpc[u] = ksrc[o + HALF];
+      vpa[u] = vsrc[o];
+      vpc[u] = vsrc[o + HALF];
+    }
+    kw1 = to_f32(((const T*)e.k_w)[ic]);
+    kw2 = to_f32(((const T*)e.k_w)[ic + HALF]);
+    epage = e.pages[b];
+    eslot = e.slots[b];
+#pragma unroll
     for (int h = 0; h < REP; ++h)
 #pragma unroll
       for (int u = 0; u < kQB; ++u) asm volatile("" ::"v"(qpa[h][u]), "v"(qpc[h][u]));
-    asm volatile("" ::"v"(qw1), "v"(qw2), "v"(qfr), "v"(epos));
+    asm volatile("" ::"v"(qw1), "v"(qw2), "v"(qfr), "v"(epos), "v"(kw1), "v"(kw2));
+#pragma unroll
+    for (int u = 0; u < kQB; ++u)
+      asm volatile("" ::"v"(kpa[u]), "v"(kpc[u]), "v"(vpa[u]), "v"(vpc[u]));
   } else {
 #pragma unroll
     for (int j = 0; j < KB; ++j)
@@ -639,10 +660,18 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   T* qs = (T*)((uint8_t*)smem + k3_slab_offset(NWV, REP, D, pps) + k3_slab_bytes(NWV, D));
   T* kn = qs + REP * D;
   T* vn = kn + D;
-  // EPI: the epilogue's arithmetic for each q head (split partials added in
-  // split order, rounded, per-head RMSNorm, RoPE; one pair per lane), run
-  // while the first chunks' loads are in flight
-  auto epi_q = [&]() {
+  // EPI, before any K/V load: the epilogue's arithmetic (split partials added
+  // in split order, rounded, per-head RMSNorm, RoPE; one pair per lane) for
+  // the REP q heads into LDS, then the B operand from there. The wave whose
+  // split holds the new token (the sequence's last split) also computes this
+  // kv head's k and v, stores them at (page, slot) as the epilogue does, and
+  // keeps them in LDS: the chunk loaded from the pool holds that row's old
+  // contents, so consume() patches it from there.
+  const bool owner = EPI && sp == nsb - 1;
+  if constexpr (EPI) {
+    float ecs[1], esn[1];
+    rope_cs<T>(epos, qfr, ecs[0], esn[0]);         // shared by the q heads and k
+    const float qw1a[1] = {qw1}, qw2a[1] = {qw2};
 #pragma unroll
     for (int h = 0; h < REP; ++h) {
       float a = qpa[h][0], cc = qpc[h][0];
@@ -659,11 +688,51 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
         cc = cc + pp[HALF];
       }
       float x1[1] = {round_to<T>(a)}, x2[1] = {round_to<T>(cc)};
-      const float w1[1] = {qw1}, w2[1] = {qw2}, fr[1] = {qfr};
-      norm_rope_pre<T, 1>(x1, x2, HALF, w1, w2, e.eps, epos, fr);
+      norm_rope_cs<T, 1>(x1, x2, HALF, qw1a, qw2a, e.eps, ecs, esn);
       if (lane < HALF) {
         qs[h * D + lane] = from_f32<T>(x1[0]);
         qs[h * D + lane + HALF] = from_f32<T>(x2[0]);
+      }
+    }
+    if (owner) {
+      float ka = kpa[0], kc = kpc[0], va = vpa[0], vc = vpc[0];
+#pragma unroll
+      for (int u = 1; u < kQB; ++u) {
+        if (u < e.nsplit) {
+          ka = ka + kpa[u];
+          kc = kc + kpc[u];
+          va = va + vpa[u];
+          vc = vc + vpc[u];
+        }
+      }
+      for (int s2 = kQB; s2 < e.nsplit; ++s2) {
+        const size_t o = (size_t)s2 * qplane;
+        ka = ka + ksrc[o];
+        kc = kc + ksrc[o + HALF];
+        va = va + vsrc[o];
+        vc = vc + vsrc[o + HALF];
+      }
+      float k1[1] = {round_to<T>(ka)}, k2[1] = {round_to<T>(kc)};
+      const float kw1a[1] = {kw1}, kw2a[1] = {kw2};
+      norm_rope_cs<T, 1>(k1, k2, HALF, kw1a, kw2a, e.eps, ecs, esn);
+      const float v1 = round_to<T>(va), v2 = round_to<T>(vc);
+      // a (page, slot) outside the pool is dropped rather than written
+      const uint64_t page = (uint64_t)epage, slot = (uint64_t)eslot;
+      const bool in_pool = page < (uint64_t)num_blocks && slot < (uint64_t)P;
+      if (lane < HALF) {
+        kn[lane] = from_f32<T>(k1[0]);
+        kn[lane + HALF] = from_f32<T>(k2[0]);
+        vn[lane] = from_f32<T>(v1);
+        vn[lane + HALF] = from_f32<T>(v2);
+        if (in_pool) {
+          const size_t off = ((page * P + slot) * KV + kvh) * D;
+          T* kd = (T*)e.k_dst + off;
+          T* vd = (T*)e.v_dst + off;
+          kd[lane] = from_f32<T>(k1[0]);
+          kd[lane + HALF] = from_f32<T>(k2[0]);
+          vd[lane] = from_f32<T>(v1);
+          vd[lane + HALF] = from_f32<T>(v2);
+        }
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -672,67 +741,7 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
 #pragma unroll
     for (int j = 0; j < KB; ++j)
       qb[j] = *(const u32x4_t*)(qs + min(c, REP - 1) * D + 32 * j + 8 * r);
-  };
-  // EPI: the wave whose split holds the new token (the sequence's last split)
-  // computes its k and v from the partials, stores them at (page, slot) as
-  // the epilogue does, and keeps them in LDS: the chunk loaded from the pool
-  // holds that row's old contents, so consume() patches it from there.
-  const bool owner = EPI && sp == nsb - 1;
-  auto epi_kv = [&]() {
-    const float* ksrc = e.part + (size_t)b * width + (size_t)(H + kvh) * D + ic;
-    const float* vsrc = e.part + (size_t)b * width + (size_t)(H + KV + kvh) * D + ic;
-    float kpa[kQB], kpc[kQB], vpa[kQB], vpc[kQB];
-#pragma unroll
-    for (int u = 0; u < kQB; ++u) {
-      const size_t o = (size_t)min(u, e.nsplit - 1) * qplane;
-      kpa[u] = ksrc[o];
-      kpc[u] = ksrc[o + HALF];
-      vpa[u] = vsrc[o];
-      vpc[u] = vsrc[o + HALF];
-    }
-    const float kw1 = to_f32(((const T*)e.k_w)[ic]), kw2 = to_f32(((const T*)e.k_w)[ic + HALF]);
-    const uint64_t page = (uint64_t)e.pages[b], slot = (uint64_t)e.slots[b];
-    float ka = kpa[0], kc = kpc[0], va = vpa[0], vc = vpc[0];
-#pragma unroll
-    for (int u = 1; u < kQB; ++u) {
-      if (u < e.nsplit) {
-        ka = ka + kpa[u];
-        kc = kc + kpc[u];
-        va = va + vpa[u];
-        vc = vc + vpc[u];
-      }
-    }
-    for (int s2 = kQB; s2 < e.nsplit; ++s2) {
-      const size_t o = (size_t)s2 * qplane;
-      ka = ka + ksrc[o];
-      kc = kc + ksrc[o + HALF];
-      va = va + vsrc[o];
-      vc = vc + vsrc[o + HALF];
-    }
-    float k1[1] = {round_to<T>(ka)}, k2[1] = {round_to<T>(kc)};
-    const float w1[1] = {kw1}, w2[1] = {kw2}, fr[1] = {qfr};
-    norm_rope_pre<T, 1>(k1, k2, HALF, w1, w2, e.eps, epos, fr);
-    const float v1 = round_to<T>(va), v2 = round_to<T>(vc);
-    // a (page, slot) outside the pool is dropped rather than written
-    const bool in_pool = page < (uint64_t)num_blocks && slot < (uint64_t)P;
-    if (lane < HALF) {
-      kn[lane] = from_f32<T>(k1[0]);
-      kn[lane + HALF] = from_f32<T>(k2[0]);
-      vn[lane] = from_f32<T>(v1);
-      vn[lane + HALF] = from_f32<T>(v2);
-      if (in_pool) {
-        const size_t off = ((page * P + slot) * KV + kvh) * D;
-        T* kd = (T*)e.k_dst + off;
-        T* vd = (T*)e.v_dst + off;
-        kd[lane] = from_f32<T>(k1[0]);
-        kd[lane + HALF] = from_f32<T>(k2[0]);
-        vd[lane] = from_f32<T>(v1);
-        vd[lane + HALF] = from_f32<T>(v2);
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  };
+  }
 
   float m = -INFINITY, l = 0.f;
   f32x4_t acc[DPL];
@@ -885,10 +894,6 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
     Chunk cs[DEPTH];
 #pragma unroll
     for (int i = 0; i < DEPTH; ++i) load_chunk(tstart + i * CH, cs[i]);
-    if constexpr (EPI) {
-      epi_q();
-      if (owner) epi_kv();
-    }
     bool more = true;
     for (int t0 = tstart; more; t0 += DEPTH * CH) {
 #pragma unroll
@@ -899,10 +904,6 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
           more = t0 + (i + 1) * CH < tend;
         }
       }
-    }
-  } else {
-    if constexpr (EPI) {
-      if (owner) epi_kv();                             // an empty sequence still stores k/v
     }
   }
   // l: each lane summed its own tokens; add the four lane rows of a head
