@@ -39,9 +39,10 @@ class _Bucket:
     bucket: int
     buf: StepBuffers
     graph: torch.cuda.CUDAGraph | None
-    pin_i64: list[torch.Tensor]       # ring of [4*bucket] int64: ids|positions|pages|slots
-    pin_i32: list[torch.Tensor]       # ring of [bucket*(1+W)] int32: lens|tables
-    pin_f32: list[torch.Tensor]       # ring of [4*bucket] f32: temperature|top_p|uniform|top_k
+    pin: list[torch.Tensor]           # ring of pinned byte mirrors of buf.meta
+    pin_i64: list[torch.Tensor]       # their int64 ids|positions|pages|slots
+    pin_i32: list[torch.Tensor]       # their int32 lens|tables
+    pin_f32: list[torch.Tensor]       # their f32 temperature|top_p|uniform|top_k
     done: list[torch.cuda.Event | None]
     turn: int = 0
     sampled: bool = False             # the device block holds sampling rows
@@ -77,30 +78,31 @@ class DecodeGraphRunner:
     def _build(self, bk: int) -> _Bucket:
         buf = self.model.buffers(bk, self.max_pages)
         W = self.max_pages
-        pin_i64, pin_i32, pin_f32 = [], [], []
+        e64, e32, ef = buf.meta_ends
+        pin, pin_i64, pin_i32, pin_f32 = [], [], [], []
         for _ in range(MIRRORS):
-            f = torch.zeros(4 * bk, dtype=torch.float32, pin_memory=True)
+            m = torch.zeros(ef, dtype=torch.uint8, pin_memory=True)
+            a, b, f = m[:e64].view(torch.int64), m[e64:e32].view(torch.int32), m[e32:].view(
+                torch.float32)
             f[bk:2 * bk] = 1.0                       # top_p off
-            pin_f32.append(f)
-            a = torch.zeros(4 * bk, dtype=torch.int64, pin_memory=True)
-            b = torch.zeros(bk * (1 + W), dtype=torch.int32, pin_memory=True)
             a[2 * bk:3 * bk] = self.scratch          # pages of padding rows
             b[0:bk] = 1                              # lens of padding rows
             b[bk:].view(bk, W)[:, 0] = self.scratch  # their table points at scratch
+            pin.append(m)
             pin_i64.append(a)
             pin_i32.append(b)
+            pin_f32.append(f)
         # device side starts from the same "all padding" state
-        buf.flat_i64[:4 * bk].copy_(pin_i64[0].to(self.device))
-        buf.flat_i32.copy_(pin_i32[0].to(self.device))
-        st = _Bucket(bk, buf, None, pin_i64, pin_i32, pin_f32, [None] * MIRRORS)
+        buf.meta.copy_(pin[0].to(self.device))
+        st = _Bucket(bk, buf, None, pin, pin_i64, pin_i32, pin_f32, [None] * MIRRORS)
         if self.capture:
             self._capture(st)
         return st
 
     def _body(self, st: _Bucket) -> None:
         c = self.cache
+        # the sampler writes the next ids over buf.ids (device-fed decode_loop)
         self.model.step(st.buf, c.k_pool, c.v_pool, c.num_blocks, c.page_size)
-        st.buf.ids.copy_(st.buf.next_ids)    # device-fed ids for decode_loop
 
     def _capture(self, st: _Bucket) -> None:
         s = torch.cuda.Stream(self.device)
@@ -150,13 +152,9 @@ class DecodeGraphRunner:
         tables[B:].zero_()
         tables[B:, 0] = self.scratch
         buf = st.buf
-        if ids is not None:
-            buf.flat_i64[:4 * bk].copy_(a, non_blocking=True)
-        else:
-            buf.meta_i64.copy_(a[bk:4 * bk], non_blocking=True)
-        buf.flat_i32.copy_(b, non_blocking=True)
         f = st.pin_f32[j]
-        if sampling is not None or st.sampled:
+        send_f32 = sampling is not None or st.sampled
+        if send_f32:
             f.zero_()
             f[bk:2 * bk] = 1.0
             st.sampled = False
@@ -170,7 +168,11 @@ class DecodeGraphRunner:
                     f[2 * bk + i] = u[i]
                     f[3 * bk:4 * bk].view(torch.int32)[i] = sp.top_k
                     st.sampled = True
-            buf.flat_f32.copy_(f, non_blocking=True)
+        # one copy: ids (when given) .. tables (.. the sampling block)
+        _, e32, ef = buf.meta_ends
+        lo = 0 if ids is not None else 8 * bk
+        hi = ef if send_f32 else e32
+        buf.meta[lo:hi].copy_(st.pin[j][lo:hi], non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(torch.cuda.current_stream(self.device))
         st.done[j] = ev

@@ -339,7 +339,8 @@ class Qwen3DecodeModel:
 
         Reads buf.ids/positions/pages/slots/lens/tables and the sampling
         block (temperature 0 = greedy); writes buf.logits (bf16 [B, vocab]),
-        buf.next_ids (int64 [B]), buf.logprob and buf.status. k_pool/v_pool
+        buf.next_ids (int64 [B], the same memory as buf.ids: the next step's
+        input), buf.logprob and buf.status. k_pool/v_pool
         are [layers, NB, P, KV, D]; layer l's new k/v go to
         (pages[b], slots[b]) before attention reads lens[b] tokens.
         """
@@ -631,21 +632,26 @@ class StepBuffers:
                 self.cfgs[name] = lin.swiglu_plan(B, tilings.get(name))[0]
             else:
                 self.cfgs[name] = lin.plan(B, tilings.get(name))[0]
-        # int64 block: ids | positions | pages | slots | next_ids ; int32 block: lens | tables
-        self.flat_i64 = torch.zeros(5 * B, dtype=torch.int64, device=dev)
-        self.flat_i32 = torch.zeros(B * (1 + self.max_pages), dtype=torch.int32, device=dev)
+        # The host-written inputs are one byte block, so a step needs one copy:
+        # int64 ids | positions | pages | slots, then int32 lens | tables, then
+        # the sampling block f32 temperature | top_p | uniform | top_k (int32
+        # bits; temperature 0 = greedy). `meta_ends` are the ends of the three
+        # parts in bytes. The sampler writes the next step's ids over `ids`.
+        e64 = 8 * 4 * B
+        e32 = e64 + 4 * B * (1 + self.max_pages)
+        self.meta_ends = (e64, e32, e32 + 4 * 4 * B)
+        self.meta = torch.zeros(self.meta_ends[2], dtype=torch.uint8, device=dev)
+        self.flat_i64 = self.meta[:e64].view(torch.int64)
+        self.flat_i32 = self.meta[e64:e32].view(torch.int32)
+        self.flat_f32 = self.meta[e32:].view(torch.float32)
         self.ids = self.flat_i64[0:B]
         self.positions = self.flat_i64[B:2 * B]
         self.pages = self.flat_i64[2 * B:3 * B]
         self.slots = self.flat_i64[3 * B:4 * B]
-        self.next_ids = self.flat_i64[4 * B:5 * B]
-        self.meta_i64 = self.flat_i64[B:4 * B]        # host-written: positions|pages|slots
+        self.next_ids = self.ids
         self.lens = self.flat_i32[0:B]
         self.tables = self.flat_i32[B:].view(B, self.max_pages)
         self.lens.fill_(1)
-        # sampling block: temperature | top_p | uniform | top_k (int32 bits);
-        # temperature 0 = greedy
-        self.flat_f32 = torch.zeros(4 * B, dtype=torch.float32, device=dev)
         self.temperature = self.flat_f32[0:B]
         self.top_p = self.flat_f32[B:2 * B]
         self.uniform = self.flat_f32[2 * B:3 * B]
