@@ -149,6 +149,14 @@ class PagedCacheView:
         c.v_pages[layer_idx][rows, slots] = v_new[0].permute(1, 0, 2).to(c.dtype)
         self._lens[layer_idx] = base + s
 
+    def reserve(self, n: int) -> list[tuple[int, int]]:
+        """Make room for n more tokens after layer 0's length; return each
+        one's (block id, slot) in position order. Like `write`, it allocates
+        before anything is written; lengths are not advanced."""
+        base, page = self.seq_len, self.cache.page_size
+        self._grow_to((base + n + page - 1) // page)
+        return [(self.table[p // page], p % page) for p in range(base, base + n)]
+
     def ensure_append_capacity(self, layer_idx: int) -> tuple[int, int]:
         """Make room for one more token at layer `layer_idx`; return its
         (block id, slot). Allocates only when the append position starts a page."""

@@ -334,8 +334,15 @@ class Qwen3DecodeModel:
                            tilings if tilings is not None else self.tilings.get(batch))
 
     def step(self, buf: "StepBuffers", k_pool: torch.Tensor, v_pool: torch.Tensor,
-             num_blocks: int, page_size: int) -> None:
+             num_blocks: int, page_size: int, *, fused_attn: bool = True,
+             head_rows: torch.Tensor | None = None) -> torch.Tensor | None:
         """Launch one decode step on the current stream.
+
+        fused_attn=False keeps the qkv epilogue (which writes every row's new
+        k/v) and K3 as two launches; rows that attend to each other's new
+        tokens (prefill rows of one sequence) need that order. head_rows:
+        int64 row indices; only their logits are computed, [len, vocab] in
+        the activation dtype, returned instead of sampling.
 
         Reads buf.ids/positions/pages/slots/lens/tables and the sampling
         block (temperature 0 = greedy); writes buf.logits (bf16 [B, vocab]),
@@ -361,7 +368,7 @@ class Qwen3DecodeModel:
                                 dt, st), "embedding")
         # K3 runs the qkv epilogue itself where it supports the shape (one
         # launch fewer per layer, the same bits)
-        fused_attn = bool(L.acorn_paged_attention_qkv_supported(
+        fused_attn = fused_attn and bool(L.acorn_paged_attention_qkv_supported(
             nq, nkv, D, page_size, buf.max_pages, buf.num_splits, dt, wdt))
         prev_ks = 0             # splits of the previous layer's down-projection partials
         for li, lw in enumerate(self.layers):
@@ -418,6 +425,16 @@ class Qwen3DecodeModel:
         check(L.acorn_fused_add_rmsnorm_partials(
             ptr(buf.part_down), prev_ks, ptr(buf.res), ptr(buf.res), ptr(self.norm),
             ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
+        if head_rows is not None:
+            n = int(head_rows.numel())
+            hx = buf.normed.index_select(0, head_rows)
+            ch, _ = self.lm_head.plan(n)
+            out = torch.empty(n, cfg.vocab_size, dtype=buf.logits.dtype, device=self.device)
+            ws = (torch.empty(ch.ksplit, n, cfg.vocab_size, dtype=torch.float32,
+                              device=self.device)
+                  if ch.ksplit > 1 and self.lm_head.fmt != _lib.WFMT_F32 else None)
+            self.lm_head.launch(hx, n, ch, out=out, part=ws, stream=st)
+            return out
         self.lm_head.launch(buf.normed, B, buf.cfgs["lm_head"], out=buf.logits,
                             part=buf.ws_lm, stream=st)
         # next token: greedy rows (temperature 0) take the argmax, the others
@@ -426,6 +443,7 @@ class Qwen3DecodeModel:
                              ptr(buf.temperature), ptr(buf.top_k), ptr(buf.top_p),
                              ptr(buf.uniform), ptr(buf.next_ids), ptr(buf.logprob), None,
                              ptr(buf.status), st), "sample")
+        return None
 
     def fused_swiglu(self, batch: int) -> bool:
         """The gate|up launch carries the SwiGLU epilogue (decode sizes, and
@@ -576,6 +594,80 @@ class Qwen3DecodeModel:
             for li in range(self.cfg.num_hidden_layers):
                 v._lens[li] = v._lens.get(li, 0) + 1
         return buf.logits.float()
+
+    def forward_prefill_batch(self, input_ids: torch.Tensor, views, *,
+                              real_lens) -> torch.Tensor:
+        """Batched prefill (qwen3.py:597-639): input_ids [N, Lmax] (right
+        padded; pad values unused) + real_lens[i] -> fp32 logits [N, vocab]
+        of each row's last real token. Every view starts empty; its KV gets
+        the row's real_lens[i] tokens."""
+        N, Lmax = input_ids.shape
+        if len(views) != N or len(real_lens) != N:
+            raise ValueError(f"views/real_lens must match the batch: N={N}, "
+                             f"len(views)={len(views)}, len(real_lens)={len(real_lens)}")
+        if min(real_lens) < 1 or max(real_lens) > Lmax:
+            raise ValueError(f"real_lens must lie in [1, Lmax]: min={min(real_lens)}, "
+                             f"max={max(real_lens)}, Lmax={Lmax}")
+        if any(v.seq_len != 0 for v in views):
+            raise ValueError("forward_prefill_batch: every view must start empty "
+                             "(forward_extend continues a sequence)")
+        return self.forward_extend(input_ids, views, starts=[0] * N, chunk_lens=list(real_lens))
+
+    def forward_extend(self, input_ids: torch.Tensor, views, *, starts: list[int],
+                       chunk_lens: list[int]) -> torch.Tensor:
+        """Chunked prefill (qwen3.py:641-686): input_ids [N, Lc_max] (right
+        padded) + starts[i] (= views[i]'s KV length) + chunk_lens[i] -> fp32
+        logits [N, vocab] at each row's position start + len - 1.
+
+        The rows of all chunks are packed into one launch sequence of the
+        decode step, one row per token: token p of a sequence is a row with
+        position p, KV target (table[p // P], p % P) and length p + 1, so K3
+        gives it causal attention over the cache. The qkv epilogue writes
+        every row's k/v before K3 runs (fused_attn=False), which is what lets
+        a row read the tokens of the same chunk before it. GEMMs run at
+        M = total rows; lm_head only for each chunk's last row."""
+        N, Lc = input_ids.shape
+        if len(views) != N or len(starts) != N or len(chunk_lens) != N:
+            raise ValueError(f"views/starts/chunk_lens must match the batch: N={N}, "
+                             f"len(views)={len(views)}, len(starts)={len(starts)}, "
+                             f"len(chunk_lens)={len(chunk_lens)}")
+        if min(chunk_lens) < 1 or max(chunk_lens) > Lc or min(starts) < 0:
+            raise ValueError(f"chunk_lens must lie in [1, Lc_max] and starts be >= 0: "
+                             f"min(len)={min(chunk_lens)}, max(len)={max(chunk_lens)}, "
+                             f"Lc_max={Lc}, min(start)={min(starts)}")
+        for v, s in zip(views, starts):
+            if v.seq_len != s:
+                raise ValueError(f"forward_extend: view KV length {v.seq_len} != start {s}")
+        cache = views[0].cache
+        P = cache.page_size
+        targets = [v.reserve(n) for v, n in zip(views, chunk_lens)]
+        W = max(len(v.table) for v in views)
+        ids, pos, pages, slots, lens, tabs = [], [], [], [], [], []
+        for i, (v, s, n) in enumerate(zip(views, starts, chunk_lens)):
+            ids.append(input_ids[i, :n].to(torch.int64))
+            pos += list(range(s, s + n))
+            pages += [p for p, _ in targets[i]]
+            slots += [q for _, q in targets[i]]
+            lens += list(range(s + 1, s + n + 1))
+            row = torch.zeros(W, dtype=torch.int32)
+            row[:len(v.table)] = torch.tensor(v.table, dtype=torch.int32)
+            tabs.append(row.expand(n, W))
+        R = len(pos)
+        buf = self.buffers(R, W)
+        dev = self.device
+        buf.ids.copy_(torch.cat(ids).to(dev))
+        buf.positions.copy_(torch.tensor(pos, dtype=torch.int64))
+        buf.pages.copy_(torch.tensor(pages, dtype=torch.int64))
+        buf.slots.copy_(torch.tensor(slots, dtype=torch.int64))
+        buf.lens.copy_(torch.tensor(lens, dtype=torch.int32))
+        buf.tables.copy_(torch.cat(tabs))
+        last = torch.tensor(chunk_lens, dtype=torch.int64).cumsum(0) - 1
+        out = self.step(buf, cache.k_pool, cache.v_pool, cache.num_blocks, P,
+                        fused_attn=False, head_rows=last.to(dev))
+        for v, n in zip(views, chunk_lens):
+            for li in range(self.cfg.num_hidden_layers):
+                v._lens[li] = v._lens.get(li, 0) + n
+        return out.float()
 
 
 def _dense_linear(w: torch.Tensor, dtype: torch.dtype) -> QLinear:

@@ -1,0 +1,128 @@
+"""Prefill and chunked prefill (forward_prefill_batch, forward_extend;
+acorninfer/models/qwen3.py:597-686) on the decode kernels, one row per token,
+against the CPU oracle of the reference's SDPA path (oracle/qwen3_ref.py:
+a whole-prompt forward, pinned against HF Qwen3) and against the GPU's own
+token-by-token decode of the same prompt.
+
+- fp32: the last prompt position's logits equal the oracle's within fp32
+  reduction drift, and greedy decoding continued on the prefilled cache gives
+  the oracle's ids; the KV pages equal those of the token-by-token path.
+- bf16: a ragged batch of three prompts, each row's last logits within the
+  decode tests' norm-relative tolerance of the oracle's (argmax equal where
+  the top-2 margin is at least 0.05); two chunks through forward_extend equal
+  the one-shot prefill.
+"""
+import pytest
+import torch
+
+from acorninfer_amd.cache.pager import PagedCacheView
+from acorninfer_amd.config import Qwen3Config
+from acorninfer_amd.models.qwen3 import Qwen3DecodeModel, random_state_dict
+from model_utils import feed_prompt, new_cache, release
+from oracle.qwen3_ref import Qwen3Ref, generate_greedy
+
+SEED = 20261101
+MARGIN = 0.05
+
+
+def _ids(n, vocab, seed):
+    return torch.randint(0, vocab, (n,), generator=torch.Generator().manual_seed(seed)).tolist()
+
+
+def _padded(prompts, device):
+    L = max(len(p) for p in prompts)
+    x = torch.zeros(len(prompts), L, dtype=torch.int64)
+    for i, p in enumerate(prompts):
+        x[i, :len(p)] = torch.tensor(p)
+    return x.to(device)
+
+
+def _rel(a, b):
+    return ((a.double() - b.double()).norm() / b.double().norm()).item()
+
+
+@pytest.mark.gpu
+def test_prefill_fp32_matches_oracle_and_decode_continues():
+    cfg = Qwen3Config.qwen3_0_6b().with_layers(4)
+    sd = random_state_dict(cfg, seed=SEED, std=0.02, dtype=torch.float32)
+    prompt = _ids(37, cfg.vocab_size, SEED + 1)       # 2 pages and a 5-token tail
+    ref = Qwen3Ref(cfg, sd, torch.float32)
+    want_ids, want_logits = generate_greedy(ref, prompt, 12)
+    model = Qwen3DecodeModel.from_state_dict(cfg, sd, dtype=torch.float32, device="cuda")
+    print("\n[fp32 prefill: 4 layers, prompt 37, 12 new]", flush=True)
+    alloc, cache = new_cache(model, 12)
+    view = PagedCacheView(cache)
+    logits = model.forward_prefill_batch(_padded([prompt], model.device), [view],
+                                         real_lens=[len(prompt)])[0]
+    assert view.seq_len == len(prompt)
+    got = []
+    for t in range(12):
+        torch.testing.assert_close(logits.cpu(), want_logits[t], rtol=1e-3, atol=1e-3)
+        got.append(int(logits.argmax()))
+        logits = model.forward_decode(torch.tensor([[got[-1]]], device=model.device), [view])[0]
+    assert got == want_ids
+    # the KV pages equal the token-by-token path's
+    alloc2, cache2 = new_cache(model, 12)
+    view2 = PagedCacheView(cache2)
+    feed_prompt(model, view2, prompt)
+    n = len(prompt)
+    for li in range(cfg.num_hidden_layers):
+        for pages, pages2 in ((cache.k_pages, cache2.k_pages), (cache.v_pages, cache2.v_pages)):
+            a = pages[li][torch.tensor(view.table)].reshape(-1, *pages[li].shape[2:])[:n]
+            b = pages2[li][torch.tensor(view2.table)].reshape(-1, *pages2[li].shape[2:])[:n]
+            torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-5)
+    release(alloc, [view])
+    release(alloc2, [view2])
+    alloc.assert_balanced()
+
+
+@pytest.mark.gpu
+def test_prefill_batch_ragged_bf16_matches_oracle():
+    cfg = Qwen3Config.qwen3_0_6b().with_layers(4)
+    sd = random_state_dict(cfg, seed=SEED + 2, std=0.02, dtype=torch.bfloat16)
+    prompts = [_ids(n, cfg.vocab_size, SEED + 10 + n) for n in (5, 33, 17)]
+    ref = Qwen3Ref(cfg, sd, torch.bfloat16)
+    model = Qwen3DecodeModel.from_state_dict(cfg, sd, weight_format="bf16", device="cuda")
+    alloc, cache = new_cache(model, 16)
+    views = [PagedCacheView(cache) for _ in prompts]
+    got = model.forward_prefill_batch(_padded(prompts, model.device), views,
+                                      real_lens=[len(p) for p in prompts]).cpu()
+    for i, p in enumerate(prompts):
+        want = ref.forward(torch.tensor([p]), num_logits_to_keep=1)[0, -1]
+        rel = _rel(got[i], want)
+        top2 = want.topk(2).values
+        print(f"\n[bf16 prefill row {i} (len {len(p)}): rel err {rel:.3g}]", flush=True)
+        assert rel < 3e-2
+        if (top2[0] - top2[1]).item() >= MARGIN:
+            assert int(got[i].argmax()) == int(want.argmax())
+        assert views[i].seq_len == len(p)
+    release(alloc, views)
+    alloc.assert_balanced()
+
+
+@pytest.mark.gpu
+def test_extend_in_chunks_equals_one_shot_bf16():
+    cfg = Qwen3Config.qwen3_0_6b().with_layers(4)
+    sd = random_state_dict(cfg, seed=SEED + 3, std=0.02, dtype=torch.bfloat16)
+    model = Qwen3DecodeModel.from_state_dict(cfg, sd, weight_format="bf16", device="cuda")
+    prompt = _ids(41, cfg.vocab_size, SEED + 4)
+    alloc, cache = new_cache(model, 16)
+    one, two = PagedCacheView(cache), PagedCacheView(cache)
+    whole = model.forward_prefill_batch(_padded([prompt], model.device), [one],
+                                        real_lens=[41])[0].cpu()
+    model.forward_prefill_batch(_padded([prompt[:20]], model.device), [two], real_lens=[20])
+    part = model.forward_extend(_padded([prompt[20:]], model.device), [two], starts=[20],
+                                chunk_lens=[21])[0].cpu()
+    assert two.seq_len == 41
+    assert _rel(part, whole) < 3e-2
+    for li in range(cfg.num_hidden_layers):
+        a = cache.k_pages[li][torch.tensor(one.table)].reshape(-1, cfg.num_key_value_heads,
+                                                              cfg.head_dim)[:41].float()
+        b = cache.k_pages[li][torch.tensor(two.table)].reshape(-1, cfg.num_key_value_heads,
+                                                              cfg.head_dim)[:41].float()
+        assert _rel(b, a) < 3e-2
+    with pytest.raises(ValueError):
+        model.forward_extend(_padded([prompt[:4]], model.device), [two], starts=[40],
+                             chunk_lens=[4])
+    release(alloc, [one, two])
+    alloc.assert_balanced()
