@@ -653,7 +653,13 @@ class Qwen3DecodeModel:
             row[:len(v.table)] = torch.tensor(v.table, dtype=torch.int32)
             tabs.append(row.expand(n, W))
         R = len(pos)
-        buf = self.buffers(R, W)
+        # the step buffers of the last shape are kept (a prompt batch often repeats it)
+        key = (R, W)
+        cached = getattr(self, "_extend_buf", None)
+        if cached is None or cached[0] != key:
+            self._extend_buf = None
+            self._extend_buf = (key, self.buffers(R, W))
+        buf = self._extend_buf[1]
         dev = self.device
         buf.ids.copy_(torch.cat(ids).to(dev))
         buf.positions.copy_(torch.tensor(pos, dtype=torch.int64))

@@ -16,6 +16,9 @@ The JSON line also carries:
   events on its own stream: a hipGraph of one step's GEMM launches (36 x
   {qkv, o, gate|up, down} + lm_head, the step's own weights and buffers) is
   replayed and timed; achieved = algorithmic bytes of those launches / time.
+- extra (unless --no-extra): other batch sizes and formats, and the batched
+  prefill (forward_prefill_batch) of C prompts of L random ids: ms per call
+  and prompt tokens per second.
 - cpu_baseline: the CPU oracle of the reference's path (oracle/qwen3_ref.py,
   fp32 torch on the host cores) on a bounded sample of the same workload
   (C sequences at context L, a few decode steps of a few layers plus the
@@ -115,6 +118,37 @@ def time_decode(runner, views, first, steps: int, warmup: int, sampling=None):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     return dt, log
+
+
+def prefill_benchmark(model, cfg, batch: int, prompt_len: int, seed: int, reps: int = 3):
+    """Batched prefill (forward_prefill_batch) of `batch` prompts of
+    `prompt_len` random ids into a fresh cache: ms per call (wall clock around
+    synchronised calls, after one warm-up call) and prompt tok/s."""
+    import torch
+
+    from acorninfer_amd.cache.pager import BlockAllocator, PagedCacheView, PagedKVCache
+
+    P = 16
+    per = -(-prompt_len // P)
+    alloc = BlockAllocator(batch * per + 1)
+    cache = PagedKVCache(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim, P, alloc,
+                         "cuda", model.dtype)
+    ids = torch.randint(0, cfg.vocab_size, (batch, prompt_len),
+                        generator=torch.Generator().manual_seed(seed)).cuda()
+    times = []
+    for r in range(reps + 1):
+        views = [PagedCacheView(cache) for _ in range(batch)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.forward_prefill_batch(ids, views, real_lens=[prompt_len] * batch)
+        torch.cuda.synchronize()
+        if r:
+            times.append(time.perf_counter() - t0)
+        for v in views:
+            for blk in v.table:
+                alloc.free(blk)
+    ms = 1e3 * sorted(times)[len(times) // 2]
+    return ms, batch * prompt_len / ms * 1e3
 
 
 def gemm_roofline(model, runner, batch: int, reps: int = 5):
@@ -430,6 +464,12 @@ def main() -> None:
                            "GBps": round(v["bytes"] / v["us"] / 1e3, 1)}
                        for k, v in model.tune_report.items()}}
     if not args.no_extra:
+        # configuration 4's prompts: prefill of C x 512 random ids (TTFT of a batch)
+        for c in (1, args.batch):
+            ms_p, tps = prefill_benchmark(model, cfg, c, args.prompt_len, args.seed + 7)
+            extra[f"bf16_prefill_C{c}_ms"] = round(ms_p, 3)
+            extra[f"bf16_prefill_C{c}_tok_s"] = round(tps, 1)
+            _log(f"bf16 prefill C={c} x {args.prompt_len}: {ms_p:.2f} ms ({tps:.0f} tok/s)")
         del model, cache, runner
         torch.cuda.empty_cache()
         for fmt, c in (("bf16", 1), ("w4a16", 8), ("w4a16", 1)):
