@@ -151,6 +151,46 @@ def prefill_benchmark(model, cfg, batch: int, prompt_len: int, seed: int, reps: 
     return ms, batch * prompt_len / ms * 1e3
 
 
+def engine_benchmark(model, cfg, concurrency: int, prompt_len: int, new_tokens: int,
+                     seed: int):
+    """Configuration 4 end to end: `concurrency` greedy requests of
+    `prompt_len` random ids and `new_tokens` generated tokens each, submitted
+    at once to the Engine (continuous batching: batched prefill, then the
+    graph-captured decode step). Returns (generated tok/s over the wall time
+    of the whole run, mean time to first token in ms)."""
+    import torch
+
+    from acorninfer_amd.engine.engine import Engine
+    from acorninfer_amd.sampler import SamplingParams
+
+    P = 16
+    blocks = concurrency * -(-(prompt_len + new_tokens + 1) // P) + 8
+    eng = Engine(model, num_blocks=blocks, max_running=concurrency, watermark_blocks=1,
+                 max_model_len=prompt_len + new_tokens + 1, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    greedy = SamplingParams(temperature=0.0)
+    never = frozenset({-1})
+
+    def run(n_new):
+        ids = [eng.submit(torch.randint(0, cfg.vocab_size, (prompt_len,), generator=g).tolist(),
+                          greedy, max_tokens=n_new, eos_ids=never) for _ in range(concurrency)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while eng.has_pending():
+            eng.step()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        ttft = [1e3 * (eng.seqs[i].first_token_at - t0) for i in ids]
+        for i in ids:
+            eng.drop(i)
+        return dt, sum(ttft) / len(ttft)
+
+    run(4)                                    # warm-up: captures the decode graph
+    dt, ttft = run(new_tokens)
+    eng.assert_balanced()
+    return concurrency * new_tokens / dt, ttft
+
+
 def gemm_roofline(model, runner, batch: int, reps: int = 5):
     """Time one step's GEMM launches (hipGraph on a private stream, HIP events
     on that stream). Returns (achieved GB/s, per-step bytes, per-step µs,
@@ -470,7 +510,15 @@ def main() -> None:
             extra[f"bf16_prefill_C{c}_ms"] = round(ms_p, 3)
             extra[f"bf16_prefill_C{c}_tok_s"] = round(tps, 1)
             _log(f"bf16 prefill C={c} x {args.prompt_len}: {ms_p:.2f} ms ({tps:.0f} tok/s)")
-        del model, cache, runner
+        # configuration 4 end to end through the Engine (prefill + decode)
+        del cache, runner
+        torch.cuda.empty_cache()
+        e2e, ttft = engine_benchmark(model, cfg, args.batch, args.prompt_len, 256, args.seed + 9)
+        extra[f"bf16_engine_C{args.batch}_tok_s"] = round(e2e, 1)
+        extra[f"bf16_engine_C{args.batch}_ttft_ms"] = round(ttft, 2)
+        _log(f"bf16 engine C={args.batch}, {args.prompt_len} + 256 tokens: {e2e:.1f} tok/s "
+             f"end to end, TTFT {ttft:.1f} ms")
+        del model
         torch.cuda.empty_cache()
         for fmt, c in (("bf16", 1), ("w4a16", 8), ("w4a16", 1)):
             m2, c2, r2, v2, f2 = build_workload(cfg, fmt, c, args.prompt_len, total, args.seed,
