@@ -925,13 +925,17 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
           __builtin_memcpy(out + orow * D + DPL * (4 * r + i), w, sizeof(w));
         }
       } else {
+        // the split's normalised output acc / l in fp16 (|acc / l| <= max |v|),
+        // half the bytes of fp32 partials to write here and read in the combine
         const size_t slot = orow * S + sp;
+        const float inv = 1.0f / l;
+        _Float16* wp = (_Float16*)ws_acc + slot * D;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float f[DPL];
+          _Float16 f[DPL];
 #pragma unroll
-          for (int j = 0; j < DPL; ++j) f[j] = acc[j][i];
-          __builtin_memcpy(ws_acc + slot * D + DPL * (4 * r + i), f, sizeof(f));
+          for (int j = 0; j < DPL; ++j) f[j] = (_Float16)(acc[j][i] * inv);
+          __builtin_memcpy(wp + DPL * (4 * r + i), f, sizeof(f));
         }
         if (r == 0) {
           ws_m[slot] = m;
@@ -972,7 +976,7 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
       out[orow * D + d] = from_f32<T>(num / den);
     } else {
       const size_t slot = orow * S + sp;
-      ws_acc[slot * D + d] = num;
+      ((_Float16*)ws_acc)[slot * D + d] = (_Float16)(num / den);  // normalised, as above
       if (d == 0) {
         ws_m[slot] = M;
         ws_l[slot] = den;
@@ -994,7 +998,9 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
 // in a fixed order.
 constexpr int kCombineWaves = 4;
 
-template <typename T, int D>
+// NORM: the MFMA kernel's partials, each split's normalised output acc / l in
+// fp16 (weight w_s l_s); else fp32 unnormalised acc (weight w_s).
+template <typename T, int D, bool NORM>
 __global__ __launch_bounds__(kCombineWaves * kWave) void paged_attn_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
     const float* __restrict__ ws_l, T* __restrict__ out, const int32_t* __restrict__ lens,
@@ -1008,6 +1014,7 @@ __global__ __launch_bounds__(kCombineWaves * kWave) void paged_attn_combine_kern
   const float* m = ws_m + row * S;
   const float* l = ws_l + row * S;
   const float* src = ws_acc + row * S * D;
+  const _Float16* srch = (const _Float16*)ws_acc + row * S * D;
   const int pps = (table_stride + S - 1) / S;
   float a[DL];
 #pragma unroll
@@ -1031,7 +1038,10 @@ __global__ __launch_bounds__(kCombineWaves * kWave) void paged_attn_combine_kern
     for (int k = 0; k < SPW; ++k) {
       const int s = min(s0 + wid + kCombineWaves * k, S - 1);
 #pragma unroll
-      for (int i = 0; i < DL; ++i) x[k][i] = src[(size_t)s * D + min(d0 + i, D - 1)];
+      for (int i = 0; i < DL; ++i) {
+        const size_t e = (size_t)s * D + min(d0 + i, D - 1);
+        x[k][i] = NORM ? (float)srch[e] : src[e];
+      }
     }
     // The empty asm pins the requests (with the length above) ahead of the
     // early exit; otherwise they sink below it and cost a second round trip.
@@ -1058,7 +1068,7 @@ __global__ __launch_bounds__(kCombineWaves * kWave) void paged_attn_combine_kern
 #pragma unroll
     for (int k = 0; k < SPW; ++k) {
       const int s = s0 + wid + kCombineWaves * k;
-      const float w = __shfl(wl, wid + kCombineWaves * k);
+      const float w = __shfl(NORM ? wl * ll : wl, wid + kCombineWaves * k);
       if (s < nsb) {
 #pragma unroll
         for (int i = 0; i < DL; ++i) a[i] += w * x[k][i];
@@ -1141,7 +1151,9 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
   }
   ACORN_LAUNCH_CHECK();
   if (S > 1) {
-    paged_attn_combine_kernel<T, D><<<dim3((unsigned)(B * H)), dim3(kCombineWaves * kWave), 0, st>>>(
+    // the MFMA kernel (bf16 / fp16, D >= 64) writes normalised fp16 partials
+    constexpr bool kNorm = D >= 64 && !std::is_same<T, float>::value;
+    paged_attn_combine_kernel<T, D, kNorm><<<dim3((unsigned)(B * H)), dim3(kCombineWaves * kWave), 0, st>>>(
         ws_acc, ws_m, ws_l, (T*)out, lens, (int)H, (int)P, (int)table_stride, (int)S);
     ACORN_LAUNCH_CHECK();
   }

@@ -121,7 +121,8 @@ int acorn_qkv_epilogue(const float* part, int64_t nsplit, void* q_out, void* k_p
  * out: [B, H, D]. Token t of sequence b lives at (tables[b, t/P], t%P);
  * q head h reads kv head h / (H/KV). One workgroup serves all H/KV q heads of
  * a kv head (GQA reuse). Workspace: ws_acc [B*H*num_splits*D] fp32 and
- * ws_ml [2*B*H*num_splits] fp32, caller-owned.
+ * ws_ml [2*B*H*num_splits] fp32, caller-owned (bf16/fp16 activations with
+ * D >= 64 keep each split's normalised output there in fp16, using half of it).
  */
 int acorn_paged_attention(const void* q, const void* k_pages, const void* v_pages,
                           const int32_t* tables, const int32_t* seq_lens, void* out,
