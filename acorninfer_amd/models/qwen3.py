@@ -701,11 +701,12 @@ def _dense_linear(w: torch.Tensor, dtype: torch.dtype) -> QLinear:
 
 
 UNIT_PAGES = 4      # K3 split size the heuristic aims for (pages)
+SMALL_GRID_PAGES = 1024   # below this many (sequence, kv head, page) units: 1-page splits
 MAX_SPLITS = 64     # bound on K3 splits per (sequence, kv head)
 
 
 def attention_splits(batch: int, kv_heads: int, max_pages: int, *,
-                     unit_pages: int = UNIT_PAGES, max_splits: int = MAX_SPLITS) -> int:
+                     unit_pages: int | None = None, max_splits: int = MAX_SPLITS) -> int:
     """K3 split count S for block tables `max_pages` wide.
 
     K3 gives every split the same pps = ceil(max_pages / S) pages, so a
@@ -715,8 +716,11 @@ def attention_splits(batch: int, kv_heads: int, max_pages: int, *,
     the CUs, whatever the mix of context lengths. S is capped at `max_splits`
     (workspace B*H*S*(D+2) floats; K3 writes and the combine reads one
     partial per used split), so very wide tables get proportionally larger
-    splits."""
-    del batch, kv_heads  # the unit size, not the grid, sets the balance
+    splits. A small grid (batch * kv_heads * max_pages below
+    SMALL_GRID_PAGES, e.g. one sequence) uses 1-page splits instead, so that
+    its few waves each wait for one chunk rather than walk four."""
+    if unit_pages is None:
+        unit_pages = 1 if batch * kv_heads * max_pages < SMALL_GRID_PAGES else UNIT_PAGES
     return max(1, min(-(-max_pages // unit_pages), max_splits))
 
 
