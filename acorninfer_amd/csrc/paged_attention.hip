@@ -660,89 +660,7 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   T* qs = (T*)((uint8_t*)smem + k3_slab_offset(NWV, REP, D, pps) + k3_slab_bytes(NWV, D));
   T* kn = qs + REP * D;
   T* vn = kn + D;
-  // EPI, before any K/V load: the epilogue's arithmetic (split partials added
-  // in split order, rounded, per-head RMSNorm, RoPE; one pair per lane) for
-  // the REP q heads into LDS, then the B operand from there. The wave whose
-  // split holds the new token (the sequence's last split) also computes this
-  // kv head's k and v, stores them at (page, slot) as the epilogue does, and
-  // keeps them in LDS: the chunk loaded from the pool holds that row's old
-  // contents, so consume() patches it from there.
   const bool owner = EPI && sp == nsb - 1;
-  if constexpr (EPI) {
-    float ecs[1], esn[1];
-    rope_cs<T>(epos, qfr, ecs[0], esn[0]);         // shared by the q heads and k
-    const float qw1a[1] = {qw1}, qw2a[1] = {qw2};
-#pragma unroll
-    for (int h = 0; h < REP; ++h) {
-      float a = qpa[h][0], cc = qpc[h][0];
-#pragma unroll
-      for (int u = 1; u < kQB; ++u) {
-        if (u < e.nsplit) {
-          a = a + qpa[h][u];
-          cc = cc + qpc[h][u];
-        }
-      }
-      for (int s2 = kQB; s2 < e.nsplit; ++s2) {
-        const float* pp = qsrc + (size_t)s2 * qplane + h * D;
-        a = a + pp[0];
-        cc = cc + pp[HALF];
-      }
-      float x1[1] = {round_to<T>(a)}, x2[1] = {round_to<T>(cc)};
-      norm_rope_cs<T, 1>(x1, x2, HALF, qw1a, qw2a, e.eps, ecs, esn);
-      if (lane < HALF) {
-        qs[h * D + lane] = from_f32<T>(x1[0]);
-        qs[h * D + lane + HALF] = from_f32<T>(x2[0]);
-      }
-    }
-    if (owner) {
-      float ka = kpa[0], kc = kpc[0], va = vpa[0], vc = vpc[0];
-#pragma unroll
-      for (int u = 1; u < kQB; ++u) {
-        if (u < e.nsplit) {
-          ka = ka + kpa[u];
-          kc = kc + kpc[u];
-          va = va + vpa[u];
-          vc = vc + vpc[u];
-        }
-      }
-      for (int s2 = kQB; s2 < e.nsplit; ++s2) {
-        const size_t o = (size_t)s2 * qplane;
-        ka = ka + ksrc[o];
-        kc = kc + ksrc[o + HALF];
-        va = va + vsrc[o];
-        vc = vc + vsrc[o + HALF];
-      }
-      float k1[1] = {round_to<T>(ka)}, k2[1] = {round_to<T>(kc)};
-      const float kw1a[1] = {kw1}, kw2a[1] = {kw2};
-      norm_rope_cs<T, 1>(k1, k2, HALF, kw1a, kw2a, e.eps, ecs, esn);
-      const float v1 = round_to<T>(va), v2 = round_to<T>(vc);
-      // a (page, slot) outside the pool is dropped rather than written
-      const uint64_t page = (uint64_t)epage, slot = (uint64_t)eslot;
-      const bool in_pool = page < (uint64_t)num_blocks && slot < (uint64_t)P;
-      if (lane < HALF) {
-        kn[lane] = from_f32<T>(k1[0]);
-        kn[lane + HALF] = from_f32<T>(k2[0]);
-        vn[lane] = from_f32<T>(v1);
-        vn[lane + HALF] = from_f32<T>(v2);
-        if (in_pool) {
-          const size_t off = ((page * P + slot) * KV + kvh) * D;
-          T* kd = (T*)e.k_dst + off;
-          T* vd = (T*)e.v_dst + off;
-          kd[lane] = from_f32<T>(k1[0]);
-          kd[lane + HALF] = from_f32<T>(k2[0]);
-          vd[lane] = from_f32<T>(v1);
-          vd[lane + HALF] = from_f32<T>(v2);
-        }
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // the B operand: head min(c, REP-1), dims 32 j + 8 r ...
-#pragma unroll
-    for (int j = 0; j < KB; ++j)
-      qb[j] = *(const u32x4_t*)(qs + min(c, REP - 1) * D + 32 * j + 8 * r);
-  }
-
   float m = -INFINITY, l = 0.f;
   f32x4_t acc[DPL];
 #pragma unroll
@@ -889,11 +807,98 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
     }
   };
 
+  // EPI: the epilogue's arithmetic (split partials added in split order,
+  // rounded, per-head RMSNorm, RoPE; one pair per lane) for the REP q heads
+  // into LDS, then the B operand from there. The wave whose split holds the
+  // new token (the sequence's last split) also computes this kv head's k and
+  // v, stores them at (page, slot) as the epilogue does, and keeps them in
+  // LDS: the chunk loaded from the pool holds that row's old contents, so
+  // consume() patches it from there. The split's first chunk is requested
+  // before this work, so that its round trip overlaps it (one-page splits
+  // have no other); the load is unconditional and in bounds (a split that
+  // exists has a page, the block ids are clamped, a zero length reads the
+  // first row of a valid page).
+  Chunk cs[DEPTH];
+  if constexpr (EPI) {
+    load_chunk(tstart, cs[0]);
+    float ecs[1], esn[1];
+    rope_cs<T>(epos, qfr, ecs[0], esn[0]);         // shared by the q heads and k
+    const float qw1a[1] = {qw1}, qw2a[1] = {qw2};
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+      float a = qpa[h][0], cc = qpc[h][0];
+#pragma unroll
+      for (int u = 1; u < kQB; ++u) {
+        if (u < e.nsplit) {
+          a = a + qpa[h][u];
+          cc = cc + qpc[h][u];
+        }
+      }
+      for (int s2 = kQB; s2 < e.nsplit; ++s2) {
+        const float* pp = qsrc + (size_t)s2 * qplane + h * D;
+        a = a + pp[0];
+        cc = cc + pp[HALF];
+      }
+      float x1[1] = {round_to<T>(a)}, x2[1] = {round_to<T>(cc)};
+      norm_rope_cs<T, 1>(x1, x2, HALF, qw1a, qw2a, e.eps, ecs, esn);
+      if (lane < HALF) {
+        qs[h * D + lane] = from_f32<T>(x1[0]);
+        qs[h * D + lane + HALF] = from_f32<T>(x2[0]);
+      }
+    }
+    if (owner) {
+      float ka = kpa[0], kc = kpc[0], va = vpa[0], vc = vpc[0];
+#pragma unroll
+      for (int u = 1; u < kQB; ++u) {
+        if (u < e.nsplit) {
+          ka = ka + kpa[u];
+          kc = kc + kpc[u];
+          va = va + vpa[u];
+          vc = vc + vpc[u];
+        }
+      }
+      for (int s2 = kQB; s2 < e.nsplit; ++s2) {
+        const size_t o = (size_t)s2 * qplane;
+        ka = ka + ksrc[o];
+        kc = kc + ksrc[o + HALF];
+        va = va + vsrc[o];
+        vc = vc + vsrc[o + HALF];
+      }
+      float k1[1] = {round_to<T>(ka)}, k2[1] = {round_to<T>(kc)};
+      const float kw1a[1] = {kw1}, kw2a[1] = {kw2};
+      norm_rope_cs<T, 1>(k1, k2, HALF, kw1a, kw2a, e.eps, ecs, esn);
+      const float v1 = round_to<T>(va), v2 = round_to<T>(vc);
+      // a (page, slot) outside the pool is dropped rather than written
+      const uint64_t page = (uint64_t)epage, slot = (uint64_t)eslot;
+      const bool in_pool = page < (uint64_t)num_blocks && slot < (uint64_t)P;
+      if (lane < HALF) {
+        kn[lane] = from_f32<T>(k1[0]);
+        kn[lane + HALF] = from_f32<T>(k2[0]);
+        vn[lane] = from_f32<T>(v1);
+        vn[lane + HALF] = from_f32<T>(v2);
+        if (in_pool) {
+          const size_t off = ((page * P + slot) * KV + kvh) * D;
+          T* kd = (T*)e.k_dst + off;
+          T* vd = (T*)e.v_dst + off;
+          kd[lane] = from_f32<T>(k1[0]);
+          kd[lane + HALF] = from_f32<T>(k2[0]);
+          vd[lane] = from_f32<T>(v1);
+          vd[lane + HALF] = from_f32<T>(v2);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the B operand: head min(c, REP-1), dims 32 j + 8 r ...
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      qb[j] = *(const u32x4_t*)(qs + min(c, REP - 1) * D + 32 * j + 8 * r);
+  }
+
   if (tstart < tend) {
     // DEPTH chunks in flight: chunk slot i is refilled right after use
-    Chunk cs[DEPTH];
 #pragma unroll
-    for (int i = 0; i < DEPTH; ++i) load_chunk(tstart + i * CH, cs[i]);
+    for (int i = EPI ? 1 : 0; i < DEPTH; ++i) load_chunk(tstart + i * CH, cs[i]);
     bool more = true;
     for (int t0 = tstart; more; t0 += DEPTH * CH) {
 #pragma unroll

@@ -29,6 +29,50 @@ namespace {
 constexpr int kNT = 1024;
 constexpr double kFix = 1099511627776.0;  // 2^40
 
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x2v __attribute__((ext_vector_type(2)));
+
+// Element e of a 16-byte vector of T as float.
+template <typename T> __device__ __forceinline__ float word_elem(const u32x4v& w, int e);
+template <> __device__ __forceinline__ float word_elem<__bf16>(const u32x4v& w, int e) {
+  return (e & 1) ? bf16_hi(w[e / 2]) : bf16_lo(w[e / 2]);
+}
+template <> __device__ __forceinline__ float word_elem<_Float16>(const u32x4v& w, int e) {
+  const uint32_t v = w[e / 2];
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)((e & 1) ? v >> 16 : v & 0xffffu));
+}
+template <> __device__ __forceinline__ float word_elem<float>(const u32x4v& w, int e) {
+  return __uint_as_float(w[e]);
+}
+
+// Exponent fields of a 16-byte vector folded into a running unsigned max
+// (per 16-bit half for the half types): a field of all ones, i.e. an inf or
+// NaN somewhere, survives as the maximum.
+template <typename T> struct ExpBits;
+template <> struct ExpBits<__bf16> { static constexpr uint32_t kMask = 0x7F807F80u; };
+template <> struct ExpBits<_Float16> { static constexpr uint32_t kMask = 0x7C007C00u; };
+template <> struct ExpBits<float> { static constexpr uint32_t kMask = 0x7F800000u; };
+template <typename T> __device__ __forceinline__ uint32_t fold_exp(uint32_t acc, const u32x4v& w) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t x = w[i] & ExpBits<T>::kMask;
+    if constexpr (sizeof(T) == 2)
+      acc = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(
+                                             __builtin_bit_cast(u16x2v, acc),
+                                             __builtin_bit_cast(u16x2v, x)));
+    else
+      acc = max(acc, x);
+  }
+  return acc;
+}
+template <typename T> __device__ __forceinline__ bool exp_all_ones(uint32_t acc) {
+  constexpr uint32_t m = ExpBits<T>::kMask;
+  if constexpr (sizeof(T) == 2)
+    return (acc & 0xffffu) == (m & 0xffffu) || (acc >> 16) == (m >> 16);
+  else
+    return acc == m;
+}
+
 __device__ __forceinline__ uint32_t okey(float x) {
   const uint32_t u = __float_as_uint(x);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -94,6 +138,13 @@ __global__ __launch_bounds__(kNT) void sample_kernel(
   // bf16 row is two rounds of requests); a scalar tail. Vector indices past
   // the row re-read its last vector (unconditional loads keep the wait
   // counts static) and are not visited.
+  // A single workgroup reads the whole row, so the per-element work is what
+  // bounds it: per vector only its maximum is compared with the running one
+  // (the vector index of the first strict improvement is kept) and the
+  // exponent fields are folded into an integer max for the finiteness test.
+  // After the loop the kept vector is read again and its first element equal
+  // to the maximum taken: the thread's first maximum in index order, as an
+  // element-by-element scan would find.
   float bv = -INFINITY;
   int64_t bi = INT64_MAX;
   bool bad = false;
@@ -107,24 +158,43 @@ __global__ __launch_bounds__(kNT) void sample_kernel(
   {
     constexpr int E = 16 / sizeof(T);                 // elements per vector
     constexpr int kUnroll = 10;
-    struct Vec16 {
-      T v[E];
-    };
     const bool aligned = ((uintptr_t)row % 16) == 0;
     const int64_t nvec = aligned ? V / E : 0;
-    const Vec16* rv = (const Vec16*)row;
+    const u32x4v* rv = (const u32x4v*)row;
+    float vbest = -INFINITY;
+    int64_t jbest = -1;
+    uint32_t emax = 0;
     for (int64_t j0 = tid; j0 < nvec; j0 += (int64_t)kNT * kUnroll) {
-      Vec16 buf[kUnroll];
+      u32x4v buf[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) buf[u] = rv[min(j0 + (int64_t)u * kNT, nvec - 1)];
+      // (the empty asm keeps every load ahead of the guarded uses below;
+      // a load sunk into a guarded block is waited for on its own)
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) asm volatile("" ::"v"(buf[u]));
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int64_t j = j0 + (int64_t)u * kNT;
         if (j < nvec) {
+          float vm = word_elem<T>(buf[u], 0);
 #pragma unroll
-          for (int e = 0; e < E; ++e) visit(to_f32(buf[u].v[e]), j * E + e);
+          for (int e = 1; e < E; ++e) vm = fmaxf(vm, word_elem<T>(buf[u], e));
+          emax = fold_exp<T>(emax, buf[u]);
+          if (vm > vbest) {
+            vbest = vm;
+            jbest = j;
+          }
         }
       }
+    }
+    if (exp_all_ones<T>(emax)) bad = true;
+    if (jbest >= 0) {
+      const u32x4v w = rv[jbest];
+      int ebest = E - 1;
+#pragma unroll
+      for (int e = E - 2; e >= 0; --e) ebest = word_elem<T>(w, e) == vbest ? e : ebest;
+      bv = vbest;
+      bi = jbest * E + ebest;
     }
     for (int64_t i = nvec * E + tid; i < V; i += kNT) visit(to_f32(row[i]), i);
   }

@@ -558,7 +558,13 @@ class Qwen3DecodeModel:
                 act = name == "gate_up" and not sw
                 red = name == "qkv"                   # the qkv epilogue reads its partials
                 nrm = name in ("o", "down")           # ... K1 those of o and down
-                for c in candidates(batch, lins[0].N, lins[0].K, lins[0].fmt, swiglu=sw):
+                cands = candidates(batch, lins[0].N, lins[0].K, lins[0].fmt, swiglu=sw)
+                if red:
+                    # the fused K3 requests QKV_SPLITS_UP_FRONT split partials
+                    # with its first loads; each further split costs it a
+                    # round trip, which the timed reduction does not show
+                    cands = [c for c in cands if c.ksplit <= QKV_SPLITS_UP_FRONT] or cands
+                for c in cands:
                     us = self.time_projection(lins, batch, c, swiglu=sw, with_act=act,
                                               with_reduce=red, with_norm=nrm)
                     if verbose:
@@ -703,6 +709,7 @@ def _dense_linear(w: torch.Tensor, dtype: torch.dtype) -> QLinear:
 UNIT_PAGES = 4      # K3 split size the heuristic aims for (pages)
 SMALL_GRID_PAGES = 1024   # below this many (sequence, kv head, page) units: 1-page splits
 MAX_SPLITS = 64     # bound on K3 splits per (sequence, kv head)
+QKV_SPLITS_UP_FRONT = 4   # qkv split partials the fused K3 loads up front (kQB)
 
 
 def attention_splits(batch: int, kv_heads: int, max_pages: int, *,
