@@ -128,3 +128,41 @@ def test_deterministic_and_graph_replay():
     run()
     assert torch.equal(first, tok)
     assert graph_replays_match(run, lambda: tok)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("V", [151936, 151935, 1000])
+def test_greedy_is_first_maximum(dtype, V):
+    """Temperature 0 against torch.argmax (first maximal index) on rows built
+    to tie: the maximum in several 16-byte vectors of one thread and of
+    different threads, twice inside one vector, +0/-0 as the maximum, in the
+    scalar tail, and a constant row. An odd V puts every other row off
+    16-byte alignment (the kernel's scalar path) and leaves a tail."""
+    from acorninfer_amd.sampler import sample_batch
+    E = 16 // torch.tensor([], dtype=dtype).element_size()   # elements per 16-byte vector
+    g = torch.Generator().manual_seed(V)
+    x = (torch.randn(6, V, generator=g) * 3).clamp(-20, 20)
+    top = 40.0
+    for i in [9001, 5 * E + 3, (5 + 1024) * E, 7 * E + E - 1]:   # same thread / other threads
+        if i < V:
+            x[1, i] = top
+    x[2, 3 * E + 1] = top                                        # twice in one vector
+    x[2, 3 * E + E - 1] = top
+    x[3] = -x[3].abs() - 1.0                                     # the maximum is a zero
+    x[3, 50] = 0.0
+    x[3, 100] = -0.0
+    x[3, 20] = -0.0
+    x[4, V - 1] = top                                            # last element, and earlier
+    x[4, V // 3] = top
+    x[5] = 1.0                                                   # constant row
+    logits = x.to(dtype)
+    B = logits.shape[0]
+    zeros = torch.zeros(B, device="cuda")
+    tok, lp, st = sample_batch(logits.cuda(), zeros, torch.zeros(B, dtype=torch.int32,
+                                                                   device="cuda"),
+                               torch.ones(B, device="cuda"), zeros)
+    assert st.cpu().eq(0).all()
+    want = torch.argmax(logits.float(), dim=1)
+    assert tok.cpu().tolist() == want.tolist()
+    assert lp.cpu().eq(0).all()
