@@ -12,6 +12,10 @@ in:
   per K and V (one allocation for the whole pool; layer l's pages stay the
   reference's per-layer tensors as views). `scatter_decode` is the HIP
   kernel acorn_kv_scatter.
+- Speculative verify (pager.py:115-148, 211-244): `scatter_verify` writes an
+  m-token window per sequence with the same scatter kernel,
+  `ensure_append_capacity_n` reserves the window, `set_lens` rolls a length
+  back after a partial accept.
 - `PagedCacheView` (pager.py:151-259): the block table is a `list[int]`
   shared with the caller; written length is tracked per layer; token t of a
   sequence lives at (table[t // P], t % P). `ensure_append_capacity`
@@ -115,6 +119,32 @@ class PagedKVCache:
         for view in views:
             view._lens[layer_idx] = view._lens.get(layer_idx, 0) + 1
 
+    def scatter_verify(self, views: list["PagedCacheView"], layer_idx: int, k: torch.Tensor,
+                       v: torch.Tensor, pages: torch.Tensor, slots: torch.Tensor) -> None:
+        """Verify-step write of an m-token window per sequence (pager.py:115-148):
+        k_pages[l][pages[b, j], slots[b, j]] = k[b, :, j, :] (same for v), then
+        each view's layer length grows by m. k/v [B, KV, m, D]; pages/slots
+        [B, m] int64 from ensure_append_capacity_n. The window is flattened to
+        B*m rows in (b, j) order and written by the decode scatter kernel
+        (m = 1 is scatter_decode). Capacity was reserved beforehand, so this
+        never raises BlockExhausted."""
+        B = len(views)
+        m = k.shape[2]
+        assert m == v.shape[2], "scatter_verify requires equal k/v window sizes"
+        assert B == k.shape[0] == v.shape[0] == pages.shape[0] == slots.shape[0]
+        assert pages.shape[1] == slots.shape[1] == m, "pages/slots must be [B, m]"
+        kc = k.permute(0, 2, 1, 3).reshape(B * m, k.shape[1], k.shape[3]).to(self.dtype).contiguous()
+        vc = v.permute(0, 2, 1, 3).reshape(B * m, v.shape[1], v.shape[3]).to(self.dtype).contiguous()
+        pg = pages.reshape(-1).to(device=self.device, dtype=torch.int64).contiguous()
+        sl = slots.reshape(-1).to(device=self.device, dtype=torch.int64).contiguous()
+        rc = lib().acorn_kv_scatter(
+            ptr(kc), ptr(vc), ptr(self.k_pages[layer_idx]), ptr(self.v_pages[layer_idx]),
+            ptr(pg), ptr(sl), B * m, self.num_kv_heads, self.head_dim, self.page_size,
+            self.num_blocks, dtype_code(kc), stream_ptr(self.device))
+        check(rc, "scatter_verify")
+        for view in views:
+            view._lens[layer_idx] = view._lens.get(layer_idx, 0) + m
+
 
 class PagedCacheView:
     """Per-sequence view: a block table (shared list) and per-layer lengths."""
@@ -164,6 +194,27 @@ class PagedCacheView:
         page = self.cache.page_size
         self._grow_to(base // page + 1)
         return self.table[base // page], base % page
+
+    def ensure_append_capacity_n(self, layer_idx: int, n: int) -> list[tuple[int, int]]:
+        """Room for n more tokens at layer `layer_idx` (pager.py:211-227): the
+        table grows to ceil((len + n) / P) blocks as `write` would, then each
+        position's (block id, slot) in order. A BlockExhausted part-way keeps
+        the blocks already taken in the table; lengths are not advanced
+        (scatter_verify commits them). n = 1 is ensure_append_capacity."""
+        base = self._lens.get(layer_idx, 0)
+        page = self.cache.page_size
+        self._grow_to((base + n + page - 1) // page)
+        return [(self.table[p // page], p % page) for p in range(base, base + n)]
+
+    def set_lens(self, layer_idx: int, new_len: int) -> None:
+        """Roll layer `layer_idx` back to `new_len` written tokens after a
+        verify step accepted fewer than it wrote (pager.py:229-244). Blocks stay
+        in the table (the dead slots are rewritten by the next window); moving
+        forward is a ValueError (only writes advance a length)."""
+        cur = self._lens.get(layer_idx, 0)
+        if new_len > cur:
+            raise ValueError(f"set_lens is rollback-only: new_len {new_len} > written {cur}")
+        self._lens[layer_idx] = new_len
 
     def update(self, layer_idx: int, k_new: torch.Tensor, v_new: torch.Tensor
                ) -> tuple[torch.Tensor, torch.Tensor]:

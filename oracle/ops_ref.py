@@ -10,6 +10,9 @@ Pins (tests/test_oracle_ops.py):
   q=0 -> mean of V; output invariant under relabelling the pool's blocks.
 - build_tables_ref: the reference's known answers
   test_ops_paged_attention.py:157-191.
+- paged_verify_ref: a window of 1 equals paged_attention_ref; a float64
+  brute force over an explicit causal mask; k = 0 gives the exact mean of
+  each row's visible v.
 """
 from __future__ import annotations
 
@@ -101,6 +104,45 @@ def paged_attention_brute(q, k_pages, v_pages, tables, seq_lens):
             for t in range(L):
                 page = int(tables[b, t // P])
                 out[b, h] += (w[t] / z) * v_pages[page, t % P, kv].double()
+    return out
+
+
+def paged_verify_ref(q, k_pages, v_pages, tables, seq_lens):
+    """ops/paged_verify.py:96-123 (and the dense reference of
+    tests/test_paged_verify.py:35-58): q [B, m, H, D]; seq_lens[b] = len + m
+    counts the whole window. Row (b, j) attends to tokens 0 .. seq_lens[b] -
+    (m - 1 - j) - 1 of sequence b (its history and the window's first j + 1
+    tokens), with the decode oracle's gather, GQA map and fp32 softmax; the
+    result is cast to q.dtype."""
+    B, M, H, D = q.shape
+    rows = []
+    for b in range(B):
+        for j in range(M):
+            Lj = int(seq_lens[b]) - (M - 1 - j)
+            rows.append(paged_attention_ref(q[b, j][None], k_pages, v_pages, tables[b][None],
+                                            torch.tensor([Lj]))[0])
+    return torch.stack(rows, 0).view(B, M, H, D)
+
+
+def paged_verify_brute(q, k_pages, v_pages, tables, seq_lens):
+    """Independent float64 brute force: the whole window's keys gathered once
+    per sequence, scores over all seq_lens[b] tokens, future positions masked
+    with an explicit [m, L] causal mask before a row-wise softmax."""
+    B, M, H, D = q.shape
+    NB, P, KV, _ = k_pages.shape
+    rep = H // KV
+    out = torch.zeros(B, M, H, D, dtype=torch.float64)
+    for b in range(B):
+        L = int(seq_lens[b])
+        pos = torch.arange(L)
+        k = torch.stack([k_pages[int(tables[b, t // P]), t % P] for t in range(L)]).double()
+        v = torch.stack([v_pages[int(tables[b, t // P]), t % P] for t in range(L)]).double()
+        limit = torch.tensor([L - (M - 1 - j) for j in range(M)])
+        visible = pos[None, :] < limit[:, None]                       # [m, L]
+        for h in range(H):
+            s = q[b, :, h].double() @ k[:, h // rep].T * (D ** -0.5)   # [m, L]
+            s = s.masked_fill(~visible, float("-inf"))
+            out[b, :, h] = torch.softmax(s, dim=-1) @ v[:, h // rep]
     return out
 
 
