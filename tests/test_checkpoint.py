@@ -1,0 +1,65 @@
+"""The quantised safetensors format (models/checkpoint.py), on the CPU: a
+model written by save_quantized and read back by load_quantized holds the
+same bytes in every weight, scale and norm, in the same fused and
+interleaved layout, for bf16, w8a16 and w4a16; the file keeps the
+reference's module names and the int4 packing of quant/quantize.py:85-101
+(unpacking a stored q_proj gives the quantiser's own nibbles)."""
+import pytest
+import torch
+
+from acorninfer_amd.config import Qwen3Config
+from acorninfer_amd.models.checkpoint import load_quantized, save_quantized
+from acorninfer_amd.models.qwen3 import Qwen3DecodeModel, random_state_dict
+from acorninfer_amd.quant import quantize as Q
+
+
+def _model(fmt):
+    cfg = Qwen3Config.qwen3_0_6b().with_layers(2)
+    sd = random_state_dict(cfg, seed=4, std=0.02, dtype=torch.float32)
+    return cfg, sd, Qwen3DecodeModel.from_state_dict(cfg, sd, weight_format=fmt, device="cpu")
+
+
+def _same(a, b):
+    assert (a is None) == (b is None)
+    if a is not None:
+        assert a.dtype == b.dtype and a.shape == b.shape and torch.equal(a, b)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "w8a16", "w4a16"])
+def test_round_trip_is_bit_exact(fmt, tmp_path):
+    cfg, _, m = _model(fmt)
+    path = str(tmp_path / "model.safetensors")
+    save_quantized(m, path)
+    r = load_quantized(path, device="cpu")
+    assert r.cfg == cfg
+    _same(r.embed, m.embed)
+    _same(r.norm, m.norm)
+    for La, Lb in zip(m.layers, r.layers):
+        for n in ("input_norm", "post_norm", "q_norm", "k_norm"):
+            _same(getattr(Lb, n), getattr(La, n))
+        for n in ("qkv", "o", "gate_up", "down"):
+            a, b = getattr(La, n), getattr(Lb, n)
+            assert (a.fmt, a.N, a.K, a.il16) == (b.fmt, b.N, b.K, b.il16)
+            _same(b.w, a.w)
+            _same(b.scale, a.scale)
+            _same(b.zero, a.zero)
+    _same(r.lm_head.w, m.lm_head.w)
+    _same(r.lm_head.scale, m.lm_head.scale)
+
+
+def test_file_uses_reference_names_and_packing(tmp_path):
+    from safetensors import safe_open
+    cfg, sd, m = _model("w4a16")
+    path = str(tmp_path / "w4.safetensors")
+    save_quantized(m, path)
+    with safe_open(path, framework="pt") as f:
+        keys = set(f.keys())
+        meta = f.metadata()
+        qw = f.get_tensor("layers.1.self_attn.q_proj.qweight")
+        sc = f.get_tensor("layers.1.self_attn.q_proj.scales")
+        assert "layers.1.mlp.gate_proj.qweight" in keys and "lm_head.scales" in keys
+        assert "layers.0.self_attn.k_norm.weight" in keys
+        assert not any(k.endswith(".zeros") for k in keys)      # symmetric weights
+    assert meta["format"] == "w4a16" and meta["group_size"] == "128"
+    u, s = Q.quantize_w4_sym(sd["layers.1.self_attn.q_proj.weight"])
+    assert torch.equal(Q.unpack_w4(qw), u) and torch.equal(sc, s)
