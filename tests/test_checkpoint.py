@@ -63,3 +63,24 @@ def test_file_uses_reference_names_and_packing(tmp_path):
     assert meta["format"] == "w4a16" and meta["group_size"] == "128"
     u, s = Q.quantize_w4_sym(sd["layers.1.self_attn.q_proj.weight"])
     assert torch.equal(Q.unpack_w4(qw), u) and torch.equal(sc, s)
+
+
+@pytest.mark.gpu
+def test_loaded_w4_model_decodes_identically_on_the_gpu(tmp_path):
+    """The file loaded straight onto the GPU runs the decode step to the same
+    logits, bit for bit, as the model it was written from."""
+    from acorninfer_amd.cache.pager import PagedCacheView
+    from model_utils import feed_prompt, new_cache
+    cfg = Qwen3Config.qwen3_0_6b().with_layers(2)
+    sd = random_state_dict(cfg, seed=4, std=0.02, dtype=torch.float32)
+    m = Qwen3DecodeModel.from_state_dict(cfg, sd, weight_format="w4a16", device="cuda")
+    path = str(tmp_path / "w4.safetensors")
+    save_quantized(m, path)
+    r = load_quantized(path, device="cuda")
+    assert r.lm_head.w.is_cuda and r.layers[0].gate_up.w.is_cuda
+    prompt = [11, 4093, 77, 150000, 5]
+    outs = []
+    for model in (m, r):
+        _, cache = new_cache(model, 8)
+        outs.append(feed_prompt(model, PagedCacheView(cache), prompt))
+    assert torch.equal(outs[0], outs[1])
