@@ -73,12 +73,18 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
 
 // int4: 8 nibbles (columns c..c+7) -> bf16 (128+u) in MFMA item order
 // (p, p+4) per dword.
+// The mask and the bias are made opaque register values (an SGPR and a VGPR):
+// with literal operands the compiler emits v_and_b32 + v_or_b32 (gfx950's
+// VOP3 forms take no literal), with registers it can use one v_and_or_b32.
 __device__ __forceinline__ u32x4 unpack_w4(uint32_t w) {
+  uint32_t m = 0x000F000Fu, c = 0x43004300u;
+  asm("" : "+s"(m));
+  asm("" : "+v"(c));
   u32x4 r;
-  r[0] = (w & 0x000F000Fu) | 0x43004300u;
-  r[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  r[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  r[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  r[0] = (w & m) | c;
+  r[1] = ((w >> 4) & m) | c;
+  r[2] = ((w >> 8) & m) | c;
+  r[3] = ((w >> 12) & m) | c;
   return r;
 }
 
