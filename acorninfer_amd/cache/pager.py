@@ -56,21 +56,22 @@ class BlockAllocator:
 
     def allocate(self) -> int:
         if not self._free:
-            raise BlockExhausted("no free KV blocks")
+            raise BlockExhausted(f"all {self.total} KV blocks are in use")
         block = self._free.pop()
         self._live.add(block)
         return block
 
     def free(self, block: int) -> None:
         if block not in self._live:
-            raise ValueError(f"block {block} is not live (double free or invalid)")
+            raise ValueError(f"free({block}): that block is not allocated")
         self._live.remove(block)
         self._free.append(block)
 
     def assert_balanced(self) -> None:
         """Raise (also under `python -O`) if any block is still live."""
         if self._live:
-            raise AssertionError(f"KV leak: blocks {sorted(self._live)} never freed")
+            raise AssertionError(f"KV leak: {len(self._live)} block(s) still allocated: "
+                                 f"{sorted(self._live)}")
 
 
 class PagedKVCache:
@@ -97,6 +98,25 @@ class PagedKVCache:
         """Elements between layer l and l+1 of the pool."""
         return self.num_blocks * self.page_size * self.num_kv_heads * self.head_dim
 
+    def _check_rows(self, k, v, pages, slots) -> None:
+        """The kernel indexes k/v with the pool's kv-head count and head size,
+        and writes (page, slot) into the pool: reject what does not fit (the
+        reference's torch indexing raises IndexError for an out-of-range
+        index; this costs one device-to-host read when pages/slots live on
+        the GPU)."""
+        for name, t in (("k", k), ("v", v)):
+            assert t.dim() == 4 and t.shape[1] == self.num_kv_heads and \
+                t.shape[3] == self.head_dim, \
+                f"{name} is {tuple(t.shape)}; the pool holds {self.num_kv_heads} kv heads " \
+                f"of {self.head_dim}"
+        if pages.numel() == 0:
+            return
+        bad = ((pages < 0) | (pages >= self.num_blocks)).any() | \
+              ((slots < 0) | (slots >= self.page_size)).any()
+        if bool(bad):
+            raise IndexError(f"(page, slot) outside the pool of {self.num_blocks} blocks x "
+                             f"{self.page_size} slots")
+
     def scatter_decode(self, views: list["PagedCacheView"], layer_idx: int, k: torch.Tensor,
                        v: torch.Tensor, pages: torch.Tensor, slots: torch.Tensor) -> None:
         """Decode-step batched write (pager.py:87-113): k_pages[l][pages[b], slots[b]] =
@@ -105,8 +125,9 @@ class PagedKVCache:
         k/v [B, KV, 1, D]; pages/slots [B] int64 from ensure_append_capacity.
         """
         B = len(views)
-        assert k.shape[2] == 1 and v.shape[2] == 1, "scatter_decode is decode-only (s=1)"
+        assert k.shape[2] == 1 and v.shape[2] == 1, "scatter_decode writes one token per row"
         assert B == k.shape[0] == v.shape[0] == pages.shape[0] == slots.shape[0]
+        self._check_rows(k, v, pages, slots)
         kc = k.to(self.dtype).contiguous()
         vc = v.to(self.dtype).contiguous()
         pg = pages.to(device=self.device, dtype=torch.int64).contiguous()
@@ -130,9 +151,10 @@ class PagedKVCache:
         never raises BlockExhausted."""
         B = len(views)
         m = k.shape[2]
-        assert m == v.shape[2], "scatter_verify requires equal k/v window sizes"
+        assert m == v.shape[2], "k and v must hold windows of the same length"
         assert B == k.shape[0] == v.shape[0] == pages.shape[0] == slots.shape[0]
-        assert pages.shape[1] == slots.shape[1] == m, "pages/slots must be [B, m]"
+        assert pages.shape[1] == slots.shape[1] == m, "one (page, slot) per window token"
+        self._check_rows(k, v, pages, slots)
         kc = k.permute(0, 2, 1, 3).reshape(B * m, k.shape[1], k.shape[3]).to(self.dtype).contiguous()
         vc = v.permute(0, 2, 1, 3).reshape(B * m, v.shape[1], v.shape[3]).to(self.dtype).contiguous()
         pg = pages.reshape(-1).to(device=self.device, dtype=torch.int64).contiguous()
@@ -213,7 +235,8 @@ class PagedCacheView:
         forward is a ValueError (only writes advance a length)."""
         cur = self._lens.get(layer_idx, 0)
         if new_len > cur:
-            raise ValueError(f"set_lens is rollback-only: new_len {new_len} > written {cur}")
+            raise ValueError(f"set_lens can only move a length back: asked for {new_len}, "
+                             f"{cur} written")
         self._lens[layer_idx] = new_len
 
     def update(self, layer_idx: int, k_new: torch.Tensor, v_new: torch.Tensor

@@ -95,21 +95,60 @@ def load_quantized(path: str, *, device="cuda") -> Qwen3DecodeModel:
     from safetensors.torch import load_file
     with safe_open(path, framework="pt") as f:
         meta = f.metadata() or {}
+    for key in ("format", "config"):
+        if key not in meta:
+            raise ValueError(f"{path}: metadata has no {key!r} entry (not a save_quantized file)")
+    if meta["format"] not in FORMATS:
+        raise ValueError(f"{path}: unknown weight format {meta['format']!r}")
     fmt = FORMATS[meta["format"]]
+    if fmt != WFMT_BF16:
+        if meta.get("group_size") != "128":
+            raise ValueError(f"{path}: group size {meta.get('group_size')!r}; the kernels use 128")
+        if fmt == WFMT_W4 and not meta.get("packing", "").startswith("uint8 [N, K/2], low nibble"):
+            raise ValueError(f"{path}: int4 packing {meta.get('packing')!r} is not low-nibble-even")
     # JSON has no tuples: sequence fields of the config come back as lists
     cfg = Qwen3Config(**{k: tuple(v) if isinstance(v, list) else v
                          for k, v in json.loads(meta["config"]).items()})
     sd = load_file(path, device=str(torch.device(device)))
 
+    def tensor(name: str, shape: tuple, dtype: torch.dtype) -> torch.Tensor:
+        t = sd.get(name)
+        if t is None:
+            raise ValueError(f"{path}: tensor {name} is missing")
+        if tuple(t.shape) != shape or t.dtype != dtype:
+            raise ValueError(f"{path}: {name} is {tuple(t.shape)} {t.dtype}, "
+                             f"the config needs {shape} {dtype}")
+        return t
+
+    H, D, I = cfg.hidden_size, cfg.head_dim, cfg.intermediate_size
+    qn, kvn = cfg.num_attention_heads * D, cfg.num_key_value_heads * D
+    shapes = {"q_proj": (qn, H), "k_proj": (kvn, H), "v_proj": (kvn, H), "o_proj": (H, qn),
+              "gate_proj": (I, H), "up_proj": (I, H), "down_proj": (H, I),
+              "lm_head": (cfg.vocab_size, H)}
+
     def lin(*names: str) -> QLinear:
+        parts = []
+        for n in names:
+            N, K = shapes[n.rsplit(".", 1)[-1]]
+            if fmt == WFMT_BF16:
+                parts.append((tensor(f"{n}.weight", (N, K), torch.bfloat16), None, None))
+                continue
+            if K % 128:
+                raise ValueError(f"{path}: {n} has K={K}, not a multiple of the group size 128")
+            if fmt == WFMT_W8:
+                parts.append((tensor(f"{n}.qweight", (N, K), torch.int8),
+                              tensor(f"{n}.scales", (N,), torch.float16), None))
+            else:
+                zs = (tensor(f"{n}.zeros", (N, K // 128), torch.float16)
+                      if f"{names[0]}.zeros" in sd else None)
+                parts.append((tensor(f"{n}.qweight", (N, K // 2), torch.uint8),
+                              tensor(f"{n}.scales", (N, K // 128), torch.float16), zs))
+        w = torch.cat([p[0] for p in parts], 0).contiguous()
+        K = shapes[names[0].rsplit(".", 1)[-1]][1]
         if fmt == WFMT_BF16:
-            w = torch.cat([sd[f"{n}.weight"] for n in names], 0).contiguous()
-            return QLinear(fmt, w, w.shape[0], w.shape[1])
-        w = torch.cat([sd[f"{n}.qweight"] for n in names], 0).contiguous()
-        s = torch.cat([sd[f"{n}.scales"] for n in names], 0).contiguous()
-        z = (torch.cat([sd[f"{n}.zeros"] for n in names], 0).contiguous()
-             if f"{names[0]}.zeros" in sd else None)
-        K = w.shape[1] * (2 if fmt == WFMT_W4 else 1)
+            return QLinear(fmt, w, w.shape[0], K)
+        s = torch.cat([p[1] for p in parts], 0).contiguous()
+        z = None if parts[0][2] is None else torch.cat([p[2] for p in parts], 0).contiguous()
         return QLinear(fmt, w, w.shape[0], K, s, z)
 
     layers = []
@@ -118,13 +157,16 @@ def load_quantized(path: str, *, device="cuda") -> Qwen3DecodeModel:
         gu = lin(f"{p}.mlp.gate_proj", f"{p}.mlp.up_proj")
         if gu.N % 32 == 0:
             gu = gu.interleaved()
-        norms = [sd[f"{p}.{n}.weight"] for n in _NORMS]
+        norms = [tensor(f"{p}.{n}.weight", (D if "self_attn" in n else H,), torch.bfloat16)
+                 for n in _NORMS]
         layers.append(LayerWeights(
             input_norm=norms[0], post_norm=norms[1], q_norm=norms[2], k_norm=norms[3],
             qkv=lin(f"{p}.self_attn.q_proj", f"{p}.self_attn.k_proj", f"{p}.self_attn.v_proj"),
             o=lin(f"{p}.self_attn.o_proj"), gate_up=gu, down=lin(f"{p}.mlp.down_proj")))
-    return Qwen3DecodeModel(cfg, embed=sd["embed_tokens.weight"], layers=layers,
-                            norm=sd["norm.weight"], lm_head=lin("lm_head"), dtype=torch.bfloat16)
+    return Qwen3DecodeModel(cfg, embed=tensor("embed_tokens.weight", (cfg.vocab_size, H),
+                                              torch.bfloat16),
+                            layers=layers, norm=tensor("norm.weight", (H,), torch.bfloat16),
+                            lm_head=lin("lm_head"), dtype=torch.bfloat16)
 
 
 __all__ = ["save_quantized", "load_quantized"]

@@ -346,9 +346,10 @@ class Qwen3DecodeModel:
 
     # ------------------------------------------------------------------ decode --
     def buffers(self, batch: int, max_pages: int, num_splits: int | None = None,
-                tilings: dict | None = None) -> "StepBuffers":
+                tilings: dict | None = None, *, prefill: bool = False) -> "StepBuffers":
         return StepBuffers(self, batch, max_pages, num_splits,
-                           tilings if tilings is not None else self.tilings.get(batch))
+                           tilings if tilings is not None else self.tilings.get(batch),
+                           prefill=prefill)
 
     def step(self, buf: "StepBuffers", k_pool: torch.Tensor, v_pool: torch.Tensor,
              num_blocks: int, page_size: int, *, fused_attn: bool = True,
@@ -444,9 +445,11 @@ class Qwen3DecodeModel:
             ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
         if head_rows is not None:
             n = int(head_rows.numel())
+            if n == 0:
+                return torch.empty(0, cfg.vocab_size, dtype=buf.x.dtype, device=self.device)
             hx = buf.normed.index_select(0, head_rows)
             ch, _ = self.lm_head.plan(n)
-            out = torch.empty(n, cfg.vocab_size, dtype=buf.logits.dtype, device=self.device)
+            out = torch.empty(n, cfg.vocab_size, dtype=buf.x.dtype, device=self.device)
             ws = (torch.empty(ch.ksplit, n, cfg.vocab_size, dtype=torch.float32,
                               device=self.device)
                   if ch.ksplit > 1 and self.lm_head.fmt != _lib.WFMT_F32 else None)
@@ -676,7 +679,7 @@ class Qwen3DecodeModel:
         W = max(len(v.table) for v in views)
         ids, pos, pages, slots, lens, tabs = [], [], [], [], [], []
         for i, (v, s, n) in enumerate(zip(views, starts, chunk_lens)):
-            ids.append(input_ids[i, :n].to(torch.int64))
+            ids.append(input_ids[i, :n].to(torch.int64).cpu())
             pos += list(range(s, s + n))
             pages += [p for p, _ in targets[i]]
             slots += [q for _, q in targets[i]]
@@ -685,27 +688,41 @@ class Qwen3DecodeModel:
             row[:len(v.table)] = torch.tensor(v.table, dtype=torch.int32)
             tabs.append(row.expand(n, W))
         R = len(pos)
-        # the step buffers of the last shape are kept (a prompt batch often repeats it)
-        key = (R, W)
-        cached = getattr(self, "_extend_buf", None)
-        if cached is None or cached[0] != key:
-            self._extend_buf = None
-            self._extend_buf = (key, self.buffers(R, W))
-        buf = self._extend_buf[1]
-        dev = self.device
-        buf.ids.copy_(torch.cat(ids).to(dev))
-        buf.positions.copy_(torch.tensor(pos, dtype=torch.int64))
-        buf.pages.copy_(torch.tensor(pages, dtype=torch.int64))
-        buf.slots.copy_(torch.tensor(slots, dtype=torch.int64))
-        buf.lens.copy_(torch.tensor(lens, dtype=torch.int32))
-        buf.tables.copy_(torch.cat(tabs))
+        ids_all = torch.cat(ids)
+        pos_all = torch.tensor(pos, dtype=torch.int64)
+        pages_all = torch.tensor(pages, dtype=torch.int64)
+        slots_all = torch.tensor(slots, dtype=torch.int64)
+        lens_all = torch.tensor(lens, dtype=torch.int32)
+        tabs_all = torch.cat(tabs)
         last = torch.tensor(chunk_lens, dtype=torch.int64).cumsum(0) - 1
-        out = self.step(buf, cache.k_pool, cache.v_pool, cache.num_blocks, P,
-                        fused_attn=False, head_rows=last.to(dev))
+        dev = self.device
+        # Rows run in blocks of at most EXTEND_MAX_ROWS, in order: a block's
+        # layer-l attention reads the k/v that earlier blocks wrote at layer l,
+        # so this is chunked prefill over the packed rows.
+        outs = []
+        for r0 in range(0, R, EXTEND_MAX_ROWS):
+            r1 = min(R, r0 + EXTEND_MAX_ROWS)
+            Rb = r1 - r0
+            # the step buffers of the last shape are kept (a prompt batch often repeats it)
+            key = (Rb, W)
+            cached = getattr(self, "_extend_buf", None)
+            if cached is None or cached[0] != key:
+                self._extend_buf = None
+                self._extend_buf = (key, self.buffers(Rb, W, prefill=True))
+            buf = self._extend_buf[1]
+            buf.ids.copy_(ids_all[r0:r1])
+            buf.positions.copy_(pos_all[r0:r1])
+            buf.pages.copy_(pages_all[r0:r1])
+            buf.slots.copy_(slots_all[r0:r1])
+            buf.lens.copy_(lens_all[r0:r1])
+            buf.tables.copy_(tabs_all[r0:r1])
+            heads = last[(last >= r0) & (last < r1)] - r0
+            outs.append(self.step(buf, cache.k_pool, cache.v_pool, cache.num_blocks, P,
+                                  fused_attn=False, head_rows=heads.to(dev)))
         for v, n in zip(views, chunk_lens):
             for li in range(self.cfg.num_hidden_layers):
                 v._lens[li] = v._lens.get(li, 0) + n
-        return out.float()
+        return torch.cat(outs).float()
 
 
 def _dense_linear(w: torch.Tensor, dtype: torch.dtype) -> QLinear:
@@ -716,6 +733,8 @@ def _dense_linear(w: torch.Tensor, dtype: torch.dtype) -> QLinear:
 
 
 UNIT_PAGES = 4      # K3 split size the heuristic aims for (pages)
+EXTEND_MAX_ROWS = 8192    # prefill rows per launch sequence (K3's grid holds <= 65535)
+PREFILL_WS_BYTES = 256 << 20   # cap on a prefill launch's K3 split workspace
 SMALL_GRID_PAGES = 1024   # below this many (sequence, kv head, page) units: 1-page splits
 MAX_SPLITS = 64     # bound on K3 splits per (sequence, kv head)
 WIDE_GRID = 256     # (sequence, kv head) pairs that fill the CUs on their own ...
@@ -759,6 +778,7 @@ class StepBuffers:
     num_splits: int | None = None
     tilings: dict | None = None       # name -> requested Tiling (0 fields = planner)
     cfgs: dict = field(default_factory=dict)
+    prefill: bool = False             # prompt rows: no decode logits / lm_head workspace
 
     def __post_init__(self):
         m = self.model
@@ -768,6 +788,10 @@ class StepBuffers:
         nq, nkv, inter = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.intermediate_size
         if self.num_splits is None:
             self.num_splits = attention_splits(B, nkv, self.max_pages)
+            if self.prefill:
+                # one row per prompt token: bound the split workspace
+                cap = PREFILL_WS_BYTES // max(1, B * nq * (D + 2) * 4)
+                self.num_splits = max(1, min(self.num_splits, cap))
         lw = m.layers[0]
         tilings = self.tilings or {}
         self.swiglu = m.fused_swiglu(B)
@@ -820,8 +844,12 @@ class StepBuffers:
         self.part_gu = z(self.cfgs["gate_up"].ksplit, B, 2 * inter, dtype=f32)
         self.part_down = z(self.cfgs["down"].ksplit, B, H, dtype=f32)
         ks_lm = self.cfgs["lm_head"].ksplit
-        self.ws_lm = z(ks_lm, B, cfg.vocab_size, dtype=f32) if ks_lm > 1 else None
         S = self.num_splits
-        self.ws_acc = z(B * nq * S * D, dtype=f32)
-        self.ws_ml = z(2 * B * nq * S, dtype=f32)
-        self.logits = z(B, cfg.vocab_size, dtype=dt)
+        self.ws_acc = z(B * nq * S * D, dtype=f32) if S > 1 else None
+        self.ws_ml = z(2 * B * nq * S, dtype=f32) if S > 1 else None
+        if self.prefill:
+            # step(head_rows=...) computes the few logits it needs on its own
+            self.ws_lm = self.logits = None
+        else:
+            self.ws_lm = z(ks_lm, B, cfg.vocab_size, dtype=f32) if ks_lm > 1 else None
+            self.logits = z(B, cfg.vocab_size, dtype=dt)

@@ -46,10 +46,18 @@ def sample_batch(logits: torch.Tensor, temperature: torch.Tensor, top_k: torch.T
     token = torch.empty(B, dtype=torch.int64, device=dev) if token is None else token
     logprob = torch.empty(B, dtype=torch.float32, device=dev) if logprob is None else logprob
     status = torch.empty(B, dtype=torch.int32, device=dev) if status is None else status
-    assert temperature.dtype == torch.float32 and top_p.dtype == torch.float32
-    assert top_k.dtype == torch.int32 and uniform.dtype == torch.float32
+    # the kernel reads and writes element r of each of these for every row r < B
+    for name, t, dt in (("temperature", temperature, torch.float32),
+                        ("top_k", top_k, torch.int32), ("top_p", top_p, torch.float32),
+                        ("uniform", uniform, torch.float32), ("token", token, torch.int64),
+                        ("logprob", logprob, torch.float32), ("status", status, torch.int32)):
+        assert t.dtype == dt, f"sample_batch: {name} must be {dt}, got {t.dtype}"
+        assert t.device == dev, f"sample_batch: {name} is on {t.device}, logits on {dev}"
+        assert t.is_contiguous() and t.numel() >= B, \
+            f"sample_batch: {name} needs {B} contiguous elements, has {t.numel()}"
     if processed is not None:
         assert processed.shape == (B, V) and processed.dtype == torch.float32
+        assert processed.device == dev and processed.is_contiguous()
     rc = lib().acorn_sample(ptr(lg), B, V, dtype_code(lg), ptr(temperature), ptr(top_k),
                             ptr(top_p), ptr(uniform), ptr(token), ptr(logprob), ptr(processed),
                             ptr(status), stream_ptr(dev))

@@ -10,7 +10,6 @@ Modules:
   ops_ref     K1 / K2 / K3 / RMSNorm / RoPE and block-table restatements (torch CPU)
   quant_ref   W8 / W4 quantise, pack, dequant, GEMM references (numpy)
   sampler_ref temperature -> top-k -> top-p processing and inverse-CDF draw
-  pager_ref   block allocator + paged cache views (host logic, torch CPU)
   qwen3_ref   Qwen3 dense model: SDPA prefill/decode path and greedy loop
 
 How each function is pinned (golden vectors, known answers, closed forms,

@@ -111,6 +111,49 @@ class Qwen3Ref:
             h = h[:, -num_logits_to_keep:, :]
         return self._linear(h, "lm_head").float()
 
+    @torch.no_grad()
+    def decode_ragged(self, ids: list[int], caches: list) -> torch.Tensor:
+        """One decode step of B sequences whose caches hold different
+        lengths (Qwen3ForCausalLM.forward_decode, qwen3.py:520-595, batched
+        over per-sequence caches): the projections run on all B rows at once,
+        RoPE uses each row's own position (its cache length) and attention
+        reads each row's own cache, as `forward([[id]], cache_b)` does for one
+        sequence. Returns fp32 logits [B, vocab]; each cache grows by one.
+        Pinned against B separate `forward` calls (tests/test_oracle_model.py)."""
+        cfg = self.cfg
+        B = len(ids)
+        nq, nkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        eps = cfg.rms_norm_eps
+        pos = [0 if c[0][0] is None else c[0][0].shape[2] for c in caches]
+        rope = [self._rope(torch.tensor([p])) for p in pos]
+        h = self.w["embed_tokens.weight"][torch.tensor(ids)][:, None]          # [B, 1, H]
+        for i in range(cfg.num_hidden_layers):
+            p = f"layers.{i}."
+            a = f"layers.{i}.self_attn."
+            x = rmsnorm_ref(h, self.w[p + "input_layernorm.weight"], eps)
+            q = self._linear(x, a + "q_proj").view(B, 1, nq, D).transpose(1, 2)
+            k = self._linear(x, a + "k_proj").view(B, 1, nkv, D).transpose(1, 2)
+            v = self._linear(x, a + "v_proj").view(B, 1, nkv, D).transpose(1, 2)
+            q = rmsnorm_ref(q, self.w[a + "q_norm.weight"], eps)
+            k = rmsnorm_ref(k, self.w[a + "k_norm.weight"], eps)
+            outs = []
+            for b in range(B):
+                c, sn = rope[b][0][None, None], rope[b][1][None, None]
+                qb = q[b:b + 1] * c + self._rotate_half(q[b:b + 1]) * sn
+                kb = k[b:b + 1] * c + self._rotate_half(k[b:b + 1]) * sn
+                kc, vc = caches[b][i]
+                kb = kb if kc is None else torch.cat([kc, kb], dim=2)
+                vb = v[b:b + 1] if vc is None else torch.cat([vc, v[b:b + 1]], dim=2)
+                caches[b][i] = [kb, vb]
+                rep = nq // nkv
+                outs.append(F.scaled_dot_product_attention(
+                    qb, kb.repeat_interleave(rep, dim=1), vb.repeat_interleave(rep, dim=1)))
+            attn = torch.cat(outs).transpose(1, 2).reshape(B, 1, -1)
+            h = h + self._linear(attn, a + "o_proj")
+            h = h + self._mlp(i, rmsnorm_ref(h, self.w[p + "post_attention_layernorm.weight"], eps))
+        h = rmsnorm_ref(h, self.w["norm.weight"], eps)
+        return self._linear(h, "lm_head").float()[:, 0]
+
 
 @torch.no_grad()
 def generate_greedy(model: Qwen3Ref, prompt: list[int], max_new_tokens: int, *,

@@ -65,6 +65,40 @@ def test_file_uses_reference_names_and_packing(tmp_path):
     assert torch.equal(Q.unpack_w4(qw), u) and torch.equal(sc, s)
 
 
+@pytest.fixture(scope="module")
+def w4_file(tmp_path_factory):
+    _, _, m = _model("w4a16")
+    path = str(tmp_path_factory.mktemp("ckpt") / "w4.safetensors")
+    save_quantized(m, path)
+    return path
+
+
+@pytest.mark.parametrize("case", ["short_scales", "wrong_dtype", "missing", "group", "packing"])
+def test_load_rejects_a_file_that_does_not_match_its_config(case, w4_file, tmp_path):
+    """A file whose tensors or metadata disagree with its own config raises
+    ValueError on load instead of reaching the kernels."""
+    from safetensors import safe_open
+    from safetensors.torch import save_file
+    with safe_open(w4_file, framework="pt") as f:
+        meta = dict(f.metadata())
+        t = {k: f.get_tensor(k) for k in f.keys()}
+    name = "layers.1.mlp.down_proj"
+    if case == "short_scales":
+        t[name + ".scales"] = t[name + ".scales"][:, :-1].contiguous()
+    elif case == "wrong_dtype":
+        t[name + ".qweight"] = t[name + ".qweight"].to(torch.int8)
+    elif case == "missing":
+        del t["layers.0.self_attn.v_proj.scales"]
+    elif case == "group":
+        meta["group_size"] = "64"
+    else:
+        meta["packing"] = "uint8 [N, K/2], high nibble = even k"
+    bad = str(tmp_path / "bad.safetensors")
+    save_file(t, bad, metadata=meta)
+    with pytest.raises(ValueError):
+        load_quantized(bad, device="cpu")
+
+
 @pytest.mark.gpu
 def test_loaded_w4_model_decodes_identically_on_the_gpu(tmp_path):
     """The file loaded straight onto the GPU runs the decode step to the same

@@ -181,6 +181,39 @@ def test_baseline_config2_full_size():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("S", [64, 16, 1])
+def test_long_context_table_512(S):
+    """Configuration 5's contexts: B=8, lengths up to 8192 (one exactly 8192,
+    one 8191, one short), tables 512 pages wide over a 4608-block pool. S=64
+    is the split cap the decode step uses there (8-page splits, one-wave
+    workgroups), S=16 gives 32-page splits (the multi-wave form merged in
+    LDS), S=1 one split per sequence over up to 512 pages."""
+    from acorninfer_amd.ops.paged_attention import paged_decode_attention, plan_splits
+    g = torch.Generator().manual_seed(8192)
+    B, H, KV, D, P, W = 8, 32, 8, 128, 16, 512
+    lens = torch.randint(1024, 8193, (B,), generator=g, dtype=torch.int32)
+    lens[0], lens[1], lens[2] = 8192, 8191, 17
+    NB = int(sum(-(-int(n) // P) for n in lens)) + 64
+    perm = torch.randperm(NB, generator=g).to(torch.int32)
+    tables = torch.randint(0, NB, (B, W), generator=g, dtype=torch.int32)  # junk past the end
+    off = 0
+    for b in range(B):
+        n = -(-int(lens[b]) // P)
+        tables[b, :n] = perm[off:off + n]
+        off += n
+    kp = torch.randn(NB, P, KV, D, generator=g).bfloat16()
+    vp = torch.randn(NB, P, KV, D, generator=g).bfloat16()
+    q = (torch.randn(B, H, D, generator=g) * 2).bfloat16()
+    assert plan_splits(B, KV, W) == 64
+    ref = paged_attention_ref(q, kp, vp, tables, lens)
+    out = paged_decode_attention(q.cuda(), kp.cuda(), vp.cuda(), tables.cuda(), lens.cuda(), S)
+    torch.testing.assert_close(out.cpu(), ref, **TOL_BF16)
+    rel = ((out.cpu().double() - ref.double()).norm() / ref.double().norm()).item()
+    assert rel < 2e-2
+    print(f"\n[ctx<=8192 W=512 S={S} max|diff|={max_abs_diff(out, ref):.3g} rel={rel:.3g}]")
+
+
+@pytest.mark.gpu
 def test_deterministic_and_graph_replay():
     from acorninfer_amd.ops.paged_attention import paged_decode_attention
     q, kp, vp, tb, lens, S = next(_gen(torch.bfloat16, [(3, 32, 8, 128, 16, [513, 77, 1024], 8)]))

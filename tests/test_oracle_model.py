@@ -87,3 +87,36 @@ def test_generate_greedy_forced_stream_and_eos():
     # the chosen EOS is appended, then generation stops (generate.py:104-105)
     ids3, _ = generate_greedy(ref, prompt, 8, eos_ids=frozenset({ids[2]}))
     assert ids3 == ids[:3]
+
+
+def test_decode_ragged_equals_per_sequence_forward():
+    """The batched ragged decode step equals one forward([[id]], cache) per
+    sequence (different cache lengths, one empty), and grows each cache by one
+    token; a planted per-row position mistake (every row at position 0) is
+    caught."""
+    sd = _sd(seed=6)
+    ref = Qwen3Ref(CFG, sd, torch.float32)
+    g = torch.Generator().manual_seed(7)
+    hist = [5, 0, 17, 2]
+    caches, solo = [], []
+    for n in hist:
+        c, s = ref.new_cache(), ref.new_cache()
+        if n:
+            ids = torch.randint(0, CFG.vocab_size, (1, n), generator=g)
+            ref.forward(ids, c)
+            ref.forward(ids, s)
+        caches.append(c)
+        solo.append(s)
+    for step in range(3):
+        ids = torch.randint(0, CFG.vocab_size, (len(hist),), generator=g).tolist()
+        got = ref.decode_ragged(ids, caches)
+        want = torch.stack([ref.forward(torch.tensor([[t]]), s)[0, -1] for t, s in zip(ids, solo)])
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+    assert [c[0][0].shape[2] for c in caches] == [n + 3 for n in hist]
+    # planted mistake: the positions of every row forced to 0
+    bad = Qwen3Ref(CFG, sd, torch.float32)
+    bad._rope = lambda positions, f=bad._rope: f(torch.zeros_like(positions))
+    c2 = [[[x.clone() for x in layer] for layer in c] for c in caches]
+    ids = [1, 2, 3, 4]
+    assert not torch.allclose(bad.decode_ragged(ids, c2), ref.decode_ragged(ids, caches),
+                              rtol=1e-3, atol=1e-3)

@@ -71,12 +71,20 @@ def test_scatter_decode_bit_exact(dtype):
         for li in range(2):
             v._lens[li] = n
     targets = [v.ensure_append_capacity(1) for v in views]
-    pages = torch.tensor([p for p, _ in targets] + [10**6], device="cuda")  # last: outside pool
-    slots = torch.tensor([s for _, s in targets] + [0], device="cuda")
+    pages = torch.tensor([p for p, _ in targets], device="cuda")
+    slots = torch.tensor([s for _, s in targets], device="cuda")
     k = torch.randn(4, 8, 1, 128, device="cuda").to(dtype)
     v = torch.randn(4, 8, 1, 128, device="cuda").to(dtype)
     before_k = cache.k_pages[1].clone()
-    cache.scatter_decode(views + [PagedCacheView(cache)], 1, k, v, pages, slots)
+    # a target outside the pool is an IndexError, as the reference's indexing raises
+    with pytest.raises(IndexError):
+        cache.scatter_decode(views + [PagedCacheView(cache)], 1, k, v,
+                             torch.cat([pages, pages.new_tensor([10**6])]),
+                             torch.cat([slots, slots.new_tensor([0])]))
+    with pytest.raises(AssertionError):            # kv heads of another pool
+        cache.scatter_decode(views, 1, k[:3, :4], v[:3, :4], pages, slots)
+    assert torch.equal(cache.k_pages[1], before_k) and [vw._lens[1] for vw in views] == [5, 16, 33]
+    cache.scatter_decode(views, 1, k[:3], v[:3], pages, slots)
     want_k, want_v = before_k.clone(), cache.v_pages[1].clone() * 0
     for b, (p, s) in enumerate(targets):
         want_k[p, s] = k[b, :, 0]
@@ -84,3 +92,14 @@ def test_scatter_decode_bit_exact(dtype):
     assert torch.equal(cache.k_pages[1], want_k)
     assert torch.equal(cache.v_pages[1], want_v)
     assert [vw._lens[1] for vw in views] == [6, 17, 34]
+    # the kernel itself skips a row whose (page, slot) lies outside the pool
+    from acorninfer_amd._lib import dtype_code, lib, ptr, stream_ptr
+    kk = k[3:].reshape(1, 8, 128).contiguous()
+    for bad_page, bad_slot in ((10**6, 0), (-1, 0), (pages[0].item(), 16)):
+        pg = torch.tensor([bad_page], device="cuda")
+        sl = torch.tensor([bad_slot], device="cuda")
+        assert lib().acorn_kv_scatter(ptr(kk), ptr(kk), ptr(cache.k_pages[1]),
+                                      ptr(cache.v_pages[1]), ptr(pg), ptr(sl), 1, 8, 128, 16,
+                                      cache.num_blocks, dtype_code(kk), stream_ptr("cuda")) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(cache.k_pages[1], want_k) and torch.equal(cache.v_pages[1], want_v)

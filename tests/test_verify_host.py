@@ -93,6 +93,6 @@ def test_set_lens_is_rollback_only():
     view._lens[0] = 18
     view.set_lens(0, 16)
     assert view.seq_len == 16
-    with pytest.raises(ValueError, match="rollback-only"):
+    with pytest.raises(ValueError, match="only move a length back"):
         view.set_lens(0, 17)
     view.set_lens(0, 16)                               # same length is allowed
