@@ -24,7 +24,8 @@ F32, F16, BF16 = 0, 1, 2
 WFMT_BF16, WFMT_W8, WFMT_W4, WFMT_F32 = 0, 1, 2, 3
 
 OK = 0
-ERR_SHAPE, ERR_DTYPE, ERR_VALUE, ERR_UNSUPPORTED, ERR_HIP = -1, -2, -3, -4, -1000
+ERR_SHAPE, ERR_DTYPE, ERR_VALUE, ERR_UNSUPPORTED, ERR_SCRATCH, ERR_HIP = -1, -2, -3, -4, -5, -1000
+K3_SCRATCH_BYTES = 32 << 20     # ACORN_K3_SCRATCH_BYTES
 
 _DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -47,6 +48,8 @@ _SIGNATURES = {
                            _i64, _vp, _vp, _f32, _vp, _vp, _i32, _i32, _vp],
     "acorn_paged_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                               _i64, _i64, _i64, _i64, _f32, _i32, _vp],
+    "acorn_paged_attention_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                      _i64, _i64, _i64, _i64, _f32, _i32, _vp],
     "acorn_paged_attention_qkv": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                                   _vp, _vp, _f32, _vp, _vp, _i32, _i32, _vp],
@@ -102,6 +105,9 @@ def check(rc: int, op: str) -> None:
         raise ValueError(f"{op}: unsupported dtype")
     if rc == ERR_VALUE:
         raise ValueError(f"{op}: bad argument")
+    if rc == ERR_SCRATCH:
+        raise ValueError(f"{op}: the request needs more than the {K3_SCRATCH_BYTES >> 20} MiB "
+                         "of fixed device scratch of the allocation-free entry point")
     if rc == ERR_UNSUPPORTED:
         raise NotImplementedError(f"{op}: configuration not supported by the HIP kernels")
     if rc <= ERR_HIP:

@@ -21,6 +21,7 @@
 //    needed;
 //  * the next chunk's K/V are loaded before the current chunk is consumed;
 //  * scores live in the log2 domain (exp2), the workspace m is log2-domain.
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1217,6 +1218,80 @@ extern "C" int acorn_paged_attention(const void* q, const void* k_pages, const v
     case ACORN_BF16: return dispatch_d<__bf16>(D, rep, q, k_pages, v_pages, tables, seq_lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, table_stride, num_splits, scale, st);
   }
   return ACORN_ERR_DTYPE;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free K3: the split partials live in this file-scope array, one
+// copy per GPU, held until the process ends. Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol);
+// it passes the device address hipGetSymbolAddress returns, looked up once per
+// device with that device current and kept in g_scratch.
+constexpr size_t kScratchBytes = (size_t)ACORN_K3_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];
+
+// This device's copy of `scratch`, for a launch on `st`, which must belong
+// to the current device.
+int scratch_for(hipStream_t st, unsigned char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return ACORN_ERR_HIP - (int)e;
+  if (st != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(st, &sdev);
+    if (e != hipSuccess) return ACORN_ERR_HIP - (int)e;
+    if (sdev != dev) return ACORN_ERR_VALUE;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return ACORN_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return ACORN_ERR_HIP - (int)e;
+    g_scratch[dev] = p;
+  }
+  *out = (unsigned char*)g_scratch[dev];
+  return ACORN_OK;
+}
+
+}  // namespace
+
+extern "C" int acorn_paged_attention_noalloc(const void* q, const void* k_pages,
+                                             const void* v_pages, const int32_t* tables,
+                                             const int32_t* seq_lens, void* out, int64_t B,
+                                             int64_t H, int64_t KV, int64_t D, int64_t P,
+                                             int64_t num_blocks, int64_t table_stride,
+                                             int64_t num_splits, float scale, int dtype,
+                                             void* stream) {
+  // the shape contract of acorn_paged_attention, checked before the size
+  if (B < 0 || H <= 0 || KV <= 0 || D <= 0 || P <= 0 || num_blocks <= 0 || num_splits < 1 ||
+      table_stride < 1)
+    return ACORN_ERR_SHAPE;
+  if (num_splits > 65535 || KV > 65535 || B > 65535 || H > 65535 || D > 65535)
+    return ACORN_ERR_SHAPE;
+  if (B == 0) return ACORN_OK;
+  float* ws_acc = nullptr;
+  float* ws_ml = nullptr;
+  if (num_splits > 1) {
+    // partials [B*H*S*D] fp32, then m|l [2*B*H*S] fp32 (each B, H, S, D
+    // < 2^16, so the products fit in 64 bits)
+    const size_t rows = (size_t)B * (size_t)H * (size_t)num_splits;
+    const size_t acc_bytes = (rows * (size_t)D * 4 + 255) / 256 * 256;
+    if (acc_bytes + rows * 8 > kScratchBytes) return ACORN_ERR_SCRATCH;
+    unsigned char* base = nullptr;
+    const int rc = scratch_for((hipStream_t)stream, &base);
+    if (rc != ACORN_OK) return rc;
+    ws_acc = (float*)base;
+    ws_ml = (float*)(base + acc_bytes);
+  }
+  return acorn_paged_attention(q, k_pages, v_pages, tables, seq_lens, out, ws_acc, ws_ml, B, H,
+                               KV, D, P, num_blocks, table_stride, num_splits, scale, dtype,
+                               stream);
 }
 
 extern "C" int acorn_paged_attention_qkv_supported(int64_t H, int64_t KV, int64_t D, int64_t P,

@@ -42,7 +42,12 @@ extern "C" {
 #define ACORN_ERR_DTYPE (-2)       /* unsupported dtype combination */
 #define ACORN_ERR_VALUE (-3)       /* bad argument value (reference: ValueError) */
 #define ACORN_ERR_UNSUPPORTED (-4) /* configuration not built (reference: NotImplementedError) */
+#define ACORN_ERR_SCRATCH (-5)     /* request exceeds the fixed scratch of an allocation-free
+                                      entry point */
 #define ACORN_ERR_HIP (-1000)      /* ACORN_ERR_HIP - hipError_t */
+
+/* Size of the fixed device scratch of acorn_paged_attention_noalloc (bytes). */
+#define ACORN_K3_SCRATCH_BYTES (32 << 20)
 
 /* Library version, bumped when an entry point changes meaning. */
 int acorn_version(void);
@@ -129,6 +134,29 @@ int acorn_paged_attention(const void* q, const void* k_pages, const void* v_page
                           float* ws_acc, float* ws_ml, int64_t B, int64_t H, int64_t KV,
                           int64_t D, int64_t P, int64_t num_blocks, int64_t table_stride,
                           int64_t num_splits, float scale, int dtype, void* stream);
+
+/*
+ * acorn_paged_attention with no workspace arguments, for callers that cannot
+ * allocate device memory (code under hipGraph capture, serving loops and
+ * harnesses that forbid hipMalloc). No counterpart in the reference.
+ * Arguments and results are those of acorn_paged_attention (the same kernels,
+ * the same bits). The split partials (B*H*num_splits*(D+2) fp32 values, the
+ * first part rounded up to 256 bytes) live in a static device array of
+ * ACORN_K3_SCRATCH_BYTES per GPU, held until the process ends; a larger
+ * request returns ACORN_ERR_SCRATCH and launches nothing (num_splits == 1
+ * needs none). Nothing in the scratch has to start at zero: every partial the
+ * combine reads is written by the same call. The array is looked up once per
+ * device, on the first call with that device current (make that call outside
+ * graph capture); `stream` must belong to the current device
+ * (ACORN_ERR_VALUE otherwise). Calls that overlap on one GPU (concurrent
+ * streams, or graphs replayed concurrently) share the array and race.
+ * It calls no hipMalloc, hipFree or other allocating routine.
+ */
+int acorn_paged_attention_noalloc(const void* q, const void* k_pages, const void* v_pages,
+                                  const int32_t* tables, const int32_t* seq_lens, void* out,
+                                  int64_t B, int64_t H, int64_t KV, int64_t D, int64_t P,
+                                  int64_t num_blocks, int64_t table_stride, int64_t num_splits,
+                                  float scale, int dtype, void* stream);
 
 /*
  * Decode-step fusion of acorn_qkv_epilogue with K3: the attention kernel
