@@ -1,0 +1,121 @@
+// Device helpers shared by the weight-only GEMM kernels (quant_gemm.hip and
+// w4_decode.hip), the W4B block-layout index maps, and the interface of the
+// int4 decode kernel that quant_gemm.hip's planner dispatches to.
+#pragma once
+
+#include "common.h"
+
+namespace acorn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// int4: 8 nibbles (columns c..c+7) -> bf16 (128+u) in MFMA item order
+// (p, p+4) per dword.
+// The mask and the bias are made opaque register values (an SGPR and a VGPR):
+// with literal operands the compiler emits v_and_b32 + v_or_b32 (gfx950's
+// VOP3 forms take no literal), with registers it can use one v_and_or_b32.
+__device__ __forceinline__ u32x4 unpack_w4(uint32_t w) {
+  uint32_t m = 0x000F000Fu, c = 0x43004300u;
+  asm("" : "+s"(m));
+  asm("" : "+v"(c));
+  u32x4 r;
+  r[0] = (w & m) | c;
+  r[1] = ((w >> 4) & m) | c;
+  r[2] = ((w >> 8) & m) | c;
+  r[3] = ((w >> 12) & m) | c;
+  return r;
+}
+
+// x staged for the int4 kernels: the 8 bf16 of a 16-byte piece reordered to
+// [x0,x4,x1,x5,x2,x6,x3,x7], unpack_w4's pairing of the nibbles of a dword.
+__device__ __forceinline__ u32x4 w4_order_x(u32x4 w) {
+  u32x4 t;
+  t[0] = __builtin_amdgcn_perm(w[2], w[0], 0x05040100u);
+  t[1] = __builtin_amdgcn_perm(w[2], w[0], 0x07060302u);
+  t[2] = __builtin_amdgcn_perm(w[3], w[1], 0x05040100u);
+  t[3] = __builtin_amdgcn_perm(w[3], w[1], 0x07060302u);
+  return t;
+}
+
+// NDW consecutive dwords from a 4*NDW-byte aligned address (one vector load
+// per 16 bytes).
+template <int NDW>
+__device__ __forceinline__ void load_dwords(const void* p, uint32_t (&d)[NDW]) {
+  if constexpr (NDW == 1) {
+    d[0] = *(const uint32_t*)p;
+  } else if constexpr (NDW == 2) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 t = *(const u32x2*)p;
+    d[0] = t[0];
+    d[1] = t[1];
+  } else {
+    static_assert(NDW % 4 == 0, "whole 16-byte pieces");
+#pragma unroll
+    for (int c = 0; c < NDW / 4; ++c) {
+      const u32x4 t = *(const u32x4*)((const uint32_t*)p + 4 * c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[4 * c + j] = t[j];
+    }
+  }
+}
+
+// fp16 number h of a run of packed halves, as float; used as an FMA operand
+// the conversion folds into v_fma_mix_f32's operand select.
+template <int NDW>
+__device__ __forceinline__ float half_f(const uint32_t (&d)[NDW], int h) {
+  return (float)__builtin_bit_cast(h16x2, d[h / 2])[h & 1];
+}
+
+// SwiGLU epilogue of the fused gate|up projection: g, u rounded to bf16,
+// act = round(round(silu(g)) * u), silu(g) = g / (1 + exp(-g)) in fp32
+// (models/qwen3.py:392-396, each torch bf16 op rounded).
+__device__ __forceinline__ float swiglu_bf16(float g, float u) {
+#pragma clang fp contract(off)
+  g = (float)(__bf16)g;
+  u = (float)(__bf16)u;
+  const float sg = (float)(__bf16)(g / (1.0f + expf(-g)));
+  return sg * u;
+}
+
+// ---- W4B: int4 weights in 1 KB blocks (ACORN_WFMT_W4B) -------------------
+// Block (n/16, g) holds rows 16*(n/16) .. +15 x the 128 k of group g as one
+// wave's MFMA A operand: lane (c%4)*16 + n%16 has the 16 bytes of row n,
+// k in [32c, 32c+32) (c = k/32 within the tensor, natural nibble order).
+__host__ __device__ inline size_t w4b_chunk_offset(int64_t n, int64_t c, int64_t K) {
+  return ((size_t)(n / 16) * (size_t)(K / 128) + (size_t)(c / 4)) * 1024 +
+         (size_t)((c % 4) * 16 + n % 16) * 16;
+}
+// Scale (zero) of row n, group g: records of 4 rows x 4 groups per lane
+// group, so a lane's scales of consecutive groups are contiguous.
+__host__ __device__ inline size_t w4b_half_index(int64_t n, int64_t g, int64_t K) {
+  return ((size_t)(n / 16) * (size_t)(K / 512) + (size_t)(g / 4)) * 64 +
+         (size_t)((n % 16) / 4) * 16 + (size_t)(g % 4) * 4 + (size_t)(n % 4);
+}
+
+// ---- the W4B decode kernel (w4_decode.hip) ----------------------------------
+// cfg knobs: rt (row tiles of 16 per wave), upw (groups per pipeline stage),
+// nw (waves per workgroup, each with its own rt tiles), ksplit, depth
+// (stages in flight per wave); 0 = choose.
+struct W4bPlan {
+  int rt, upw, nw, ksplit, depth;
+  int R;           // x rows staged in LDS (power of 2 >= M)
+  int groups;      // workgroups along N
+  size_t lds;      // dynamic LDS bytes
+  bool swiglu;
+};
+int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4bPlan* p);
+// out (bf16 [M,N], or act [M,N/2] for swiglu) when given and ksplit == 1;
+// otherwise fp32 partials part[ksplit, M, N].
+int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale,
+               const void* zero, void* out, float* part, int64_t M, int64_t N, int64_t K,
+               hipStream_t st);
+
+}  // namespace acorn

@@ -43,15 +43,11 @@
 //    XCD's whole L2.
 #include <algorithm>
 
-#include "common.h"
+#include "gemm_common.h"
 
 using namespace acorn;
 
 namespace {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int WFMT> struct Fmt;
 template <> struct Fmt<ACORN_WFMT_BF16> {
@@ -66,27 +62,8 @@ template <> struct Fmt<ACORN_WFMT_W4> {
   static constexpr int KU = 128, MPU = 4, BPK_NUM = 1, BPK_DEN = 2;
 };
 
-__device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-// int4: 8 nibbles (columns c..c+7) -> bf16 (128+u) in MFMA item order
-// (p, p+4) per dword.
-// The mask and the bias are made opaque register values (an SGPR and a VGPR):
-// with literal operands the compiler emits v_and_b32 + v_or_b32 (gfx950's
-// VOP3 forms take no literal), with registers it can use one v_and_or_b32.
-__device__ __forceinline__ u32x4 unpack_w4(uint32_t w) {
-  uint32_t m = 0x000F000Fu, c = 0x43004300u;
-  asm("" : "+s"(m));
-  asm("" : "+v"(c));
-  u32x4 r;
-  r[0] = (w & m) | c;
-  r[1] = ((w >> 4) & m) | c;
-  r[2] = ((w >> 8) & m) | c;
-  r[3] = ((w >> 12) & m) | c;
-  return r;
-}
+// int4 in either layout (natural rows, or the 1 KB blocks of W4B)
+template <int WFMT> constexpr bool kIsW4 = WFMT == ACORN_WFMT_W4 || WFMT == ACORN_WFMT_W4B;
 
 // Byte I of v as float (selects v_cvt_f32_ubyteI).
 template <int I> __device__ __forceinline__ float ubyte_f32(uint32_t v) {
@@ -103,28 +80,6 @@ __device__ __forceinline__ u32x4 unpack_w8(uint32_t lo, uint32_t hi) {
   r[2] = pack_bf16x2(ubyte_f32<0>(hi), ubyte_f32<1>(hi));
   r[3] = pack_bf16x2(ubyte_f32<2>(hi), ubyte_f32<3>(hi));
   return r;
-}
-
-// NDW consecutive dwords from a 4*NDW-byte aligned address (one vector load
-// per 16 bytes).
-template <int NDW>
-__device__ __forceinline__ void load_dwords(const void* p, uint32_t (&d)[NDW]) {
-  if constexpr (NDW == 1) {
-    d[0] = *(const uint32_t*)p;
-  } else if constexpr (NDW == 2) {
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    const u32x2 t = *(const u32x2*)p;
-    d[0] = t[0];
-    d[1] = t[1];
-  } else {
-    static_assert(NDW % 4 == 0, "whole 16-byte pieces");
-#pragma unroll
-    for (int c = 0; c < NDW / 4; ++c) {
-      const u32x4 t = *(const u32x4*)((const uint32_t*)p + 4 * c);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) d[4 * c + j] = t[j];
-    }
-  }
 }
 
 // fp16 number u of a run of packed halves (even u in the low half).
@@ -161,17 +116,6 @@ struct KArgs {
   int ksplit;
   int log2R;       // LDS rows per m tile = 1 << log2R
 };
-
-// SwiGLU epilogue of the fused gate|up projection: g, u rounded to bf16,
-// act = round(round(silu(g)) * u), silu(g) = g / (1 + exp(-g)) in fp32
-// (models/qwen3.py:392-396, each torch bf16 op rounded).
-__device__ __forceinline__ float swiglu_bf16(float g, float u) {
-#pragma clang fp contract(off)
-  g = (float)(__bf16)g;
-  u = (float)(__bf16)u;
-  const float sg = (float)(__bf16)(g / (1.0f + expf(-g)));
-  return sg * u;
-}
 
 // Grid: x = tile groups, y = ksplit, z = m blocks of 16*MT rows.
 // SWIGLU: RT == 2, the tile's first 16 weight rows are gate rows and the next
@@ -382,15 +326,7 @@ __global__ __launch_bounds__(NW * kWave, NW == 8 ? 2 : 3) void wgemm_kernel(KArg
   auto x_store = [&](int p, u32x4 w) {
     const int c = p % CPR, rr = p / CPR;
     const int mt = rr / R, row = rr % R;
-    if constexpr (WFMT == ACORN_WFMT_W4) {
-      // items [x0,x4,x1,x5,x2,x6,x3,x7] to match unpack_w4's pairing
-      u32x4 t;
-      t[0] = __builtin_amdgcn_perm(w[2], w[0], 0x05040100u);
-      t[1] = __builtin_amdgcn_perm(w[2], w[0], 0x07060302u);
-      t[2] = __builtin_amdgcn_perm(w[3], w[1], 0x05040100u);
-      t[3] = __builtin_amdgcn_perm(w[3], w[1], 0x07060302u);
-      w = t;
-    }
+    if constexpr (WFMT == ACORN_WFMT_W4) w = w4_order_x(w);
     xs[((size_t)mt * CPR + c) * R + row] = w;
   };
   u32x4 xv[XB];
@@ -539,7 +475,7 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
   constexpr int CPR = BK / 8;                         // 16-byte x chunks per row per step
   constexpr int XR = BM * CPR / 256;                  // 16-byte x loads per thread per step
   constexpr int TPR = 256 / BN;                       // threads per weight row
-  constexpr int WR = WFMT == ACORN_WFMT_W4 ? 1 : WFMT == ACORN_WFMT_W8 ? 2 : 4;
+  constexpr int WR = kIsW4<WFMT> ? 1 : WFMT == ACORN_WFMT_W8 ? 2 : 4;
   static_assert(XR >= 1 && MB >= 1 && NB >= 1 && BK / TPR == 32, "unsupported tile");
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* xs = (__bf16*)smem;                         // [2][BM][KP]
@@ -582,14 +518,16 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
   };
   // int4: the tile's group scales (and zeros) for this K range, loaded once
   const int G = kper / 128;
-  if constexpr (WFMT == ACORN_WFMT_W4) {
+  if constexpr (kIsW4<WFMT>) {
     // eight independent loads in flight per thread per round
     for (int i0 = 0; i0 < BN * G; i0 += 256 * 8) {
       _Float16 sv[8], zv[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int i = min(i0 + tid + 256 * u, BN * G - 1);
-        const size_t gi = (size_t)(n0 + i / G) * (K / 128) + kb / 128 + i % G;
+        const int n = n0 + i / G, g = kb / 128 + i % G;
+        const size_t gi = WFMT == ACORN_WFMT_W4B ? w4b_half_index(n, g, K)
+                                                 : (size_t)n * (K / 128) + g;
         sv[u] = a.scale[gi];
         zv[u] = a.zero ? a.zero[gi] : (_Float16)0.f;
       }
@@ -616,7 +554,10 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
       xr[j] = *(const u32x4*)(a.x + (size_t)m * K + k0 + 8 * ch);
     }
     const size_t wk = (size_t)(n0 + wrow) * K + k0 + 32 * wpart;   // weight element index
-    if constexpr (WFMT == ACORN_WFMT_W4) {
+    if constexpr (WFMT == ACORN_WFMT_W4B) {
+      // the same 16 bytes (row n, 32-k chunk c) in the 1 KB block layout
+      wr[0] = *(const u32x4*)(a.w + w4b_chunk_offset(n0 + wrow, (k0 + 32 * wpart) / 32, K));
+    } else if constexpr (WFMT == ACORN_WFMT_W4) {
       wr[0] = *(const u32x4*)(a.w + wk / 2);
     } else if constexpr (WFMT == ACORN_WFMT_W8) {
 #pragma unroll
@@ -640,7 +581,7 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
       *(u32x4*)(xd + row * KP + 8 * ch) = xr[j];
     }
     __bf16* wd = wsm + (s & 1) * BN * KP + wrow * KP + 32 * wpart;
-    if constexpr (WFMT == ACORN_WFMT_W4) {
+    if constexpr (kIsW4<WFMT>) {
       const int g = (min(s, nsteps - 1) * BK + 32 * wpart) / 128;
       const float gs = (float)gsl[wrow * G + g];
       const float gz = a.zero ? (float)gsl[BN * G + wrow * G + g] : -8.f * gs;
@@ -753,7 +694,8 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
 size_t tile_lds_bytes(int wfmt, int bm, int bn, int64_t kper) {
   const int kp = kTileKN / bn + 8;
   size_t b = (size_t)2 * (bm + bn) * kp * 2;
-  if (wfmt == ACORN_WFMT_W4) b += (size_t)2 * bn * (kper / 128) * 2;  // scales + zeros
+  if (wfmt == ACORN_WFMT_W4 || wfmt == ACORN_WFMT_W4B)
+    b += (size_t)2 * bn * (kper / 128) * 2;  // scales + zeros
   return b;
 }
 
@@ -775,7 +717,9 @@ struct Tiling {
   int mt, R, nk, ntiles, mblocks, groups;
   size_t lds;
   int swiglu;                    // fused SwiGLU epilogue (rt == 2, ksplit == 1)
-  int kind;                      // 0 = streaming kernel, 1 = tiled kernel (rt == 0, upw = BM)
+  int kind;                      // 0 = streaming kernel, 1 = tiled kernel (rt == 0, upw = BM),
+                                 // 2 = W4B decode kernel (tpw = its pipeline depth)
+  W4bPlan w4b;
 };
 
 int ilog2_ceil(int v) {
@@ -818,7 +762,8 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
   const int bn = (req_bn == 64 || req_bn == 128) ? req_bn : M <= 64 ? 64 : 128;
   if (N % bn) return ACORN_ERR_UNSUPPORTED;
   const int bk = kTileKN / bn;
-  const int align = wfmt == ACORN_WFMT_W4 ? std::max(128, bk) : bk;
+  const int align = (wfmt == ACORN_WFMT_W4 || wfmt == ACORN_WFMT_W4B) ? std::max(128, bk) : bk;
+  if (wfmt == ACORN_WFMT_W4B && (K % 512 || N % 16)) return ACORN_ERR_SHAPE;
   if (K % align) return ACORN_ERR_SHAPE;
   const int bm = (req_bm == 32 || req_bm == 64 || req_bm == 128) ? req_bm
                  : M <= 32 ? 32 : M <= 64 ? 64 : 128;
@@ -842,7 +787,8 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
   } else {
     ks = 1;
     const int64_t tiles = (int64_t)t->ntiles * t->mblocks;
-    const double wbytes = (double)N * K * (wfmt == ACORN_WFMT_W4 ? 0.5 : wfmt == ACORN_WFMT_W8 ? 1 : 2);
+    const double wbytes = (double)N * K * ((wfmt == ACORN_WFMT_W4 || wfmt == ACORN_WFMT_W4B) ? 0.5
+                                           : wfmt == ACORN_WFMT_W8 ? 1 : 2);
     while (tiles * ks < 2 * kCUs) {
       int64_t nx = ks + 1;
       while (nx <= units && units % nx) ++nx;
@@ -871,6 +817,26 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   if (M <= 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   t->swiglu = swiglu;
   t->kind = 0;
+  if (wfmt == ACORN_WFMT_W4B && M <= 16 && !(cfg && cfg[0] == 0 && cfg[1] >= 32)) {
+    // decode sizes in the block layout: the W4B decode kernel
+    const int rc = w4b_make_plan(M, N, K, cfg, swiglu, &t->w4b);
+    if (rc) return rc;
+    t->kind = 2;
+    t->rt = t->w4b.rt;
+    t->upw = t->w4b.upw;
+    t->nw = t->w4b.nw;
+    t->ksplit = t->w4b.ksplit;
+    t->tpw = t->w4b.depth;
+    t->mt = 1;
+    t->R = t->w4b.R;
+    t->ntiles = (int)(N / 16);
+    t->mblocks = 1;
+    t->groups = t->w4b.groups;
+    t->lds = t->w4b.lds;
+    return ACORN_OK;
+  }
+  if (wfmt == ACORN_WFMT_W4B && (swiglu || (cfg && cfg[0] > 0)))
+    return ACORN_ERR_UNSUPPORTED;  // M > 16 in the block layout: the tiled kernel only
   // the tiled kernel: the default for M > 16; for M <= 16 on request (rt 0
   // with an M tile of 32 or more in upw)
   if (!swiglu && ((M > 16 && (!cfg || cfg[0] <= 0)) || (cfg && cfg[0] == 0 && cfg[1] >= 32)))
@@ -1076,7 +1042,8 @@ int dispatch_tiled(const Tiling& t, const KArgs& a, hipStream_t st) {
 
 int plan_entry(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg, bool swiglu) {
   if (!cfg) return ACORN_ERR_VALUE;
-  if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4)
+  if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
+      wfmt != ACORN_WFMT_W4B)
     return ACORN_ERR_DTYPE;
   Tiling t;
   const int rc = make_plan(M, N, K, wfmt, cfg, &t, swiglu);
@@ -1115,11 +1082,15 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
   a.tpw = t.tpw;
   a.ksplit = t.ksplit;
   a.log2R = ilog2_ceil(t.R);
-  if (t.kind == 1) {
+  if (t.kind == 2) {
+    rc = w4b_launch(t.w4b, x, w, scale, zero, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K,
+                    st);
+  } else if (t.kind == 1) {
     switch (wfmt) {
       case ACORN_WFMT_BF16: rc = dispatch_tiled<ACORN_WFMT_BF16>(t, a, st); break;
       case ACORN_WFMT_W8: rc = dispatch_tiled<ACORN_WFMT_W8>(t, a, st); break;
       case ACORN_WFMT_W4: rc = dispatch_tiled<ACORN_WFMT_W4>(t, a, st); break;
+      case ACORN_WFMT_W4B: rc = dispatch_tiled<ACORN_WFMT_W4B>(t, a, st); break;
     }
   } else {
     switch (wfmt) {
@@ -1158,7 +1129,7 @@ extern "C" int acorn_quant_gemm(const void* x, const void* w, const void* scale,
                                 const void* zero, void* out_bf16, float* part, int64_t M,
                                 int64_t N, int64_t K, int wfmt, const int* cfg, void* stream) {
   if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
-      wfmt != ACORN_WFMT_F32)
+      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_F32)
     return ACORN_ERR_DTYPE;
   if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   if (M == 0) return ACORN_OK;
@@ -1181,7 +1152,8 @@ extern "C" int acorn_quant_gemm(const void* x, const void* w, const void* scale,
 extern "C" int acorn_quant_gemm_swiglu(const void* x, const void* w, const void* scale,
                                        const void* zero, void* act, int64_t M, int64_t N,
                                        int64_t K, int wfmt, const int* cfg, void* stream) {
-  if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4)
+  if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
+      wfmt != ACORN_WFMT_W4B)
     return ACORN_ERR_DTYPE;
   if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   if (M == 0) return ACORN_OK;

@@ -1,0 +1,348 @@
+// Weight-only int4 GEMM at decode sizes (M <= 16) over the W4B block layout.
+//
+// y[M,N] = x[M,K] @ ((u - 8) * s)^T: u the stored nibble (symmetric int4
+// v = u - 8, the reference's m7 spike format with zero = -8 s,
+// scripts/m7_spike.py:152-231), s fp16 per (row, 128-k group), bf16 x,
+// fp32 accumulation.
+//
+// Built for the gfx950 memory path:
+//  * The weights of 16 rows x 128 k (one group) are one contiguous 1 KB block
+//    in MFMA A-operand order (ACORN_WFMT_W4B). A wave reads a block with one
+//    16-byte load per lane (whole cache lines, non-temporal policy) and feeds
+//    four v_mfma_f32_16x16x32_bf16 from it; no data moves between lanes.
+//  * int4 -> bf16 (128 + u): one v_and_or_b32 per bf16 pair, plus a shift for
+//    three of the four pairs of a dword. The k pairing this implies is applied
+//    to x once, when x is staged in LDS.
+//  * Per group: y += s * (C - 136 X), C the group's MFMA sum over the biased
+//    weights and X the sum of x over the group (one MFMA against ones per
+//    group, once per workgroup): two VALU per output row and group; the fp16
+//    scale is read from its packed pair by v_fma_mix_f32.
+//  * The waves of a workgroup share the staged x and each owns RT row tiles
+//    over the workgroup's whole K range, so nothing is reduced across waves:
+//    after the staging barrier a wave only streams, computes and stores.
+//  * Each wave keeps DEPTH stages (UPW groups x RT row tiles) of loads in
+//    flight. Every load is unconditional and the stage count is a multiple
+//    of DEPTH, so the compiler's wait counts are static.
+//  * Split-K (ksplit > 1) writes fp32 partials [ksplit, M, N], summed in split
+//    order by the consumer (bitwise deterministic).
+#include "gemm_common.h"
+
+using namespace acorn;
+
+namespace {
+
+struct W4bArgs {
+  const __bf16* x;
+  const uint8_t* w;
+  const _Float16* scale;
+  __bf16* out;    // bf16 [M, N] (act [M, N/2] with SWIGLU) when ksplit == 1
+  float* part;    // fp32 [ksplit, M, N] otherwise
+  int M, N, K;
+  int kr;         // K range of a workgroup (a multiple of 128 * UPW * DEPTH)
+  int log2R;      // x rows staged = 1 << log2R >= M
+};
+
+template <int RT, int UPW>
+struct Stage {
+  u32x4 w[RT][UPW];          // unit (rt, u): this lane's 16 bytes of block (tile, group)
+  uint32_t s[RT][2 * UPW];   // fp16 scales: half 4u + i is row 4*lg + i of group u
+};
+
+// Grid: x = groups of NW*RT row tiles, y = ksplit. Block: NW waves.
+template <int RT, int UPW, int DEPTH, int NW, bool SWIGLU>
+__global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
+  constexpr int NT = NW * kWave;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lg = lane >> 4, lr = lane & 15;
+  const int R = 1 << a.log2R;
+  const int KR = a.kr, kr0 = blockIdx.y * KR;
+  const int GR = KR / 128, CPR = KR / 8;
+  const int G = a.K / 128, G4 = a.K / 512;
+  const int t0 = (blockIdx.x * NW + wid) * RT;   // this wave's first row tile
+  const bool active = t0 < a.N / 16;              // (N / 16) % RT == 0 by the plan
+  const int tt = active ? t0 : 0;                 // idle waves read tile 0, store nothing
+  // LDS: x pieces [CPR][R] (16 bytes each, W4 k order) | group sums [GR][16]
+  u32x4* xs = (u32x4*)smem;
+  float* xgs = (float*)(smem + (size_t)CPR * R * 16);
+
+  const int ns = GR / UPW;                        // stages of this wave
+  const uint8_t* wb = a.w + ((size_t)tt * G + kr0 / 128) * 1024 + lane * 16;
+  auto load = [&](int s, Stage<RT, UPW>& r) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int u = 0; u < UPW; ++u)
+        r.w[rt][u] = load_nt((const u32x4*)(wb + ((size_t)rt * G + s * UPW + u) * 1024));
+    const int g = kr0 / 128 + s * UPW;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+      load_dwords(a.scale + ((((size_t)(tt + rt) * G4 + g / 4) * 4 + lg) * 16 + (g % 4) * 4),
+                  r.s[rt]);
+  };
+
+  // ---- the first DEPTH stages, then x ---------------------------------------
+  Stage<RT, UPW> ring[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+
+  // x [M, kr0 .. kr0+KR) into LDS: piece p = c * R + row (consecutive threads
+  // write consecutive 16 bytes); rows past M re-read row M-1 (their slots
+  // feed only output columns that are never stored).
+  constexpr int XB = 8;
+  const int xtotal = R * CPR;
+  for (int p0 = threadIdx.x; p0 < xtotal; p0 += NT * XB) {
+    u32x4 xv[XB];
+#pragma unroll
+    for (int u = 0; u < XB; ++u) {
+      const int p = min(p0 + u * NT, xtotal - 1);
+      const int m = min(p & (R - 1), a.M - 1), c = p >> a.log2R;
+      xv[u] = *(const u32x4*)(a.x + (size_t)m * a.K + kr0 + c * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < XB; ++u)
+      if (p0 + u * NT < xtotal) xs[p0 + u * NT] = w4_order_x(xv[u]);
+  }
+  __syncthreads();
+  // X per (group, column): an MFMA of ones against the group's x
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  const int xrow = lr & (R - 1);
+  for (int g = wid; g < GR; g += NW) {
+    f32x4 xg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xg = mfma(ones, xs[(g * 16 + 4 * lg + j) * R + xrow], xg);
+    if (lg == 0) xgs[g * 16 + lr] = xg[0];
+  }
+  __syncthreads();
+  if (!active) return;
+
+  // ---- stream ------------------------------------------------------------------
+  f32x4 acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const Stage<RT, UPW>& r, int s) {
+#pragma unroll
+    for (int u = 0; u < UPW; ++u) {
+      const int gl = s * UPW + u;
+      const u32x4* xp = xs + (gl * 16 + 4 * lg) * R + xrow;
+      u32x4 b[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = xp[j * R];
+      const float xg = xgs[gl * 16 + lr];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        f32x4 cc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cc = mfma(unpack_w4(r.w[rt][u][j]), b[j], cc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[rt][i] = __builtin_fmaf(half_f(r.s[rt], 4 * u + i),
+                                      __builtin_fmaf(xg, -136.f, cc[i]), acc[rt][i]);
+      }
+    }
+  };
+  int s0 = 0;
+  for (; s0 + DEPTH < ns; s0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      compute(ring[d], s0 + d);
+      load(s0 + DEPTH + d, ring[d]);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) compute(ring[d], s0 + d);
+
+  // ---- store: lane (lr, lg) holds rows 4*lg .. 4*lg+3 of column lr ------------
+  const int m = lr;
+  if (m >= a.M) return;
+  if constexpr (SWIGLU) {
+    // tiles 2j (gate) and 2j+1 (up) hold the 16 outputs of block j
+    const int NA = a.N / 2;
+#pragma unroll
+    for (int p = 0; p < RT / 2; ++p) {
+      const int n = (t0 / 2 + p) * 16 + 4 * lg;
+      uint32_t v[2];
+      v[0] = pack_bf16x2(swiglu_bf16(acc[2 * p][0], acc[2 * p + 1][0]),
+                         swiglu_bf16(acc[2 * p][1], acc[2 * p + 1][1]));
+      v[1] = pack_bf16x2(swiglu_bf16(acc[2 * p][2], acc[2 * p + 1][2]),
+                         swiglu_bf16(acc[2 * p][3], acc[2 * p + 1][3]));
+      __builtin_memcpy(a.out + (size_t)m * NA + n, v, sizeof(v));
+    }
+  } else if (a.out) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int n = (t0 + rt) * 16 + 4 * lg;
+      uint32_t v[2] = {pack_bf16x2(acc[rt][0], acc[rt][1]), pack_bf16x2(acc[rt][2], acc[rt][3])};
+      __builtin_memcpy(a.out + (size_t)m * a.N + n, v, sizeof(v));
+    }
+  } else {
+    float* dst = a.part + ((size_t)blockIdx.y * a.M + m) * a.N;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) *(f32x4*)(dst + (t0 + rt) * 16 + 4 * lg) = acc[rt];
+  }
+}
+
+size_t w4b_lds(int R, int64_t kr) { return (size_t)kr * R * 2 + (size_t)(kr / 128) * 64; }
+
+template <int RT, int UPW, int DEPTH, int NW>
+int launch4(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
+  auto kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, false>;
+  int variant = 0;
+  if constexpr (RT >= 2) {
+    if (p.swiglu) {
+      kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, true>;
+      variant = 1;
+    }
+  }
+  static bool raised[2] = {false, false};  // once per kernel, before any graph capture
+  if (!raised[variant] && p.lds > 64 * 1024) {
+    (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    raised[variant] = true;
+  }
+  dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(NW * kWave);
+  kfn<<<grid, block, p.lds, st>>>(a);
+  return ACORN_OK;
+}
+
+template <int RT, int UPW, int DEPTH>
+int launch3(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
+  switch (p.nw) {
+    case 2: return launch4<RT, UPW, DEPTH, 2>(p, a, st);
+    case 4: return launch4<RT, UPW, DEPTH, 4>(p, a, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+template <int RT, int UPW>
+int launch2(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
+  switch (p.depth) {
+    case 1: return launch3<RT, UPW, 1>(p, a, st);
+    case 2: return launch3<RT, UPW, 2>(p, a, st);
+    case 4:
+      if constexpr (RT * UPW <= 2) return launch3<RT, UPW, 4>(p, a, st);
+      break;
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+template <int RT>
+int launch1(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
+  switch (p.upw) {
+    case 1: return launch2<RT, 1>(p, a, st);
+    case 2: return launch2<RT, 2>(p, a, st);
+    case 4:
+      if constexpr (RT <= 2) return launch2<RT, 4>(p, a, st);
+      break;
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+int divisor_at_least(int64_t n, int64_t v) {
+  while (v <= n && n % v) ++v;
+  return v <= n ? (int)v : 0;
+}
+
+}  // namespace
+
+namespace acorn {
+
+// Valid knobs: rt 1/2/4 (swiglu 2/4, N/16 divisible by rt), upw 1/2/4
+// (rt*upw <= 8), nw 2/4, depth 1/2/4 (rt*upw*depth <= 8). ksplit divides the
+// per-row stage count so that every workgroup's K range holds a whole number
+// of DEPTH-stage rounds; with 0 it grows from 1 until about two workgroups
+// per CU are launched, while the x of one workgroup fits its LDS budget and
+// each K range keeps at least 512 k.
+int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4bPlan* p) {
+  if (M < 1 || M > 16) return ACORN_ERR_UNSUPPORTED;
+  if (N % 16 || K % 512) return ACORN_ERR_SHAPE;
+  if (swiglu && N % 32) return ACORN_ERR_SHAPE;
+  const int64_t ntiles = N / 16, G = K / 128;
+  int rt = cfg && cfg[0] > 0 ? cfg[0] : 2;
+  int upw = cfg && cfg[1] > 0 ? cfg[1] : 2;
+  int nw = cfg && cfg[2] > 0 ? cfg[2] : 4;
+  const int req_ks = cfg ? cfg[3] : 0, req_depth = cfg ? cfg[4] : 0;
+  if (swiglu && rt < 2) rt = 2;
+  if (rt != 1 && rt != 2 && rt != 4) return ACORN_ERR_UNSUPPORTED;
+  while (rt > (swiglu ? 2 : 1) && ntiles % rt) rt /= 2;
+  if (ntiles % rt) return ACORN_ERR_UNSUPPORTED;
+  if (upw != 1 && upw != 2 && upw != 4) return ACORN_ERR_UNSUPPORTED;
+  if (rt * upw > 8) return ACORN_ERR_UNSUPPORTED;
+  if (nw != 2 && nw != 4) return ACORN_ERR_UNSUPPORTED;
+  int R = 1;
+  while (R < M) R *= 2;
+  const int64_t stages = G / upw;            // per row over the whole K
+  if (G % upw) return ACORN_ERR_SHAPE;
+  const size_t lds_cap = 160 * 1024, lds_default = 80 * 1024;
+  const int64_t groups = (ntiles / rt + nw - 1) / nw;
+  int ks;
+  if (swiglu) {
+    ks = 1;
+  } else if (req_ks > 0) {
+    ks = divisor_at_least(stages, req_ks);
+    while (ks && w4b_lds(R, K / ks) > lds_cap) ks = divisor_at_least(stages, ks + 1);
+    if (!ks) return ACORN_ERR_UNSUPPORTED;
+  } else {
+    ks = 1;
+    while (w4b_lds(R, K / ks) > lds_default) {
+      const int nx = divisor_at_least(stages, ks + 1);
+      if (!nx) break;
+      ks = nx;
+    }
+    while (groups * ks < 2 * 256) {
+      const int nx = divisor_at_least(stages, ks + 1);
+      if (!nx || K / nx < 512) break;
+      ks = nx;
+    }
+  }
+  if (w4b_lds(R, K / ks) > lds_cap) return ACORN_ERR_UNSUPPORTED;
+  const int64_t ns = stages / ks;
+  int depth = req_depth > 0 ? req_depth : 4;
+  if (depth != 1 && depth != 2 && depth != 4) return ACORN_ERR_UNSUPPORTED;
+  while (depth > 1 && (ns % depth || rt * upw * depth > 8)) depth /= 2;
+  p->rt = rt;
+  p->upw = upw;
+  p->nw = nw;
+  p->ksplit = ks;
+  p->depth = depth;
+  p->R = R;
+  p->groups = (int)groups;
+  p->lds = w4b_lds(R, K / ks);
+  p->swiglu = swiglu;
+  if (groups > 0x7fffffff || ks > 65535) return ACORN_ERR_SHAPE;
+  return ACORN_OK;
+}
+
+int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale,
+               const void* zero, void* out, float* part, int64_t M, int64_t N, int64_t K,
+               hipStream_t st) {
+  if (zero) return ACORN_ERR_UNSUPPORTED;  // the block layout is the symmetric format
+  if (!x || !w || !scale) return ACORN_ERR_VALUE;
+  // bf16 (or SwiGLU act) output only with one split; else fp32 partials
+  if (p.ksplit > 1) out = nullptr;
+  if (!out && (!part || p.swiglu)) return ACORN_ERR_VALUE;
+  W4bArgs a;
+  a.x = (const __bf16*)x;
+  a.w = (const uint8_t*)w;
+  a.scale = (const _Float16*)scale;
+  a.out = (__bf16*)out;
+  a.part = part;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.kr = (int)(K / p.ksplit);
+  int l = 0;
+  while ((1 << l) < p.R) ++l;
+  a.log2R = l;
+  int rc = ACORN_ERR_UNSUPPORTED;
+  switch (p.rt) {
+    case 1: rc = launch1<1>(p, a, st); break;
+    case 2: rc = launch1<2>(p, a, st); break;
+    case 4: rc = launch1<4>(p, a, st); break;
+  }
+  if (rc) return rc;
+  ACORN_LAUNCH_CHECK();
+  return ACORN_OK;
+}
+
+}  // namespace acorn

@@ -32,15 +32,17 @@ import json
 import torch
 
 from acorninfer_amd.config import Qwen3Config
-from acorninfer_amd.models.qwen3 import (FORMATS, WFMT_BF16, WFMT_W4, WFMT_W8, LayerWeights,
-                                         QLinear, Qwen3DecodeModel)
+from acorninfer_amd.models.qwen3 import (FORMATS, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8,
+                                         LayerWeights, QLinear, Qwen3DecodeModel)
 from acorninfer_amd.ops.quant_gemm import deinterleave16
 
 FORMAT_NAMES = {v: k for k, v in FORMATS.items()}
+FORMAT_NAMES[WFMT_W4B] = "w4a16"      # the in-memory block layout of int4
 _NORMS = ("input_layernorm", "post_attention_layernorm", "self_attn.q_norm", "self_attn.k_norm")
 
 
 def _linear_tensors(name: str, lin: QLinear, out: dict) -> None:
+    lin = lin.natural()                   # files hold the reference's [N, K/2] packing
     if lin.fmt == WFMT_BF16:
         out[f"{name}.weight"] = lin.w
     elif lin.fmt in (WFMT_W8, WFMT_W4):
@@ -54,6 +56,7 @@ def _linear_tensors(name: str, lin: QLinear, out: dict) -> None:
 
 def _rows(lin: QLinear, bounds: list[int], names: list[str], out: dict) -> None:
     """Split a fused projection back into the reference's modules by rows."""
+    lin = lin.natural()
     t = {"w": lin.w, "scale": lin.scale, "zero": lin.zero}
     if lin.il16:
         t = {k: (None if v is None else deinterleave16(v)) for k, v in t.items()}
@@ -149,7 +152,7 @@ def load_quantized(path: str, *, device="cuda") -> Qwen3DecodeModel:
             return QLinear(fmt, w, w.shape[0], K)
         s = torch.cat([p[1] for p in parts], 0).contiguous()
         z = None if parts[0][2] is None else torch.cat([p[2] for p in parts], 0).contiguous()
-        return QLinear(fmt, w, w.shape[0], K, s, z)
+        return QLinear(fmt, w, w.shape[0], K, s, z).blocked()
 
     layers = []
     for i in range(cfg.num_hidden_layers):

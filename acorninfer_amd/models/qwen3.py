@@ -37,8 +37,8 @@ from dataclasses import dataclass, field
 import torch
 
 from acorninfer_amd import _lib
-from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W8, check, dtype_code, lib,
-                                 ptr, stream_ptr)
+from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, check,
+                                 dtype_code, lib, ptr, stream_ptr)
 from acorninfer_amd.config import Qwen3Config
 from acorninfer_amd.quant import quantize as Q
 
@@ -95,7 +95,9 @@ class QLinear:
 
     bf16: w [N,K] bf16.  w8a16: w int8 [N,K], scale fp16 [N].
     w4a16: w uint8 [N,K/2] (low nibble = even k), scale fp16 [N,K/128], zero
-    None (symmetric) or fp16 [N,K/128].
+    None (symmetric) or fp16 [N,K/128]; symmetric weights with N % 16 == 0
+    and K % 512 == 0 are held in the decode kernel's 1 KB block layout
+    (fmt WFMT_W4B, quantize.to_w4b: the same bytes and tensor shapes).
     """
     fmt: int
     w: torch.Tensor
@@ -115,8 +117,23 @@ class QLinear:
             return cls(fmt, q.contiguous(), N, K, s.contiguous())
         if fmt == WFMT_W4:
             u, s = Q.quantize_w4_sym(w)
-            return cls(fmt, Q.pack_w4(u).contiguous(), N, K, s.contiguous())
+            return cls(fmt, Q.pack_w4(u).contiguous(), N, K, s.contiguous()).blocked()
         raise ValueError(f"unknown weight format {fmt}")
+
+    def blocked(self) -> "QLinear":
+        """Symmetric int4 in the W4B block layout where the shape allows it
+        (N % 16 == 0, K % 512 == 0); any other weight unchanged."""
+        if self.fmt != WFMT_W4 or self.zero is not None or self.N % 16 or self.K % 512:
+            return self
+        wb, sb = Q.to_w4b(self.w, self.scale)
+        return QLinear(WFMT_W4B, wb, self.N, self.K, sb, None, il16=self.il16)
+
+    def natural(self) -> "QLinear":
+        """The same weight with int4 in the natural [N, K/2] layout."""
+        if self.fmt != WFMT_W4B:
+            return self
+        w, s = Q.from_w4b(self.w, self.scale)
+        return QLinear(WFMT_W4, w, self.N, self.K, s, None, il16=self.il16)
 
     def interleaved(self) -> "QLinear":
         """The same [gate; up] weight with rows (and scales, zeros) in the
@@ -133,9 +150,10 @@ class QLinear:
         elif self.fmt == WFMT_W8:
             d = Q.dequant_w8(self.w, self.scale)
         else:
-            u = Q.unpack_w4(self.w)
-            zero = self.zero if self.zero is not None else Q.sym_zero(self.scale)
-            d = Q.dequant_w4(u, self.scale, zero)
+            nat = self.natural()
+            u = Q.unpack_w4(nat.w)
+            zero = nat.zero if nat.zero is not None else Q.sym_zero(nat.scale)
+            d = Q.dequant_w4(u, nat.scale, zero)
         if self.il16:
             from acorninfer_amd.ops.quant_gemm import deinterleave16
             d = deinterleave16(d)

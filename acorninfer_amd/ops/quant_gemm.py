@@ -21,8 +21,8 @@ from typing import NamedTuple
 
 import torch
 
-from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W8, check, lib, ptr,
-                                 require_gpu, stream_ptr)
+from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, check, lib,
+                                 ptr, require_gpu, stream_ptr)
 
 CLASSES = {
     "qo": (4096, 4096),
@@ -74,6 +74,9 @@ class Tiling(NamedTuple):
     Tiled kernel (M > 16 with rt == 0, the default there): upw is the M tile
     BM (32 / 64 / 128), nw the N tile BN (64 / 128), ksplit the K split; the
     planner reports (0, BM, BN, ksplit, 1).
+    int4 decode kernel (WFMT_W4B, M <= 16): rt row tiles per wave, upw
+    128-k groups per pipeline stage, nw waves per workgroup (each its own
+    rows), ksplit, and tpw = stages in flight per wave.
     """
     rt: int = 0
     upw: int = 0
@@ -279,10 +282,16 @@ def _time_cfg(fn, reps: int = 20) -> float:
 def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[Tiling]:
     """The planner's default plus a neighbourhood of valid tilings (distinct
     full choices only) for a load-time sweep."""
-    seen, out = set(), []
     planner = swiglu_plan if swiglu else plan
     base, _ = planner(M, N, K, wfmt)
     reqs = [Tiling()]
+    if wfmt == WFMT_W4B and M <= DECODE_M_MAX:
+        reqs += _w4b_requests(swiglu)
+        if not swiglu:
+            for bn in (64, 128):
+                for ks in (1, 2, 4, 8, 16):
+                    reqs.append(Tiling(0, 32, bn, ks, 0))
+        return _resolve(reqs, planner, M, N, K, wfmt, base)
     for rt in (1, 2, 4):
         for upw in (2, 4, 8, 16):
             for nw in (2, 4, 8):
@@ -311,6 +320,28 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
         for bn in (64, 128):
             for ks in (1, 2, 4, 8, 16):
                 reqs.append(Tiling(0, 32, bn, ks, 0))
+    return _resolve(reqs, planner, M, N, K, wfmt, base)
+
+
+def _w4b_requests(swiglu: bool) -> list[Tiling]:
+    """Requests covering the int4 decode kernel's knobs: up to 8 KB of
+    weights in flight per wave (rt * upw * depth <= 8), and split counts
+    from one to sixteen."""
+    reqs = []
+    for rt in ((2, 4) if swiglu else (1, 2, 4)):
+        for upw in (1, 2, 4):
+            for depth in (1, 2, 4):
+                if rt * upw * depth > 8:
+                    continue
+                for nw in (2, 4):
+                    for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
+                        reqs.append(Tiling(rt, upw, nw, ks, depth))
+    return reqs
+
+
+def _resolve(reqs, planner, M, N, K, wfmt, base) -> list[Tiling]:
+    """The distinct full tilings the planner makes of `reqs`, the default first."""
+    seen, out = set(), []
     for r in reqs:
         try:
             t, _ = planner(M, N, K, wfmt, r)

@@ -101,6 +101,41 @@ def unpack_w4(p: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def to_w4b(packed: torch.Tensor, scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Natural packed int4 [N, K/2] + scale [N, K/128] -> the same bytes in
+    the decode kernel's 1 KB block layout (ACORN_WFMT_W4B), kept in tensors
+    of the same shapes: 16-byte chunk (row n, k in [32c, 32c+32)) moves to
+    block (n // 16, c // 4), lane (c % 4) * 16 + n % 16; the scale of (n, g)
+    to record (n // 16, g // 4, (n % 16) // 4) at position (g % 4) * 4 + n % 4.
+    Rows 16t..16t+15 of both tensors hold row tile t, so 16-row block
+    permutations (interleave16) commute with the conversion. N % 16 == 0 and
+    K % 512 == 0."""
+    n, kh = packed.shape
+    k = 2 * kh
+    if n % 16 or k % 512 or scale.shape != (n, k // 128):
+        raise ValueError(f"to_w4b needs N % 16 == 0, K % 512 == 0 and scale [N, K/128]: "
+                         f"packed {tuple(packed.shape)}, scale {tuple(scale.shape)}")
+    wb = (packed.reshape(n // 16, 16, k // 128, 4, 16)      # tile, row, group, chunk, byte
+          .permute(0, 2, 3, 1, 4).reshape(n, kh).contiguous())
+    sb = (scale.reshape(n // 16, 4, 4, k // 512, 4)        # tile, lg, i, g4, gg
+          .permute(0, 3, 1, 4, 2).reshape(n, k // 128).contiguous())
+    return wb, sb
+
+
+def from_w4b(wb: torch.Tensor, sb: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Inverse of to_w4b."""
+    n, kh = wb.shape
+    k = 2 * kh
+    if n % 16 or k % 512 or sb.shape != (n, k // 128):
+        raise ValueError(f"from_w4b needs N % 16 == 0, K % 512 == 0 and scale [N, K/128]: "
+                         f"packed {tuple(wb.shape)}, scale {tuple(sb.shape)}")
+    packed = (wb.reshape(n // 16, k // 128, 4, 16, 16)     # tile, group, chunk, row, byte
+              .permute(0, 3, 1, 2, 4).reshape(n, kh).contiguous())
+    scale = (sb.reshape(n // 16, k // 512, 4, 4, 4)        # tile, g4, lg, gg, i
+             .permute(0, 2, 4, 1, 3).reshape(n, k // 128).contiguous())
+    return packed, scale
+
+
 def dequant_w8(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """fp32 [N,K] = q * scale[:, None]."""
     return q.float() * scale.float()[:, None]

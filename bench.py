@@ -350,7 +350,7 @@ def kernel_benchmarks(seed: int = 23, only_attention: bool = False,
                                         generator=g)
                     sc = (0.005 + 0.015 * torch.rand(n, k // 128, device="cuda",
                                                      generator=g)).half()
-                    lins.append(QLinear(wf, wq4, n, k, sc))
+                    lins.append(QLinear(wf, wq4, n, k, sc).blocked())   # the model's layout
                 else:
                     wq8 = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda",
                                         generator=g)
@@ -359,7 +359,7 @@ def kernel_benchmarks(seed: int = 23, only_attention: bool = False,
             for M in (1, 8, 64, 256):
                 xm = torch.randn(M, k, device="cuda", generator=g).bfloat16()
                 best = None
-                cands = candidates(M, n, k, wf)
+                cands = candidates(M, n, k, lins[0].fmt)
                 for c in cands:
                     t = lins[0].plan(M, c)[0]
                     part = torch.empty(t.ksplit, M, n, device="cuda")

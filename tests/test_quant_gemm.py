@@ -203,7 +203,7 @@ def test_bucket_boundaries_and_classes():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["bf16", "w8", "w4"])
+@pytest.mark.parametrize("fmt", ["bf16", "w8", "w4", "w4b"])
 @pytest.mark.parametrize("m", [1, 8, 16, 40, 256])
 def test_every_candidate_tiling_matches(fmt, m):
     """Every tiling the load-time sweep may pick (streaming kernel: row tiles
@@ -212,8 +212,9 @@ def test_every_candidate_tiling_matches(fmt, m):
     partial last M tile at M = 40) gives the oracle's result on the o shape
     (K=4096) and the down shape (K=12288); tilings differ only in fp32
     summation order."""
-    from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, WFMT_W8
+    from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8
     from acorninfer_amd.ops.quant_gemm import _launch, candidates
+    from acorninfer_amd.quant.quantize import to_w4b
     for cls in ("o", "down"):
         n, k = SHAPES[cls]
         if fmt == "bf16":
@@ -222,9 +223,12 @@ def test_every_candidate_tiling_matches(fmt, m):
         elif fmt == "w8":
             q, s, wref = _w8(cls)
             args, wf = (q, s, None), WFMT_W8
-        else:
+        elif fmt == "w4":
             p, s, wref = _w4(cls)
             args, wf = (p, s, None), WFMT_W4
+        else:
+            p, s, wref = _w4(cls)
+            args, wf = (*to_w4b(p, s), None), WFMT_W4B
         x = _x(m, k, 9)
         ref = _ref(x, wref)
         cands = candidates(m, n, k, wf)
@@ -236,6 +240,80 @@ def test_every_candidate_tiling_matches(fmt, m):
             assert r <= GEMM_REL, f"{cls} {tuple(c)}: rel err {r:.3g}"
             outs.append(out)
         print(f"\n[{fmt} M={m} {cls}: {len(cands)} tilings ok]")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cls", list(SHAPES))
+@pytest.mark.parametrize("m", MS)
+def test_w4b_config3_matches_dequant_matmul(cls, m):
+    """The decode model's int4 layout (W4B blocks) at every configuration-3
+    shape and M, with the planner's tiling: the int4 decode kernel for
+    M <= 16, the tiled kernel above."""
+    from acorninfer_amd._lib import WFMT_W4B
+    from acorninfer_amd.ops.quant_gemm import _launch
+    from acorninfer_amd.quant.quantize import to_w4b
+    p, s, wref = _w4(cls)
+    wb, sb = to_w4b(p, s)
+    n, k = SHAPES[cls]
+    x = _x(m, k, 10)
+    out = _launch(x, wb, sb, None, WFMT_W4B, n, None, None)
+    r = rel_err(out, _ref(x, wref))
+    assert r <= GEMM_REL, f"rel err {r:.3g}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [40, 256])
+def test_w4b_tiled_equals_natural_bitwise(m):
+    """The tiled kernel does the same arithmetic on both int4 layouts, only
+    its addressing differs: W4B and natural W4 give the same bits at every
+    tiled candidate."""
+    from acorninfer_amd._lib import WFMT_W4, WFMT_W4B
+    from acorninfer_amd.ops.quant_gemm import _launch, candidates
+    from acorninfer_amd.quant.quantize import to_w4b
+    p, s, _ = _w4("down")
+    wb, sb = to_w4b(p, s)
+    n, k = SHAPES["down"]
+    x = _x(m, k, 11)
+    cands = [c for c in candidates(m, n, k, WFMT_W4B) if c.rt == 0]
+    assert len(cands) >= 4
+    for c in cands:
+        a = _launch(x, wb, sb, None, WFMT_W4B, n, c, None)
+        b = _launch(x, p, s, None, WFMT_W4, n, c, None)
+        assert torch.equal(a, b), tuple(c)
+
+
+@pytest.mark.gpu
+def test_w4b_split_partials_deterministic_and_graph_replay():
+    """W4B partials at several split counts sum (in split order) to the same
+    result within fp32 rounding, repeat bitwise, and replay bitwise in a
+    hipGraph."""
+    from acorninfer_amd._lib import WFMT_W4B
+    from acorninfer_amd.ops.quant_gemm import Tiling, _launch, gemm_partials
+    from acorninfer_amd.quant.quantize import to_w4b
+    for cls, splits in (("o", (1, 2)), ("down", (2, 3, 4, 6, 12))):
+        p, s, wref = _w4(cls)
+        wb, sb = to_w4b(p, s)
+        n, k = SHAPES[cls]
+        x = _x(8, k, 12)
+        ref = _ref(x, wref)
+        for ks in splits:               # ks = 1: fp32 output through the partials buffer
+            t = Tiling(2, 2, 4, ks, 2)
+            part = torch.empty(ks, 8, n, device="cuda")
+            gemm_partials(x, wb, sb, None, WFMT_W4B, part, t)
+            acc = part[0].clone()
+            for i in range(1, ks):
+                acc += part[i]
+            assert rel_err(acc, ref) <= GEMM_REL, (cls, ks)
+            part2 = torch.empty_like(part)
+            gemm_partials(x, wb, sb, None, WFMT_W4B, part2, t)
+            assert torch.equal(part, part2)
+    p, s, _ = _w4("down")
+    wb, sb = to_w4b(p, s)
+    x = _x(8, 12288, 12)
+    out = torch.empty(8, 4096, dtype=torch.bfloat16, device="cuda")
+    t = Tiling(2, 2, 4, 3, 2)
+    assert graph_replays_match(lambda: _launch(x, wb, sb, None, WFMT_W4B, 4096, t, out),
+                               lambda: out)
 
 
 def _swiglu_ref(x, wg, wu):
@@ -267,7 +345,7 @@ def test_fused_swiglu_every_tiling(fmt, m):
     x = (torch.randn(m, k, generator=g)).bfloat16().cuda()
     ref = _swiglu_ref(x, deq[:inter], deq[inter:])
     st = stream_ptr()
-    cands = candidates(m, 2 * inter, k, wf, swiglu=True)
+    cands = candidates(m, 2 * inter, k, lin.fmt, swiglu=True)
     assert len(cands) >= 4
     for c in cands:
         act = torch.full((m, inter), float("nan"), dtype=torch.bfloat16, device="cuda")
