@@ -102,10 +102,12 @@ __host__ __device__ inline size_t w4b_half_index(int64_t n, int64_t g, int64_t K
 
 // ---- the W4B decode kernel (w4_decode.hip) ----------------------------------
 // cfg knobs: rt (row tiles of 16 per wave), upw (groups per pipeline stage),
-// nw (waves per workgroup, each with its own rt tiles), ksplit, depth
-// (stages in flight per wave); 0 = choose.
+// nw (waves per workgroup; 10*nw + kw when kw waves share rows and split K),
+// ksplit, depth (stages in flight per wave); 0 = choose.
 struct W4bPlan {
   int rt, upw, nw, ksplit, depth;
+  int kw;          // K slices per row group (waves sharing rows)
+  int nw_field;    // the cfg value of nw (nw, or 10*nw + kw)
   int R;           // x rows staged in LDS (power of 2 >= M)
   int groups;      // workgroups along N
   size_t lds;      // dynamic LDS bytes

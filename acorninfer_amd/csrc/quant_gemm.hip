@@ -824,7 +824,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
     t->kind = 2;
     t->rt = t->w4b.rt;
     t->upw = t->w4b.upw;
-    t->nw = t->w4b.nw;
+    t->nw = t->w4b.nw_field;
     t->ksplit = t->w4b.ksplit;
     t->tpw = t->w4b.depth;
     t->mt = 1;

@@ -17,9 +17,12 @@
 //    weights and X the sum of x over the group (one MFMA against ones per
 //    group, once per workgroup): two VALU per output row and group; the fp16
 //    scale is read from its packed pair by v_fma_mix_f32.
-//  * The waves of a workgroup share the staged x and each owns RT row tiles
-//    over the workgroup's whole K range, so nothing is reduced across waves:
-//    after the staging barrier a wave only streams, computes and stores.
+//  * The waves of a workgroup share the staged x. They form NW/KW row groups
+//    of RT row tiles; the KW waves of a row group split the workgroup's K
+//    range and add their results through LDS in fixed order at the end
+//    (KW = 1: each wave owns its rows over the whole range and stores them
+//    itself). K slices inside a workgroup give small projections many waves
+//    without split-K partials or a second pass.
 //  * Each wave keeps DEPTH stages (UPW groups x RT row tiles) of loads in
 //    flight. Every load is unconditional and the stage count is a multiple
 //    of DEPTH, so the compiler's wait counts are static.
@@ -38,7 +41,7 @@ struct W4bArgs {
   __bf16* out;    // bf16 [M, N] (act [M, N/2] with SWIGLU) when ksplit == 1
   float* part;    // fp32 [ksplit, M, N] otherwise
   int M, N, K;
-  int kr;         // K range of a workgroup (a multiple of 128 * UPW * DEPTH)
+  int kr;         // K range of a workgroup (a multiple of 128 * KW * UPW * DEPTH)
   int log2R;      // x rows staged = 1 << log2R >= M
 };
 
@@ -48,9 +51,10 @@ struct Stage {
   uint32_t s[RT][2 * UPW];   // fp16 scales: half 4u + i is row 4*lg + i of group u
 };
 
-// Grid: x = groups of NW*RT row tiles, y = ksplit. Block: NW waves.
-template <int RT, int UPW, int DEPTH, int NW, bool SWIGLU>
+// Grid: x = groups of (NW/KW)*RT row tiles, y = ksplit. Block: NW waves.
+template <int RT, int UPW, int DEPTH, int NW, int KW, bool SWIGLU>
 __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
+  static_assert(NW % KW == 0, "K slices divide the waves");
   constexpr int NT = NW * kWave;
   extern __shared__ __align__(16) unsigned char smem[];
   const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -59,46 +63,56 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   const int KR = a.kr, kr0 = blockIdx.y * KR;
   const int GR = KR / 128, CPR = KR / 8;
   const int G = a.K / 128, G4 = a.K / 512;
-  const int t0 = (blockIdx.x * NW + wid) * RT;   // this wave's first row tile
+  const int rg = wid / KW, kq = wid % KW;        // row group, K slice
+  const int t0 = (blockIdx.x * (NW / KW) + rg) * RT;   // the row group's first tile
   const bool active = t0 < a.N / 16;              // (N / 16) % RT == 0 by the plan
   const int tt = active ? t0 : 0;                 // idle waves read tile 0, store nothing
   // LDS: x pieces [CPR][R] (16 bytes each, W4 k order) | group sums [GR][16]
+  //      | K-slice results [NW][RT][4][64] (KW > 1)
   u32x4* xs = (u32x4*)smem;
   float* xgs = (float*)(smem + (size_t)CPR * R * 16);
 
-  const int ns = GR / UPW;                        // stages of this wave
-  const uint8_t* wb = a.w + ((size_t)tt * G + kr0 / 128) * 1024 + lane * 16;
+  const int GW = GR / KW, gw0 = kq * GW;          // this wave's groups of the range
+  const int ns = GW / UPW;                        // stages of this wave
+  const uint8_t* wb = a.w + ((size_t)tt * G + kr0 / 128 + gw0) * 1024 + lane * 16;
   auto load = [&](int s, Stage<RT, UPW>& r) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int u = 0; u < UPW; ++u)
         r.w[rt][u] = load_nt((const u32x4*)(wb + ((size_t)rt * G + s * UPW + u) * 1024));
-    const int g = kr0 / 128 + s * UPW;
+    const int g = kr0 / 128 + gw0 + s * UPW;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
       load_dwords(a.scale + ((((size_t)(tt + rt) * G4 + g / 4) * 4 + lg) * 16 + (g % 4) * 4),
                   r.s[rt]);
   };
 
-  // ---- the first DEPTH stages, then x ---------------------------------------
+  // ---- x's first pieces, then the first DEPTH stages, then the rest of x ------
+  // x [M, kr0 .. kr0+KR) goes to LDS as piece p = c * R + row (consecutive
+  // threads write consecutive 16 bytes); rows past M re-read row M-1 (their
+  // slots feed only output columns that are never stored). The first XB
+  // pieces per thread are requested before the weights, so waiting for them
+  // (an L2 round trip) does not wait for the weights: loads complete in order.
+  constexpr int XB = 8;
+  const int xtotal = R * CPR;
+  auto x_load = [&](int p) -> u32x4 {
+    p = min(p, xtotal - 1);
+    const int m = min(p & (R - 1), a.M - 1), c = p >> a.log2R;
+    return *(const u32x4*)(a.x + (size_t)m * a.K + kr0 + c * 8);
+  };
+  u32x4 xv[XB];
+#pragma unroll
+  for (int u = 0; u < XB; ++u) xv[u] = x_load((int)threadIdx.x + u * NT);
   Stage<RT, UPW> ring[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
-
-  // x [M, kr0 .. kr0+KR) into LDS: piece p = c * R + row (consecutive threads
-  // write consecutive 16 bytes); rows past M re-read row M-1 (their slots
-  // feed only output columns that are never stored).
-  constexpr int XB = 8;
-  const int xtotal = R * CPR;
-  for (int p0 = threadIdx.x; p0 < xtotal; p0 += NT * XB) {
-    u32x4 xv[XB];
 #pragma unroll
-    for (int u = 0; u < XB; ++u) {
-      const int p = min(p0 + u * NT, xtotal - 1);
-      const int m = min(p & (R - 1), a.M - 1), c = p >> a.log2R;
-      xv[u] = *(const u32x4*)(a.x + (size_t)m * a.K + kr0 + c * 8);
-    }
+  for (int u = 0; u < XB; ++u)
+    if ((int)threadIdx.x + u * NT < xtotal) xs[threadIdx.x + u * NT] = w4_order_x(xv[u]);
+  for (int p0 = threadIdx.x + NT * XB; p0 < xtotal; p0 += NT * XB) {
+#pragma unroll
+    for (int u = 0; u < XB; ++u) xv[u] = x_load(p0 + u * NT);
 #pragma unroll
     for (int u = 0; u < XB; ++u)
       if (p0 + u * NT < xtotal) xs[p0 + u * NT] = w4_order_x(xv[u]);
@@ -114,7 +128,6 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
     if (lg == 0) xgs[g * 16 + lr] = xg[0];
   }
   __syncthreads();
-  if (!active) return;
 
   // ---- stream ------------------------------------------------------------------
   f32x4 acc[RT];
@@ -123,7 +136,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   auto compute = [&](const Stage<RT, UPW>& r, int s) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
-      const int gl = s * UPW + u;
+      const int gl = gw0 + s * UPW + u;
       const u32x4* xp = xs + (gl * 16 + 4 * lg) * R + xrow;
       u32x4 b[4];
 #pragma unroll
@@ -139,18 +152,41 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
           acc[rt][i] = __builtin_fmaf(half_f(r.s[rt], 4 * u + i),
                                       __builtin_fmaf(xg, -136.f, cc[i]), acc[rt][i]);
       }
+      // one group at a time: without this fence the scheduler hoists the
+      // unpacking of later groups and the register ring no longer fits
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
-  int s0 = 0;
-  for (; s0 + DEPTH < ns; s0 += DEPTH) {
+  if (active) {
+    int s0 = 0;
+    for (; s0 + DEPTH < ns; s0 += DEPTH) {
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      compute(ring[d], s0 + d);
-      load(s0 + DEPTH + d, ring[d]);
+      for (int d = 0; d < DEPTH; ++d) {
+        compute(ring[d], s0 + d);
+        load(s0 + DEPTH + d, ring[d]);
+      }
     }
-  }
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) compute(ring[d], s0 + d);
+    for (int d = 0; d < DEPTH; ++d) compute(ring[d], s0 + d);
+  }
+  if constexpr (KW > 1) {
+    // the K slices of a row group, added in slice order by slice 0
+    float* red = xgs + GR * 16;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[((wid * RT + rt) * 4 + i) * kWave + lane] = acc[rt][i];
+    __syncthreads();
+    if (kq != 0) return;
+#pragma unroll
+    for (int q = 1; q < KW; ++q)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[rt][i] += red[(((wid + q) * RT + rt) * 4 + i) * kWave + lane];
+  }
+  if (!active) return;
 
   // ---- store: lane (lr, lg) holds rows 4*lg .. 4*lg+3 of column lr ------------
   const int m = lr;
@@ -182,15 +218,18 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   }
 }
 
-size_t w4b_lds(int R, int64_t kr) { return (size_t)kr * R * 2 + (size_t)(kr / 128) * 64; }
+size_t w4b_lds(int R, int64_t kr, int nw, int kw, int rt) {
+  return (size_t)kr * R * 2 + (size_t)(kr / 128) * 64 +
+         (kw > 1 ? (size_t)nw * rt * 4 * kWave * 4 : 0);
+}
 
-template <int RT, int UPW, int DEPTH, int NW>
-int launch4(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
-  auto kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, false>;
+template <int RT, int UPW, int DEPTH, int NW, int KW>
+int launch5(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
+  auto kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, KW, false>;
   int variant = 0;
   if constexpr (RT >= 2) {
     if (p.swiglu) {
-      kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, true>;
+      kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, KW, true>;
       variant = 1;
     }
   }
@@ -205,11 +244,16 @@ int launch4(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
   return ACORN_OK;
 }
 
+// (waves, K slices) per workgroup
 template <int RT, int UPW, int DEPTH>
 int launch3(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
-  switch (p.nw) {
-    case 2: return launch4<RT, UPW, DEPTH, 2>(p, a, st);
-    case 4: return launch4<RT, UPW, DEPTH, 4>(p, a, st);
+  switch (p.nw * 16 + p.kw) {
+    case 2 * 16 + 1: return launch5<RT, UPW, DEPTH, 2, 1>(p, a, st);
+    case 4 * 16 + 1: return launch5<RT, UPW, DEPTH, 4, 1>(p, a, st);
+    case 4 * 16 + 2: return launch5<RT, UPW, DEPTH, 4, 2>(p, a, st);
+    case 4 * 16 + 4: return launch5<RT, UPW, DEPTH, 4, 4>(p, a, st);
+    case 8 * 16 + 2: return launch5<RT, UPW, DEPTH, 8, 2>(p, a, st);
+    case 8 * 16 + 4: return launch5<RT, UPW, DEPTH, 8, 4>(p, a, st);
   }
   return ACORN_ERR_UNSUPPORTED;
 }
@@ -220,7 +264,10 @@ int launch2(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
     case 1: return launch3<RT, UPW, 1>(p, a, st);
     case 2: return launch3<RT, UPW, 2>(p, a, st);
     case 4:
-      if constexpr (RT * UPW <= 2) return launch3<RT, UPW, 4>(p, a, st);
+      if constexpr (RT * UPW <= 4 && RT < 4) return launch3<RT, UPW, 4>(p, a, st);
+      break;
+    case 8:
+      if constexpr (RT * UPW <= 2) return launch3<RT, UPW, 8>(p, a, st);
       break;
   }
   return ACORN_ERR_UNSUPPORTED;
@@ -232,7 +279,7 @@ int launch1(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
     case 1: return launch2<RT, 1>(p, a, st);
     case 2: return launch2<RT, 2>(p, a, st);
     case 4:
-      if constexpr (RT <= 2) return launch2<RT, 4>(p, a, st);
+      if constexpr (RT == 1) return launch2<RT, 4>(p, a, st);
       break;
   }
   return ACORN_ERR_UNSUPPORTED;
@@ -247,12 +294,14 @@ int divisor_at_least(int64_t n, int64_t v) {
 
 namespace acorn {
 
-// Valid knobs: rt 1/2/4 (swiglu 2/4, N/16 divisible by rt), upw 1/2/4
-// (rt*upw <= 8), nw 2/4, depth 1/2/4 (rt*upw*depth <= 8). ksplit divides the
-// per-row stage count so that every workgroup's K range holds a whole number
-// of DEPTH-stage rounds; with 0 it grows from 1 until about two workgroups
-// per CU are launched, while the x of one workgroup fits its LDS budget and
-// each K range keeps at least 512 k.
+// Valid knobs: rt 1/2/4 (swiglu 2/4; N/16 divisible by rt), upw 1/2/4
+// (rt*upw <= 8, rt 4 with upw <= 2), depth 1/2/4/8 (rt*upw*depth <= 16), and
+// the wave layout in the nw field: 2 or 4 = that many waves with one K slice,
+// 10*nw + kw = nw waves in nw/kw row groups of kw K slices (42, 44, 82, 84).
+// ksplit and kw divide the per-row stage count G/upw so that every wave's K
+// range holds a whole number of depth-stage rounds. With 0 the split grows
+// from 1 until about two workgroups per CU are launched, while one
+// workgroup's x fits its LDS budget and each K range keeps at least 512 k.
 int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4bPlan* p) {
   if (M < 1 || M > 16) return ACORN_ERR_UNSUPPORTED;
   if (N % 16 || K % 512) return ACORN_ERR_SHAPE;
@@ -260,54 +309,66 @@ int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   const int64_t ntiles = N / 16, G = K / 128;
   int rt = cfg && cfg[0] > 0 ? cfg[0] : 2;
   int upw = cfg && cfg[1] > 0 ? cfg[1] : 2;
-  int nw = cfg && cfg[2] > 0 ? cfg[2] : 4;
+  const int nwf = cfg && cfg[2] > 0 ? cfg[2] : 4;
   const int req_ks = cfg ? cfg[3] : 0, req_depth = cfg ? cfg[4] : 0;
+  const int nw = nwf < 10 ? nwf : nwf / 10, kw = nwf < 10 ? 1 : nwf % 10;
+  const bool layout_ok = (kw == 1 && (nw == 2 || nw == 4)) ||
+                         (nw == 4 && (kw == 2 || kw == 4)) || (nw == 8 && (kw == 2 || kw == 4));
+  if (!layout_ok) return ACORN_ERR_UNSUPPORTED;
   if (swiglu && rt < 2) rt = 2;
   if (rt != 1 && rt != 2 && rt != 4) return ACORN_ERR_UNSUPPORTED;
   while (rt > (swiglu ? 2 : 1) && ntiles % rt) rt /= 2;
   if (ntiles % rt) return ACORN_ERR_UNSUPPORTED;
   if (upw != 1 && upw != 2 && upw != 4) return ACORN_ERR_UNSUPPORTED;
-  if (rt * upw > 8) return ACORN_ERR_UNSUPPORTED;
-  if (nw != 2 && nw != 4) return ACORN_ERR_UNSUPPORTED;
+  if (rt * upw > 8 || (rt == 4 && upw > 2) || (rt == 2 && upw > 2)) return ACORN_ERR_UNSUPPORTED;
   int R = 1;
   while (R < M) R *= 2;
-  const int64_t stages = G / upw;            // per row over the whole K
   if (G % upw) return ACORN_ERR_SHAPE;
+  const int64_t stages = G / upw;            // per row over the whole K
+  if (stages % kw) return ACORN_ERR_UNSUPPORTED;
+  const int64_t slices = stages / kw;        // per K slice with one split
   const size_t lds_cap = 160 * 1024, lds_default = 80 * 1024;
-  const int64_t groups = (ntiles / rt + nw - 1) / nw;
+  const int64_t rows_per_wg = (int64_t)(nw / kw) * rt;
+  const int64_t groups = (ntiles / rt + nw / kw - 1) / (nw / kw);
+  auto lds = [&](int ks) { return w4b_lds(R, K / ks, nw, kw, rt); };
   int ks;
   if (swiglu) {
     ks = 1;
   } else if (req_ks > 0) {
-    ks = divisor_at_least(stages, req_ks);
-    while (ks && w4b_lds(R, K / ks) > lds_cap) ks = divisor_at_least(stages, ks + 1);
+    ks = divisor_at_least(slices, req_ks);
+    while (ks && lds(ks) > lds_cap) ks = divisor_at_least(slices, ks + 1);
     if (!ks) return ACORN_ERR_UNSUPPORTED;
   } else {
     ks = 1;
-    while (w4b_lds(R, K / ks) > lds_default) {
-      const int nx = divisor_at_least(stages, ks + 1);
+    while (lds(ks) > lds_default) {
+      const int nx = divisor_at_least(slices, ks + 1);
       if (!nx) break;
       ks = nx;
     }
     while (groups * ks < 2 * 256) {
-      const int nx = divisor_at_least(stages, ks + 1);
-      if (!nx || K / nx < 512) break;
+      const int nx = divisor_at_least(slices, ks + 1);
+      if (!nx || K / nx / kw < 512) break;
       ks = nx;
     }
   }
-  if (w4b_lds(R, K / ks) > lds_cap) return ACORN_ERR_UNSUPPORTED;
-  const int64_t ns = stages / ks;
+  if (lds(ks) > lds_cap) return ACORN_ERR_UNSUPPORTED;
+  const int64_t ns = slices / ks;            // stages of one wave
   int depth = req_depth > 0 ? req_depth : 4;
-  if (depth != 1 && depth != 2 && depth != 4) return ACORN_ERR_UNSUPPORTED;
-  while (depth > 1 && (ns % depth || rt * upw * depth > 8)) depth /= 2;
+  if (depth != 1 && depth != 2 && depth != 4 && depth != 8) return ACORN_ERR_UNSUPPORTED;
+  while (depth > 1 && (ns % depth || rt * upw * depth > 16 || (rt == 4 && depth > 2) ||
+                       (rt * upw > 2 && depth > 4)))
+    depth /= 2;
+  (void)rows_per_wg;
   p->rt = rt;
   p->upw = upw;
   p->nw = nw;
+  p->kw = kw;
+  p->nw_field = nwf < 10 ? nw : nwf;
   p->ksplit = ks;
   p->depth = depth;
   p->R = R;
   p->groups = (int)groups;
-  p->lds = w4b_lds(R, K / ks);
+  p->lds = lds(ks);
   p->swiglu = swiglu;
   if (groups > 0x7fffffff || ks > 65535) return ACORN_ERR_SHAPE;
   return ACORN_OK;

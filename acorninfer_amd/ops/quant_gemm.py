@@ -75,8 +75,9 @@ class Tiling(NamedTuple):
     BM (32 / 64 / 128), nw the N tile BN (64 / 128), ksplit the K split; the
     planner reports (0, BM, BN, ksplit, 1).
     int4 decode kernel (WFMT_W4B, M <= 16): rt row tiles per wave, upw
-    128-k groups per pipeline stage, nw waves per workgroup (each its own
-    rows), ksplit, and tpw = stages in flight per wave.
+    128-k groups per pipeline stage, nw waves per workgroup (2 or 4 each on
+    its own rows; 10*nw + kw: kw waves share rows and split K), ksplit, and
+    tpw = stages in flight per wave.
     """
     rt: int = 0
     upw: int = 0
@@ -324,16 +325,18 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
 
 
 def _w4b_requests(swiglu: bool) -> list[Tiling]:
-    """Requests covering the int4 decode kernel's knobs: up to 8 KB of
-    weights in flight per wave (rt * upw * depth <= 8), and split counts
+    """Requests covering the int4 decode kernel's knobs: up to 16 KB of
+    weights in flight per wave (rt * upw * depth <= 16), and split counts
     from one to sixteen."""
     reqs = []
     for rt in ((2, 4) if swiglu else (1, 2, 4)):
-        for upw in (1, 2, 4):
-            for depth in (1, 2, 4):
-                if rt * upw * depth > 8:
+        for upw in ((1, 2, 4) if rt == 1 else (1, 2)):
+            for depth in (1, 2, 4, 8):
+                if rt * upw * depth > 16:
                     continue
-                for nw in (2, 4):
+                # waves per workgroup: 2 or 4 each on its own rows, or
+                # 10*nw + kw with kw waves splitting K over shared rows
+                for nw in (4, 42, 82):
                     for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
                         reqs.append(Tiling(rt, upw, nw, ks, depth))
     return reqs

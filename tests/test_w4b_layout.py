@@ -81,25 +81,30 @@ def test_shape_guard():
 def test_planner_w4b_decode(M, N, K):
     """The default W4B tiling, and every requested one the planner accepts,
     obey the kernel's contract:
-    rt divides N/16, upw in {1,2,4}, rt*upw*depth <= 8, the K range of a
-    split holds a whole number of depth-stage rounds, LDS fits."""
+    rt divides N/16, upw in {1,2,4}, rt*upw*depth <= 16, a supported wave
+    layout, each wave's K range holds a whole number of depth-stage rounds,
+    LDS fits."""
     lib = _lib.lib()
-    reqs = [(0, 0, 0, 0, 0), (4, 1, 2, 0, 2), (1, 4, 4, 3, 2), (2, 2, 4, 5, 4)]
+    reqs = [(0, 0, 0, 0, 0), (4, 1, 2, 0, 2), (1, 4, 4, 3, 2), (2, 2, 4, 5, 4), (1, 2, 84, 1, 4),
+            (2, 1, 42, 2, 8)]
     for r in reqs:
         cfg = (ctypes.c_int * 6)(*r, 0)
         rc = lib.acorn_gemm_plan(M, N, K, _lib.WFMT_W4B, cfg)
         if r != reqs[0] and rc == _lib.ERR_UNSUPPORTED:
             continue                  # a request the shape cannot honour is refused
         assert rc == 0, (r, rc)
-        rt, upw, nw, ks, depth = cfg[:5]
+        rt, upw, nwf, ks, depth = cfg[:5]
+        nw, kw = (nwf, 1) if nwf < 10 else (nwf // 10, nwf % 10)
+        assert (nw, kw) in ((2, 1), (4, 1), (4, 2), (4, 4), (8, 2), (8, 4))
         assert rt in (1, 2, 4) and (N // 16) % rt == 0
-        assert upw in (1, 2, 4) and nw in (2, 4) and depth in (1, 2, 4)
-        assert rt * upw * depth <= 8
+        assert upw in (1, 2, 4) and depth in (1, 2, 4, 8)
+        assert rt * upw <= 8 and rt * upw * depth <= 16
         groups = K // 128
-        assert groups % (ks * upw) == 0
-        assert (groups // ks // upw) % depth == 0
+        assert groups % (ks * kw * upw) == 0
+        assert (groups // ks // kw // upw) % depth == 0
         R = 1 << (M - 1).bit_length()
-        assert (K // ks) * R * 2 + (K // ks // 128) * 64 <= 160 * 1024
+        red = nw * rt * 4 * 64 * 4 if kw > 1 else 0
+        assert (K // ks) * R * 2 + (K // ks // 128) * 64 + red <= 160 * 1024
 
 
 @pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
