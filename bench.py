@@ -1,7 +1,8 @@
 """Decode throughput of the Qwen3-8B-shaped hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--format bf16|w4a16|w8a16]
-                    [--batch C] [--prompt-len L] [--extra] [--no-cpu-baseline]
+                    [--batch C] [--prompt-len L] [--no-extra] [--no-kernels]
+                    [--no-cpu-baseline]
 
 A step is one hipGraph-replayed decode step of C sequences (BASELINE
 configuration 4: Qwen3-8B shape, 36 layers, random-init weights N(0, 0.02),
@@ -16,13 +17,21 @@ The JSON line also carries:
   events on its own stream: a hipGraph of one step's GEMM launches (36 x
   {qkv, o, gate|up, down} + lm_head, the step's own weights and buffers) is
   replayed and timed; achieved = algorithmic bytes of those launches / time.
-- extra (unless --no-extra): other batch sizes and formats, and the batched
-  prefill (forward_prefill_batch) of C prompts of L random ids: ms per call
-  and prompt tokens per second.
-- cpu_baseline: the CPU oracle of the reference's path (oracle/qwen3_ref.py,
-  fp32 torch on the host cores) on a bounded sample of the same workload
-  (C sequences at context L, a few decode steps of a few layers plus the
-  lm_head), scaled to the 36-layer step.
+  `in_step` is the same launches' time inside the captured step, read from
+  the committed rocprofv3 summary of that step; `traffic` the HBM bytes from
+  the committed FETCH_SIZE / WRITE_SIZE summary.
+- extra (unless --no-extra): the reference's decode_batch protocol (one
+  host copy per step) at the headline size, other batch sizes and formats
+  (W4A16 and W8A16 at C=8 with their own GEMM rooflines, configuration 5),
+  the batched prefill and configuration 4 end to end through the Engine.
+- extra.kernels (unless --no-kernels): the isolated kernels at
+  configurations 2 (K3, K1, K2), 5 (K3 + combine over one layer's pages at
+  C=8 and C=64) and 3 (int4 / int8 GEMM at every shape and M = 1/8/64/256,
+  HBM and MFMA fractions).
+- cpu_baseline: BASELINE configuration 1 run whole on the CPU oracle of the
+  reference's path (oracle/qwen3_ref.py, fp32 torch on the host cores),
+  the CPU oracles of the kernels at configuration 2/3 shapes, and the GPU
+  path on the same configuration-1 workload.
 """
 from __future__ import annotations
 
@@ -36,6 +45,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0     # dense bf16 MFMA (the int4 / int8 paths compute in bf16)
 
 
 def _log(msg: str) -> None:
@@ -63,8 +73,28 @@ def measured_traffic(fmt: str, batch: int):
     return None
 
 
+def in_step_gemm(fmt: str, batch: int, nbytes: int):
+    """The GEMM launches' time inside the captured step, from the committed
+    rocprofv3 kernel-trace summary of that step (the line's `achieved` times
+    them back to back in a graph of their own): µs per step and the same
+    bytes' fraction of peak, or None when no such summary exists."""
+    path = os.path.join(ROOT, "profiles", f"decode_{fmt}_C{batch}_step_breakdown.txt")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("gemm_in_step_us_per_step:"):
+                    us = float(line.split(":", 1)[1])
+                    return {"us_per_step": us, "frac": round(nbytes / (us * 1e-6) / 1e9 /
+                                                             HBM_PEAK_GBS, 4),
+                            "source": os.path.relpath(path, ROOT)}
+    except OSError:
+        pass
+    return None
+
+
 def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int, seed: int,
-                   tune: bool = True, prompt_lens: list[int] | None = None):
+                   tune: bool = True, prompt_lens: list[int] | None = None,
+                   tilings: dict | None = None):
     import torch
 
     from acorninfer_amd.cache.pager import BlockAllocator, PagedCacheView, PagedKVCache
@@ -77,7 +107,14 @@ def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int,
     _log(f"model {fmt}: {model.weight_bytes() / 1e9:.3f} GB weights in "
          f"{time.perf_counter() - t0:.1f} s")
     report = {}
-    if tune:
+    if tilings is not None:
+        # a fixed choice (e.g. an unprofiled run's, for a profiled one)
+        from acorninfer_amd.ops.quant_gemm import Tiling
+        model.tilings[batch] = {k: Tiling(*v) for k, v in tilings.items() if k != "swiglu"}
+        model.swiglu_choice[batch] = bool(tilings.get("swiglu", True))
+        report = {k: {"tiling": tuple(v), "us": float("nan"), "bytes": 1}
+                  for k, v in model.tilings[batch].items()}
+    elif tune:
         t0 = time.perf_counter()
         report = model.tune(batch)
         _log(f"tuned C={batch} in {time.perf_counter() - t0:.1f} s: " + ", ".join(
@@ -118,6 +155,24 @@ def time_decode(runner, views, first, steps: int, warmup: int, sampling=None):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     return dt, log
+
+
+def time_decode_batch(runner, views, first, steps: int):
+    """The reference's step protocol (DecodeGraphRunner.decode_batch: the
+    step's tokens come back to the host after every step) over `steps`
+    steps; seconds."""
+    import torch
+    from types import SimpleNamespace
+    seqs = [SimpleNamespace(generated_ids=[t]) for t in first]
+    runner.decode_batch(seqs, views)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        toks = runner.decode_batch(seqs, views)
+        for s_, t in zip(seqs, toks):
+            s_.generated_ids.append(t)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
 
 
 def prefill_benchmark(model, cfg, batch: int, prompt_len: int, seed: int, reps: int = 3):
@@ -191,6 +246,12 @@ def engine_benchmark(model, cfg, concurrency: int, prompt_len: int, new_tokens: 
     return concurrency * new_tokens / dt, ttft
 
 
+def gemm_step_bytes(model, batch: int) -> int:
+    """Algorithmic bytes of one decode step's GEMM launches."""
+    lins = [lin for lw in model.layers for lin in (lw.qkv, lw.o, lw.gate_up, lw.down)]
+    return sum(_gemm_bytes(lin, batch) for lin in lins + [model.lm_head])
+
+
 def gemm_roofline(model, runner, batch: int, reps: int = 5):
     """Time one step's GEMM launches (hipGraph on a private stream, HIP events
     on that stream). Returns (achieved GB/s, per-step bytes, per-step µs,
@@ -257,15 +318,28 @@ def _time_graph(body, reps: int = 10) -> float:
 
 
 def kernel_benchmarks(seed: int = 23, only_attention: bool = False,
-                      attn_splits: list[int] | None = None) -> dict:
-    """Isolated kernels at BASELINE configurations 2 and 3 (algorithmic bytes
-    / time, HIP events around hipGraph replays)."""
+                      attn_splits: list[int] | None = None, gemm_ms=(1, 8, 64, 256),
+                      with_attention: bool = True) -> dict:
+    """Isolated kernels at BASELINE configurations 2, 3 and 5 (algorithmic
+    bytes / time, HIP events around hipGraph replays)."""
+    out = {}
+    if with_attention or only_attention:
+        out.update(attention_benchmarks(seed, attn_splits))
+    if only_attention:
+        return out
+    if with_attention:
+        out.update(norm_benchmarks(seed))
+    out.update(gemm_benchmarks(seed, gemm_ms))
+    return out
+
+
+def attention_benchmarks(seed: int, attn_splits: list[int] | None = None) -> dict:
+    """K3 (+ combine) at configuration 2 and at configuration 5's contexts."""
     import torch
 
     from acorninfer_amd import _lib
     from acorninfer_amd._lib import lib, ptr
-    from acorninfer_amd.models.qwen3 import QLinear, attention_splits
-    from acorninfer_amd.ops.quant_gemm import candidates
+    from acorninfer_amd.models.qwen3 import attention_splits
 
     out = {}
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -311,8 +385,55 @@ def kernel_benchmarks(seed: int = 23, only_attention: bool = False,
                          "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "splits": S,
                          "mean_ctx": round(float(lens.float().mean()), 1)}
     del pools
-    if only_attention:
-        return out
+    # ---- K3 (+ combine) at configuration 5's long contexts: one layer's pages
+    # for C sequences of U[1024, 8192] tokens (the decode step's split rule)
+    for C in (8, 64):
+        clens = torch.randint(1024, 8193, (C,), generator=torch.Generator().manual_seed(seed + 5))
+        npg = [-(-int(L) // P) for L in clens]
+        nb5 = sum(npg) + 1
+        w5 = -(-8193 // P)
+        perm5 = torch.randperm(nb5, generator=torch.Generator().manual_seed(seed + 6))
+        tb5 = torch.zeros(C, w5, dtype=torch.int32)
+        o = 0
+        for b in range(C):
+            tb5[b, :npg[b]] = perm5[o:o + npg[b]].to(torch.int32)
+            o += npg[b]
+        kp5 = torch.empty(nb5, P, KV, D, device="cuda", dtype=torch.bfloat16).normal_(generator=g)
+        vp5 = torch.empty_like(kp5).normal_(generator=g)
+        q5 = torch.randn(C, H, D, device="cuda", generator=g).bfloat16()
+        o5 = torch.empty_like(q5)
+        S5 = attention_splits(C, KV, w5)
+        acc5 = torch.empty(C * H * S5 * D, device="cuda")
+        ml5 = torch.empty(2 * C * H * S5, device="cuda")
+        tb5c, ln5 = tb5.cuda(), clens.to(torch.int32).cuda()
+
+        def k3c5(st):
+            for _ in range(4):
+                _lib.check(lib().acorn_paged_attention(
+                    ptr(q5), ptr(kp5), ptr(vp5), ptr(tb5c), ptr(ln5), ptr(o5), ptr(acc5),
+                    ptr(ml5), C, H, KV, D, P, nb5, w5, S5, D ** -0.5, st_code, st.cuda_stream),
+                    "K3")
+        us5 = _time_graph(k3c5, 5) / 4
+        nb = int(clens.sum()) * KV * D * 2 * 2 + 2 * C * H * D * 2 + 4 * sum(npg) + 4 * C
+        out[f"K3_config5_C{C}"] = {"us": round(us5, 2), "bytes": nb,
+                                   "GBps": round(nb / us5 / 1e3, 1),
+                                   "frac": round(nb / us5 / 1e3 / HBM_PEAK_GBS, 4), "splits": S5,
+                                   "mean_ctx": round(float(clens.float().mean()), 1)}
+        del kp5, vp5, acc5, ml5
+        torch.cuda.empty_cache()
+    return out
+
+
+def norm_benchmarks(seed: int) -> dict:
+    """K1 and K2 at configuration-2 sizes (latency-bound: µs per call)."""
+    import torch
+
+    from acorninfer_amd import _lib
+    from acorninfer_amd._lib import lib, ptr
+
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(seed + 2)
+    lens = torch.randint(512, 4097, (8,), generator=torch.Generator().manual_seed(seed))
     # ---- K1 / K2 at configuration-2 sizes (latency-bound: µs) ----------
     x = torch.randn(8, 4096, device="cuda", generator=g).bfloat16()
     res = torch.randn(8, 4096, device="cuda", generator=g).bfloat16()
@@ -337,7 +458,25 @@ def kernel_benchmarks(seed: int = 23, only_attention: bool = False,
                 ptr(qq), ptr(kk), 8, 32, 8, 128, ptr(wq), ptr(wq), 1e-6, ptr(pos), 1,
                 ptr(invf), _lib.BF16, _lib.BF16, st.cuda_stream), "K2")
     out["K2_qknorm_rope_us"] = round(_time_graph(k2, 5) / 100, 2)
+    return out
+
+
+def gemm_benchmarks(seed: int, gemm_ms=(1, 8, 64, 256), fixed: dict | None = None) -> dict:
+    """The int4 / int8 GEMM at configuration 3's shapes and M. `fixed` maps
+    "{w4|w8}_{shape}_M{M}" to a tiling to time instead of searching (a
+    profiled run takes an unprofiled run's choice)."""
+    import torch
+
+    from acorninfer_amd import _lib
+    from acorninfer_amd.models.qwen3 import QLinear
+    from acorninfer_amd.ops.quant_gemm import Tiling, candidates
+
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(seed + 3)
     # ---- quant GEMM, configuration 3 -------------------------------------
+    # int4 in the decode model's block layout and int8 per channel; every
+    # candidate tiling is timed once (one graph of 16 launches over distinct
+    # weights), the fastest four again with 64 launches x 3 replays
     shapes = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (24576, 4096),
               "down": (4096, 12288)}
     for fmt_name, wf in (("w4", _lib.WFMT_W4), ("w8", _lib.WFMT_W8)):
@@ -356,79 +495,193 @@ def kernel_benchmarks(seed: int = 23, only_attention: bool = False,
                                         generator=g)
                     sc = (0.005 + 0.015 * torch.rand(n, device="cuda", generator=g)).half()
                     lins.append(QLinear(wf, wq8, n, k, sc))
-            for M in (1, 8, 64, 256):
+            for M in gemm_ms:
                 xm = torch.randn(M, k, device="cuda", generator=g).bfloat16()
-                best = None
-                cands = candidates(M, n, k, lins[0].fmt)
-                for c in cands:
-                    t = lins[0].plan(M, c)[0]
+
+                def timed(t, nl, reps):
                     part = torch.empty(t.ksplit, M, n, device="cuda")
                     ob = torch.empty(M, n, device="cuda").bfloat16()
 
-                    nl = max(64, len(lins))
-
-                    def gemm(st, t=t, part=part, ob=ob, nl=nl):
+                    def gemm(st):
                         for i in range(nl):
                             lins[i % len(lins)].launch(xm, M, t, out=ob, part=part,
                                                        stream=st.cuda_stream)
-                    us = _time_graph(gemm, 3) / nl
-                    if best is None or us < best[0]:
-                        best = (us, t)
+                    return _time_graph(gemm, reps) / nl
+
+                key = f"{fmt_name}_{name}_M{M}"
+                if fixed is not None:
+                    if key not in fixed:
+                        continue
+                    first = [(0.0, Tiling(*fixed[key]))]
+                else:
+                    first = sorted((timed(lins[0].plan(M, c)[0], 16, 1), c)
+                                   for c in candidates(M, n, k, lins[0].fmt))
+                best = min((timed(lins[0].plan(M, c)[0], 64, 3), c) for _, c in first[:4])
+                t = lins[0].plan(M, best[1])[0]
                 nb = lins[0].nbytes() + 2 * M * k + 2 * M * n
                 flops = 2 * M * n * k
-                out[f"gemm_{fmt_name}_{name}_M{M}"] = {
+                out[f"gemm_{key}"] = {
                     "us": round(best[0], 2), "GBps": round(nb / best[0] / 1e3, 1),
                     "frac_hbm": round(nb / best[0] / 1e3 / HBM_PEAK_GBS, 4),
-                    "TFLOPs": round(flops / best[0] / 1e6, 2), "tiling": tuple(best[1])}
+                    "TFLOPs": round(flops / best[0] / 1e6, 2),
+                    "frac_mfma": round(flops / best[0] / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "tiling": tuple(t), "candidates": len(first)}
             del lins
             torch.cuda.empty_cache()
     return out
 
 
-def cpu_baseline(cfg, batch: int, prompt_len: int, layers: int = 2, steps: int = 2):
-    """The CPU oracle (fp32 torch) on a bounded sample of the same step:
-    `layers` of the 36 layers plus the lm_head, `steps` decode steps of
-    `batch` sequences at context `prompt_len`; the per-step time is scaled to
-    36 layers."""
+def cpu_baseline(seed: int = 20261027, new_tokens: int = 32, prompt_len: int = 32) -> dict:
+    """BASELINE configuration 1 on the CPU oracle of the reference's path
+    (oracle/qwen3_ref.py: the SDPA decode path and greedy loop of
+    generate.py:55-110, fp32 torch on the host cores): the Qwen3-0.6B-shaped
+    model (28 layers, fp32 weights N(0, 0.02), norms 1), batch 1, a prompt of
+    `prompt_len` random ids, `new_tokens` greedy tokens, EOS disabled. tok/s
+    is the reference's formula (bench.py:68-99): generated tokens / (time of
+    the last token - submit), prefill included; decode-only tok/s beside it.
+    Also the CPU oracles of the kernels at configuration 2 / 3 shapes (µs per
+    call, median of a few calls): K3 paged attention, K1, K2, and the
+    dequantise + matmul GEMM anchors at M = 8."""
+    import numpy as np
     import torch
 
+    from acorninfer_amd.config import Qwen3Config
     from acorninfer_amd.models.qwen3 import random_state_dict
+    from oracle import ops_ref, quant_ref
     from oracle.qwen3_ref import Qwen3Ref
 
     threads = torch.get_num_threads()
-    sub = cfg.with_layers(layers)
-    sd = random_state_dict(sub, seed=5, std=0.02, dtype=torch.float32)
-    ref = Qwen3Ref(sub, sd, torch.float32)
+    t_all = time.perf_counter()
+    cfg = Qwen3Config.qwen3_0_6b()
+    sd = random_state_dict(cfg, seed=seed, std=0.02, dtype=torch.float32)
+    ref = Qwen3Ref(cfg, sd, torch.float32)
     del sd
-    g = torch.Generator().manual_seed(6)
-    shape = (batch, cfg.num_key_value_heads, prompt_len, cfg.head_dim)
-    cache = [[torch.randn(*shape, generator=g), torch.randn(*shape, generator=g)]
-             for _ in range(layers)]
-    ids = torch.randint(0, cfg.vocab_size, (batch, 1), generator=g)
-    # split the step into the layer part and the lm_head part
-    t_total = 0.0
-    for _ in range(steps):
+    prompt = torch.randint(0, cfg.vocab_size, (prompt_len,),
+                           generator=torch.Generator().manual_seed(seed + 3)).tolist()
+    with torch.no_grad():
+        cache = ref.new_cache()
         t0 = time.perf_counter()
-        ref.forward(ids, cache)
-        t_total += time.perf_counter() - t0
-    per_step_sample = t_total / steps
-    h = torch.randn(batch, 1, cfg.hidden_size, generator=g)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        ref._linear(h, "lm_head")
-    t_head = (time.perf_counter() - t0) / steps
-    t_layers = max(per_step_sample - t_head, 0.0)
-    t_step = t_layers * cfg.num_hidden_layers / layers + t_head
+        last = ref.forward(torch.tensor([prompt]), cache, num_logits_to_keep=1)[0, -1]
+        t_first = time.perf_counter()
+        ids = [int(last.argmax())]
+        for _ in range(new_tokens - 1):
+            last = ref.forward(torch.tensor([[ids[-1]]]), cache)[0, -1]
+            ids.append(int(last.argmax()))
+        t_last = time.perf_counter()
+    del ref, cache
+
+    def med_us(fn, reps=3):
+        fn()
+        ts = []
+        for _ in range(reps):
+            a = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - a)
+        return round(1e6 * sorted(ts)[len(ts) // 2], 1)
+
+    kernels = {}
+    g = torch.Generator().manual_seed(seed + 4)
+    # K3 at configuration 2
+    B, H, KV, D, P, NB = 8, 32, 8, 128, 16, 4096
+    lens = torch.randint(512, 4097, (B,), generator=g)
+    perm = torch.randperm(NB, generator=g)
+    tables = torch.zeros(B, 256, dtype=torch.int32)
+    o = 0
+    for b in range(B):
+        n = -(-int(lens[b]) // P)
+        tables[b, :n] = perm[o:o + n].to(torch.int32)
+        o += n
+    kp = torch.randn(NB, P, KV, D, generator=g).bfloat16()
+    vp = torch.randn(NB, P, KV, D, generator=g).bfloat16()
+    q = torch.randn(B, H, D, generator=g).bfloat16()
+    kernels["K3_config2_us"] = med_us(lambda: ops_ref.paged_attention_ref(q, kp, vp, tables, lens))
+    del kp, vp
+    x = torch.randn(8, 4096, generator=g).bfloat16()
+    r = torch.randn(8, 4096, generator=g).bfloat16()
+    w = torch.ones(4096).bfloat16()
+    kernels["K1_8x4096_us"] = med_us(lambda: ops_ref.fused_add_rmsnorm_ref(x, r, w, 1e-6), 10)
+    kk = torch.randn(8, 8, 1, 128, generator=g).bfloat16()
+    qq = torch.randn(8, 32, 1, 128, generator=g).bfloat16()
+    wq = torch.ones(128).bfloat16()
+    invf = ops_ref.inv_freq_ref(128, 1e6)
+    pos = (lens - 1).long()
+    kernels["K2_qknorm_rope_us"] = med_us(
+        lambda: ops_ref.qknorm_rope_ref(qq, kk, wq, wq, 1e-6, pos, invf), 10)
+    # GEMM anchors at configuration 3, M = 8: dequantise (numpy) + fp32 matmul
+    rng = np.random.default_rng(seed + 5)
+    xm = torch.randn(8, 12288, generator=g)
+    for name, (n, k) in {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (24576, 4096),
+                         "down": (4096, 12288)}.items():
+        u = rng.integers(0, 16, (n, k), dtype=np.uint8)
+        s4 = (0.005 + 0.015 * rng.random((n, k // 128))).astype(np.float16)
+        xs = xm[:, :k]
+        kernels[f"gemm_w4_{name}_M8_us"] = med_us(
+            lambda: xs @ torch.from_numpy(quant_ref.dequant_w4_sym_ref(u, s4)).T, 1)
+        q8 = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        s8 = (0.005 + 0.015 * rng.random(n)).astype(np.float16)
+        kernels[f"gemm_w8_{name}_M8_us"] = med_us(
+            lambda: xs @ torch.from_numpy(quant_ref.dequant_w8_ref(q8, s8)).T, 1)
+        del u, q8
     return {
-        "value": round(batch / t_step, 4),
+        "value": round(new_tokens / (t_last - t0), 3),
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle/qwen3_ref.py fp32 on {threads} host threads: {steps} decode steps "
-                   f"of {batch} sequences at context {prompt_len}, {layers} of "
-                   f"{cfg.num_hidden_layers} layers + lm_head, scaled to "
-                   f"{cfg.num_hidden_layers} layers ({t_step:.2f} s/step)"),
+        "sample": (f"BASELINE configuration 1 whole: oracle/qwen3_ref.py (the reference's SDPA "
+                   f"decode path) fp32 on {threads} host threads, Qwen3-0.6B shape (28 layers), "
+                   f"batch 1, prompt {prompt_len} random ids, {new_tokens} greedy tokens; "
+                   f"tok/s = tokens / (last token - submit), prefill included"),
+        "decode_only_tok_s": round((new_tokens - 1) / (t_last - t_first), 3),
+        "ttft_ms": round(1e3 * (t_first - t0), 1),
+        "kernels_us": kernels,
+        "wall_s": round(time.perf_counter() - t_all, 1),
     }
+
+
+def gpu_config1(seed: int = 20261027, new_tokens: int = 32, prompt_len: int = 32) -> dict:
+    """The same configuration-1 run on the GPU path (fp32 parity kernels and
+    the bf16 production kernels): prefill of the prompt, then the
+    graph-captured step for the remaining tokens; tok/s with the CPU
+    baseline's formula."""
+    import torch
+
+    from acorninfer_amd.cache.pager import BlockAllocator, PagedCacheView, PagedKVCache
+    from acorninfer_amd.config import Qwen3Config
+    from acorninfer_amd.engine.graph_runner import DecodeGraphRunner
+    from acorninfer_amd.models.qwen3 import Qwen3DecodeModel, random_state_dict
+    from types import SimpleNamespace
+
+    cfg = Qwen3Config.qwen3_0_6b()
+    prompt = torch.randint(0, cfg.vocab_size, (prompt_len,),
+                           generator=torch.Generator().manual_seed(seed + 3)).tolist()
+    out = {}
+    for dtype, tag in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        sd = random_state_dict(cfg, seed=seed, std=0.02, dtype=dtype, device="cuda")
+        model = Qwen3DecodeModel.from_state_dict(cfg, sd, dtype=dtype, device="cuda")
+        del sd
+        alloc = BlockAllocator(16)
+        cache = PagedKVCache(cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim, 16,
+                             alloc, "cuda", dtype)
+        runner = DecodeGraphRunner(model, cache, alloc, max_model_len=prompt_len + new_tokens + 8,
+                                   buckets=(1,))
+        times = []
+        for rep in range(2):                     # the first run captures the graph
+            view = PagedCacheView(cache)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            logits = model.forward_prefill_batch(torch.tensor([prompt], device="cuda"), [view],
+                                                 real_lens=[prompt_len])
+            ids = [int(logits[0].argmax())]
+            for _ in range(new_tokens - 1):
+                ids.append(runner.decode_batch([SimpleNamespace(generated_ids=ids)], [view])[0])
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+            for blk in view.table:
+                alloc.free(blk)
+        out[f"config1_{tag}_tok_s"] = round(new_tokens / times[-1], 2)
+        del model, runner, cache
+        torch.cuda.empty_cache()
+    return out
 
 
 def main() -> None:
@@ -446,14 +699,26 @@ def main() -> None:
     ap.add_argument("--no-extra", action="store_true", help="only the C=8 bf16 headline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-tune", action="store_true", help="use the planner's default tilings")
-    ap.add_argument("--kernels", action="store_true",
-                    help="also time the isolated kernels at configurations 2 and 3")
+    ap.add_argument("--tilings", default="",
+                    help="JSON {projection: [rt, upw, nw, ksplit, tpw], 'swiglu': bool} for the "
+                         "headline workload instead of tuning (a profiled run takes an "
+                         "unprofiled run's choice: the profiler distorts the tuner's timings)")
+    ap.add_argument("--no-kernels", action="store_true",
+                    help="skip the isolated kernels at configurations 2, 3 and 5")
     ap.add_argument("--splits", default="",
                     help="with --mode attention: comma-separated K3 split counts to time")
-    ap.add_argument("--mode", default="full", choices=["full", "step", "attention", "copy"],
+    ap.add_argument("--mode", default="full",
+                    choices=["full", "step", "attention", "kernels", "copy"],
                     help="profiling workloads: 'step' = decode steps only (no JSON line), "
-                         "'attention' = K3 at configuration 2 only, 'copy' = the 1 GiB "
+                         "'attention' = K3 at configuration 2 only, 'kernels' = the isolated "
+                         "kernels only (configurations 2, 3, 5), 'copy' = the 1 GiB "
                          "copy that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--gemm-m", default="",
+                    help="with --mode kernels: comma-separated M of the configuration-3 GEMMs "
+                         "only (no attention / norm kernels)")
+    ap.add_argument("--gemm-tilings", default="",
+                    help="with --mode kernels --gemm-m: JSON {'{w4|w8}_{shape}_M{M}': tiling} "
+                         "timed instead of searched")
     ap.add_argument("--seed", type=int, default=20261027)
     args = ap.parse_args()
 
@@ -474,6 +739,14 @@ def main() -> None:
         torch.cuda.synchronize()
         _log("copied 1 GiB x 5")
         return
+    if args.mode == "kernels":
+        ms = tuple(int(m) for m in args.gemm_m.split(",")) if args.gemm_m else (1, 8, 64, 256)
+        if args.gemm_tilings:
+            print(json.dumps(gemm_benchmarks(23, ms, json.loads(args.gemm_tilings))), flush=True)
+        else:
+            print(json.dumps(kernel_benchmarks(gemm_ms=ms, with_attention=not args.gemm_m)),
+                  flush=True)
+        return
     if args.mode == "attention":
         sweep = [int(x) for x in args.splits.split(",")] if args.splits else None
         _log(f"K3 configuration 2: {kernel_benchmarks(only_attention=True, attn_splits=sweep)}")
@@ -482,16 +755,23 @@ def main() -> None:
     if args.layers:
         cfg = cfg.with_layers(args.layers)
     total = args.warmup + args.steps
-    model, cache, runner, views, first = build_workload(cfg, args.format, args.batch,
-                                                        args.prompt_len, total, args.seed,
-                                                        tune=not args.no_tune)
+    # room for the decode_batch protocol's steps after the timed decode_loop ones
+    model, cache, runner, views, first = build_workload(
+        cfg, args.format, args.batch, args.prompt_len, total + args.steps + 2, args.seed,
+        tune=not args.no_tune,
+        tilings=json.loads(args.tilings) if args.tilings else None)
+    tilings_arg = json.dumps({**{k: list(v) for k, v in model.tilings.get(args.batch, {}).items()},
+                              "swiglu": model.fused_swiglu(args.batch)}, separators=(",", ":"))
+    _log(f"tilings of this run (--tilings): {tilings_arg}")
     _log(f"graph captured for C={args.batch}; warmup {args.warmup}, timed {args.steps}")
     dt, log = time_decode(runner, views, first, args.steps, args.warmup)
     tok_s = args.batch * args.steps / dt
     ms = dt * 1e3 / args.steps
     _log(f"decode: {tok_s:.1f} tok/s, {ms:.3f} ms/step; last tokens {log[-1].tolist()}")
     if args.mode == "step":
+        _log(f"GEMM algorithmic bytes per step: {gemm_step_bytes(model, args.batch)}")
         return
+    dtb = time_decode_batch(runner, views, log[-1].tolist(), args.steps)
     gbs, nbytes, us, nl = gemm_roofline(model, runner, args.batch)
     _log(f"GEMM: {nl} launches/step, {nbytes / 1e9:.3f} GB, {us:.1f} us -> {gbs:.0f} GB/s")
     step_bytes = model.weight_bytes() + sum(
@@ -500,6 +780,8 @@ def main() -> None:
     extra = {"step_hbm_bound_ms": round(step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3, 4),
              "step_roofline_frac": round(step_bytes / (HBM_PEAK_GBS * 1e9) / (dt / args.steps), 4),
              "gemm_us_per_step": round(us, 2), "gemm_launches_per_step": nl,
+             f"{args.format}_C{args.batch}_decode_batch_tok_s": round(args.batch * args.steps / dtb, 2),
+             "tilings_arg": tilings_arg,
              "tuned": {k: {"tiling": v["tiling"], "us": v["us"],
                            "GBps": round(v["bytes"] / v["us"] / 1e3, 1)}
                        for k, v in model.tune_report.items()}}
@@ -520,13 +802,24 @@ def main() -> None:
              f"end to end, TTFT {ttft:.1f} ms")
         del model
         torch.cuda.empty_cache()
-        for fmt, c in (("bf16", 1), ("w4a16", 8), ("w4a16", 1)):
+        for fmt, c in (("bf16", 1), ("w4a16", 8), ("w4a16", 1), ("w8a16", 8)):
             m2, c2, r2, v2, f2 = build_workload(cfg, fmt, c, args.prompt_len, total, args.seed,
                                                 tune=not args.no_tune)
             dt2, _ = time_decode(r2, v2, f2, args.steps, args.warmup)
             extra[f"{fmt}_C{c}_tok_s"] = round(c * args.steps / dt2, 2)
             extra[f"{fmt}_C{c}_ms_per_step"] = round(dt2 * 1e3 / args.steps, 4)
             _log(f"{fmt} C={c}: {c * args.steps / dt2:.1f} tok/s")
+            if c == 8 and fmt != "bf16":
+                # the quantised formats' own GEMM roofline (the line's is bf16's)
+                g2, nb2, us2, nl2 = gemm_roofline(m2, r2, c)
+                extra[f"{fmt}_C8_gemm_roofline"] = {
+                    "achieved_GBps": round(g2, 1), "frac": round(g2 / HBM_PEAK_GBS, 4),
+                    "bytes_per_step": nb2, "us_per_step": round(us2, 2), "launches": nl2,
+                    "traffic": measured_traffic(fmt, c), "in_step": in_step_gemm(fmt, c, nb2),
+                    "tilings_arg": json.dumps(
+                        {**{k: list(v) for k, v in m2.tilings.get(c, {}).items()},
+                         "swiglu": m2.fused_swiglu(c)}, separators=(",", ":"))}
+                _log(f"{fmt} C=8 GEMM: {nb2 / 1e9:.3f} GB in {us2:.1f} us -> {g2:.0f} GB/s")
             del m2, c2, r2
             torch.cuda.empty_cache()
         # configuration 4's largest concurrency: C=32, bf16, prompts of 512
@@ -554,15 +847,17 @@ def main() -> None:
                  f"{c * args.steps / dt2:.1f} tok/s")
             del m2, c2, r2
             torch.cuda.empty_cache()
-    if args.kernels:
+    if not args.no_kernels:
         t0 = time.perf_counter()
         extra["kernels"] = kernel_benchmarks()
         _log(f"kernel benchmarks in {time.perf_counter() - t0:.1f} s: {extra['kernels']}")
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
-        cpu = cpu_baseline(cfg, args.batch, args.prompt_len)
-        _log(f"cpu baseline {cpu['value']} tok/s in {time.perf_counter() - t0:.1f} s")
+        cpu = cpu_baseline()
+        cpu["gpu_same_workload"] = gpu_config1()
+        _log(f"cpu baseline (configuration 1) {cpu['value']} tok/s, GPU "
+             f"{cpu['gpu_same_workload']} in {time.perf_counter() - t0:.1f} s")
     line = {
         "metric": "decode tok/s Qwen3-8B C=1/8 (bf16, W4A16); kernel HBM GB/s vs 8 TB/s peak",
         "value": round(tok_s, 2),
@@ -583,8 +878,9 @@ def main() -> None:
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(args.format, args.batch),
-                     "kernel": "wgemm_kernel (all projections of one step)",
-                     "bytes_per_step": nbytes, "us_per_step": round(us, 2)},
+                     "kernel": "weight-streaming GEMMs (all projections of one step)",
+                     "bytes_per_step": nbytes, "us_per_step": round(us, 2),
+                     "in_step": in_step_gemm(args.format, args.batch, nbytes)},
         "cpu_baseline": cpu,
         "extra": extra,
     }
