@@ -696,10 +696,25 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
       const T* kb = k_pages + base + (spare ? 0 : v_off);
       const T* vb = v_pages + base + (spare ? 0 : v_off);
       const int vstep = spare ? 0 : tok_stride;
+      if constexpr (VW == 4) {
+        // D = 128: each instruction reads four tokens' whole 256-byte rows,
+        // read once per step, so with the non-temporal policy
 #pragma unroll
-      for (int j = 0; j < 4; ++j) __builtin_memcpy(ch.kr[j], kb + j * vstep, sizeof(ch.kr[j]));
+        for (int j = 0; j < 4; ++j) {
+          const u32x4_t kv4 = load_nt((const u32x4_t*)(kb + j * vstep));
+          const u32x4_t vv4 = load_nt((const u32x4_t*)(vb + j * vstep));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) __builtin_memcpy(ch.v[j], vb + j * vstep, sizeof(ch.v[j]));
+          for (int w = 0; w < 4; ++w) {
+            ch.kr[j][w] = kv4[w];
+            ch.v[j][w] = vv4[w];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) __builtin_memcpy(ch.kr[j], kb + j * vstep, sizeof(ch.kr[j]));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) __builtin_memcpy(ch.v[j], vb + j * vstep, sizeof(ch.v[j]));
+      }
     } else {
       // pages smaller than a chunk: one lookup per token, rows past the end
       // read as zero

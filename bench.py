@@ -415,6 +415,20 @@ def attention_benchmarks(seed: int, attn_splits: list[int] | None = None) -> dic
                     "K3")
         us5 = _time_graph(k3c5, 5) / 4
         nb = int(clens.sum()) * KV * D * 2 * 2 + 2 * C * H * D * 2 + 4 * sum(npg) + 4 * C
+        if attn_splits:
+            sweep = {}
+            for n in attn_splits:
+                acc5 = torch.empty(C * H * n * D, device="cuda")
+                ml5 = torch.empty(2 * C * H * n, device="cuda")
+
+                def k3n(st, n=n, acc5=acc5, ml5=ml5):
+                    for _ in range(4):
+                        _lib.check(lib().acorn_paged_attention(
+                            ptr(q5), ptr(kp5), ptr(vp5), ptr(tb5c), ptr(ln5), ptr(o5),
+                            ptr(acc5), ptr(ml5), C, H, KV, D, P, nb5, w5, n, D ** -0.5,
+                            st_code, st.cuda_stream), "K3")
+                sweep[n] = round(_time_graph(k3n, 5) / 4, 2)
+            out[f"K3_config5_C{C}_split_sweep_us"] = sweep
         out[f"K3_config5_C{C}"] = {"us": round(us5, 2), "bytes": nb,
                                    "GBps": round(nb / us5 / 1e3, 1),
                                    "frac": round(nb / us5 / 1e3 / HBM_PEAK_GBS, 4), "splits": S5,
