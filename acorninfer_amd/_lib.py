@@ -50,6 +50,8 @@ _SIGNATURES = {
                               _i64, _i64, _i64, _i64, _f32, _i32, _vp],
     "acorn_paged_attention_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                       _i64, _i64, _i64, _i64, _f32, _i32, _vp],
+    "acorn_paged_prefill_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                      _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _vp],
     "acorn_paged_attention_qkv": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                                   _vp, _vp, _f32, _vp, _vp, _i32, _i32, _vp],

@@ -1209,6 +1209,211 @@ int dispatch_d(int64_t D, int64_t rep, const void* q, const void* kp, const void
   return ACORN_ERR_UNSUPPORTED;
 }
 
+// ---------------------------------------------------------------------------
+// Prefill attention: query-tiled flash attention over the paged cache with a
+// causal mask, for a chunked prefill whose new rows' K/V are already in the
+// pool. Row j of sequence n (q row seq_row0[n] + j) sits at position
+// seq_pos0[n] + j and attends to that sequence's tokens 0 .. its position.
+// The decode K3's MFMA layout with the 16 columns of S^T = K Q^T being 16
+// consecutive query tokens of one head instead of the heads of one token:
+//  * a workgroup of QT*REP waves serves QT tiles of 16 query tokens x the REP
+//    q heads of one kv head; every wave walks the same 16-token key chunks
+//    (one page of the kv head's rows), so each chunk is fetched from HBM once
+//    per workgroup and the other waves read it from the caches;
+//  * per chunk: D/32 v_mfma_f32_16x16x32 for the scores, the online softmax
+//    per query column (lazy max), D/16 v_mfma_f32_16x16x16 for P V;
+//  * keys past a query's position are masked in the chunks that cross the
+//    diagonal; the first chunk always holds key 0, so every column's max is
+//    finite from the start.
+// A query tile reads its sequence's keys once per kv head: O(L^2 / 16) bytes
+// per prompt of L tokens, against O(L^2) for one decode row per token.
+template <typename T, int D, int REP, int QT>
+__global__ __launch_bounds__(QT * REP * kWave) void paged_prefill_kernel(
+    const T* __restrict__ q, const T* __restrict__ k_pages, const T* __restrict__ v_pages,
+    const int32_t* __restrict__ tables, const int32_t* __restrict__ seq_row0,
+    const int32_t* __restrict__ seq_pos0, const int32_t* __restrict__ seq_nq, T* __restrict__ out,
+    int R, int H, int KV, int P, int num_blocks, int table_stride, float scale_log2) {
+  constexpr int KB = D / 32, DPL = D / 16, VW = DPL / 2, CH = 16, DEPTH = 2;
+  constexpr int KPITCH = 2 * D + 16;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int kvh = blockIdx.y, n = blockIdx.z;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int r = lane >> 4, c = lane & 15;
+  const int hq = wid % REP, sub = wid / REP;
+  const int h = kvh * REP + hq;
+  const int pos0 = seq_pos0[n];
+  const int row0 = seq_row0[n];
+  // rows past q's R rows are not served (so bad metadata cannot reach past q / out)
+  const int nq = row0 < 0 || pos0 < 0 ? 0 : min(seq_nq[n], R - row0);
+  const int j0 = (blockIdx.x * QT + sub) * CH;        // this wave's first query row
+  const int wg_j0 = blockIdx.x * QT * CH;
+  if (wg_j0 >= nq) return;                            // uniform over the workgroup
+  const int nvalid = min(CH, nq - j0);
+  if (nvalid <= 0) return;                            // an idle wave of the last tile (no barriers here)
+  // keys of the workgroup's last query, so that all waves walk the same chunks
+  const int L = pos0 + min(wg_j0 + QT * CH, nq);
+  const int pc = pos0 + j0 + min(c, nvalid - 1);      // this column's position
+  const int32_t* trow = tables + (size_t)n * table_stride;
+  const int pshift = __builtin_ctz(P);
+  u32x4_t qb[KB];
+  {
+    const size_t qrow = (size_t)(row0 + j0 + min(c, nvalid - 1));
+#pragma unroll
+    for (int jb = 0; jb < KB; ++jb)
+      qb[jb] = *(const u32x4_t*)(q + (qrow * H + h) * D + 32 * jb + 8 * r);
+  }
+  uint8_t* kslab = smem + (size_t)wid * CH * KPITCH;
+  const int tok_stride = KV * D;
+  const int v_off = 4 * r * tok_stride + DPL * c;
+  struct Chunk {
+    uint32_t kr[4][VW];
+    uint32_t v[4][VW];
+  };
+  const int tlast = max(L - 1, 0) / CH * CH;
+  auto load_chunk = [&](int t0, Chunk& ch) {
+    const bool spare = t0 > tlast;
+    t0 = min(t0, tlast);
+    const unsigned pg0 = (unsigned)trow[min(t0 >> pshift, table_stride - 1)];
+    const int pg = __builtin_amdgcn_readfirstlane(pg0 < (unsigned)num_blocks ? (int)pg0 : 0);
+    const size_t base = ((size_t)pg * P + (t0 & (P - 1))) * tok_stride + (size_t)kvh * D;
+    const T* kb = k_pages + base + (spare ? 0 : v_off);
+    const T* vb = v_pages + base + (spare ? 0 : v_off);
+    const int vstep = spare ? 0 : tok_stride;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      __builtin_memcpy(ch.kr[jj], kb + jj * vstep, sizeof(ch.kr[jj]));
+      __builtin_memcpy(ch.v[jj], vb + jj * vstep, sizeof(ch.v[jj]));
+    }
+  };
+  float m = -INFINITY, l = 0.f;
+  f32x4_t acc[DPL];
+#pragma unroll
+  for (int jj = 0; jj < DPL; ++jj) acc[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](int t0, Chunk& ch) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      uint8_t* dst = kslab + (4 * r + jj) * KPITCH + 2 * DPL * c;
+#pragma unroll
+      for (int w = 0; w < VW; ++w) ((uint32_t*)dst)[w] = ch.kr[jj][w];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int jb = 0; jb < KB; ++jb)
+      sc = mfma16x16x32<T>(*(const u32x4_t*)(kslab + c * KPITCH + 2 * (32 * jb + 8 * r)), qb[jb], sc);
+    float s[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = sc[i] * scale_log2;
+    if (t0 + CH - 1 > pos0 + j0) {                 // the chunk crosses some column's diagonal
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kidx = t0 + 4 * r + i;
+        if (kidx > pc) s[i] = -INFINITY;
+        if (kidx >= L) {
+#pragma unroll
+          for (int w = 0; w < VW; ++w) ch.v[i][w] = 0u;
+        }
+      }
+    }
+    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    if (__builtin_amdgcn_ballot_w64(mx > m + kMaxSlack) != 0) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int jj = 0; jj < DPL; ++jj) acc[jj] *= alpha;
+    }
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pr[i] = round_to<T>(__builtin_amdgcn_exp2f(s[i] - m));
+      l += pr[i];
+    }
+    const u32x2_t pb = {pack2<T>(pr[0], pr[1]), pack2<T>(pr[2], pr[3])};
+#pragma unroll
+    for (int jj = 0; jj < DPL; ++jj) {
+      const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
+      const u32x2_t va = {__builtin_amdgcn_perm(ch.v[1][jj / 2], ch.v[0][jj / 2], sel),
+                          __builtin_amdgcn_perm(ch.v[3][jj / 2], ch.v[2][jj / 2], sel)};
+      acc[jj] = mfma16x16x16<T>(va, pb, acc[jj]);
+    }
+  };
+  Chunk cs[DEPTH];
+#pragma unroll
+  for (int i = 0; i < DEPTH; ++i) load_chunk(i * CH, cs[i]);
+  bool more = L > 0;
+  for (int t0 = 0; more; t0 += DEPTH * CH) {
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i) {
+      if (more) {
+        consume(t0 + i * CH, cs[i]);
+        load_chunk(t0 + (i + DEPTH) * CH, cs[i]);
+        more = t0 + (i + 1) * CH < L;
+      }
+    }
+  }
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  // lane (r, c) holds dims DPL (4 r + i) + jj of query column c
+  if (c < nvalid) {
+    const size_t orow = (size_t)(row0 + j0 + c) * H + h;
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t w[VW];
+#pragma unroll
+      for (int jj = 0; jj < VW; ++jj)
+        w[jj] = pack2<T>(acc[2 * jj][i] * inv, acc[2 * jj + 1][i] * inv);
+      __builtin_memcpy(out + orow * D + DPL * (4 * r + i), w, sizeof(w));
+    }
+  }
+}
+
+constexpr int kPrefillTiles = 2;   // 16-token query tiles per workgroup
+
+template <typename T, int D, int REP>
+int launch_prefill(const void* q, const void* kp, const void* vp, const int32_t* tables,
+                   const int32_t* row0, const int32_t* pos0, const int32_t* nq, void* out,
+                   int64_t N, int64_t R, int64_t max_nq, int64_t H, int64_t KV, int64_t P,
+                   int64_t num_blocks, int64_t table_stride, float scale, hipStream_t st) {
+  // 8 q heads per kv head: one tile per workgroup (16 waves would cap a wave at 128 VGPRs)
+  constexpr int QT = REP >= 8 ? 1 : kPrefillTiles;
+  const int64_t tiles = (max_nq + 16 * QT - 1) / (16 * QT);
+  const size_t lds = (size_t)QT * REP * 16 * (2 * D + 16);
+  auto kfn = paged_prefill_kernel<T, D, REP, QT>;
+  static bool lds_raised = false;
+  if (!lds_raised && lds > 64 * 1024) {
+    (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    lds_raised = true;
+  }
+  kfn<<<dim3((unsigned)tiles, (unsigned)KV, (unsigned)N), dim3(QT * REP * kWave), lds, st>>>(
+      (const T*)q, (const T*)kp, (const T*)vp, tables, row0, pos0, nq, (T*)out, (int)R, (int)H,
+      (int)KV, (int)P, (int)num_blocks, (int)table_stride, scale * kLog2e);
+  ACORN_LAUNCH_CHECK();
+  return ACORN_OK;
+}
+
+template <typename T, int D>
+int prefill_rep(int64_t rep, const void* q, const void* kp, const void* vp,
+                const int32_t* tables, const int32_t* row0, const int32_t* pos0,
+                const int32_t* nq, void* out, int64_t N, int64_t R, int64_t max_nq, int64_t H,
+                int64_t KV, int64_t P, int64_t num_blocks, int64_t ts, float scale,
+                hipStream_t st) {
+  switch (rep) {
+    case 1: return launch_prefill<T, D, 1>(q, kp, vp, tables, row0, pos0, nq, out, N, R, max_nq, H, KV, P, num_blocks, ts, scale, st);
+    case 2: return launch_prefill<T, D, 2>(q, kp, vp, tables, row0, pos0, nq, out, N, R, max_nq, H, KV, P, num_blocks, ts, scale, st);
+    case 4: return launch_prefill<T, D, 4>(q, kp, vp, tables, row0, pos0, nq, out, N, R, max_nq, H, KV, P, num_blocks, ts, scale, st);
+    case 8: return launch_prefill<T, D, 8>(q, kp, vp, tables, row0, pos0, nq, out, N, R, max_nq, H, KV, P, num_blocks, ts, scale, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
 }  // namespace
 
 extern "C" int acorn_paged_attention(const void* q, const void* k_pages, const void* v_pages,
@@ -1233,6 +1438,36 @@ extern "C" int acorn_paged_attention(const void* q, const void* k_pages, const v
     case ACORN_BF16: return dispatch_d<__bf16>(D, rep, q, k_pages, v_pages, tables, seq_lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, table_stride, num_splits, scale, st);
   }
   return ACORN_ERR_DTYPE;
+}
+
+extern "C" int acorn_paged_prefill_attention(const void* q, const void* k_pages,
+                                             const void* v_pages, const int32_t* tables,
+                                             const int32_t* seq_row0, const int32_t* seq_pos0,
+                                             const int32_t* seq_nq, void* out, int64_t N,
+                                             int64_t R, int64_t max_nq, int64_t H, int64_t KV,
+                                             int64_t D, int64_t P, int64_t num_blocks,
+                                             int64_t table_stride, float scale, int dtype,
+                                             void* stream) {
+  if (N < 0 || R < 0 || max_nq < 0 || H <= 0 || KV <= 0 || D <= 0 || P <= 0 ||
+      num_blocks <= 0 || table_stride < 1)
+    return ACORN_ERR_SHAPE;
+  if ((P & (P - 1)) != 0 || P % 16 != 0 || H % KV != 0) return ACORN_ERR_SHAPE;
+  if (KV > 65535 || N > 65535 || R > 0x7fffffff || max_nq > 0x7fffffff) return ACORN_ERR_SHAPE;
+  if (N == 0 || R == 0 || max_nq == 0) return ACORN_OK;
+  if (!q || !k_pages || !v_pages || !tables || !seq_row0 || !seq_pos0 || !seq_nq || !out)
+    return ACORN_ERR_VALUE;
+  const int64_t rep = H / KV;
+  hipStream_t st = (hipStream_t)stream;
+  if (D != 64 && D != 128) return ACORN_ERR_UNSUPPORTED;
+  switch (dtype) {
+    case ACORN_F16:
+      return D == 64 ? prefill_rep<_Float16, 64>(rep, q, k_pages, v_pages, tables, seq_row0, seq_pos0, seq_nq, out, N, R, max_nq, H, KV, P, num_blocks, table_stride, scale, st)
+                     : prefill_rep<_Float16, 128>(rep, q, k_pages, v_pages, tables, seq_row0, seq_pos0, seq_nq, out, N, R, max_nq, H, KV, P, num_blocks, table_stride, scale, st);
+    case ACORN_BF16:
+      return D == 64 ? prefill_rep<__bf16, 64>(rep, q, k_pages, v_pages, tables, seq_row0, seq_pos0, seq_nq, out, N, R, max_nq, H, KV, P, num_blocks, table_stride, scale, st)
+                     : prefill_rep<__bf16, 128>(rep, q, k_pages, v_pages, tables, seq_row0, seq_pos0, seq_nq, out, N, R, max_nq, H, KV, P, num_blocks, table_stride, scale, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
 }
 
 // ---------------------------------------------------------------------------

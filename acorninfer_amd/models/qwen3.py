@@ -40,6 +40,7 @@ from acorninfer_amd import _lib
 from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, check,
                                  dtype_code, lib, ptr, stream_ptr)
 from acorninfer_amd.config import Qwen3Config
+from acorninfer_amd.ops.paged_attention import prefill_supported
 from acorninfer_amd.quant import quantize as Q
 
 MI355X_CUS = 256
@@ -287,6 +288,9 @@ class Qwen3DecodeModel:
         # Switches with the reference's names (qwen3.py:487-489).
         self.attention_backend = "hip"
         self.fused_ops = True
+        # prefill attention as the query-tiled kernel where it is built for
+        # the shapes (False: K3 with one row per prompt token)
+        self.tiled_prefill = True
         # batch -> {projection name -> Tiling}, filled by tune()
         self.tilings: dict[int, dict] = {}
         self.swiglu_choice: dict[int, bool] = {}
@@ -371,14 +375,18 @@ class Qwen3DecodeModel:
 
     def step(self, buf: "StepBuffers", k_pool: torch.Tensor, v_pool: torch.Tensor,
              num_blocks: int, page_size: int, *, fused_attn: bool = True,
-             head_rows: torch.Tensor | None = None) -> torch.Tensor | None:
+             head_rows: torch.Tensor | None = None,
+             segments: "PrefillSegments | None" = None) -> torch.Tensor | None:
         """Launch one decode step on the current stream.
 
         fused_attn=False keeps the qkv epilogue (which writes every row's new
         k/v) and K3 as two launches; rows that attend to each other's new
         tokens (prefill rows of one sequence) need that order. head_rows:
         int64 row indices; only their logits are computed, [len, vocab] in
-        the activation dtype, returned instead of sampling.
+        the activation dtype, returned instead of sampling. segments: the
+        rows are runs of consecutive positions of a few sequences (a prefill
+        chunk); attention then runs as the query-tiled prefill kernel over
+        those runs (buf.tables / buf.lens unused) instead of one K3 row each.
 
         Reads buf.ids/positions/pages/slots/lens/tables and the sampling
         block (temperature 0 = greedy); writes buf.logits (bf16 [B, vocab]),
@@ -435,11 +443,19 @@ class Qwen3DecodeModel:
                     ptr(buf.slots), B, nq, nkv, D, page_size, num_blocks, ptr(lw.q_norm),
                     ptr(lw.k_norm), eps, ptr(buf.positions), ptr(self.inv_freq), dt, wdt, st),
                     "qkv_epilogue")
-                # K3
-                check(L.acorn_paged_attention(
-                    ptr(buf.q), kp, vp, ptr(buf.tables), ptr(buf.lens), ptr(buf.attn),
-                    ptr(buf.ws_acc), ptr(buf.ws_ml), B, nq, nkv, D, page_size, num_blocks,
-                    buf.max_pages, buf.num_splits, float(self.scale), dt, st), "K3")
+                if segments is not None:
+                    sg = segments
+                    check(L.acorn_paged_prefill_attention(
+                        ptr(buf.q), kp, vp, ptr(sg.tables), ptr(sg.row0), ptr(sg.pos0),
+                        ptr(sg.nq), ptr(buf.attn), sg.count, B, sg.max_nq, nq, nkv, D,
+                        page_size, num_blocks, sg.tables.shape[1], float(self.scale), dt, st),
+                        "prefill attention")
+                else:
+                    # K3
+                    check(L.acorn_paged_attention(
+                        ptr(buf.q), kp, vp, ptr(buf.tables), ptr(buf.lens), ptr(buf.attn),
+                        ptr(buf.ws_acc), ptr(buf.ws_ml), B, nq, nkv, D, page_size, num_blocks,
+                        buf.max_pages, buf.num_splits, float(self.scale), dt, st), "K3")
             # o projection -> K1 (reduce + residual add + post-attention norm)
             co = buf.cfgs["o"]
             lw.o.launch(buf.attn, B, co, part=buf.part_o, stream=st)
@@ -674,11 +690,14 @@ class Qwen3DecodeModel:
 
         The rows of all chunks are packed into one launch sequence of the
         decode step, one row per token: token p of a sequence is a row with
-        position p, KV target (table[p // P], p % P) and length p + 1, so K3
-        gives it causal attention over the cache. The qkv epilogue writes
-        every row's k/v before K3 runs (fused_attn=False), which is what lets
-        a row read the tokens of the same chunk before it. GEMMs run at
-        M = total rows; lm_head only for each chunk's last row."""
+        position p and KV target (table[p // P], p % P). The qkv epilogue
+        writes every row's k/v before attention runs (fused_attn=False),
+        which is what lets a row read the tokens of the same chunk before it.
+        Attention is the query-tiled prefill kernel over each sequence's run
+        of rows (causal over the cache, 16 query tokens per MFMA tile); for
+        shapes it is not built for (fp32, head_dim 16/32), K3 with one row
+        per token and length p + 1. GEMMs run at M = total rows; lm_head
+        only for each chunk's last row."""
         N, Lc = input_ids.shape
         if len(views) != N or len(starts) != N or len(chunk_lens) != N:
             raise ValueError(f"views/starts/chunk_lens must match the batch: N={N}, "
@@ -693,6 +712,9 @@ class Qwen3DecodeModel:
                 raise ValueError(f"forward_extend: view KV length {v.seq_len} != start {s}")
         cache = views[0].cache
         P = cache.page_size
+        cfg = self.cfg
+        tiled = self.tiled_prefill and prefill_supported(
+            self.dtype, cfg.head_dim, P, cfg.num_attention_heads, cfg.num_key_value_heads)
         targets = [v.reserve(n) for v, n in zip(views, chunk_lens)]
         W = max(len(v.table) for v in views)
         ids, pos, pages, slots, lens, tabs = [], [], [], [], [], []
@@ -704,15 +726,16 @@ class Qwen3DecodeModel:
             lens += list(range(s + 1, s + n + 1))
             row = torch.zeros(W, dtype=torch.int32)
             row[:len(v.table)] = torch.tensor(v.table, dtype=torch.int32)
-            tabs.append(row.expand(n, W))
+            tabs.append(row)
         R = len(pos)
         ids_all = torch.cat(ids)
         pos_all = torch.tensor(pos, dtype=torch.int64)
         pages_all = torch.tensor(pages, dtype=torch.int64)
         slots_all = torch.tensor(slots, dtype=torch.int64)
         lens_all = torch.tensor(lens, dtype=torch.int32)
-        tabs_all = torch.cat(tabs)
-        last = torch.tensor(chunk_lens, dtype=torch.int64).cumsum(0) - 1
+        seq_tabs = torch.stack(tabs)                                  # [N, W]
+        first = torch.tensor([0] + list(chunk_lens), dtype=torch.int64).cumsum(0)
+        last = first[1:] - 1
         dev = self.device
         # Rows run in blocks of at most EXTEND_MAX_ROWS, in order: a block's
         # layer-l attention reads the k/v that earlier blocks wrote at layer l,
@@ -722,25 +745,66 @@ class Qwen3DecodeModel:
             r1 = min(R, r0 + EXTEND_MAX_ROWS)
             Rb = r1 - r0
             # the step buffers of the last shape are kept (a prompt batch often repeats it)
-            key = (Rb, W)
+            # (the prefill kernel reads per-sequence tables: no per-row table)
+            key = (Rb, 1 if tiled else W)
             cached = getattr(self, "_extend_buf", None)
             if cached is None or cached[0] != key:
                 self._extend_buf = None
-                self._extend_buf = (key, self.buffers(Rb, W, prefill=True))
+                self._extend_buf = (key, self.buffers(Rb, key[1], prefill=True))
             buf = self._extend_buf[1]
             buf.ids.copy_(ids_all[r0:r1])
             buf.positions.copy_(pos_all[r0:r1])
             buf.pages.copy_(pages_all[r0:r1])
             buf.slots.copy_(slots_all[r0:r1])
-            buf.lens.copy_(lens_all[r0:r1])
-            buf.tables.copy_(tabs_all[r0:r1])
+            segs = None
+            if tiled:
+                segs = PrefillSegments.for_rows(first, starts, seq_tabs, r0, r1, dev)
+            else:
+                buf.lens.copy_(lens_all[r0:r1])
+                for i in range(N):                 # each sequence's table on its rows
+                    a, b = max(int(first[i]), r0), min(int(first[i + 1]), r1)
+                    if a < b:
+                        buf.tables[a - r0:b - r0].copy_(seq_tabs[i].expand(b - a, W))
             heads = last[(last >= r0) & (last < r1)] - r0
             outs.append(self.step(buf, cache.k_pool, cache.v_pool, cache.num_blocks, P,
-                                  fused_attn=False, head_rows=heads.to(dev)))
+                                  fused_attn=False, head_rows=heads.to(dev), segments=segs))
         for v, n in zip(views, chunk_lens):
             for li in range(self.cfg.num_hidden_layers):
                 v._lens[li] = v._lens.get(li, 0) + n
         return torch.cat(outs).float()
+
+
+@dataclass
+class PrefillSegments:
+    """The sequences of one block of prefill rows, as the prefill attention
+    kernel reads them: sequence n's rows are block rows row0[n] ..
+    row0[n] + nq[n] - 1 at positions pos0[n] + j, with block table tables[n]
+    (all int32 on the device)."""
+    tables: torch.Tensor    # [count, W]
+    row0: torch.Tensor      # [count]
+    pos0: torch.Tensor      # [count]
+    nq: torch.Tensor        # [count]
+    count: int
+    max_nq: int
+
+    @classmethod
+    def for_rows(cls, first: torch.Tensor, starts: list[int], seq_tabs: torch.Tensor,
+                 r0: int, r1: int, device) -> "PrefillSegments":
+        """Rows [r0, r1) of a packing where sequence i holds rows
+        first[i] .. first[i + 1] - 1 from KV position starts[i]."""
+        sel, row0, pos0, nq = [], [], [], []
+        for i in range(len(starts)):
+            a, b = max(int(first[i]), r0), min(int(first[i + 1]), r1)
+            if a < b:
+                sel.append(i)
+                row0.append(a - r0)
+                pos0.append(starts[i] + a - int(first[i]))
+                nq.append(b - a)
+        meta = torch.tensor([row0, pos0, nq], dtype=torch.int32)
+        blob = torch.cat([meta.reshape(-1), seq_tabs[sel].reshape(-1)]).to(device)
+        n = len(sel)
+        return cls(blob[3 * n:].view(n, seq_tabs.shape[1]), blob[0:n], blob[n:2 * n],
+                   blob[2 * n:3 * n], n, max(nq))
 
 
 def _dense_linear(w: torch.Tensor, dtype: torch.dtype) -> QLinear:

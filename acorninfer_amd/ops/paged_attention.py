@@ -62,6 +62,48 @@ def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torc
     return out
 
 
+def prefill_supported(dtype: torch.dtype, head_dim: int, page_size: int, num_heads: int,
+                      kv_heads: int) -> bool:
+    """Shapes acorn_paged_prefill_attention is built for."""
+    return (dtype in (torch.bfloat16, torch.float16) and head_dim in (64, 128)
+            and page_size % 16 == 0 and (page_size & (page_size - 1)) == 0
+            and num_heads % kv_heads == 0 and num_heads // kv_heads in (1, 2, 4, 8))
+
+
+def paged_prefill_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                            tables: torch.Tensor, seq_row0: torch.Tensor,
+                            seq_pos0: torch.Tensor, seq_nq: torch.Tensor, max_nq: int, *,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal prefill attention over the paged cache (acorn_paged_prefill_attention).
+
+    q [R,H,D]: the prompt rows of N sequences, packed; sequence n's rows
+    q[seq_row0[n] : seq_row0[n] + seq_nq[n]] sit at positions seq_pos0[n] +
+    j and attend to the sequence's tokens 0 .. their own position, whose K/V
+    (the new rows' included) are already in k/v_pages through tables[n].
+    Returns [R,H,D] in q.dtype (rows not covered by a sequence are left as
+    they were in `out`)."""
+    require_gpu(q, k_pages, v_pages, tables, seq_row0, seq_pos0, seq_nq)
+    R, H, D = q.shape
+    NB, P, KV, _ = k_pages.shape
+    N = seq_row0.shape[0]
+    assert H % KV == 0 and P % 16 == 0 and D in (64, 128)
+    assert v_pages.shape == k_pages.shape and k_pages.shape[3] == D
+    assert tables.shape[0] == N and seq_pos0.shape[0] == N and seq_nq.shape[0] == N
+    for t in (tables, seq_row0, seq_pos0, seq_nq):
+        assert t.dtype == torch.int32 and t.is_contiguous()
+    assert k_pages.is_contiguous() and v_pages.is_contiguous()
+    assert q.dtype == k_pages.dtype == v_pages.dtype
+    q2 = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q2)
+    rc = lib().acorn_paged_prefill_attention(
+        ptr(q2), ptr(k_pages), ptr(v_pages), ptr(tables), ptr(seq_row0), ptr(seq_pos0),
+        ptr(seq_nq), ptr(out), N, R, int(max_nq), H, KV, D, P, NB, max(1, tables.shape[1]),
+        float(D ** -0.5), dtype_code(q2), stream_ptr(q.device))
+    check(rc, "paged_prefill_attention")
+    return out
+
+
 def num_splits_for(B: int, num_heads: int, *, sm_count: int = _SM_COUNT,
                    max_splits: int = 8) -> int:
     """The reference's split heuristic (paged_attention.py:155-158), unchanged:

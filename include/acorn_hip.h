@@ -189,6 +189,27 @@ int acorn_paged_attention_qkv(const float* part, int64_t nsplit, void* k_pages, 
                               int wdtype, void* stream);
 
 /*
+ * Prefill attention over the paged cache: causal softmax(q . K^T * scale) V for
+ * the rows of a (chunked) prefill whose new K/V are already in the pool.
+ * Replaces the per-row SDPA of acorninfer/models/qwen3.py:291-382 (the
+ * prefill attention of forward_prefill_batch / forward_extend, :597-686).
+ *   q, out [R, H, D] (rows of all N sequences); sequence n's rows are
+ *   q[seq_row0[n] .. seq_row0[n] + seq_nq[n]), at positions seq_pos0[n] + j;
+ *   row j attends to the sequence's tokens 0 .. seq_pos0[n] + j, stored at
+ *   (tables[n, t / P], t % P) of k/v_pages [num_blocks, P, KV, D].
+ *   max_nq >= every seq_nq[n] (rows past max_nq, or past row R - 1, are not
+ *   written); seq_* int32 [N]; tables int32 [N, table_stride].
+ * bf16 / fp16, D in {64, 128}, P a multiple of 16, H/KV in {1, 2, 4, 8}; no
+ * workspace (one pass per 16-token query tile, no split).
+ */
+int acorn_paged_prefill_attention(const void* q, const void* k_pages, const void* v_pages,
+                                  const int32_t* tables, const int32_t* seq_row0,
+                                  const int32_t* seq_pos0, const int32_t* seq_nq, void* out,
+                                  int64_t N, int64_t R, int64_t max_nq, int64_t H, int64_t KV,
+                                  int64_t D, int64_t P, int64_t num_blocks, int64_t table_stride,
+                                  float scale, int dtype, void* stream);
+
+/*
  * 1 when acorn_paged_attention_qkv supports the shape: bf16 or fp16
  * activations with norm weights of the same dtype, D in {64, 128}, H/KV in
  * {1, 2, 4, 8}, pages of a multiple of 16 tokens and splits of at most 16

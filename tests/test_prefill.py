@@ -1,5 +1,6 @@
 """Prefill and chunked prefill (forward_prefill_batch, forward_extend;
-acorninfer/models/qwen3.py:597-686) on the decode kernels, one row per token,
+acorninfer/models/qwen3.py:597-686): the decode step's kernels with one row
+per token and, for bf16 / fp16, the query-tiled prefill attention kernel,
 against the CPU oracle of the reference's SDPA path (oracle/qwen3_ref.py:
 a whole-prompt forward, pinned against HF Qwen3) and against the GPU's own
 token-by-token decode of the same prompt.
@@ -10,7 +11,9 @@ token-by-token decode of the same prompt.
 - bf16: a ragged batch of three prompts, each row's last logits within the
   decode tests' norm-relative tolerance of the oracle's (argmax equal where
   the top-2 margin is at least 0.05); two chunks through forward_extend equal
-  the one-shot prefill.
+  the one-shot prefill; the tiled prefill attention and K3 with one row per
+  token give the same logits and KV on a ragged batch and on an
+  8192-token prompt that crosses the launch-block boundary.
 """
 import pytest
 import torch
@@ -151,3 +154,37 @@ def test_prefill_at_library_sizes_bf16_matches_oracle():
         assert rel < 3e-2
     release(alloc, views)
     alloc.assert_balanced()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens", [(5, 33, 17, 200), (8300,)])
+def test_tiled_prefill_attention_equals_k3_rows_bf16(lens):
+    """The model's prefill with the query-tiled attention kernel against the
+    same prefill with K3 (one decode row per token): last-row logits and
+    every layer's KV. 8300 tokens is two launch blocks (8192 rows each), so
+    the second block's tiles read the first block's KV from the pool."""
+    cfg = Qwen3Config.qwen3_0_6b().with_layers(2)
+    sd = random_state_dict(cfg, seed=SEED + 6, std=0.02, dtype=torch.bfloat16)
+    model = Qwen3DecodeModel.from_state_dict(cfg, sd, weight_format="bf16", device="cuda")
+    prompts = [_ids(n, cfg.vocab_size, SEED + 30 + n) for n in lens]
+    pages = sum(-(-n // 16) for n in lens) + 4
+    got = {}
+    for tiled in (True, False):
+        print(f"\n[prefill {lens} tokens, tiled attention {tiled}]", flush=True)
+        model.tiled_prefill = tiled
+        alloc, cache = new_cache(model, pages)
+        views = [PagedCacheView(cache) for _ in prompts]
+        logits = model.forward_prefill_batch(_padded(prompts, model.device), views,
+                                             real_lens=list(lens)).cpu()
+        # the last layer's k (layer 0's k/v are computed before any attention)
+        kv = [cache.k_pages[-1][torch.tensor(v.table)].reshape(-1, cfg.num_key_value_heads,
+                                                             cfg.head_dim)[:n].float().cpu()
+              for v, n in zip(views, lens)]
+        got[tiled] = (logits, kv)
+        release(alloc, views)
+    model.tiled_prefill = True
+    for i in range(len(lens)):
+        rel = _rel(got[True][0][i], got[False][0][i])
+        print(f"\n[row {i} ({lens[i]} tokens): tiled vs K3 rows rel err {rel:.3g}]", flush=True)
+        assert rel < 3e-2
+        assert _rel(got[True][1][i], got[False][1][i]) < 3e-2
