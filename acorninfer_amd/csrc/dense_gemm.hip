@@ -1,0 +1,209 @@
+// Large-M bf16 projection GEMM (prefill sizes): out[M, N] = x[M, K] . w[N, K]^T
+// with x and w both K-contiguous, fp32 accumulation, bf16 or fp32 output.
+//
+// Shape of the work, for gfx950's v_mfma_f32_16x16x32_bf16:
+//  * a workgroup of 4 waves owns a (4 WN) (n) x BM (m) output tile; wave w
+//    owns the WN weight rows [WN w, WN w + WN) of it and all BM columns, so a
+//    wave holds WN/16 x BM/16 accumulator blocks;
+//  * weights go from global memory straight into registers in the MFMA A
+//    operand layout (lane (r, c) of a 16-row block holds 8 consecutive k of
+//    row c at k = 8 r): each weight byte is read by exactly one wave, no LDS;
+//  * x goes through LDS: the workgroup stages the BM x 64 slice of a K step
+//    once and all 4 waves read their B operands from it (double-buffered,
+//    one barrier per K step);
+//  * weights are prefetched DEPTH K steps ahead in a register ring, x one
+//    step ahead (scheduling fences keep the x loads at the top of the step
+//    and its LDS store after the MFMAs); DEPTH divides the step count, so the
+//    loop has no data-dependent branch and the wait counts are static; loads
+//    past the last step re-read it;
+//  * launches with fewer tiles than CUs split K (blockIdx.y): split s sums
+//    its K range into its own fp32 plane, which the consumer adds in order;
+//  * workgroup ids are remapped so that consecutive tiles run on one XCD
+//    (the dispatcher deals ids round-robin over the 8 XCDs), and the tiles of
+//    an XCD cover 4 weight tiles x 8 x tiles, which share its L2.
+// Per 32 k a wave reads BM/16 B operands (1 KB each) from LDS for
+// WN/16 x BM/16 MFMAs: 16 WN/16 FLOPs per LDS byte (64 at WN = 64). The
+// direct weight loads touch 16 rows x 64 B per instruction (half lines), which
+// with one wave per SIMD is what holds the kernel near 0.8 PFLOP/s at
+// M >= 2048 (hipBLASLt, with both operands staged through LDS by DMA, reaches
+// 1.1-1.4 on the same shapes).
+#include <hip/hip_runtime.h>
+
+#include "acorn_hip.h"
+#include "gemm_common.h"
+
+namespace acorn {
+namespace {
+
+constexpr int kDenseBK = 64;               // k per step
+constexpr int kXPitch = kDenseBK * 2 + 16; // bytes per staged x row (padded by 8 bf16)
+
+template <typename OUT, int WN, int BM, int DEPTH>
+__global__ __launch_bounds__(256, 1) void dense_gemm_kernel(const __bf16* __restrict__ x,
+                                                            const __bf16* __restrict__ w,
+                                                            OUT* __restrict__ out, int M, int N,
+                                                            int K, int tiles_n, int tiles_m,
+                                                            int steps) {
+  constexpr int NB = WN / 16;                       // accumulator blocks along n (per wave)
+  constexpr int MB = BM / 16;                       // accumulator blocks along m
+  constexpr int XP = BM * kDenseBK / 8 / 256;       // 16-byte x pieces per thread per step
+  __shared__ __align__(16) uint8_t xs[2][BM * kXPitch];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int r = lane >> 4, c = lane & 15;
+  // tile of this workgroup: XCD-contiguous ids, then groups of 4 weight tiles
+  const int G = tiles_n * tiles_m;
+  int t = blockIdx.x;
+  if (G % 8 == 0) t = (t % 8) * (G / 8) + t / 8;
+  constexpr int GN = 4;
+  const int group = t / (GN * tiles_m);
+  const int first_n = group * GN;
+  const int gsize = min(tiles_n - first_n, GN);
+  const int in_group = t - group * GN * tiles_m;
+  const int tn = first_n + in_group % gsize;
+  const int tm = in_group / gsize;
+  const int n0 = tn * 4 * WN + wid * WN;
+  const int m0 = tm * BM;
+  // split blockIdx.y of the K range: `steps` K steps from k = blockIdx.y * steps * 64,
+  // written to its own fp32 plane of out
+  const int kbase = blockIdx.y * steps * kDenseBK;
+  out += (size_t)blockIdx.y * M * N;
+
+  // weight rows of the wave's NB blocks (rows past N re-read row N - 1)
+  const __bf16* wrow[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+    wrow[nb] = w + (size_t)min(n0 + 16 * nb + c, N - 1) * K + kbase + 8 * r;
+  // the x pieces this thread stages: row p / 8, k (p % 8) * 8 of the step
+  const __bf16* xrow[XP];
+  uint32_t xoff[XP];
+#pragma unroll
+  for (int i = 0; i < XP; ++i) {
+    const int p = tid + 256 * i;
+    xrow[i] = x + (size_t)min(m0 + p / 8, M - 1) * K + kbase + (p % 8) * 8;
+    xoff[i] = (uint32_t)((p / 8) * kXPitch + (p % 8) * 16);
+  }
+  u32x4 wr[DEPTH][NB][2];
+  u32x4 xr[XP];
+  auto load_w = [&](int s, u32x4 (&dst)[NB][2]) {
+    const int k0 = s * kDenseBK;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) dst[nb][kk] = *(const u32x4*)(wrow[nb] + k0 + 32 * kk);
+  };
+  auto load_x = [&](int s) {
+    const int k0 = s * kDenseBK;
+#pragma unroll
+    for (int i = 0; i < XP; ++i) xr[i] = *(const u32x4*)(xrow[i] + k0);
+  };
+  auto store_x = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < XP; ++i) *(u32x4*)(xs[b] + xoff[i]) = xr[i];
+  };
+  f32x4 acc[NB][MB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) load_w(min(d, steps - 1), wr[d]);
+  load_x(0);
+  store_x(0);
+  __syncthreads();
+  for (int s0 = 0; s0 < steps; s0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int s = s0 + d;
+      const int b = s & 1;
+      load_x(min(s + 1, steps - 1));
+      // keep the x loads here, a whole step ahead of their LDS store (the
+      // scheduler would sink them next to it and expose their latency)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        u32x4 xb[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          xb[mb] = *(const u32x4*)(xs[b] + (16 * mb + c) * kXPitch + 64 * kk + 16 * r);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = mfma(wr[d][nb][kk], xb[mb], acc[nb][mb]);
+      }
+      // and the LDS store of the next step's x after this step's MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+      load_w(min(s + DEPTH, steps - 1), wr[d]);
+      store_x(b ^ 1);
+      __syncthreads();
+    }
+  }
+  // lane (r, c) of block (nb, mb) holds out[m0 + 16 mb + c][n0 + 16 nb + 4 r + i]
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = m0 + 16 * mb + c;
+    if (m >= M) continue;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int n = n0 + 16 * nb + 4 * r;
+      if (n >= N) continue;
+      OUT* o = out + (size_t)m * N + n;
+      if constexpr (sizeof(OUT) == 4) {
+        *(f32x4*)o = acc[nb][mb];
+      } else {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        u32x2 v;
+        v[0] = pack_bf16x2(acc[nb][mb][0], acc[nb][mb][1]);
+        v[1] = pack_bf16x2(acc[nb][mb][2], acc[nb][mb][3]);
+        *(u32x2*)o = v;
+      }
+    }
+  }
+}
+
+template <typename OUT, int WN, int BM, int DEPTH>
+int launch(const void* x, const void* w, void* out, int64_t M, int64_t N, int64_t K, int ks,
+           hipStream_t st) {
+  const int64_t tiles_n = (N + 4 * WN - 1) / (4 * WN), tiles_m = (M + BM - 1) / BM;
+  if (tiles_n * tiles_m > 0x7fffffff) return ACORN_ERR_SHAPE;
+  dense_gemm_kernel<OUT, WN, BM, DEPTH>
+      <<<dim3((unsigned)(tiles_n * tiles_m), (unsigned)ks), dim3(256), 0, st>>>(
+          (const __bf16*)x, (const __bf16*)w, (OUT*)out, (int)M, (int)N, (int)K, (int)tiles_n,
+          (int)tiles_m, (int)(K / kDenseBK / ks));
+  return ACORN_OK;
+}
+
+template <typename OUT>
+int dispatch(int wn, int bm, int depth, const void* x, const void* w, void* out, int64_t M,
+             int64_t N, int64_t K, int ks, hipStream_t st) {
+  if (wn == 64) {
+    if (bm == 128 && depth == 2) return launch<OUT, 64, 128, 2>(x, w, out, M, N, K, ks, st);
+    if (bm == 128 && depth == 4) return launch<OUT, 64, 128, 4>(x, w, out, M, N, K, ks, st);
+    if (bm == 64 && depth == 2) return launch<OUT, 64, 64, 2>(x, w, out, M, N, K, ks, st);
+    if (bm == 64 && depth == 4) return launch<OUT, 64, 64, 4>(x, w, out, M, N, K, ks, st);
+  } else if (wn == 128) {
+    if (bm == 64 && depth == 2) return launch<OUT, 128, 64, 2>(x, w, out, M, N, K, ks, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+
+bool dense_gemm_supported(int64_t N, int64_t K, int wn, int bm, int depth, int ks) {
+  const bool built = wn == 64 ? (bm == 64 || bm == 128) && (depth == 2 || depth == 4)
+                   : wn == 128 ? bm == 64 && depth == 2
+                               : false;
+  return built && ks >= 1 && ks <= 64 && N % 4 == 0 && K % kDenseBK == 0 &&
+         (K / kDenseBK) % ((int64_t)depth * ks) == 0;
+}
+
+int dense_gemm_launch(const void* x, const void* w, void* out_bf16, float* out_f32, int64_t M,
+                      int64_t N, int64_t K, int wn, int bm, int depth, int ks, hipStream_t st) {
+  if (!dense_gemm_supported(N, K, wn, bm, depth, ks)) return ACORN_ERR_UNSUPPORTED;
+  if (out_f32) return dispatch<float>(wn, bm, depth, x, w, out_f32, M, N, K, ks, st);
+  if (ks != 1) return ACORN_ERR_VALUE;
+  return dispatch<__bf16>(wn, bm, depth, x, w, out_bf16, M, N, K, 1, st);
+}
+
+}  // namespace acorn

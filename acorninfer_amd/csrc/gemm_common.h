@@ -120,4 +120,14 @@ int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale
                const void* zero, void* out, float* part, int64_t M, int64_t N, int64_t K,
                hipStream_t st);
 
+// ---- the large-M bf16 GEMM (dense_gemm.hip) ---------------------------------
+// out[M,N] = x[M,K] . w[N,K]^T, bf16 operands: (4 wn) x bm output tiles (wn
+// weight rows per wave: 64 or 128; bm 64 or 128), weights prefetched `depth`
+// K steps of 64 ahead (2 or 4), the K range cut into ks splits. fp32 output
+// when out_f32 is given (split s into out_f32 + s*M*N), else bf16 into
+// out_bf16 (ks == 1 only).
+bool dense_gemm_supported(int64_t N, int64_t K, int wn, int bm, int depth, int ks);
+int dense_gemm_launch(const void* x, const void* w, void* out_bf16, float* out_f32, int64_t M,
+                      int64_t N, int64_t K, int wn, int bm, int depth, int ks, hipStream_t st);
+
 }  // namespace acorn

@@ -718,7 +718,9 @@ struct Tiling {
   size_t lds;
   int swiglu;                    // fused SwiGLU epilogue (rt == 2, ksplit == 1)
   int kind;                      // 0 = streaming kernel, 1 = tiled kernel (rt == 0, upw = BM),
-                                 // 2 = W4B decode kernel (tpw = its pipeline depth)
+                                 // 2 = W4B decode kernel (tpw = its pipeline depth),
+                                 // 3 = large-M bf16 kernel (rt == kDenseRT, upw = BM,
+                                 //     nw = weight rows per wave, tpw = prefetch depth)
   W4bPlan w4b;
 };
 
@@ -812,11 +814,50 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
 // cfg: {rt, upw, nw, ksplit, tpw}; 0 = choose. swiglu: fused SwiGLU epilogue,
 // which fixes rt = 2 and ksplit = 1. For M > 16 an rt of 0 selects the tiled
 // kernel (upw = its BM), rt >= 1 the streaming kernel.
+// bf16 at prefill sizes: the large-M kernel (dense_gemm.hip) by default from
+// this many rows on, or on request (rt == kDenseRT).
+constexpr int kDenseRT = -2;
+constexpr int64_t kDenseMinM = 512;
+
 int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling* t,
               bool swiglu = false) {
   if (M <= 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   t->swiglu = swiglu;
   t->kind = 0;
+  const bool no_request = !cfg || (cfg[0] == 0 && cfg[1] == 0 && cfg[2] == 0 && cfg[3] <= 1 &&
+                                   cfg[4] == 0);
+  if (wfmt == ACORN_WFMT_BF16 && !swiglu &&
+      ((cfg && cfg[0] == kDenseRT) || (no_request && M >= kDenseMinM))) {
+    const bool req = cfg && cfg[0] == kDenseRT;
+    const int bm = req && cfg[1] > 0 ? cfg[1] : 128;
+    const int wn = req && cfg[2] > 0 ? cfg[2] : 64;
+    const int depth = req && cfg[4] > 0 ? cfg[4] : 4;
+    int ks = req && cfg[3] > 0 ? cfg[3] : 1;
+    if (!(req && cfg[3] > 0)) {
+      // split K while the launch has fewer workgroups than CUs
+      const int64_t tiles = ((N + 4 * wn - 1) / (4 * wn)) * ((M + bm - 1) / bm);
+      while (tiles * ks < kCUs && ks < 8 && dense_gemm_supported(N, K, wn, bm, depth, 2 * ks))
+        ks *= 2;
+    }
+    if (dense_gemm_supported(N, K, wn, bm, depth, ks)) {
+      t->kind = 3;
+      t->rt = kDenseRT;
+      t->upw = bm;
+      t->nw = wn;
+      t->ksplit = ks;
+      t->tpw = depth;
+      t->mt = 1;
+      t->R = bm;
+      t->nk = (int)(K / 64);
+      t->ntiles = (int)((N + 4 * wn - 1) / (4 * wn));
+      t->mblocks = (int)((M + bm - 1) / bm);
+      t->groups = 1;
+      t->lds = 0;
+      return ACORN_OK;
+    }
+    if (req) return ACORN_ERR_UNSUPPORTED;
+  }
+  if (cfg && cfg[0] == kDenseRT) return ACORN_ERR_UNSUPPORTED;
   if (wfmt == ACORN_WFMT_W4B && M <= 16 && !(cfg && cfg[0] == 0 && cfg[1] >= 32)) {
     // decode sizes in the block layout: the W4B decode kernel
     const int rc = w4b_make_plan(M, N, K, cfg, swiglu, &t->w4b);
@@ -1082,7 +1123,12 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
   a.tpw = t.tpw;
   a.ksplit = t.ksplit;
   a.log2R = ilog2_ceil(t.R);
-  if (t.kind == 2) {
+  if (t.kind == 3) {
+    // bf16 straight into out (one split), else fp32 split planes into part
+    const bool direct = out_bf16 && t.ksplit == 1;
+    rc = dense_gemm_launch(x, w, direct ? out_bf16 : nullptr, direct ? nullptr : part, M, N, K,
+                           t.nw, t.upw, t.tpw, t.ksplit, st);
+  } else if (t.kind == 2) {
     rc = w4b_launch(t.w4b, x, w, scale, zero, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K,
                     st);
   } else if (t.kind == 1) {

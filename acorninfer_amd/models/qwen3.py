@@ -45,11 +45,12 @@ from acorninfer_amd.quant import quantize as Q
 
 MI355X_CUS = 256
 FORMATS = {"bf16": WFMT_BF16, "w8a16": WFMT_W8, "w4a16": WFMT_W4}
-# bf16 projections with at least this many rows (prefill sizes) are plain
-# dense GEMMs: they go to hipBLASLt (fp32 results), which runs them at
-# 1.2-1.4 PFLOP/s here against 0.6-0.7 for the tiled kernel; the reference
-# runs its bf16 projections through F.linear as well. Marker tiling:
-LIBRARY_M_MIN = 1024
+# bf16 projections at prefill sizes run on the library's large-M kernel
+# (its planner's default from DENSE_M_MIN rows, tiling rt == DENSE_RT).
+# LIBRARY_RT is a tiling marker that sends a bf16 projection to torch.mm
+# (hipBLASLt) instead: a comparison point for tests and measurements only.
+DENSE_M_MIN = 512
+DENSE_RT = -2
 LIBRARY_RT = -1
 
 
@@ -168,10 +169,10 @@ class QLinear:
         return n
 
     def plan(self, M: int, tiling=None):
-        """(Tiling, output tiles) from the library planner; bf16 at
-        M >= LIBRARY_M_MIN (no tiling requested): the hipBLASLt marker."""
+        """(Tiling, output tiles) from the library planner (a LIBRARY_RT
+        request is passed through: torch.mm)."""
         from acorninfer_amd.ops.quant_gemm import Tiling, plan
-        if tiling is None and self.fmt == WFMT_BF16 and M >= LIBRARY_M_MIN:
+        if tiling is not None and tiling[0] == LIBRARY_RT:
             return Tiling(LIBRARY_RT, 0, 0, 1, 0), None
         return plan(M, self.N, self.K, self.fmt, tiling)
 
@@ -183,7 +184,7 @@ class QLinear:
         if self.fmt == _lib.WFMT_F32:
             part, out = (out if part is None else part), None
         if tiling[0] == LIBRARY_RT:
-            # hipBLASLt on torch's current stream, which is the step's
+            # torch.mm (hipBLASLt) on torch's current stream, which is the step's
             xs = x[:M]
             if out is not None:
                 torch.mm(xs, self.w.t(), out=out[:M])
@@ -291,6 +292,9 @@ class Qwen3DecodeModel:
         # prefill attention as the query-tiled kernel where it is built for
         # the shapes (False: K3 with one row per prompt token)
         self.tiled_prefill = True
+        # bf16 projections of prefill rows: "own" (the library's large-M
+        # kernel) or "library" (torch.mm, i.e. hipBLASLt)
+        self.prefill_gemm = "own"
         # batch -> {projection name -> Tiling}, filled by tune()
         self.tilings: dict[int, dict] = {}
         self.swiglu_choice: dict[int, bool] = {}
@@ -746,11 +750,16 @@ class Qwen3DecodeModel:
             Rb = r1 - r0
             # the step buffers of the last shape are kept (a prompt batch often repeats it)
             # (the prefill kernel reads per-sequence tables: no per-row table)
-            key = (Rb, 1 if tiled else W)
+            key = (Rb, 1 if tiled else W, self.prefill_gemm)
             cached = getattr(self, "_extend_buf", None)
             if cached is None or cached[0] != key:
                 self._extend_buf = None
-                self._extend_buf = (key, self.buffers(Rb, key[1], prefill=True))
+                lib_t = None
+                if self.prefill_gemm == "library" and self.layers[0].qkv.fmt == WFMT_BF16:
+                    from acorninfer_amd.ops.quant_gemm import Tiling
+                    lt = Tiling(LIBRARY_RT, 0, 0, 1, 0)
+                    lib_t = {"qkv": lt, "o": lt, "gate_up": lt, "down": lt}
+                self._extend_buf = (key, self.buffers(Rb, key[1], tilings=lib_t, prefill=True))
             buf = self._extend_buf[1]
             buf.ids.copy_(ids_all[r0:r1])
             buf.positions.copy_(pos_all[r0:r1])

@@ -78,6 +78,10 @@ class Tiling(NamedTuple):
     128-k groups per pipeline stage, nw waves per workgroup (2 or 4 each on
     its own rows; 10*nw + kw: kw waves share rows and split K), ksplit, and
     tpw = stages in flight per wave.
+    Large-M bf16 kernel (the default for bf16 from 512 rows, or rt == -2):
+    upw is the M tile (64 / 128), nw the weight rows per wave (64 / 128; a
+    workgroup's weight tile is 4 nw), tpw the weight prefetch depth in 64-k
+    steps (2 / 4); reported as (-2, BM, rows per wave, 1, depth).
     """
     rt: int = 0
     upw: int = 0

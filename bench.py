@@ -23,11 +23,15 @@ The JSON line also carries:
 - extra (unless --no-extra): the reference's decode_batch protocol (one
   host copy per step) at the headline size, other batch sizes and formats
   (W4A16 and W8A16 at C=8 with their own GEMM rooflines, configuration 5),
-  the batched prefill and configuration 4 end to end through the Engine.
+  the batched prefill (C x 512, and one 8192-token prompt with the bf16
+  projections on this library's large-M kernel and on hipBLASLt) and
+  configuration 4 end to end through the Engine.
 - extra.kernels (unless --no-kernels): the isolated kernels at
   configurations 2 (K3, K1, K2), 5 (K3 + combine over one layer's pages at
-  C=8 and C=64) and 3 (int4 / int8 GEMM at every shape and M = 1/8/64/256,
-  HBM and MFMA fractions).
+  C=8 and C=64; prefill attention over an 8192-token prompt and 8 x 512
+  against K3 with one row per token) and 3 (int4 / int8 GEMM at every shape
+  and M = 1/8/64/256, HBM and MFMA fractions; the bf16 large-M GEMM at
+  M = 512/2048/8192 against hipBLASLt).
 - cpu_baseline: BASELINE configuration 1 run whole on the CPU oracle of the
   reference's path (oracle/qwen3_ref.py, fp32 torch on the host cores),
   the CPU oracles of the kernels at configuration 2/3 shapes, and the GPU
@@ -36,6 +40,7 @@ The JSON line also carries:
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -330,6 +335,7 @@ def kernel_benchmarks(seed: int = 23, only_attention: bool = False,
     if with_attention:
         out.update(norm_benchmarks(seed))
     out.update(gemm_benchmarks(seed, gemm_ms))
+    out.update(dense_gemm_benchmarks(seed))
     return out
 
 
@@ -435,6 +441,62 @@ def attention_benchmarks(seed: int, attn_splits: list[int] | None = None) -> dic
                                    "mean_ctx": round(float(clens.float().mean()), 1)}
         del kp5, vp5, acc5, ml5
         torch.cuda.empty_cache()
+    out.update(prefill_attention_benchmarks(seed))
+    return out
+
+
+def prefill_attention_benchmarks(seed: int) -> dict:
+    """Prefill attention of one layer, Qwen3-8B heads: one 8192-token prompt
+    (configuration 5's longest) and 8 prompts of 512 (configuration 4's), the
+    query-tiled kernel against K3 with one decode row per token. FLOPs are the
+    causal algorithmic count 4 * H * D * sum over rows of (position + 1)."""
+    import torch
+
+    from acorninfer_amd import _lib
+    from acorninfer_amd._lib import lib, ptr
+
+    out = {}
+    H, KV, D, P = 32, 8, 128, 16
+    g = torch.Generator(device="cuda").manual_seed(seed + 11)
+    for n, L in ((1, 8192), (8, 512)):
+        R, per = n * L, L // P
+        nb = n * per + 1
+        kp = torch.empty(nb, P, KV, D, device="cuda", dtype=torch.bfloat16).normal_(generator=g)
+        vp = torch.empty_like(kp).normal_(generator=g)
+        q = torch.randn(R, H, D, device="cuda", generator=g).bfloat16()
+        o = torch.empty_like(q)
+        perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed + 12))
+        tabs = perm[:n * per].view(n, per).to(torch.int32).cuda()
+        row0 = torch.arange(n, dtype=torch.int32, device="cuda") * L
+        pos0 = torch.zeros(n, dtype=torch.int32, device="cuda")
+        nq = torch.full((n,), L, dtype=torch.int32, device="cuda")
+        # K3 rows: one decode row per token, length position + 1
+        rtabs = tabs.repeat_interleave(L, 0).contiguous()
+        rlens = torch.arange(1, L + 1, dtype=torch.int32, device="cuda").repeat(n)
+        S = 4
+        acc = torch.empty(R * H * S * D, device="cuda")
+        ml = torch.empty(2 * R * H * S, device="cuda")
+
+        def tiled(st):
+            _lib.check(lib().acorn_paged_prefill_attention(
+                ptr(q), ptr(kp), ptr(vp), ptr(tabs), ptr(row0), ptr(pos0), ptr(nq), ptr(o),
+                n, R, L, H, KV, D, P, nb, per, D ** -0.5, _lib.BF16, st.cuda_stream),
+                "prefill attention")
+
+        def rows(st):
+            _lib.check(lib().acorn_paged_attention(
+                ptr(q), ptr(kp), ptr(vp), ptr(rtabs), ptr(rlens), ptr(o), ptr(acc), ptr(ml),
+                R, H, KV, D, P, nb, per, S, D ** -0.5, _lib.BF16, st.cuda_stream), "K3")
+
+        us = _time_graph(tiled, 10)
+        us_rows = _time_graph(rows, 2)
+        flops = 4.0 * H * D * n * L * (L + 1) / 2
+        out[f"prefill_attention_{n}x{L}"] = {
+            "us": round(us, 1), "TFLOPs": round(flops / us / 1e6, 1),
+            "frac_mfma": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "k3_rows_us": round(us_rows, 1), "speedup_vs_k3_rows": round(us_rows / us, 2)}
+        del kp, vp, acc, ml
+        torch.cuda.empty_cache()
     return out
 
 
@@ -472,6 +534,50 @@ def norm_benchmarks(seed: int) -> dict:
                 ptr(qq), ptr(kk), 8, 32, 8, 128, ptr(wq), ptr(wq), 1e-6, ptr(pos), 1,
                 ptr(invf), _lib.BF16, _lib.BF16, st.cuda_stream), "K2")
     out["K2_qknorm_rope_us"] = round(_time_graph(k2, 5) / 100, 2)
+    return out
+
+
+def dense_gemm_benchmarks(seed: int) -> dict:
+    """bf16 projections at prefill M (configuration 3's shapes): this
+    library's large-M kernel (its planner's tiling) against torch.mm
+    (hipBLASLt), fp32 output as the prefill step consumes it; TFLOP/s and the
+    fraction of the 2.5 PFLOP/s dense bf16 peak."""
+    import torch
+
+    from acorninfer_amd import _lib
+    from acorninfer_amd._lib import lib, ptr
+    from acorninfer_amd.ops.quant_gemm import plan
+
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(seed + 21)
+    shapes = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (24576, 4096),
+              "down": (4096, 12288)}
+    for M in (512, 2048, 8192):
+        for name, (n, k) in shapes.items():
+            x = torch.randn(M, k, device="cuda", generator=g).bfloat16()
+            w = (0.02 * torch.randn(n, k, device="cuda", generator=g)).bfloat16()
+            t, _ = plan(M, n, k, _lib.WFMT_BF16)
+            part = torch.empty(t.ksplit, M, n, device="cuda")
+            arr = (ctypes.c_int * 6)(*t, 0)
+
+            def own(st):
+                for _ in range(4):
+                    _lib.check(lib().acorn_quant_gemm(ptr(x), ptr(w), None, None, None,
+                                                      ptr(part), M, n, k, _lib.WFMT_BF16, arr,
+                                                      st.cuda_stream), "dense GEMM")
+
+            def library(st):
+                for _ in range(4):
+                    torch.ops.aten.mm.dtype_out(x, w.t(), torch.float32, out=part[0])
+
+            fl = 2.0 * M * n * k
+            us, us_lib = _time_graph(own, 3) / 4, _time_graph(library, 3) / 4
+            out[f"dense_gemm_{name}_M{M}"] = {
+                "us": round(us, 1), "TFLOPs": round(fl / us / 1e6, 1),
+                "frac_mfma": round(fl / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
+                "hipblaslt_us": round(us_lib, 1), "tiling": list(t)}
+            del x, w, part
+    torch.cuda.empty_cache()
     return out
 
 
@@ -806,6 +912,17 @@ def main() -> None:
             extra[f"bf16_prefill_C{c}_ms"] = round(ms_p, 3)
             extra[f"bf16_prefill_C{c}_tok_s"] = round(tps, 1)
             _log(f"bf16 prefill C={c} x {args.prompt_len}: {ms_p:.2f} ms ({tps:.0f} tok/s)")
+        # configuration 5's longest prompt: one 8192-token prefill, with the
+        # projections on this library's large-M kernel and on hipBLASLt
+        for how in ("own", "library"):
+            model.prefill_gemm = how
+            ms_p, tps = prefill_benchmark(model, cfg, 1, 8192, args.seed + 8, reps=2)
+            sfx = "" if how == "own" else "_hipblaslt_gemm"
+            extra[f"bf16_prefill_1x8192{sfx}_ms"] = round(ms_p, 3)
+            extra[f"bf16_prefill_1x8192{sfx}_tok_s"] = round(tps, 1)
+            _log(f"bf16 prefill 1 x 8192 ({how} GEMM): {ms_p:.2f} ms ({tps:.0f} tok/s)")
+        model.prefill_gemm = "own"
+        model._extend_buf = None
         # configuration 4 end to end through the Engine (prefill + decode)
         del cache, runner
         torch.cuda.empty_cache()
