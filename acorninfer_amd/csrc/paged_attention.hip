@@ -1214,31 +1214,45 @@ int dispatch_d(int64_t D, int64_t rep, const void* q, const void* kp, const void
 // causal mask, for a chunked prefill whose new rows' K/V are already in the
 // pool. Row j of sequence n (q row seq_row0[n] + j) sits at position
 // seq_pos0[n] + j and attends to that sequence's tokens 0 .. its position.
-// The decode K3's MFMA layout with the 16 columns of S^T = K Q^T being 16
-// consecutive query tokens of one head instead of the heads of one token:
-//  * a workgroup of QT*REP waves serves QT tiles of 16 query tokens x the REP
-//    q heads of one kv head; every wave walks the same 16-token key chunks
-//    (one page of the kv head's rows), so each chunk is fetched from HBM once
-//    per workgroup and the other waves read it from the caches;
-//  * per chunk: D/32 v_mfma_f32_16x16x32 for the scores, the online softmax
-//    per query column (lazy max), D/16 v_mfma_f32_16x16x16 for P V;
-//  * keys past a query's position are masked in the chunks that cross the
-//    diagonal; the first chunk always holds key 0, so every column's max is
-//    finite from the start.
-// A query tile reads its sequence's keys once per kv head: O(L^2 / 16) bytes
-// per prompt of L tokens, against O(L^2) for one decode row per token.
-template <typename T, int D, int REP, int QT>
-__global__ __launch_bounds__(QT * REP * kWave) void paged_prefill_kernel(
+// It uses the decode K3's MFMA layout with the 16 columns of S^T = K Q^T being
+// 16 consecutive query tokens of one head instead of the heads of one token:
+//  * a workgroup serves the REP q heads of one kv head for QG x 32 query
+//    tokens: wave (head, group) owns two 16-token query blocks (QW = 2), so
+//    every K / V operand it reads feeds two MFMAs;
+//  * the kv head's keys are walked in chunks of 32 tokens that the whole
+//    workgroup stages in LDS once (K and V rows, coalesced 16-byte loads, two
+//    buffers, one barrier per chunk); the next chunk's loads are in flight
+//    while the current one is consumed, and its page ids one chunk earlier;
+//  * per 16 keys and query block: D/32 v_mfma_f32_16x16x32 for the scores,
+//    the online softmax per query column (lazy max), D/16
+//    v_mfma_f32_16x16x16 for P V; blocks whose queries all precede the keys
+//    skip them; keys past a query's position are masked where a chunk
+//    crosses the diagonal, and the first chunk holds key 0, so every
+//    column's max is finite from the start; rows past the last key re-read
+//    it (finite, masked);
+//  * the longest query tiles (the last ones) are dispatched first.
+// A workgroup reads its keys once for REP x QG x 32 query rows: O(L^2 / 32)
+// K / V bytes per prompt of L tokens and kv head, against O(L^2) for one
+// decode row per token.
+template <typename T, int D, int REP, int QG, int KC>
+__global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
     const T* __restrict__ q, const T* __restrict__ k_pages, const T* __restrict__ v_pages,
     const int32_t* __restrict__ tables, const int32_t* __restrict__ seq_row0,
     const int32_t* __restrict__ seq_pos0, const int32_t* __restrict__ seq_nq, T* __restrict__ out,
     int R, int H, int KV, int P, int num_blocks, int table_stride, float scale_log2) {
-  constexpr int KB = D / 32, DPL = D / 16, VW = DPL / 2, CH = 16, DEPTH = 2;
-  constexpr int KPITCH = 2 * D + 16;
-  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int QW = 2;                          // 16-query blocks per wave
+  constexpr int NT = REP * QG * kWave;           // threads
+  constexpr int KB = D / 32, DPL = D / 16, VW = DPL / 2;
+  constexpr int PITCH = 2 * D + 16;              // bytes per staged row (padded)
+  constexpr int RP = 2 * D / 16;                 // 16-byte pieces per K / V row
+  constexpr int PPT = 2 * KC * RP / NT;          // pieces per thread per chunk
+  constexpr int WQ = QG * QW * 16;               // query rows per workgroup
+  static_assert(2 * KC * RP % NT == 0 && PPT >= 1, "whole pieces per thread");
+  __shared__ __align__(16) uint8_t kvs[2][2 * KC * PITCH];   // [buffer][K rows | V rows]
   const int kvh = blockIdx.y, n = blockIdx.z;
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int lane = threadIdx.x % kWave;
+  const int tid = threadIdx.x;
+  const int wid = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
   const int r = lane >> 4, c = lane & 15;
   const int hq = wid % REP, sub = wid / REP;
   const int h = kvh * REP + hq;
@@ -1246,155 +1260,193 @@ __global__ __launch_bounds__(QT * REP * kWave) void paged_prefill_kernel(
   const int row0 = seq_row0[n];
   // rows past q's R rows are not served (so bad metadata cannot reach past q / out)
   const int nq = row0 < 0 || pos0 < 0 ? 0 : min(seq_nq[n], R - row0);
-  const int j0 = (blockIdx.x * QT + sub) * CH;        // this wave's first query row
-  const int wg_j0 = blockIdx.x * QT * CH;
-  if (wg_j0 >= nq) return;                            // uniform over the workgroup
-  const int nvalid = min(CH, nq - j0);
-  if (nvalid <= 0) return;                            // an idle wave of the last tile (no barriers here)
-  // keys of the workgroup's last query, so that all waves walk the same chunks
-  const int L = pos0 + min(wg_j0 + QT * CH, nq);
-  const int pc = pos0 + j0 + min(c, nvalid - 1);      // this column's position
+  const int wg_j0 = (gridDim.x - 1 - blockIdx.x) * WQ;          // longest tiles first
+  if (wg_j0 >= nq) return;                                       // uniform over the workgroup
+  const int j0 = wg_j0 + sub * QW * 16;                          // this wave's first query row
+  const int nvalid = max(0, min(QW * 16, nq - j0));              // 0: the wave only stages
+  const int L = pos0 + min(wg_j0 + WQ, nq);                      // keys of the workgroup's last query
+  const int nchunks = (L + KC - 1) / KC;
   const int32_t* trow = tables + (size_t)n * table_stride;
   const int pshift = __builtin_ctz(P);
-  u32x4_t qb[KB];
-  {
-    const size_t qrow = (size_t)(row0 + j0 + min(c, nvalid - 1));
-#pragma unroll
-    for (int jb = 0; jb < KB; ++jb)
-      qb[jb] = *(const u32x4_t*)(q + (qrow * H + h) * D + 32 * jb + 8 * r);
-  }
-  uint8_t* kslab = smem + (size_t)wid * CH * KPITCH;
   const int tok_stride = KV * D;
-  const int v_off = 4 * r * tok_stride + DPL * c;
-  struct Chunk {
-    uint32_t kr[4][VW];
-    uint32_t v[4][VW];
-  };
-  const int tlast = max(L - 1, 0) / CH * CH;
-  auto load_chunk = [&](int t0, Chunk& ch) {
-    const bool spare = t0 > tlast;
-    t0 = min(t0, tlast);
-    const unsigned pg0 = (unsigned)trow[min(t0 >> pshift, table_stride - 1)];
-    const int pg = __builtin_amdgcn_readfirstlane(pg0 < (unsigned)num_blocks ? (int)pg0 : 0);
-    const size_t base = ((size_t)pg * P + (t0 & (P - 1))) * tok_stride + (size_t)kvh * D;
-    const T* kb = k_pages + base + (spare ? 0 : v_off);
-    const T* vb = v_pages + base + (spare ? 0 : v_off);
-    const int vstep = spare ? 0 : tok_stride;
+
+  // the queries: block qw's column c is query row j0 + 16 qw + c (clamped)
+  u32x4_t qb[QW][KB];
+  int pc[QW];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      __builtin_memcpy(ch.kr[jj], kb + jj * vstep, sizeof(ch.kr[jj]));
-      __builtin_memcpy(ch.v[jj], vb + jj * vstep, sizeof(ch.v[jj]));
-    }
-  };
-  float m = -INFINITY, l = 0.f;
-  f32x4_t acc[DPL];
-#pragma unroll
-  for (int jj = 0; jj < DPL; ++jj) acc[jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  auto consume = [&](int t0, Chunk& ch) {
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      uint8_t* dst = kslab + (4 * r + jj) * KPITCH + 2 * DPL * c;
-#pragma unroll
-      for (int w = 0; w < VW; ++w) ((uint32_t*)dst)[w] = ch.kr[jj][w];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+  for (int qw = 0; qw < QW; ++qw) {
+    const int jc = min(16 * qw + c, max(nvalid - 1, 0));
+    pc[qw] = pos0 + j0 + jc;
+    const size_t qrow = (size_t)(row0 + min(j0 + jc, nq - 1));
 #pragma unroll
     for (int jb = 0; jb < KB; ++jb)
-      sc = mfma16x16x32<T>(*(const u32x4_t*)(kslab + c * KPITCH + 2 * (32 * jb + 8 * r)), qb[jb], sc);
-    float s[4];
+      qb[qw][jb] = *(const u32x4_t*)(q + (qrow * H + h) * D + 32 * jb + 8 * r);
+  }
+
+  // staging: piece i of this thread is K (i < PPT/2) or V, row pr[i], 16-byte column pcol[i]
+  int prow[PPT];
+  uint32_t poff[PPT];
+  const T* pbase[PPT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = sc[i] * scale_log2;
-    if (t0 + CH - 1 > pos0 + j0) {                 // the chunk crosses some column's diagonal
+  for (int i = 0; i < PPT; ++i) {
+    const int p = tid + NT * i;
+    const int kind = p / (KC * RP);                // 0: K, 1: V
+    const int pcol = p % RP;
+    prow[i] = (p % (KC * RP)) / RP;
+    poff[i] = (uint32_t)(kind * KC * PITCH + prow[i] * PITCH + pcol * 16);
+    pbase[i] = (kind ? v_pages : k_pages) + (size_t)kvh * D + pcol * 8;
+  }
+  auto page_of = [&](int chunk, int i) {
+    const int t = min(chunk * KC + prow[i], L - 1);
+    const unsigned pg = (unsigned)trow[min(t >> pshift, table_stride - 1)];
+    return pg < (unsigned)num_blocks ? (int)pg : 0;
+  };
+  int pg[PPT], pg_next[PPT];
+  u32x4_t stage[PPT];
+  auto load_chunk = [&](int chunk, const int (&pgs)[PPT]) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int t = min(chunk * KC + prow[i], L - 1);
+      stage[i] = *(const u32x4_t*)(pbase[i] + ((size_t)pgs[i] * P + (t & (P - 1))) * tok_stride);
+    }
+  };
+  auto store_chunk = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) *(u32x4_t*)(kvs[b] + poff[i]) = stage[i];
+  };
+
+  float m[QW], l[QW];
+  f32x4_t acc[QW][DPL];
+#pragma unroll
+  for (int qw = 0; qw < QW; ++qw) {
+    m[qw] = -INFINITY;
+    l[qw] = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < DPL; ++jj) acc[qw][jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  // one 16-key sub-chunk at LDS rows [16 ss, 16 ss + 16) of buffer b, keys from t0
+  auto consume = [&](int b, int ss, int t0) {
+    const uint8_t* kbuf = kvs[b] + 16 * ss * PITCH;
+    const uint8_t* vbuf = kvs[b] + KC * PITCH + 16 * ss * PITCH;
+    u32x4_t kf[KB];
+#pragma unroll
+    for (int jb = 0; jb < KB; ++jb)
+      kf[jb] = *(const u32x4_t*)(kbuf + c * PITCH + 2 * (32 * jb + 8 * r));
+    u32x2_t pb[QW];
+    bool live[QW];
+#pragma unroll
+    for (int qw = 0; qw < QW; ++qw) {
+      // the block's queries all precede these keys, or it has none: nothing to add
+      live[qw] = 16 * qw < nvalid && t0 <= pos0 + j0 + min(16 * qw + 15, nvalid - 1);
+      if (!live[qw]) continue;
+      f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jb = 0; jb < KB; ++jb) sc = mfma16x16x32<T>(kf[jb], qb[qw][jb], sc);
+      float sv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = sc[i] * scale_log2;
+      if (t0 + 15 > pos0 + j0 + 16 * qw) {     // the sub-chunk crosses some column's diagonal
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (t0 + 4 * r + i > pc[qw]) sv[i] = -INFINITY;
+      }
+      float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+      if (__builtin_amdgcn_ballot_w64(mx > m[qw] + kMaxSlack) != 0) {
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m[qw], mx);
+        const float alpha = __builtin_amdgcn_exp2f(m[qw] - mn);
+        m[qw] = mn;
+        l[qw] *= alpha;
+#pragma unroll
+        for (int jj = 0; jj < DPL; ++jj) acc[qw][jj] *= alpha;
+      }
+      float pr[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int kidx = t0 + 4 * r + i;
-        if (kidx > pc) s[i] = -INFINITY;
-        if (kidx >= L) {
-#pragma unroll
-          for (int w = 0; w < VW; ++w) ch.v[i][w] = 0u;
-        }
+        pr[i] = round_to<T>(__builtin_amdgcn_exp2f(sv[i] - m[qw]));
+        l[qw] += pr[i];
       }
+      pb[qw] = u32x2_t{pack2<T>(pr[0], pr[1]), pack2<T>(pr[2], pr[3])};
     }
-    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    if (__builtin_amdgcn_ballot_w64(mx > m + kMaxSlack) != 0) {
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mn = fmaxf(m, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m - mn);
-      m = mn;
-      l *= alpha;
+    if (!live[0] && !live[QW - 1]) return;
+    // lane (r, c): V rows 4 r .. 4 r + 3, dims [DPL c, DPL c + DPL)
+    uint32_t vr[4][VW];
 #pragma unroll
-      for (int jj = 0; jj < DPL; ++jj) acc[jj] *= alpha;
-    }
-    float pr[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      pr[i] = round_to<T>(__builtin_amdgcn_exp2f(s[i] - m));
-      l += pr[i];
-    }
-    const u32x2_t pb = {pack2<T>(pr[0], pr[1]), pack2<T>(pr[2], pr[3])};
+    for (int jj = 0; jj < 4; ++jj)
+      __builtin_memcpy(vr[jj], vbuf + (4 * r + jj) * PITCH + 2 * DPL * c, sizeof(vr[jj]));
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) {
       const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
-      const u32x2_t va = {__builtin_amdgcn_perm(ch.v[1][jj / 2], ch.v[0][jj / 2], sel),
-                          __builtin_amdgcn_perm(ch.v[3][jj / 2], ch.v[2][jj / 2], sel)};
-      acc[jj] = mfma16x16x16<T>(va, pb, acc[jj]);
+      const u32x2_t va = {__builtin_amdgcn_perm(vr[1][jj / 2], vr[0][jj / 2], sel),
+                          __builtin_amdgcn_perm(vr[3][jj / 2], vr[2][jj / 2], sel)};
+#pragma unroll
+      for (int qw = 0; qw < QW; ++qw)
+        if (live[qw]) acc[qw][jj] = mfma16x16x16<T>(va, pb[qw], acc[qw][jj]);
     }
   };
-  Chunk cs[DEPTH];
+
+  // prologue: chunk 0 staged, chunk 1's loads and page ids in flight
 #pragma unroll
-  for (int i = 0; i < DEPTH; ++i) load_chunk(i * CH, cs[i]);
-  bool more = L > 0;
-  for (int t0 = 0; more; t0 += DEPTH * CH) {
+  for (int i = 0; i < PPT; ++i) pg[i] = page_of(0, i);
+  load_chunk(0, pg);
 #pragma unroll
-    for (int i = 0; i < DEPTH; ++i) {
-      if (more) {
-        consume(t0 + i * CH, cs[i]);
-        load_chunk(t0 + (i + DEPTH) * CH, cs[i]);
-        more = t0 + (i + 1) * CH < L;
-      }
+  for (int i = 0; i < PPT; ++i) pg_next[i] = page_of(min(1, nchunks - 1), i);
+  store_chunk(0);
+  load_chunk(min(1, nchunks - 1), pg_next);
+  __syncthreads();
+  for (int ci = 0; ci < nchunks; ++ci) {
+    const int b = ci & 1;
+    // page ids two chunks ahead
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) pg[i] = page_of(min(ci + 2, nchunks - 1), i);
+    __builtin_amdgcn_sched_barrier(0);
+    if (nvalid > 0) {
+#pragma unroll
+      for (int ss = 0; ss < KC / 16; ++ss) consume(b, ss, ci * KC + 16 * ss);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    store_chunk(b ^ 1);                         // chunk ci + 1 (its buffer was last read in ci - 1)
+    __builtin_amdgcn_sched_barrier(0);
+    load_chunk(min(ci + 2, nchunks - 1), pg);
+    __syncthreads();
   }
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  // lane (r, c) holds dims DPL (4 r + i) + jj of query column c
-  if (c < nvalid) {
-    const size_t orow = (size_t)(row0 + j0 + c) * H + h;
-    const float inv = 1.0f / l;
+  if (nvalid == 0) return;
+  // lane (r, c) of block qw holds dims DPL (4 r + i) + jj of query column 16 qw + c
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t w[VW];
+  for (int qw = 0; qw < QW; ++qw) {
+    float lt = l[qw];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    if (16 * qw + c < nvalid) {
+      const size_t orow = (size_t)(row0 + j0 + 16 * qw + c) * H + h;
+      const float inv = 1.0f / lt;
 #pragma unroll
-      for (int jj = 0; jj < VW; ++jj)
-        w[jj] = pack2<T>(acc[2 * jj][i] * inv, acc[2 * jj + 1][i] * inv);
-      __builtin_memcpy(out + orow * D + DPL * (4 * r + i), w, sizeof(w));
+      for (int i = 0; i < 4; ++i) {
+        uint32_t w[VW];
+#pragma unroll
+        for (int jj = 0; jj < VW; ++jj)
+          w[jj] = pack2<T>(acc[qw][2 * jj][i] * inv, acc[qw][2 * jj + 1][i] * inv);
+        __builtin_memcpy(out + orow * D + DPL * (4 * r + i), w, sizeof(w));
+      }
     }
   }
 }
 
-constexpr int kPrefillTiles = 2;   // 16-token query tiles per workgroup
+constexpr int kPrefillChunk = 32;   // keys staged per barrier (64 measured no faster)
 
 template <typename T, int D, int REP>
 int launch_prefill(const void* q, const void* kp, const void* vp, const int32_t* tables,
                    const int32_t* row0, const int32_t* pos0, const int32_t* nq, void* out,
                    int64_t N, int64_t R, int64_t max_nq, int64_t H, int64_t KV, int64_t P,
                    int64_t num_blocks, int64_t table_stride, float scale, hipStream_t st) {
-  // 8 q heads per kv head: one tile per workgroup (16 waves would cap a wave at 128 VGPRs)
-  constexpr int QT = REP >= 8 ? 1 : kPrefillTiles;
-  const int64_t tiles = (max_nq + 16 * QT - 1) / (16 * QT);
-  const size_t lds = (size_t)QT * REP * 16 * (2 * D + 16);
-  auto kfn = paged_prefill_kernel<T, D, REP, QT>;
-  static bool lds_raised = false;
-  if (!lds_raised && lds > 64 * 1024) {
-    (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              160 * 1024);
-    lds_raised = true;
-  }
-  kfn<<<dim3((unsigned)tiles, (unsigned)KV, (unsigned)N), dim3(QT * REP * kWave), lds, st>>>(
-      (const T*)q, (const T*)kp, (const T*)vp, tables, row0, pos0, nq, (T*)out, (int)R, (int)H,
-      (int)KV, (int)P, (int)num_blocks, (int)table_stride, scale * kLog2e);
+  // four waves per workgroup (eight for 8 q heads per kv head), 32 query rows each
+  constexpr int QG = REP >= 4 ? 1 : 4 / REP;
+  const int64_t tiles = (max_nq + 32 * QG - 1) / (32 * QG);
+  paged_prefill_kernel<T, D, REP, QG, kPrefillChunk>
+      <<<dim3((unsigned)tiles, (unsigned)KV, (unsigned)N), dim3(REP * QG * kWave), 0, st>>>(
+          (const T*)q, (const T*)kp, (const T*)vp, tables, row0, pos0, nq, (T*)out, (int)R,
+          (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, scale * kLog2e);
   ACORN_LAUNCH_CHECK();
   return ACORN_OK;
 }
