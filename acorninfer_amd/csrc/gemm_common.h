@@ -100,7 +100,7 @@ __host__ __device__ inline size_t w4b_half_index(int64_t n, int64_t g, int64_t K
          (size_t)((n % 16) / 4) * 16 + (size_t)(g % 4) * 4 + (size_t)(n % 4);
 }
 
-// ---- the W4B decode kernel (w4_decode.hip) ----------------------------------
+// ---- the W4B decode kernel (w4_decode.hip), M <= 64 -------------------------
 // cfg knobs: rt (row tiles of 16 per wave), upw (groups per pipeline stage),
 // nw (waves per workgroup; 10*nw + kw when kw waves share rows and split K),
 // ksplit, depth (stages in flight per wave); 0 = choose.
@@ -109,6 +109,7 @@ struct W4bPlan {
   int kw;          // K slices per row group (waves sharing rows)
   int nw_field;    // the cfg value of nw (nw, or 10*nw + kw)
   int R;           // x rows staged in LDS (power of 2 >= M)
+  int mb;          // 16-column blocks of x per wave (M <= 16 mb)
   int groups;      // workgroups along N
   size_t lds;      // dynamic LDS bytes
   bool swiglu;

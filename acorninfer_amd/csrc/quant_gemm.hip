@@ -858,8 +858,10 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
     if (req) return ACORN_ERR_UNSUPPORTED;
   }
   if (cfg && cfg[0] == kDenseRT) return ACORN_ERR_UNSUPPORTED;
-  if (wfmt == ACORN_WFMT_W4B && M <= 16 && !(cfg && cfg[0] == 0 && cfg[1] >= 32)) {
-    // decode sizes in the block layout: the W4B decode kernel
+  if (wfmt == ACORN_WFMT_W4B && ((M <= 16 && !(cfg && cfg[0] == 0 && cfg[1] >= 32)) ||
+                                  (M <= 64 && cfg && cfg[0] > 0))) {
+    // decode sizes in the block layout: the W4B decode kernel (up to 64 rows
+    // of x on request)
     const int rc = w4b_make_plan(M, N, K, cfg, swiglu, &t->w4b);
     if (rc) return rc;
     t->kind = 2;
@@ -877,7 +879,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
     return ACORN_OK;
   }
   if (wfmt == ACORN_WFMT_W4B && (swiglu || (cfg && cfg[0] > 0)))
-    return ACORN_ERR_UNSUPPORTED;  // M > 16 in the block layout: the tiled kernel only
+    return ACORN_ERR_UNSUPPORTED;  // M > 64 in the block layout: the tiled kernel only
   // the tiled kernel: the default for M > 16; for M <= 16 on request (rt 0
   // with an M tile of 32 or more in upw)
   if (!swiglu && ((M > 16 && (!cfg || cfg[0] <= 0)) || (cfg && cfg[0] == 0 && cfg[1] >= 32)))

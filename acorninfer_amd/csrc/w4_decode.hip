@@ -1,4 +1,4 @@
-// Weight-only int4 GEMM at decode sizes (M <= 16) over the W4B block layout.
+// Weight-only int4 GEMM at decode sizes (M <= 64) over the W4B block layout.
 //
 // y[M,N] = x[M,K] @ ((u - 8) * s)^T: u the stored nibble (symmetric int4
 // v = u - 8, the reference's m7 spike format with zero = -8 s,
@@ -28,6 +28,10 @@
 //    of DEPTH, so the compiler's wait counts are static.
 //  * Split-K (ksplit > 1) writes fp32 partials [ksplit, M, N], summed in split
 //    order by the consumer (bitwise deterministic).
+//  * M up to 64 (a decode bucket of 32 or 64 sequences, configuration 3's
+//    M = 64): MB = ceil(M / 16) column blocks of x per wave. Every unpacked
+//    weight operand feeds MB MFMAs and every x operand RT, so the same loads
+//    carry MB times the arithmetic; x is staged for 16 MB rows.
 #include "gemm_common.h"
 
 using namespace acorn;
@@ -42,7 +46,7 @@ struct W4bArgs {
   float* part;    // fp32 [ksplit, M, N] otherwise
   int M, N, K;
   int kr;         // K range of a workgroup (a multiple of 128 * KW * UPW * DEPTH)
-  int log2R;      // x rows staged = 1 << log2R >= M
+  int log2R;      // x rows staged = 1 << log2R >= M (16 MB when MB > 1)
 };
 
 template <int RT, int UPW>
@@ -52,9 +56,11 @@ struct Stage {
 };
 
 // Grid: x = groups of (NW/KW)*RT row tiles, y = ksplit. Block: NW waves.
-template <int RT, int UPW, int DEPTH, int NW, int KW, bool SWIGLU>
+// MB: 16-column blocks of x (MB = 1: M <= 16, R rows staged; else R = 16 MB).
+template <int RT, int UPW, int DEPTH, int NW, int KW, bool SWIGLU, int MB = 1>
 __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   static_assert(NW % KW == 0, "K slices divide the waves");
+  constexpr int RS = 16 * MB;                     // x-sum columns per group
   constexpr int NT = NW * kWave;
   extern __shared__ __align__(16) unsigned char smem[];
   const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -67,8 +73,8 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   const int t0 = (blockIdx.x * (NW / KW) + rg) * RT;   // the row group's first tile
   const bool active = t0 < a.N / 16;              // (N / 16) % RT == 0 by the plan
   const int tt = active ? t0 : 0;                 // idle waves read tile 0, store nothing
-  // LDS: x pieces [CPR][R] (16 bytes each, W4 k order) | group sums [GR][16]
-  //      | K-slice results [NW][RT][4][64] (KW > 1)
+  // LDS: x pieces [CPR][R] (16 bytes each, W4 k order) | group sums [GR][RS]
+  //      | K-slice results [NW][RT][MB][4][64] (KW > 1)
   u32x4* xs = (u32x4*)smem;
   float* xgs = (float*)(smem + (size_t)CPR * R * 16);
 
@@ -118,39 +124,71 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
       if (p0 + u * NT < xtotal) xs[p0 + u * NT] = w4_order_x(xv[u]);
   }
   __syncthreads();
-  // X per (group, column): an MFMA of ones against the group's x
+  // X per (group, column): an MFMA of ones against the group's x. Column
+  // block mb of a lane is x row col(mb) (MB = 1: rows past R repeat).
   const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
-  const int xrow = lr & (R - 1);
-  for (int g = wid; g < GR; g += NW) {
+  const int xrow = MB == 1 ? (lr & (R - 1)) : lr;
+  for (int q = wid; q < GR * MB; q += NW) {
+    const int g = q / MB, mb = q % MB;
     f32x4 xg = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xg = mfma(ones, xs[(g * 16 + 4 * lg + j) * R + xrow], xg);
-    if (lg == 0) xgs[g * 16 + lr] = xg[0];
+    for (int j = 0; j < 4; ++j)
+      xg = mfma(ones, xs[(g * 16 + 4 * lg + j) * R + mb * 16 + xrow], xg);
+    if (lg == 0) xgs[g * RS + mb * 16 + lr] = xg[0];
   }
   __syncthreads();
 
   // ---- stream ------------------------------------------------------------------
-  f32x4 acc[RT];
+  f32x4 acc[RT][MB];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[rt][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto compute = [&](const Stage<RT, UPW>& r, int s) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
       const int gl = gw0 + s * UPW + u;
-      const u32x4* xp = xs + (gl * 16 + 4 * lg) * R + xrow;
-      u32x4 b[4];
+      if constexpr (MB == 1) {
+        const u32x4* xp = xs + (gl * 16 + 4 * lg) * R + xrow;
+        u32x4 b[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = xp[j * R];
-      const float xg = xgs[gl * 16 + lr];
+        for (int j = 0; j < 4; ++j) b[j] = xp[j * R];
+        const float xg = xgs[gl * 16 + lr];
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        f32x4 cc = {0.f, 0.f, 0.f, 0.f};
+        for (int rt = 0; rt < RT; ++rt) {
+          f32x4 cc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) cc = mfma(unpack_w4(r.w[rt][u][j]), b[j], cc);
+          for (int j = 0; j < 4; ++j) cc = mfma(unpack_w4(r.w[rt][u][j]), b[j], cc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          acc[rt][i] = __builtin_fmaf(half_f(r.s[rt], 4 * u + i),
-                                      __builtin_fmaf(xg, -136.f, cc[i]), acc[rt][i]);
+          for (int i = 0; i < 4; ++i)
+            acc[rt][0][i] = __builtin_fmaf(half_f(r.s[rt], 4 * u + i),
+                                           __builtin_fmaf(xg, -136.f, cc[i]), acc[rt][0][i]);
+        }
+      } else {
+        // the RT tiles' unpacked operands, then one column block at a time
+        u32x4 aw[RT][4];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) aw[rt][j] = unpack_w4(r.w[rt][u][j]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const u32x4* xp = xs + (gl * 16 + 4 * lg) * R + mb * 16 + lr;
+          u32x4 b[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) b[j] = xp[j * R];
+          const float xg = xgs[gl * RS + mb * 16 + lr];
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            f32x4 cc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cc = mfma(aw[rt][j], b[j], cc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              acc[rt][mb][i] = __builtin_fmaf(half_f(r.s[rt], 4 * u + i),
+                                              __builtin_fmaf(xg, -136.f, cc[i]), acc[rt][mb][i]);
+          }
+        }
       }
       // one group at a time: without this fence the scheduler hoists the
       // unpacking of later groups and the register ring no longer fits
@@ -171,11 +209,14 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   }
   if constexpr (KW > 1) {
     // the K slices of a row group, added in slice order by slice 0
-    float* red = xgs + GR * 16;
+    float* red = xgs + GR * RS;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[((wid * RT + rt) * 4 + i) * kWave + lane] = acc[rt][i];
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          red[(((wid * RT + rt) * MB + mb) * 4 + i) * kWave + lane] = acc[rt][mb][i];
     __syncthreads();
     if (kq != 0) return;
 #pragma unroll
@@ -183,53 +224,59 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          acc[rt][i] += red[(((wid + q) * RT + rt) * 4 + i) * kWave + lane];
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            acc[rt][mb][i] += red[((((wid + q) * RT + rt) * MB + mb) * 4 + i) * kWave + lane];
   }
   if (!active) return;
 
-  // ---- store: lane (lr, lg) holds rows 4*lg .. 4*lg+3 of column lr ------------
-  const int m = lr;
-  if (m >= a.M) return;
-  if constexpr (SWIGLU) {
-    // tiles 2j (gate) and 2j+1 (up) hold the 16 outputs of block j
-    const int NA = a.N / 2;
+  // ---- store: lane (lr, lg) holds rows 4*lg .. 4*lg+3 of column 16 mb + lr ---
 #pragma unroll
-    for (int p = 0; p < RT / 2; ++p) {
-      const int n = (t0 / 2 + p) * 16 + 4 * lg;
-      uint32_t v[2];
-      v[0] = pack_bf16x2(swiglu_bf16(acc[2 * p][0], acc[2 * p + 1][0]),
-                         swiglu_bf16(acc[2 * p][1], acc[2 * p + 1][1]));
-      v[1] = pack_bf16x2(swiglu_bf16(acc[2 * p][2], acc[2 * p + 1][2]),
-                         swiglu_bf16(acc[2 * p][3], acc[2 * p + 1][3]));
-      __builtin_memcpy(a.out + (size_t)m * NA + n, v, sizeof(v));
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = mb * 16 + lr;
+    if (m >= a.M) break;
+    if constexpr (SWIGLU) {
+      // tiles 2j (gate) and 2j+1 (up) hold the 16 outputs of block j
+      const int NA = a.N / 2;
+#pragma unroll
+      for (int p = 0; p < RT / 2; ++p) {
+        const int n = (t0 / 2 + p) * 16 + 4 * lg;
+        uint32_t v[2];
+        v[0] = pack_bf16x2(swiglu_bf16(acc[2 * p][mb][0], acc[2 * p + 1][mb][0]),
+                           swiglu_bf16(acc[2 * p][mb][1], acc[2 * p + 1][mb][1]));
+        v[1] = pack_bf16x2(swiglu_bf16(acc[2 * p][mb][2], acc[2 * p + 1][mb][2]),
+                           swiglu_bf16(acc[2 * p][mb][3], acc[2 * p + 1][mb][3]));
+        __builtin_memcpy(a.out + (size_t)m * NA + n, v, sizeof(v));
+      }
+    } else if (a.out) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const int n = (t0 + rt) * 16 + 4 * lg;
+        uint32_t v[2] = {pack_bf16x2(acc[rt][mb][0], acc[rt][mb][1]),
+                         pack_bf16x2(acc[rt][mb][2], acc[rt][mb][3])};
+        __builtin_memcpy(a.out + (size_t)m * a.N + n, v, sizeof(v));
+      }
+    } else {
+      float* dst = a.part + ((size_t)blockIdx.y * a.M + m) * a.N;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) *(f32x4*)(dst + (t0 + rt) * 16 + 4 * lg) = acc[rt][mb];
     }
-  } else if (a.out) {
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const int n = (t0 + rt) * 16 + 4 * lg;
-      uint32_t v[2] = {pack_bf16x2(acc[rt][0], acc[rt][1]), pack_bf16x2(acc[rt][2], acc[rt][3])};
-      __builtin_memcpy(a.out + (size_t)m * a.N + n, v, sizeof(v));
-    }
-  } else {
-    float* dst = a.part + ((size_t)blockIdx.y * a.M + m) * a.N;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) *(f32x4*)(dst + (t0 + rt) * 16 + 4 * lg) = acc[rt];
   }
 }
 
-size_t w4b_lds(int R, int64_t kr, int nw, int kw, int rt) {
-  return (size_t)kr * R * 2 + (size_t)(kr / 128) * 64 +
-         (kw > 1 ? (size_t)nw * rt * 4 * kWave * 4 : 0);
+size_t w4b_lds(int R, int64_t kr, int nw, int kw, int rt, int mb) {
+  return (size_t)kr * R * 2 + (size_t)(kr / 128) * 16 * mb * 4 +
+         (kw > 1 ? (size_t)nw * rt * mb * 4 * kWave * 4 : 0);
 }
 
-template <int RT, int UPW, int DEPTH, int NW, int KW>
+template <int RT, int UPW, int DEPTH, int NW, int KW, int MB>
 int launch5(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
-  auto kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, KW, false>;
+  auto kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, KW, false, MB>;
   int variant = 0;
-  if constexpr (RT >= 2) {
+  if constexpr (RT >= 2 && MB == 1) {
     if (p.swiglu) {
-      kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, KW, true>;
+      kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, KW, true, MB>;
       variant = 1;
     }
   }
@@ -245,41 +292,55 @@ int launch5(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
 }
 
 // (waves, K slices) per workgroup
-template <int RT, int UPW, int DEPTH>
+template <int RT, int UPW, int DEPTH, int MB>
 int launch3(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
   switch (p.nw * 16 + p.kw) {
-    case 2 * 16 + 1: return launch5<RT, UPW, DEPTH, 2, 1>(p, a, st);
-    case 4 * 16 + 1: return launch5<RT, UPW, DEPTH, 4, 1>(p, a, st);
-    case 4 * 16 + 2: return launch5<RT, UPW, DEPTH, 4, 2>(p, a, st);
-    case 4 * 16 + 4: return launch5<RT, UPW, DEPTH, 4, 4>(p, a, st);
-    case 8 * 16 + 2: return launch5<RT, UPW, DEPTH, 8, 2>(p, a, st);
-    case 8 * 16 + 4: return launch5<RT, UPW, DEPTH, 8, 4>(p, a, st);
+    case 2 * 16 + 1: return launch5<RT, UPW, DEPTH, 2, 1, MB>(p, a, st);
+    case 4 * 16 + 1: return launch5<RT, UPW, DEPTH, 4, 1, MB>(p, a, st);
+    case 4 * 16 + 2: return launch5<RT, UPW, DEPTH, 4, 2, MB>(p, a, st);
+    case 4 * 16 + 4: return launch5<RT, UPW, DEPTH, 4, 4, MB>(p, a, st);
+    case 8 * 16 + 2: return launch5<RT, UPW, DEPTH, 8, 2, MB>(p, a, st);
+    case 8 * 16 + 4: return launch5<RT, UPW, DEPTH, 8, 4, MB>(p, a, st);
   }
   return ACORN_ERR_UNSUPPORTED;
 }
 
-template <int RT, int UPW>
+// MB > 1 (more arithmetic per loaded byte) is built for one or two stages in
+// flight of one or two groups
+template <int RT, int UPW, int MB>
 int launch2(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
   switch (p.depth) {
-    case 1: return launch3<RT, UPW, 1>(p, a, st);
-    case 2: return launch3<RT, UPW, 2>(p, a, st);
+    case 1: return launch3<RT, UPW, 1, MB>(p, a, st);
+    case 2: return launch3<RT, UPW, 2, MB>(p, a, st);
     case 4:
-      if constexpr (RT * UPW <= 4 && RT < 4) return launch3<RT, UPW, 4>(p, a, st);
+      if constexpr (MB == 1 && RT * UPW <= 4 && RT < 4) return launch3<RT, UPW, 4, MB>(p, a, st);
       break;
     case 8:
-      if constexpr (RT * UPW <= 2) return launch3<RT, UPW, 8>(p, a, st);
+      if constexpr (MB == 1 && RT * UPW <= 2) return launch3<RT, UPW, 8, MB>(p, a, st);
       break;
   }
   return ACORN_ERR_UNSUPPORTED;
 }
 
-template <int RT>
+template <int RT, int MB>
 int launch1(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
   switch (p.upw) {
-    case 1: return launch2<RT, 1>(p, a, st);
-    case 2: return launch2<RT, 2>(p, a, st);
+    case 1: return launch2<RT, 1, MB>(p, a, st);
+    case 2: return launch2<RT, 2, MB>(p, a, st);
     case 4:
-      if constexpr (RT == 1) return launch2<RT, 4>(p, a, st);
+      if constexpr (RT == 1 && MB == 1) return launch2<RT, 4, MB>(p, a, st);
+      break;
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+template <int MB>
+int launch_rt(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
+  switch (p.rt) {
+    case 1: return launch1<1, MB>(p, a, st);
+    case 2: return launch1<2, MB>(p, a, st);
+    case 4:
+      if constexpr (MB <= 2) return launch1<4, MB>(p, a, st);
       break;
   }
   return ACORN_ERR_UNSUPPORTED;
@@ -302,8 +363,12 @@ namespace acorn {
 // range holds a whole number of depth-stage rounds. With 0 the split grows
 // from 1 until about two workgroups per CU are launched, while one
 // workgroup's x fits its LDS budget and each K range keeps at least 512 k.
+// 16 < M <= 64 uses mb = ceil(M / 16) column blocks (32 or 64 x rows staged)
+// with rt * mb <= 8, upw and depth 1 or 2, and no fused SwiGLU.
 int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4bPlan* p) {
-  if (M < 1 || M > 16) return ACORN_ERR_UNSUPPORTED;
+  if (M < 1 || M > 64) return ACORN_ERR_UNSUPPORTED;
+  const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  if (mb > 1 && swiglu) return ACORN_ERR_UNSUPPORTED;
   if (N % 16 || K % 512) return ACORN_ERR_SHAPE;
   if (swiglu && N % 32) return ACORN_ERR_SHAPE;
   const int64_t ntiles = N / 16, G = K / 128;
@@ -321,8 +386,10 @@ int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   if (ntiles % rt) return ACORN_ERR_UNSUPPORTED;
   if (upw != 1 && upw != 2 && upw != 4) return ACORN_ERR_UNSUPPORTED;
   if (rt * upw > 8 || (rt == 4 && upw > 2) || (rt == 2 && upw > 2)) return ACORN_ERR_UNSUPPORTED;
+  if (mb > 1 && (rt * mb > 8 || upw > 2)) return ACORN_ERR_UNSUPPORTED;
   int R = 1;
   while (R < M) R *= 2;
+  if (mb > 1) R = 16 * mb;
   if (G % upw) return ACORN_ERR_SHAPE;
   const int64_t stages = G / upw;            // per row over the whole K
   if (stages % kw) return ACORN_ERR_UNSUPPORTED;
@@ -330,7 +397,7 @@ int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   const size_t lds_cap = 160 * 1024, lds_default = 80 * 1024;
   const int64_t rows_per_wg = (int64_t)(nw / kw) * rt;
   const int64_t groups = (ntiles / rt + nw / kw - 1) / (nw / kw);
-  auto lds = [&](int ks) { return w4b_lds(R, K / ks, nw, kw, rt); };
+  auto lds = [&](int ks) { return w4b_lds(R, K / ks, nw, kw, rt, mb); };
   int ks;
   if (swiglu) {
     ks = 1;
@@ -353,10 +420,10 @@ int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   }
   if (lds(ks) > lds_cap) return ACORN_ERR_UNSUPPORTED;
   const int64_t ns = slices / ks;            // stages of one wave
-  int depth = req_depth > 0 ? req_depth : 4;
+  int depth = req_depth > 0 ? req_depth : mb > 1 ? 2 : 4;
   if (depth != 1 && depth != 2 && depth != 4 && depth != 8) return ACORN_ERR_UNSUPPORTED;
   while (depth > 1 && (ns % depth || rt * upw * depth > 16 || (rt == 4 && depth > 2) ||
-                       (rt * upw > 2 && depth > 4)))
+                       (rt * upw > 2 && depth > 4) || (mb > 1 && depth > 2)))
     depth /= 2;
   (void)rows_per_wg;
   p->rt = rt;
@@ -367,6 +434,7 @@ int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   p->ksplit = ks;
   p->depth = depth;
   p->R = R;
+  p->mb = mb;
   p->groups = (int)groups;
   p->lds = lds(ks);
   p->swiglu = swiglu;
@@ -396,10 +464,10 @@ int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale
   while ((1 << l) < p.R) ++l;
   a.log2R = l;
   int rc = ACORN_ERR_UNSUPPORTED;
-  switch (p.rt) {
-    case 1: rc = launch1<1>(p, a, st); break;
-    case 2: rc = launch1<2>(p, a, st); break;
-    case 4: rc = launch1<4>(p, a, st); break;
+  switch (p.mb) {
+    case 1: rc = launch_rt<1>(p, a, st); break;
+    case 2: rc = launch_rt<2>(p, a, st); break;
+    case 4: rc = launch_rt<4>(p, a, st); break;
   }
   if (rc) return rc;
   ACORN_LAUNCH_CHECK();

@@ -829,7 +829,8 @@ PREFILL_WS_BYTES = 256 << 20   # cap on a prefill launch's K3 split workspace
 SMALL_GRID_PAGES = 1024   # below this many (sequence, kv head, page) units: 1-page splits
 MAX_SPLITS = 64     # bound on K3 splits per (sequence, kv head)
 WIDE_GRID = 256     # (sequence, kv head) pairs that fill the CUs on their own ...
-ONE_SPLIT_MAX_PAGES = 64   # ... take one split over tables this wide
+ONE_SPLIT_MAX_PAGES = 64   # ... take one split over tables this wide,
+WIDE_UNIT_PAGES = 16       # ... and splits of this many pages over wider ones
 QKV_SPLITS_UP_FRONT = 4   # qkv split partials the fused K3 loads up front (kQB)
 RETIME_TOP = 4      # tune(): candidates timed a second time ...
 RETIME_REPS = 12    # ... with this many graph replays
@@ -852,9 +853,15 @@ def attention_splits(batch: int, kv_heads: int, max_pages: int, *,
     fills the CUs with (sequence, kv head) pairs alone (WIDE_GRID) over
     tables of at most ONE_SPLIT_MAX_PAGES pages takes one split: each pair
     is one workgroup of four waves merged in LDS, with no combine launch
-    (C = 32 at 512 tokens: 4.43 against 4.56 ms per step)."""
-    if unit_pages is None and batch * kv_heads >= WIDE_GRID and max_pages <= ONE_SPLIT_MAX_PAGES:
-        return 1
+    (C = 32 at 512 tokens: 4.43 against 4.56 ms per step). Over wider tables
+    such a grid takes WIDE_UNIT_PAGES-page splits, the longest that still run
+    as one-wave workgroups: half the partials of 8-page splits for the
+    combine (C = 64 over prompts U[1024, 8192], 512-page tables: K3 + combine
+    220 against 234 us per layer)."""
+    if unit_pages is None and batch * kv_heads >= WIDE_GRID:
+        if max_pages <= ONE_SPLIT_MAX_PAGES:
+            return 1
+        unit_pages = WIDE_UNIT_PAGES
     if unit_pages is None:
         unit_pages = 1 if batch * kv_heads * max_pages < SMALL_GRID_PAGES else UNIT_PAGES
     return max(1, min(-(-max_pages // unit_pages), max_splits))

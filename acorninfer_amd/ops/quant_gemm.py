@@ -40,6 +40,7 @@ FUSED_CLASSES = {
 _CLS_BY_SHAPE = {v: k for k, v in CLASSES.items()}
 
 DECODE_M_MAX = 16
+W4B_M_MAX = 64      # the int4 decode kernel takes up to this many rows on request
 M_BUCKETS_LARGE = ("s", "m", "l")
 _M_REP_M = {"s": 64, "m": 256, "l": 1024}
 
@@ -74,10 +75,10 @@ class Tiling(NamedTuple):
     Tiled kernel (M > 16 with rt == 0, the default there): upw is the M tile
     BM (32 / 64 / 128), nw the N tile BN (64 / 128), ksplit the K split; the
     planner reports (0, BM, BN, ksplit, 1).
-    int4 decode kernel (WFMT_W4B, M <= 16): rt row tiles per wave, upw
-    128-k groups per pipeline stage, nw waves per workgroup (2 or 4 each on
-    its own rows; 10*nw + kw: kw waves share rows and split K), ksplit, and
-    tpw = stages in flight per wave.
+    int4 decode kernel (WFMT_W4B, M <= 16, and 16 < M <= 64 with rt >= 1):
+    rt row tiles per wave, upw 128-k groups per pipeline stage, nw waves per
+    workgroup (2 or 4 each on its own rows; 10*nw + kw: kw waves share rows
+    and split K), ksplit, and tpw = stages in flight per wave.
     Large-M bf16 kernel (the default for bf16 from 512 rows, or rt == -2):
     upw is the M tile (64 / 128), nw the weight rows per wave (64 / 128; a
     workgroup's weight tile is 4 nw), tpw the weight prefetch depth in 64-k
@@ -316,6 +317,8 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
                     reqs.append(Tiling(0, upw, nw, ks, tpw))
     if M > DECODE_M_MAX and not swiglu:
         reqs = [r for r in reqs if r.rt > 0]      # rt 0 means the tiled kernel here
+        if wfmt == WFMT_W4B and M <= W4B_M_MAX:
+            reqs = _w4b_wide_requests()           # the int4 kernel with 2 or 4 x blocks
         for bm in (32, 64, 128):
             for bn in (64, 128):
                 for ks in (0, 1, 2, 4, 8):
@@ -330,8 +333,9 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
 
 def _w4b_requests(swiglu: bool) -> list[Tiling]:
     """Requests covering the int4 decode kernel's knobs: up to 16 KB of
-    weights in flight per wave (rt * upw * depth <= 16), and split counts
-    from one to sixteen."""
+    weights in flight per wave (rt * upw * depth <= 16), every wave layout
+    (4 waves on their own rows; 4 or 8 waves in row groups of 2 or 4 K
+    slices), and split counts from one to sixteen."""
     reqs = []
     for rt in ((2, 4) if swiglu else (1, 2, 4)):
         for upw in ((1, 2, 4) if rt == 1 else (1, 2)):
@@ -340,10 +344,19 @@ def _w4b_requests(swiglu: bool) -> list[Tiling]:
                     continue
                 # waves per workgroup: 2 or 4 each on its own rows, or
                 # 10*nw + kw with kw waves splitting K over shared rows
-                for nw in (4, 42, 82):
+                for nw in (4, 42, 82, 44, 84):
                     for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
                         reqs.append(Tiling(rt, upw, nw, ks, depth))
     return reqs
+
+
+def _w4b_wide_requests() -> list[Tiling]:
+    """The int4 decode kernel's knobs for 16 < M <= 64 (32 or 64 staged x
+    rows): rt * column blocks <= 8, one or two groups per stage, one or two
+    stages in flight."""
+    return [Tiling(rt, upw, nw, ks, depth)
+            for rt in (1, 2, 4) for upw in (1, 2) for depth in (1, 2)
+            for nw in (2, 4, 42, 44, 82, 84) for ks in (0, 1, 2, 3, 4, 6, 8, 12, 16)]
 
 
 def _resolve(reqs, planner, M, N, K, wfmt, base) -> list[Tiling]:

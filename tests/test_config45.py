@@ -277,5 +277,9 @@ def test_config5_w4a16_sampled_c64(w4_pair):
     caches = _Caches(model, lens, seed=SEED + 64, ref_dtype=torch.float32)
     alloc, cache, views = caches.pairs[0]
     print(f"\n[config5 w4a16 C={C}: mean history {sum(lens) / C:.0f}]", flush=True)
+    model.tune(C)          # the bench's choice at this bucket (tiled or wide int4 kernel)
+    print(f"  tilings {model.tilings[C]}", flush=True)
     runner = DecodeGraphRunner(model, cache, alloc, max_model_len=8192 + 64, seed=SEED + 1)
     _sampled_steps(model, ref, runner, caches, views, C, 3, SEED + 1, "config5 C=64")
+    st = runner.states[64]
+    assert st.buf.num_splits == 33 and st.buf.max_pages == 516   # 16-page K3 splits

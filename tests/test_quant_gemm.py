@@ -283,6 +283,35 @@ def test_w4b_tiled_equals_natural_bitwise(m):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m", [17, 32, 40, 64])
+def test_w4b_wide_decode_kernel_matches(m):
+    """The int4 decode kernel above 16 rows (two or four 16-column blocks of
+    x per wave; the rows past M of the last block clamped to row M-1 and
+    never stored) at every tiling the load-time sweep offers it, on the o
+    shape (K=4096) and the down shape (K=12288), against the dequantised
+    matmul; each output row also equals the same kernel's result for that
+    row alone up to fp32 summation order (the blocks do not mix rows)."""
+    from acorninfer_amd._lib import WFMT_W4B
+    from acorninfer_amd.ops.quant_gemm import _launch, candidates
+    from acorninfer_amd.quant.quantize import to_w4b
+    for cls in ("o", "down"):
+        p, s, wref = _w4(cls)
+        wb, sb = to_w4b(p, s)
+        n, k = SHAPES[cls]
+        x = _x(m, k, 12)
+        ref = _ref(x, wref)
+        cands = [c for c in candidates(m, n, k, WFMT_W4B) if c.rt > 0]
+        assert len(cands) >= 8, len(cands)
+        for c in cands:
+            out = _launch(x, wb, sb, None, WFMT_W4B, n, c, None)
+            r = rel_err(out, ref)
+            assert r <= GEMM_REL, f"{cls} M={m} {tuple(c)}: rel err {r:.3g}"
+        last = _launch(x[m - 1:], wb, sb, None, WFMT_W4B, n, None, None)
+        assert rel_err(out[m - 1:], last) <= 1e-5
+        print(f"\n[w4b wide M={m} {cls}: {len(cands)} tilings ok]")
+
+
+@pytest.mark.gpu
 def test_w4b_split_partials_deterministic_and_graph_replay():
     """W4B partials at several split counts sum (in split order) to the same
     result within fp32 rounding, repeat bitwise, and replay bitwise in a
