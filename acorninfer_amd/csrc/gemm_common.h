@@ -121,6 +121,20 @@ int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale
                const void* zero, void* out, float* part, int64_t M, int64_t N, int64_t K,
                hipStream_t st);
 
+// ---- the int4 GEMM for 17..256 rows (w4_decode.hip) ----------------------------
+// cfg knobs (rt = kMidRT marks the request): upw = row tiles per wave (1, 2),
+// nw = waves (4, 8), ksplit, tpw = groups in flight (2, 4); 64 x rows per
+// workgroup, x streamed through LDS one 128-k group at a time.
+struct W4mPlan {
+  int rt, nw, ksplit, depth;
+  int groups;      // row blocks of nw * rt * 16 rows
+  int mblocks;     // blocks of 64 x rows
+  size_t lds;
+};
+int w4m_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, W4mPlan* p);
+int w4m_launch(const W4mPlan& p, const void* x, const void* w, const void* scale, void* out,
+               float* part, int64_t M, int64_t N, int64_t K, hipStream_t st);
+
 // ---- the large-M bf16 GEMM (dense_gemm.hip) ---------------------------------
 // out[M,N] = x[M,K] . w[N,K]^T, bf16 operands: (4 wn) x bm output tiles (wn
 // weight rows per wave: 64 or 128; bm 64 or 128), weights prefetched `depth`

@@ -720,8 +720,11 @@ struct Tiling {
   int kind;                      // 0 = streaming kernel, 1 = tiled kernel (rt == 0, upw = BM),
                                  // 2 = W4B decode kernel (tpw = its pipeline depth),
                                  // 3 = large-M bf16 kernel (rt == kDenseRT, upw = BM,
-                                 //     nw = weight rows per wave, tpw = prefetch depth)
+                                 //     nw = weight rows per wave, tpw = prefetch depth),
+                                 // 4 = W4B mid-M kernel (rt == kMidRT, upw = row tiles
+                                 //     per wave, nw = waves, tpw = groups in flight)
   W4bPlan w4b;
+  W4mPlan w4m;
 };
 
 int ilog2_ceil(int v) {
@@ -818,6 +821,8 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
 // this many rows on, or on request (rt == kDenseRT).
 constexpr int kDenseRT = -2;
 constexpr int64_t kDenseMinM = 512;
+// W4B above 16 rows on request (rt == kMidRT): the mid-M int4 kernel
+constexpr int kMidRT = -3;
 
 int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling* t,
               bool swiglu = false) {
@@ -858,6 +863,25 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
     if (req) return ACORN_ERR_UNSUPPORTED;
   }
   if (cfg && cfg[0] == kDenseRT) return ACORN_ERR_UNSUPPORTED;
+  if (cfg && cfg[0] == kMidRT) {
+    if (wfmt != ACORN_WFMT_W4B || swiglu || M <= 16) return ACORN_ERR_UNSUPPORTED;
+    const int rc = w4m_make_plan(M, N, K, cfg, &t->w4m);
+    if (rc) return rc;
+    t->kind = 4;
+    t->rt = kMidRT;
+    t->upw = t->w4m.rt;
+    t->nw = t->w4m.nw;
+    t->ksplit = t->w4m.ksplit;
+    t->tpw = t->w4m.depth;
+    t->mt = 1;
+    t->R = 1;
+    t->nk = 0;
+    t->ntiles = t->w4m.groups;
+    t->mblocks = t->w4m.mblocks;
+    t->groups = t->w4m.groups;
+    t->lds = t->w4m.lds;
+    return ACORN_OK;
+  }
   if (wfmt == ACORN_WFMT_W4B && ((M <= 16 && !(cfg && cfg[0] == 0 && cfg[1] >= 32)) ||
                                   (M <= 64 && cfg && cfg[0] > 0))) {
     // decode sizes in the block layout: the W4B decode kernel (up to 64 rows
@@ -1133,6 +1157,9 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
   } else if (t.kind == 2) {
     rc = w4b_launch(t.w4b, x, w, scale, zero, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K,
                     st);
+  } else if (t.kind == 4) {
+    if (zero) return ACORN_ERR_UNSUPPORTED;  // the block layout is the symmetric format
+    rc = w4m_launch(t.w4m, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
   } else if (t.kind == 1) {
     switch (wfmt) {
       case ACORN_WFMT_BF16: rc = dispatch_tiled<ACORN_WFMT_BF16>(t, a, st); break;

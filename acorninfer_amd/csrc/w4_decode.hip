@@ -265,6 +265,178 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// int4 GEMM for batches of 17..256 rows (a decode bucket of 64, configuration
+// 3's M = 64 / 256), on the same W4B blocks. At these M the cost is moving x:
+// every workgroup needs x for its K range, so the rows per workgroup set the x
+// traffic (N / rows re-reads of it) and the split count the partial traffic.
+// Here a workgroup of NW waves owns NW * RT 16-row tiles (256 rows at NW = 8,
+// RT = 2) x 64 columns of x over a K range, and x moves through LDS one
+// 128-k group at a time:
+//  * every thread loads its share of the group's x (2 or 4 pieces of 16 bytes)
+//    and each wave its RT weight blocks and their scales, DEPTH groups ahead in
+//    a register ring (the loads of a group are issued together, so waiting for
+//    the oldest group never waits for a later one);
+//  * per group: the x pieces go to LDS (two buffers), one barrier, four waves
+//    form X (the sum of x over the group, per column) with MFMAs against ones,
+//    a second barrier, then each wave runs RT x 4 x 4 MFMAs: the unpacked
+//    weight operands of a tile feed the four column blocks, each x operand the
+//    RT tiles, and y += s (C - 136 X) as in the decode kernel;
+//  * the M blocks of one (row block, split) are dealt to one XCD, so their
+//    weight re-reads come from its L2;
+//  * split-K partials as everywhere else: fp32 [ksplit, M, N], summed in split
+//    order by the consumer.
+struct W4mArgs {
+  const __bf16* x;
+  const uint8_t* w;
+  const _Float16* scale;
+  __bf16* out;    // bf16 [M, N] when ksplit == 1
+  float* part;    // fp32 [ksplit, M, N] otherwise
+  int M, N, K;
+  int kr;         // K range of a split (a multiple of 128 * DEPTH)
+};
+
+constexpr int kMidBM = 64;                      // columns (x rows) per workgroup
+constexpr int kMidMB = kMidBM / 16;
+
+template <int RT, int NW, int DEPTH>
+__global__ __launch_bounds__(NW * kWave, 1) void w4b_mid_kernel(W4mArgs a) {
+  constexpr int NT = NW * kWave;
+  constexpr int XPT = kMidBM * 16 / NT;          // x pieces per thread per group
+  static_assert(XPT >= 1 && kMidBM * 16 % NT == 0, "whole x pieces per thread");
+  extern __shared__ __align__(16) unsigned char smem[];
+  u32x4* xs = (u32x4*)smem;                      // [2][16 pieces][64 rows]
+  float* xsum = (float*)(smem + 2 * 16 * kMidBM * 16);   // [2][64]
+  const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lg = lane >> 4, lr = lane & 15;
+  int tile, split, mblk;
+  {
+    const int ntl = gridDim.x, nks = gridDim.y, nmb = gridDim.z;
+    const int lin = blockIdx.x + ntl * (blockIdx.y + nks * blockIdx.z);
+    const int units = ntl * nks;
+    int unit;
+    if (nmb > 1 && units % 8 == 0) {
+      const int xcd = lin % 8, j = lin / 8;
+      unit = xcd * (units / 8) + j / nmb;
+      mblk = j % nmb;
+    } else {
+      unit = lin % units;
+      mblk = lin / units;
+    }
+    tile = unit % ntl;
+    split = unit / ntl;
+  }
+  const int G = a.K / 128, G4 = a.K / 512;
+  const int t0 = (tile * NW + wid) * RT;         // this wave's first 16-row tile
+  const int gbase = split * (a.kr / 128);
+  const int nch = a.kr / 128;
+  const int m0 = mblk * kMidBM;
+
+  struct Slot {
+    u32x4 x[XPT];
+    u32x4 w[RT];
+    uint32_t s[RT][2];
+  };
+  // piece p of a group: k piece p / 64 (8 k), x row p % 64 (rows past M
+  // re-read row M - 1; their columns are never stored)
+  auto load = [&](int c, Slot& sl) {
+    const int g = gbase + min(c, nch - 1);
+#pragma unroll
+    for (int u = 0; u < XPT; ++u) {
+      const int p = (int)threadIdx.x + NT * u;
+      const int m = min(m0 + p % kMidBM, a.M - 1);
+      sl.x[u] = *(const u32x4*)(a.x + (size_t)m * a.K + g * 128 + (p / kMidBM) * 8);
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const size_t t = (size_t)(t0 + rt);
+      sl.w[rt] = load_nt((const u32x4*)(a.w + (t * G + g) * 1024 + lane * 16));
+      load_dwords(a.scale + (((t * G4 + g / 4) * 4 + lg) * 16 + (g % 4) * 4), sl.s[rt]);
+    }
+  };
+
+  f32x4 acc[RT][kMidMB];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mb = 0; mb < kMidMB; ++mb) acc[rt][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+
+  auto group = [&](int c, const Slot& sl) {
+    const int b = c & 1;
+    u32x4* xb = xs + b * 16 * kMidBM;
+#pragma unroll
+    for (int u = 0; u < XPT; ++u) xb[threadIdx.x + NT * u] = w4_order_x(sl.x[u]);
+    __syncthreads();
+    if (wid < kMidMB) {
+      f32x4 xg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xg = mfma(ones, xb[(4 * lg + j) * kMidBM + wid * 16 + lr], xg);
+      if (lg == 0) xsum[b * kMidBM + wid * 16 + lr] = xg[0];
+    }
+    __syncthreads();
+    u32x4 aw[RT][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) aw[rt][j] = unpack_w4(sl.w[rt][j]);
+#pragma unroll
+    for (int mb = 0; mb < kMidMB; ++mb) {
+      u32x4 bx[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bx[j] = xb[(4 * lg + j) * kMidBM + mb * 16 + lr];
+      const float xg = xsum[b * kMidBM + mb * 16 + lr];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        f32x4 cc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cc = mfma(aw[rt][j], bx[j], cc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[rt][mb][i] = __builtin_fmaf(half_f(sl.s[rt], i), __builtin_fmaf(xg, -136.f, cc[i]),
+                                          acc[rt][mb][i]);
+      }
+    }
+  };
+
+  Slot ring[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+  for (int c0 = 0; c0 < nch; c0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      group(c0 + d, ring[d]);
+      load(c0 + d + DEPTH, ring[d]);   // past the end: re-reads the last group
+    }
+  }
+
+  // lane (lr, lg) holds rows 4 lg .. 4 lg + 3 of tile t0 + rt, column 16 mb + lr
+#pragma unroll
+  for (int mb = 0; mb < kMidMB; ++mb) {
+    const int m = m0 + mb * 16 + lr;
+    if (m >= a.M) break;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int n = (t0 + rt) * 16 + 4 * lg;
+      if (a.out) {
+        uint32_t v[2] = {pack_bf16x2(acc[rt][mb][0], acc[rt][mb][1]),
+                         pack_bf16x2(acc[rt][mb][2], acc[rt][mb][3])};
+        __builtin_memcpy(a.out + (size_t)m * a.N + n, v, sizeof(v));
+      } else {
+        *(f32x4*)(a.part + ((size_t)split * a.M + m) * a.N + n) = acc[rt][mb];
+      }
+    }
+  }
+}
+
+template <int RT, int NW, int DEPTH>
+int launch_mid(const W4mPlan& p, const W4mArgs& a, hipStream_t st) {
+  w4b_mid_kernel<RT, NW, DEPTH><<<dim3((unsigned)p.groups, (unsigned)p.ksplit,
+                                       (unsigned)p.mblocks),
+                                  dim3(NW * kWave), p.lds, st>>>(a);
+  return ACORN_OK;
+}
+
 size_t w4b_lds(int R, int64_t kr, int nw, int kw, int rt, int mb) {
   return (size_t)kr * R * 2 + (size_t)(kr / 128) * 16 * mb * 4 +
          (kw > 1 ? (size_t)nw * rt * mb * 4 * kWave * 4 : 0);
@@ -468,6 +640,82 @@ int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale
     case 1: rc = launch_rt<1>(p, a, st); break;
     case 2: rc = launch_rt<2>(p, a, st); break;
     case 4: rc = launch_rt<4>(p, a, st); break;
+  }
+  if (rc) return rc;
+  ACORN_LAUNCH_CHECK();
+  return ACORN_OK;
+}
+
+// Knobs: rt (16-row tiles per wave) 1 or 2, nw (waves) 4 or 8, ksplit, depth
+// (groups in flight) 2 or 4, except rt 2 with 8 waves and depth 4 (its
+// registers spill); N must be a whole number of NW * RT * 16 row
+// blocks, K of 128-k groups, and each split's group count of depth rounds. With
+// ksplit 0 the split grows from 1 while the launch has fewer workgroups than
+// 256 (two rounds of CUs at most) and each split keeps 4 depth rounds.
+int w4m_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, W4mPlan* p) {
+  if (M < 1 || M > 65535 * (int64_t)kMidBM) return ACORN_ERR_SHAPE;
+  if (K % 512) return ACORN_ERR_SHAPE;
+  const int rt = cfg && cfg[1] > 0 ? cfg[1] : 2;
+  const int nw = cfg && cfg[2] > 0 ? cfg[2] : 8;
+  const int req_ks = cfg ? cfg[3] : 0;
+  const int depth = cfg && cfg[4] > 0 ? cfg[4] : 2;
+  if ((rt != 1 && rt != 2) || (nw != 4 && nw != 8) || (depth != 2 && depth != 4) ||
+      (rt == 2 && nw == 8 && depth == 4))
+    return ACORN_ERR_UNSUPPORTED;
+  const int64_t rows = (int64_t)nw * rt * 16;
+  if (N % rows) return ACORN_ERR_UNSUPPORTED;
+  const int64_t G = K / 128, groups = N / rows, mblocks = (M + kMidBM - 1) / kMidBM;
+  auto fits = [&](int64_t ks) { return ks >= 1 && G % ks == 0 && (G / ks) % depth == 0; };
+  int64_t ks;
+  if (req_ks > 0) {
+    ks = req_ks;
+    while (ks <= G && !fits(ks)) ++ks;
+    if (ks > G) return ACORN_ERR_UNSUPPORTED;
+  } else {
+    ks = 1;
+    if (!fits(1)) return ACORN_ERR_UNSUPPORTED;
+    while (groups * mblocks * ks < 256) {
+      int64_t nx = ks + 1;
+      while (nx <= G && !fits(nx)) ++nx;
+      if (nx > G || G / nx < 4 * depth) break;
+      ks = nx;
+    }
+  }
+  if (groups > 0x7fffffff || ks > 65535 || mblocks > 65535) return ACORN_ERR_SHAPE;
+  p->rt = rt;
+  p->nw = nw;
+  p->ksplit = (int)ks;
+  p->depth = depth;
+  p->groups = (int)groups;
+  p->mblocks = (int)mblocks;
+  p->lds = (size_t)2 * 16 * kMidBM * 16 + (size_t)2 * kMidBM * 4;
+  return ACORN_OK;
+}
+
+int w4m_launch(const W4mPlan& p, const void* x, const void* w, const void* scale, void* out,
+               float* part, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+  if (!x || !w || !scale) return ACORN_ERR_VALUE;
+  if (p.ksplit > 1) out = nullptr;
+  if (!out && !part) return ACORN_ERR_VALUE;
+  W4mArgs a;
+  a.x = (const __bf16*)x;
+  a.w = (const uint8_t*)w;
+  a.scale = (const _Float16*)scale;
+  a.out = (__bf16*)out;
+  a.part = part;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.kr = (int)(K / p.ksplit);
+  int rc = ACORN_ERR_UNSUPPORTED;
+  switch (p.rt * 100 + p.nw * 10 + p.depth) {
+    case 142: rc = launch_mid<1, 4, 2>(p, a, st); break;
+    case 144: rc = launch_mid<1, 4, 4>(p, a, st); break;
+    case 182: rc = launch_mid<1, 8, 2>(p, a, st); break;
+    case 184: rc = launch_mid<1, 8, 4>(p, a, st); break;
+    case 242: rc = launch_mid<2, 4, 2>(p, a, st); break;
+    case 244: rc = launch_mid<2, 4, 4>(p, a, st); break;
+    case 282: rc = launch_mid<2, 8, 2>(p, a, st); break;
   }
   if (rc) return rc;
   ACORN_LAUNCH_CHECK();

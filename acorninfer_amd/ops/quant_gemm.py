@@ -41,6 +41,7 @@ _CLS_BY_SHAPE = {v: k for k, v in CLASSES.items()}
 
 DECODE_M_MAX = 16
 W4B_M_MAX = 64      # the int4 decode kernel takes up to this many rows on request
+MID_RT = -3         # Tiling.rt of the int4 mid-M kernel (W4B, M > 16)
 M_BUCKETS_LARGE = ("s", "m", "l")
 _M_REP_M = {"s": 64, "m": 256, "l": 1024}
 
@@ -79,6 +80,9 @@ class Tiling(NamedTuple):
     rt row tiles per wave, upw 128-k groups per pipeline stage, nw waves per
     workgroup (2 or 4 each on its own rows; 10*nw + kw: kw waves share rows
     and split K), ksplit, and tpw = stages in flight per wave.
+    int4 mid-M kernel (WFMT_W4B, M > 16, rt == -3): upw row tiles per wave
+    (1 / 2), nw waves (4 / 8), ksplit, tpw 128-k groups in flight (2 / 4);
+    64 x rows per workgroup, streamed through LDS a group at a time.
     Large-M bf16 kernel (the default for bf16 from 512 rows, or rt == -2):
     upw is the M tile (64 / 128), nw the weight rows per wave (64 / 128; a
     workgroup's weight tile is 4 nw), tpw the weight prefetch depth in 64-k
@@ -319,6 +323,10 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
         reqs = [r for r in reqs if r.rt > 0]      # rt 0 means the tiled kernel here
         if wfmt == WFMT_W4B and M <= W4B_M_MAX:
             reqs = _w4b_wide_requests()           # the int4 kernel with 2 or 4 x blocks
+        if wfmt == WFMT_W4B:
+            reqs += [Tiling(MID_RT, rt, nw, ks, depth)   # the mid-M int4 kernel
+                     for rt in (1, 2) for nw in (4, 8) for depth in (2, 4)
+                     for ks in (0, 1, 2, 4, 8, 16)]
         for bm in (32, 64, 128):
             for bn in (64, 128):
                 for ks in (0, 1, 2, 4, 8):

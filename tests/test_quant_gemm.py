@@ -312,6 +312,36 @@ def test_w4b_wide_decode_kernel_matches(m):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m", [17, 64, 100, 256])
+def test_w4b_mid_kernel_matches(m):
+    """The int4 mid-M kernel (x through LDS a group at a time, 64 x rows per
+    workgroup; M = 17 and 100 leave a partial last block, 256 spreads four M
+    blocks over an XCD) at every tiling the sweep offers it, on the qkv shape
+    (N = 6144, 24 row blocks of 256) and the down shape (K = 12288), against
+    the dequantised matmul; one split and four give the same result up to fp32
+    summation order (bf16 outputs within one ulp)."""
+    from acorninfer_amd._lib import WFMT_W4B
+    from acorninfer_amd.ops.quant_gemm import MID_RT, Tiling, _launch, candidates
+    from acorninfer_amd.quant.quantize import to_w4b
+    for cls in ("qkv", "down"):
+        p, s, wref = _w4(cls)
+        wb, sb = to_w4b(p, s)
+        n, k = SHAPES[cls]
+        x = _x(m, k, 13)
+        ref = _ref(x, wref)
+        cands = [c for c in candidates(m, n, k, WFMT_W4B) if c.rt == MID_RT]
+        assert len(cands) >= 8, len(cands)
+        for c in cands:
+            out = _launch(x, wb, sb, None, WFMT_W4B, n, c, None)
+            r = rel_err(out, ref)
+            assert r <= GEMM_REL, f"{cls} M={m} {tuple(c)}: rel err {r:.3g}"
+        one = _launch(x, wb, sb, None, WFMT_W4B, n, Tiling(MID_RT, 2, 4, 1, 2), None)
+        four = _launch(x, wb, sb, None, WFMT_W4B, n, Tiling(MID_RT, 2, 4, 4, 2), None)
+        assert rel_err(one, four) <= 1e-3      # bf16 outputs: a few one-ulp flips
+        print(f"\n[w4b mid M={m} {cls}: {len(cands)} tilings ok]")
+
+
+@pytest.mark.gpu
 def test_w4b_split_partials_deterministic_and_graph_replay():
     """W4B partials at several split counts sum (in split order) to the same
     result within fp32 rounding, repeat bitwise, and replay bitwise in a
