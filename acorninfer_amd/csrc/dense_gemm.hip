@@ -22,11 +22,12 @@
 //    (the dispatcher deals ids round-robin over the 8 XCDs), and the tiles of
 //    an XCD cover 4 weight tiles x 8 x tiles, which share its L2.
 // Per 32 k a wave reads BM/16 B operands (1 KB each) from LDS for
-// WN/16 x BM/16 MFMAs: 16 WN/16 FLOPs per LDS byte (64 at WN = 64). The
-// direct weight loads touch 16 rows x 64 B per instruction (half lines), which
-// with one wave per SIMD is what holds the kernel near 0.8 PFLOP/s at
-// M >= 2048 (hipBLASLt, with both operands staged through LDS by DMA, reaches
-// 1.1-1.4 on the same shapes).
+// WN/16 x BM/16 MFMAs. With one wave per SIMD this form stays near 0.8-0.9
+// PFLOP/s at M >= 2048 (reading the weights in whole lines through an LDS slab
+// instead was slower: the loads are not its bound). From 1024 rows the
+// planner takes the second form below, 256 x 256 tiles with both operands in
+// LDS and two waves per SIMD: 1.0-1.06 PFLOP/s at M = 2048-8192 (hipBLASLt:
+// 1.2-1.4).
 #include <hip/hip_runtime.h>
 
 #include "acorn_hip.h"
@@ -162,6 +163,138 @@ __global__ __launch_bounds__(256, 1) void dense_gemm_kernel(const __bf16* __rest
   }
 }
 
+// Both operands through LDS (bm == kLdsTile): a workgroup of 8 waves (two per
+// SIMD, so one wave's LDS and memory waits overlap the other's MFMAs) owns a
+// 256 (n) x 256 (m) output tile; wave (wn, wm) of its 2 x 4 grid owns 128 x 64
+// of it (8 x 4 accumulator blocks). Per K step of 64 the workgroup stages the
+// step's 256 weight rows and 256 x rows from registers into padded LDS rows
+// (whole 128-byte lines: 8 consecutive threads per row; two buffers, one
+// barrier per step), with the next step's global loads in flight in
+// registers; each wave then reads 8 A and 4 B operands per 32 k for 32 MFMAs
+// (5.3 FLOPs per LDS byte against 2 for the 64 x 128 wave tile above).
+constexpr int kLdsTile = 256;
+
+template <typename OUT, int DEPTH>
+__global__ __launch_bounds__(512, 1) void dense_lds_kernel(const __bf16* __restrict__ x,
+                                                           const __bf16* __restrict__ w,
+                                                           OUT* __restrict__ out, int M, int N,
+                                                           int K, int tiles_n, int tiles_m,
+                                                           int steps) {
+  constexpr int T = kLdsTile, NT = 512;
+  constexpr int PPT = T * 8 / NT;                   // 16-byte pieces per thread per operand
+  constexpr int NB = 8, MB = 4;                     // accumulator blocks per wave
+  __shared__ __align__(16) uint8_t sw[2][T * kXPitch];
+  __shared__ __align__(16) uint8_t sx[2][T * kXPitch];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wid = tid >> 6;
+  const int r = lane >> 4, c = lane & 15;
+  const int G = tiles_n * tiles_m;
+  int t = blockIdx.x;
+  if (G % 8 == 0) t = (t % 8) * (G / 8) + t / 8;
+  constexpr int GN = 4;
+  const int group = t / (GN * tiles_m);
+  const int first_n = group * GN;
+  const int gsize = min(tiles_n - first_n, GN);
+  const int in_group = t - group * GN * tiles_m;
+  const int tn = first_n + in_group % gsize;
+  const int tm = in_group / gsize;
+  const int n0 = tn * T, m0 = tm * T;
+  const int wn = (wid & 1) * 128, wm = (wid >> 1) * 64;
+  const int kbase = blockIdx.y * steps * kDenseBK;
+  out += (size_t)blockIdx.y * M * N;
+
+  // piece q = tid + 512 u of an operand: row q / 8, 16-byte piece q % 8;
+  // row offsets are recomputed per load (registers go to the accumulators)
+  const __bf16* wb = w + kbase + (tid % 8) * 8;
+  const __bf16* xb = x + kbase + (tid % 8) * 8;
+  const int wr0 = n0 + tid / 8, xr0 = m0 + tid / 8;
+  const uint32_t soff = (uint32_t)((tid / 8) * kXPitch + (tid % 8) * 16);
+  struct Stage {
+    u32x4 w[PPT], x[PPT];
+  };
+  auto gload = [&](int s, Stage& st) {
+    const int k0 = min(s, steps - 1) * kDenseBK;
+#pragma unroll
+    for (int u = 0; u < PPT; ++u)
+      st.w[u] = load_nt((const u32x4*)(wb + (size_t)min(wr0 + 64 * u, N - 1) * K + k0));
+#pragma unroll
+    for (int u = 0; u < PPT; ++u)
+      st.x[u] = *(const u32x4*)(xb + (size_t)min(xr0 + 64 * u, M - 1) * K + k0);
+  };
+  auto lstore = [&](int b, const Stage& st) {
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) *(u32x4*)(sw[b] + soff + u * 64 * kXPitch) = st.w[u];
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) *(u32x4*)(sx[b] + soff + u * 64 * kXPitch) = st.x[u];
+  };
+  f32x4 acc[NB][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int b) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      u32x4 a[NB], bx[MB];
+#pragma unroll
+      for (int j = 0; j < MB; ++j)
+        bx[j] = *(const u32x4*)(sx[b] + (wm + 16 * j + c) * kXPitch + 64 * kk + 16 * r);
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+        a[i] = *(const u32x4*)(sw[b] + (wn + 16 * i + c) * kXPitch + 64 * kk + 16 * r);
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j) acc[i][j] = mfma(a[i], bx[j], acc[i][j]);
+    }
+  };
+
+  Stage st;
+  gload(0, st);
+  lstore(0, st);
+  gload(1, st);
+  __syncthreads();
+  for (int s = 0; s < steps; ++s) {
+    compute(s & 1);
+    lstore((s + 1) & 1, st);                         // harmless past the end
+    gload(s + 2, st);
+    __syncthreads();
+  }
+  // lane (r, c) of block (i, j) holds out[m0 + wm + 16 j + c][n0 + wn + 16 i + 4 r + e]
+#pragma unroll
+  for (int j = 0; j < MB; ++j) {
+    const int m = m0 + wm + 16 * j + c;
+    if (m >= M) continue;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int n = n0 + wn + 16 * i + 4 * r;
+      if (n >= N) continue;
+      OUT* o = out + (size_t)m * N + n;
+      if constexpr (sizeof(OUT) == 4) {
+        *(f32x4*)o = acc[i][j];
+      } else {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        u32x2 v;
+        v[0] = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
+        v[1] = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
+        *(u32x2*)o = v;
+      }
+    }
+  }
+}
+
+template <typename OUT, int DEPTH>
+int launch_lds(const void* x, const void* w, void* out, int64_t M, int64_t N, int64_t K, int ks,
+               hipStream_t st) {
+  const int64_t tiles_n = (N + kLdsTile - 1) / kLdsTile, tiles_m = (M + kLdsTile - 1) / kLdsTile;
+  if (tiles_n * tiles_m > 0x7fffffff) return ACORN_ERR_SHAPE;
+  dense_lds_kernel<OUT, DEPTH>
+      <<<dim3((unsigned)(tiles_n * tiles_m), (unsigned)ks), dim3(512), 0, st>>>(
+          (const __bf16*)x, (const __bf16*)w, (OUT*)out, (int)M, (int)N, (int)K, (int)tiles_n,
+          (int)tiles_m, (int)(K / kDenseBK / ks));
+  return ACORN_OK;
+}
+
 template <typename OUT, int WN, int BM, int DEPTH>
 int launch(const void* x, const void* w, void* out, int64_t M, int64_t N, int64_t K, int ks,
            hipStream_t st) {
@@ -177,7 +310,9 @@ int launch(const void* x, const void* w, void* out, int64_t M, int64_t N, int64_
 template <typename OUT>
 int dispatch(int wn, int bm, int depth, const void* x, const void* w, void* out, int64_t M,
              int64_t N, int64_t K, int ks, hipStream_t st) {
-  if (wn == 64) {
+  if (bm == kLdsTile) {
+    if (depth == 2) return launch_lds<OUT, 2>(x, w, out, M, N, K, ks, st);
+  } else if (wn == 64) {
     if (bm == 128 && depth == 2) return launch<OUT, 64, 128, 2>(x, w, out, M, N, K, ks, st);
     if (bm == 128 && depth == 4) return launch<OUT, 64, 128, 4>(x, w, out, M, N, K, ks, st);
     if (bm == 64 && depth == 2) return launch<OUT, 64, 64, 2>(x, w, out, M, N, K, ks, st);
@@ -191,7 +326,8 @@ int dispatch(int wn, int bm, int depth, const void* x, const void* w, void* out,
 }  // namespace
 
 bool dense_gemm_supported(int64_t N, int64_t K, int wn, int bm, int depth, int ks) {
-  const bool built = wn == 64 ? (bm == 64 || bm == 128) && (depth == 2 || depth == 4)
+  const bool built = bm == kLdsTile ? wn == 64 && depth == 2
+                   : wn == 64 ? (bm == 64 || bm == 128) && (depth == 2 || depth == 4)
                    : wn == 128 ? bm == 64 && depth == 2
                                : false;
   return built && ks >= 1 && ks <= 64 && N % 4 == 0 && K % kDenseBK == 0 &&

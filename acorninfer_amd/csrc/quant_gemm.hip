@@ -821,6 +821,7 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
 // this many rows on, or on request (rt == kDenseRT).
 constexpr int kDenseRT = -2;
 constexpr int64_t kDenseMinM = 512;
+constexpr int64_t kDenseLdsM = 1024;
 // W4B above 16 rows on request (rt == kMidRT): the mid-M int4 kernel
 constexpr int kMidRT = -3;
 
@@ -834,9 +835,10 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   if (wfmt == ACORN_WFMT_BF16 && !swiglu &&
       ((cfg && cfg[0] == kDenseRT) || (no_request && M >= kDenseMinM))) {
     const bool req = cfg && cfg[0] == kDenseRT;
-    const int bm = req && cfg[1] > 0 ? cfg[1] : 128;
+    // from kDenseLdsM rows the 256 x 256 tiles with both operands in LDS
+    const int bm = req && cfg[1] > 0 ? cfg[1] : M >= kDenseLdsM ? 256 : 128;
     const int wn = req && cfg[2] > 0 ? cfg[2] : 64;
-    const int depth = req && cfg[4] > 0 ? cfg[4] : 4;
+    const int depth = req && cfg[4] > 0 ? cfg[4] : bm == 256 ? 2 : 4;
     int ks = req && cfg[3] > 0 ? cfg[3] : 1;
     if (!(req && cfg[3] > 0)) {
       // split K while the launch has fewer workgroups than CUs
