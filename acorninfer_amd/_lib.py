@@ -58,6 +58,7 @@ _SIGNATURES = {
     "acorn_paged_attention_qkv_supported": [_i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32],
     "acorn_quant_gemm": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp],
     "acorn_splitk_reduce": [_vp, _i64, _i64, _vp, _i32, _vp],
+    "acorn_dequant_w4b": [_vp, _vp, _vp, _i64, _i64, _vp],
     "acorn_gemm_plan": [_i64, _i64, _i64, _i32, _vp],
     "acorn_quant_gemm_swiglu": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp],
     "acorn_gemm_swiglu_plan": [_i64, _i64, _i64, _i32, _vp],

@@ -134,6 +134,9 @@ struct W4mPlan {
 int w4m_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, W4mPlan* p);
 int w4m_launch(const W4mPlan& p, const void* x, const void* w, const void* scale, void* out,
                float* part, int64_t M, int64_t N, int64_t K, hipStream_t st);
+// W4B weights -> bf16 [N, K] in row order (N % 16 == 0, K % 512 == 0).
+int w4b_dequant(const void* w, const void* scale, void* out, int64_t N, int64_t K,
+                hipStream_t st);
 
 // ---- the large-M bf16 GEMM (dense_gemm.hip) ---------------------------------
 // out[M,N] = x[M,K] . w[N,K]^T, bf16 operands: (4 wn) x bm output tiles (wn

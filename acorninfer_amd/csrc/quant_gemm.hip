@@ -1239,6 +1239,11 @@ extern "C" int acorn_quant_gemm_swiglu(const void* x, const void* w, const void*
                     (hipStream_t)stream);
 }
 
+extern "C" int acorn_dequant_w4b(const void* w, const void* scale, void* out_bf16, int64_t N,
+                                 int64_t K, void* stream) {
+  return w4b_dequant(w, scale, out_bf16, N, K, (hipStream_t)stream);
+}
+
 extern "C" int acorn_splitk_reduce(const float* part, int64_t nsplit, int64_t count, void* out,
                                    int dtype, void* stream) {
   if (nsplit < 1 || count < 0) return ACORN_ERR_SHAPE;

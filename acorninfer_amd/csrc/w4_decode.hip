@@ -723,3 +723,57 @@ int w4m_launch(const W4mPlan& p, const void* x, const void* w, const void* scale
 }
 
 }  // namespace acorn
+
+// ---- W4B -> bf16 [N, K] (prefill-sized projections) ------------------------
+// out[n, k] = bf16_rne((u - 8) * s(n, k / 128)). (u - 8) * s is exact in fp32
+// (a 4-bit integer times an 11-bit significand), so the result is the
+// weight rounded once to bf16. One thread per 16-byte piece (one row, 32 k):
+// a wave reads one 1 KB block with one load instruction and writes the
+// block's 16 rows x 128 k as 4 KB of whole 64-byte row segments.
+namespace {
+
+__global__ __launch_bounds__(256) void w4b_dequant_kernel(const u32x4* __restrict__ w,
+                                                          const _Float16* __restrict__ scale,
+                                                          __bf16* __restrict__ out, int64_t K,
+                                                          size_t pieces) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= pieces) return;
+  const int64_t G = K / 128;
+  const size_t blk = i / 64;
+  const int lane = (int)(i % 64);
+  const int64_t n = (int64_t)(blk / G) * 16 + lane % 16;
+  const int64_t g = (int64_t)(blk % G);
+  const int64_t k0 = g * 128 + (lane / 16) * 32;
+  const float s = (float)scale[w4b_half_index(n, g, K)];
+  const u32x4 v = load_nt(w + i);
+  u32x4* dst = (u32x4*)(out + n * K + k0);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t byte = (v[q] >> (8 * j)) & 0xffu;
+      o[j] = pack_bf16x2((float)((int)(byte & 15u) - 8) * s, (float)((int)(byte >> 4) - 8) * s);
+    }
+    dst[q] = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+}  // namespace
+
+namespace acorn {
+
+int w4b_dequant(const void* w, const void* scale, void* out, int64_t N, int64_t K,
+                hipStream_t st) {
+  if (N <= 0 || K <= 0 || N % 16 || K % 512) return ACORN_ERR_SHAPE;
+  if (!w || !scale || !out) return ACORN_ERR_VALUE;
+  const size_t pieces = (size_t)N * (size_t)(K / 32);
+  const size_t blocks = (pieces + 255) / 256;
+  if (blocks > 0x7fffffffu) return ACORN_ERR_SHAPE;
+  w4b_dequant_kernel<<<(unsigned)blocks, 256, 0, st>>>((const u32x4*)w, (const _Float16*)scale,
+                                                       (__bf16*)out, K, pieces);
+  ACORN_LAUNCH_CHECK();
+  return ACORN_OK;
+}
+
+}  // namespace acorn

@@ -52,6 +52,13 @@ FORMATS = {"bf16": WFMT_BF16, "w8a16": WFMT_W8, "w4a16": WFMT_W4}
 DENSE_M_MIN = 512
 DENSE_RT = -2
 LIBRARY_RT = -1
+# int4 (W4B) projections from DEQUANT_M_MIN rows: the weights are dequantised
+# to bf16 into a step workspace (acorn_dequant_w4b) and multiplied by the
+# large-M bf16 kernel (tiling rt == DEQUANT_RT, the other fields the bf16
+# kernel's). At prefill sizes the MFMA work dominates and that kernel's rate
+# outweighs the extra pass over the weights.
+DEQUANT_M_MIN = 2048
+DEQUANT_RT = -4
 
 
 def dispatch_linear(mod, x: torch.Tensor) -> torch.Tensor:
@@ -168,19 +175,30 @@ class QLinear:
                 n += t.numel() * t.element_size()
         return n
 
-    def plan(self, M: int, tiling=None):
+    def plan(self, M: int, tiling=None, workspace: bool = False):
         """(Tiling, output tiles) from the library planner (a LIBRARY_RT
-        request is passed through: torch.mm)."""
+        request is passed through: torch.mm). workspace: the caller holds a
+        bf16 weight workspace, so int4 weights take the dequantise + bf16
+        GEMM route by default from DEQUANT_M_MIN rows (a DEQUANT_RT request
+        takes it at any size)."""
         from acorninfer_amd.ops.quant_gemm import Tiling, plan
         if tiling is not None and tiling[0] == LIBRARY_RT:
             return Tiling(LIBRARY_RT, 0, 0, 1, 0), None
+        if self.fmt == WFMT_W4B and (
+                (tiling is not None and tiling[0] == DEQUANT_RT) or
+                (workspace and (tiling is None or not any(tiling)) and M >= DEQUANT_M_MIN)):
+            rest = tuple(tiling[1:]) if tiling is not None else (0, 0, 0, 0)
+            t, tiles = plan(M, self.N, self.K, WFMT_BF16, Tiling(DENSE_RT, *rest))
+            return Tiling(DEQUANT_RT, *t[1:]), tiles
         return plan(M, self.N, self.K, self.fmt, tiling)
 
     def launch(self, x: torch.Tensor, M: int, tiling, *, out: torch.Tensor | None = None,
-               part: torch.Tensor | None = None, stream: int) -> None:
+               part: torch.Tensor | None = None, wtmp: torch.Tensor | None = None,
+               stream: int) -> None:
         """out given: bf16 [M, N] (part is the split-K workspace when
         tiling.ksplit > 1); out None: fp32 partials [ksplit, M, N] into part.
-        fp32 weights always write fp32 through part."""
+        fp32 weights always write fp32 through part. A DEQUANT_RT tiling
+        dequantises into wtmp (bf16, at least N * K elements) first."""
         if self.fmt == _lib.WFMT_F32:
             part, out = (out if part is None else part), None
         if tiling[0] == LIBRARY_RT:
@@ -190,6 +208,20 @@ class QLinear:
                 torch.mm(xs, self.w.t(), out=out[:M])
             else:
                 torch.ops.aten.mm.dtype_out(xs, self.w.t(), torch.float32, out=part[0])
+            return
+        if tiling[0] == DEQUANT_RT:
+            if self.fmt != WFMT_W4B:
+                raise ValueError("a DEQUANT_RT tiling needs W4B weights")
+            if (wtmp is None or wtmp.dtype != torch.bfloat16 or
+                    wtmp.numel() < self.N * self.K):
+                raise ValueError(f"int4 GEMM at {M} rows (DEQUANT_RT) needs a bf16 weight "
+                                 f"workspace of {self.N * self.K} elements")
+            check(lib().acorn_dequant_w4b(ptr(self.w), ptr(self.scale), ptr(wtmp), self.N,
+                                          self.K, stream), "dequant_w4b")
+            arr = (ctypes.c_int * 6)(DENSE_RT, *tiling[1:], 0)
+            rc = lib().acorn_quant_gemm(ptr(x), ptr(wtmp), None, None, ptr(out), ptr(part), M,
+                                        self.N, self.K, WFMT_BF16, arr, stream)
+            check(rc, "quant_gemm(dequantised int4)")
             return
         arr = (ctypes.c_int * 6)(*tiling, 0)
         rc = lib().acorn_quant_gemm(ptr(x), ptr(self.w), ptr(self.scale), ptr(self.zero),
@@ -292,8 +324,10 @@ class Qwen3DecodeModel:
         # prefill attention as the query-tiled kernel where it is built for
         # the shapes (False: K3 with one row per prompt token)
         self.tiled_prefill = True
-        # bf16 projections of prefill rows: "own" (the library's large-M
-        # kernel) or "library" (torch.mm, i.e. hipBLASLt)
+        # projections of prefill rows: "own" (bf16 on the library's large-M
+        # kernel; int4 dequantised onto it from DEQUANT_M_MIN rows), "library"
+        # (bf16 on torch.mm, i.e. hipBLASLt) or "int4" (int4 weights on the
+        # int4 kernels at every size)
         self.prefill_gemm = "own"
         # batch -> {projection name -> Tiling}, filled by tune()
         self.tilings: dict[int, dict] = {}
@@ -431,7 +465,7 @@ class Qwen3DecodeModel:
                     ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
             # qkv projection -> fp32 partials -> K2 epilogue (+ KV scatter)
             cq = buf.cfgs["qkv"]
-            lw.qkv.launch(buf.normed, B, cq, part=buf.part_qkv, stream=st)
+            lw.qkv.launch(buf.normed, B, cq, part=buf.part_qkv, wtmp=buf.wtmp, stream=st)
             kp = kbase + li * layer_elems * esz
             vp = vbase + li * layer_elems * esz
             if fused_attn:
@@ -462,7 +496,7 @@ class Qwen3DecodeModel:
                         buf.max_pages, buf.num_splits, float(self.scale), dt, st), "K3")
             # o projection -> K1 (reduce + residual add + post-attention norm)
             co = buf.cfgs["o"]
-            lw.o.launch(buf.attn, B, co, part=buf.part_o, stream=st)
+            lw.o.launch(buf.attn, B, co, part=buf.part_o, wtmp=buf.wtmp, stream=st)
             check(L.acorn_fused_add_rmsnorm_partials(
                 ptr(buf.part_o), co.ksplit, ptr(buf.res), ptr(buf.res), ptr(lw.post_norm),
                 ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
@@ -471,11 +505,12 @@ class Qwen3DecodeModel:
             if buf.swiglu:
                 lw.gate_up.launch_swiglu(buf.normed, B, cg, buf.act, st)
             else:
-                lw.gate_up.launch(buf.normed, B, cg, part=buf.part_gu, stream=st)
+                lw.gate_up.launch(buf.normed, B, cg, part=buf.part_gu, wtmp=buf.wtmp,
+                                   stream=st)
                 check(L.acorn_silu_mul(ptr(buf.part_gu), cg.ksplit, None, ptr(buf.act), B, inter,
                                        int(lw.gate_up.il16), dt, st), "silu_mul")
             cd = buf.cfgs["down"]
-            lw.down.launch(buf.act, B, cd, part=buf.part_down, stream=st)
+            lw.down.launch(buf.act, B, cd, part=buf.part_down, wtmp=buf.wtmp, stream=st)
             prev_ks = cd.ksplit
         # final norm (reduce + residual add) -> lm_head -> greedy
         check(L.acorn_fused_add_rmsnorm_partials(
@@ -532,6 +567,8 @@ class Qwen3DecodeModel:
         t = planner(M, _native_cfg(tiling, M))[0]
         x = torch.randn(M, lin0.K, device=self.device).to(self.dtype)
         part = torch.empty(t.ksplit, M, lin0.N, dtype=torch.float32, device=self.device)
+        wtmp = (torch.empty(lin0.N * lin0.K, dtype=torch.bfloat16, device=self.device)
+                if t.rt == DEQUANT_RT else None)
         act = torch.empty(M, lin0.N // 2, dtype=self.dtype, device=self.device)
         red = torch.empty(M, lin0.N, dtype=self.dtype, device=self.device) if with_reduce else None
         if with_norm:
@@ -546,7 +583,7 @@ class Qwen3DecodeModel:
                     if swiglu:
                         lin.launch_swiglu(x, M, t, act, s.cuda_stream)
                     else:
-                        lin.launch(x, M, t, part=part, stream=s.cuda_stream)
+                        lin.launch(x, M, t, part=part, wtmp=wtmp, stream=s.cuda_stream)
                         if with_act:   # the separate activation the fused form saves
                             check(lib().acorn_silu_mul(ptr(part), t.ksplit, None, ptr(act), M,
                                                        lin.N // 2, int(lin.il16),
@@ -755,10 +792,16 @@ class Qwen3DecodeModel:
             if cached is None or cached[0] != key:
                 self._extend_buf = None
                 lib_t = None
-                if self.prefill_gemm == "library" and self.layers[0].qkv.fmt == WFMT_BF16:
+                lw = self.layers[0]
+                if self.prefill_gemm == "library" and lw.qkv.fmt == WFMT_BF16:
                     from acorninfer_amd.ops.quant_gemm import Tiling
                     lt = Tiling(LIBRARY_RT, 0, 0, 1, 0)
                     lib_t = {"qkv": lt, "o": lt, "gate_up": lt, "down": lt}
+                elif self.prefill_gemm == "int4" and lw.qkv.fmt == WFMT_W4B:
+                    # the int4 planner's full choices (explicit: no dequantisation)
+                    lib_t = {n: lin.plan(Rb)[0] for n, lin in (
+                        ("qkv", lw.qkv), ("o", lw.o), ("gate_up", lw.gate_up),
+                        ("down", lw.down))}
                 self._extend_buf = (key, self.buffers(Rb, key[1], tilings=lib_t, prefill=True))
             buf = self._extend_buf[1]
             buf.ids.copy_(ids_all[r0:r1])
@@ -898,7 +941,12 @@ class StepBuffers:
             if name == "gate_up" and self.swiglu:
                 self.cfgs[name] = lin.swiglu_plan(B, tilings.get(name))[0]
             else:
-                self.cfgs[name] = lin.plan(B, tilings.get(name))[0]
+                self.cfgs[name] = lin.plan(B, tilings.get(name), workspace=name != "lm_head")[0]
+        # bf16 copy of one int4 projection at a time (DEQUANT_RT tilings)
+        nk = [lin.N * lin.K for name, lin in (("qkv", lw.qkv), ("o", lw.o),
+                                             ("gate_up", lw.gate_up), ("down", lw.down))
+              if self.cfgs[name][0] == DEQUANT_RT]
+        self.wtmp = (torch.empty(max(nk), dtype=torch.bfloat16, device=dev) if nk else None)
         # The host-written inputs are one byte block, so a step needs one copy:
         # int64 ids | positions | pages | slots, then int32 lens | tables, then
         # the sampling block f32 temperature | top_p | uniform | top_k (int32

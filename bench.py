@@ -976,6 +976,23 @@ def main() -> None:
             extra[f"w4a16_C{c}_long_sampled_mean_ctx"] = round(sum(plens) / c, 1)
             _log(f"w4a16 C={c} long sampled (mean ctx {sum(plens) / c:.0f}): "
                  f"{c * args.steps / dt2:.1f} tok/s")
+            if c == 8:
+                # configuration 5's longest prompt in W4A16: one 8192-token
+                # prefill, int4 projections dequantised onto the bf16 kernel
+                # ("own") and on the int4 kernels themselves
+                del c2, r2
+                torch.cuda.empty_cache()
+                for how in ("own", "int4"):
+                    m2.prefill_gemm = how
+                    ms_p, tps = prefill_benchmark(m2, cfg, 1, 8192, args.seed + 8, reps=2)
+                    sfx = "" if how == "own" else "_int4_gemm"
+                    extra[f"w4a16_prefill_1x8192{sfx}_ms"] = round(ms_p, 3)
+                    extra[f"w4a16_prefill_1x8192{sfx}_tok_s"] = round(tps, 1)
+                    _log(f"w4a16 prefill 1 x 8192 ({how}): {ms_p:.2f} ms ({tps:.0f} tok/s)")
+                m2._extend_buf = None
+                del m2
+                torch.cuda.empty_cache()
+                continue
             del m2, c2, r2
             torch.cuda.empty_cache()
     if not args.no_kernels:

@@ -264,6 +264,19 @@ int acorn_quant_gemm_swiglu(const void* x, const void* w, const void* scale, con
 /* Tiling of acorn_quant_gemm_swiglu, as acorn_gemm_plan. */
 int acorn_gemm_swiglu_plan(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg);
 
+/*
+ * ACORN_WFMT_W4B weights (symmetric int4, scale fp16 per 128-k group) -> bf16
+ * [N, K] in the weight's row order: out[n, k] = bf16_rne((u - 8) * s), the
+ * dequantisation the reference's large-M quantised GEMM applies in-kernel
+ * before its bf16 dot (acorninfer/ops/quant_gemm.py:175-183: int -> fp32 x
+ * scale -> bf16). With acorn_quant_gemm on ACORN_WFMT_BF16 it forms the
+ * int4 GEMM at prefill sizes (thousands of rows), where the bf16 MFMA kernel
+ * outruns any in-kernel unpacking. N % 16 == 0, K % 512 == 0; out holds
+ * N * K bf16 (the caller's workspace).
+ */
+int acorn_dequant_w4b(const void* w, const void* scale, void* out_bf16, int64_t N, int64_t K,
+                      void* stream);
+
 /* Deterministic split-K reduction: out[M*N] = round_T(sum_s part[s, M*N]). */
 int acorn_splitk_reduce(const float* part, int64_t nsplit, int64_t count, void* out,
                         int dtype, void* stream);

@@ -157,6 +157,49 @@ def test_prefill_at_dense_gemm_sizes_bf16_matches_oracle():
 
 
 @pytest.mark.gpu
+def test_prefill_w4a16_dequant_route_matches_oracle():
+    """int4 weights at >= 2048 rows: every projection dequantises into the step
+    workspace and runs on the large-M bf16 kernel; the last-row logits stay
+    within the decode tests' tolerance of the oracle on the dequantised
+    weights, as with the int4 kernels below that size."""
+    from acorninfer_amd.models.qwen3 import DEQUANT_M_MIN, DEQUANT_RT
+    cfg = Qwen3Config.qwen3_0_6b().with_layers(2)
+    sd = random_state_dict(cfg, seed=SEED + 7, std=0.02, dtype=torch.bfloat16)
+    model = Qwen3DecodeModel.from_state_dict(cfg, sd, weight_format="w4a16", device="cuda")
+    prompts = [_ids(n, cfg.vocab_size, SEED + 40 + n) for n in (1500, 700)]
+    assert sum(len(p) for p in prompts) >= DEQUANT_M_MIN
+    dq = dict(sd)
+    nq, nkv = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim
+    for i, L in enumerate(model.layers):
+        p = f"layers.{i}."
+        qkv, gu = L.qkv.dense().cpu(), L.gate_up.dense().cpu()
+        dq[p + "self_attn.q_proj.weight"] = qkv[:nq]
+        dq[p + "self_attn.k_proj.weight"] = qkv[nq:nq + nkv]
+        dq[p + "self_attn.v_proj.weight"] = qkv[nq + nkv:]
+        dq[p + "self_attn.o_proj.weight"] = L.o.dense().cpu()
+        dq[p + "mlp.gate_proj.weight"] = gu[:cfg.intermediate_size]
+        dq[p + "mlp.up_proj.weight"] = gu[cfg.intermediate_size:]
+        dq[p + "mlp.down_proj.weight"] = L.down.dense().cpu()
+    dq["lm_head.weight"] = model.lm_head.dense().cpu()
+    ref = Qwen3Ref(cfg, dq, torch.float32)
+    alloc, cache = new_cache(model, 160)
+    views = [PagedCacheView(cache) for _ in prompts]
+    got = model.forward_prefill_batch(_padded(prompts, model.device), views,
+                                      real_lens=[len(p) for p in prompts]).cpu()
+    buf = model._extend_buf[1]
+    assert all(buf.cfgs[n].rt == DEQUANT_RT for n in ("qkv", "o", "gate_up", "down"))
+    assert buf.wtmp.numel() == 2 * cfg.intermediate_size * cfg.hidden_size
+    for i, p in enumerate(prompts):
+        want = ref.forward(torch.tensor([p]), num_logits_to_keep=1)[0, -1]
+        rel = _rel(got[i], want)
+        print(f"\n[w4a16 prefill {len(p)} tokens in a {sum(map(len, prompts))}-row launch: "
+              f"rel err {rel:.3g}]", flush=True)
+        assert rel < 3e-2
+    release(alloc, views)
+    alloc.assert_balanced()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("lens", [(5, 33, 17, 200), (8300,)])
 def test_tiled_prefill_attention_equals_k3_rows_bf16(lens):
     """The model's prefill with the query-tiled attention kernel against the

@@ -342,6 +342,69 @@ def test_w4b_mid_kernel_matches(m):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("cls", ["qkv", "down"])
+def test_dequant_w4b_bitwise(cls):
+    """acorn_dequant_w4b writes the oracle's fp32 dequantised weight ((u - 8)
+    * s) rounded once to bf16, bit for bit, in row order, also for rows in
+    the gate|up 16-row interleave (the blocks move with their rows)."""
+    from acorninfer_amd._lib import check, lib, ptr, stream_ptr
+    from acorninfer_amd.ops.quant_gemm import interleave16
+    from acorninfer_amd.quant.quantize import to_w4b
+    p, s, wref = _w4(cls)
+    n, k = SHAPES[cls]
+    want = wref.to(torch.bfloat16)
+    for perm in (False, True):
+        pp, ss, ww = (interleave16(p), interleave16(s), interleave16(want)) if perm else (p, s, want)
+        wb, sb = to_w4b(pp, ss)
+        out = torch.full((n, k), float("nan"), dtype=torch.bfloat16, device="cuda")
+        check(lib().acorn_dequant_w4b(ptr(wb), ptr(sb), ptr(out), n, k, stream_ptr(out.device)),
+              "dequant_w4b")
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ww.view(torch.int16)), f"{cls} il16={perm}"
+    # shape contract: rows in 16s, K in 512s (checked on the host, nothing launched)
+    for bad in ((n - 8, k), (n, k - 128)):
+        assert lib().acorn_dequant_w4b(ptr(wb), ptr(sb), ptr(out), *bad, None) == -1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [2048, 2100])
+def test_w4b_dequant_route_equals_bf16_gemm(m):
+    """The int4 GEMM at prefill sizes (DEQUANT_RT: dequantise into a workspace,
+    then the large-M bf16 kernel) gives bit for bit what that kernel gives on
+    the bf16-rounded weights, within GEMM_REL of the float64 anchor on the
+    unrounded ones; 2100 rows leave a ragged last M tile."""
+    from acorninfer_amd._lib import WFMT_W4B
+    from acorninfer_amd.models.qwen3 import DEQUANT_RT, QLinear
+    from acorninfer_amd.ops.quant_gemm import Tiling, bf16_gemm
+    from acorninfer_amd.quant.quantize import to_w4b
+    from oracle.quant_ref import gemm_ref
+    for cls in ("qkv", "down"):
+        p, s, wref = _w4(cls)
+        n, k = SHAPES[cls]
+        wb, sb = to_w4b(p, s)
+        lin = QLinear(WFMT_W4B, wb, n, k, sb)
+        t, _ = lin.plan(m, workspace=True)
+        assert t.rt == DEQUANT_RT, t
+        assert lin.plan(m)[0].rt != DEQUANT_RT          # no workspace: the int4 kernels
+        assert lin.plan(m, Tiling(DEQUANT_RT))[0] == t
+        x = _x(m, k, 31)
+        wtmp = torch.empty(n * k, dtype=torch.bfloat16, device="cuda")
+        out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        part = torch.empty(t.ksplit, m, n, dtype=torch.float32, device="cuda")
+        st = torch.cuda.current_stream().cuda_stream
+        with pytest.raises(ValueError):
+            lin.launch(x, m, t, out=out, part=part, stream=st)
+        lin.launch(x, m, t, out=out, part=part, wtmp=wtmp, stream=st)
+        want = bf16_gemm(x, wref.to(torch.bfloat16).contiguous())
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), cls
+        ref = torch.from_numpy(gemm_ref(x.float().cpu().numpy(), wref.cpu().numpy()))
+        r = rel_err(out.cpu(), ref)
+        print(f"\n[w4b dequant route M={m} {cls}: rel err {r:.3g} vs float64]")
+        assert r <= GEMM_REL
+
+
+@pytest.mark.gpu
 def test_w4b_split_partials_deterministic_and_graph_replay():
     """W4B partials at several split counts sum (in split order) to the same
     result within fp32 rounding, repeat bitwise, and replay bitwise in a
