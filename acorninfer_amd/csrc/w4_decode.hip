@@ -727,35 +727,46 @@ int w4m_launch(const W4mPlan& p, const void* x, const void* w, const void* scale
 // ---- W4B -> bf16 [N, K] (prefill-sized projections) ------------------------
 // out[n, k] = bf16_rne((u - 8) * s(n, k / 128)). (u - 8) * s is exact in fp32
 // (a 4-bit integer times an 11-bit significand), so the result is the
-// weight rounded once to bf16. One thread per 16-byte piece (one row, 32 k):
-// a wave reads one 1 KB block with one load instruction and writes the
-// block's 16 rows x 128 k as 4 KB of whole 64-byte row segments.
+// weight rounded once to bf16. One wave per 1 KB block (16 rows x 128 k;
+// 4 KB of output). The output is four fifths of the traffic, so every store
+// instruction writes whole 128-byte lines: 8 lanes per line (16 bytes = 8 k
+// each), 8 rows per instruction, 4 instructions per block. A lane's loads
+// follow its stores: 4 bytes (8 nibbles) per line it writes, from the block's
+// 16-byte piece (chunk c, row r); each load instruction reads two whole
+// lines of the block.
 namespace {
 
-__global__ __launch_bounds__(256) void w4b_dequant_kernel(const u32x4* __restrict__ w,
+__global__ __launch_bounds__(256) void w4b_dequant_kernel(const uint32_t* __restrict__ w,
                                                           const _Float16* __restrict__ scale,
                                                           __bf16* __restrict__ out, int64_t K,
-                                                          size_t pieces) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= pieces) return;
+                                                          int64_t blocks) {
+  const int64_t b = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+  if (b >= blocks) return;
+  const int lane = threadIdx.x % kWave;
+  const int j = lane & 7, rr = lane >> 3;
   const int64_t G = K / 128;
-  const size_t blk = i / 64;
-  const int lane = (int)(i % 64);
-  const int64_t n = (int64_t)(blk / G) * 16 + lane % 16;
-  const int64_t g = (int64_t)(blk % G);
-  const int64_t k0 = g * 128 + (lane / 16) * 32;
-  const float s = (float)scale[w4b_half_index(n, g, K)];
-  const u32x4 v = load_nt(w + i);
-  u32x4* dst = (u32x4*)(out + n * K + k0);
+  const int64_t t = b / G, g = b % G;
+  const uint32_t* blk = w + b * 256;
+  uint32_t d[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    uint32_t o[4];
+  for (int i = 0; i < 4; ++i) {
+    const int h = i >> 1, r = (i & 1) * 8 + rr, c = 2 * h + (j >> 2);
+    d[i] = __builtin_nontemporal_load(blk + (c * 16 + r) * 4 + (j & 3));
+  }
+  float s[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t byte = (v[q] >> (8 * j)) & 0xffu;
-      o[j] = pack_bf16x2((float)((int)(byte & 15u) - 8) * s, (float)((int)(byte >> 4) - 8) * s);
+  for (int e = 0; e < 2; ++e) s[e] = (float)scale[w4b_half_index(t * 16 + e * 8 + rr, g, K)];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int h = i >> 1, r = (i & 1) * 8 + rr;
+    const float sc = s[i & 1];
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t byte = (d[i] >> (8 * q)) & 0xffu;
+      o[q] = pack_bf16x2((float)((int)(byte & 15u) - 8) * sc, (float)((int)(byte >> 4) - 8) * sc);
     }
-    dst[q] = u32x4{o[0], o[1], o[2], o[3]};
+    *(u32x4*)(out + (t * 16 + r) * K + g * 128 + 64 * h + 8 * j) = o;
   }
 }
 
@@ -767,11 +778,11 @@ int w4b_dequant(const void* w, const void* scale, void* out, int64_t N, int64_t 
                 hipStream_t st) {
   if (N <= 0 || K <= 0 || N % 16 || K % 512) return ACORN_ERR_SHAPE;
   if (!w || !scale || !out) return ACORN_ERR_VALUE;
-  const size_t pieces = (size_t)N * (size_t)(K / 32);
-  const size_t blocks = (pieces + 255) / 256;
-  if (blocks > 0x7fffffffu) return ACORN_ERR_SHAPE;
-  w4b_dequant_kernel<<<(unsigned)blocks, 256, 0, st>>>((const u32x4*)w, (const _Float16*)scale,
-                                                       (__bf16*)out, K, pieces);
+  const int64_t blocks = (N / 16) * (K / 128);
+  const int64_t wgs = (blocks + 3) / 4;
+  if (wgs > 0x7fffffff) return ACORN_ERR_SHAPE;
+  w4b_dequant_kernel<<<(unsigned)wgs, 256, 0, st>>>((const uint32_t*)w, (const _Float16*)scale,
+                                                    (__bf16*)out, K, blocks);
   ACORN_LAUNCH_CHECK();
   return ACORN_OK;
 }
