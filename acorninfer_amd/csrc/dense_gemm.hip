@@ -24,10 +24,11 @@
 // Per 32 k a wave reads BM/16 B operands (1 KB each) from LDS for
 // WN/16 x BM/16 MFMAs. With one wave per SIMD this form stays near 0.8-0.9
 // PFLOP/s at M >= 2048 (reading the weights in whole lines through an LDS slab
-// instead was slower: the loads are not its bound). From 1024 rows the
-// planner takes the second form below, 256 x 256 tiles with both operands in
-// LDS and two waves per SIMD: 1.0-1.06 PFLOP/s at M = 2048-8192 (hipBLASLt:
-// 1.2-1.4).
+// instead was slower: the loads are not its bound). Two 256 x 256 forms
+// follow, both operands in LDS and two waves per SIMD: one stages through
+// registers (1.0-1.06 PFLOP/s at M = 2048-8192), the other loads straight
+// into LDS (global_load_lds) through a 4-stage ring, the planner's default
+// from 1024 rows (1.09-1.26 PFLOP/s at M = 8192; hipBLASLt: 1.3-1.4).
 #include <hip/hip_runtime.h>
 
 #include "acorn_hip.h"
@@ -283,6 +284,187 @@ __global__ __launch_bounds__(512, 1) void dense_lds_kernel(const __bf16* __restr
   }
 }
 
+// Direct-to-LDS form (bm == kLdsTile, wn == 128): a workgroup of 4 waves, one
+// per SIMD, owns a 256 x 256 output tile; wave (wn, wm) of its 2 x 2 grid owns
+// 128 x 128 of it (8 x 8 accumulator blocks, 256 accumulator registers), so
+// every operand it reads from LDS feeds 8 MFMAs (8 FLOPs per LDS byte). Both
+// operands go from memory into LDS with global_load_lds_dwordx4 (no staging
+// registers, no LDS store instructions), 32 k per stage through a ring of 4
+// stages: the loads of stage s + 3 are issued while stage s is multiplied, and
+// the operands of stage s + 1 are read into the second register set. Rows are
+// 64 bytes, unpadded: 16-byte piece p of row R sits at slot p ^ f(R),
+// f(R) = ((R >> 1) ^ (R >> 3)) & 3, which puts the 8 (or 16) rows that one
+// LDS cycle serves for an MFMA operand read on distinct banks. One barrier per
+// stage; the memory waits are explicit (vmcnt counts this wave's loads).
+constexpr int kDlBK = 32;                 // k per stage
+constexpr int kDlStages = 4;
+constexpr int kDlOpBytes = kLdsTile * kDlBK * 2;   // one operand of one stage: 16 KB
+
+__device__ __forceinline__ int dl_swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+template <typename OUT, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __restrict__ x,
+                                                              const __bf16* __restrict__ w,
+                                                              OUT* __restrict__ out, int M,
+                                                              int N, int K, int tiles_n,
+                                                              int tiles_m, int steps) {
+  constexpr int T = kLdsTile;
+  constexpr int NB = 8, MB = 32 / NW;          // wave tile 128 x 16 MB
+  constexpr int LPW = 16 / NW;                 // 1 KB loads per wave per operand per stage
+  __shared__ __align__(1024) uint8_t lds[kDlStages][2][kDlOpBytes];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane >> 4, c = lane & 15;
+  const int G = tiles_n * tiles_m;
+  int t = blockIdx.x;
+  if (G % 8 == 0) t = (t % 8) * (G / 8) + t / 8;
+  constexpr int GN = 4;
+  const int group = t / (GN * tiles_m);
+  const int first_n = group * GN;
+  const int gsize = min(tiles_n - first_n, GN);
+  const int in_group = t - group * GN * tiles_m;
+  const int tn = first_n + in_group % gsize;
+  const int tm = in_group / gsize;
+  const int n0 = tn * T, m0 = tm * T;
+  const int wn = (wid & 1) * 128, wm = (wid >> 1) * 16 * MB;
+  const int kbase = blockIdx.y * steps * kDlBK;
+  out += (size_t)blockIdx.y * M * N;
+
+  // load j of this wave fills rows 16 (LPW wid + j) .. + 15 of an operand:
+  // lane L writes row 16 (LPW wid + j) + L / 4, slot L % 4, with global piece
+  // (L % 4) ^ f(row)
+  const __bf16* wsrc[LPW];
+  const __bf16* xsrc[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int row = 16 * (LPW * wid + j) + (lane >> 2);
+    const int piece = (lane & 3) ^ dl_swz(row);
+    wsrc[j] = w + (size_t)min(n0 + row, N - 1) * K + kbase + 8 * piece;
+    xsrc[j] = x + (size_t)min(m0 + row, M - 1) * K + kbase + 8 * piece;
+  }
+  // operand reads: block i's row wn + 16 i + c, piece r; f(row) repeats every
+  // two blocks (32 rows), so blocks i and i + 2 differ by 2048 bytes
+  uint32_t aoff[2], boff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int ra = wn + 16 * i + c, rb = wm + 16 * i + c;
+    aoff[i] = (uint32_t)(ra * 64 + 16 * (r ^ dl_swz(ra)));
+    boff[i] = (uint32_t)(rb * 64 + 16 * (r ^ dl_swz(rb)));
+  }
+
+  // the LDS DMA is issued from inline assembly, so the compiler neither
+  // orders LDS reads behind it nor waits for it: the explicit vmcnt waits
+  // below do (this wave's loads; the barrier makes every wave's visible)
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)(&lds[0][0][0]);
+  auto dma = [&](const __bf16* src, uint32_t dst) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(src), "s"(dst) : "memory", "m0");
+#pragma clang diagnostic pop
+  };
+  auto issue = [&](int s) {
+    const int b = s & (kDlStages - 1);
+    const int k0 = min(s, steps - 1) * kDlBK;
+    const uint32_t base = lds0 + (uint32_t)(b * 2 * kDlOpBytes + LPW * wid * 1024);
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) dma(wsrc[j] + k0, base + j * 1024);
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) dma(xsrc[j] + k0, base + kDlOpBytes + j * 1024);
+  };
+  auto opA = [&](int s, int i) {
+    return *(const u32x4*)(&lds[s & (kDlStages - 1)][0][aoff[i & 1] + 2048 * (i >> 1)]);
+  };
+  auto opB = [&](int s, int j) {
+    return *(const u32x4*)(&lds[s & (kDlStages - 1)][1][boff[j & 1] + 2048 * (j >> 1)]);
+  };
+
+  f32x4 acc[NB][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // one stage: row i's 8 MFMAs, then a[i] is refilled with stage s + 1's
+  // block i (its last use in this stage is done); bn receives stage s + 1's
+  // x operands up front, into the set this stage does not read
+  u32x4 a[NB], b0[MB], b1[MB];
+  auto stage = [&](int s, const u32x4 (&bc)[MB], u32x4 (&bn)[MB]) {
+#pragma unroll
+    for (int j = 0; j < MB; ++j) bn[j] = opB(s + 1, j);
+    issue(s + 3);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+#pragma unroll
+      for (int j = 0; j < MB; ++j) acc[i][j] = mfma(a[i], bc[j], acc[i][j]);
+      a[i] = opA(s + 1, i);
+      // keep the refill here, a stage ahead of its use
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // vmcnt(n) with the other counters left open (gfx9 encoding)
+#define ACORN_DL_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+  constexpr int LPS = 2 * LPW;        // this wave's loads per stage
+  issue(0);
+  issue(1);
+  issue(2);
+  ACORN_DL_VMCNT(2 * LPS);            // this wave's stage-0 loads have landed
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NB; ++i) a[i] = opA(0, i);
+#pragma unroll
+  for (int j = 0; j < MB; ++j) b0[j] = opB(0, j);
+  // iteration s: stage s + 1 lands (barrier; its reads go to the registers
+  // this stage frees), stage s + 3's loads go into the buffer stage s - 1
+  // used (every wave finished reading it before this barrier)
+  for (int s = 0; s < steps; s += 2) {      // steps is even
+    ACORN_DL_VMCNT(LPS);
+    __syncthreads();
+    stage(s, b0, b1);
+    ACORN_DL_VMCNT(LPS);
+    __syncthreads();
+    stage(s + 1, b1, b0);
+  }
+#undef ACORN_DL_VMCNT
+  __builtin_amdgcn_s_waitcnt(0);      // no LDS write of this wave outlives it
+
+  // lane (r, c) of block (i, j) holds out[m0 + wm + 16 j + c][n0 + wn + 16 i + 4 r + e]
+#pragma unroll
+  for (int j = 0; j < MB; ++j) {
+    const int m = m0 + wm + 16 * j + c;
+    if (m >= M) continue;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int n = n0 + wn + 16 * i + 4 * r;
+      if (n >= N) continue;
+      OUT* o = out + (size_t)m * N + n;
+      if constexpr (sizeof(OUT) == 4) {
+        *(f32x4*)o = acc[i][j];
+      } else {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        u32x2 v;
+        v[0] = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
+        v[1] = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
+        *(u32x2*)o = v;
+      }
+    }
+  }
+}
+
+template <typename OUT, int NW>
+int launch_dl(const void* x, const void* w, void* out, int64_t M, int64_t N, int64_t K, int ks,
+              hipStream_t st) {
+  const int64_t tiles_n = (N + kLdsTile - 1) / kLdsTile, tiles_m = (M + kLdsTile - 1) / kLdsTile;
+  if (tiles_n * tiles_m > 0x7fffffff) return ACORN_ERR_SHAPE;
+  dense_dl_kernel<OUT, NW>
+      <<<dim3((unsigned)(tiles_n * tiles_m), (unsigned)ks), dim3(NW * 64), 0, st>>>(
+      (const __bf16*)x, (const __bf16*)w, (OUT*)out, (int)M, (int)N, (int)K, (int)tiles_n,
+      (int)tiles_m, (int)(K / kDlBK / ks));
+  return ACORN_OK;
+}
+
 template <typename OUT, int DEPTH>
 int launch_lds(const void* x, const void* w, void* out, int64_t M, int64_t N, int64_t K, int ks,
                hipStream_t st) {
@@ -311,7 +493,8 @@ template <typename OUT>
 int dispatch(int wn, int bm, int depth, const void* x, const void* w, void* out, int64_t M,
              int64_t N, int64_t K, int ks, hipStream_t st) {
   if (bm == kLdsTile) {
-    if (depth == 2) return launch_lds<OUT, 2>(x, w, out, M, N, K, ks, st);
+    if (wn == 64 && depth == 2) return launch_lds<OUT, 2>(x, w, out, M, N, K, ks, st);
+    if (wn == 128 && depth == kDlStages) return launch_dl<OUT, 8>(x, w, out, M, N, K, ks, st);
   } else if (wn == 64) {
     if (bm == 128 && depth == 2) return launch<OUT, 64, 128, 2>(x, w, out, M, N, K, ks, st);
     if (bm == 128 && depth == 4) return launch<OUT, 64, 128, 4>(x, w, out, M, N, K, ks, st);
@@ -326,6 +509,9 @@ int dispatch(int wn, int bm, int depth, const void* x, const void* w, void* out,
 }  // namespace
 
 bool dense_gemm_supported(int64_t N, int64_t K, int wn, int bm, int depth, int ks) {
+  if (bm == kLdsTile && wn == 128)   // direct-to-LDS form: 32 k per stage
+    return depth == kDlStages && ks >= 1 && ks <= 64 && N % 4 == 0 && K % kDlBK == 0 &&
+           (K / kDlBK) % (2 * ks) == 0;
   const bool built = bm == kLdsTile ? wn == 64 && depth == 2
                    : wn == 64 ? (bm == 64 || bm == 128) && (depth == 2 || depth == 4)
                    : wn == 128 ? bm == 64 && depth == 2

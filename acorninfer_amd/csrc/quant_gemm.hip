@@ -837,12 +837,17 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
     const bool req = cfg && cfg[0] == kDenseRT;
     // from kDenseLdsM rows the 256 x 256 tiles with both operands in LDS
     const int bm = req && cfg[1] > 0 ? cfg[1] : M >= kDenseLdsM ? 256 : 128;
-    const int wn = req && cfg[2] > 0 ? cfg[2] : 64;
-    const int depth = req && cfg[4] > 0 ? cfg[4] : bm == 256 ? 2 : 4;
+    const int wn = req && cfg[2] > 0              ? cfg[2]
+                   : bm == 256 && !(req && cfg[4] == 2) ? 128    // depth 2: the staged form
+                                                        : 64;
+    // (bm 256: wn 64 is the register-staged form, depth 2; wn 128 the
+    // direct-to-LDS form, a 4-stage ring)
+    const int depth = req && cfg[4] > 0 ? cfg[4] : bm == 256 ? (wn == 128 ? 4 : 2) : 4;
+    const int ntile = bm == 256 ? 256 : 4 * wn;    // weight rows per workgroup
     int ks = req && cfg[3] > 0 ? cfg[3] : 1;
     if (!(req && cfg[3] > 0)) {
       // split K while the launch has fewer workgroups than CUs
-      const int64_t tiles = ((N + 4 * wn - 1) / (4 * wn)) * ((M + bm - 1) / bm);
+      const int64_t tiles = ((N + ntile - 1) / ntile) * ((M + bm - 1) / bm);
       while (tiles * ks < kCUs && ks < 8 && dense_gemm_supported(N, K, wn, bm, depth, 2 * ks))
         ks *= 2;
     }
@@ -856,7 +861,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
       t->mt = 1;
       t->R = bm;
       t->nk = (int)(K / 64);
-      t->ntiles = (int)((N + 4 * wn - 1) / (4 * wn));
+      t->ntiles = (int)((N + ntile - 1) / ntile);
       t->mblocks = (int)((M + bm - 1) / bm);
       t->groups = 1;
       t->lds = 0;

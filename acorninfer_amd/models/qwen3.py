@@ -52,16 +52,13 @@ FORMATS = {"bf16": WFMT_BF16, "w8a16": WFMT_W8, "w4a16": WFMT_W4}
 DENSE_M_MIN = 512
 DENSE_RT = -2
 LIBRARY_RT = -1
-# int4 (W4B) projections from DEQUANT_M_MIN rows (DEQUANT_M_MIN_LARGE for
-# weights of at least DEQUANT_LARGE_NK elements): the weights are dequantised
-# to bf16 into a step workspace (acorn_dequant_w4b) and multiplied by the
-# large-M bf16 kernel (tiling rt == DEQUANT_RT, the other fields the bf16
-# kernel's). At prefill sizes the MFMA work dominates and that kernel's rate
-# outweighs the extra pass over the weights (measured crossovers on MI355X:
-# about 2048 rows for the 8B model's qkv and o, 1024 for gate|up and down).
-DEQUANT_M_MIN = 2048
-DEQUANT_M_MIN_LARGE = 1024
-DEQUANT_LARGE_NK = 1 << 25
+# int4 (W4B) projections from DEQUANT_M_MIN rows: the weights are
+# dequantised to bf16 into a step workspace (acorn_dequant_w4b) and
+# multiplied by the large-M bf16 kernel (tiling rt == DEQUANT_RT, the other
+# fields the bf16 kernel's). At prefill sizes the MFMA work dominates and that
+# kernel's rate outweighs the extra pass over the weights (on MI355X the
+# 8B model's qkv breaks even at 1024 rows, the other projections gain there).
+DEQUANT_M_MIN = 1024
 DEQUANT_RT = -4
 
 
@@ -183,16 +180,14 @@ class QLinear:
         """(Tiling, output tiles) from the library planner (a LIBRARY_RT
         request is passed through: torch.mm). workspace: the caller holds a
         bf16 weight workspace, so int4 weights take the dequantise + bf16
-        GEMM route by default from DEQUANT_M_MIN rows (DEQUANT_M_MIN_LARGE for
-        large weights; a DEQUANT_RT request takes it at any size)."""
+        GEMM route by default from DEQUANT_M_MIN rows (a DEQUANT_RT request
+        takes it at any size)."""
         from acorninfer_amd.ops.quant_gemm import Tiling, plan
         if tiling is not None and tiling[0] == LIBRARY_RT:
             return Tiling(LIBRARY_RT, 0, 0, 1, 0), None
         if self.fmt == WFMT_W4B and (
                 (tiling is not None and tiling[0] == DEQUANT_RT) or
-                (workspace and (tiling is None or not any(tiling)) and M >= (
-                    DEQUANT_M_MIN_LARGE if self.N * self.K >= DEQUANT_LARGE_NK
-                    else DEQUANT_M_MIN))):
+                (workspace and (tiling is None or not any(tiling)) and M >= DEQUANT_M_MIN)):
             rest = tuple(tiling[1:]) if tiling is not None else (0, 0, 0, 0)
             t, tiles = plan(M, self.N, self.K, WFMT_BF16, Tiling(DENSE_RT, *rest))
             return Tiling(DEQUANT_RT, *t[1:]), tiles

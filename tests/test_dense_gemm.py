@@ -57,9 +57,12 @@ def test_planner_routes_prefill_sizes_to_the_dense_kernel():
     t, tiles = plan(512, 4096, 4096, WFMT_BF16)
     assert t == Tiling(DENSE_RT, 128, 64, 4, 4) and tiles == 16 * 4   # 64 tiles x 4 splits
     assert plan(1023, 4096, 4096, WFMT_BF16)[0].upw == 128
-    assert plan(8192, 4096, 4096, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 64, 1, 2)  # LDS form
+    # from 1024 rows: 256 x 256 tiles, both operands by direct-to-LDS loads
+    assert plan(8192, 4096, 4096, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 1, 4)
+    assert plan(8192, 4096, 4096, WFMT_BF16, Tiling(DENSE_RT, 256, 64))[0] == \
+        Tiling(DENSE_RT, 256, 64, 1, 2)                              # register-staged form
     assert plan(511, 4096, 4096, WFMT_BF16)[0].rt != DENSE_RT       # tiled kernel below 512
-    assert plan(4096, 4096, 192, WFMT_BF16)[0].rt != DENSE_RT       # 3 K steps: depth 2 does not divide
+    assert plan(4096, 4096, 192, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 1, 4)  # 6 stages of 32
     assert plan(4096, 4096, 4096, WFMT_W8)[0].rt != DENSE_RT        # bf16 weights only
     assert plan(64, 4096, 4096, WFMT_BF16, Tiling(DENSE_RT, 64, 0, 1, 4))[0] == \
         Tiling(DENSE_RT, 64, 64, 1, 4)                               # on request at any M
@@ -69,11 +72,12 @@ def test_planner_routes_prefill_sizes_to_the_dense_kernel():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("wn,bm,depth", [(64, 128, 2), (64, 128, 4), (64, 64, 2), (64, 64, 4),
-                                         (128, 64, 2), (64, 256, 2)])
+                                         (128, 64, 2), (64, 256, 2), (128, 256, 4)])
 def test_dense_gemm_matches_float64(wn, bm, depth):
     from acorninfer_amd.ops.quant_gemm import Tiling
     for i, (M, N, K) in enumerate(SMALL):
-        if (K // 64) % depth:
+        # the direct-to-LDS form (256, 128) runs 32-k stages in pairs
+        if ((K // 32) % 2 if (bm, wn) == (256, 128) else (K // 64) % depth):
             continue
         print(f"\n[dense GEMM M={M} N={N} K={K} wn={wn} bm={bm} depth={depth}]", flush=True)
         x, w = _operands(M, N, K, 100 + i)
@@ -102,14 +106,14 @@ def test_dense_gemm_config3_at_prefill_m(cls):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("bm", [128, 256])
-def test_dense_gemm_deterministic_graph_and_bounds(bm):
+@pytest.mark.parametrize("bm,wn,depth", [(128, 0, 2), (256, 0, 2), (256, 128, 4)])
+def test_dense_gemm_deterministic_graph_and_bounds(bm, wn, depth):
     from acorninfer_amd._lib import WFMT_BF16
     from acorninfer_amd.ops.quant_gemm import Tiling, gemm_partials
     M, N, K = 600, 516, 256
     x, w = _operands(M, N, K, 3)
     xd, wd = x.cuda(), w.cuda()
-    t = Tiling(DENSE_RT, bm, 0, 1, 2)
+    t = Tiling(DENSE_RT, bm, wn, 1, depth)
     big = torch.full((M + 7, N), 9.0, device="cuda")       # 7 guard rows after the output
     part = big[:M].view(1, M, N)
     gemm_partials(xd, wd, None, None, WFMT_BF16, part, t)
