@@ -292,15 +292,19 @@ __global__ __launch_bounds__(512, 1) void dense_lds_kernel(const __bf16* __restr
 // registers, no LDS store instructions), 32 k per stage through a ring of 4
 // stages: the loads of stage s + 3 are issued while stage s is multiplied, and
 // the operands of stage s + 1 are read into the second register set. Rows are
-// 64 bytes, unpadded: 16-byte piece p of row R sits at slot p ^ f(R),
-// f(R) = ((R >> 1) ^ (R >> 3)) & 3, which puts the 8 (or 16) rows that one
-// LDS cycle serves for an MFMA operand read on distinct banks. One barrier per
-// stage; the memory waits are explicit (vmcnt counts this wave's loads).
+// 64 bytes, unpadded: 16-byte piece p of row R sits at slot p ^ ((R >> 1) & 3).
+// An MFMA operand read (lane (r, c): row c of a 16-row block, piece r) then
+// runs without LDS bank conflicts on gfx950 (a probe of ds_read_b128
+// patterns: this one, like a linear read, shows no conflict cycles; padded
+// 144- or 80-byte rows, unswizzled 64-byte rows and ((R >> 1) ^ (R >> 3)) & 3
+// all add 20%). One barrier per stage; the memory waits are explicit (vmcnt
+// counts this wave's loads). A fifth stage (all 160 KB of LDS) measured 2-3%
+// slower.
 constexpr int kDlBK = 32;                 // k per stage
 constexpr int kDlStages = 4;
 constexpr int kDlOpBytes = kLdsTile * kDlBK * 2;   // one operand of one stage: 16 KB
 
-__device__ __forceinline__ int dl_swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+__device__ __forceinline__ int dl_swz(int row) { return (row >> 1) & 3; }
 
 template <typename OUT, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __restrict__ x,
@@ -343,15 +347,10 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
     wsrc[j] = w + (size_t)min(n0 + row, N - 1) * K + kbase + 8 * piece;
     xsrc[j] = x + (size_t)min(m0 + row, M - 1) * K + kbase + 8 * piece;
   }
-  // operand reads: block i's row wn + 16 i + c, piece r; f(row) repeats every
-  // two blocks (32 rows), so blocks i and i + 2 differ by 2048 bytes
-  uint32_t aoff[2], boff[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int ra = wn + 16 * i + c, rb = wm + 16 * i + c;
-    aoff[i] = (uint32_t)(ra * 64 + 16 * (r ^ dl_swz(ra)));
-    boff[i] = (uint32_t)(rb * 64 + 16 * (r ^ dl_swz(rb)));
-  }
+  // operand reads: block i's row wn + 16 i + c, piece r; the swizzle depends
+  // on c only, so block i sits 1024 bytes after block 0
+  const uint32_t aoff = (uint32_t)((wn + c) * 64 + 16 * (r ^ dl_swz(c)));
+  const uint32_t boff = (uint32_t)((wm + c) * 64 + 16 * (r ^ dl_swz(c)));
 
   // the LDS DMA is issued from inline assembly, so the compiler neither
   // orders LDS reads behind it nor waits for it: the explicit vmcnt waits
@@ -374,10 +373,10 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
     for (int j = 0; j < LPW; ++j) dma(xsrc[j] + k0, base + kDlOpBytes + j * 1024);
   };
   auto opA = [&](int s, int i) {
-    return *(const u32x4*)(&lds[s & (kDlStages - 1)][0][aoff[i & 1] + 2048 * (i >> 1)]);
+    return *(const u32x4*)(&lds[s & (kDlStages - 1)][0][aoff + 1024 * i]);
   };
   auto opB = [&](int s, int j) {
-    return *(const u32x4*)(&lds[s & (kDlStages - 1)][1][boff[j & 1] + 2048 * (j >> 1)]);
+    return *(const u32x4*)(&lds[s & (kDlStages - 1)][1][boff + 1024 * j]);
   };
 
   f32x4 acc[NB][MB];
