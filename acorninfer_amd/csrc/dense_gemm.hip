@@ -306,7 +306,7 @@ constexpr int kDlOpBytes = kLdsTile * kDlBK * 2;   // one operand of one stage: 
 
 __device__ __forceinline__ int dl_swz(int row) { return (row >> 1) & 3; }
 
-template <typename OUT, int NW>
+template <typename OUT, int NW, bool SWIGLU = false>
 __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __restrict__ x,
                                                               const __bf16* __restrict__ w,
                                                               OUT* __restrict__ out, int M,
@@ -429,6 +429,28 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
 #undef ACORN_DL_VMCNT
   __builtin_amdgcn_s_waitcnt(0);      // no LDS write of this wave outlives it
 
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  if constexpr (SWIGLU) {
+    // gate|up rows interleaved in 16-row blocks: the wave's blocks 2q (gate)
+    // and 2q + 1 (up) hold the same 16 outputs, pair (n0 + wn) / 32 + q;
+    // out is act [M, N / 2]
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int m = m0 + wm + 16 * j + c;
+      if (m >= M) continue;
+#pragma unroll
+      for (int q = 0; q < NB / 2; ++q) {
+        const int nb = n0 + wn + 32 * q;
+        if (nb >= N) continue;
+        const f32x4 g = acc[2 * q][j], u = acc[2 * q + 1][j];
+        u32x2 v;
+        v[0] = pack_bf16x2(swiglu_bf16(g[0], u[0]), swiglu_bf16(g[1], u[1]));
+        v[1] = pack_bf16x2(swiglu_bf16(g[2], u[2]), swiglu_bf16(g[3], u[3]));
+        *(u32x2*)(out + (size_t)m * (N / 2) + nb / 2 + 4 * r) = v;
+      }
+    }
+    return;
+  }
   // lane (r, c) of block (i, j) holds out[m0 + wm + 16 j + c][n0 + wn + 16 i + 4 r + e]
 #pragma unroll
   for (int j = 0; j < MB; ++j) {
@@ -442,7 +464,6 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
       if constexpr (sizeof(OUT) == 4) {
         *(f32x4*)o = acc[i][j];
       } else {
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
         u32x2 v;
         v[0] = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
         v[1] = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
@@ -452,12 +473,12 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
   }
 }
 
-template <typename OUT, int NW>
+template <typename OUT, int NW, bool SWIGLU = false>
 int launch_dl(const void* x, const void* w, void* out, int64_t M, int64_t N, int64_t K, int ks,
               hipStream_t st) {
   const int64_t tiles_n = (N + kLdsTile - 1) / kLdsTile, tiles_m = (M + kLdsTile - 1) / kLdsTile;
   if (tiles_n * tiles_m > 0x7fffffff) return ACORN_ERR_SHAPE;
-  dense_dl_kernel<OUT, NW>
+  dense_dl_kernel<OUT, NW, SWIGLU>
       <<<dim3((unsigned)(tiles_n * tiles_m), (unsigned)ks), dim3(NW * 64), 0, st>>>(
       (const __bf16*)x, (const __bf16*)w, (OUT*)out, (int)M, (int)N, (int)K, (int)tiles_n,
       (int)tiles_m, (int)(K / kDlBK / ks));
@@ -525,6 +546,17 @@ int dense_gemm_launch(const void* x, const void* w, void* out_bf16, float* out_f
   if (out_f32) return dispatch<float>(wn, bm, depth, x, w, out_f32, M, N, K, ks, st);
   if (ks != 1) return ACORN_ERR_VALUE;
   return dispatch<__bf16>(wn, bm, depth, x, w, out_bf16, M, N, K, 1, st);
+}
+
+bool dense_gemm_swiglu_supported(int64_t N, int64_t K, int wn, int bm, int depth) {
+  return bm == kLdsTile && wn == 128 && N % 32 == 0 &&
+         dense_gemm_supported(N, K, wn, bm, depth, 1);
+}
+
+int dense_gemm_swiglu_launch(const void* x, const void* w, void* act, int64_t M, int64_t N,
+                             int64_t K, int wn, int bm, int depth, hipStream_t st) {
+  if (!dense_gemm_swiglu_supported(N, K, wn, bm, depth)) return ACORN_ERR_UNSUPPORTED;
+  return launch_dl<__bf16, 8, true>(x, w, act, M, N, K, 1, st);
 }
 
 }  // namespace acorn

@@ -145,6 +145,11 @@ int w4b_dequant(const void* w, const void* scale, void* out, int64_t N, int64_t 
 // when out_f32 is given (split s into out_f32 + s*M*N), else bf16 into
 // out_bf16 (ks == 1 only).
 bool dense_gemm_supported(int64_t N, int64_t K, int wn, int bm, int depth, int ks);
+// gate|up (16-row interleave) with the SwiGLU epilogue: act [M, N / 2] bf16,
+// one split, the direct-to-LDS form (bm 256, wn 128) and N % 32 == 0
+bool dense_gemm_swiglu_supported(int64_t N, int64_t K, int wn, int bm, int depth);
+int dense_gemm_swiglu_launch(const void* x, const void* w, void* act, int64_t M, int64_t N,
+                             int64_t K, int wn, int bm, int depth, hipStream_t st);
 int dense_gemm_launch(const void* x, const void* w, void* out_bf16, float* out_f32, int64_t M,
                       int64_t N, int64_t K, int wn, int bm, int depth, int ks, hipStream_t st);
 

@@ -832,8 +832,10 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   t->kind = 0;
   const bool no_request = !cfg || (cfg[0] == 0 && cfg[1] == 0 && cfg[2] == 0 && cfg[3] <= 1 &&
                                    cfg[4] == 0);
-  if (wfmt == ACORN_WFMT_BF16 && !swiglu &&
-      ((cfg && cfg[0] == kDenseRT) || (no_request && M >= kDenseMinM))) {
+  // the SwiGLU epilogue is built into the direct-to-LDS form only (from
+  // kDenseLdsM rows, or on request)
+  if (wfmt == ACORN_WFMT_BF16 &&
+      ((cfg && cfg[0] == kDenseRT) || (no_request && M >= (swiglu ? kDenseLdsM : kDenseMinM)))) {
     const bool req = cfg && cfg[0] == kDenseRT;
     // from kDenseLdsM rows the 256 x 256 tiles with both operands in LDS
     const int bm = req && cfg[1] > 0 ? cfg[1] : M >= kDenseLdsM ? 256 : 128;
@@ -845,13 +847,14 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
     const int depth = req && cfg[4] > 0 ? cfg[4] : bm == 256 ? (wn == 128 ? 4 : 2) : 4;
     const int ntile = bm == 256 ? 256 : 4 * wn;    // weight rows per workgroup
     int ks = req && cfg[3] > 0 ? cfg[3] : 1;
-    if (!(req && cfg[3] > 0)) {
+    if (!(req && cfg[3] > 0) && !swiglu) {
       // split K while the launch has fewer workgroups than CUs
       const int64_t tiles = ((N + ntile - 1) / ntile) * ((M + bm - 1) / bm);
       while (tiles * ks < kCUs && ks < 8 && dense_gemm_supported(N, K, wn, bm, depth, 2 * ks))
         ks *= 2;
     }
-    if (dense_gemm_supported(N, K, wn, bm, depth, ks)) {
+    if (swiglu ? ks == 1 && dense_gemm_swiglu_supported(N, K, wn, bm, depth)
+               : dense_gemm_supported(N, K, wn, bm, depth, ks)) {
       t->kind = 3;
       t->rt = kDenseRT;
       t->upw = bm;
@@ -1159,8 +1162,9 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
   if (t.kind == 3) {
     // bf16 straight into out (one split), else fp32 split planes into part
     const bool direct = out_bf16 && t.ksplit == 1;
-    rc = dense_gemm_launch(x, w, direct ? out_bf16 : nullptr, direct ? nullptr : part, M, N, K,
-                           t.nw, t.upw, t.tpw, t.ksplit, st);
+    rc = t.swiglu ? dense_gemm_swiglu_launch(x, w, out_bf16, M, N, K, t.nw, t.upw, t.tpw, st)
+                  : dense_gemm_launch(x, w, direct ? out_bf16 : nullptr, direct ? nullptr : part,
+                                      M, N, K, t.nw, t.upw, t.tpw, t.ksplit, st);
   } else if (t.kind == 2) {
     rc = w4b_launch(t.w4b, x, w, scale, zero, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K,
                     st);

@@ -60,6 +60,9 @@ LIBRARY_RT = -1
 # 8B model's qkv breaks even at 1024 rows, the other projections gain there).
 DEQUANT_M_MIN = 1024
 DEQUANT_RT = -4
+# prefill blocks from this many rows run gate|up with the large-M kernel's
+# SwiGLU epilogue (act written directly: no fp32 gate|up output, no silu_mul)
+PREFILL_SWIGLU_M = 1024
 
 
 def dispatch_linear(mod, x: torch.Tensor) -> torch.Tensor:
@@ -193,6 +196,16 @@ class QLinear:
             return Tiling(DEQUANT_RT, *t[1:]), tiles
         return plan(M, self.N, self.K, self.fmt, tiling)
 
+    def _dequant(self, wtmp: torch.Tensor | None, M: int, stream: int) -> None:
+        """W4B -> bf16 [N, K] into wtmp (the first half of a DEQUANT_RT launch)."""
+        if self.fmt != WFMT_W4B:
+            raise ValueError("a DEQUANT_RT tiling needs W4B weights")
+        if wtmp is None or wtmp.dtype != torch.bfloat16 or wtmp.numel() < self.N * self.K:
+            raise ValueError(f"int4 GEMM at {M} rows (DEQUANT_RT) needs a bf16 weight "
+                             f"workspace of {self.N * self.K} elements")
+        check(lib().acorn_dequant_w4b(ptr(self.w), ptr(self.scale), ptr(wtmp), self.N, self.K,
+                                      stream), "dequant_w4b")
+
     def launch(self, x: torch.Tensor, M: int, tiling, *, out: torch.Tensor | None = None,
                part: torch.Tensor | None = None, wtmp: torch.Tensor | None = None,
                stream: int) -> None:
@@ -211,14 +224,7 @@ class QLinear:
                 torch.ops.aten.mm.dtype_out(xs, self.w.t(), torch.float32, out=part[0])
             return
         if tiling[0] == DEQUANT_RT:
-            if self.fmt != WFMT_W4B:
-                raise ValueError("a DEQUANT_RT tiling needs W4B weights")
-            if (wtmp is None or wtmp.dtype != torch.bfloat16 or
-                    wtmp.numel() < self.N * self.K):
-                raise ValueError(f"int4 GEMM at {M} rows (DEQUANT_RT) needs a bf16 weight "
-                                 f"workspace of {self.N * self.K} elements")
-            check(lib().acorn_dequant_w4b(ptr(self.w), ptr(self.scale), ptr(wtmp), self.N,
-                                          self.K, stream), "dequant_w4b")
+            self._dequant(wtmp, M, stream)
             arr = (ctypes.c_int * 6)(DENSE_RT, *tiling[1:], 0)
             rc = lib().acorn_quant_gemm(ptr(x), ptr(wtmp), None, None, ptr(out), ptr(part), M,
                                         self.N, self.K, WFMT_BF16, arr, stream)
@@ -230,17 +236,29 @@ class QLinear:
                                     stream)
         check(rc, "quant_gemm")
 
-    def swiglu_plan(self, M: int, tiling=None):
-        from acorninfer_amd.ops.quant_gemm import swiglu_plan
+    def swiglu_plan(self, M: int, tiling=None, workspace: bool = False):
+        """As plan, for the fused gate|up + SwiGLU launch (int4 at prefill
+        sizes: dequantised onto the bf16 kernel's SwiGLU form)."""
+        from acorninfer_amd.ops.quant_gemm import Tiling, swiglu_plan
+        if self.fmt == WFMT_W4B and (
+                (tiling is not None and tiling[0] == DEQUANT_RT) or
+                (workspace and (tiling is None or not any(tiling)) and M >= DEQUANT_M_MIN)):
+            rest = tuple(tiling[1:]) if tiling is not None else (0, 0, 0, 0)
+            t, tiles = swiglu_plan(M, self.N, self.K, WFMT_BF16, Tiling(DENSE_RT, *rest))
+            return Tiling(DEQUANT_RT, *t[1:]), tiles
         return swiglu_plan(M, self.N, self.K, self.fmt, tiling)
 
     def launch_swiglu(self, x: torch.Tensor, M: int, tiling, act: torch.Tensor,
-                      stream: int) -> None:
-        """Fused gate|up + SwiGLU (il16 weights): act [M, N/2] bf16."""
-        arr = (ctypes.c_int * 6)(*tiling, 0)
-        rc = lib().acorn_quant_gemm_swiglu(ptr(x), ptr(self.w), ptr(self.scale),
-                                           ptr(self.zero), ptr(act), M, self.N, self.K,
-                                           self.fmt, arr, stream)
+                      stream: int, wtmp: torch.Tensor | None = None) -> None:
+        """Fused gate|up + SwiGLU (il16 weights): act [M, N/2] bf16. A
+        DEQUANT_RT tiling dequantises into wtmp first, as launch does."""
+        w, fmt, arr = self.w, self.fmt, (ctypes.c_int * 6)(*tiling, 0)
+        if tiling[0] == DEQUANT_RT:
+            self._dequant(wtmp, M, stream)
+            w, fmt, arr = wtmp, WFMT_BF16, (ctypes.c_int * 6)(DENSE_RT, *tiling[1:], 0)
+        scale = self.scale if fmt != WFMT_BF16 else None
+        rc = lib().acorn_quant_gemm_swiglu(ptr(x), ptr(w), ptr(scale), ptr(self.zero), ptr(act),
+                                           M, self.N, self.K, fmt, arr, stream)
         check(rc, "quant_gemm_swiglu")
 
 
@@ -504,7 +522,7 @@ class Qwen3DecodeModel:
             # MLP: gate|up (+ fused SwiGLU) -> act -> down partials
             cg = buf.cfgs["gate_up"]
             if buf.swiglu:
-                lw.gate_up.launch_swiglu(buf.normed, B, cg, buf.act, st)
+                lw.gate_up.launch_swiglu(buf.normed, B, cg, buf.act, st, wtmp=buf.wtmp)
             else:
                 lw.gate_up.launch(buf.normed, B, cg, part=buf.part_gu, wtmp=buf.wtmp,
                                    stream=st)
@@ -538,6 +556,13 @@ class Qwen3DecodeModel:
                              ptr(buf.uniform), ptr(buf.next_ids), ptr(buf.logprob), None,
                              ptr(buf.status), st), "sample")
         return None
+
+    def prefill_swiglu(self, rows: int) -> bool:
+        """A prefill block of `rows` runs gate|up with the SwiGLU epilogue of
+        the large-M bf16 kernel (bf16 weights, or int4 dequantised onto it):
+        from PREFILL_SWIGLU_M rows, gate|up in the 16-row interleave."""
+        gu = self.layers[0].gate_up
+        return gu.il16 and rows >= PREFILL_SWIGLU_M and gu.fmt in (WFMT_BF16, WFMT_W4B)
 
     def fused_swiglu(self, batch: int) -> bool:
         """The gate|up launch carries the SwiGLU epilogue (decode sizes, and
@@ -936,11 +961,14 @@ class StepBuffers:
                 self.num_splits = max(1, min(self.num_splits, cap))
         lw = m.layers[0]
         tilings = self.tilings or {}
-        self.swiglu = m.fused_swiglu(B)
+        # prefill blocks: the large-M kernel's SwiGLU epilogue unless a
+        # tiling is requested for gate|up (hipBLASLt, or the int4 kernels)
+        self.swiglu = (m.prefill_swiglu(B) and "gate_up" not in tilings if self.prefill
+                       else m.fused_swiglu(B))
         for name, lin in (("qkv", lw.qkv), ("o", lw.o), ("gate_up", lw.gate_up),
                           ("down", lw.down), ("lm_head", m.lm_head)):
             if name == "gate_up" and self.swiglu:
-                self.cfgs[name] = lin.swiglu_plan(B, tilings.get(name))[0]
+                self.cfgs[name] = lin.swiglu_plan(B, tilings.get(name), workspace=True)[0]
             else:
                 self.cfgs[name] = lin.plan(B, tilings.get(name), workspace=name != "lm_head")[0]
         # bf16 copy of one int4 projection at a time (DEQUANT_RT tilings)
@@ -988,7 +1016,9 @@ class StepBuffers:
         self.act = z(B, inter)
         self.part_qkv = z(self.cfgs["qkv"].ksplit, B, (nq + 2 * nkv) * D, dtype=f32)
         self.part_o = z(self.cfgs["o"].ksplit, B, H, dtype=f32)
-        self.part_gu = z(self.cfgs["gate_up"].ksplit, B, 2 * inter, dtype=f32)
+        # (the fused SwiGLU writes act directly: no gate|up partials at prefill sizes)
+        self.part_gu = (None if self.swiglu and self.prefill else
+                        z(self.cfgs["gate_up"].ksplit, B, 2 * inter, dtype=f32))
         self.part_down = z(self.cfgs["down"].ksplit, B, H, dtype=f32)
         ks_lm = self.cfgs["lm_head"].ksplit
         S = self.num_splits

@@ -483,3 +483,43 @@ def test_fused_swiglu_every_tiling(fmt, m):
                                     _lib.BF16, st), "silu_mul")
     assert rel_err(act2, ref) <= 1e-2
     print(f"\n[swiglu {fmt} M={m}: {len(cands)} tilings ok]")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["bf16", "w4"])
+@pytest.mark.parametrize("m", [1100, 2048])
+def test_fused_swiglu_at_prefill_sizes(fmt, m):
+    """gate|up + SwiGLU at prefill sizes (the large-M kernel's epilogue; int4
+    dequantised onto it): bit for bit the one-split fp32 output of the same
+    kernel through silu_mul, and within 1e-2 of the oracle's separate
+    projections + activation. inter = 1088: the last 256-row weight tile is
+    half full; 1100 rows leave a ragged last M tile."""
+    from acorninfer_amd import _lib
+    from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, lib, ptr, stream_ptr
+    from acorninfer_amd.models.qwen3 import DENSE_RT, DEQUANT_RT, QLinear
+    from acorninfer_amd.ops.quant_gemm import Tiling
+    inter, k = 1088, 1024
+    g = torch.Generator().manual_seed(37)
+    w = (0.02 * torch.randn(2 * inter, k, generator=g)).bfloat16().cuda()
+    lin = QLinear.from_dense(w, {"bf16": WFMT_BF16, "w4": WFMT_W4}[fmt]).interleaved()
+    deq = lin.dense()
+    x = torch.randn(m, k, generator=g).bfloat16().cuda()
+    ref = _swiglu_ref(x, deq[:inter], deq[inter:])
+    st = stream_ptr()
+    t, _ = lin.swiglu_plan(m, workspace=True)
+    assert t.rt == (DENSE_RT if fmt == "bf16" else DEQUANT_RT) and t.ksplit == 1, t
+    wtmp = torch.empty(2 * inter * k, dtype=torch.bfloat16, device="cuda")
+    act = torch.full((m, inter), float("nan"), dtype=torch.bfloat16, device="cuda")
+    lin.launch_swiglu(x, m, t, act, st, wtmp=wtmp)
+    # the unfused route on the same kernel: one fp32 plane -> silu_mul(il16)
+    tp = Tiling(t.rt, t.upw, t.nw, 1, t.tpw)
+    part = torch.empty(1, m, 2 * inter, device="cuda")
+    lin.launch(x, m, tp, part=part, wtmp=wtmp, stream=st)
+    act2 = torch.empty(m, inter, dtype=torch.bfloat16, device="cuda")
+    _lib.check(lib().acorn_silu_mul(ptr(part), 1, None, ptr(act2), m, inter, 1, _lib.BF16, st),
+               "silu_mul")
+    torch.cuda.synchronize()
+    assert torch.equal(act, act2)
+    r = rel_err(act, ref)
+    print(f"\n[swiglu {fmt} M={m} at prefill size: rel err {r:.3g}]")
+    assert r <= 1e-2
