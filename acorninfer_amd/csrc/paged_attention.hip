@@ -1223,9 +1223,11 @@ int dispatch_d(int64_t D, int64_t rep, const void* q, const void* kp, const void
 //    workgroup stages in LDS once (K and V rows, coalesced 16-byte loads, two
 //    buffers, one barrier per chunk); the next chunk's loads are in flight
 //    while the current one is consumed, and its page ids one chunk earlier;
-//  * per 16 keys and query block: D/32 v_mfma_f32_16x16x32 for the scores,
+//  * per 32 keys and query block: 2 D/32 v_mfma_f32_16x16x32 for the scores,
 //    the online softmax per query column (lazy max), D/16
-//    v_mfma_f32_16x16x16 for P V; blocks whose queries all precede the keys
+//    v_mfma_f32_16x16x32 for P V (the scores of the two 16-key halves are its
+//    B operand as they lie; 16x16x16 runs at half the rate on gfx950); blocks
+//    whose queries all precede the keys
 //    skip them; keys past a query's position are masked where a chunk
 //    crosses the diagonal, and the first chunk holds key 0, so every
 //    column's max is finite from the start; rows past the last key re-read
@@ -1248,6 +1250,7 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
   constexpr int PPT = 2 * KC * RP / NT;          // pieces per thread per chunk
   constexpr int WQ = QG * QW * 16;               // query rows per workgroup
   static_assert(2 * KC * RP % NT == 0 && PPT >= 1, "whole pieces per thread");
+  static_assert(KC == 32, "a chunk is the 32 keys of one P V MFMA");
   __shared__ __align__(16) uint8_t kvs[2][2 * KC * PITCH];   // [buffer][K rows | V rows]
   const int kvh = blockIdx.y, n = blockIdx.z;
   const int tid = threadIdx.x;
@@ -1324,33 +1327,47 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) acc[qw][jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
-  // one 16-key sub-chunk at LDS rows [16 ss, 16 ss + 16) of buffer b, keys from t0
-  auto consume = [&](int b, int ss, int t0) {
-    const uint8_t* kbuf = kvs[b] + 16 * ss * PITCH;
-    const uint8_t* vbuf = kvs[b] + KC * PITCH + 16 * ss * PITCH;
-    u32x4_t kf[KB];
+  // one 32-key chunk of buffer b, keys from t0: the scores of its two 16-key
+  // halves (S^T = K Q^T, lane (r, c) holds keys 4 r .. 4 r + 3 of each half
+  // for query c) are exactly the B operand of one v_mfma_f32_16x16x32 for
+  // P V when the MFMA's k slot s of lane group r stands for key 4 r + s
+  // (s < 4) or 16 + 4 r + s - 4 (half 1); the V^T operand follows the same
+  // key order, so P never moves between lanes
+  auto consume = [&](int b, int t0) {
+    const uint8_t* kbuf = kvs[b];
+    const uint8_t* vbuf = kvs[b] + KC * PITCH;
+    u32x4_t kf[2][KB];
 #pragma unroll
-    for (int jb = 0; jb < KB; ++jb)
-      kf[jb] = *(const u32x4_t*)(kbuf + c * PITCH + 2 * (32 * jb + 8 * r));
-    u32x2_t pb[QW];
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int jb = 0; jb < KB; ++jb)
+        kf[hh][jb] = *(const u32x4_t*)(kbuf + (16 * hh + c) * PITCH + 2 * (32 * jb + 8 * r));
+    u32x4_t pb[QW];
     bool live[QW];
 #pragma unroll
     for (int qw = 0; qw < QW; ++qw) {
       // the block's queries all precede these keys, or it has none: nothing to add
       live[qw] = 16 * qw < nvalid && t0 <= pos0 + j0 + min(16 * qw + 15, nvalid - 1);
       if (!live[qw]) continue;
-      f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+      float sv[8];
 #pragma unroll
-      for (int jb = 0; jb < KB; ++jb) sc = mfma16x16x32<T>(kf[jb], qb[qw][jb], sc);
-      float sv[4];
+      for (int hh = 0; hh < 2; ++hh) {
+        f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sv[i] = sc[i] * scale_log2;
-      if (t0 + 15 > pos0 + j0 + 16 * qw) {     // the sub-chunk crosses some column's diagonal
+        for (int jb = 0; jb < KB; ++jb) sc = mfma16x16x32<T>(kf[hh][jb], qb[qw][jb], sc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (t0 + 4 * r + i > pc[qw]) sv[i] = -INFINITY;
+        for (int i = 0; i < 4; ++i) sv[4 * hh + i] = sc[i] * scale_log2;
       }
-      float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+      if (t0 + KC - 1 > pos0 + j0 + 16 * qw) {   // the chunk crosses some column's diagonal
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (t0 + 16 * hh + 4 * r + i > pc[qw]) sv[4 * hh + i] = -INFINITY;
+      }
+      float mx = sv[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
       if (__builtin_amdgcn_ballot_w64(mx > m[qw] + kMaxSlack) != 0) {
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -1361,28 +1378,33 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) acc[qw][jj] *= alpha;
       }
-      float pr[4];
+      float pr[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 8; ++i) {
         pr[i] = round_to<T>(__builtin_amdgcn_exp2f(sv[i] - m[qw]));
         l[qw] += pr[i];
       }
-      pb[qw] = u32x2_t{pack2<T>(pr[0], pr[1]), pack2<T>(pr[2], pr[3])};
+      pb[qw] = u32x4_t{pack2<T>(pr[0], pr[1]), pack2<T>(pr[2], pr[3]), pack2<T>(pr[4], pr[5]),
+                       pack2<T>(pr[6], pr[7])};
     }
     if (!live[0] && !live[QW - 1]) return;
-    // lane (r, c): V rows 4 r .. 4 r + 3, dims [DPL c, DPL c + DPL)
-    uint32_t vr[4][VW];
+    // lane (r, c): V rows 4 r .. 4 r + 3 of each half, dims [DPL c, DPL c + DPL)
+    uint32_t vr[8][VW];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-      __builtin_memcpy(vr[jj], vbuf + (4 * r + jj) * PITCH + 2 * DPL * c, sizeof(vr[jj]));
+    for (int jj = 0; jj < 8; ++jj)
+      __builtin_memcpy(vr[jj], vbuf + (16 * (jj >> 2) + 4 * r + (jj & 3)) * PITCH + 2 * DPL * c,
+                       sizeof(vr[jj]));
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) {
       const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
-      const u32x2_t va = {__builtin_amdgcn_perm(vr[1][jj / 2], vr[0][jj / 2], sel),
-                          __builtin_amdgcn_perm(vr[3][jj / 2], vr[2][jj / 2], sel)};
+      const int e = jj / 2;
+      const u32x4_t va = {__builtin_amdgcn_perm(vr[1][e], vr[0][e], sel),
+                          __builtin_amdgcn_perm(vr[3][e], vr[2][e], sel),
+                          __builtin_amdgcn_perm(vr[5][e], vr[4][e], sel),
+                          __builtin_amdgcn_perm(vr[7][e], vr[6][e], sel)};
 #pragma unroll
       for (int qw = 0; qw < QW; ++qw)
-        if (live[qw]) acc[qw][jj] = mfma16x16x16<T>(va, pb[qw], acc[qw][jj]);
+        if (live[qw]) acc[qw][jj] = mfma16x16x32<T>(va, pb[qw], acc[qw][jj]);
     }
   };
 
@@ -1401,10 +1423,7 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
 #pragma unroll
     for (int i = 0; i < PPT; ++i) pg[i] = page_of(min(ci + 2, nchunks - 1), i);
     __builtin_amdgcn_sched_barrier(0);
-    if (nvalid > 0) {
-#pragma unroll
-      for (int ss = 0; ss < KC / 16; ++ss) consume(b, ss, ci * KC + 16 * ss);
-    }
+    if (nvalid > 0) consume(b, ci * KC);
     __builtin_amdgcn_sched_barrier(0);
     store_chunk(b ^ 1);                         // chunk ci + 1 (its buffer was last read in ci - 1)
     __builtin_amdgcn_sched_barrier(0);
