@@ -48,14 +48,14 @@ __device__ __forceinline__ void norm_rope_cs(float (&x1)[NP], float (&x2)[NP], i
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
-    const int i = threadIdx.x + j * kWave;
+    const int i = (threadIdx.x & (kWave - 1)) + j * kWave;
     if (i < half) ss += x1[j] * x1[j] + x2[j] * x2[j];
   }
   ss = wave_sum(ss);
   const float inv = 1.0f / sqrtf(ss / (float)(2 * half) + eps);
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
-    const int i = threadIdx.x + j * kWave;
+    const int i = (threadIdx.x & (kWave - 1)) + j * kWave;
     if (i < half) {
       x1[j] = round_to<T>((x1[j] * inv) * w1[j]);
       x2[j] = round_to<T>((x2[j] * inv) * w2[j]);

@@ -84,14 +84,17 @@ __global__ __launch_bounds__(kWave) void qknorm_rope_kernel(
 
 // Decode-step epilogue of the fused qkv projection. Rows per batch entry:
 // [0, H) q heads, [H, H+KV) k heads, [H+KV, H+2KV) v heads. One wavefront per
-// row; lane pairs (i, i + half), NP per lane. Everything the row needs (the
-// first kSplitBatch split partials of each element, the norm weights, the
-// frequencies, the position and the page slot) is requested before any of it
-// is used: one memory round trip. Indices past the row re-read its last pair
-// (unconditional loads keep the wait counts static); those lanes store
-// nothing. Partials are added in split order, as acorn::sum_splits does.
-template <typename T, typename TW, int NP>
-__global__ __launch_bounds__(kWave) void qkv_epilogue_kernel(
+// row, kEpiWaves rows per workgroup; lane pairs (i, i + half), NP per lane.
+// Everything the row needs (the first kSplitBatch split partials of each
+// element, the norm weights, the frequencies, the position and the page slot)
+// is requested before any of it is used: one memory round trip (ONE: the
+// partials are one plane, requested once). Indices past the row re-read its
+// last pair (unconditional loads keep the wait counts static); those lanes
+// store nothing. Partials are added in split order, as acorn::sum_splits does.
+constexpr int kEpiWaves = 4;
+
+template <typename T, typename TW, int NP, bool ONE>
+__global__ __launch_bounds__(kEpiWaves * kWave) void qkv_epilogue_kernel(
     const float* __restrict__ part, int nsplit, T* __restrict__ q_out,
     T* __restrict__ k_pages, T* __restrict__ v_pages, const int64_t* __restrict__ pages,
     const int64_t* __restrict__ slots, int batch, int H, int KV, int D, int P,
@@ -99,20 +102,24 @@ __global__ __launch_bounds__(kWave) void qkv_epilogue_kernel(
     const int64_t* __restrict__ pos, const float* __restrict__ inv_freq) {
 #pragma clang fp contract(off)
   const int rows_per_b = H + 2 * KV;
-  const int b = blockIdx.x / rows_per_b;
-  const int h = blockIdx.x % rows_per_b;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * kEpiWaves + (int)(threadIdx.x / kWave);
+  if (row >= batch * rows_per_b) return;      // whole waves
+  const int b = row / rows_per_b;
+  const int h = row % rows_per_b;
   const int half = D / 2;
   const size_t width = (size_t)rows_per_b * D;
   const size_t plane = (size_t)batch * width;
   const float* src = part + (size_t)b * width + (size_t)h * D;
   const TW* w = h < H ? q_w : k_w;  // v rows load them too, unused
   // ---- requests ----
-  float pa[NP][kSplitBatch], pc[NP][kSplitBatch], w1[NP], w2[NP], fr[NP];
+  constexpr int NB = ONE ? 1 : kSplitBatch;
+  float pa[NP][NB], pc[NP][NB], w1[NP], w2[NP], fr[NP];
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
-    const int ic = min(threadIdx.x + j * kWave, half - 1);
+    const int ic = min(lane + j * kWave, half - 1);
 #pragma unroll
-    for (int u = 0; u < kSplitBatch; ++u) {
+    for (int u = 0; u < NB; ++u) {
       const float* p = src + (size_t)min(u, nsplit - 1) * plane + ic;
       pa[j][u] = p[0];
       pc[j][u] = p[half];
@@ -129,14 +136,14 @@ __global__ __launch_bounds__(kWave) void qkv_epilogue_kernel(
   for (int j = 0; j < NP; ++j) {
     float a = pa[j][0], c = pc[j][0];
 #pragma unroll
-    for (int u = 1; u < kSplitBatch; ++u) {
+    for (int u = 1; u < NB; ++u) {
       if (u < nsplit) {
         a = a + pa[j][u];
         c = c + pc[j][u];
       }
     }
-    const int ic = min(threadIdx.x + j * kWave, half - 1);
-    for (int sp = kSplitBatch; sp < nsplit; ++sp) {
+    const int ic = min(lane + j * kWave, half - 1);
+    for (int sp = NB; sp < nsplit; ++sp) {
       const float* q = src + (size_t)sp * plane + ic;
       a = a + q[0];
       c = c + q[half];
@@ -162,7 +169,7 @@ __global__ __launch_bounds__(kWave) void qkv_epilogue_kernel(
   }
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
-    const int i = threadIdx.x + j * kWave;
+    const int i = lane + j * kWave;
     if (dst && i < half) {
       dst[i] = from_f32<T>(x1[j]);
       dst[i + half] = from_f32<T>(x2[j]);
@@ -204,8 +211,12 @@ int launch_qkv(const float* part, int64_t nsplit, void* q_out, void* kp, void* v
                const int64_t* pages, const int64_t* slots, int64_t batch, int64_t H, int64_t KV,
                int64_t D, int64_t P, int64_t NB, const void* qw, const void* kw, float eps,
                const int64_t* pos, const float* inv_freq, hipStream_t st) {
-  dim3 grid((unsigned)(batch * (H + 2 * KV))), block(kWave);
-  auto kfn = D <= 2 * kWave ? qkv_epilogue_kernel<T, TW, 1> : qkv_epilogue_kernel<T, TW, kMaxPairs>;
+  const int64_t rows = batch * (H + 2 * KV);
+  dim3 grid((unsigned)((rows + kEpiWaves - 1) / kEpiWaves)), block(kEpiWaves * kWave);
+  auto kfn = D <= 2 * kWave ? (nsplit == 1 ? qkv_epilogue_kernel<T, TW, 1, true>
+                                           : qkv_epilogue_kernel<T, TW, 1, false>)
+                            : (nsplit == 1 ? qkv_epilogue_kernel<T, TW, kMaxPairs, true>
+                                           : qkv_epilogue_kernel<T, TW, kMaxPairs, false>);
   kfn<<<grid, block, 0, st>>>(
       part, (int)nsplit, (T*)q_out, (T*)kp, (T*)vp, pages, slots, (int)batch, (int)H, (int)KV,
       (int)D, (int)P, NB, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
