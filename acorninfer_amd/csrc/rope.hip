@@ -177,6 +177,67 @@ __global__ __launch_bounds__(kEpiWaves * kWave) void qkv_epilogue_kernel(
   }
 }
 
+// Prefill sizes (one split, head_dim 128): one wavefront per token row, lane
+// i owning pair (i, i + 64) of every head, so the row's cos/sin (the same for
+// all of its q and k heads) are computed once per row instead of once per
+// head; the heads' partials are requested 8 heads at a time. The same
+// arithmetic as qkv_epilogue_kernel, so the same bits.
+constexpr int kRowHeads = 8;
+constexpr int64_t kEpiRowsMin = 256;   // token rows from which the row form is used
+
+template <typename T, typename TW>
+__global__ __launch_bounds__(kEpiWaves * kWave) void qkv_epilogue_rows_kernel(
+    const float* __restrict__ part, T* __restrict__ q_out, T* __restrict__ k_pages,
+    T* __restrict__ v_pages, const int64_t* __restrict__ pages,
+    const int64_t* __restrict__ slots, int batch, int H, int KV, int P, int64_t num_blocks,
+    const TW* __restrict__ q_w, const TW* __restrict__ k_w, float eps,
+    const int64_t* __restrict__ pos, const float* __restrict__ inv_freq) {
+#pragma clang fp contract(off)
+  constexpr int D = 128, HALF = 64;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int b = blockIdx.x * kEpiWaves + (int)(threadIdx.x / kWave);
+  if (b >= batch) return;                     // whole waves
+  const int NH = H + 2 * KV;
+  const float* src = part + (size_t)b * NH * D + lane;
+  float cs[1], sn[1];
+  rope_cs<T>((float)pos[b], inv_freq[lane], cs[0], sn[0]);
+  const float qw1[1] = {to_f32(q_w[lane])}, qw2[1] = {to_f32(q_w[lane + HALF])};
+  const float kw1[1] = {to_f32(k_w[lane])}, kw2[1] = {to_f32(k_w[lane + HALF])};
+  const uint64_t page = (uint64_t)pages[b], slot = (uint64_t)slots[b];
+  // a (page, slot) outside the pool is dropped rather than written
+  const bool in_pool = page < (uint64_t)num_blocks && slot < (uint64_t)P;
+  const size_t kv_off = in_pool ? (page * P + slot) * KV * D : 0;
+  for (int h0 = 0; h0 < NH; h0 += kRowHeads) {
+    float a[kRowHeads], c[kRowHeads];
+#pragma unroll
+    for (int u = 0; u < kRowHeads; ++u) {
+      const float* p = src + (size_t)min(h0 + u, NH - 1) * D;
+      a[u] = p[0];
+      c[u] = p[HALF];
+    }
+#pragma unroll
+    for (int u = 0; u < kRowHeads; ++u) {
+      const int h = h0 + u;
+      if (h >= NH) break;                       // uniform
+      float x1[1] = {round_to<T>(a[u])}, x2[1] = {round_to<T>(c[u])};
+      T* dst;
+      if (h < H) {
+        norm_rope_cs<T, 1>(x1, x2, HALF, qw1, qw2, eps, cs, sn);
+        dst = q_out + ((size_t)b * H + h) * D;
+      } else if (h < H + KV) {
+        norm_rope_cs<T, 1>(x1, x2, HALF, kw1, kw2, eps, cs, sn);
+        dst = in_pool ? k_pages + kv_off + (size_t)(h - H) * D : nullptr;
+      } else {
+        dst = in_pool ? v_pages + kv_off + (size_t)(h - H - KV) * D : nullptr;
+      }
+      if (dst) {
+        dst[lane] = from_f32<T>(x1[0]);
+        dst[lane + HALF] = from_f32<T>(x2[0]);
+      }
+    }
+  }
+}
+
 bool head_dim_ok(int64_t D) { return D >= 2 && D <= 2 * kMaxPairs * kWave && (D & (D - 1)) == 0; }
 
 template <typename T>
@@ -211,6 +272,14 @@ int launch_qkv(const float* part, int64_t nsplit, void* q_out, void* kp, void* v
                const int64_t* pages, const int64_t* slots, int64_t batch, int64_t H, int64_t KV,
                int64_t D, int64_t P, int64_t NB, const void* qw, const void* kw, float eps,
                const int64_t* pos, const float* inv_freq, hipStream_t st) {
+  if (nsplit == 1 && D == 128 && batch >= kEpiRowsMin) {
+    qkv_epilogue_rows_kernel<T, TW>
+        <<<dim3((unsigned)((batch + kEpiWaves - 1) / kEpiWaves)), dim3(kEpiWaves * kWave), 0,
+           st>>>(part, (T*)q_out, (T*)kp, (T*)vp, pages, slots, (int)batch, (int)H, (int)KV,
+                 (int)P, NB, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
+    ACORN_LAUNCH_CHECK();
+    return ACORN_OK;
+  }
   const int64_t rows = batch * (H + 2 * KV);
   dim3 grid((unsigned)((rows + kEpiWaves - 1) / kEpiWaves)), block(kEpiWaves * kWave);
   auto kfn = D <= 2 * kWave ? (nsplit == 1 ? qkv_epilogue_kernel<T, TW, 1, true>

@@ -126,3 +126,61 @@ def test_fused_rejects_unsupported_without_launching():
                                      None, None, _lib.BF16, _lib.BF16, None)
     with pytest.raises(NotImplementedError):
         _lib.check(rc, "K3+epilogue")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_qkv_epilogue_row_form_equals_per_head_form(dtype):
+    """At prefill sizes (256+ rows, one split, head_dim 128) the qkv epilogue
+    runs one wave per token row (cos/sin once per row); below, one wave per
+    (row, head). 300 rows in one call against the same rows as two calls of
+    150: the same q bits and pool bits, and q against the oracle's norm + RoPE
+    (positions up to 8191, where the angles are largest). Rows 7 and 200 carry
+    a page outside the pool: nothing is written for them."""
+    B, H, KV, D, P = 300, 32, 8, 128, 16
+    eps = 1e-6
+    g = torch.Generator().manual_seed(91)
+    nb = B // P + 4
+    width = (H + 2 * KV) * D
+    part = torch.randn(1, B, width, generator=g) * 0.5
+    q_w = (1.0 + 0.2 * torch.randn(D, generator=g)).to(dtype)
+    k_w = (1.0 + 0.2 * torch.randn(D, generator=g)).to(dtype)
+    pos = torch.randint(0, 8192, (B,), generator=g, dtype=torch.int64)
+    pages = torch.randperm(nb, generator=g)[:B // P + 1].repeat_interleave(P)[:B].clone()
+    slots = torch.arange(B, dtype=torch.int64) % P
+    pages[7] = nb + 5
+    pages[200] = -1
+    inv_freq = inv_freq_ref(D, 1e6).float()
+    L = _lib.lib()
+    ptr, dt = _lib.ptr, _lib.dtype_code(torch.empty(0, dtype=dtype))
+    dev = torch.device("cuda:0")
+    st = _lib.stream_ptr(dev)
+    part_d, qw_d, kw_d = part.to(dev), q_w.to(dev), k_w.to(dev)
+    pos_d, pg_d, sl_d, fr_d = pos.to(dev), pages.to(dev), slots.to(dev), inv_freq.to(dev)
+    pools = []
+    outs = []
+    for chunks in ((0, B), (0, 150, B)):
+        kp = torch.full((nb, P, KV, D), 7.0, dtype=dtype, device=dev)
+        vp = torch.full((nb, P, KV, D), 7.0, dtype=dtype, device=dev)
+        q = torch.empty(B, H, D, dtype=dtype, device=dev)
+        for a, b in zip(chunks[:-1], chunks[1:]):
+            n = b - a
+            _lib.check(L.acorn_qkv_epilogue(
+                ptr(part_d[:, a:b].contiguous()), 1, ptr(q[a:b]), ptr(kp), ptr(vp),
+                ptr(pg_d[a:b]), ptr(sl_d[a:b]), n, H, KV, D, P, nb, ptr(qw_d), ptr(kw_d), eps,
+                ptr(pos_d[a:b]), ptr(fr_d), dt, dt, st), "qkv_epilogue")
+        torch.cuda.synchronize()
+        outs.append(q.cpu())
+        pools.append((kp.cpu(), vp.cpu()))
+    iv = torch.int16 if dtype != torch.float32 else torch.int32
+    assert torch.equal(outs[0].view(iv), outs[1].view(iv))
+    for a, b in zip(pools[0], pools[1]):
+        assert torch.equal(a.view(iv), b.view(iv))
+    x = part[0].to(dtype).view(B, H + 2 * KV, D)
+    qn, _ = qknorm_rope_ref(x[:, :H, None, :], x[:, H:H + KV, None, :], q_w, k_w, eps, pos,
+                            inv_freq)
+    tol = TOL_BF16 if dtype != torch.float32 else dict(rtol=1e-5, atol=1e-5)
+    assert torch.allclose(outs[0].float(), qn[:, :, 0].float(), **tol)
+    # the rows with a page outside the pool wrote nothing; the others did
+    kp0 = pools[0][0]
+    assert bool((kp0 == 7.0).sum() == (nb * P - (B - 2)) * KV * D)
