@@ -28,7 +28,7 @@
 // follow, both operands in LDS and two waves per SIMD: one stages through
 // registers (1.0-1.06 PFLOP/s at M = 2048-8192), the other loads straight
 // into LDS (global_load_lds) through a 4-stage ring, the planner's default
-// from 1024 rows (1.09-1.26 PFLOP/s at M = 8192; hipBLASLt: 1.3-1.4).
+// from 512 rows (1.19-1.28 PFLOP/s at M = 8192; hipBLASLt: 1.3-1.5).
 #include <hip/hip_runtime.h>
 
 #include "acorn_hip.h"

@@ -821,7 +821,7 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
 // this many rows on, or on request (rt == kDenseRT).
 constexpr int kDenseRT = -2;
 constexpr int64_t kDenseMinM = 512;
-constexpr int64_t kDenseLdsM = 1024;
+constexpr int64_t kDenseLdsM = 512;
 // W4B above 16 rows on request (rt == kMidRT): the mid-M int4 kernel
 constexpr int kMidRT = -3;
 

@@ -61,8 +61,9 @@ LIBRARY_RT = -1
 DEQUANT_M_MIN = 1024
 DEQUANT_RT = -4
 # prefill blocks from this many rows run gate|up with the large-M kernel's
-# SwiGLU epilogue (act written directly: no fp32 gate|up output, no silu_mul)
-PREFILL_SWIGLU_M = 1024
+# SwiGLU epilogue (act written directly: no fp32 gate|up output, no silu_mul);
+# int4 weights once they take the dequantise route
+PREFILL_SWIGLU_M = 512
 
 
 def dispatch_linear(mod, x: torch.Tensor) -> torch.Tensor:
@@ -559,10 +560,12 @@ class Qwen3DecodeModel:
 
     def prefill_swiglu(self, rows: int) -> bool:
         """A prefill block of `rows` runs gate|up with the SwiGLU epilogue of
-        the large-M bf16 kernel (bf16 weights, or int4 dequantised onto it):
-        from PREFILL_SWIGLU_M rows, gate|up in the 16-row interleave."""
+        the large-M bf16 kernel (bf16 weights from PREFILL_SWIGLU_M rows, int4
+        dequantised onto it from DEQUANT_M_MIN), gate|up in the 16-row
+        interleave."""
         gu = self.layers[0].gate_up
-        return gu.il16 and rows >= PREFILL_SWIGLU_M and gu.fmt in (WFMT_BF16, WFMT_W4B)
+        return gu.il16 and rows >= PREFILL_SWIGLU_M and (
+            gu.fmt == WFMT_BF16 or (gu.fmt == WFMT_W4B and rows >= DEQUANT_M_MIN))
 
     def fused_swiglu(self, batch: int) -> bool:
         """The gate|up launch carries the SwiGLU epilogue (decode sizes, and

@@ -84,9 +84,12 @@ class Tiling(NamedTuple):
     (1 / 2), nw waves (4 / 8), ksplit, tpw 128-k groups in flight (2 / 4);
     64 x rows per workgroup, streamed through LDS a group at a time.
     Large-M bf16 kernel (the default for bf16 from 512 rows, or rt == -2):
-    upw is the M tile (64 / 128), nw the weight rows per wave (64 / 128; a
+    upw is the M tile. 64 / 128: nw the weight rows per wave (64 / 128; a
     workgroup's weight tile is 4 nw), tpw the weight prefetch depth in 64-k
-    steps (2 / 4); reported as (-2, BM, rows per wave, 1, depth).
+    steps (2 / 4). 256 (256 x 256 tiles): nw 64 with tpw 2 stages both
+    operands through registers; nw 128 with tpw 4 loads them straight into
+    LDS through a 4-stage ring (the default). Reported as (-2, BM, nw,
+    ksplit, tpw).
     """
     rt: int = 0
     upw: int = 0

@@ -255,7 +255,7 @@ int acorn_quant_gemm(const void* x, const void* w, const void* scale, const void
  * rows of the same outputs (scales / zeros interleaved the same way); N is
  * the interleaved row count (2 * intermediate), act is [M, N/2] bf16.
  * Decode sizes (M <= 16; cfg as for acorn_quant_gemm, rt is 2 and ksplit 1
- * by construction), and bf16 weights at prefill sizes (from 1024 rows, or
+ * by construction), and bf16 weights at prefill sizes (from 512 rows, or
  * cfg[0] == -2: the large-M kernel's 256 x 256 direct-to-LDS form, ksplit 1,
  * N % 32 == 0), where the act is bitwise what acorn_silu_mul gives on the
  * one-split fp32 output.

@@ -54,11 +54,13 @@ def _run(x, w, tiling, fp32):
 def test_planner_routes_prefill_sizes_to_the_dense_kernel():
     from acorninfer_amd._lib import WFMT_BF16, WFMT_W8
     from acorninfer_amd.ops.quant_gemm import Tiling, plan
+    # from 512 rows: 256 x 256 tiles, both operands by direct-to-LDS loads,
+    # split K while the tiles (16 x 2 here) leave CUs idle
     t, tiles = plan(512, 4096, 4096, WFMT_BF16)
-    assert t == Tiling(DENSE_RT, 128, 64, 4, 4) and tiles == 16 * 4   # 64 tiles x 4 splits
-    assert plan(1023, 4096, 4096, WFMT_BF16)[0].upw == 128
-    # from 1024 rows: 256 x 256 tiles, both operands by direct-to-LDS loads
+    assert t == Tiling(DENSE_RT, 256, 128, 8, 4) and tiles == 16 * 2
     assert plan(8192, 4096, 4096, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 1, 4)
+    assert plan(512, 4096, 4096, WFMT_BF16, Tiling(DENSE_RT, 128))[0] == \
+        Tiling(DENSE_RT, 128, 64, 4, 4)                              # the 128-row form
     assert plan(8192, 4096, 4096, WFMT_BF16, Tiling(DENSE_RT, 256, 64))[0] == \
         Tiling(DENSE_RT, 256, 64, 1, 2)                              # register-staged form
     assert plan(511, 4096, 4096, WFMT_BF16)[0].rt != DENSE_RT       # tiled kernel below 512
