@@ -828,8 +828,10 @@ def main() -> None:
     ap.add_argument("--splits", default="",
                     help="with --mode attention: comma-separated K3 split counts to time")
     ap.add_argument("--mode", default="full",
-                    choices=["full", "step", "attention", "kernels", "copy"],
+                    choices=["full", "step", "attention", "kernels", "copy", "prefill"],
                     help="profiling workloads: 'step' = decode steps only (no JSON line), "
+                         "'prefill' = --batch prompts of --prompt-len random ids prefilled "
+                         "(one warm-up call, --steps timed calls; no JSON line), "
                          "'attention' = K3 at configuration 2 only, 'kernels' = the isolated "
                          "kernels only (configurations 2, 3, 5), 'copy' = the 1 GiB "
                          "copy that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE")
@@ -874,6 +876,14 @@ def main() -> None:
     cfg = Qwen3Config.qwen3_8b()
     if args.layers:
         cfg = cfg.with_layers(args.layers)
+    if args.mode == "prefill":
+        from acorninfer_amd.models.qwen3 import Qwen3DecodeModel
+        model = Qwen3DecodeModel.random_init(cfg, weight_format=args.format, device="cuda:0")
+        ms_p, tps = prefill_benchmark(model, cfg, args.batch, args.prompt_len, args.seed,
+                                      reps=args.steps)
+        _log(f"{args.format} prefill {args.batch} x {args.prompt_len}: {ms_p:.2f} ms "
+             f"({tps:.0f} prompt tok/s)")
+        return
     total = args.warmup + args.steps
     # room for the decode_batch protocol's steps after the timed decode_loop ones
     model, cache, runner, views, first = build_workload(
