@@ -1219,7 +1219,7 @@ int dispatch_d(int64_t D, int64_t rep, const void* q, const void* kp, const void
 //  * a workgroup serves the REP q heads of one kv head for QG x 32 query
 //    tokens: wave (head, group) owns two 16-token query blocks (QW = 2), so
 //    every K / V operand it reads feeds two MFMAs;
-//  * the kv head's keys are walked in chunks of 32 tokens that the whole
+//  * the kv head's keys are walked in chunks of 64 tokens that the whole
 //    workgroup stages in LDS once (K and V rows, coalesced 16-byte loads, two
 //    buffers, one barrier per chunk); the next chunk's loads are in flight
 //    while the current one is consumed, and its page ids one chunk earlier;
@@ -1250,7 +1250,7 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
   constexpr int PPT = 2 * KC * RP / NT;          // pieces per thread per chunk
   constexpr int WQ = QG * QW * 16;               // query rows per workgroup
   static_assert(2 * KC * RP % NT == 0 && PPT >= 1, "whole pieces per thread");
-  static_assert(KC == 32, "a chunk is the 32 keys of one P V MFMA");
+  static_assert(KC % 32 == 0, "a chunk is whole 32-key P V MFMAs");
   __shared__ __align__(16) uint8_t kvs[2][2 * KC * PITCH];   // [buffer][K rows | V rows]
   const int kvh = blockIdx.y, n = blockIdx.z;
   const int tid = threadIdx.x;
@@ -1333,9 +1333,9 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
   // P V when the MFMA's k slot s of lane group r stands for key 4 r + s
   // (s < 4) or 16 + 4 r + s - 4 (half 1); the V^T operand follows the same
   // key order, so P never moves between lanes
-  auto consume = [&](int b, int t0) {
-    const uint8_t* kbuf = kvs[b];
-    const uint8_t* vbuf = kvs[b] + KC * PITCH;
+  auto consume = [&](int b, int sub, int t0) {
+    const uint8_t* kbuf = kvs[b] + 32 * sub * PITCH;
+    const uint8_t* vbuf = kvs[b] + KC * PITCH + 32 * sub * PITCH;
     u32x4_t kf[2][KB];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
@@ -1358,7 +1358,7 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[4 * hh + i] = sc[i] * scale_log2;
       }
-      if (t0 + KC - 1 > pos0 + j0 + 16 * qw) {   // the chunk crosses some column's diagonal
+      if (t0 + 31 > pos0 + j0 + 16 * qw) {       // the keys cross some column's diagonal
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
@@ -1423,7 +1423,10 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
 #pragma unroll
     for (int i = 0; i < PPT; ++i) pg[i] = page_of(min(ci + 2, nchunks - 1), i);
     __builtin_amdgcn_sched_barrier(0);
-    if (nvalid > 0) consume(b, ci * KC);
+    if (nvalid > 0) {
+#pragma unroll
+      for (int sub = 0; sub < KC / 32; ++sub) consume(b, sub, ci * KC + 32 * sub);
+    }
     __builtin_amdgcn_sched_barrier(0);
     store_chunk(b ^ 1);                         // chunk ci + 1 (its buffer was last read in ci - 1)
     __builtin_amdgcn_sched_barrier(0);
@@ -1452,7 +1455,7 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
   }
 }
 
-constexpr int kPrefillChunk = 32;   // keys staged per barrier (64 measured no faster)
+constexpr int kPrefillChunk = 64;   // keys staged per barrier (32: 3% slower at 8192 tokens)
 
 template <typename T, int D, int REP>
 int launch_prefill(const void* q, const void* kp, const void* vp, const int32_t* tables,
