@@ -828,10 +828,11 @@ def main() -> None:
     ap.add_argument("--splits", default="",
                     help="with --mode attention: comma-separated K3 split counts to time")
     ap.add_argument("--mode", default="full",
-                    choices=["full", "step", "attention", "kernels", "copy", "prefill"],
+                    choices=["full", "step", "attention", "kernels", "copy", "prefill", "dense"],
                     help="profiling workloads: 'step' = decode steps only (no JSON line), "
                          "'prefill' = --batch prompts of --prompt-len random ids prefilled "
-                         "(one warm-up call, --steps timed calls; no JSON line), "
+                         "(one warm-up call, --steps timed calls; no JSON line), 'dense' = "
+                         "the large-M bf16 GEMMs at M = 512 / 2048 / 8192 against hipBLASLt, "
                          "'attention' = K3 at configuration 2 only, 'kernels' = the isolated "
                          "kernels only (configurations 2, 3, 5), 'copy' = the 1 GiB "
                          "copy that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE")
@@ -868,6 +869,9 @@ def main() -> None:
         else:
             print(json.dumps(kernel_benchmarks(gemm_ms=ms, with_attention=not args.gemm_m)),
                   flush=True)
+        return
+    if args.mode == "dense":
+        print(json.dumps(dense_gemm_benchmarks(23)), flush=True)
         return
     if args.mode == "attention":
         sweep = [int(x) for x in args.splits.split(",")] if args.splits else None
