@@ -211,29 +211,34 @@ def prefill_benchmark(model, cfg, batch: int, prompt_len: int, seed: int, reps: 
     return ms, batch * prompt_len / ms * 1e3
 
 
-def engine_benchmark(model, cfg, concurrency: int, prompt_len: int, new_tokens: int,
-                     seed: int):
-    """Configuration 4 end to end: `concurrency` greedy requests of
-    `prompt_len` random ids and `new_tokens` generated tokens each, submitted
-    at once to the Engine (continuous batching: batched prefill, then the
-    graph-captured decode step). Returns (generated tok/s over the wall time
-    of the whole run, mean time to first token in ms)."""
+def engine_benchmark(model, cfg, concurrency: int, prompt_len, new_tokens: int, seed: int,
+                     sampling=None, warm_len: int | None = None):
+    """Configurations 4 and 5 end to end: `concurrency` requests of random ids
+    (prompt_len: one length, or a list of one per request) and `new_tokens`
+    generated tokens each, submitted at once to the Engine (continuous
+    batching: batched prefill, then the graph-captured decode step); greedy
+    unless `sampling` (a SamplingParams) is given. A warm-up run with prompts
+    of `warm_len` tokens (default: the same lengths) captures the decode graph
+    first. Returns (generated tok/s over the wall time of the whole run, mean
+    time to first token in ms)."""
     import torch
 
     from acorninfer_amd.engine.engine import Engine
     from acorninfer_amd.sampler import SamplingParams
 
     P = 16
-    blocks = concurrency * -(-(prompt_len + new_tokens + 1) // P) + 8
+    lens = list(prompt_len) if isinstance(prompt_len, (list, tuple)) else [prompt_len] * concurrency
+    longest = max(lens)
+    blocks = sum(-(-(n + new_tokens + 1) // P) for n in lens) + 8
     eng = Engine(model, num_blocks=blocks, max_running=concurrency, watermark_blocks=1,
-                 max_model_len=prompt_len + new_tokens + 1, seed=seed)
+                 max_model_len=longest + new_tokens + 1, seed=seed)
     g = torch.Generator().manual_seed(seed)
-    greedy = SamplingParams(temperature=0.0)
+    sp = sampling if sampling is not None else SamplingParams(temperature=0.0)
     never = frozenset({-1})
 
-    def run(n_new):
-        ids = [eng.submit(torch.randint(0, cfg.vocab_size, (prompt_len,), generator=g).tolist(),
-                          greedy, max_tokens=n_new, eos_ids=never) for _ in range(concurrency)]
+    def run(n_new, plens):
+        ids = [eng.submit(torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist(),
+                          sp, max_tokens=n_new, eos_ids=never) for n in plens]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         while eng.has_pending():
@@ -245,8 +250,8 @@ def engine_benchmark(model, cfg, concurrency: int, prompt_len: int, new_tokens: 
             eng.drop(i)
         return dt, sum(ttft) / len(ttft)
 
-    run(4)                                    # warm-up: captures the decode graph
-    dt, ttft = run(new_tokens)
+    run(4, [warm_len] * concurrency if warm_len else lens)   # warm-up: captures the decode graph
+    dt, ttft = run(new_tokens, lens)
     eng.assert_balanced()
     return concurrency * new_tokens / dt, ttft
 
@@ -990,6 +995,22 @@ def main() -> None:
             extra[f"w4a16_C{c}_long_sampled_mean_ctx"] = round(sum(plens) / c, 1)
             _log(f"w4a16 C={c} long sampled (mean ctx {sum(plens) / c:.0f}): "
                  f"{c * args.steps / dt2:.1f} tok/s")
+            if c == 64:
+                # configuration 5 end to end through the Engine: the same 64
+                # prompt lengths prefilled, then 128 sampled tokens each
+                del c2, r2
+                torch.cuda.empty_cache()
+                e2e, ttft = engine_benchmark(m2, cfg, c, plens, 128, args.seed + 11,
+                                             sampling=SamplingParams(temperature=0.6, top_p=0.95,
+                                                                     top_k=20),
+                                             warm_len=64)
+                extra["w4a16_engine_C64_long_tok_s"] = round(e2e, 1)
+                extra["w4a16_engine_C64_long_ttft_ms"] = round(ttft, 1)
+                _log(f"w4a16 engine C=64, prompts U[1024, 8192] + 128 sampled tokens: "
+                     f"{e2e:.1f} tok/s end to end, mean TTFT {ttft:.0f} ms")
+                del m2
+                torch.cuda.empty_cache()
+                continue
             if c == 8:
                 # configuration 5's longest prompt in W4A16: one 8192-token
                 # prefill, int4 projections dequantised onto the bf16 kernel
