@@ -185,9 +185,9 @@ __global__ __launch_bounds__(kEpiWaves * kWave) void qkv_epilogue_kernel(
 constexpr int kRowHeads = 8;
 constexpr int64_t kEpiRowsMin = 256;   // token rows from which the row form is used
 
-template <typename T, typename TW>
+template <typename T, typename TW, typename PT>
 __global__ __launch_bounds__(kEpiWaves * kWave) void qkv_epilogue_rows_kernel(
-    const float* __restrict__ part, T* __restrict__ q_out, T* __restrict__ k_pages,
+    const PT* __restrict__ part, T* __restrict__ q_out, T* __restrict__ k_pages,
     T* __restrict__ v_pages, const int64_t* __restrict__ pages,
     const int64_t* __restrict__ slots, int batch, int H, int KV, int P, int64_t num_blocks,
     const TW* __restrict__ q_w, const TW* __restrict__ k_w, float eps,
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kEpiWaves * kWave) void qkv_epilogue_rows_kernel(
   const int b = blockIdx.x * kEpiWaves + (int)(threadIdx.x / kWave);
   if (b >= batch) return;                     // whole waves
   const int NH = H + 2 * KV;
-  const float* src = part + (size_t)b * NH * D + lane;
+  const PT* src = part + (size_t)b * NH * D + lane;
   float cs[1], sn[1];
   rope_cs<T>((float)pos[b], inv_freq[lane], cs[0], sn[0]);
   const float qw1[1] = {to_f32(q_w[lane])}, qw2[1] = {to_f32(q_w[lane + HALF])};
@@ -211,9 +211,9 @@ __global__ __launch_bounds__(kEpiWaves * kWave) void qkv_epilogue_rows_kernel(
     float a[kRowHeads], c[kRowHeads];
 #pragma unroll
     for (int u = 0; u < kRowHeads; ++u) {
-      const float* p = src + (size_t)min(h0 + u, NH - 1) * D;
-      a[u] = p[0];
-      c[u] = p[HALF];
+      const PT* p = src + (size_t)min(h0 + u, NH - 1) * D;
+      a[u] = to_f32(p[0]);
+      c[u] = to_f32(p[HALF]);
     }
 #pragma unroll
     for (int u = 0; u < kRowHeads; ++u) {
@@ -272,11 +272,18 @@ int launch_qkv(const float* part, int64_t nsplit, void* q_out, void* kp, void* v
                const int64_t* pages, const int64_t* slots, int64_t batch, int64_t H, int64_t KV,
                int64_t D, int64_t P, int64_t NB, const void* qw, const void* kw, float eps,
                const int64_t* pos, const float* inv_freq, hipStream_t st) {
-  if (nsplit == 1 && D == 128 && batch >= kEpiRowsMin) {
-    qkv_epilogue_rows_kernel<T, TW>
-        <<<dim3((unsigned)((batch + kEpiWaves - 1) / kEpiWaves)), dim3(kEpiWaves * kWave), 0,
-           st>>>(part, (T*)q_out, (T*)kp, (T*)vp, pages, slots, (int)batch, (int)H, (int)KV,
-                 (int)P, NB, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
+  // nsplit == 0: part holds the projection's output in T (one rounded plane)
+  if (nsplit == 0 && (D != 128 || batch < kEpiRowsMin)) return ACORN_ERR_UNSUPPORTED;
+  if (nsplit <= 1 && D == 128 && batch >= kEpiRowsMin) {
+    const dim3 grid((unsigned)((batch + kEpiWaves - 1) / kEpiWaves)), block(kEpiWaves * kWave);
+    if (nsplit == 0)
+      qkv_epilogue_rows_kernel<T, TW, T><<<grid, block, 0, st>>>(
+          (const T*)part, (T*)q_out, (T*)kp, (T*)vp, pages, slots, (int)batch, (int)H, (int)KV,
+          (int)P, NB, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
+    else
+      qkv_epilogue_rows_kernel<T, TW, float><<<grid, block, 0, st>>>(
+          part, (T*)q_out, (T*)kp, (T*)vp, pages, slots, (int)batch, (int)H, (int)KV, (int)P,
+          NB, (const TW*)qw, (const TW*)kw, eps, pos, inv_freq);
     ACORN_LAUNCH_CHECK();
     return ACORN_OK;
   }
@@ -347,7 +354,7 @@ extern "C" int acorn_qkv_epilogue(const float* part, int64_t nsplit, void* q_out
                                   const void* k_w, float eps, const int64_t* positions,
                                   const float* inv_freq, int dtype, int wdtype, void* stream) {
   if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || page_size <= 0 || num_blocks <= 0 ||
-      nsplit < 1 || !head_dim_ok(head_dim))
+      nsplit < 0 || !head_dim_ok(head_dim))
     return ACORN_ERR_SHAPE;
   if (batch == 0) return ACORN_OK;
   if (!part || !q_out || !k_pages || !v_pages || !pages || !slots || !q_w || !k_w ||

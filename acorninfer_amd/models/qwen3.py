@@ -64,6 +64,9 @@ DEQUANT_RT = -4
 # SwiGLU epilogue (act written directly: no fp32 gate|up output, no silu_mul);
 # int4 weights once they take the dequantise route
 PREFILL_SWIGLU_M = 512
+# and from this many rows (the qkv epilogue's row form) qkv / o / down write
+# the activation dtype directly when they run in one split on that kernel
+PREFILL_DIRECT_M = 256
 
 
 def dispatch_linear(mod, x: torch.Tensor) -> torch.Tensor:
@@ -349,6 +352,10 @@ class Qwen3DecodeModel:
         # (bf16 on torch.mm, i.e. hipBLASLt) or "int4" (int4 weights on the
         # int4 kernels at every size)
         self.prefill_gemm = "own"
+        # prefill blocks whose qkv / o / down run on the large-M kernel in one
+        # split take their output in the activation dtype (half the bytes of
+        # an fp32 plane, the same bits after the consumer's rounding)
+        self.prefill_direct = True
         # batch -> {projection name -> Tiling}, filled by tune()
         self.tilings: dict[int, dict] = {}
         self.swiglu_choice: dict[int, bool] = {}
@@ -470,22 +477,37 @@ class Qwen3DecodeModel:
                                 dt, st), "embedding")
         # K3 runs the qkv epilogue itself where it supports the shape (one
         # launch fewer per layer, the same bits)
-        fused_attn = fused_attn and bool(L.acorn_paged_attention_qkv_supported(
-            nq, nkv, D, page_size, buf.max_pages, buf.num_splits, dt, wdt))
-        prev_ks = 0             # splits of the previous layer's down-projection partials
-        for li, lw in enumerate(self.layers):
-            # K1: input norm (layer 0 from the embedding; later layers reduce
-            # the previous down projection's partials and add the residual)
-            if prev_ks == 0:
-                check(L.acorn_fused_add_rmsnorm(ptr(buf.x), None, ptr(buf.res), ptr(lw.input_norm),
+        fused_attn = fused_attn and not buf.direct and bool(
+            L.acorn_paged_attention_qkv_supported(nq, nkv, D, page_size, buf.max_pages,
+                                                  buf.num_splits, dt, wdt))
+
+        def k1(first: bool, y, part, ks: int, w) -> None:
+            """K1 after a projection: the residual add + RMSNorm from its
+            output in the activation dtype (y), or from its fp32 partials; the
+            first norm of the step takes the embedding as the residual."""
+            if first:
+                check(L.acorn_fused_add_rmsnorm(ptr(buf.x), None, ptr(buf.res), ptr(w),
+                                                ptr(buf.normed), B, H, eps, dt, wdt, st), "K1")
+            elif y is not None:
+                check(L.acorn_fused_add_rmsnorm(ptr(y), ptr(buf.res), ptr(buf.res), ptr(w),
                                                 ptr(buf.normed), B, H, eps, dt, wdt, st), "K1")
             else:
                 check(L.acorn_fused_add_rmsnorm_partials(
-                    ptr(buf.part_down), prev_ks, ptr(buf.res), ptr(buf.res), ptr(lw.input_norm),
-                    ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
-            # qkv projection -> fp32 partials -> K2 epilogue (+ KV scatter)
+                    ptr(part), ks, ptr(buf.res), ptr(buf.res), ptr(w), ptr(buf.normed), None, B,
+                    H, eps, dt, wdt, st), "K1")
+
+        y_qkv = buf.y_qkv if buf.direct else None
+        y_o = buf.y_o if buf.direct else None
+        y_down = buf.y_down if buf.direct else None
+        prev_ks = 0             # splits of the previous layer's down-projection partials
+        for li, lw in enumerate(self.layers):
+            # K1: input norm (layer 0 from the embedding; later layers reduce
+            # the previous down projection's output and add the residual)
+            k1(li == 0, y_down, buf.part_down, prev_ks, lw.input_norm)
+            # qkv projection -> fp32 partials (or its T output) -> K2 epilogue (+ KV scatter)
             cq = buf.cfgs["qkv"]
-            lw.qkv.launch(buf.normed, B, cq, part=buf.part_qkv, wtmp=buf.wtmp, stream=st)
+            lw.qkv.launch(buf.normed, B, cq, out=y_qkv, part=buf.part_qkv, wtmp=buf.wtmp,
+                          stream=st)
             kp = kbase + li * layer_elems * esz
             vp = vbase + li * layer_elems * esz
             if fused_attn:
@@ -497,7 +519,8 @@ class Qwen3DecodeModel:
                     ptr(buf.positions), ptr(self.inv_freq), dt, wdt, st), "K3+epilogue")
             else:
                 check(L.acorn_qkv_epilogue(
-                    ptr(buf.part_qkv), cq.ksplit, ptr(buf.q), kp, vp, ptr(buf.pages),
+                    ptr(y_qkv) if buf.direct else ptr(buf.part_qkv),
+                    0 if buf.direct else cq.ksplit, ptr(buf.q), kp, vp, ptr(buf.pages),
                     ptr(buf.slots), B, nq, nkv, D, page_size, num_blocks, ptr(lw.q_norm),
                     ptr(lw.k_norm), eps, ptr(buf.positions), ptr(self.inv_freq), dt, wdt, st),
                     "qkv_epilogue")
@@ -516,10 +539,8 @@ class Qwen3DecodeModel:
                         buf.max_pages, buf.num_splits, float(self.scale), dt, st), "K3")
             # o projection -> K1 (reduce + residual add + post-attention norm)
             co = buf.cfgs["o"]
-            lw.o.launch(buf.attn, B, co, part=buf.part_o, wtmp=buf.wtmp, stream=st)
-            check(L.acorn_fused_add_rmsnorm_partials(
-                ptr(buf.part_o), co.ksplit, ptr(buf.res), ptr(buf.res), ptr(lw.post_norm),
-                ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
+            lw.o.launch(buf.attn, B, co, out=y_o, part=buf.part_o, wtmp=buf.wtmp, stream=st)
+            k1(False, y_o, buf.part_o, co.ksplit, lw.post_norm)
             # MLP: gate|up (+ fused SwiGLU) -> act -> down partials
             cg = buf.cfgs["gate_up"]
             if buf.swiglu:
@@ -530,12 +551,11 @@ class Qwen3DecodeModel:
                 check(L.acorn_silu_mul(ptr(buf.part_gu), cg.ksplit, None, ptr(buf.act), B, inter,
                                        int(lw.gate_up.il16), dt, st), "silu_mul")
             cd = buf.cfgs["down"]
-            lw.down.launch(buf.act, B, cd, part=buf.part_down, wtmp=buf.wtmp, stream=st)
+            lw.down.launch(buf.act, B, cd, out=y_down, part=buf.part_down, wtmp=buf.wtmp,
+                           stream=st)
             prev_ks = cd.ksplit
         # final norm (reduce + residual add) -> lm_head -> greedy
-        check(L.acorn_fused_add_rmsnorm_partials(
-            ptr(buf.part_down), prev_ks, ptr(buf.res), ptr(buf.res), ptr(self.norm),
-            ptr(buf.normed), None, B, H, eps, dt, wdt, st), "K1")
+        k1(False, y_down, buf.part_down, prev_ks, self.norm)
         if head_rows is not None:
             n = int(head_rows.numel())
             if n == 0:
@@ -816,7 +836,7 @@ class Qwen3DecodeModel:
             Rb = r1 - r0
             # the step buffers of the last shape are kept (a prompt batch often repeats it)
             # (the prefill kernel reads per-sequence tables: no per-row table)
-            key = (Rb, 1 if tiled else W, self.prefill_gemm)
+            key = (Rb, 1 if tiled else W, self.prefill_gemm, self.prefill_direct)
             cached = getattr(self, "_extend_buf", None)
             if cached is None or cached[0] != key:
                 self._extend_buf = None
@@ -1017,12 +1037,25 @@ class StepBuffers:
         self.q = z(B, nq, D)
         self.attn = z(B, nq * D)
         self.act = z(B, inter)
-        self.part_qkv = z(self.cfgs["qkv"].ksplit, B, (nq + 2 * nkv) * D, dtype=f32)
-        self.part_o = z(self.cfgs["o"].ksplit, B, H, dtype=f32)
+        # prefill: qkv / o / down straight to the activation dtype when each is
+        # one split on the large-M kernel (the epilogue and K1 read it as is)
+        large = (DENSE_RT, DEQUANT_RT)
+        self.direct = (self.prefill and m.prefill_direct and D == 128 and B >= PREFILL_DIRECT_M
+                       and dt == torch.bfloat16 and
+                       all(self.cfgs[n].rt in large and self.cfgs[n].ksplit == 1
+                           for n in ("qkv", "o", "down")))
+        if self.direct:
+            self.y_qkv = z(B, (nq + 2 * nkv) * D)
+            self.y_o = z(B, H)
+            self.y_down = z(B, H)
+            self.part_qkv = self.part_o = None
+        else:
+            self.part_qkv = z(self.cfgs["qkv"].ksplit, B, (nq + 2 * nkv) * D, dtype=f32)
+            self.part_o = z(self.cfgs["o"].ksplit, B, H, dtype=f32)
         # (the fused SwiGLU writes act directly: no gate|up partials at prefill sizes)
         self.part_gu = (None if self.swiglu and self.prefill else
                         z(self.cfgs["gate_up"].ksplit, B, 2 * inter, dtype=f32))
-        self.part_down = z(self.cfgs["down"].ksplit, B, H, dtype=f32)
+        self.part_down = None if self.direct else z(self.cfgs["down"].ksplit, B, H, dtype=f32)
         ks_lm = self.cfgs["lm_head"].ksplit
         S = self.num_splits
         self.ws_acc = z(B * nq * S * D, dtype=f32) if S > 1 else None

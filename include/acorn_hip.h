@@ -116,7 +116,10 @@ int acorn_qknorm_rope_inplace(void* q, void* k, int64_t batch, int64_t q_heads,
  * k_pages/v_pages [num_blocks, page, KV, D] at (pages[b], slots[b]) (int64);
  * a (page, slot) outside [0, num_blocks) x [0, page_size) is not written.
  * Semantics = qwen3.py:180-192 followed by cache/pager.py:87-113
- * (scatter_decode). No single reference function.
+ * (scatter_decode). No single reference function. nsplit == 0: `part` holds
+ * the projection's output already rounded to T, [batch, (H + 2*KV)*D] (a
+ * one-split GEMM that wrote T), the same bits as one fp32 plane of it; built
+ * for D == 128 from 256 rows (ACORN_ERR_UNSUPPORTED otherwise).
  */
 int acorn_qkv_epilogue(const float* part, int64_t nsplit, void* q_out, void* k_pages,
                        void* v_pages, const int64_t* pages, const int64_t* slots,

@@ -157,6 +157,43 @@ def test_prefill_at_dense_gemm_sizes_bf16_matches_oracle():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["bf16", "w4a16"])
+def test_prefill_direct_outputs_equal_partials(fmt):
+    """Prefill blocks whose qkv / o / down run in one split on the large-M
+    kernel write them in bf16 and the qkv epilogue / K1 read that; the same
+    prefill through fp32 planes gives the same logits and KV bits. 1500 rows:
+    the dense kernel (bf16 from 512 rows, int4 dequantised from 1024) with
+    the SwiGLU epilogue."""
+    from acorninfer_amd.models.qwen3 import DENSE_RT, DEQUANT_RT, PREFILL_DIRECT_M
+    from acorninfer_amd.ops.quant_gemm import Tiling
+    cfg = Qwen3Config.qwen3_0_6b().with_layers(2)
+    sd = random_state_dict(cfg, seed=SEED + 9, std=0.02, dtype=torch.bfloat16)
+    model = Qwen3DecodeModel.from_state_dict(cfg, sd, weight_format=fmt, device="cuda")
+    prompts = [_ids(n, cfg.vocab_size, SEED + 60 + n) for n in (700, 400, 400)]
+    rows = sum(map(len, prompts))
+    assert rows >= PREFILL_DIRECT_M
+    # one split each (this small model's planner would split K to fill the CUs)
+    t = Tiling(DENSE_RT if fmt == "bf16" else DEQUANT_RT, 256, 128, 1, 4)
+    model.tilings[rows] = {"qkv": t, "o": t, "down": t}
+    got = {}
+    for direct in (True, False):
+        model.prefill_direct = direct
+        alloc, cache = new_cache(model, 120)
+        views = [PagedCacheView(cache) for _ in prompts]
+        logits = model.forward_prefill_batch(_padded(prompts, model.device), views,
+                                             real_lens=[len(p) for p in prompts])
+        assert model._extend_buf[1].direct == direct
+        got[direct] = (logits.cpu(), cache.k_pool.clone(), cache.v_pool.clone())
+        release(alloc, views)
+    model.prefill_direct = True
+    for a, b in zip(got[True], got[False]):
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                           b.view(torch.int16) if b.dtype == torch.bfloat16 else b)
+    del model.tilings[rows]
+    print(f"\n[{fmt} prefill {rows} rows: direct outputs == fp32 planes]")
+
+
+@pytest.mark.gpu
 def test_prefill_w4a16_dequant_route_matches_oracle():
     """int4 weights at >= 2048 rows: every projection dequantises into the step
     workspace and runs on the large-M bf16 kernel; the last-row logits stay
