@@ -503,6 +503,23 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
          ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
+// Two floats rounded to T's grid, packed lo | hi << 16; sum gains the two
+// rounded values (lo first).
+template <typename T>
+__device__ __forceinline__ uint32_t pack_sum(float lo, float hi, float& sum) {
+  if constexpr (std::is_same<T, __bf16>::value) {
+    const uint32_t u = pack_bf16x2(lo, hi);
+    sum += bf16_lo(u);
+    sum += bf16_hi(u);
+    return u;
+  } else {
+    const float a = round_to<T>(lo), b = round_to<T>(hi);
+    sum += a;
+    sum += b;
+    return pack2<T>(a, b);
+  }
+}
+
 // Byte offset of the per-wave K slabs in the MFMA kernel's dynamic LDS:
 // after the wave partials [NWV][REP][D], their (m, l) and the split's pps
 // block ids, rounded up to 16 bytes.
@@ -1222,16 +1239,21 @@ int dispatch_d(int64_t D, int64_t rep, const void* q, const void* kp, const void
 //  * the kv head's keys are walked in chunks of 64 tokens that the whole
 //    workgroup stages in LDS once (K and V rows, coalesced 16-byte loads, two
 //    buffers, one barrier per chunk); the next chunk's loads are in flight
-//    while the current one is consumed, and its page ids one chunk earlier;
+//    while the current one is consumed, and its page ids one chunk earlier.
+//    Rows are padded to 2 D + 32 bytes: the score operand reads (16 rows x
+//    64 bytes) and the transposing V reads (16 rows x 32 bytes) then run
+//    without LDS bank conflicts on gfx950 (a probe: 2 D + 16 adds conflict
+//    cycles to the former and 2 D to both);
 //  * per 32 keys and query block: 2 D/32 v_mfma_f32_16x16x32 for the scores,
-//    the online softmax per query column (lazy max), D/16
-//    v_mfma_f32_16x16x32 for P V (the scores of the two 16-key halves are its
-//    B operand as they lie; 16x16x16 runs at half the rate on gfx950); blocks
-//    whose queries all precede the keys
-//    skip them; keys past a query's position are masked where a chunk
-//    crosses the diagonal, and the first chunk holds key 0, so every
-//    column's max is finite from the start; rows past the last key re-read
-//    it (finite, masked);
+//    the online softmax per query column (lazy max; the scale is applied
+//    inside the exp2 argument by one fma), D/16 v_mfma_f32_16x16x32 for P V
+//    (the scores of the two 16-key halves are its B operand as they lie;
+//    16x16x16 runs at half the rate on gfx950; the V^T operand comes from
+//    LDS through ds_read_b64_tr_b16, no register transposes); blocks whose
+//    queries all precede the keys skip the scores and add P = 0; keys past a
+//    query's position are masked where a chunk crosses the diagonal, and the
+//    first chunk holds key 0, so every column's max is finite from the
+//    start; rows past the last key re-read it (finite, masked);
 //  * the longest query tiles (the last ones) are dispatched first.
 // A workgroup reads its keys once for REP x QG x 32 query rows: O(L^2 / 32)
 // K / V bytes per prompt of L tokens and kv head, against O(L^2) for one
@@ -1244,14 +1266,15 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
     int R, int H, int KV, int P, int num_blocks, int table_stride, float scale_log2) {
   constexpr int QW = 2;                          // 16-query blocks per wave
   constexpr int NT = REP * QG * kWave;           // threads
-  constexpr int KB = D / 32, DPL = D / 16, VW = DPL / 2;
-  constexpr int PITCH = 2 * D + 16;              // bytes per staged row (padded)
+  constexpr int KB = D / 32, DPL = D / 16;
+  constexpr int KPITCH = 2 * D + 32;             // bytes per staged K row (padded)
+  constexpr int VPITCH = KPITCH;                 // bytes per staged V row
   constexpr int RP = 2 * D / 16;                 // 16-byte pieces per K / V row
   constexpr int PPT = 2 * KC * RP / NT;          // pieces per thread per chunk
   constexpr int WQ = QG * QW * 16;               // query rows per workgroup
   static_assert(2 * KC * RP % NT == 0 && PPT >= 1, "whole pieces per thread");
   static_assert(KC % 32 == 0, "a chunk is whole 32-key P V MFMAs");
-  __shared__ __align__(16) uint8_t kvs[2][2 * KC * PITCH];   // [buffer][K rows | V rows]
+  __shared__ __align__(16) uint8_t kvs[2][KC * (KPITCH + VPITCH)];   // [buffer][K rows | V rows]
   const int kvh = blockIdx.y, n = blockIdx.z;
   const int tid = threadIdx.x;
   const int wid = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -1296,7 +1319,8 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
     const int kind = p / (KC * RP);                // 0: K, 1: V
     const int pcol = p % RP;
     prow[i] = (p % (KC * RP)) / RP;
-    poff[i] = (uint32_t)(kind * KC * PITCH + prow[i] * PITCH + pcol * 16);
+    poff[i] = (uint32_t)(kind ? KC * KPITCH + prow[i] * VPITCH + pcol * 16
+                              : prow[i] * KPITCH + pcol * 16);
     pbase[i] = (kind ? v_pages : k_pages) + (size_t)kvh * D + pcol * 8;
   }
   auto page_of = [&](int chunk, int i) {
@@ -1332,16 +1356,22 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
   // for query c) are exactly the B operand of one v_mfma_f32_16x16x32 for
   // P V when the MFMA's k slot s of lane group r stands for key 4 r + s
   // (s < 4) or 16 + 4 r + s - 4 (half 1); the V^T operand follows the same
-  // key order, so P never moves between lanes
+  // key order, so P never moves between lanes. That operand comes from LDS
+  // transposed by ds_read_b64_tr_b16: within each 16-lane group, lane j
+  // receives element j % 4 of the 8 bytes lane 4 e + j / 4 addressed, for
+  // e = 0..3. Lane 4 e + q of group r addresses key 4 r + e (+ 16 for the
+  // second half), dims 16 jj + 4 q .. + 3, so lane (r, c) receives dim
+  // 16 jj + c of keys 4 r .. 4 r + 3: row c of block jj's A operand.
+  const uint32_t vlane = (uint32_t)((4 * r + (c >> 2)) * VPITCH + 8 * (c & 3));
   auto consume = [&](int b, int sub, int t0) {
-    const uint8_t* kbuf = kvs[b] + 32 * sub * PITCH;
-    const uint8_t* vbuf = kvs[b] + KC * PITCH + 32 * sub * PITCH;
+    const uint8_t* kbuf = kvs[b] + 32 * sub * KPITCH;
+    const uint8_t* vbuf = kvs[b] + KC * KPITCH + 32 * sub * VPITCH;
     u32x4_t kf[2][KB];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
       for (int jb = 0; jb < KB; ++jb)
-        kf[hh][jb] = *(const u32x4_t*)(kbuf + (16 * hh + c) * PITCH + 2 * (32 * jb + 8 * r));
+        kf[hh][jb] = *(const u32x4_t*)(kbuf + (16 * hh + c) * KPITCH + 2 * (32 * jb + 8 * r));
     u32x4_t pb[QW];
     bool live[QW];
 #pragma unroll
@@ -1349,14 +1379,14 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
       // the block's queries all precede these keys, or it has none: nothing to add
       live[qw] = 16 * qw < nvalid && t0 <= pos0 + j0 + min(16 * qw + 15, nvalid - 1);
       if (!live[qw]) continue;
-      float sv[8];
+      float sv[8];                               // raw scores; scaled inside the exp2
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int jb = 0; jb < KB; ++jb) sc = mfma16x16x32<T>(kf[hh][jb], qb[qw][jb], sc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sv[4 * hh + i] = sc[i] * scale_log2;
+        for (int i = 0; i < 4; ++i) sv[4 * hh + i] = sc[i];
       }
       if (t0 + 31 > pos0 + j0 + 16 * qw) {       // the keys cross some column's diagonal
 #pragma unroll
@@ -1368,6 +1398,7 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
       float mx = sv[0];
 #pragma unroll
       for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+      mx *= scale_log2;                          // scale_log2 > 0: the max of the scaled scores
       if (__builtin_amdgcn_ballot_w64(mx > m[qw] + kMaxSlack) != 0) {
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -1378,34 +1409,35 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
 #pragma unroll
         for (int jj = 0; jj < DPL; ++jj) acc[qw][jj] *= alpha;
       }
-      float pr[8];
+      const float nm = -m[qw];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        pr[i] = round_to<T>(__builtin_amdgcn_exp2f(sv[i] - m[qw]));
-        l[qw] += pr[i];
-      }
-      pb[qw] = u32x4_t{pack2<T>(pr[0], pr[1]), pack2<T>(pr[2], pr[3]), pack2<T>(pr[4], pr[5]),
-                       pack2<T>(pr[6], pr[7])};
+      for (int i = 0; i < 4; ++i)
+        pb[qw][i] = pack_sum<T>(__builtin_amdgcn_exp2f(__builtin_fmaf(sv[2 * i], scale_log2, nm)),
+                                __builtin_amdgcn_exp2f(__builtin_fmaf(sv[2 * i + 1], scale_log2, nm)),
+                                l[qw]);
     }
     if (!live[0] && !live[QW - 1]) return;
-    // lane (r, c): V rows 4 r .. 4 r + 3 of each half, dims [DPL c, DPL c + DPL)
-    uint32_t vr[8][VW];
+    // a block without live queries adds P = 0 (V rows are finite), so the
+    // P V MFMAs below run unconditionally
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj)
-      __builtin_memcpy(vr[jj], vbuf + (16 * (jj >> 2) + 4 * r + (jj & 3)) * PITCH + 2 * DPL * c,
-                       sizeof(vr[jj]));
+    for (int qw = 0; qw < QW; ++qw)
+      if (!live[qw]) pb[qw] = u32x4_t{0u, 0u, 0u, 0u};
+    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+    const __attribute__((address_space(3))) uint8_t* vl =
+        (const __attribute__((address_space(3))) uint8_t*)vbuf + vlane;
+    u32x4_t va[DPL];
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) {
-      const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
-      const int e = jj / 2;
-      const u32x4_t va = {__builtin_amdgcn_perm(vr[1][e], vr[0][e], sel),
-                          __builtin_amdgcn_perm(vr[3][e], vr[2][e], sel),
-                          __builtin_amdgcn_perm(vr[5][e], vr[4][e], sel),
-                          __builtin_amdgcn_perm(vr[7][e], vr[6][e], sel)};
-#pragma unroll
-      for (int qw = 0; qw < QW; ++qw)
-        if (live[qw]) acc[qw][jj] = mfma16x16x32<T>(va, pb[qw], acc[qw][jj]);
+      const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vl + 32 * jj));
+      const s16x4_t hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vl + 16 * VPITCH + 32 * jj));
+      const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
+      va[jj] = u32x4_t{l2[0], l2[1], h2[0], h2[1]};
     }
+#pragma unroll
+    for (int jj = 0; jj < DPL; ++jj)
+#pragma unroll
+      for (int qw = 0; qw < QW; ++qw) acc[qw][jj] = mfma16x16x32<T>(va[jj], pb[qw], acc[qw][jj]);
   };
 
   // prologue: chunk 0 staged, chunk 1's loads and page ids in flight
@@ -1434,7 +1466,7 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
     __syncthreads();
   }
   if (nvalid == 0) return;
-  // lane (r, c) of block qw holds dims DPL (4 r + i) + jj of query column 16 qw + c
+  // lane (r, c) of block qw holds dims 16 jj + 4 r + i of query column 16 qw + c
 #pragma unroll
   for (int qw = 0; qw < QW; ++qw) {
     float lt = l[qw];
@@ -1444,12 +1476,10 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
       const size_t orow = (size_t)(row0 + j0 + 16 * qw + c) * H + h;
       const float inv = 1.0f / lt;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t w[VW];
-#pragma unroll
-        for (int jj = 0; jj < VW; ++jj)
-          w[jj] = pack2<T>(acc[qw][2 * jj][i] * inv, acc[qw][2 * jj + 1][i] * inv);
-        __builtin_memcpy(out + orow * D + DPL * (4 * r + i), w, sizeof(w));
+      for (int jj = 0; jj < DPL; ++jj) {
+        const u32x2_t w = {pack2<T>(acc[qw][jj][0] * inv, acc[qw][jj][1] * inv),
+                           pack2<T>(acc[qw][jj][2] * inv, acc[qw][jj][3] * inv)};
+        *(u32x2_t*)(out + orow * D + 16 * jj + 4 * r) = w;
       }
     }
   }
