@@ -1309,37 +1309,36 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
       qb[qw][jb] = *(const u32x4_t*)(q + (qrow * H + h) * D + 32 * jb + 8 * r);
   }
 
-  // staging: piece i of this thread is K (i < PPT/2) or V, row pr[i], 16-byte column pcol[i]
-  int prow[PPT];
-  uint32_t poff[PPT];
-  const T* pbase[PPT];
-#pragma unroll
-  for (int i = 0; i < PPT; ++i) {
-    const int p = tid + NT * i;
-    const int kind = p / (KC * RP);                // 0: K, 1: V
-    const int pcol = p % RP;
-    prow[i] = (p % (KC * RP)) / RP;
-    poff[i] = (uint32_t)(kind ? KC * KPITCH + prow[i] * VPITCH + pcol * 16
-                              : prow[i] * KPITCH + pcol * 16);
-    pbase[i] = (kind ? v_pages : k_pages) + (size_t)kvh * D + pcol * 8;
-  }
+  // staging: this thread moves the 16-byte column pcol of rows prow0 + i NT / RP
+  // (i < PH) of K and of V; a row's K and V pieces share its page id
+  static_assert(NT % RP == 0 && PPT % 2 == 0, "whole rows per wave");
+  constexpr int PH = PPT / 2, RSTEP = NT / RP;
+  const int pcol = tid % RP, prow0 = tid / RP;
+  const uint32_t poff0 = (uint32_t)(prow0 * KPITCH + pcol * 16);
+  const T* kbase = k_pages + (size_t)kvh * D + pcol * 8;
+  const T* vbase = v_pages + (size_t)kvh * D + pcol * 8;
   auto page_of = [&](int chunk, int i) {
-    const int t = min(chunk * KC + prow[i], L - 1);
+    const int t = min(chunk * KC + prow0 + i * RSTEP, L - 1);
     const unsigned pg = (unsigned)trow[min(t >> pshift, table_stride - 1)];
     return pg < (unsigned)num_blocks ? (int)pg : 0;
   };
-  int pg[PPT], pg_next[PPT];
+  int pg[PH], pg_next[PH];
   u32x4_t stage[PPT];
-  auto load_chunk = [&](int chunk, const int (&pgs)[PPT]) {
+  auto load_chunk = [&](int chunk, const int (&pgs)[PH]) {
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const int t = min(chunk * KC + prow[i], L - 1);
-      stage[i] = *(const u32x4_t*)(pbase[i] + ((size_t)pgs[i] * P + (t & (P - 1))) * tok_stride);
+    for (int i = 0; i < PH; ++i) {
+      const int t = min(chunk * KC + prow0 + i * RSTEP, L - 1);
+      const size_t off = ((size_t)pgs[i] * P + (t & (P - 1))) * tok_stride;
+      stage[i] = *(const u32x4_t*)(kbase + off);
+      stage[PH + i] = *(const u32x4_t*)(vbase + off);
     }
   };
   auto store_chunk = [&](int b) {
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) *(u32x4_t*)(kvs[b] + poff[i]) = stage[i];
+    for (int i = 0; i < PH; ++i) {
+      *(u32x4_t*)(kvs[b] + poff0 + i * RSTEP * KPITCH) = stage[i];
+      *(u32x4_t*)(kvs[b] + KC * KPITCH + poff0 + i * RSTEP * VPITCH) = stage[PH + i];
+    }
   };
 
   float m[QW], l[QW];
@@ -1363,7 +1362,19 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
   // second half), dims 16 jj + 4 q .. + 3, so lane (r, c) receives dim
   // 16 jj + c of keys 4 r .. 4 r + 3: row c of block jj's A operand.
   const uint32_t vlane = (uint32_t)((4 * r + (c >> 2)) * VPITCH + 8 * (c & 3));
-  auto consume = [&](int b, int sub, int t0) {
+  // One 32-key step, software-pipelined by one step: this step's score
+  // MFMAs are issued first, then the previous step's P V MFMAs (va / pb,
+  // held in registers across the chunk barrier), and this step's softmax
+  // runs while those execute; its P and V operands are left in va / pb.
+  u32x4_t va[DPL], pb[QW];
+  bool pend = false;                             // va / pb hold a step whose P V is due
+  auto pv = [&]() {
+#pragma unroll
+    for (int jj = 0; jj < DPL; ++jj)
+#pragma unroll
+      for (int qw = 0; qw < QW; ++qw) acc[qw][jj] = mfma16x16x32<T>(va[jj], pb[qw], acc[qw][jj]);
+  };
+  auto step = [&](int b, int sub, int t0) {
     const uint8_t* kbuf = kvs[b] + 32 * sub * KPITCH;
     const uint8_t* vbuf = kvs[b] + KC * KPITCH + 32 * sub * VPITCH;
     u32x4_t kf[2][KB];
@@ -1372,22 +1383,37 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
 #pragma unroll
       for (int jb = 0; jb < KB; ++jb)
         kf[hh][jb] = *(const u32x4_t*)(kbuf + (16 * hh + c) * KPITCH + 2 * (32 * jb + 8 * r));
-    u32x4_t pb[QW];
+    f32x4_t S[QW][2];
     bool live[QW];
 #pragma unroll
     for (int qw = 0; qw < QW; ++qw) {
       // the block's queries all precede these keys, or it has none: nothing to add
       live[qw] = 16 * qw < nvalid && t0 <= pos0 + j0 + min(16 * qw + 15, nvalid - 1);
       if (!live[qw]) continue;
-      float sv[8];                               // raw scores; scaled inside the exp2
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+        S[qw][hh] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int jb = 0; jb < KB; ++jb) sc = mfma16x16x32<T>(kf[hh][jb], qb[qw][jb], sc);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sv[4 * hh + i] = sc[i];
+        for (int jb = 0; jb < KB; ++jb)
+          S[qw][hh] = mfma16x16x32<T>(kf[hh][jb], qb[qw][jb], S[qw][hh]);
       }
+    }
+    if (pend) pv();
+    pend = live[0] || live[QW - 1];
+    if (!pend) return;
+#pragma unroll
+    for (int qw = 0; qw < QW; ++qw) {
+      // a block without live queries adds P = 0 (V rows are finite), so the
+      // P V MFMAs run unconditionally
+      if (!live[qw]) {
+        pb[qw] = u32x4_t{0u, 0u, 0u, 0u};
+        continue;
+      }
+      float sv[8];                               // raw scores; scaled inside the exp2
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[4 * hh + i] = S[qw][hh][i];
       if (t0 + 31 > pos0 + j0 + 16 * qw) {       // the keys cross some column's diagonal
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
@@ -1416,16 +1442,9 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
                                 __builtin_amdgcn_exp2f(__builtin_fmaf(sv[2 * i + 1], scale_log2, nm)),
                                 l[qw]);
     }
-    if (!live[0] && !live[QW - 1]) return;
-    // a block without live queries adds P = 0 (V rows are finite), so the
-    // P V MFMAs below run unconditionally
-#pragma unroll
-    for (int qw = 0; qw < QW; ++qw)
-      if (!live[qw]) pb[qw] = u32x4_t{0u, 0u, 0u, 0u};
     typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
     const __attribute__((address_space(3))) uint8_t* vl =
         (const __attribute__((address_space(3))) uint8_t*)vbuf + vlane;
-    u32x4_t va[DPL];
 #pragma unroll
     for (int jj = 0; jj < DPL; ++jj) {
       const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vl + 32 * jj));
@@ -1434,18 +1453,14 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
       const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
       va[jj] = u32x4_t{l2[0], l2[1], h2[0], h2[1]};
     }
-#pragma unroll
-    for (int jj = 0; jj < DPL; ++jj)
-#pragma unroll
-      for (int qw = 0; qw < QW; ++qw) acc[qw][jj] = mfma16x16x32<T>(va[jj], pb[qw], acc[qw][jj]);
   };
 
   // prologue: chunk 0 staged, chunk 1's loads and page ids in flight
 #pragma unroll
-  for (int i = 0; i < PPT; ++i) pg[i] = page_of(0, i);
+  for (int i = 0; i < PH; ++i) pg[i] = page_of(0, i);
   load_chunk(0, pg);
 #pragma unroll
-  for (int i = 0; i < PPT; ++i) pg_next[i] = page_of(min(1, nchunks - 1), i);
+  for (int i = 0; i < PH; ++i) pg_next[i] = page_of(min(1, nchunks - 1), i);
   store_chunk(0);
   load_chunk(min(1, nchunks - 1), pg_next);
   __syncthreads();
@@ -1453,11 +1468,11 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
     const int b = ci & 1;
     // page ids two chunks ahead
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) pg[i] = page_of(min(ci + 2, nchunks - 1), i);
+    for (int i = 0; i < PH; ++i) pg[i] = page_of(min(ci + 2, nchunks - 1), i);
     __builtin_amdgcn_sched_barrier(0);
     if (nvalid > 0) {
 #pragma unroll
-      for (int sub = 0; sub < KC / 32; ++sub) consume(b, sub, ci * KC + 32 * sub);
+      for (int sub = 0; sub < KC / 32; ++sub) step(b, sub, ci * KC + 32 * sub);
     }
     __builtin_amdgcn_sched_barrier(0);
     store_chunk(b ^ 1);                         // chunk ci + 1 (its buffer was last read in ci - 1)
@@ -1466,6 +1481,7 @@ __global__ __launch_bounds__(REP * QG * kWave, 2) void paged_prefill_kernel(
     __syncthreads();
   }
   if (nvalid == 0) return;
+  if (pend) pv();
   // lane (r, c) of block qw holds dims 16 jj + 4 r + i of query column 16 qw + c
 #pragma unroll
   for (int qw = 0; qw < QW; ++qw) {
