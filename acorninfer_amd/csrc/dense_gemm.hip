@@ -27,8 +27,9 @@
 // instead was slower: the loads are not its bound). Two 256 x 256 forms
 // follow, both operands in LDS and two waves per SIMD: one stages through
 // registers (1.0-1.06 PFLOP/s at M = 2048-8192), the other loads straight
-// into LDS (global_load_lds) through a 4-stage ring, the planner's default
-// from 512 rows (1.19-1.28 PFLOP/s at M = 8192; hipBLASLt: 1.3-1.5).
+// into LDS (global_load_lds) in whole 128-byte rows through two pair-of-stage
+// buffers, the planner's default from 512 rows (1.11-1.33 PFLOP/s at
+// M = 8192; hipBLASLt: 1.3-1.5).
 #include <hip/hip_runtime.h>
 
 #include "acorn_hip.h"
@@ -284,27 +285,29 @@ __global__ __launch_bounds__(512, 1) void dense_lds_kernel(const __bf16* __restr
   }
 }
 
-// Direct-to-LDS form (bm == kLdsTile, wn == 128): a workgroup of 4 waves, one
-// per SIMD, owns a 256 x 256 output tile; wave (wn, wm) of its 2 x 2 grid owns
-// 128 x 128 of it (8 x 8 accumulator blocks, 256 accumulator registers), so
-// every operand it reads from LDS feeds 8 MFMAs (8 FLOPs per LDS byte). Both
-// operands go from memory into LDS with global_load_lds_dwordx4 (no staging
-// registers, no LDS store instructions), 32 k per stage through a ring of 4
-// stages: the loads of stage s + 3 are issued while stage s is multiplied, and
-// the operands of stage s + 1 are read into the second register set. Rows are
-// 64 bytes, unpadded: 16-byte piece p of row R sits at slot p ^ ((R >> 1) & 3).
-// An MFMA operand read (lane (r, c): row c of a 16-row block, piece r) then
-// runs without LDS bank conflicts on gfx950 (a probe of ds_read_b128
-// patterns: this one, like a linear read, shows no conflict cycles; padded
-// 144- or 80-byte rows, unswizzled 64-byte rows and ((R >> 1) ^ (R >> 3)) & 3
-// all add 20%). One barrier per stage; the memory waits are explicit (vmcnt
-// counts this wave's loads). A fifth stage (all 160 KB of LDS) measured 2-3%
-// slower.
+// Direct-to-LDS form (bm == kLdsTile, wn == 128): a workgroup of NW = 8 waves,
+// two per SIMD, owns a 256 x 256 output tile; wave (wn, wm) of its 2 x 4 grid
+// owns 128 x 64 of it (8 x 4 accumulator blocks), so every weight operand it
+// reads from LDS feeds 4 MFMAs and every x operand 8. Both operands go from
+// memory into LDS with global_load_lds_dwordx4 (no staging registers, no LDS
+// store instructions). A stage is 32 k (one v_mfma_f32_16x16x32 deep); the
+// loads move a pair of stages at once, in whole 128-byte rows (64 k), into a
+// ring of two pair buffers (128 KB): while pair d is multiplied, pair d + 1
+// is in flight, and each stage reads the next stage's operands into the
+// second register set. 16-byte piece p of row R sits at slot p ^ ((R >> 1) & 7)
+// of its 128-byte LDS row; an MFMA operand read (lane (r, c): row c of a
+// 16-row block, piece 4 h + r of stage half h) then touches every bank group
+// once per 16 lanes. One barrier per pair of stages; the memory waits are
+// explicit (vmcnt counts this wave's loads). Measured alternatives at M = 8192
+// on the 8B shapes: half-line loads (64-byte rows, one stage per load, a ring
+// of four stages, one barrier per stage) 3-6% slower; a fifth such stage (all
+// 160 KB of LDS) slower again; four waves of 128 x 128 5-7% slower; two
+// workgroups of 4 waves per CU (3 stages each) 15% slower. An ablation copy
+// without the memory-to-LDS loads runs at 1.9-2.25 PFLOP/s, one without the
+// LDS operand reads at 1.26-1.41: the loads bound the kernel.
 constexpr int kDlBK = 32;                 // k per stage
-constexpr int kDlStages = 4;
+constexpr int kDlStages = 4;              // LDS stages: two pair buffers
 constexpr int kDlOpBytes = kLdsTile * kDlBK * 2;   // one operand of one stage: 16 KB
-
-__device__ __forceinline__ int dl_swz(int row) { return (row >> 1) & 3; }
 
 template <typename OUT, int NW, bool SWIGLU = false>
 __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __restrict__ x,
@@ -314,8 +317,9 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
                                                               int tiles_m, int steps) {
   constexpr int T = kLdsTile;
   constexpr int NB = 8, MB = 32 / NW;          // wave tile 128 x 16 MB
-  constexpr int LPW = 16 / NW;                 // 1 KB loads per wave per operand per stage
-  __shared__ __align__(1024) uint8_t lds[kDlStages][2][kDlOpBytes];
+  constexpr int LPW = 32 / NW;                 // 1 KB loads per wave per operand per pair of stages
+  constexpr int PAIR = 2 * kDlOpBytes;         // one operand of a pair of stages: 256 rows x 128 B
+  __shared__ __align__(1024) uint8_t lds[2][2][PAIR];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -335,22 +339,25 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
   const int kbase = blockIdx.y * steps * kDlBK;
   out += (size_t)blockIdx.y * M * N;
 
-  // load j of this wave fills rows 16 (LPW wid + j) .. + 15 of an operand:
-  // lane L writes row 16 (LPW wid + j) + L / 4, slot L % 4, with global piece
-  // (L % 4) ^ f(row)
+  // a pair of stages (64 k) is loaded at once, in whole 128-byte rows: load j
+  // of this wave fills rows 8 (LPW wid + j) .. + 7 of an operand, lane L
+  // writing row 8 (LPW wid + j) + L / 8, slot L % 8, with global piece
+  // (L % 8) ^ ((row >> 1) & 7)
   const __bf16* wsrc[LPW];
   const __bf16* xsrc[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
-    const int row = 16 * (LPW * wid + j) + (lane >> 2);
-    const int piece = (lane & 3) ^ dl_swz(row);
+    const int row = 8 * (LPW * wid + j) + (lane >> 3);
+    const int piece = (lane & 7) ^ ((row >> 1) & 7);
     wsrc[j] = w + (size_t)min(n0 + row, N - 1) * K + kbase + 8 * piece;
     xsrc[j] = x + (size_t)min(m0 + row, M - 1) * K + kbase + 8 * piece;
   }
-  // operand reads: block i's row wn + 16 i + c, piece r; the swizzle depends
-  // on c only, so block i sits 1024 bytes after block 0
-  const uint32_t aoff = (uint32_t)((wn + c) * 64 + 16 * (r ^ dl_swz(c)));
-  const uint32_t boff = (uint32_t)((wm + c) * 64 + 16 * (r ^ dl_swz(c)));
+  // operand reads of stage half h: block i's row wn + 16 i + c, piece 4 h + r
+  // at slot (4 h + r) ^ (c >> 1); block i sits 2048 bytes after block 0
+  const uint32_t aoff0 = (uint32_t)((wn + c) * 128 + 16 * (r ^ (c >> 1)));
+  const uint32_t aoff1 = (uint32_t)((wn + c) * 128 + 16 * ((4 + r) ^ (c >> 1)));
+  const uint32_t boff0 = (uint32_t)((wm + c) * 128 + 16 * (r ^ (c >> 1)));
+  const uint32_t boff1 = (uint32_t)((wm + c) * 128 + 16 * ((4 + r) ^ (c >> 1)));
 
   // the LDS DMA is issued from inline assembly, so the compiler neither
   // orders LDS reads behind it nor waits for it: the explicit vmcnt waits
@@ -363,20 +370,20 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
                  :: "v"(src), "s"(dst) : "memory", "m0");
 #pragma clang diagnostic pop
   };
-  auto issue = [&](int s) {
-    const int b = s & (kDlStages - 1);
-    const int k0 = min(s, steps - 1) * kDlBK;
-    const uint32_t base = lds0 + (uint32_t)(b * 2 * kDlOpBytes + LPW * wid * 1024);
+  const int pairs = steps / 2;
+  auto issue = [&](int d) {                    // stages 2 d, 2 d + 1 into buffer d & 1
+    const int k0 = min(d, pairs - 1) * 2 * kDlBK;
+    const uint32_t base = lds0 + (uint32_t)((d & 1) * 2 * PAIR + LPW * wid * 1024);
 #pragma unroll
     for (int j = 0; j < LPW; ++j) dma(wsrc[j] + k0, base + j * 1024);
 #pragma unroll
-    for (int j = 0; j < LPW; ++j) dma(xsrc[j] + k0, base + kDlOpBytes + j * 1024);
+    for (int j = 0; j < LPW; ++j) dma(xsrc[j] + k0, base + PAIR + j * 1024);
   };
   auto opA = [&](int s, int i) {
-    return *(const u32x4*)(&lds[s & (kDlStages - 1)][0][aoff + 1024 * i]);
+    return *(const u32x4*)(&lds[(s >> 1) & 1][0][((s & 1) ? aoff1 : aoff0) + 2048 * i]);
   };
   auto opB = [&](int s, int j) {
-    return *(const u32x4*)(&lds[s & (kDlStages - 1)][1][boff + 1024 * j]);
+    return *(const u32x4*)(&lds[(s >> 1) & 1][1][((s & 1) ? boff1 : boff0) + 2048 * j]);
   };
 
   f32x4 acc[NB][MB];
@@ -391,7 +398,6 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
   auto stage = [&](int s, const u32x4 (&bc)[MB], u32x4 (&bn)[MB]) {
 #pragma unroll
     for (int j = 0; j < MB; ++j) bn[j] = opB(s + 1, j);
-    issue(s + 3);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -405,26 +411,25 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
   // vmcnt(n) with the other counters left open (gfx9 encoding)
 #define ACORN_DL_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
-  constexpr int LPS = 2 * LPW;        // this wave's loads per stage
+  constexpr int LPS = 2 * LPW;        // this wave's loads per pair of stages
   issue(0);
   issue(1);
-  issue(2);
-  ACORN_DL_VMCNT(2 * LPS);            // this wave's stage-0 loads have landed
+  ACORN_DL_VMCNT(LPS);                // this wave's pair-0 loads have landed
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < NB; ++i) a[i] = opA(0, i);
 #pragma unroll
   for (int j = 0; j < MB; ++j) b0[j] = opB(0, j);
-  // iteration s: stage s + 1 lands (barrier; its reads go to the registers
-  // this stage frees), stage s + 3's loads go into the buffer stage s - 1
-  // used (every wave finished reading it before this barrier)
-  for (int s = 0; s < steps; s += 2) {      // steps is even
-    ACORN_DL_VMCNT(LPS);
+  // pair d: stage 2 d reads stage 2 d + 1's operands (same buffer); then
+  // pair d + 1 has landed everywhere (barrier) and every wave has read its
+  // last operands from buffer d & 1, which receives pair d + 2; stage 2 d + 1
+  // reads pair d + 1's first operands
+  for (int d = 0; d < pairs; ++d) {
+    stage(2 * d, b0, b1);
+    ACORN_DL_VMCNT(0);
     __syncthreads();
-    stage(s, b0, b1);
-    ACORN_DL_VMCNT(LPS);
-    __syncthreads();
-    stage(s + 1, b1, b0);
+    issue(d + 2);
+    stage(2 * d + 1, b1, b0);
   }
 #undef ACORN_DL_VMCNT
   __builtin_amdgcn_s_waitcnt(0);      // no LDS write of this wave outlives it
