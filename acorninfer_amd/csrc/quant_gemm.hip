@@ -848,10 +848,20 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
     const int ntile = bm == 256 ? 256 : 4 * wn;    // weight rows per workgroup
     int ks = req && cfg[3] > 0 ? cfg[3] : 1;
     if (!(req && cfg[3] > 0) && !swiglu) {
-      // split K while the launch has fewer workgroups than CUs
+      // split K while the launch has fewer workgroups than CUs; the 256 x 256
+      // form (one workgroup per CU) stops before a second round of workgroups:
+      // at M = 512 / 2048 one round with fewer splits measured faster (qkv
+      // 37 vs 49 us with 4 / 8 splits at 512 rows, 106 vs 115 us with 1 / 2 at
+      // 2048) since every split adds an fp32 plane of traffic
       const int64_t tiles = ((N + ntile - 1) / ntile) * ((M + bm - 1) / bm);
-      while (tiles * ks < kCUs && ks < 8 && dense_gemm_supported(N, K, wn, bm, depth, 2 * ks))
-        ks *= 2;
+      if (bm == 256) {
+        while (tiles * 2 * ks <= kCUs && ks < 8 &&
+               dense_gemm_supported(N, K, wn, bm, depth, 2 * ks))
+          ks *= 2;
+      } else {
+        while (tiles * ks < kCUs && ks < 8 && dense_gemm_supported(N, K, wn, bm, depth, 2 * ks))
+          ks *= 2;
+      }
     }
     if (swiglu ? ks == 1 && dense_gemm_swiglu_supported(N, K, wn, bm, depth)
                : dense_gemm_supported(N, K, wn, bm, depth, ks)) {

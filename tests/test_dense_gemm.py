@@ -58,6 +58,12 @@ def test_planner_routes_prefill_sizes_to_the_dense_kernel():
     # split K while the tiles (16 x 2 here) leave CUs idle
     t, tiles = plan(512, 4096, 4096, WFMT_BF16)
     assert t == Tiling(DENSE_RT, 256, 128, 8, 4) and tiles == 16 * 2
+    # ... but not into a second round of workgroups: 24 x 2 tiles take 4 splits,
+    # 24 x 8 and 96 x 2 none
+    assert plan(512, 6144, 4096, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 4, 4)
+    assert plan(2048, 6144, 4096, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 1, 4)
+    assert plan(512, 24576, 4096, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 1, 4)
+    assert plan(2048, 4096, 4096, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 2, 4)
     assert plan(8192, 4096, 4096, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 1, 4)
     assert plan(512, 4096, 4096, WFMT_BF16, Tiling(DENSE_RT, 128))[0] == \
         Tiling(DENSE_RT, 128, 64, 4, 4)                              # the 128-row form
