@@ -56,9 +56,11 @@ LIBRARY_RT = -1
 # dequantised to bf16 into a step workspace (acorn_dequant_w4b) and
 # multiplied by the large-M bf16 kernel (tiling rt == DEQUANT_RT, the other
 # fields the bf16 kernel's). At prefill sizes the MFMA work dominates and that
-# kernel's rate outweighs the extra pass over the weights (on MI355X the
-# 8B model's qkv breaks even at 1024 rows, the other projections gain there).
-DEQUANT_M_MIN = 1024
+# kernel's rate outweighs the extra pass over the weights: on MI355X a W4A16
+# 8B prefill of 512 / 768 tokens takes 15.0 / 19.7 ms this way against
+# 15.9 / 25.4 ms on the int4 kernels; below 512 rows (where the bf16 kernel
+# is not the 256 x 256 form) the int4 kernels win (8.6 vs 13.4 ms at 256).
+DEQUANT_M_MIN = 512
 DEQUANT_RT = -4
 # prefill blocks from this many rows run gate|up with the large-M kernel's
 # SwiGLU epilogue (act written directly: no fp32 gate|up output, no silu_mul);
