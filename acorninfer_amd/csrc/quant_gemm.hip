@@ -817,10 +817,15 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
 // cfg: {rt, upw, nw, ksplit, tpw}; 0 = choose. swiglu: fused SwiGLU epilogue,
 // which fixes rt = 2 and ksplit = 1. For M > 16 an rt of 0 selects the tiled
 // kernel (upw = its BM), rt >= 1 the streaming kernel.
-// bf16 at prefill sizes: the large-M kernel (dense_gemm.hip) by default from
-// this many rows on, or on request (rt == kDenseRT).
+// bf16 at prefill sizes: the large-M kernel (dense_gemm.hip, its 256 x 256
+// direct-to-LDS form) by default from kDenseMinM rows on, or on request
+// (rt == kDenseRT); with the SwiGLU epilogue from kDenseLdsM rows. At 256 /
+// 384 rows on the 8B shapes the 256 x 256 form took qkv 26.9 / 36.5 us,
+// gate|up 62.4 / 110.2, down 37.3 / 48.6 against 35.4 / 45.8, 86.1 / 142.3,
+// 44.6 / 77.5 on the tiled kernel; the fused SwiGLU (one split) does not pay
+// below 512 rows.
 constexpr int kDenseRT = -2;
-constexpr int64_t kDenseMinM = 512;
+constexpr int64_t kDenseMinM = 256;
 constexpr int64_t kDenseLdsM = 512;
 // W4B above 16 rows on request (rt == kMidRT): the mid-M int4 kernel
 constexpr int kMidRT = -3;
@@ -837,8 +842,8 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   if (wfmt == ACORN_WFMT_BF16 &&
       ((cfg && cfg[0] == kDenseRT) || (no_request && M >= (swiglu ? kDenseLdsM : kDenseMinM)))) {
     const bool req = cfg && cfg[0] == kDenseRT;
-    // from kDenseLdsM rows the 256 x 256 tiles with both operands in LDS
-    const int bm = req && cfg[1] > 0 ? cfg[1] : M >= kDenseLdsM ? 256 : 128;
+    // from kDenseMinM rows the 256 x 256 tiles with both operands in LDS
+    const int bm = req && cfg[1] > 0 ? cfg[1] : M >= kDenseMinM ? 256 : 128;
     const int wn = req && cfg[2] > 0              ? cfg[2]
                    : bm == 256 && !(req && cfg[4] == 2) ? 128    // depth 2: the staged form
                                                         : 64;
@@ -855,7 +860,7 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
       // 2048) since every split adds an fp32 plane of traffic
       const int64_t tiles = ((N + ntile - 1) / ntile) * ((M + bm - 1) / bm);
       if (bm == 256) {
-        while (tiles * 2 * ks <= kCUs && ks < 8 &&
+        while (tiles * 2 * ks <= kCUs && ks < 16 &&
                dense_gemm_supported(N, K, wn, bm, depth, 2 * ks))
           ks *= 2;
       } else {

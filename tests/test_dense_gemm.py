@@ -54,7 +54,7 @@ def _run(x, w, tiling, fp32):
 def test_planner_routes_prefill_sizes_to_the_dense_kernel():
     from acorninfer_amd._lib import WFMT_BF16, WFMT_W8
     from acorninfer_amd.ops.quant_gemm import Tiling, plan
-    # from 512 rows: 256 x 256 tiles, both operands by direct-to-LDS loads,
+    # from 256 rows: 256 x 256 tiles, both operands by direct-to-LDS loads,
     # split K while the tiles (16 x 2 here) leave CUs idle
     t, tiles = plan(512, 4096, 4096, WFMT_BF16)
     assert t == Tiling(DENSE_RT, 256, 128, 8, 4) and tiles == 16 * 2
@@ -69,7 +69,9 @@ def test_planner_routes_prefill_sizes_to_the_dense_kernel():
         Tiling(DENSE_RT, 128, 64, 4, 4)                              # the 128-row form
     assert plan(8192, 4096, 4096, WFMT_BF16, Tiling(DENSE_RT, 256, 64))[0] == \
         Tiling(DENSE_RT, 256, 64, 1, 2)                              # register-staged form
-    assert plan(511, 4096, 4096, WFMT_BF16)[0].rt != DENSE_RT       # tiled kernel below 512
+    assert plan(255, 4096, 4096, WFMT_BF16)[0].rt != DENSE_RT       # tiled kernel below 256
+    assert plan(256, 6144, 4096, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 8, 4)
+    assert plan(256, 4096, 12288, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 16, 4)
     assert plan(4096, 4096, 192, WFMT_BF16)[0] == Tiling(DENSE_RT, 256, 128, 1, 4)  # 6 stages of 32
     assert plan(4096, 4096, 4096, WFMT_W8)[0].rt != DENSE_RT        # bf16 weights only
     assert plan(64, 4096, 4096, WFMT_BF16, Tiling(DENSE_RT, 64, 0, 1, 4))[0] == \
