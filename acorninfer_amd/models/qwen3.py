@@ -58,8 +58,8 @@ LIBRARY_RT = -1
 # fields the bf16 kernel's). At prefill sizes the MFMA work dominates and that
 # kernel's rate outweighs the extra pass over the weights: on MI355X a W4A16
 # 8B prefill of 512 / 768 tokens takes 15.0 / 19.7 ms this way against
-# 15.9 / 25.4 ms on the int4 kernels; below 512 rows (where the bf16 kernel
-# is not the 256 x 256 form) the int4 kernels win (8.6 vs 13.4 ms at 256).
+# 15.9 / 25.4 ms on the int4 kernels; below 512 rows the int4 kernels win
+# (8.5-9.2 vs 12.8 ms at 256 tokens).
 DEQUANT_M_MIN = 512
 DEQUANT_RT = -4
 # prefill blocks from this many rows run gate|up with the large-M kernel's

@@ -83,7 +83,7 @@ class Tiling(NamedTuple):
     int4 mid-M kernel (WFMT_W4B, M > 16, rt == -3): upw row tiles per wave
     (1 / 2), nw waves (4 / 8), ksplit, tpw 128-k groups in flight (2 / 4);
     64 x rows per workgroup, streamed through LDS a group at a time.
-    Large-M bf16 kernel (the default for bf16 from 512 rows, or rt == -2):
+    Large-M bf16 kernel (the default for bf16 from 256 rows, or rt == -2):
     upw is the M tile. 64 / 128: nw the weight rows per wave (64 / 128; a
     workgroup's weight tile is 4 nw), tpw the weight prefetch depth in 64-k
     steps (2 / 4). 256 (256 x 256 tiles): nw 64 with tpw 2 stages both
