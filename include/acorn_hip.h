@@ -276,7 +276,7 @@ int acorn_gemm_swiglu_plan(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg);
  * dequantisation the reference's large-M quantised GEMM applies in-kernel
  * before its bf16 dot (acorninfer/ops/quant_gemm.py:175-183: int -> fp32 x
  * scale -> bf16). With acorn_quant_gemm on ACORN_WFMT_BF16 it forms the
- * int4 GEMM at prefill sizes (thousands of rows), where the bf16 MFMA kernel
+ * int4 GEMM at prefill sizes (from about 512 rows), where the bf16 MFMA kernel
  * outruns any in-kernel unpacking. N % 16 == 0, K % 512 == 0; out holds
  * N * K bf16 (the caller's workspace).
  */
