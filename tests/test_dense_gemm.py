@@ -101,17 +101,23 @@ def test_dense_gemm_matches_float64(wn, bm, depth):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M", [2048, 256, 300])
 @pytest.mark.parametrize("cls", list(CONFIG3))
-def test_dense_gemm_config3_at_prefill_m(cls):
-    """The default plan at M = 2048 (a 2048-token prompt) on configuration 3's
-    shapes, fp32 partials against the fp32 matmul of the same operands."""
+def test_dense_gemm_config3_at_prefill_m(cls, M):
+    """The default plan at M = 2048 (a 2048-token prompt) and at 256 / 300
+    rows (the smallest that take the 256 x 256 form, up to 16 K splits, a
+    ragged last tile) on configuration 3's shapes, fp32 partials against the
+    fp32 matmul of the same operands."""
+    from acorninfer_amd._lib import WFMT_BF16
+    from acorninfer_amd.ops.quant_gemm import plan
     N, K = CONFIG3[cls]
-    x, w = _operands(2048, N, K, 7)
+    assert plan(M, N, K, WFMT_BF16)[0][:3] == (DENSE_RT, 256, 128)
+    x, w = _operands(M, N, K, 7)
     xd, wd = x.cuda(), w.cuda()
     got = _run(xd, wd, None, True)
     ref = xd.float() @ wd.float().T
     rel = ((got - ref).norm() / ref.norm()).item()
-    print(f"\n[dense GEMM {cls} M=2048: rel err vs fp32 matmul {rel:.3g}]", flush=True)
+    print(f"\n[dense GEMM {cls} M={M}: rel err vs fp32 matmul {rel:.3g}]", flush=True)
     assert rel < 1e-5
 
 
