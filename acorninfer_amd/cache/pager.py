@@ -100,16 +100,18 @@ class PagedKVCache:
 
     def _check_rows(self, k, v, pages, slots) -> None:
         """The kernel indexes k/v with the pool's kv-head count and head size,
-        and writes (page, slot) into the pool: reject what does not fit (the
-        reference's torch indexing raises IndexError for an out-of-range
-        index; this costs one device-to-host read when pages/slots live on
-        the GPU)."""
+        and writes (page, slot) into the pool: reject what does not fit. With
+        pages/slots on the host an out-of-range target raises IndexError, as
+        the reference's torch indexing does. Targets already on the GPU are
+        not read back (that would synchronise the stream and break graph
+        capture): the scatter kernel skips a row whose (page, slot) lies
+        outside the pool and writes nothing for it."""
         for name, t in (("k", k), ("v", v)):
             assert t.dim() == 4 and t.shape[1] == self.num_kv_heads and \
                 t.shape[3] == self.head_dim, \
                 f"{name} is {tuple(t.shape)}; the pool holds {self.num_kv_heads} kv heads " \
                 f"of {self.head_dim}"
-        if pages.numel() == 0:
+        if pages.numel() == 0 or pages.is_cuda or slots.is_cuda:
             return
         bad = ((pages < 0) | (pages >= self.num_blocks)).any() | \
               ((slots < 0) | (slots >= self.page_size)).any()

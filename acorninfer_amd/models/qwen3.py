@@ -46,12 +46,10 @@ from acorninfer_amd.quant import quantize as Q
 MI355X_CUS = 256
 FORMATS = {"bf16": WFMT_BF16, "w8a16": WFMT_W8, "w4a16": WFMT_W4}
 # bf16 projections at prefill sizes run on the library's large-M kernel
-# (its planner's default from DENSE_M_MIN rows, tiling rt == DENSE_RT).
-# LIBRARY_RT is a tiling marker that sends a bf16 projection to torch.mm
-# (hipBLASLt) instead: a comparison point for tests and measurements only.
-DENSE_M_MIN = 512
+# (its planner's default from DENSE_M_MIN rows, tiling rt == DENSE_RT: the
+# 256 x 256 direct-to-LDS form; kDenseMinM in csrc/quant_gemm.hip).
+DENSE_M_MIN = 256
 DENSE_RT = -2
-LIBRARY_RT = -1
 # int4 (W4B) projections from DEQUANT_M_MIN rows: the weights are
 # dequantised to bf16 into a step workspace (acorn_dequant_w4b) and
 # multiplied by the large-M bf16 kernel (tiling rt == DEQUANT_RT, the other
@@ -186,14 +184,11 @@ class QLinear:
         return n
 
     def plan(self, M: int, tiling=None, workspace: bool = False):
-        """(Tiling, output tiles) from the library planner (a LIBRARY_RT
-        request is passed through: torch.mm). workspace: the caller holds a
-        bf16 weight workspace, so int4 weights take the dequantise + bf16
-        GEMM route by default from DEQUANT_M_MIN rows (a DEQUANT_RT request
-        takes it at any size)."""
+        """(Tiling, output tiles) from the library planner. workspace: the
+        caller holds a bf16 weight workspace, so int4 weights take the
+        dequantise + bf16 GEMM route by default from DEQUANT_M_MIN rows (a
+        DEQUANT_RT request takes it at any size)."""
         from acorninfer_amd.ops.quant_gemm import Tiling, plan
-        if tiling is not None and tiling[0] == LIBRARY_RT:
-            return Tiling(LIBRARY_RT, 0, 0, 1, 0), None
         if self.fmt == WFMT_W4B and (
                 (tiling is not None and tiling[0] == DEQUANT_RT) or
                 (workspace and (tiling is None or not any(tiling)) and M >= DEQUANT_M_MIN)):
@@ -221,14 +216,6 @@ class QLinear:
         dequantises into wtmp (bf16, at least N * K elements) first."""
         if self.fmt == _lib.WFMT_F32:
             part, out = (out if part is None else part), None
-        if tiling[0] == LIBRARY_RT:
-            # torch.mm (hipBLASLt) on torch's current stream, which is the step's
-            xs = x[:M]
-            if out is not None:
-                torch.mm(xs, self.w.t(), out=out[:M])
-            else:
-                torch.ops.aten.mm.dtype_out(xs, self.w.t(), torch.float32, out=part[0])
-            return
         if tiling[0] == DEQUANT_RT:
             self._dequant(wtmp, M, stream)
             arr = (ctypes.c_int * 6)(DENSE_RT, *tiling[1:], 0)
@@ -350,9 +337,8 @@ class Qwen3DecodeModel:
         # the shapes (False: K3 with one row per prompt token)
         self.tiled_prefill = True
         # projections of prefill rows: "own" (bf16 on the library's large-M
-        # kernel; int4 dequantised onto it from DEQUANT_M_MIN rows), "library"
-        # (bf16 on torch.mm, i.e. hipBLASLt) or "int4" (int4 weights on the
-        # int4 kernels at every size)
+        # kernel; int4 dequantised onto it from DEQUANT_M_MIN rows) or "int4"
+        # (int4 weights on the int4 kernels at every size)
         self.prefill_gemm = "own"
         # prefill blocks whose qkv / o / down run on the large-M kernel in one
         # split take their output in the activation dtype (half the bytes of
@@ -632,7 +618,7 @@ class Qwen3DecodeModel:
             def body():
                 for lin in lins:
                     if swiglu:
-                        lin.launch_swiglu(x, M, t, act, s.cuda_stream)
+                        lin.launch_swiglu(x, M, t, act, s.cuda_stream, wtmp=wtmp)
                     else:
                         lin.launch(x, M, t, part=part, wtmp=wtmp, stream=s.cuda_stream)
                         if with_act:   # the separate activation the fused form saves
@@ -844,11 +830,10 @@ class Qwen3DecodeModel:
                 self._extend_buf = None
                 lib_t = None
                 lw = self.layers[0]
-                if self.prefill_gemm == "library" and lw.qkv.fmt == WFMT_BF16:
-                    from acorninfer_amd.ops.quant_gemm import Tiling
-                    lt = Tiling(LIBRARY_RT, 0, 0, 1, 0)
-                    lib_t = {"qkv": lt, "o": lt, "gate_up": lt, "down": lt}
-                elif self.prefill_gemm == "int4" and lw.qkv.fmt == WFMT_W4B:
+                if self.prefill_gemm not in ("own", "int4"):
+                    raise ValueError(f"prefill_gemm must be 'own' or 'int4', not "
+                                     f"{self.prefill_gemm!r}")
+                if self.prefill_gemm == "int4" and lw.qkv.fmt == WFMT_W4B:
                     # the int4 planner's full choices (explicit: no dequantisation)
                     lib_t = {n: lin.plan(Rb)[0] for n, lin in (
                         ("qkv", lw.qkv), ("o", lw.o), ("gate_up", lw.gate_up),
@@ -987,7 +972,7 @@ class StepBuffers:
         lw = m.layers[0]
         tilings = self.tilings or {}
         # prefill blocks: the large-M kernel's SwiGLU epilogue unless a
-        # tiling is requested for gate|up (hipBLASLt, or the int4 kernels)
+        # tiling is requested for gate|up (the int4 kernels)
         self.swiglu = (m.prefill_swiglu(B) and "gate_up" not in tilings if self.prefill
                        else m.fused_swiglu(B))
         for name, lin in (("qkv", lw.qkv), ("o", lw.o), ("gate_up", lw.gate_up),

@@ -47,9 +47,13 @@ def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torc
     assert tables.is_contiguous() and seq_lens.is_contiguous()
     assert tables.dtype == torch.int32 and seq_lens.dtype == torch.int32
     assert k_pages.dtype == q.dtype == v_pages.dtype
+    # a sequence holds >= 1 token, so its table row holds >= 1 page (the
+    # width passed below is raised to 1 only for an empty batch)
+    assert B == 0 or tables.shape[1] >= 1, "tables must hold at least one page per sequence"
     q2 = q.contiguous()
     if out is None:
         out = torch.empty((B, H, D), dtype=q.dtype, device=q.device)
+    _check_out(out, (B, H, D), q)
     if workspace is None and S > 1:
         workspace = (torch.empty(B * H * S * D, dtype=torch.float32, device=q.device),
                      torch.empty(2 * B * H * S, dtype=torch.float32, device=q.device))
@@ -60,6 +64,14 @@ def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torc
         dtype_code(q2), stream_ptr(q.device))
     check(rc, "paged_decode_attention")
     return out
+
+
+def _check_out(out: torch.Tensor, shape: tuple, q: torch.Tensor) -> None:
+    """A caller-supplied output is written through its raw pointer: it must
+    be exactly the result's shape, dtype and device, and contiguous."""
+    assert tuple(out.shape) == tuple(shape), f"out must be {tuple(shape)}, not {tuple(out.shape)}"
+    assert out.dtype == q.dtype, f"out dtype {out.dtype} != q dtype {q.dtype}"
+    assert out.device == q.device and out.is_contiguous(), "out must be contiguous on q's device"
 
 
 def prefill_supported(dtype: torch.dtype, head_dim: int, page_size: int, num_heads: int,
@@ -93,9 +105,11 @@ def paged_prefill_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: tor
         assert t.dtype == torch.int32 and t.is_contiguous()
     assert k_pages.is_contiguous() and v_pages.is_contiguous()
     assert q.dtype == k_pages.dtype == v_pages.dtype
+    assert N == 0 or tables.shape[1] >= 1, "tables must hold at least one page per sequence"
     q2 = q.contiguous()
     if out is None:
         out = torch.empty_like(q2)
+    _check_out(out, (R, H, D), q)
     rc = lib().acorn_paged_prefill_attention(
         ptr(q2), ptr(k_pages), ptr(v_pages), ptr(tables), ptr(seq_row0), ptr(seq_pos0),
         ptr(seq_nq), ptr(out), N, R, int(max_nq), H, KV, D, P, NB, max(1, tables.shape[1]),

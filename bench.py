@@ -23,9 +23,12 @@ The JSON line also carries:
 - extra (unless --no-extra): the reference's decode_batch protocol (one
   host copy per step) at the headline size, other batch sizes and formats
   (W4A16 and W8A16 at C=8 with their own GEMM rooflines, configuration 5),
-  the batched prefill (C x 512, and one 8192-token prompt with the bf16
-  projections on this library's large-M kernel and on hipBLASLt) and
+  the batched prefill (C x 512, and one 8192-token prompt) and
   configuration 4 end to end through the Engine.
+- decode: the metric's figures in one object (bf16 / W4A16 tok/s at C=1 and
+  C=8, W8A16 at C=8, each format's GEMM fraction of peak in a graph of the
+  step's GEMM launches and inside the step, K3's fraction at configurations
+  2 and 5); the run's last stderr lines restate them.
 - extra.kernels (unless --no-kernels): the isolated kernels at
   configurations 2 (K3, K1, K2), 5 (K3 + combine over one layer's pages at
   C=8 and C=64; prefill attention over an 8192-token prompt and 8 x 512
@@ -122,9 +125,7 @@ def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int,
     elif tune:
         t0 = time.perf_counter()
         report = model.tune(batch)
-        _log(f"tuned C={batch} in {time.perf_counter() - t0:.1f} s: " + ", ".join(
-            f"{k} {v['tiling']} {v['us']:.1f}us {v['bytes'] / v['us'] / 1e3:.0f}GB/s"
-            for k, v in report.items()))
+        _log(f"tuned {fmt} C={batch} in {time.perf_counter() - t0:.1f} s")
     P = 16
     lens = prompt_lens if prompt_lens is not None else [prompt_len] * batch
     max_len = max(lens) + total_steps + 1
@@ -578,9 +579,9 @@ def dense_gemm_benchmarks(seed: int) -> dict:
             fl = 2.0 * M * n * k
             us, us_lib = _time_graph(own, 3) / 4, _time_graph(library, 3) / 4
             out[f"dense_gemm_{name}_M{M}"] = {
-                "us": round(us, 1), "TFLOPs": round(fl / us / 1e6, 1),
+                "us": round(us, 1),
                 "frac_mfma": round(fl / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
-                "hipblaslt_us": round(us_lib, 1), "tiling": list(t)}
+                "hipblaslt_us": round(us_lib, 1)}
             del x, w, part
     torch.cuda.empty_cache()
     return out
@@ -646,11 +647,10 @@ def gemm_benchmarks(seed: int, gemm_ms=(1, 8, 64, 256), fixed: dict | None = Non
                 nb = lins[0].nbytes() + 2 * M * k + 2 * M * n
                 flops = 2 * M * n * k
                 out[f"gemm_{key}"] = {
-                    "us": round(best[0], 2), "GBps": round(nb / best[0] / 1e3, 1),
+                    "us": round(best[0], 2),
                     "frac_hbm": round(nb / best[0] / 1e3 / HBM_PEAK_GBS, 4),
-                    "TFLOPs": round(flops / best[0] / 1e6, 2),
                     "frac_mfma": round(flops / best[0] / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
-                    "tiling": tuple(t), "candidates": len(first)}
+                    "tiling": ",".join(map(str, t))}
             del lins
             torch.cuda.empty_cache()
     return out
@@ -809,6 +809,60 @@ def gpu_config1(seed: int = 20261027, new_tokens: int = 32, prompt_len: int = 32
     return out
 
 
+def decode_summary(tok_s, ms, gbs, nbytes, args, extra) -> dict:
+    """The metric's decode figures in one place: tok/s of bf16 / W4A16 at
+    C=1 and C=8 and W8A16 at C=8, each format's GEMM fraction of the 8 TB/s
+    peak (timed as a graph of the step's GEMM launches, and inside the
+    captured step from the committed profile), and K3's fraction at
+    configurations 2 and 5. Figures a --no-extra / --no-kernels run skips
+    are None."""
+    head = f"{args.format}_C{args.batch}"
+    out = {f"{head}_tok_s": round(tok_s, 2), f"{head}_ms_per_step": round(ms, 4)}
+    for k in ("bf16_C1", "w4a16_C8", "w4a16_C1", "w8a16_C8"):
+        if k != head:
+            out[f"{k}_tok_s"] = extra.get(f"{k}_tok_s")
+            out[f"{k}_ms_per_step"] = extra.get(f"{k}_ms_per_step")
+    ins = in_step_gemm(args.format, args.batch, nbytes)
+    graph = {head: round(gbs / HBM_PEAK_GBS, 4)}
+    in_step = {head: ins["frac"] if ins else None}
+    for fmt in ("w4a16", "w8a16"):
+        r = extra.get(f"{fmt}_C8_gemm_roofline")
+        if r:
+            graph[f"{fmt}_C8"] = r["frac"]
+            in_step[f"{fmt}_C8"] = r["in_step"]["frac"] if r.get("in_step") else None
+    out["gemm_frac_graph"] = graph
+    out["gemm_frac_in_step"] = in_step
+    kern = extra.get("kernels", {})
+    out["K3_frac"] = {k: kern[f"K3_{k}"]["frac"] for k in ("config2", "config5_C8", "config5_C64")
+                      if f"K3_{k}" in kern}
+    return out
+
+
+def summary_lines(line: dict) -> list[str]:
+    """A few short lines that restate the decode figures at the end of the
+    run's output (a reader of the last lines sees the whole metric)."""
+    d = line["decode"]
+
+    def f(v, nd=1):
+        return "n/a" if v is None else f"{v:.{nd}f}"
+
+    toks = " | ".join(f"{k[:-6].replace('_', ' ')} {f(v)}" for k, v in d.items()
+                      if k.endswith("_tok_s"))
+    gemm = " | ".join(f"{k} {f(v, 3)}/{f(d['gemm_frac_in_step'].get(k), 3)}"
+                      for k, v in d["gemm_frac_graph"].items())
+    k3 = " | ".join(f"{k} {f(v, 3)}" for k, v in d["K3_frac"].items()) or "n/a"
+    cpu = line.get("cpu_baseline")
+    out = [f"summary decode tok/s: {toks}",
+           f"summary GEMM frac of 8 TB/s (graph/in-step): {gemm}",
+           f"summary K3 frac of 8 TB/s: {k3}",
+           f"summary value {line['value']} {line['unit']} at {line['ms_per_step']} ms/step; "
+           f"roofline frac {line['roofline']['frac']}"]
+    if cpu:
+        out.append(f"summary cpu baseline: {cpu['value']} {cpu['unit']} on {cpu['cores']} "
+                   f"threads ({cpu['kind']})")
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -931,16 +985,13 @@ def main() -> None:
             extra[f"bf16_prefill_C{c}_ms"] = round(ms_p, 3)
             extra[f"bf16_prefill_C{c}_tok_s"] = round(tps, 1)
             _log(f"bf16 prefill C={c} x {args.prompt_len}: {ms_p:.2f} ms ({tps:.0f} tok/s)")
-        # configuration 5's longest prompt: one 8192-token prefill, with the
-        # projections on this library's large-M kernel and on hipBLASLt
-        for how in ("own", "library"):
-            model.prefill_gemm = how
-            ms_p, tps = prefill_benchmark(model, cfg, 1, 8192, args.seed + 8, reps=2)
-            sfx = "" if how == "own" else "_hipblaslt_gemm"
-            extra[f"bf16_prefill_1x8192{sfx}_ms"] = round(ms_p, 3)
-            extra[f"bf16_prefill_1x8192{sfx}_tok_s"] = round(tps, 1)
-            _log(f"bf16 prefill 1 x 8192 ({how} GEMM): {ms_p:.2f} ms ({tps:.0f} tok/s)")
-        model.prefill_gemm = "own"
+        # configuration 5's longest prompt: one 8192-token prefill (the
+        # projections on this library's large-M kernel; its GEMMs against
+        # hipBLASLt are in kernels.dense_gemm_*)
+        ms_p, tps = prefill_benchmark(model, cfg, 1, 8192, args.seed + 8, reps=2)
+        extra["bf16_prefill_1x8192_ms"] = round(ms_p, 3)
+        extra["bf16_prefill_1x8192_tok_s"] = round(tps, 1)
+        _log(f"bf16 prefill 1 x 8192: {ms_p:.2f} ms ({tps:.0f} tok/s)")
         model._extend_buf = None
         # configuration 4 end to end through the Engine (prefill + decode)
         del cache, runner
@@ -1033,14 +1084,14 @@ def main() -> None:
     if not args.no_kernels:
         t0 = time.perf_counter()
         extra["kernels"] = kernel_benchmarks()
-        _log(f"kernel benchmarks in {time.perf_counter() - t0:.1f} s: {extra['kernels']}")
+        _log(f"kernel benchmarks in {time.perf_counter() - t0:.1f} s")
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
         cpu = cpu_baseline()
         cpu["gpu_same_workload"] = gpu_config1()
-        _log(f"cpu baseline (configuration 1) {cpu['value']} tok/s, GPU "
-             f"{cpu['gpu_same_workload']} in {time.perf_counter() - t0:.1f} s")
+        _log(f"cpu baseline (configuration 1) {cpu['value']} tok/s in "
+             f"{time.perf_counter() - t0:.1f} s")
     line = {
         "metric": "decode tok/s Qwen3-8B C=1/8 (bf16, W4A16); kernel HBM GB/s vs 8 TB/s peak",
         "value": round(tok_s, 2),
@@ -1058,6 +1109,7 @@ def main() -> None:
                                f"{args.prompt_len}, {args.format}, hipGraph step, page 16",
                    "batch": args.batch, "prompt_len": args.prompt_len,
                    "layers": cfg.num_hidden_layers, "weights": args.format},
+        "decode": decode_summary(tok_s, ms, gbs, nbytes, args, extra),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(args.format, args.batch),
@@ -1067,7 +1119,9 @@ def main() -> None:
         "cpu_baseline": cpu,
         "extra": extra,
     }
-    print(json.dumps(line), flush=True)
+    print(json.dumps(line, separators=(",", ":")), flush=True)
+    for msg in summary_lines(line):
+        _log(msg)
 
 
 if __name__ == "__main__":

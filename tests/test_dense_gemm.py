@@ -1,5 +1,6 @@
 """Large-M bf16 GEMM (csrc/dense_gemm.hip, the bf16 projections at prefill
-sizes: acorninfer/models/qwen3.py:21-47's F.linear for M >= 512 rows).
+sizes: acorninfer/models/qwen3.py:21-47's F.linear; the planner's default
+from 256 rows, DENSE_M_MIN).
 
 Oracle: the float64 product of the same bf16 operands. fp32 output must
 match it to fp32 accumulation drift (a dropped k step, a wrong row or column,

@@ -132,16 +132,23 @@ def test_extend_in_chunks_equals_one_shot_bf16():
 
 
 @pytest.mark.gpu
-def test_prefill_at_dense_gemm_sizes_bf16_matches_oracle():
-    """>= 512 rows: the bf16 projections run on the large-M GEMM kernel."""
-    from acorninfer_amd.models.qwen3 import DENSE_M_MIN, DENSE_RT
+@pytest.mark.parametrize("lens", [(600, 500), (200, 100)])
+def test_prefill_at_dense_gemm_sizes_bf16_matches_oracle(lens):
+    """>= DENSE_M_MIN (256) rows: the bf16 projections run on the large-M
+    GEMM kernel with the planner's default split. 300 rows take its 8-16
+    K-split plans through the qkv epilogue, K1 and silu_mul (no SwiGLU
+    epilogue below 512 rows); 1100 rows the SwiGLU epilogue."""
+    from acorninfer_amd.models.qwen3 import DENSE_M_MIN, DENSE_RT, PREFILL_SWIGLU_M
     cfg = Qwen3Config.qwen3_0_6b().with_layers(2)
     sd = random_state_dict(cfg, seed=SEED + 5, std=0.02, dtype=torch.bfloat16)
-    prompts = [_ids(n, cfg.vocab_size, SEED + 20 + n) for n in (600, 500)]
-    assert sum(len(p) for p in prompts) >= DENSE_M_MIN
+    prompts = [_ids(n, cfg.vocab_size, SEED + 20 + n) for n in lens]
+    rows = sum(len(p) for p in prompts)
+    assert rows >= DENSE_M_MIN
     ref = Qwen3Ref(cfg, sd, torch.bfloat16)
     model = Qwen3DecodeModel.from_state_dict(cfg, sd, weight_format="bf16", device="cuda")
-    assert model.layers[0].qkv.plan(1100)[0][0] == DENSE_RT
+    for lin in (model.layers[0].qkv, model.layers[0].o, model.layers[0].down):
+        assert lin.plan(rows)[0][0] == DENSE_RT
+    assert model.prefill_swiglu(rows) == (rows >= PREFILL_SWIGLU_M)
     alloc, cache = new_cache(model, 80)
     views = [PagedCacheView(cache) for _ in prompts]
     got = model.forward_prefill_batch(_padded(prompts, model.device), views,

@@ -3,7 +3,8 @@ the C-ABI: on two calls in a row (the second smaller) its output equals
 acorn_paged_attention's with caller-owned workspaces bit for bit (the same
 kernels) and the oracle within the bf16 bar; a request beyond the fixed
 scratch is refused with ACORN_ERR_SCRATCH before anything is launched; one
-split needs no scratch at any size."""
+split needs no scratch at any size; after one warm-up call the entry point
+records into a hipGraph and every replay equals the workspace entry point."""
 import pytest
 import torch
 
@@ -54,10 +55,14 @@ def test_noalloc_equals_workspace_entry_on_two_calls_second_smaller():
         want = torch.empty_like(q)
         got = torch.full_like(q, float("nan"))
         assert _call(False, q, kp, vp, tables, lens, S, want) == 0
-        before = torch.cuda.memory_allocated()
+        torch.cuda.synchronize()
+        # torch's allocator and the device's free memory (a hipMalloc inside
+        # the library would show in the second)
+        before, free_before = torch.cuda.memory_allocated(), torch.cuda.mem_get_info()[0]
         assert _call(True, q, kp, vp, tables, lens, S, got) == 0
         torch.cuda.synchronize()
         assert torch.cuda.memory_allocated() == before
+        assert torch.cuda.mem_get_info()[0] == free_before
         assert torch.equal(got, want)
         torch.testing.assert_close(got.cpu(), paged_attention_ref(*host), **TOL_BF16)
 
@@ -81,3 +86,31 @@ def test_noalloc_refuses_more_than_its_scratch():
     assert _call(False, q, kp, vp, tables, lens, 1, want) == 0
     torch.cuda.synchronize()
     assert torch.equal(out, want)
+
+
+@pytest.mark.gpu
+def test_noalloc_graph_capture_replays_bitwise():
+    """Captured after one warm-up call (which looks up the scratch address),
+    the entry point replays with the same bits as the workspace entry point,
+    replay after replay, with eager work and synchronisation in between."""
+    B, S = 8, 64
+    host = _inputs(B, 512, 4096, 256, 11)
+    q, kp, vp, tables, lens = (t.cuda() for t in host)
+    want = torch.empty_like(q)
+    assert _call(False, q, kp, vp, tables, lens, S, want) == 0
+    out = torch.empty_like(q)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        assert _call(True, q, kp, vp, tables, lens, S, out) == 0     # warm-up
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            assert _call(True, q, kp, vp, tables, lens, S, out) == 0
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {rep}"
