@@ -17,8 +17,9 @@ __device__ __forceinline__ f32x4 mfma(u32x4 a, u32x4 b, f32x4 c) {
                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// int4: 8 nibbles (columns c..c+7) -> bf16 (128+u) in MFMA item order
-// (p, p+4) per dword.
+// int4: the 8 nibbles of a W4B word -> bf16 (128+u) pairs (nibble q, nibble
+// q+4), q = 0..3: in the W4B nibble order (k offsets 0,2,4,6,1,3,5,7) that is
+// k offsets (2q, 2q+1), the natural order of x.
 // The mask and the bias are made opaque register values (an SGPR and a VGPR):
 // with literal operands the compiler emits v_and_b32 + v_or_b32 (gfx950's
 // VOP3 forms take no literal), with registers it can use one v_and_or_b32.
@@ -32,17 +33,6 @@ __device__ __forceinline__ u32x4 unpack_w4(uint32_t w) {
   r[2] = ((w >> 8) & m) | c;
   r[3] = ((w >> 12) & m) | c;
   return r;
-}
-
-// x staged for the int4 kernels: the 8 bf16 of a 16-byte piece reordered to
-// [x0,x4,x1,x5,x2,x6,x3,x7], unpack_w4's pairing of the nibbles of a dword.
-__device__ __forceinline__ u32x4 w4_order_x(u32x4 w) {
-  u32x4 t;
-  t[0] = __builtin_amdgcn_perm(w[2], w[0], 0x05040100u);
-  t[1] = __builtin_amdgcn_perm(w[2], w[0], 0x07060302u);
-  t[2] = __builtin_amdgcn_perm(w[3], w[1], 0x05040100u);
-  t[3] = __builtin_amdgcn_perm(w[3], w[1], 0x07060302u);
-  return t;
 }
 
 // NDW consecutive dwords from a 4*NDW-byte aligned address (one vector load
@@ -67,11 +57,23 @@ __device__ __forceinline__ void load_dwords(const void* p, uint32_t (&d)[NDW]) {
   }
 }
 
-// fp16 number h of a run of packed halves, as float; used as an FMA operand
-// the conversion folds into v_fma_mix_f32's operand select.
+// s_h * v + acc in fp32, s_h the fp16 number h of a run of packed halves
+// (exactly converted): one v_fma_mix_f32 that selects the half of the packed
+// dword itself. It is asm because the compiler, left to convert the half,
+// shifts the high halves out right where their load is issued, which makes it
+// wait for that load there (and, as loads complete in order, for every load
+// before it): a register ring of weight and scale loads then never has more
+// than one stage in flight. h must fold to a constant.
 template <int NDW>
-__device__ __forceinline__ float half_f(const uint32_t (&d)[NDW], int h) {
-  return (float)__builtin_bit_cast(h16x2, d[h / 2])[h & 1];
+__device__ __forceinline__ float fma_half(const uint32_t (&d)[NDW], int h, float v, float acc) {
+  float r;
+  if (h & 1)
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=v"(r) : "v"(d[h / 2]), "v"(v), "v"(acc));
+  else
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]"
+        : "=v"(r) : "v"(d[h / 2]), "v"(v), "v"(acc));
+  return r;
 }
 
 // SwiGLU epilogue of the fused gate|up projection: g, u rounded to bf16,
@@ -88,7 +90,9 @@ __device__ __forceinline__ float swiglu_bf16(float g, float u) {
 // ---- W4B: int4 weights in 1 KB blocks (ACORN_WFMT_W4B) -------------------
 // Block (n/16, g) holds rows 16*(n/16) .. +15 x the 128 k of group g as one
 // wave's MFMA A operand: lane (c%4)*16 + n%16 has the 16 bytes of row n,
-// k in [32c, 32c+32) (c = k/32 within the tensor, natural nibble order).
+// k in [32c, 32c+32) (c = k/32 within the tensor); word j of those bytes
+// holds k 32c + 8j .. + 7 with nibble p (bits 4p..4p+3) at k offset
+// 0,2,4,6,1,3,5,7 for p = 0..7.
 __host__ __device__ inline size_t w4b_chunk_offset(int64_t n, int64_t c, int64_t K) {
   return ((size_t)(n / 16) * (size_t)(K / 128) + (size_t)(c / 4)) * 1024 +
          (size_t)((c % 4) * 16 + n % 16) * 16;
@@ -100,15 +104,18 @@ __host__ __device__ inline size_t w4b_half_index(int64_t n, int64_t g, int64_t K
          (size_t)((n % 16) / 4) * 16 + (size_t)(g % 4) * 4 + (size_t)(n % 4);
 }
 
-// ---- the W4B decode kernel (w4_decode.hip), M <= 64 -------------------------
+// ---- the W4B decode kernels (w4_decode.hip), M <= 64 ------------------------
 // cfg knobs: rt (row tiles of 16 per wave), upw (groups per pipeline stage),
-// nw (waves per workgroup; 10*nw + kw when kw waves share rows and split K),
-// ksplit, depth (stages in flight per wave); 0 = choose.
+// nw (waves per workgroup; above 16 rows 10*nw + kw when kw waves share rows
+// and split K), ksplit, depth (stages in flight per wave); 0 = choose.
+// M <= 16 runs the direct kernel (x read into MFMA registers by every wave),
+// 16 < M <= 64 the kernel that stages x in LDS.
 struct W4bPlan {
+  bool direct;     // the M <= 16 kernel
   int rt, upw, nw, ksplit, depth;
   int kw;          // K slices per row group (waves sharing rows)
   int nw_field;    // the cfg value of nw (nw, or 10*nw + kw)
-  int R;           // x rows staged in LDS (power of 2 >= M)
+  int R;           // x rows staged in LDS (16 mb; M for the direct kernel)
   int mb;          // 16-column blocks of x per wave (M <= 16 mb)
   int groups;      // workgroups along N
   size_t lds;      // dynamic LDS bytes

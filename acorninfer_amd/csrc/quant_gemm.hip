@@ -65,6 +65,18 @@ template <> struct Fmt<ACORN_WFMT_W4> {
 // int4 in either layout (natural rows, or the 1 KB blocks of W4B)
 template <int WFMT> constexpr bool kIsW4 = WFMT == ACORN_WFMT_W4 || WFMT == ACORN_WFMT_W4B;
 
+// x staged for the streaming kernel over natural-layout int4 (low nibble =
+// even k): the 8 bf16 of a 16-byte piece reordered to [x0,x4,x1,x5,x2,x6,x3,
+// x7], unpack_w4's pairing (nibble q, nibble q+4) of a natural word.
+__device__ __forceinline__ u32x4 w4_order_x(u32x4 w) {
+  u32x4 t;
+  t[0] = __builtin_amdgcn_perm(w[2], w[0], 0x05040100u);
+  t[1] = __builtin_amdgcn_perm(w[2], w[0], 0x07060302u);
+  t[2] = __builtin_amdgcn_perm(w[3], w[1], 0x05040100u);
+  t[3] = __builtin_amdgcn_perm(w[3], w[1], 0x07060302u);
+  return t;
+}
+
 // Byte I of v as float (selects v_cvt_f32_ubyteI).
 template <int I> __device__ __forceinline__ float ubyte_f32(uint32_t v) {
   return (float)((v >> (8 * I)) & 0xffu);
@@ -594,10 +606,18 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
         // bit-field extract per nibble ahead of each v_cvt_f32_ubyteN
         asm volatile("" : "+v"(lo), "+v"(hi));
         u32x4 o;
-        o[0] = pack_bf16x2(ubyte_f32<0>(lo) * gs + gz, ubyte_f32<0>(hi) * gs + gz);
-        o[1] = pack_bf16x2(ubyte_f32<1>(lo) * gs + gz, ubyte_f32<1>(hi) * gs + gz);
-        o[2] = pack_bf16x2(ubyte_f32<2>(lo) * gs + gz, ubyte_f32<2>(hi) * gs + gz);
-        o[3] = pack_bf16x2(ubyte_f32<3>(lo) * gs + gz, ubyte_f32<3>(hi) * gs + gz);
+        if constexpr (WFMT == ACORN_WFMT_W4B) {
+          // W4B nibble order: lo's bytes are k offsets 0, 4, 1, 5 and hi's 2, 6, 3, 7
+          o[0] = pack_bf16x2(ubyte_f32<0>(lo) * gs + gz, ubyte_f32<2>(lo) * gs + gz);
+          o[1] = pack_bf16x2(ubyte_f32<0>(hi) * gs + gz, ubyte_f32<2>(hi) * gs + gz);
+          o[2] = pack_bf16x2(ubyte_f32<1>(lo) * gs + gz, ubyte_f32<3>(lo) * gs + gz);
+          o[3] = pack_bf16x2(ubyte_f32<1>(hi) * gs + gz, ubyte_f32<3>(hi) * gs + gz);
+        } else {
+          o[0] = pack_bf16x2(ubyte_f32<0>(lo) * gs + gz, ubyte_f32<0>(hi) * gs + gz);
+          o[1] = pack_bf16x2(ubyte_f32<1>(lo) * gs + gz, ubyte_f32<1>(hi) * gs + gz);
+          o[2] = pack_bf16x2(ubyte_f32<2>(lo) * gs + gz, ubyte_f32<2>(hi) * gs + gz);
+          o[3] = pack_bf16x2(ubyte_f32<3>(lo) * gs + gz, ubyte_f32<3>(hi) * gs + gz);
+        }
         *(u32x4*)(wd + 8 * d) = o;
       }
     } else if constexpr (WFMT == ACORN_WFMT_W8) {

@@ -11,12 +11,155 @@
 //    16-byte load per lane (whole cache lines, non-temporal policy) and feeds
 //    four v_mfma_f32_16x16x32_bf16 from it; no data moves between lanes.
 //  * int4 -> bf16 (128 + u): one v_and_or_b32 per bf16 pair, plus a shift for
-//    three of the four pairs of a dword. The k pairing this implies is applied
-//    to x once, when x is staged in LDS.
+//    three of the four pairs of a dword. The layout stores each dword's
+//    nibbles in the order that pairing needs (k offsets 0,2,4,6 | 1,3,5,7), so
+//    the unpacked operand is in natural k order and x is used as it is.
 //  * Per group: y += s * (C - 136 X), C the group's MFMA sum over the biased
-//    weights and X the sum of x over the group (one MFMA against ones per
-//    group, once per workgroup): two VALU per output row and group; the fp16
-//    scale is read from its packed pair by v_fma_mix_f32.
+//    weights and X the sum of x over the group; the fp16 scale is read from
+//    its packed pair by v_fma_mix_f32.
+//  * Split-K (ksplit > 1) writes fp32 partials [ksplit, M, N], summed in split
+//    order by the consumer (bitwise deterministic).
+//
+// Two kernels:
+//  * M <= 16 (decode buckets up to 16): w4b_direct_kernel. Every wave is
+//    independent: its x operands come from memory (L2) straight into MFMA B
+//    registers with its weights, so no wave waits for a workgroup to stage x
+//    or for a barrier before its first MFMA. X and the bias come from one more
+//    MFMA chain per group (a constant -136 operand against x) that seeds the
+//    tiles' accumulators.
+//  * 16 < M <= 64 (decode buckets of 32 and 64, configuration 3's M = 64):
+//    w4b_decode_kernel, MB = 2 or 4 16-column blocks of x per wave with x
+//    staged in LDS by the workgroup (every unpacked weight operand feeds MB
+//    MFMAs and every x operand RT, so the same loads carry MB times the
+//    arithmetic).
+#include "gemm_common.h"
+
+using namespace acorn;
+
+namespace {
+
+// ---- M <= 16 ----------------------------------------------------------------
+struct W4dArgs {
+  const __bf16* x;
+  const uint8_t* w;
+  const _Float16* scale;
+  __bf16* out;    // bf16 [M, N] (act [M, N/2] with SWIGLU) when ksplit == 1
+  float* part;    // fp32 [ksplit, M, N] otherwise
+  int M, N, K;
+  int kr;         // K range of a split (a multiple of 128 * UPW * DEPTH)
+};
+
+template <int RT, int UPW>
+struct DStage {
+  u32x4 w[RT][UPW];          // unit (rt, u): this lane's 16 bytes of block (tile, group)
+  u32x4 x[UPW][4];           // B operand of MFMA j of group u: x row lr, k 32 lg + 8 j ..
+  uint32_t s[RT][2 * UPW];   // fp16 scales: half 4u + i is row 4 lg + i of group u
+};
+
+// bf16 -136 in every slot: an MFMA of it against x gives -136 X per column
+constexpr uint32_t kNeg136x2 = 0xC308C308u;
+
+// Grid: x = tile groups of NW * RT 16-row tiles, y = ksplit; block NW waves.
+// Wave w of workgroup b owns tiles (b NW + w) RT .. + RT - 1 over the split's K
+// range, DEPTH stages of UPW groups in flight. Lane (lr, lg) holds x row
+// min(lr, M - 1) (rows past M feed only columns that are never stored).
+template <int RT, int UPW, int DEPTH, int NW, bool SWIGLU>
+__global__ __launch_bounds__(NW * kWave) void w4b_direct_kernel(W4dArgs a) {
+  const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lg = lane >> 4, lr = lane & 15;
+  const int G = a.K / 128, G4 = a.K / 512;
+  const int t0 = (blockIdx.x * NW + wid) * RT;
+  const bool active = t0 < a.N / 16;              // (N / 16) % RT == 0 by the plan
+  const int tt = active ? t0 : 0;                 // idle waves read tile 0, store nothing
+  const int kr0 = blockIdx.y * a.kr;
+  const unsigned g0 = (unsigned)(kr0 / 128);
+  const int ns = a.kr / (128 * UPW);              // stages, a multiple of DEPTH
+  const uint8_t* wb = a.w + ((size_t)tt * G + g0) * 1024 + lane * 16;
+  const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kr0 + 32 * lg;
+  const _Float16* sb = a.scale + (size_t)tt * G4 * 64 + lg * 16;
+  auto load = [&](int s, DStage<RT, UPW>& r) {
+#pragma unroll
+    for (int u = 0; u < UPW; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r.x[u][j] = *(const u32x4*)(xb + (s * UPW + u) * 128 + 8 * j);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int u = 0; u < UPW; ++u)
+        r.w[rt][u] = load_nt((const u32x4*)(wb + ((size_t)rt * G + s * UPW + u) * 1024));
+    const unsigned g = g0 + (unsigned)(s * UPW);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+      load_dwords(sb + (size_t)rt * G4 * 64 + (g / 4) * 64 + (g % 4) * 4, r.s[rt]);
+  };
+
+  DStage<RT, UPW> ring[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+  f32x4 acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const u32x4 neg136 = {kNeg136x2, kNeg136x2, kNeg136x2, kNeg136x2};
+  auto compute = [&](const DStage<RT, UPW>& r) {
+#pragma unroll
+    for (int u = 0; u < UPW; ++u) {
+      f32x4 xb136 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xb136 = mfma(neg136, r.x[u][j], xb136);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        f32x4 cc = xb136;                          // C - 136 X
+#pragma unroll
+        for (int j = 0; j < 4; ++j) cc = mfma(unpack_w4(r.w[rt][u][j]), r.x[u][j], cc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[rt][i] = fma_half(r.s[rt], 4 * u + i, cc[i], acc[rt][i]);
+      }
+      // one group at a time: without this fence the scheduler hoists the
+      // unpacking of later groups and the register ring no longer fits
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  int s0 = 0;
+  for (; s0 + DEPTH < ns; s0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      compute(ring[d]);
+      load(s0 + DEPTH + d, ring[d]);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) compute(ring[d]);
+  if (!active || lr >= a.M) return;
+
+  // lane (lr, lg) holds rows 4 lg .. 4 lg + 3 of each tile, column (x row) lr
+  if constexpr (SWIGLU) {
+    // tiles 2p (gate) and 2p + 1 (up) hold the 16 outputs of block t0 / 2 + p
+    const int NA = a.N / 2;
+#pragma unroll
+    for (int p = 0; p < RT / 2; ++p) {
+      const int n = (t0 / 2 + p) * 16 + 4 * lg;
+      uint32_t v[2];
+      v[0] = pack_bf16x2(swiglu_bf16(acc[2 * p][0], acc[2 * p + 1][0]),
+                         swiglu_bf16(acc[2 * p][1], acc[2 * p + 1][1]));
+      v[1] = pack_bf16x2(swiglu_bf16(acc[2 * p][2], acc[2 * p + 1][2]),
+                         swiglu_bf16(acc[2 * p][3], acc[2 * p + 1][3]));
+      __builtin_memcpy(a.out + (size_t)lr * NA + n, v, sizeof(v));
+    }
+  } else if (a.out) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int n = (t0 + rt) * 16 + 4 * lg;
+      uint32_t v[2] = {pack_bf16x2(acc[rt][0], acc[rt][1]), pack_bf16x2(acc[rt][2], acc[rt][3])};
+      __builtin_memcpy(a.out + (size_t)lr * a.N + n, v, sizeof(v));
+    }
+  } else {
+    float* dst = a.part + ((size_t)blockIdx.y * a.M + lr) * a.N;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) *(f32x4*)(dst + (t0 + rt) * 16 + 4 * lg) = acc[rt];
+  }
+}
+
+// ---- 16 < M <= 64 -----------------------------------------------------------
 //  * The waves of a workgroup share the staged x. They form NW/KW row groups
 //    of RT row tiles; the KW waves of a row group split the workgroup's K
 //    range and add their results through LDS in fixed order at the end
@@ -26,27 +169,16 @@
 //  * Each wave keeps DEPTH stages (UPW groups x RT row tiles) of loads in
 //    flight. Every load is unconditional and the stage count is a multiple
 //    of DEPTH, so the compiler's wait counts are static.
-//  * Split-K (ksplit > 1) writes fp32 partials [ksplit, M, N], summed in split
-//    order by the consumer (bitwise deterministic).
-//  * M up to 64 (a decode bucket of 32 or 64 sequences, configuration 3's
-//    M = 64): MB = ceil(M / 16) column blocks of x per wave. Every unpacked
-//    weight operand feeds MB MFMAs and every x operand RT, so the same loads
-//    carry MB times the arithmetic; x is staged for 16 MB rows.
-#include "gemm_common.h"
-
-using namespace acorn;
-
-namespace {
-
+//  * X per (group, column) is an MFMA of ones against the staged x, once per
+//    workgroup.
 struct W4bArgs {
   const __bf16* x;
   const uint8_t* w;
   const _Float16* scale;
-  __bf16* out;    // bf16 [M, N] (act [M, N/2] with SWIGLU) when ksplit == 1
+  __bf16* out;    // bf16 [M, N] when ksplit == 1
   float* part;    // fp32 [ksplit, M, N] otherwise
   int M, N, K;
   int kr;         // K range of a workgroup (a multiple of 128 * KW * UPW * DEPTH)
-  int log2R;      // x rows staged = 1 << log2R >= M (16 MB when MB > 1)
 };
 
 template <int RT, int UPW>
@@ -56,16 +188,16 @@ struct Stage {
 };
 
 // Grid: x = groups of (NW/KW)*RT row tiles, y = ksplit. Block: NW waves.
-// MB: 16-column blocks of x (MB = 1: M <= 16, R rows staged; else R = 16 MB).
-template <int RT, int UPW, int DEPTH, int NW, int KW, bool SWIGLU, int MB = 1>
+// MB: 16-column blocks of x (2 or 4; R = 16 MB rows staged).
+template <int RT, int UPW, int DEPTH, int NW, int KW, int MB>
 __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   static_assert(NW % KW == 0, "K slices divide the waves");
-  constexpr int RS = 16 * MB;                     // x-sum columns per group
+  static_assert(MB == 2 || MB == 4, "M <= 16 is the direct kernel's");
+  constexpr int R = 16 * MB;                      // x rows staged
   constexpr int NT = NW * kWave;
   extern __shared__ __align__(16) unsigned char smem[];
   const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lg = lane >> 4, lr = lane & 15;
-  const int R = 1 << a.log2R;
   const int KR = a.kr, kr0 = blockIdx.y * KR;
   const int GR = KR / 128, CPR = KR / 8;
   const int G = a.K / 128, G4 = a.K / 512;
@@ -73,7 +205,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   const int t0 = (blockIdx.x * (NW / KW) + rg) * RT;   // the row group's first tile
   const bool active = t0 < a.N / 16;              // (N / 16) % RT == 0 by the plan
   const int tt = active ? t0 : 0;                 // idle waves read tile 0, store nothing
-  // LDS: x pieces [CPR][R] (16 bytes each, W4 k order) | group sums [GR][RS]
+  // LDS: x pieces [CPR][R] (16 bytes each) | group sums [GR][R]
   //      | K-slice results [NW][RT][MB][4][64] (KW > 1)
   u32x4* xs = (u32x4*)smem;
   float* xgs = (float*)(smem + (size_t)CPR * R * 16);
@@ -87,7 +219,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
 #pragma unroll
       for (int u = 0; u < UPW; ++u)
         r.w[rt][u] = load_nt((const u32x4*)(wb + ((size_t)rt * G + s * UPW + u) * 1024));
-    const int g = kr0 / 128 + gw0 + s * UPW;
+    const unsigned g = (unsigned)(kr0 / 128 + gw0 + s * UPW);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
       load_dwords(a.scale + ((((size_t)(tt + rt) * G4 + g / 4) * 4 + lg) * 16 + (g % 4) * 4),
@@ -104,7 +236,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   const int xtotal = R * CPR;
   auto x_load = [&](int p) -> u32x4 {
     p = min(p, xtotal - 1);
-    const int m = min(p & (R - 1), a.M - 1), c = p >> a.log2R;
+    const int m = min(p % R, a.M - 1), c = p / R;
     return *(const u32x4*)(a.x + (size_t)m * a.K + kr0 + c * 8);
   };
   u32x4 xv[XB];
@@ -115,26 +247,23 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
 #pragma unroll
   for (int u = 0; u < XB; ++u)
-    if ((int)threadIdx.x + u * NT < xtotal) xs[threadIdx.x + u * NT] = w4_order_x(xv[u]);
+    if ((int)threadIdx.x + u * NT < xtotal) xs[threadIdx.x + u * NT] = xv[u];
   for (int p0 = threadIdx.x + NT * XB; p0 < xtotal; p0 += NT * XB) {
 #pragma unroll
     for (int u = 0; u < XB; ++u) xv[u] = x_load(p0 + u * NT);
 #pragma unroll
     for (int u = 0; u < XB; ++u)
-      if (p0 + u * NT < xtotal) xs[p0 + u * NT] = w4_order_x(xv[u]);
+      if (p0 + u * NT < xtotal) xs[p0 + u * NT] = xv[u];
   }
   __syncthreads();
-  // X per (group, column): an MFMA of ones against the group's x. Column
-  // block mb of a lane is x row col(mb) (MB = 1: rows past R repeat).
+  // X per (group, column): an MFMA of ones against the group's x
   const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
-  const int xrow = MB == 1 ? (lr & (R - 1)) : lr;
   for (int q = wid; q < GR * MB; q += NW) {
     const int g = q / MB, mb = q % MB;
     f32x4 xg = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      xg = mfma(ones, xs[(g * 16 + 4 * lg + j) * R + mb * 16 + xrow], xg);
-    if (lg == 0) xgs[g * RS + mb * 16 + lr] = xg[0];
+    for (int j = 0; j < 4; ++j) xg = mfma(ones, xs[(g * 16 + 4 * lg + j) * R + mb * 16 + lr], xg);
+    if (lg == 0) xgs[g * R + mb * 16 + lr] = xg[0];
   }
   __syncthreads();
 
@@ -148,46 +277,28 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
       const int gl = gw0 + s * UPW + u;
-      if constexpr (MB == 1) {
-        const u32x4* xp = xs + (gl * 16 + 4 * lg) * R + xrow;
+      // the RT tiles' unpacked operands, then one column block at a time
+      u32x4 aw[RT][4];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) aw[rt][j] = unpack_w4(r.w[rt][u][j]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const u32x4* xp = xs + (gl * 16 + 4 * lg) * R + mb * 16 + lr;
         u32x4 b[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) b[j] = xp[j * R];
-        const float xg = xgs[gl * 16 + lr];
+        const float xg = xgs[gl * R + mb * 16 + lr];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
           f32x4 cc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int j = 0; j < 4; ++j) cc = mfma(unpack_w4(r.w[rt][u][j]), b[j], cc);
+          for (int j = 0; j < 4; ++j) cc = mfma(aw[rt][j], b[j], cc);
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            acc[rt][0][i] = __builtin_fmaf(half_f(r.s[rt], 4 * u + i),
-                                           __builtin_fmaf(xg, -136.f, cc[i]), acc[rt][0][i]);
-        }
-      } else {
-        // the RT tiles' unpacked operands, then one column block at a time
-        u32x4 aw[RT][4];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) aw[rt][j] = unpack_w4(r.w[rt][u][j]);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          const u32x4* xp = xs + (gl * 16 + 4 * lg) * R + mb * 16 + lr;
-          u32x4 b[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) b[j] = xp[j * R];
-          const float xg = xgs[gl * RS + mb * 16 + lr];
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) {
-            f32x4 cc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) cc = mfma(aw[rt][j], b[j], cc);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              acc[rt][mb][i] = __builtin_fmaf(half_f(r.s[rt], 4 * u + i),
-                                              __builtin_fmaf(xg, -136.f, cc[i]), acc[rt][mb][i]);
-          }
+            acc[rt][mb][i] = fma_half(r.s[rt], 4 * u + i, __builtin_fmaf(xg, -136.f, cc[i]),
+                                      acc[rt][mb][i]);
         }
       }
       // one group at a time: without this fence the scheduler hoists the
@@ -209,7 +320,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   }
   if constexpr (KW > 1) {
     // the K slices of a row group, added in slice order by slice 0
-    float* red = xgs + GR * RS;
+    float* red = xgs + GR * R;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -236,20 +347,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   for (int mb = 0; mb < MB; ++mb) {
     const int m = mb * 16 + lr;
     if (m >= a.M) break;
-    if constexpr (SWIGLU) {
-      // tiles 2j (gate) and 2j+1 (up) hold the 16 outputs of block j
-      const int NA = a.N / 2;
-#pragma unroll
-      for (int p = 0; p < RT / 2; ++p) {
-        const int n = (t0 / 2 + p) * 16 + 4 * lg;
-        uint32_t v[2];
-        v[0] = pack_bf16x2(swiglu_bf16(acc[2 * p][mb][0], acc[2 * p + 1][mb][0]),
-                           swiglu_bf16(acc[2 * p][mb][1], acc[2 * p + 1][mb][1]));
-        v[1] = pack_bf16x2(swiglu_bf16(acc[2 * p][mb][2], acc[2 * p + 1][mb][2]),
-                           swiglu_bf16(acc[2 * p][mb][3], acc[2 * p + 1][mb][3]));
-        __builtin_memcpy(a.out + (size_t)m * NA + n, v, sizeof(v));
-      }
-    } else if (a.out) {
+    if (a.out) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         const int n = (t0 + rt) * 16 + 4 * lg;
@@ -366,7 +464,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void w4b_mid_kernel(W4mArgs a) {
     const int b = c & 1;
     u32x4* xb = xs + b * 16 * kMidBM;
 #pragma unroll
-    for (int u = 0; u < XPT; ++u) xb[threadIdx.x + NT * u] = w4_order_x(sl.x[u]);
+    for (int u = 0; u < XPT; ++u) xb[threadIdx.x + NT * u] = sl.x[u];
     __syncthreads();
     if (wid < kMidMB) {
       f32x4 xg = {0.f, 0.f, 0.f, 0.f};
@@ -393,8 +491,8 @@ __global__ __launch_bounds__(NW * kWave, 1) void w4b_mid_kernel(W4mArgs a) {
         for (int j = 0; j < 4; ++j) cc = mfma(aw[rt][j], bx[j], cc);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          acc[rt][mb][i] = __builtin_fmaf(half_f(sl.s[rt], i), __builtin_fmaf(xg, -136.f, cc[i]),
-                                          acc[rt][mb][i]);
+          acc[rt][mb][i] = fma_half(sl.s[rt], i, __builtin_fmaf(xg, -136.f, cc[i]),
+                                    acc[rt][mb][i]);
       }
     }
   };
@@ -438,25 +536,69 @@ int launch_mid(const W4mPlan& p, const W4mArgs& a, hipStream_t st) {
 }
 
 size_t w4b_lds(int R, int64_t kr, int nw, int kw, int rt, int mb) {
-  return (size_t)kr * R * 2 + (size_t)(kr / 128) * 16 * mb * 4 +
+  return (size_t)kr * R * 2 + (size_t)(kr / 128) * R * 4 +
          (kw > 1 ? (size_t)nw * rt * mb * 4 * kWave * 4 : 0);
 }
 
-template <int RT, int UPW, int DEPTH, int NW, int KW, int MB>
-int launch5(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
-  auto kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, KW, false, MB>;
-  int variant = 0;
-  if constexpr (RT >= 2 && MB == 1) {
+// ---- launchers: the direct kernel (M <= 16) ---------------------------------
+template <int RT, int UPW, int DEPTH, int NW>
+int launch_direct(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(NW * kWave);
+  if constexpr (RT >= 2) {
     if (p.swiglu) {
-      kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, KW, true, MB>;
-      variant = 1;
+      w4b_direct_kernel<RT, UPW, DEPTH, NW, true><<<grid, block, 0, st>>>(a);
+      return ACORN_OK;
     }
   }
-  static bool raised[2] = {false, false};  // once per kernel, before any graph capture
-  if (!raised[variant] && p.lds > 64 * 1024) {
+  if (p.swiglu) return ACORN_ERR_UNSUPPORTED;
+  w4b_direct_kernel<RT, UPW, DEPTH, NW, false><<<grid, block, 0, st>>>(a);
+  return ACORN_OK;
+}
+
+template <int RT, int UPW, int DEPTH>
+int direct_nw(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
+  switch (p.nw) {
+    case 1: return launch_direct<RT, UPW, DEPTH, 1>(p, a, st);
+    case 4: return launch_direct<RT, UPW, DEPTH, 4>(p, a, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+// registers of one stage (dwords per lane): weights, x operands, scales
+constexpr int direct_stage_dwords(int rt, int upw) { return 4 * (rt + 4) * upw + 2 * rt * upw; }
+constexpr int kDirectRingDwords = 160;   // the ring's budget (depth x stage)
+
+template <int RT, int UPW>
+int direct_depth(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
+  switch (p.depth) {
+    case 1: return direct_nw<RT, UPW, 1>(p, a, st);
+    case 2: return direct_nw<RT, UPW, 2>(p, a, st);
+    case 4:
+      if constexpr (4 * direct_stage_dwords(RT, UPW) <= kDirectRingDwords)
+        return direct_nw<RT, UPW, 4>(p, a, st);
+      break;
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+template <int RT>
+int direct_upw(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
+  switch (p.upw) {
+    case 1: return direct_depth<RT, 1>(p, a, st);
+    case 2: return direct_depth<RT, 2>(p, a, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+// ---- launchers: the LDS kernel (16 < M <= 64) -------------------------------
+template <int RT, int UPW, int DEPTH, int NW, int KW, int MB>
+int launch5(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
+  auto kfn = w4b_decode_kernel<RT, UPW, DEPTH, NW, KW, MB>;
+  static bool raised = false;  // once per kernel, before any graph capture
+  if (!raised && p.lds > 64 * 1024) {
     (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
                               160 * 1024);
-    raised[variant] = true;
+    raised = true;
   }
   dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(NW * kWave);
   kfn<<<grid, block, p.lds, st>>>(a);
@@ -477,19 +619,12 @@ int launch3(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
   return ACORN_ERR_UNSUPPORTED;
 }
 
-// MB > 1 (more arithmetic per loaded byte) is built for one or two stages in
-// flight of one or two groups
+// one or two stages in flight of one or two groups
 template <int RT, int UPW, int MB>
 int launch2(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
   switch (p.depth) {
     case 1: return launch3<RT, UPW, 1, MB>(p, a, st);
     case 2: return launch3<RT, UPW, 2, MB>(p, a, st);
-    case 4:
-      if constexpr (MB == 1 && RT * UPW <= 4 && RT < 4) return launch3<RT, UPW, 4, MB>(p, a, st);
-      break;
-    case 8:
-      if constexpr (MB == 1 && RT * UPW <= 2) return launch3<RT, UPW, 8, MB>(p, a, st);
-      break;
   }
   return ACORN_ERR_UNSUPPORTED;
 }
@@ -499,9 +634,6 @@ int launch1(const W4bPlan& p, const W4bArgs& a, hipStream_t st) {
   switch (p.upw) {
     case 1: return launch2<RT, 1, MB>(p, a, st);
     case 2: return launch2<RT, 2, MB>(p, a, st);
-    case 4:
-      if constexpr (RT == 1 && MB == 1) return launch2<RT, 4, MB>(p, a, st);
-      break;
   }
   return ACORN_ERR_UNSUPPORTED;
 }
@@ -523,26 +655,83 @@ int divisor_at_least(int64_t n, int64_t v) {
   return v <= n ? (int)v : 0;
 }
 
+// M <= 16: rt 1/2/4 (swiglu 2/4; N/16 divisible by rt), upw 1/2, waves per
+// workgroup (nw) 1 or 4, depth 1/2/4 within the ring's register budget, and
+// split counts that give every split a whole number of depth rounds. With 0
+// the plan takes rt 2, upw 1, one wave, depth 4, and the fewest splits that
+// launch at least three waves per CU.
+int direct_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4bPlan* p) {
+  const int64_t ntiles = N / 16, G = K / 128;
+  int rt = cfg && cfg[0] > 0 ? cfg[0] : 2;
+  const int upw = cfg && cfg[1] > 0 ? cfg[1] : 1;
+  const int nw = cfg && cfg[2] > 0 ? cfg[2] : 1;
+  const int req_ks = cfg ? cfg[3] : 0;
+  int depth = cfg && cfg[4] > 0 ? cfg[4] : 4;
+  if (rt != 1 && rt != 2 && rt != 4) return ACORN_ERR_UNSUPPORTED;
+  if (swiglu && rt < 2) rt = 2;
+  while (rt > (swiglu ? 2 : 1) && ntiles % rt) rt /= 2;
+  if (ntiles % rt) return ACORN_ERR_UNSUPPORTED;
+  if (upw != 1 && upw != 2) return ACORN_ERR_UNSUPPORTED;
+  if (nw != 1 && nw != 4) return ACORN_ERR_UNSUPPORTED;
+  if (depth != 1 && depth != 2 && depth != 4) return ACORN_ERR_UNSUPPORTED;
+  while (depth > 1 && (depth * direct_stage_dwords(rt, upw) > kDirectRingDwords ||
+                       G % (upw * depth)))
+    depth /= 2;
+  if (G % (upw * depth)) return ACORN_ERR_SHAPE;
+  const int64_t q = G / (upw * depth);          // ks must divide this
+  const int64_t waves = ntiles / rt;
+  int ks;
+  if (swiglu) {
+    ks = 1;
+  } else if (req_ks > 0) {
+    ks = divisor_at_least(q, req_ks);
+    if (!ks) return ACORN_ERR_UNSUPPORTED;
+  } else {
+    ks = 1;
+    while (waves * ks < 3 * 256) {
+      const int nx = divisor_at_least(q, ks + 1);
+      if (!nx) break;
+      ks = nx;
+    }
+  }
+  const int64_t groups = (waves + nw - 1) / nw;
+  if (groups > 0x7fffffff || ks > 65535) return ACORN_ERR_SHAPE;
+  p->direct = true;
+  p->rt = rt;
+  p->upw = upw;
+  p->nw = nw;
+  p->kw = 1;
+  p->nw_field = nw;
+  p->ksplit = ks;
+  p->depth = depth;
+  p->R = (int)M;
+  p->mb = 1;
+  p->groups = (int)groups;
+  p->lds = 0;
+  p->swiglu = swiglu;
+  return ACORN_OK;
+}
+
 }  // namespace
 
 namespace acorn {
 
-// Valid knobs: rt 1/2/4 (swiglu 2/4; N/16 divisible by rt), upw 1/2/4
-// (rt*upw <= 8, rt 4 with upw <= 2), depth 1/2/4/8 (rt*upw*depth <= 16), and
-// the wave layout in the nw field: 2 or 4 = that many waves with one K slice,
-// 10*nw + kw = nw waves in nw/kw row groups of kw K slices (42, 44, 82, 84).
-// ksplit and kw divide the per-row stage count G/upw so that every wave's K
-// range holds a whole number of depth-stage rounds. With 0 the split grows
-// from 1 until about two workgroups per CU are launched, while one
-// workgroup's x fits its LDS budget and each K range keeps at least 512 k.
-// 16 < M <= 64 uses mb = ceil(M / 16) column blocks (32 or 64 x rows staged)
-// with rt * mb <= 8, upw and depth 1 or 2, and no fused SwiGLU.
+// M <= 16: the direct kernel (direct_plan). 16 < M <= 64: the LDS kernel with
+// mb = ceil(M / 16) column blocks (32 or 64 x rows staged): rt 1/2/4 with
+// rt * mb <= 8, upw and depth 1 or 2, and the wave layout in the nw field:
+// 2 or 4 = that many waves with one K slice, 10*nw + kw = nw waves in nw/kw
+// row groups of kw K slices (42, 44, 82, 84). ksplit and kw divide the
+// per-row stage count G/upw so that every wave's K range holds a whole
+// number of depth-stage rounds. With 0 the split grows from 1 until about two
+// workgroups per CU are launched, while one workgroup's x fits its LDS budget
+// and each K range keeps at least 512 k. No fused SwiGLU above 16 rows.
 int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4bPlan* p) {
   if (M < 1 || M > 64) return ACORN_ERR_UNSUPPORTED;
-  const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-  if (mb > 1 && swiglu) return ACORN_ERR_UNSUPPORTED;
   if (N % 16 || K % 512) return ACORN_ERR_SHAPE;
   if (swiglu && N % 32) return ACORN_ERR_SHAPE;
+  if (M <= 16) return direct_plan(M, N, K, cfg, swiglu, p);
+  if (swiglu) return ACORN_ERR_UNSUPPORTED;
+  const int mb = M <= 32 ? 2 : 4;
   const int64_t ntiles = N / 16, G = K / 128;
   int rt = cfg && cfg[0] > 0 ? cfg[0] : 2;
   int upw = cfg && cfg[1] > 0 ? cfg[1] : 2;
@@ -552,28 +741,20 @@ int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   const bool layout_ok = (kw == 1 && (nw == 2 || nw == 4)) ||
                          (nw == 4 && (kw == 2 || kw == 4)) || (nw == 8 && (kw == 2 || kw == 4));
   if (!layout_ok) return ACORN_ERR_UNSUPPORTED;
-  if (swiglu && rt < 2) rt = 2;
   if (rt != 1 && rt != 2 && rt != 4) return ACORN_ERR_UNSUPPORTED;
-  while (rt > (swiglu ? 2 : 1) && ntiles % rt) rt /= 2;
-  if (ntiles % rt) return ACORN_ERR_UNSUPPORTED;
-  if (upw != 1 && upw != 2 && upw != 4) return ACORN_ERR_UNSUPPORTED;
-  if (rt * upw > 8 || (rt == 4 && upw > 2) || (rt == 2 && upw > 2)) return ACORN_ERR_UNSUPPORTED;
-  if (mb > 1 && (rt * mb > 8 || upw > 2)) return ACORN_ERR_UNSUPPORTED;
-  int R = 1;
-  while (R < M) R *= 2;
-  if (mb > 1) R = 16 * mb;
+  while (rt > 1 && ntiles % rt) rt /= 2;
+  if (upw != 1 && upw != 2) return ACORN_ERR_UNSUPPORTED;
+  if (rt * mb > 8) return ACORN_ERR_UNSUPPORTED;
+  const int R = 16 * mb;
   if (G % upw) return ACORN_ERR_SHAPE;
   const int64_t stages = G / upw;            // per row over the whole K
   if (stages % kw) return ACORN_ERR_UNSUPPORTED;
   const int64_t slices = stages / kw;        // per K slice with one split
   const size_t lds_cap = 160 * 1024, lds_default = 80 * 1024;
-  const int64_t rows_per_wg = (int64_t)(nw / kw) * rt;
   const int64_t groups = (ntiles / rt + nw / kw - 1) / (nw / kw);
   auto lds = [&](int ks) { return w4b_lds(R, K / ks, nw, kw, rt, mb); };
   int ks;
-  if (swiglu) {
-    ks = 1;
-  } else if (req_ks > 0) {
+  if (req_ks > 0) {
     ks = divisor_at_least(slices, req_ks);
     while (ks && lds(ks) > lds_cap) ks = divisor_at_least(slices, ks + 1);
     if (!ks) return ACORN_ERR_UNSUPPORTED;
@@ -592,12 +773,10 @@ int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   }
   if (lds(ks) > lds_cap) return ACORN_ERR_UNSUPPORTED;
   const int64_t ns = slices / ks;            // stages of one wave
-  int depth = req_depth > 0 ? req_depth : mb > 1 ? 2 : 4;
+  int depth = req_depth > 0 ? req_depth : 2;
   if (depth != 1 && depth != 2 && depth != 4 && depth != 8) return ACORN_ERR_UNSUPPORTED;
-  while (depth > 1 && (ns % depth || rt * upw * depth > 16 || (rt == 4 && depth > 2) ||
-                       (rt * upw > 2 && depth > 4) || (mb > 1 && depth > 2)))
-    depth /= 2;
-  (void)rows_per_wg;
+  while (depth > 1 && (ns % depth || depth > 2)) depth /= 2;
+  p->direct = false;
   p->rt = rt;
   p->upw = upw;
   p->nw = nw;
@@ -609,7 +788,7 @@ int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   p->mb = mb;
   p->groups = (int)groups;
   p->lds = lds(ks);
-  p->swiglu = swiglu;
+  p->swiglu = false;
   if (groups > 0x7fffffff || ks > 65535) return ACORN_ERR_SHAPE;
   return ACORN_OK;
 }
@@ -622,24 +801,24 @@ int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale
   // bf16 (or SwiGLU act) output only with one split; else fp32 partials
   if (p.ksplit > 1) out = nullptr;
   if (!out && (!part || p.swiglu)) return ACORN_ERR_VALUE;
-  W4bArgs a;
-  a.x = (const __bf16*)x;
-  a.w = (const uint8_t*)w;
-  a.scale = (const _Float16*)scale;
-  a.out = (__bf16*)out;
-  a.part = part;
-  a.M = (int)M;
-  a.N = (int)N;
-  a.K = (int)K;
-  a.kr = (int)(K / p.ksplit);
-  int l = 0;
-  while ((1 << l) < p.R) ++l;
-  a.log2R = l;
   int rc = ACORN_ERR_UNSUPPORTED;
-  switch (p.mb) {
-    case 1: rc = launch_rt<1>(p, a, st); break;
-    case 2: rc = launch_rt<2>(p, a, st); break;
-    case 4: rc = launch_rt<4>(p, a, st); break;
+  if (p.direct) {
+    if (M > 16) return ACORN_ERR_UNSUPPORTED;
+    const W4dArgs a{(const __bf16*)x, (const uint8_t*)w, (const _Float16*)scale, (__bf16*)out,
+                    part, (int)M, (int)N, (int)K, (int)(K / p.ksplit)};
+    switch (p.rt) {
+      case 1: rc = direct_upw<1>(p, a, st); break;
+      case 2: rc = direct_upw<2>(p, a, st); break;
+      case 4: rc = direct_upw<4>(p, a, st); break;
+    }
+  } else {
+    if (M <= 16 || M > 16 * p.mb) return ACORN_ERR_UNSUPPORTED;
+    const W4bArgs a{(const __bf16*)x, (const uint8_t*)w, (const _Float16*)scale, (__bf16*)out,
+                    part, (int)M, (int)N, (int)K, (int)(K / p.ksplit)};
+    switch (p.mb) {
+      case 2: rc = launch_rt<2>(p, a, st); break;
+      case 4: rc = launch_rt<4>(p, a, st); break;
+    }
   }
   if (rc) return rc;
   ACORN_LAUNCH_CHECK();
@@ -761,10 +940,11 @@ __global__ __launch_bounds__(256) void w4b_dequant_kernel(const uint32_t* __rest
     const int h = i >> 1, r = (i & 1) * 8 + rr;
     const float sc = s[i & 1];
     u32x4 o;
+    // k offsets 2q and 2q + 1 of the word are its nibbles q and q + 4
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const uint32_t byte = (d[i] >> (8 * q)) & 0xffu;
-      o[q] = pack_bf16x2((float)((int)(byte & 15u) - 8) * sc, (float)((int)(byte >> 4) - 8) * sc);
+      const int lo = (int)((d[i] >> (4 * q)) & 15u), hi = (int)((d[i] >> (4 * q + 16)) & 15u);
+      o[q] = pack_bf16x2((float)(lo - 8) * sc, (float)(hi - 8) * sc);
     }
     *(u32x4*)(out + (t * 16 + r) * K + g * 128 + 64 * h + 8 * j) = o;
   }

@@ -343,21 +343,16 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
 
 
 def _w4b_requests(swiglu: bool) -> list[Tiling]:
-    """Requests covering the int4 decode kernel's knobs: up to 16 KB of
-    weights in flight per wave (rt * upw * depth <= 16), every wave layout
-    (4 waves on their own rows; 4 or 8 waves in row groups of 2 or 4 K
-    slices), and split counts from one to sixteen."""
+    """Requests covering the int4 direct kernel's knobs (M <= 16): 1, 2 or 4
+    row tiles per wave, one group per stage with 2 or 4 stages in flight or
+    two groups with 2, one or four independent waves per workgroup, and split
+    counts from one to sixteen (the fused SwiGLU runs in one split)."""
     reqs = []
     for rt in ((2, 4) if swiglu else (1, 2, 4)):
-        for upw in ((1, 2, 4) if rt == 1 else (1, 2)):
-            for depth in (1, 2, 4, 8):
-                if rt * upw * depth > 16:
-                    continue
-                # waves per workgroup: 2 or 4 each on its own rows, or
-                # 10*nw + kw with kw waves splitting K over shared rows
-                for nw in (4, 42, 82, 44, 84):
-                    for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
-                        reqs.append(Tiling(rt, upw, nw, ks, depth))
+        for upw, depth in ((1, 2), (1, 4), (2, 2)):
+            for nw in (1, 4):
+                for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
+                    reqs.append(Tiling(rt, upw, nw, ks, depth))
     return reqs
 
 

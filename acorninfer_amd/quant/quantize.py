@@ -101,21 +101,40 @@ def unpack_w4(p: torch.Tensor) -> torch.Tensor:
     return out
 
 
+# Nibble order inside each 32-bit word of the W4B layout: position p (bits
+# 4p .. 4p+3) holds the word's k offset W4B_NIBBLE_K[p]. The kernels turn a
+# word into four bf16 pairs as (nibble q, nibble q + 4), q = 0..3, so with k
+# offsets (2q, 2q + 1) in that pair the unpacked operand is in natural k order
+# and x needs no reordering.
+W4B_NIBBLE_K = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def _w4b_nibbles(packed: torch.Tensor, order) -> torch.Tensor:
+    """Each group of 4 bytes (8 nibbles, low nibble first) with nibble p
+    replaced by nibble order[p]."""
+    b = packed.reshape(-1, 4).to(torch.int32)
+    nib = torch.stack([(b >> 4 * (p % 2)) & 15 for p in range(2)], 2).reshape(-1, 8)
+    nib = nib[:, list(order)]
+    out = (nib[:, 0::2] | (nib[:, 1::2] << 4)).to(torch.uint8)
+    return out.reshape(packed.shape)
+
+
 def to_w4b(packed: torch.Tensor, scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Natural packed int4 [N, K/2] + scale [N, K/128] -> the same bytes in
-    the decode kernel's 1 KB block layout (ACORN_WFMT_W4B), kept in tensors
-    of the same shapes: 16-byte chunk (row n, k in [32c, 32c+32)) moves to
-    block (n // 16, c // 4), lane (c % 4) * 16 + n % 16; the scale of (n, g)
-    to record (n // 16, g // 4, (n % 16) // 4) at position (g % 4) * 4 + n % 4.
-    Rows 16t..16t+15 of both tensors hold row tile t, so 16-row block
-    permutations (interleave16) commute with the conversion. N % 16 == 0 and
-    K % 512 == 0."""
+    """Natural packed int4 [N, K/2] + scale [N, K/128] -> the decode kernels'
+    1 KB block layout (ACORN_WFMT_W4B), kept in tensors of the same shapes:
+    16-byte chunk (row n, k in [32c, 32c+32)) moves to block (n // 16, c // 4),
+    lane (c % 4) * 16 + n % 16, with the nibbles of each 32-bit word in the
+    W4B_NIBBLE_K order; the scale of (n, g) to record (n // 16, g // 4,
+    (n % 16) // 4) at position (g % 4) * 4 + n % 4. Rows 16t..16t+15 of both
+    tensors hold row tile t, so 16-row block permutations (interleave16)
+    commute with the conversion. N % 16 == 0 and K % 512 == 0."""
     n, kh = packed.shape
     k = 2 * kh
     if n % 16 or k % 512 or scale.shape != (n, k // 128):
         raise ValueError(f"to_w4b needs N % 16 == 0, K % 512 == 0 and scale [N, K/128]: "
                          f"packed {tuple(packed.shape)}, scale {tuple(scale.shape)}")
-    wb = (packed.reshape(n // 16, 16, k // 128, 4, 16)      # tile, row, group, chunk, byte
+    wb = (_w4b_nibbles(packed, W4B_NIBBLE_K)
+          .reshape(n // 16, 16, k // 128, 4, 16)           # tile, row, group, chunk, byte
           .permute(0, 2, 3, 1, 4).reshape(n, kh).contiguous())
     sb = (scale.reshape(n // 16, 4, 4, k // 512, 4)        # tile, lg, i, g4, gg
           .permute(0, 3, 1, 4, 2).reshape(n, k // 128).contiguous())
@@ -129,8 +148,9 @@ def from_w4b(wb: torch.Tensor, sb: torch.Tensor) -> tuple[torch.Tensor, torch.Te
     if n % 16 or k % 512 or sb.shape != (n, k // 128):
         raise ValueError(f"from_w4b needs N % 16 == 0, K % 512 == 0 and scale [N, K/128]: "
                          f"packed {tuple(wb.shape)}, scale {tuple(sb.shape)}")
-    packed = (wb.reshape(n // 16, k // 128, 4, 16, 16)     # tile, group, chunk, row, byte
-              .permute(0, 3, 1, 2, 4).reshape(n, kh).contiguous())
+    inv = [W4B_NIBBLE_K.index(j) for j in range(8)]
+    packed = _w4b_nibbles(wb.reshape(n // 16, k // 128, 4, 16, 16)   # tile, group, chunk, row, byte
+                          .permute(0, 3, 1, 2, 4).reshape(n, kh), inv).contiguous()
     scale = (sb.reshape(n // 16, k // 512, 4, 4, 4)        # tile, g4, lg, gg, i
              .permute(0, 2, 4, 1, 3).reshape(n, k // 128).contiguous())
     return packed, scale

@@ -306,8 +306,14 @@ def test_w4b_wide_decode_kernel_matches(m):
             out = _launch(x, wb, sb, None, WFMT_W4B, n, c, None)
             r = rel_err(out, ref)
             assert r <= GEMM_REL, f"{cls} M={m} {tuple(c)}: rel err {r:.3g}"
+        # the column blocks do not mix rows: the last row equals that row of a
+        # 17-row launch ending with it (the same kernel and tiling, two blocks)
+        tail = _launch(x[m - 17:], wb, sb, None, WFMT_W4B, n, c, None)
+        assert rel_err(out[m - 1:], tail[16:]) <= 1e-5
+        # and the direct kernel's one-row result (its -136 X is formed by an
+        # MFMA) agrees to bf16 rounding of a few outputs
         last = _launch(x[m - 1:], wb, sb, None, WFMT_W4B, n, None, None)
-        assert rel_err(out[m - 1:], last) <= 1e-5
+        assert rel_err(out[m - 1:], last) <= 1e-3
         print(f"\n[w4b wide M={m} {cls}: {len(cands)} tilings ok]")
 
 
