@@ -59,23 +59,29 @@ struct DStage {
 // bf16 -136 in every slot: an MFMA of it against x gives -136 X per column
 constexpr uint32_t kNeg136x2 = 0xC308C308u;
 
-// Grid: x = tile groups of NW * RT 16-row tiles, y = ksplit; block NW waves.
-// Wave w of workgroup b owns tiles (b NW + w) RT .. + RT - 1 over the split's K
-// range, DEPTH stages of UPW groups in flight. Lane (lr, lg) holds x row
-// min(lr, M - 1) (rows past M feed only columns that are never stored).
-template <int RT, int UPW, int DEPTH, int NW, bool SWIGLU>
-__global__ __launch_bounds__(NW * kWave) void w4b_direct_kernel(W4dArgs a) {
+// Grid: x = tile groups of RG * RT 16-row tiles, y = ksplit; block RG * KW
+// waves. Row group r of workgroup b owns tiles (b RG + r) RT .. + RT - 1; its
+// KW waves split the split's K range (KW > 1 gives a projection more waves
+// without split-K partials: they add their results through LDS in fixed
+// order at the end). Each wave keeps DEPTH stages of UPW groups in flight.
+// Lane (lr, lg) holds x row min(lr, M - 1) (rows past M feed only columns
+// that are never stored).
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU>
+__global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) {
+  constexpr int NW = RG * KW;
   const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lg = lane >> 4, lr = lane & 15;
+  const int rg = wid / KW, kq = wid % KW;
   const int G = a.K / 128, G4 = a.K / 512;
-  const int t0 = (blockIdx.x * NW + wid) * RT;
+  const int t0 = (blockIdx.x * RG + rg) * RT;
   const bool active = t0 < a.N / 16;              // (N / 16) % RT == 0 by the plan
   const int tt = active ? t0 : 0;                 // idle waves read tile 0, store nothing
-  const int kr0 = blockIdx.y * a.kr;
-  const unsigned g0 = (unsigned)(kr0 / 128);
-  const int ns = a.kr / (128 * UPW);              // stages, a multiple of DEPTH
+  const int GW = a.kr / (128 * KW);               // groups of this wave
+  const int kw0 = blockIdx.y * a.kr + kq * GW * 128;
+  const unsigned g0 = (unsigned)(kw0 / 128);
+  const int ns = GW / UPW;                        // stages, a multiple of DEPTH
   const uint8_t* wb = a.w + ((size_t)tt * G + g0) * 1024 + lane * 16;
-  const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kr0 + 32 * lg;
+  const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 32 * lg;
   const _Float16* sb = a.scale + (size_t)tt * G4 * 64 + lg * 16;
   auto load = [&](int s, DStage<RT, UPW>& r) {
 #pragma unroll
@@ -129,6 +135,24 @@ __global__ __launch_bounds__(NW * kWave) void w4b_direct_kernel(W4dArgs a) {
   }
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) compute(ring[d]);
+  if constexpr (KW > 1) {
+    // the K slices of a row group, added in slice order by slice 0
+    __shared__ f32x4 red[NW][RT][kWave];
+    if (kq != 0) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) red[wid][rt][lane] = acc[rt];
+    }
+    __syncthreads();
+    if (kq != 0) return;
+#pragma unroll
+    for (int q = 1; q < KW; ++q)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const f32x4 v = red[wid + q][rt][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[rt][i] += v[i];
+      }
+  }
   if (!active || lr >= a.M) return;
 
   // lane (lr, lg) holds rows 4 lg .. 4 lg + 3 of each tile, column (x row) lr
@@ -541,25 +565,31 @@ size_t w4b_lds(int R, int64_t kr, int nw, int kw, int rt, int mb) {
 }
 
 // ---- launchers: the direct kernel (M <= 16) ---------------------------------
-template <int RT, int UPW, int DEPTH, int NW>
+template <int RT, int UPW, int DEPTH, int RG, int KW>
 int launch_direct(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(NW * kWave);
+  const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(RG * KW * kWave);
   if constexpr (RT >= 2) {
     if (p.swiglu) {
-      w4b_direct_kernel<RT, UPW, DEPTH, NW, true><<<grid, block, 0, st>>>(a);
+      w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, true><<<grid, block, 0, st>>>(a);
       return ACORN_OK;
     }
   }
   if (p.swiglu) return ACORN_ERR_UNSUPPORTED;
-  w4b_direct_kernel<RT, UPW, DEPTH, NW, false><<<grid, block, 0, st>>>(a);
+  w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false><<<grid, block, 0, st>>>(a);
   return ACORN_OK;
 }
 
+// wave layouts (the nw field): 1 or 4 waves on their own rows, or 10 nw + kw
+// with kw waves splitting K over one row group (22, 44). Two row groups of
+// four K slices (84) gave wrong results in every instance on gfx950 while 44
+// was right; it is not built.
 template <int RT, int UPW, int DEPTH>
 int direct_nw(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
-  switch (p.nw) {
-    case 1: return launch_direct<RT, UPW, DEPTH, 1>(p, a, st);
-    case 4: return launch_direct<RT, UPW, DEPTH, 4>(p, a, st);
+  switch (p.nw_field) {
+    case 1: return launch_direct<RT, UPW, DEPTH, 1, 1>(p, a, st);
+    case 4: return launch_direct<RT, UPW, DEPTH, 4, 1>(p, a, st);
+    case 22: return launch_direct<RT, UPW, DEPTH, 1, 2>(p, a, st);
+    case 44: return launch_direct<RT, UPW, DEPTH, 1, 4>(p, a, st);
   }
   return ACORN_ERR_UNSUPPORTED;
 }
@@ -655,16 +685,17 @@ int divisor_at_least(int64_t n, int64_t v) {
   return v <= n ? (int)v : 0;
 }
 
-// M <= 16: rt 1/2/4 (swiglu 2/4; N/16 divisible by rt), upw 1/2, waves per
-// workgroup (nw) 1 or 4, depth 1/2/4 within the ring's register budget, and
-// split counts that give every split a whole number of depth rounds. With 0
-// the plan takes rt 2, upw 1, one wave, depth 4, and the fewest splits that
-// launch at least three waves per CU.
+// M <= 16: rt 1/2/4 (swiglu 2/4; N/16 divisible by rt), upw 1/2, the wave
+// layout in the nw field (1 or 4 waves on their own rows; 22, 44 = nw waves
+// in one row group of kw K slices), depth 1/2/4 within the ring's
+// register budget, and split counts that give every wave a whole number of
+// depth rounds. With 0 the plan takes rt 2, upw 1, one wave per workgroup,
+// depth 4, and the fewest splits that launch at least three waves per CU.
 int direct_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4bPlan* p) {
   const int64_t ntiles = N / 16, G = K / 128;
   int rt = cfg && cfg[0] > 0 ? cfg[0] : 2;
   const int upw = cfg && cfg[1] > 0 ? cfg[1] : 1;
-  const int nw = cfg && cfg[2] > 0 ? cfg[2] : 1;
+  const int nwf = cfg && cfg[2] > 0 ? cfg[2] : 1;
   const int req_ks = cfg ? cfg[3] : 0;
   int depth = cfg && cfg[4] > 0 ? cfg[4] : 4;
   if (rt != 1 && rt != 2 && rt != 4) return ACORN_ERR_UNSUPPORTED;
@@ -672,14 +703,15 @@ int direct_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4
   while (rt > (swiglu ? 2 : 1) && ntiles % rt) rt /= 2;
   if (ntiles % rt) return ACORN_ERR_UNSUPPORTED;
   if (upw != 1 && upw != 2) return ACORN_ERR_UNSUPPORTED;
-  if (nw != 1 && nw != 4) return ACORN_ERR_UNSUPPORTED;
+  if (nwf != 1 && nwf != 4 && nwf != 22 && nwf != 44) return ACORN_ERR_UNSUPPORTED;
+  const int nw = nwf < 10 ? nwf : nwf / 10, kw = nwf < 10 ? 1 : nwf % 10;
   if (depth != 1 && depth != 2 && depth != 4) return ACORN_ERR_UNSUPPORTED;
   while (depth > 1 && (depth * direct_stage_dwords(rt, upw) > kDirectRingDwords ||
-                       G % (upw * depth)))
+                       G % (kw * upw * depth)))
     depth /= 2;
-  if (G % (upw * depth)) return ACORN_ERR_SHAPE;
-  const int64_t q = G / (upw * depth);          // ks must divide this
-  const int64_t waves = ntiles / rt;
+  if (G % (kw * upw * depth)) return ACORN_ERR_SHAPE;
+  const int64_t q = G / (kw * upw * depth);     // ks must divide this
+  const int64_t waves = ntiles / rt * kw;
   int ks;
   if (swiglu) {
     ks = 1;
@@ -694,14 +726,15 @@ int direct_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4
       ks = nx;
     }
   }
-  const int64_t groups = (waves + nw - 1) / nw;
+  const int64_t rgs = nw / kw;                 // row groups per workgroup
+  const int64_t groups = (ntiles / rt + rgs - 1) / rgs;
   if (groups > 0x7fffffff || ks > 65535) return ACORN_ERR_SHAPE;
   p->direct = true;
   p->rt = rt;
   p->upw = upw;
   p->nw = nw;
-  p->kw = 1;
-  p->nw_field = nw;
+  p->kw = kw;
+  p->nw_field = nwf;
   p->ksplit = ks;
   p->depth = depth;
   p->R = (int)M;

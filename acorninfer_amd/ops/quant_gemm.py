@@ -76,10 +76,12 @@ class Tiling(NamedTuple):
     Tiled kernel (M > 16 with rt == 0, the default there): upw is the M tile
     BM (32 / 64 / 128), nw the N tile BN (64 / 128), ksplit the K split; the
     planner reports (0, BM, BN, ksplit, 1).
-    int4 decode kernel (WFMT_W4B, M <= 16, and 16 < M <= 64 with rt >= 1):
-    rt row tiles per wave, upw 128-k groups per pipeline stage, nw waves per
-    workgroup (2 or 4 each on its own rows; 10*nw + kw: kw waves share rows
-    and split K), ksplit, and tpw = stages in flight per wave.
+    int4 decode kernels (WFMT_W4B; M <= 16 the direct kernel, 16 < M <= 64
+    with rt >= 1 the one that stages x in LDS): rt row tiles per wave, upw
+    128-k groups per pipeline stage, nw the wave layout (M <= 16: 1 or 4
+    waves each on its own rows; above: 2 or 4; 10*nw + kw: kw waves share
+    rows and split K, 22 / 44 at M <= 16, 42 / 44 / 82 / 84 above),
+    ksplit, and tpw = stages in flight per wave.
     int4 mid-M kernel (WFMT_W4B, M > 16, rt == -3): upw row tiles per wave
     (1 / 2), nw waves (4 / 8), ksplit, tpw 128-k groups in flight (2 / 4);
     64 x rows per workgroup, streamed through LDS a group at a time.
@@ -345,12 +347,13 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
 def _w4b_requests(swiglu: bool) -> list[Tiling]:
     """Requests covering the int4 direct kernel's knobs (M <= 16): 1, 2 or 4
     row tiles per wave, one group per stage with 2 or 4 stages in flight or
-    two groups with 2, one or four independent waves per workgroup, and split
-    counts from one to sixteen (the fused SwiGLU runs in one split)."""
+    two groups with 2, one or four waves per workgroup on their own rows or 2
+    or 4 K slices over shared rows (22, 44), and split counts from one to
+    sixteen (the fused SwiGLU runs in one split)."""
     reqs = []
     for rt in ((2, 4) if swiglu else (1, 2, 4)):
         for upw, depth in ((1, 2), (1, 4), (2, 2)):
-            for nw in (1, 4):
+            for nw in (1, 4, 22, 44):
                 for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
                     reqs.append(Tiling(rt, upw, nw, ks, depth))
     return reqs

@@ -112,30 +112,33 @@ def test_shape_guard():
 def test_planner_w4b_decode(M, N, K):
     """M <= 16 (the direct kernel): the default tiling, and every requested
     one the planner accepts, obey the kernel's contract: rt in {1,2,4}
-    dividing N/16, upw in {1,2}, one or four waves per workgroup, depth in
-    {1,2,4} within the register ring's budget, and each split holding a whole
-    number of depth-stage rounds."""
+    dividing N/16, upw in {1,2}, a wave layout of 1 or 4 waves on their own
+    rows or 10 nw + kw (22, 44; 84 is refused), depth in {1,2,4} within the register
+    ring's budget, and each wave's K range holding a whole number of
+    depth-stage rounds."""
     lib = _lib.lib()
     reqs = [(0, 0, 0, 0, 0), (4, 1, 1, 0, 4), (1, 2, 4, 3, 2), (2, 2, 4, 5, 4), (2, 1, 1, 1, 4),
-            (4, 2, 1, 2, 2), (1, 1, 4, 16, 1), (2, 1, 2, 0, 4), (1, 4, 1, 0, 2)]
+            (4, 2, 1, 2, 2), (1, 1, 4, 16, 1), (2, 1, 2, 0, 4), (1, 4, 1, 0, 2), (2, 1, 44, 1, 4),
+            (2, 2, 84, 2, 2), (4, 1, 22, 0, 4), (2, 1, 42, 1, 2)]
     for r in reqs:
         cfg = (ctypes.c_int * 6)(*r, 0)
         rc = lib.acorn_gemm_plan(M, N, K, _lib.WFMT_W4B, cfg)
         if r != reqs[0] and rc == _lib.ERR_UNSUPPORTED:
             continue                  # a request the shape cannot honour is refused
         assert rc == 0, (r, rc)
-        rt, upw, nw, ks, depth = cfg[:5]
-        assert r[2] in (0, 1, 4) and r[1] in (0, 1, 2), r    # the refused knobs never plan
-        assert nw in (1, 4)
+        rt, upw, nwf, ks, depth = cfg[:5]
+        assert r[2] in (0, 1, 4, 22, 44) and r[1] in (0, 1, 2), r   # refused knobs never plan
+        assert nwf in (1, 4, 22, 44)
+        kw = 1 if nwf < 10 else nwf % 10
         assert rt in (1, 2, 4) and (N // 16) % rt == 0
         assert upw in (1, 2) and depth in (1, 2, 4)
         assert depth * (4 * (rt + 4) * upw + 2 * rt * upw) <= 160
         groups = K // 128
-        assert groups % ks == 0 and (groups // ks) % (upw * depth) == 0
+        assert groups % (ks * kw) == 0 and (groups // ks // kw) % (upw * depth) == 0
         if r[3] == 0:
             # the default split: the fewest that launch three waves per CU
-            waves = N // 16 // rt
-            assert waves * ks >= 768 or ks == groups // (upw * depth)
+            waves = N // 16 // rt * kw
+            assert waves * ks >= 768 or ks == groups // (kw * upw * depth)
 
 
 @pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
