@@ -35,6 +35,11 @@ __device__ __forceinline__ u32x4 unpack_w4(uint32_t w) {
   return r;
 }
 
+// Byte I of v as float (selects v_cvt_f32_ubyteI).
+template <int I> __device__ __forceinline__ float ubyte_f32(uint32_t v) {
+  return (float)((v >> (8 * I)) & 0xffu);
+}
+
 // NDW consecutive dwords from a 4*NDW-byte aligned address (one vector load
 // per 16 bytes).
 template <int NDW>
@@ -97,6 +102,12 @@ __host__ __device__ inline size_t w4b_chunk_offset(int64_t n, int64_t c, int64_t
   return ((size_t)(n / 16) * (size_t)(K / 128) + (size_t)(c / 4)) * 1024 +
          (size_t)((c % 4) * 16 + n % 16) * 16;
 }
+// W8B: int8 weights (stored as q + 128) in 1 KB blocks of 16 rows x 64 k;
+// the 16 bytes of row n, k in [16c, 16c+16) (c = k/16 within the tensor).
+__host__ __device__ inline size_t w8b_chunk_offset(int64_t n, int64_t c, int64_t K) {
+  return ((size_t)(n / 16) * (size_t)(K / 64) + (size_t)(c / 4)) * 1024 +
+         (size_t)((c % 4) * 16 + n % 16) * 16;
+}
 // Scale (zero) of row n, group g: records of 4 rows x 4 groups per lane
 // group, so a lane's scales of consecutive groups are contiguous.
 __host__ __device__ inline size_t w4b_half_index(int64_t n, int64_t g, int64_t K) {
@@ -144,6 +155,21 @@ int w4m_launch(const W4mPlan& p, const void* x, const void* w, const void* scale
 // W4B weights -> bf16 [N, K] in row order (N % 16 == 0, K % 512 == 0).
 int w4b_dequant(const void* w, const void* scale, void* out, int64_t N, int64_t K,
                 hipStream_t st);
+
+// ---- the W8B decode kernel (w8_decode.hip), M <= 16 ---------------------------
+// cfg knobs: rt (row tiles of 16 per wave), upw (64-k blocks per pipeline
+// stage), nw (the wave layout: 1 or 4 waves on their own rows, 22 / 44 = 2 / 4
+// waves splitting K over shared rows), ksplit, depth (stages in flight).
+struct W8bPlan {
+  int rt, upw, nw_field, rg, kw, ksplit, depth;
+  int groups;      // workgroups along N
+  bool swiglu;
+};
+int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W8bPlan* p);
+// out (bf16 [M,N], or act [M,N/2] for swiglu) when given and ksplit == 1;
+// otherwise fp32 partials part[ksplit, M, N] (each already scaled).
+int w8b_launch(const W8bPlan& p, const void* x, const void* w, const void* scale, void* out,
+               float* part, int64_t M, int64_t N, int64_t K, hipStream_t st);
 
 // ---- the large-M bf16 GEMM (dense_gemm.hip) ---------------------------------
 // out[M,N] = x[M,K] . w[N,K]^T, bf16 operands: (4 wn) x bm output tiles (wn

@@ -64,6 +64,8 @@ template <> struct Fmt<ACORN_WFMT_W4> {
 
 // int4 in either layout (natural rows, or the 1 KB blocks of W4B)
 template <int WFMT> constexpr bool kIsW4 = WFMT == ACORN_WFMT_W4 || WFMT == ACORN_WFMT_W4B;
+// int8 in either layout (natural rows, or the biased 1 KB blocks of W8B)
+template <int WFMT> constexpr bool kIsW8 = WFMT == ACORN_WFMT_W8 || WFMT == ACORN_WFMT_W8B;
 
 // x staged for the streaming kernel over natural-layout int4 (low nibble =
 // even k): the 8 bf16 of a 16-byte piece reordered to [x0,x4,x1,x5,x2,x6,x3,
@@ -77,10 +79,6 @@ __device__ __forceinline__ u32x4 w4_order_x(u32x4 w) {
   return t;
 }
 
-// Byte I of v as float (selects v_cvt_f32_ubyteI).
-template <int I> __device__ __forceinline__ float ubyte_f32(uint32_t v) {
-  return (float)((v >> (8 * I)) & 0xffu);
-}
 
 // int8: 8 signed bytes -> bf16 (128+q) in natural order.
 __device__ __forceinline__ u32x4 unpack_w8(uint32_t lo, uint32_t hi) {
@@ -487,7 +485,7 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
   constexpr int CPR = BK / 8;                         // 16-byte x chunks per row per step
   constexpr int XR = BM * CPR / 256;                  // 16-byte x loads per thread per step
   constexpr int TPR = 256 / BN;                       // threads per weight row
-  constexpr int WR = kIsW4<WFMT> ? 1 : WFMT == ACORN_WFMT_W8 ? 2 : 4;
+  constexpr int WR = kIsW4<WFMT> ? 1 : kIsW8<WFMT> ? 2 : 4;
   static_assert(XR >= 1 && MB >= 1 && NB >= 1 && BK / TPR == 32, "unsupported tile");
   extern __shared__ __align__(16) unsigned char smem[];
   __bf16* xs = (__bf16*)smem;                         // [2][BM][KP]
@@ -571,6 +569,11 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
       wr[0] = *(const u32x4*)(a.w + w4b_chunk_offset(n0 + wrow, (k0 + 32 * wpart) / 32, K));
     } else if constexpr (WFMT == ACORN_WFMT_W4) {
       wr[0] = *(const u32x4*)(a.w + wk / 2);
+    } else if constexpr (WFMT == ACORN_WFMT_W8B) {
+      // the same 16-byte pieces (row n, 16-k chunk c) in the 1 KB block layout
+#pragma unroll
+      for (int j = 0; j < WR; ++j)
+        wr[j] = *(const u32x4*)(a.w + w8b_chunk_offset(n0 + wrow, (k0 + 32 * wpart) / 16 + j, K));
     } else if constexpr (WFMT == ACORN_WFMT_W8) {
 #pragma unroll
       for (int j = 0; j < WR; ++j) wr[j] = *(const u32x4*)(a.w + wk + 16 * j);
@@ -620,14 +623,15 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
         }
         *(u32x4*)(wd + 8 * d) = o;
       }
-    } else if constexpr (WFMT == ACORN_WFMT_W8) {
+    } else if constexpr (kIsW8<WFMT>) {
 #pragma unroll
       for (int j = 0; j < WR; ++j) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          // 8 signed bytes -> bf16(q), exact; ^0x80 then -128 keeps the
-          // conversion on v_cvt_f32_ubyteN
-          const uint32_t lo = wr[j][2 * h] ^ 0x80808080u, hi = wr[j][2 * h + 1] ^ 0x80808080u;
+          // 8 signed bytes -> bf16(q), exact; ^0x80 (W8B stores q + 128
+          // already) then -128 keeps the conversion on v_cvt_f32_ubyteN
+          constexpr uint32_t kFlip = WFMT == ACORN_WFMT_W8B ? 0u : 0x80808080u;
+          const uint32_t lo = wr[j][2 * h] ^ kFlip, hi = wr[j][2 * h + 1] ^ kFlip;
           u32x4 o;
           o[0] = pack_bf16x2(ubyte_f32<0>(lo) - 128.f, ubyte_f32<1>(lo) - 128.f);
           o[1] = pack_bf16x2(ubyte_f32<2>(lo) - 128.f, ubyte_f32<3>(lo) - 128.f);
@@ -689,7 +693,7 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
   for (int i = 0; i < NB; ++i) {
     const int n = n0 + wn + 16 * i + 4 * r;
     float sc[4] = {1.f, 1.f, 1.f, 1.f};
-    if constexpr (WFMT == ACORN_WFMT_W8) {
+    if constexpr (kIsW8<WFMT>) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) sc[e] = (float)a.scale[n + e];
     }
@@ -742,8 +746,10 @@ struct Tiling {
                                  // 3 = large-M bf16 kernel (rt == kDenseRT, upw = BM,
                                  //     nw = weight rows per wave, tpw = prefetch depth),
                                  // 4 = W4B mid-M kernel (rt == kMidRT, upw = row tiles
-                                 //     per wave, nw = waves, tpw = groups in flight)
+                                 //     per wave, nw = waves, tpw = groups in flight),
+                                 // 5 = W8B decode kernel (tpw = its pipeline depth)
   W4bPlan w4b;
+  W8bPlan w8b;
   W4mPlan w4m;
 };
 
@@ -789,6 +795,7 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
   const int bk = kTileKN / bn;
   const int align = (wfmt == ACORN_WFMT_W4 || wfmt == ACORN_WFMT_W4B) ? std::max(128, bk) : bk;
   if (wfmt == ACORN_WFMT_W4B && (K % 512 || N % 16)) return ACORN_ERR_SHAPE;
+  if (wfmt == ACORN_WFMT_W8B && (K % 64 || N % 16)) return ACORN_ERR_SHAPE;
   if (K % align) return ACORN_ERR_SHAPE;
   const int bm = (req_bm == 32 || req_bm == 64 || req_bm == 128) ? req_bm
                  : M <= 32 ? 32 : M <= 64 ? 64 : 128;
@@ -813,7 +820,8 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
     ks = 1;
     const int64_t tiles = (int64_t)t->ntiles * t->mblocks;
     const double wbytes = (double)N * K * ((wfmt == ACORN_WFMT_W4 || wfmt == ACORN_WFMT_W4B) ? 0.5
-                                           : wfmt == ACORN_WFMT_W8 ? 1 : 2);
+                                           : (wfmt == ACORN_WFMT_W8 || wfmt == ACORN_WFMT_W8B) ? 1
+                                                                                            : 2);
     while (tiles * ks < 2 * kCUs) {
       int64_t nx = ks + 1;
       while (nx <= units && units % nx) ++nx;
@@ -949,6 +957,26 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   }
   if (wfmt == ACORN_WFMT_W4B && (swiglu || (cfg && cfg[0] > 0)))
     return ACORN_ERR_UNSUPPORTED;  // M > 64 in the block layout: the tiled kernel only
+  if (wfmt == ACORN_WFMT_W8B && M <= 16 && !(cfg && cfg[0] == 0 && cfg[1] >= 32)) {
+    // decode sizes in the int8 block layout: the W8B decode kernel
+    const int rc = w8b_make_plan(M, N, K, cfg, swiglu, &t->w8b);
+    if (rc) return rc;
+    t->kind = 5;
+    t->rt = t->w8b.rt;
+    t->upw = t->w8b.upw;
+    t->nw = t->w8b.nw_field;
+    t->ksplit = t->w8b.ksplit;
+    t->tpw = t->w8b.depth;
+    t->mt = 1;
+    t->R = (int)M;
+    t->ntiles = (int)(N / 16);
+    t->mblocks = 1;
+    t->groups = t->w8b.groups;
+    t->lds = 0;
+    return ACORN_OK;
+  }
+  if (wfmt == ACORN_WFMT_W8B && (swiglu || (cfg && cfg[0] > 0)))
+    return ACORN_ERR_UNSUPPORTED;  // M > 16 in the block layout: the tiled kernel only
   // the tiled kernel: the default for M > 16; for M <= 16 on request (rt 0
   // with an M tile of 32 or more in upw)
   if (!swiglu && ((M > 16 && (!cfg || cfg[0] <= 0)) || (cfg && cfg[0] == 0 && cfg[1] >= 32)))
@@ -1155,7 +1183,7 @@ int dispatch_tiled(const Tiling& t, const KArgs& a, hipStream_t st) {
 int plan_entry(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg, bool swiglu) {
   if (!cfg) return ACORN_ERR_VALUE;
   if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
-      wfmt != ACORN_WFMT_W4B)
+      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_W8B)
     return ACORN_ERR_DTYPE;
   Tiling t;
   const int rc = make_plan(M, N, K, wfmt, cfg, &t, swiglu);
@@ -1206,12 +1234,15 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
   } else if (t.kind == 4) {
     if (zero) return ACORN_ERR_UNSUPPORTED;  // the block layout is the symmetric format
     rc = w4m_launch(t.w4m, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
+  } else if (t.kind == 5) {
+    rc = w8b_launch(t.w8b, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
   } else if (t.kind == 1) {
     switch (wfmt) {
       case ACORN_WFMT_BF16: rc = dispatch_tiled<ACORN_WFMT_BF16>(t, a, st); break;
       case ACORN_WFMT_W8: rc = dispatch_tiled<ACORN_WFMT_W8>(t, a, st); break;
       case ACORN_WFMT_W4: rc = dispatch_tiled<ACORN_WFMT_W4>(t, a, st); break;
       case ACORN_WFMT_W4B: rc = dispatch_tiled<ACORN_WFMT_W4B>(t, a, st); break;
+      case ACORN_WFMT_W8B: rc = dispatch_tiled<ACORN_WFMT_W8B>(t, a, st); break;
     }
   } else {
     switch (wfmt) {
@@ -1250,7 +1281,7 @@ extern "C" int acorn_quant_gemm(const void* x, const void* w, const void* scale,
                                 const void* zero, void* out_bf16, float* part, int64_t M,
                                 int64_t N, int64_t K, int wfmt, const int* cfg, void* stream) {
   if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
-      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_F32)
+      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_W8B && wfmt != ACORN_WFMT_F32)
     return ACORN_ERR_DTYPE;
   if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   if (M == 0) return ACORN_OK;
@@ -1274,7 +1305,7 @@ extern "C" int acorn_quant_gemm_swiglu(const void* x, const void* w, const void*
                                        const void* zero, void* act, int64_t M, int64_t N,
                                        int64_t K, int wfmt, const int* cfg, void* stream) {
   if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
-      wfmt != ACORN_WFMT_W4B)
+      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_W8B)
     return ACORN_ERR_DTYPE;
   if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   if (M == 0) return ACORN_OK;

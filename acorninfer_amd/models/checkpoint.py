@@ -32,12 +32,13 @@ import json
 import torch
 
 from acorninfer_amd.config import Qwen3Config
-from acorninfer_amd.models.qwen3 import (FORMATS, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8,
+from acorninfer_amd.models.qwen3 import (FORMATS, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B,
                                          LayerWeights, QLinear, Qwen3DecodeModel)
 from acorninfer_amd.ops.quant_gemm import deinterleave16
 
 FORMAT_NAMES = {v: k for k, v in FORMATS.items()}
-FORMAT_NAMES[WFMT_W4B] = "w4a16"      # the in-memory block layout of int4
+FORMAT_NAMES[WFMT_W4B] = "w4a16"      # the in-memory block layouts of int4 and int8
+FORMAT_NAMES[WFMT_W8B] = "w8a16"
 _NORMS = ("input_layernorm", "post_attention_layernorm", "self_attn.q_norm", "self_attn.k_norm")
 
 

@@ -37,7 +37,7 @@ from dataclasses import dataclass, field
 import torch
 
 from acorninfer_amd import _lib
-from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, check,
+from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B, check,
                                  dtype_code, lib, ptr, stream_ptr)
 from acorninfer_amd.config import Qwen3Config
 from acorninfer_amd.ops.paged_attention import prefill_supported
@@ -110,11 +110,13 @@ def dispatch_linear(mod, x: torch.Tensor) -> torch.Tensor:
 class QLinear:
     """One projection y = x @ W^T in a decode weight format.
 
-    bf16: w [N,K] bf16.  w8a16: w int8 [N,K], scale fp16 [N].
+    bf16: w [N,K] bf16.  w8a16: w int8 [N,K], scale fp16 [N]; with N % 16
+    == 0 and K % 64 == 0 held in the int8 decode kernel's 1 KB block layout
+    (fmt WFMT_W8B, quantize.to_w8b: uint8 q + 128 of the same shape).
     w4a16: w uint8 [N,K/2] (low nibble = even k), scale fp16 [N,K/128], zero
     None (symmetric) or fp16 [N,K/128]; symmetric weights with N % 16 == 0
-    and K % 512 == 0 are held in the decode kernel's 1 KB block layout
-    (fmt WFMT_W4B, quantize.to_w4b: the same bytes and tensor shapes).
+    and K % 512 == 0 are held in the int4 decode kernels' 1 KB block layout
+    (fmt WFMT_W4B, quantize.to_w4b: the same tensor shapes).
     """
     fmt: int
     w: torch.Tensor
@@ -131,22 +133,30 @@ class QLinear:
             return cls(fmt, w.to(torch.bfloat16).contiguous(), N, K)
         if fmt == WFMT_W8:
             q, s = Q.quantize_w8(w)
-            return cls(fmt, q.contiguous(), N, K, s.contiguous())
+            return cls(fmt, q.contiguous(), N, K, s.contiguous()).blocked()
         if fmt == WFMT_W4:
             u, s = Q.quantize_w4_sym(w)
             return cls(fmt, Q.pack_w4(u).contiguous(), N, K, s.contiguous()).blocked()
         raise ValueError(f"unknown weight format {fmt}")
 
     def blocked(self) -> "QLinear":
-        """Symmetric int4 in the W4B block layout where the shape allows it
-        (N % 16 == 0, K % 512 == 0); any other weight unchanged."""
+        """int8 in the W8B block layout (N % 16 == 0, K % 64 == 0) and
+        symmetric int4 in the W4B block layout (N % 16 == 0, K % 512 == 0)
+        where the shape allows it; any other weight unchanged."""
+        if self.fmt == WFMT_W8 and not (self.N % 16 or self.K % 64):
+            return QLinear(WFMT_W8B, Q.to_w8b(self.w), self.N, self.K, self.scale, None,
+                           il16=self.il16)
         if self.fmt != WFMT_W4 or self.zero is not None or self.N % 16 or self.K % 512:
             return self
         wb, sb = Q.to_w4b(self.w, self.scale)
         return QLinear(WFMT_W4B, wb, self.N, self.K, sb, None, il16=self.il16)
 
     def natural(self) -> "QLinear":
-        """The same weight with int4 in the natural [N, K/2] layout."""
+        """The same weight in the reference's layouts (int8 [N, K], int4
+        [N, K/2])."""
+        if self.fmt == WFMT_W8B:
+            return QLinear(WFMT_W8, Q.from_w8b(self.w), self.N, self.K, self.scale, None,
+                           il16=self.il16)
         if self.fmt != WFMT_W4B:
             return self
         w, s = Q.from_w4b(self.w, self.scale)
@@ -164,8 +174,9 @@ class QLinear:
         """fp32 dequantised weight [N, K] in [gate; up] row order (test helper)."""
         if self.fmt in (WFMT_BF16, _lib.WFMT_F32):
             d = self.w.float()
-        elif self.fmt == WFMT_W8:
-            d = Q.dequant_w8(self.w, self.scale)
+        elif self.fmt in (WFMT_W8, WFMT_W8B):
+            nat = self.natural()
+            d = Q.dequant_w8(nat.w, nat.scale)
         else:
             nat = self.natural()
             u = Q.unpack_w4(nat.w)

@@ -21,7 +21,7 @@ from typing import NamedTuple
 
 import torch
 
-from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, check, lib,
+from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B, check, lib,
                                  ptr, require_gpu, stream_ptr)
 
 CLASSES = {
@@ -82,6 +82,9 @@ class Tiling(NamedTuple):
     waves each on its own rows; above: 2 or 4; 10*nw + kw: kw waves share
     rows and split K, 22 / 44 at M <= 16, 42 / 44 / 82 / 84 above),
     ksplit, and tpw = stages in flight per wave.
+    int8 decode kernel (WFMT_W8B, M <= 16): rt row tiles per wave, upw 64-k
+    blocks per stage, nw the wave layout (1, 4, 22, 44 as for int4), ksplit,
+    tpw = stages in flight; above 16 rows W8B runs on the tiled kernel.
     int4 mid-M kernel (WFMT_W4B, M > 16, rt == -3): upw row tiles per wave
     (1 / 2), nw waves (4 / 8), ksplit, tpw 128-k groups in flight (2 / 4);
     64 x rows per workgroup, streamed through LDS a group at a time.
@@ -300,8 +303,8 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
     planner = swiglu_plan if swiglu else plan
     base, _ = planner(M, N, K, wfmt)
     reqs = [Tiling()]
-    if wfmt == WFMT_W4B and M <= DECODE_M_MAX:
-        reqs += _w4b_requests(swiglu)
+    if wfmt in (WFMT_W4B, WFMT_W8B) and M <= DECODE_M_MAX:
+        reqs += _w4b_requests(swiglu) if wfmt == WFMT_W4B else _w8b_requests(swiglu)
         if not swiglu:
             for bn in (64, 128):
                 for ks in (1, 2, 4, 8, 16):
@@ -353,6 +356,20 @@ def _w4b_requests(swiglu: bool) -> list[Tiling]:
     reqs = []
     for rt in ((2, 4) if swiglu else (1, 2, 4)):
         for upw, depth in ((1, 2), (1, 4), (2, 2)):
+            for nw in (1, 4, 22, 44):
+                for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
+                    reqs.append(Tiling(rt, upw, nw, ks, depth))
+    return reqs
+
+
+def _w8b_requests(swiglu: bool) -> list[Tiling]:
+    """Requests covering the int8 direct kernel's knobs (M <= 16): 1, 2 or 4
+    row tiles per wave, one or two 64-k blocks per stage with 2 or 4 stages in
+    flight, the same wave layouts as the int4 kernel (1, 4, 22, 44), and split
+    counts from one to sixteen (the fused SwiGLU runs in one split)."""
+    reqs = []
+    for rt in ((2, 4) if swiglu else (1, 2, 4)):
+        for upw, depth in ((1, 4), (2, 2), (2, 4)):
             for nw in (1, 4, 22, 44):
                 for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
                     reqs.append(Tiling(rt, upw, nw, ks, depth))

@@ -156,6 +156,34 @@ def from_w4b(wb: torch.Tensor, sb: torch.Tensor) -> tuple[torch.Tensor, torch.Te
     return packed, scale
 
 
+def to_w8b(q: torch.Tensor) -> torch.Tensor:
+    """int8 [N, K] -> the int8 decode kernel's 1 KB block layout
+    (ACORN_WFMT_W8B) in a uint8 tensor of the same shape: every byte stored
+    as q + 128, and the 16 bytes of row n, k in [16c, 16c+16) moved to block
+    (n // 16, c // 4), lane (c % 4) * 16 + n % 16. The per-channel scale keeps
+    its [N] layout. Rows 16t..16t+15 hold row tile t, so 16-row block
+    permutations (interleave16) commute with the conversion. N % 16 == 0 and
+    K % 64 == 0."""
+    n, k = q.shape
+    if q.dtype != torch.int8 or n % 16 or k % 64:
+        raise ValueError(f"to_w8b needs int8 [N, K] with N % 16 == 0 and K % 64 == 0: "
+                         f"{q.dtype} {tuple(q.shape)}")
+    u = (q.to(torch.int16) + 128).to(torch.uint8)
+    return (u.reshape(n // 16, 16, k // 64, 4, 16)        # tile, row, block, chunk, byte
+            .permute(0, 2, 3, 1, 4).reshape(n, k).contiguous())
+
+
+def from_w8b(wb: torch.Tensor) -> torch.Tensor:
+    """Inverse of to_w8b."""
+    n, k = wb.shape
+    if wb.dtype != torch.uint8 or n % 16 or k % 64:
+        raise ValueError(f"from_w8b needs uint8 [N, K] with N % 16 == 0 and K % 64 == 0: "
+                         f"{wb.dtype} {tuple(wb.shape)}")
+    u = (wb.reshape(n // 16, k // 64, 4, 16, 16)           # tile, block, chunk, row, byte
+         .permute(0, 3, 1, 2, 4).reshape(n, k))
+    return (u.to(torch.int16) - 128).to(torch.int8).contiguous()
+
+
 def dequant_w8(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """fp32 [N,K] = q * scale[:, None]."""
     return q.float() * scale.float()[:, None]

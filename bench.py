@@ -600,7 +600,7 @@ def gemm_benchmarks(seed: int, gemm_ms=(1, 8, 64, 256), fixed: dict | None = Non
     out = {}
     g = torch.Generator(device="cuda").manual_seed(seed + 3)
     # ---- quant GEMM, configuration 3 -------------------------------------
-    # int4 in the decode model's block layout and int8 per channel; every
+    # int4 and int8 in the decode model's block layouts; every
     # candidate tiling is timed once (one graph of 16 launches over distinct
     # weights), the fastest four again with 64 launches x 3 replays
     shapes = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (24576, 4096),
@@ -620,7 +620,7 @@ def gemm_benchmarks(seed: int, gemm_ms=(1, 8, 64, 256), fixed: dict | None = Non
                     wq8 = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda",
                                         generator=g)
                     sc = (0.005 + 0.015 * torch.rand(n, device="cuda", generator=g)).half()
-                    lins.append(QLinear(wf, wq8, n, k, sc))
+                    lins.append(QLinear(wf, wq8, n, k, sc).blocked())   # the model's layout
             for M in gemm_ms:
                 xm = torch.randn(M, k, device="cuda", generator=g).bfloat16()
 

@@ -37,12 +37,20 @@ extern "C" {
                              only through out_part (the fp32 parity path) */
 #define ACORN_WFMT_W4B 4  /* ACORN_WFMT_W4's values in 1 KB blocks (N % 16 == 0,
                              K % 512 == 0): the 16 bytes of row n, k in
-                             [32c, 32c+32) (natural nibble order) sit at byte
-                             ((n/16)*(K/128) + c/4)*1024 + ((c%4)*16 + n%16)*16;
-                             scale / zero of (n, group g) at half index
+                             [32c, 32c+32) sit at byte
+                             ((n/16)*(K/128) + c/4)*1024 + ((c%4)*16 + n%16)*16,
+                             32-bit word j of them holding k 32c+8j .. +7 with
+                             nibble p (bits 4p..4p+3) at k offset 0,2,4,6,1,3,5,7
+                             for p = 0..7; scale of (n, group g) at half index
                              ((n/16)*(K/512) + g/4)*64 + ((n%16)/4)*16 + (g%4)*4 + n%4.
-                             Same bytes as W4; a block is one wave's MFMA
-                             A operand for 16 rows x 128 k. */
+                             Symmetric only; a block is one wave's MFMA A
+                             operand for 16 rows x 128 k. */
+#define ACORN_WFMT_W8B 5  /* ACORN_WFMT_W8's values in 1 KB blocks (N % 16 == 0,
+                             K % 64 == 0), each stored as the byte q + 128:
+                             the 16 bytes of row n, k in [16c, 16c+16) sit at
+                             byte ((n/16)*(K/64) + c/4)*1024 + ((c%4)*16 + n%16)*16;
+                             fp16 per-channel scale [N] as in W8. A block is
+                             one wave's MFMA A operands for 16 rows x 64 k. */
 
 /* error codes */
 #define ACORN_OK 0
@@ -234,6 +242,8 @@ int acorn_paged_attention_qkv_supported(int64_t H, int64_t KV, int64_t D, int64_
  *                         [N,K/128] or NULL (symmetric, zero = -8*scale)
  *   wfmt ACORN_WFMT_W4B : as W4, in the blocked layout above (the decode
  *                         model's int4 weights)
+ *   wfmt ACORN_WFMT_W8B : as W8, in the blocked layout above (the decode
+ *                         model's int8 weights)
  *   wfmt ACORN_WFMT_F32 : w fp32 [N,K], x fp32 [M,K]; fp32 result in part
  * cfg: NULL or int[6] {rt, upw, nw, ksplit, tpw, -}; 0 entries are chosen by
  * the planner (acorn_gemm_plan). With the chosen ksplit:

@@ -203,7 +203,7 @@ def test_bucket_boundaries_and_classes():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["bf16", "w8", "w4", "w4b"])
+@pytest.mark.parametrize("fmt", ["bf16", "w8", "w8b", "w4", "w4b"])
 @pytest.mark.parametrize("m", [1, 8, 16, 40, 256])
 def test_every_candidate_tiling_matches(fmt, m):
     """Every tiling the load-time sweep may pick (streaming kernel: row tiles
@@ -212,9 +212,9 @@ def test_every_candidate_tiling_matches(fmt, m):
     partial last M tile at M = 40) gives the oracle's result on the o shape
     (K=4096) and the down shape (K=12288); tilings differ only in fp32
     summation order."""
-    from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8
+    from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B
     from acorninfer_amd.ops.quant_gemm import _launch, candidates
-    from acorninfer_amd.quant.quantize import to_w4b
+    from acorninfer_amd.quant.quantize import to_w4b, to_w8b
     for cls in ("o", "down"):
         n, k = SHAPES[cls]
         if fmt == "bf16":
@@ -223,6 +223,9 @@ def test_every_candidate_tiling_matches(fmt, m):
         elif fmt == "w8":
             q, s, wref = _w8(cls)
             args, wf = (q, s, None), WFMT_W8
+        elif fmt == "w8b":
+            q, s, wref = _w8(cls)
+            args, wf = (to_w8b(q), s, None), WFMT_W8B
         elif fmt == "w4":
             p, s, wref = _w4(cls)
             args, wf = (p, s, None), WFMT_W4
@@ -240,6 +243,33 @@ def test_every_candidate_tiling_matches(fmt, m):
             assert r <= GEMM_REL, f"{cls} {tuple(c)}: rel err {r:.3g}"
             outs.append(out)
         print(f"\n[{fmt} M={m} {cls}: {len(cands)} tilings ok]")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cls", list(SHAPES))
+@pytest.mark.parametrize("m", MS)
+def test_w8b_config3_matches_dequant_matmul(cls, m):
+    """The decode model's int8 layout (W8B blocks, q + 128) at every
+    configuration-3 shape and M with the planner's tiling (the int8 decode
+    kernel for M <= 16, the tiled kernel above) against the dequantised
+    matmul (norm-wise GEMM_REL and the reference's per-class elementwise
+    TOL_W8), and equal to the natural-layout int8 GEMM up to fp32 summation
+    order."""
+    from acorninfer_amd._lib import WFMT_W8, WFMT_W8B
+    from acorninfer_amd.ops.quant_gemm import _launch
+    from acorninfer_amd.quant.quantize import from_w8b, to_w8b
+    q, s, wref = _w8(cls)
+    wb = to_w8b(q)
+    assert torch.equal(from_w8b(wb), q)
+    n, k = SHAPES[cls]
+    x = _x(m, k, 10)
+    out = _launch(x, wb, s, None, WFMT_W8B, n, None, None)
+    ref = _ref(x, wref)
+    r = rel_err(out, ref)
+    rn = rel_err(out, _launch(x, q, s, None, WFMT_W8, n, None, None))
+    print(f"\n[w8b {cls} M={m}: rel err {r:.3g}, vs natural layout {rn:.3g}]")
+    assert r <= GEMM_REL and rn <= 1e-2
+    torch.testing.assert_close(out.float(), ref, **TOL_W8[cls])
 
 
 @pytest.mark.gpu
@@ -453,12 +483,14 @@ def _swiglu_ref(x, wg, wu):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["bf16", "w8", "w4"])
+@pytest.mark.parametrize("fmt", ["bf16", "w8", "w8b", "w4"])
 @pytest.mark.parametrize("m", [1, 8, 16])
 def test_fused_swiglu_every_tiling(fmt, m):
     """gate|up with the SwiGLU epilogue (interleaved 16-row gate/up blocks) vs
     the oracle's separate projections + activation; every candidate tiling;
-    and the unfused path (partials + silu_mul on the interleaved layout)."""
+    and the unfused path (partials + silu_mul on the interleaved layout).
+    w8 is int8 in the natural layout (the streaming kernel), w8b and w4 the
+    decode model's block layouts (the int8 / int4 direct kernels)."""
     import ctypes
     from acorninfer_amd import _lib
     from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, WFMT_W8, lib, ptr, stream_ptr
@@ -467,8 +499,10 @@ def test_fused_swiglu_every_tiling(fmt, m):
     inter, k = 1024, 4096
     g = torch.Generator().manual_seed(31)
     w = (0.02 * torch.randn(2 * inter, k, generator=g)).bfloat16().cuda()
-    wf = {"bf16": WFMT_BF16, "w8": WFMT_W8, "w4": WFMT_W4}[fmt]
+    wf = {"bf16": WFMT_BF16, "w8": WFMT_W8, "w8b": WFMT_W8, "w4": WFMT_W4}[fmt]
     lin = QLinear.from_dense(w, wf).interleaved()
+    if fmt == "w8":
+        lin = lin.natural()
     deq = lin.dense()
     x = (torch.randn(m, k, generator=g)).bfloat16().cuda()
     ref = _swiglu_ref(x, deq[:inter], deq[inter:])
