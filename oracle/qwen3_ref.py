@@ -30,11 +30,24 @@ from oracle.ops_ref import inv_freq_ref, rmsnorm_ref
 class Qwen3Ref:
     """Functional Qwen3 over a state dict; KV cache = per-layer contiguous tensors."""
 
-    def __init__(self, cfg, sd: dict[str, torch.Tensor], dtype: torch.dtype = torch.float32):
+    def __init__(self, cfg, sd: dict[str, torch.Tensor], dtype: torch.dtype = torch.float32,
+                 weight_dtype: torch.dtype | None = None):
+        """dtype: activations (every op's output rounded to it, as the
+        reference's torch path rounds in that dtype). weight_dtype: the
+        projection and lm_head weights (default dtype); fp32 with bf16
+        activations keeps dequantised int4 / int8 weights exact while every
+        activation is rounded as in the bf16 path: F.linear then runs on the
+        activation widened to fp32 and its output is rounded to dtype."""
         self.cfg = cfg
         self.dtype = dtype
-        self.w = {k: v.to(device="cpu", dtype=dtype) for k, v in sd.items()}
+        wdt = dtype if weight_dtype is None else weight_dtype
+        self.w = {k: v.to(device="cpu", dtype=wdt if self._is_projection(k) else dtype)
+                  for k, v in sd.items()}
         self.inv_freq = inv_freq_ref(cfg.head_dim, cfg.rope_theta)
+
+    @staticmethod
+    def _is_projection(name: str) -> bool:
+        return name == "lm_head.weight" or name.endswith("_proj.weight")
 
     def new_cache(self) -> list[list[torch.Tensor | None]]:
         return [[None, None] for _ in range(self.cfg.num_hidden_layers)]
@@ -51,7 +64,10 @@ class Qwen3Ref:
         return torch.cat((-x2, x1), dim=-1)
 
     def _linear(self, x, name):
-        return F.linear(x, self.w[name + ".weight"])
+        w = self.w[name + ".weight"]
+        if w.dtype == x.dtype:
+            return F.linear(x, w)
+        return F.linear(x.to(w.dtype), w).to(self.dtype)
 
     def _attention(self, i, h, cos, sin, cache):
         cfg = self.cfg

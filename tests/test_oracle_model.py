@@ -120,3 +120,32 @@ def test_decode_ragged_equals_per_sequence_forward():
     ids = [1, 2, 3, 4]
     assert not torch.allclose(bad.decode_ragged(ids, c2), ref.decode_ragged(ids, caches),
                               rtol=1e-3, atol=1e-3)
+
+
+def test_weight_dtype_keeps_projection_weights_and_rounds_activations():
+    """Qwen3Ref(dtype=bf16, weight_dtype=fp32): the projection and lm_head
+    weights stay fp32 (a dequantised int4 / int8 weight stays exact), every
+    activation is rounded to bf16 as in the bf16 path. With weight_dtype ==
+    dtype it is the plain oracle bit for bit; with fp32 copies of bf16
+    weights it gives the bf16 path's logits up to fp32 accumulation order;
+    with weights that bf16 cannot hold it differs from the bf16 path (the
+    weights were not rounded)."""
+    sd = {k: v.to(torch.bfloat16) for k, v in _sd(seed=9, std=0.05).items()}
+    ids = torch.randint(0, CFG.vocab_size, (1, 11), generator=torch.Generator().manual_seed(10))
+    plain = Qwen3Ref(CFG, sd, torch.bfloat16)
+    same = Qwen3Ref(CFG, sd, torch.bfloat16, weight_dtype=torch.bfloat16)
+    assert torch.equal(plain.forward(ids), same.forward(ids))
+    wide = Qwen3Ref(CFG, sd, torch.bfloat16, weight_dtype=torch.float32)
+    assert wide.w["lm_head.weight"].dtype == torch.float32
+    assert wide.w["layers.0.mlp.down_proj.weight"].dtype == torch.float32
+    assert wide.w["layers.0.input_layernorm.weight"].dtype == torch.bfloat16
+    assert wide.w["embed_tokens.weight"].dtype == torch.bfloat16
+    a, b = plain.forward(ids), wide.forward(ids)
+    assert b.dtype == torch.float32
+    torch.testing.assert_close(b, a, rtol=2e-2, atol=2e-2)
+    # weights off the bf16 grid: the fp32-weight oracle keeps them, so its
+    # logits move away from the all-bf16 oracle's
+    off = {k: (v.float() * (1 + 2 ** -10) if k.endswith("_proj.weight") else v)
+           for k, v in sd.items()}
+    assert not torch.equal(Qwen3Ref(CFG, off, torch.bfloat16, weight_dtype=torch.float32)
+                           .forward(ids), b)
