@@ -21,7 +21,7 @@ LIB_PATH = Path(os.environ.get(
 
 # dtype / format codes (acorn_hip.h)
 F32, F16, BF16 = 0, 1, 2
-WFMT_BF16, WFMT_W8, WFMT_W4, WFMT_F32, WFMT_W4B, WFMT_W8B = 0, 1, 2, 3, 4, 5
+WFMT_BF16, WFMT_W8, WFMT_W4, WFMT_F32, WFMT_W4B, WFMT_W8B, WFMT_BF16B = 0, 1, 2, 3, 4, 5, 6
 
 OK = 0
 ERR_SHAPE, ERR_DTYPE, ERR_VALUE, ERR_UNSUPPORTED, ERR_SCRATCH, ERR_HIP = -1, -2, -3, -4, -5, -1000

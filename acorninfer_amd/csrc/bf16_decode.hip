@@ -1,0 +1,286 @@
+// bf16 GEMM at decode sizes (M <= 16) over the BF16B block layout.
+//
+// y[M,N] = x[M,K] @ W[N,K]^T, bf16 x and W, fp32 accumulation: the bf16
+// projections of a decode step (the reference's decode GEMM,
+// acorninfer/ops/decode_gemm.py:236-257, and its lm_head) at M = batch rows.
+//
+// Built like the int8 and int4 direct kernels (w8_decode.hip, w4_decode.hip),
+// with nothing to unpack:
+//  * The weights of 16 rows x 32 k are one contiguous 1 KB block
+//    (ACORN_WFMT_BF16B): lane lg * 16 + r holds row r's 8 consecutive k
+//    8 lg .. 8 lg + 7, exactly the A operand of one v_mfma_f32_16x16x32_bf16,
+//    so a wave reads a block with one 16-byte load per lane (whole cache
+//    lines, non-temporal policy) and feeds it to the MFMA as loaded. Read in
+//    the natural [N, K] layout the same operand is 16 rows x 64 bytes, half
+//    lines; that streamed 15-25% slower on the 8B shapes.
+//  * Every wave reads its x operands from memory straight into MFMA B
+//    registers with its weights (no LDS staging, no barrier before the first
+//    MFMA); a B operand serves the RT row tiles of the wave.
+//  * KW > 1 waves of a workgroup split K over the same rows and add their
+//    results through LDS in fixed order at the end.
+//  * Split-K (ksplit > 1) writes fp32 partials [ksplit, M, N], summed in split
+//    order by the consumer (bitwise deterministic).
+#include "gemm_common.h"
+
+using namespace acorn;
+
+namespace {
+
+struct BfdArgs {
+  const __bf16* x;
+  const uint8_t* w;
+  __bf16* out;    // bf16 [M, N] (act [M, N/2] with SWIGLU) when ksplit == 1
+  float* part;    // fp32 [ksplit, M, N] otherwise
+  int M, N, K;
+  int kr;         // K range of a split (a multiple of 32 * KW * UPW * DEPTH)
+};
+
+template <int RT, int UPW>
+struct BfdStage {
+  u32x4 w[RT][UPW];          // block (tile rt, block u): this lane's 16 bytes
+  u32x4 x[UPW];              // B operand of block u: x row lr, k 8 lg .. 8 lg + 7
+};
+
+// Grid: x = tile groups of RG * RT 16-row tiles, y = ksplit; block RG * KW
+// waves. Row group r of workgroup b owns tiles (b RG + r) RT .. + RT - 1; its
+// KW waves split the split's K range. Lane (lr, lg) holds x row min(lr, M - 1)
+// (rows past M feed only columns that are never stored).
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU>
+__global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a) {
+  constexpr int NW = RG * KW;
+  const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lg = lane >> 4, lr = lane & 15;
+  const int rg = wid / KW, kq = wid % KW;
+  const int KB = a.K / 32;                        // blocks per row tile
+  const int t0 = (blockIdx.x * RG + rg) * RT;
+  const bool active = t0 < a.N / 16;              // (N / 16) % RT == 0 by the plan
+  const int tt = active ? t0 : 0;                 // idle waves read tile 0, store nothing
+  const int BW = a.kr / (32 * KW);                // blocks of this wave
+  const int kw0 = blockIdx.y * a.kr + kq * BW * 32;
+  const int ns = BW / UPW;                        // stages, a multiple of DEPTH
+  const uint8_t* wb = a.w + ((size_t)tt * KB + kw0 / 32) * 1024 + lane * 16;
+  const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 8 * lg;
+  auto load = [&](int s, BfdStage<RT, UPW>& r) {
+#pragma unroll
+    for (int u = 0; u < UPW; ++u) r.x[u] = *(const u32x4*)(xb + (s * UPW + u) * 32);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int u = 0; u < UPW; ++u)
+        r.w[rt][u] = load_nt((const u32x4*)(wb + ((size_t)rt * KB + s * UPW + u) * 1024));
+  };
+
+  BfdStage<RT, UPW> ring[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+  f32x4 acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const BfdStage<RT, UPW>& r) {
+#pragma unroll
+    for (int u = 0; u < UPW; ++u)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) acc[rt] = mfma(r.w[rt][u], r.x[u], acc[rt]);
+  };
+  int s0 = 0;
+  for (; s0 + DEPTH < ns; s0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      compute(ring[d]);
+      load(s0 + DEPTH + d, ring[d]);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) compute(ring[d]);
+  if constexpr (KW > 1) {
+    // the K slices of a row group, added in slice order by slice 0
+    __shared__ f32x4 red[NW][RT][kWave];
+    if (kq != 0) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) red[wid][rt][lane] = acc[rt];
+    }
+    __syncthreads();
+    if (kq != 0) return;
+#pragma unroll
+    for (int q = 1; q < KW; ++q)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const f32x4 v = red[wid + q][rt][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[rt][i] += v[i];
+      }
+  }
+  if (!active || lr >= a.M) return;
+
+  // lane (lr, lg) holds rows 4 lg .. 4 lg + 3 of each tile, column (x row) lr
+  if constexpr (SWIGLU) {
+    // tiles 2p (gate) and 2p + 1 (up) hold the 16 outputs of block t0 / 2 + p
+    const int NA = a.N / 2;
+#pragma unroll
+    for (int p = 0; p < RT / 2; ++p) {
+      const int n = (t0 / 2 + p) * 16 + 4 * lg;
+      uint32_t v[2];
+      v[0] = pack_bf16x2(swiglu_bf16(acc[2 * p][0], acc[2 * p + 1][0]),
+                         swiglu_bf16(acc[2 * p][1], acc[2 * p + 1][1]));
+      v[1] = pack_bf16x2(swiglu_bf16(acc[2 * p][2], acc[2 * p + 1][2]),
+                         swiglu_bf16(acc[2 * p][3], acc[2 * p + 1][3]));
+      __builtin_memcpy(a.out + (size_t)lr * NA + n, v, sizeof(v));
+    }
+  } else if (a.out) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int n = (t0 + rt) * 16 + 4 * lg;
+      uint32_t v[2] = {pack_bf16x2(acc[rt][0], acc[rt][1]), pack_bf16x2(acc[rt][2], acc[rt][3])};
+      __builtin_memcpy(a.out + (size_t)lr * a.N + n, v, sizeof(v));
+    }
+  } else {
+    float* dst = a.part + ((size_t)blockIdx.y * a.M + lr) * a.N;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) *(f32x4*)(dst + (t0 + rt) * 16 + 4 * lg) = acc[rt];
+  }
+}
+
+template <int RT, int UPW, int DEPTH, int RG, int KW>
+int launch(const DirectPlan& p, const BfdArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(RG * KW * kWave);
+  if constexpr (RT >= 2) {
+    if (p.swiglu) {
+      bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, true><<<grid, block, 0, st>>>(a);
+      return ACORN_OK;
+    }
+  }
+  if (p.swiglu) return ACORN_ERR_UNSUPPORTED;
+  bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false><<<grid, block, 0, st>>>(a);
+  return ACORN_OK;
+}
+
+template <int RT, int UPW, int DEPTH>
+int by_layout(const DirectPlan& p, const BfdArgs& a, hipStream_t st) {
+  switch (p.nw_field) {
+    case 1: return launch<RT, UPW, DEPTH, 1, 1>(p, a, st);
+    case 4: return launch<RT, UPW, DEPTH, 4, 1>(p, a, st);
+    case 22: return launch<RT, UPW, DEPTH, 1, 2>(p, a, st);
+    case 44: return launch<RT, UPW, DEPTH, 1, 4>(p, a, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+// registers of one stage (dwords per lane): weights and x operands
+constexpr int stage_dwords(int rt, int upw) { return 4 * rt * upw + 4 * upw; }
+constexpr int kRingDwords = 192;   // the ring's budget (depth x stage)
+
+template <int RT, int UPW>
+int by_depth(const DirectPlan& p, const BfdArgs& a, hipStream_t st) {
+  switch (p.depth) {
+    case 2: return by_layout<RT, UPW, 2>(p, a, st);
+    case 4:
+      if constexpr (4 * stage_dwords(RT, UPW) <= kRingDwords) return by_layout<RT, UPW, 4>(p, a, st);
+      break;
+    case 8:
+      if constexpr (8 * stage_dwords(RT, UPW) <= kRingDwords) return by_layout<RT, UPW, 8>(p, a, st);
+      break;
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+template <int RT>
+int by_upw(const DirectPlan& p, const BfdArgs& a, hipStream_t st) {
+  switch (p.upw) {
+    case 1: return by_depth<RT, 1>(p, a, st);
+    case 2: return by_depth<RT, 2>(p, a, st);
+    case 4: return by_depth<RT, 4>(p, a, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
+}
+
+int divisor_at_least(int64_t n, int64_t v) {
+  while (v <= n && n % v) ++v;
+  return v <= n ? (int)v : 0;
+}
+
+}  // namespace
+
+namespace acorn {
+
+// rt 1/2/4 (swiglu 2/4; N/16 divisible by rt), upw 1/2/4 blocks of 32 k per
+// stage, the wave layout in the nw field (1 or 4 waves on their own rows; 22,
+// 44 = 2 or 4 waves splitting K over one row group), depth 2/4/8 within the
+// ring's register budget (then upw lowered where the rows are too short for
+// it), and split counts that give every wave a whole number of depth rounds. With 0 the plan takes rt 1 (2 with swiglu), upw 2,
+// one wave per workgroup, depth 4 (8 KB of weights in flight per wave), and
+// the fewest splits that launch at least three waves per CU.
+int bf16b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu,
+                    DirectPlan* p) {
+  if (M < 1 || M > 16) return ACORN_ERR_UNSUPPORTED;
+  if (N % 16 || K % 64) return ACORN_ERR_SHAPE;
+  if (swiglu && N % 32) return ACORN_ERR_SHAPE;
+  const int64_t ntiles = N / 16, KB = K / 32;
+  int rt = cfg && cfg[0] > 0 ? cfg[0] : swiglu ? 2 : 1;
+  int upw = cfg && cfg[1] > 0 ? cfg[1] : 2;
+  const int nwf = cfg && cfg[2] > 0 ? cfg[2] : 1;
+  const int req_ks = cfg ? cfg[3] : 0;
+  int depth = cfg && cfg[4] > 0 ? cfg[4] : 4;
+  if (rt != 1 && rt != 2 && rt != 4) return ACORN_ERR_UNSUPPORTED;
+  if (swiglu && rt < 2) rt = 2;
+  while (rt > (swiglu ? 2 : 1) && ntiles % rt) rt /= 2;
+  if (ntiles % rt) return ACORN_ERR_UNSUPPORTED;
+  if (upw != 1 && upw != 2 && upw != 4) return ACORN_ERR_UNSUPPORTED;
+  if (nwf != 1 && nwf != 4 && nwf != 22 && nwf != 44) return ACORN_ERR_UNSUPPORTED;
+  const int nw = nwf < 10 ? nwf : nwf / 10, kw = nwf < 10 ? 1 : nwf % 10;
+  if (depth != 2 && depth != 4 && depth != 8) return ACORN_ERR_UNSUPPORTED;
+  while (depth > 2 && (depth * stage_dwords(rt, upw) > kRingDwords || KB % (kw * upw * depth)))
+    depth /= 2;
+  while (upw > 1 && KB % (kw * upw * depth)) upw /= 2;   // short rows (K of 64 or 128)
+  if (depth * stage_dwords(rt, upw) > kRingDwords) return ACORN_ERR_UNSUPPORTED;
+  if (KB % (kw * upw * depth)) return ACORN_ERR_SHAPE;
+  const int64_t q = KB / (kw * upw * depth);    // ks must divide this
+  const int64_t waves = ntiles / rt * kw;
+  int ks;
+  if (swiglu) {
+    ks = 1;
+  } else if (req_ks > 0) {
+    ks = divisor_at_least(q, req_ks);
+    if (!ks) return ACORN_ERR_UNSUPPORTED;
+  } else {
+    ks = 1;
+    while (waves * ks < 3 * 256) {
+      const int nx = divisor_at_least(q, ks + 1);
+      if (!nx) break;
+      ks = nx;
+    }
+  }
+  const int64_t rgs = nw / kw;
+  const int64_t groups = (ntiles / rt + rgs - 1) / rgs;
+  if (groups > 0x7fffffff || ks > 65535) return ACORN_ERR_SHAPE;
+  p->rt = rt;
+  p->upw = upw;
+  p->nw_field = nwf;
+  p->rg = (int)rgs;
+  p->kw = kw;
+  p->ksplit = ks;
+  p->depth = depth;
+  p->groups = (int)groups;
+  p->swiglu = swiglu;
+  return ACORN_OK;
+}
+
+int bf16b_launch(const DirectPlan& p, const void* x, const void* w, void* out, float* part,
+                 int64_t M, int64_t N, int64_t K, hipStream_t st) {
+  if (!x || !w) return ACORN_ERR_VALUE;
+  if (M < 1 || M > 16) return ACORN_ERR_UNSUPPORTED;
+  if (p.ksplit > 1) out = nullptr;
+  if (!out && (!part || p.swiglu)) return ACORN_ERR_VALUE;
+  const BfdArgs a{(const __bf16*)x, (const uint8_t*)w, (__bf16*)out, part, (int)M, (int)N,
+                  (int)K, (int)(K / p.ksplit)};
+  int rc = ACORN_ERR_UNSUPPORTED;
+  switch (p.rt) {
+    case 1: rc = by_upw<1>(p, a, st); break;
+    case 2: rc = by_upw<2>(p, a, st); break;
+    case 4: rc = by_upw<4>(p, a, st); break;
+  }
+  if (rc) return rc;
+  ACORN_LAUNCH_CHECK();
+  return ACORN_OK;
+}
+
+}  // namespace acorn

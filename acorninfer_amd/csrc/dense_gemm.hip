@@ -41,7 +41,9 @@ namespace {
 constexpr int kDenseBK = 64;               // k per step
 constexpr int kXPitch = kDenseBK * 2 + 16; // bytes per staged x row (padded by 8 bf16)
 
-template <typename OUT, int WN, int BM, int DEPTH>
+// BLK: w in the BF16B layout (1 KB blocks of 16 rows x 32 k in the A operand
+// lane order), read at the same lanes' addresses.
+template <typename OUT, int WN, int BM, int DEPTH, bool BLK>
 __global__ __launch_bounds__(256, 1) void dense_gemm_kernel(const __bf16* __restrict__ x,
                                                             const __bf16* __restrict__ w,
                                                             OUT* __restrict__ out, int M, int N,
@@ -72,11 +74,18 @@ __global__ __launch_bounds__(256, 1) void dense_gemm_kernel(const __bf16* __rest
   const int kbase = blockIdx.y * steps * kDenseBK;
   out += (size_t)blockIdx.y * M * N;
 
-  // weight rows of the wave's NB blocks (rows past N re-read row N - 1)
+  // weight rows of the wave's NB blocks (rows past N re-read row N - 1; in
+  // blocks, tiles past N re-read the last tile), and the element step per k
+  constexpr int KSTR = BLK ? 16 : 1;
   const __bf16* wrow[NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-    wrow[nb] = w + (size_t)min(n0 + 16 * nb + c, N - 1) * K + kbase + 8 * r;
+  for (int nb = 0; nb < NB; ++nb) {
+    if constexpr (BLK)
+      wrow[nb] = w + ((size_t)min((n0 + 16 * nb) / 16, N / 16 - 1) * (K / 32) + kbase / 32) * 512 +
+                 8 * lane;
+    else
+      wrow[nb] = w + (size_t)min(n0 + 16 * nb + c, N - 1) * K + kbase + 8 * r;
+  }
   // the x pieces this thread stages: row p / 8, k (p % 8) * 8 of the step
   const __bf16* xrow[XP];
   uint32_t xoff[XP];
@@ -93,7 +102,7 @@ __global__ __launch_bounds__(256, 1) void dense_gemm_kernel(const __bf16* __rest
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) dst[nb][kk] = *(const u32x4*)(wrow[nb] + k0 + 32 * kk);
+      for (int kk = 0; kk < 2; ++kk) dst[nb][kk] = *(const u32x4*)(wrow[nb] + KSTR * (k0 + 32 * kk));
   };
   auto load_x = [&](int s) {
     const int k0 = s * kDenseBK;
@@ -311,7 +320,11 @@ constexpr int kDlBK = 32;                 // k per stage
 constexpr int kDlStages = 4;              // LDS stages: two pair buffers
 constexpr int kDlOpBytes = kLdsTile * kDlBK * 2;   // one operand of one stage: 16 KB
 
-template <typename OUT, int NW, bool SWIGLU = false>
+// BLK: w in the BF16B layout. Its loads move whole 1 KB blocks (16 rows x 32
+// k) instead of 128-byte rows; block (row tile t, stage half h) of a pair
+// sits at LDS block 2 t + h, and a lane's A operand is its own 16 bytes of a
+// block (no swizzle needed: 64 lanes read 1 KB contiguously).
+template <typename OUT, int NW, bool SWIGLU, bool BLK>
 __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __restrict__ x,
                                                               const __bf16* __restrict__ w,
                                                               OUT* __restrict__ out, int M,
@@ -345,19 +358,29 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
   // of this wave fills rows 8 (LPW wid + j) .. + 7 of an operand, lane L
   // writing row 8 (LPW wid + j) + L / 8, slot L % 8, with global piece
   // (L % 8) ^ ((row >> 1) & 7)
+  constexpr int KSTR = BLK ? 16 : 1;             // weight elements per k
   const __bf16* wsrc[LPW];
   const __bf16* xsrc[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int row = 8 * (LPW * wid + j) + (lane >> 3);
     const int piece = (lane & 7) ^ ((row >> 1) & 7);
-    wsrc[j] = w + (size_t)min(n0 + row, N - 1) * K + kbase + 8 * piece;
+    if constexpr (BLK) {
+      const int b = LPW * wid + j;                // block (tile b / 2, half b % 2)
+      wsrc[j] = w + ((size_t)min(n0 / 16 + b / 2, N / 16 - 1) * (K / 32) + kbase / 32 + b % 2) * 512 +
+                8 * lane;
+    } else {
+      wsrc[j] = w + (size_t)min(n0 + row, N - 1) * K + kbase + 8 * piece;
+    }
     xsrc[j] = x + (size_t)min(m0 + row, M - 1) * K + kbase + 8 * piece;
   }
   // operand reads of stage half h: block i's row wn + 16 i + c, piece 4 h + r
-  // at slot (4 h + r) ^ (c >> 1); block i sits 2048 bytes after block 0
-  const uint32_t aoff0 = (uint32_t)((wn + c) * 128 + 16 * (r ^ (c >> 1)));
-  const uint32_t aoff1 = (uint32_t)((wn + c) * 128 + 16 * ((4 + r) ^ (c >> 1)));
+  // at slot (4 h + r) ^ (c >> 1); block i sits 2048 bytes after block 0 (in
+  // blocks: LDS block 2 (wn / 16 + i) + h, the lane's own 16 bytes)
+  const uint32_t aoff0 = BLK ? (uint32_t)(wn * 128 + 16 * lane)
+                             : (uint32_t)((wn + c) * 128 + 16 * (r ^ (c >> 1)));
+  const uint32_t aoff1 = BLK ? aoff0 + 1024u
+                             : (uint32_t)((wn + c) * 128 + 16 * ((4 + r) ^ (c >> 1)));
   const uint32_t boff0 = (uint32_t)((wm + c) * 128 + 16 * (r ^ (c >> 1)));
   const uint32_t boff1 = (uint32_t)((wm + c) * 128 + 16 * ((4 + r) ^ (c >> 1)));
 
@@ -377,7 +400,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
     const int k0 = min(d, pairs - 1) * 2 * kDlBK;
     const uint32_t base = lds0 + (uint32_t)((d & 1) * 2 * PAIR + LPW * wid * 1024);
 #pragma unroll
-    for (int j = 0; j < LPW; ++j) dma(wsrc[j] + k0, base + j * 1024);
+    for (int j = 0; j < LPW; ++j) dma(wsrc[j] + KSTR * k0, base + j * 1024);
 #pragma unroll
     for (int j = 0; j < LPW; ++j) dma(xsrc[j] + k0, base + PAIR + j * 1024);
   };
@@ -400,7 +423,7 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
   auto issue_one = [&](int d, int i) {
     const int k0 = min(d, pairs - 1) * 2 * kDlBK;
     const uint32_t base = lds0 + (uint32_t)((d & 1) * 2 * PAIR + LPW * wid * 1024);
-    if (i < LPW) dma(wsrc[i] + k0, base + i * 1024);
+    if (i < LPW) dma(wsrc[i] + KSTR * k0, base + i * 1024);
     else dma(xsrc[i - LPW] + k0, base + PAIR + (i - LPW) * 1024);
   };
   auto stage = [&](int s, const u32x4 (&bc)[MB], u32x4 (&bn)[MB], int dq) {
@@ -486,12 +509,12 @@ __global__ __launch_bounds__(NW * 64, 1) void dense_dl_kernel(const __bf16* __re
   }
 }
 
-template <typename OUT, int NW, bool SWIGLU = false>
+template <typename OUT, int NW, bool SWIGLU, bool BLK>
 int launch_dl(const void* x, const void* w, void* out, int64_t M, int64_t N, int64_t K, int ks,
               hipStream_t st) {
   const int64_t tiles_n = (N + kLdsTile - 1) / kLdsTile, tiles_m = (M + kLdsTile - 1) / kLdsTile;
   if (tiles_n * tiles_m > 0x7fffffff) return ACORN_ERR_SHAPE;
-  dense_dl_kernel<OUT, NW, SWIGLU>
+  dense_dl_kernel<OUT, NW, SWIGLU, BLK>
       <<<dim3((unsigned)(tiles_n * tiles_m), (unsigned)ks), dim3(NW * 64), 0, st>>>(
       (const __bf16*)x, (const __bf16*)w, (OUT*)out, (int)M, (int)N, (int)K, (int)tiles_n,
       (int)tiles_m, (int)(K / kDlBK / ks));
@@ -510,38 +533,44 @@ int launch_lds(const void* x, const void* w, void* out, int64_t M, int64_t N, in
   return ACORN_OK;
 }
 
-template <typename OUT, int WN, int BM, int DEPTH>
+template <typename OUT, int WN, int BM, int DEPTH, bool BLK>
 int launch(const void* x, const void* w, void* out, int64_t M, int64_t N, int64_t K, int ks,
            hipStream_t st) {
   const int64_t tiles_n = (N + 4 * WN - 1) / (4 * WN), tiles_m = (M + BM - 1) / BM;
   if (tiles_n * tiles_m > 0x7fffffff) return ACORN_ERR_SHAPE;
-  dense_gemm_kernel<OUT, WN, BM, DEPTH>
+  dense_gemm_kernel<OUT, WN, BM, DEPTH, BLK>
       <<<dim3((unsigned)(tiles_n * tiles_m), (unsigned)ks), dim3(256), 0, st>>>(
           (const __bf16*)x, (const __bf16*)w, (OUT*)out, (int)M, (int)N, (int)K, (int)tiles_n,
           (int)tiles_m, (int)(K / kDenseBK / ks));
   return ACORN_OK;
 }
 
-template <typename OUT>
+template <typename OUT, bool BLK>
 int dispatch(int wn, int bm, int depth, const void* x, const void* w, void* out, int64_t M,
              int64_t N, int64_t K, int ks, hipStream_t st) {
   if (bm == kLdsTile) {
-    if (wn == 64 && depth == 2) return launch_lds<OUT, 2>(x, w, out, M, N, K, ks, st);
-    if (wn == 128 && depth == kDlStages) return launch_dl<OUT, 8>(x, w, out, M, N, K, ks, st);
+    if constexpr (!BLK) {
+      if (wn == 64 && depth == 2) return launch_lds<OUT, 2>(x, w, out, M, N, K, ks, st);
+    }
+    if (wn == 128 && depth == kDlStages)
+      return launch_dl<OUT, 8, false, BLK>(x, w, out, M, N, K, ks, st);
   } else if (wn == 64) {
-    if (bm == 128 && depth == 2) return launch<OUT, 64, 128, 2>(x, w, out, M, N, K, ks, st);
-    if (bm == 128 && depth == 4) return launch<OUT, 64, 128, 4>(x, w, out, M, N, K, ks, st);
-    if (bm == 64 && depth == 2) return launch<OUT, 64, 64, 2>(x, w, out, M, N, K, ks, st);
-    if (bm == 64 && depth == 4) return launch<OUT, 64, 64, 4>(x, w, out, M, N, K, ks, st);
+    if (bm == 128 && depth == 2) return launch<OUT, 64, 128, 2, BLK>(x, w, out, M, N, K, ks, st);
+    if (bm == 128 && depth == 4) return launch<OUT, 64, 128, 4, BLK>(x, w, out, M, N, K, ks, st);
+    if (bm == 64 && depth == 2) return launch<OUT, 64, 64, 2, BLK>(x, w, out, M, N, K, ks, st);
+    if (bm == 64 && depth == 4) return launch<OUT, 64, 64, 4, BLK>(x, w, out, M, N, K, ks, st);
   } else if (wn == 128) {
-    if (bm == 64 && depth == 2) return launch<OUT, 128, 64, 2>(x, w, out, M, N, K, ks, st);
+    if (bm == 64 && depth == 2) return launch<OUT, 128, 64, 2, BLK>(x, w, out, M, N, K, ks, st);
   }
   return ACORN_ERR_UNSUPPORTED;
 }
 
 }  // namespace
 
-bool dense_gemm_supported(int64_t N, int64_t K, int wn, int bm, int depth, int ks) {
+bool dense_gemm_supported(int64_t N, int64_t K, int wn, int bm, int depth, int ks, bool blocked) {
+  // the block layout: whole 16-row tiles and 64-k steps; not the
+  // register-staged 256 x 256 form
+  if (blocked && (N % 16 || K % 64 || (bm == kLdsTile && wn != 128))) return false;
   if (bm == kLdsTile && wn == 128)   // direct-to-LDS form: 32 k per stage
     return depth == kDlStages && ks >= 1 && ks <= 64 && N % 4 == 0 && K % kDlBK == 0 &&
            (K / kDlBK) % (2 * ks) == 0;
@@ -554,22 +583,27 @@ bool dense_gemm_supported(int64_t N, int64_t K, int wn, int bm, int depth, int k
 }
 
 int dense_gemm_launch(const void* x, const void* w, void* out_bf16, float* out_f32, int64_t M,
-                      int64_t N, int64_t K, int wn, int bm, int depth, int ks, hipStream_t st) {
-  if (!dense_gemm_supported(N, K, wn, bm, depth, ks)) return ACORN_ERR_UNSUPPORTED;
-  if (out_f32) return dispatch<float>(wn, bm, depth, x, w, out_f32, M, N, K, ks, st);
+                      int64_t N, int64_t K, int wn, int bm, int depth, int ks, bool blocked,
+                      hipStream_t st) {
+  if (!dense_gemm_supported(N, K, wn, bm, depth, ks, blocked)) return ACORN_ERR_UNSUPPORTED;
+  if (out_f32)
+    return blocked ? dispatch<float, true>(wn, bm, depth, x, w, out_f32, M, N, K, ks, st)
+                   : dispatch<float, false>(wn, bm, depth, x, w, out_f32, M, N, K, ks, st);
   if (ks != 1) return ACORN_ERR_VALUE;
-  return dispatch<__bf16>(wn, bm, depth, x, w, out_bf16, M, N, K, 1, st);
+  return blocked ? dispatch<__bf16, true>(wn, bm, depth, x, w, out_bf16, M, N, K, 1, st)
+                 : dispatch<__bf16, false>(wn, bm, depth, x, w, out_bf16, M, N, K, 1, st);
 }
 
-bool dense_gemm_swiglu_supported(int64_t N, int64_t K, int wn, int bm, int depth) {
+bool dense_gemm_swiglu_supported(int64_t N, int64_t K, int wn, int bm, int depth, bool blocked) {
   return bm == kLdsTile && wn == 128 && N % 32 == 0 &&
-         dense_gemm_supported(N, K, wn, bm, depth, 1);
+         dense_gemm_supported(N, K, wn, bm, depth, 1, blocked);
 }
 
 int dense_gemm_swiglu_launch(const void* x, const void* w, void* act, int64_t M, int64_t N,
-                             int64_t K, int wn, int bm, int depth, hipStream_t st) {
-  if (!dense_gemm_swiglu_supported(N, K, wn, bm, depth)) return ACORN_ERR_UNSUPPORTED;
-  return launch_dl<__bf16, 8, true>(x, w, act, M, N, K, 1, st);
+                             int64_t K, int wn, int bm, int depth, bool blocked, hipStream_t st) {
+  if (!dense_gemm_swiglu_supported(N, K, wn, bm, depth, blocked)) return ACORN_ERR_UNSUPPORTED;
+  return blocked ? launch_dl<__bf16, 8, true, true>(x, w, act, M, N, K, 1, st)
+                 : launch_dl<__bf16, 8, true, false>(x, w, act, M, N, K, 1, st);
 }
 
 }  // namespace acorn

@@ -1,6 +1,7 @@
-// Device helpers shared by the weight-only GEMM kernels (quant_gemm.hip and
-// w4_decode.hip), the W4B block-layout index maps, and the interface of the
-// int4 decode kernel that quant_gemm.hip's planner dispatches to.
+// Device helpers shared by the weight-only GEMM kernels (quant_gemm.hip,
+// w4_decode.hip, w8_decode.hip, bf16_decode.hip, dense_gemm.hip), the block
+// layouts' index maps, and the interfaces of the kernels that quant_gemm.hip's
+// planner dispatches to.
 #pragma once
 
 #include "common.h"
@@ -108,6 +109,13 @@ __host__ __device__ inline size_t w8b_chunk_offset(int64_t n, int64_t c, int64_t
   return ((size_t)(n / 16) * (size_t)(K / 64) + (size_t)(c / 4)) * 1024 +
          (size_t)((c % 4) * 16 + n % 16) * 16;
 }
+// BF16B: bf16 weights in 1 KB blocks of 16 rows x 32 k; the 8 bf16 (16
+// bytes) of row n, k in [8c, 8c+8) (c = k/8 within the tensor), as a byte
+// offset.
+__host__ __device__ inline size_t bf16b_piece_offset(int64_t n, int64_t c, int64_t K) {
+  return ((size_t)(n / 16) * (size_t)(K / 32) + (size_t)(c / 4)) * 1024 +
+         (size_t)((c % 4) * 16 + n % 16) * 16;
+}
 // Scale (zero) of row n, group g: records of 4 rows x 4 groups per lane
 // group, so a lane's scales of consecutive groups are contiguous.
 __host__ __device__ inline size_t w4b_half_index(int64_t n, int64_t g, int64_t K) {
@@ -156,34 +164,41 @@ int w4m_launch(const W4mPlan& p, const void* x, const void* w, const void* scale
 int w4b_dequant(const void* w, const void* scale, void* out, int64_t N, int64_t K,
                 hipStream_t st);
 
-// ---- the W8B decode kernel (w8_decode.hip), M <= 16 ---------------------------
-// cfg knobs: rt (row tiles of 16 per wave), upw (64-k blocks per pipeline
-// stage), nw (the wave layout: 1 or 4 waves on their own rows, 22 / 44 = 2 / 4
-// waves splitting K over shared rows), ksplit, depth (stages in flight).
-struct W8bPlan {
+// ---- the W8B and BF16B decode kernels (w8_decode.hip, bf16_decode.hip) ------
+// M <= 16, weights in 1 KB blocks, x read straight into MFMA registers.
+// cfg knobs: rt (row tiles of 16 per wave), upw (blocks per pipeline stage),
+// nw (the wave layout: 1 or 4 waves on their own rows, 22 / 44 = 2 / 4 waves
+// splitting K over shared rows), ksplit, depth (stages in flight).
+struct DirectPlan {
   int rt, upw, nw_field, rg, kw, ksplit, depth;
   int groups;      // workgroups along N
   bool swiglu;
 };
-int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W8bPlan* p);
+int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, DirectPlan* p);
 // out (bf16 [M,N], or act [M,N/2] for swiglu) when given and ksplit == 1;
 // otherwise fp32 partials part[ksplit, M, N] (each already scaled).
-int w8b_launch(const W8bPlan& p, const void* x, const void* w, const void* scale, void* out,
+int w8b_launch(const DirectPlan& p, const void* x, const void* w, const void* scale, void* out,
                float* part, int64_t M, int64_t N, int64_t K, hipStream_t st);
+int bf16b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu,
+                    DirectPlan* p);
+int bf16b_launch(const DirectPlan& p, const void* x, const void* w, void* out, float* part,
+                 int64_t M, int64_t N, int64_t K, hipStream_t st);
 
 // ---- the large-M bf16 GEMM (dense_gemm.hip) ---------------------------------
 // out[M,N] = x[M,K] . w[N,K]^T, bf16 operands: (4 wn) x bm output tiles (wn
 // weight rows per wave: 64 or 128; bm 64 or 128), weights prefetched `depth`
 // K steps of 64 ahead (2 or 4), the K range cut into ks splits. fp32 output
 // when out_f32 is given (split s into out_f32 + s*M*N), else bf16 into
-// out_bf16 (ks == 1 only).
-bool dense_gemm_supported(int64_t N, int64_t K, int wn, int bm, int depth, int ks);
+// out_bf16 (ks == 1 only). blocked: w in the BF16B layout (every form but
+// the register-staged 256 x 256 one).
+bool dense_gemm_supported(int64_t N, int64_t K, int wn, int bm, int depth, int ks, bool blocked);
 // gate|up (16-row interleave) with the SwiGLU epilogue: act [M, N / 2] bf16,
 // one split, the direct-to-LDS form (bm 256, wn 128) and N % 32 == 0
-bool dense_gemm_swiglu_supported(int64_t N, int64_t K, int wn, int bm, int depth);
+bool dense_gemm_swiglu_supported(int64_t N, int64_t K, int wn, int bm, int depth, bool blocked);
 int dense_gemm_swiglu_launch(const void* x, const void* w, void* act, int64_t M, int64_t N,
-                             int64_t K, int wn, int bm, int depth, hipStream_t st);
+                             int64_t K, int wn, int bm, int depth, bool blocked, hipStream_t st);
 int dense_gemm_launch(const void* x, const void* w, void* out_bf16, float* out_f32, int64_t M,
-                      int64_t N, int64_t K, int wn, int bm, int depth, int ks, hipStream_t st);
+                      int64_t N, int64_t K, int wn, int bm, int depth, int ks, bool blocked,
+                      hipStream_t st);
 
 }  // namespace acorn

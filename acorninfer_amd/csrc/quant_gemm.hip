@@ -577,6 +577,12 @@ __global__ __launch_bounds__(256, 2) void wgemm_tile_kernel(KArgs a) {
     } else if constexpr (WFMT == ACORN_WFMT_W8) {
 #pragma unroll
       for (int j = 0; j < WR; ++j) wr[j] = *(const u32x4*)(a.w + wk + 16 * j);
+    } else if constexpr (WFMT == ACORN_WFMT_BF16B) {
+      // the same pieces in the 1 KB block layout: an instruction covers
+      // BROWS rows x BK k, whole blocks, so again whole cache lines
+#pragma unroll
+      for (int j = 0; j < WR; ++j)
+        wr[j] = load_nt((const u32x4*)(a.w + bf16b_piece_offset(n0 + brow + BROWS * j, k0 / 8 + bpiece, K)));
     } else {
       // bf16: instruction j reads whole 16-byte pieces of rows BROWS*j + t/PPR,
       // consecutive threads consecutive pieces, so each instruction consumes
@@ -747,9 +753,11 @@ struct Tiling {
                                  //     nw = weight rows per wave, tpw = prefetch depth),
                                  // 4 = W4B mid-M kernel (rt == kMidRT, upw = row tiles
                                  //     per wave, nw = waves, tpw = groups in flight),
-                                 // 5 = W8B decode kernel (tpw = its pipeline depth)
+                                 // 5 = W8B decode kernel (tpw = its pipeline depth),
+                                 // 6 = BF16B decode kernel (tpw = its pipeline depth)
   W4bPlan w4b;
-  W8bPlan w8b;
+  DirectPlan w8b;
+  DirectPlan bf16b;
   W4mPlan w4m;
 };
 
@@ -795,7 +803,8 @@ int make_tile_plan(int64_t M, int64_t N, int64_t K, int wfmt, int req_bm, int re
   const int bk = kTileKN / bn;
   const int align = (wfmt == ACORN_WFMT_W4 || wfmt == ACORN_WFMT_W4B) ? std::max(128, bk) : bk;
   if (wfmt == ACORN_WFMT_W4B && (K % 512 || N % 16)) return ACORN_ERR_SHAPE;
-  if (wfmt == ACORN_WFMT_W8B && (K % 64 || N % 16)) return ACORN_ERR_SHAPE;
+  if ((wfmt == ACORN_WFMT_W8B || wfmt == ACORN_WFMT_BF16B) && (K % 64 || N % 16))
+    return ACORN_ERR_SHAPE;
   if (K % align) return ACORN_ERR_SHAPE;
   const int bm = (req_bm == 32 || req_bm == 64 || req_bm == 128) ? req_bm
                  : M <= 32 ? 32 : M <= 64 ? 64 : 128;
@@ -861,13 +870,18 @@ constexpr int kMidRT = -3;
 int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling* t,
               bool swiglu = false) {
   if (M <= 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
+  // the block layouts exist only for whole blocks
+  if ((wfmt == ACORN_WFMT_W8B || wfmt == ACORN_WFMT_BF16B) && (N % 16 || K % 64))
+    return ACORN_ERR_SHAPE;
+  if (wfmt == ACORN_WFMT_W4B && (N % 16 || K % 512)) return ACORN_ERR_SHAPE;
   t->swiglu = swiglu;
   t->kind = 0;
   const bool no_request = !cfg || (cfg[0] == 0 && cfg[1] == 0 && cfg[2] == 0 && cfg[3] <= 1 &&
                                    cfg[4] == 0);
   // the SwiGLU epilogue is built into the direct-to-LDS form only (from
   // kDenseLdsM rows, or on request)
-  if (wfmt == ACORN_WFMT_BF16 &&
+  const bool blocked = wfmt == ACORN_WFMT_BF16B;
+  if ((wfmt == ACORN_WFMT_BF16 || blocked) &&
       ((cfg && cfg[0] == kDenseRT) || (no_request && M >= (swiglu ? kDenseLdsM : kDenseMinM)))) {
     const bool req = cfg && cfg[0] == kDenseRT;
     // from kDenseMinM rows the 256 x 256 tiles with both operands in LDS
@@ -875,8 +889,8 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
     const int wn = req && cfg[2] > 0              ? cfg[2]
                    : bm == 256 && !(req && cfg[4] == 2) ? 128    // depth 2: the staged form
                                                         : 64;
-    // (bm 256: wn 64 is the register-staged form, depth 2; wn 128 the
-    // direct-to-LDS form, a 4-stage ring)
+    // (bm 256: wn 64 is the register-staged form, depth 2, natural weights
+    // only; wn 128 the direct-to-LDS form, a 4-stage ring)
     const int depth = req && cfg[4] > 0 ? cfg[4] : bm == 256 ? (wn == 128 ? 4 : 2) : 4;
     const int ntile = bm == 256 ? 256 : 4 * wn;    // weight rows per workgroup
     int ks = req && cfg[3] > 0 ? cfg[3] : 1;
@@ -889,15 +903,15 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
       const int64_t tiles = ((N + ntile - 1) / ntile) * ((M + bm - 1) / bm);
       if (bm == 256) {
         while (tiles * 2 * ks <= kCUs && ks < 16 &&
-               dense_gemm_supported(N, K, wn, bm, depth, 2 * ks))
+               dense_gemm_supported(N, K, wn, bm, depth, 2 * ks, blocked))
           ks *= 2;
       } else {
-        while (tiles * ks < kCUs && ks < 8 && dense_gemm_supported(N, K, wn, bm, depth, 2 * ks))
+        while (tiles * ks < kCUs && ks < 8 && dense_gemm_supported(N, K, wn, bm, depth, 2 * ks, blocked))
           ks *= 2;
       }
     }
-    if (swiglu ? ks == 1 && dense_gemm_swiglu_supported(N, K, wn, bm, depth)
-               : dense_gemm_supported(N, K, wn, bm, depth, ks)) {
+    if (swiglu ? ks == 1 && dense_gemm_swiglu_supported(N, K, wn, bm, depth, blocked)
+               : dense_gemm_supported(N, K, wn, bm, depth, ks, blocked)) {
       t->kind = 3;
       t->rt = kDenseRT;
       t->upw = bm;
@@ -977,6 +991,26 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   }
   if (wfmt == ACORN_WFMT_W8B && (swiglu || (cfg && cfg[0] > 0)))
     return ACORN_ERR_UNSUPPORTED;  // M > 16 in the block layout: the tiled kernel only
+  if (blocked && M <= 16 && !(cfg && cfg[0] == 0 && cfg[1] >= 32)) {
+    // decode sizes in the bf16 block layout: the BF16B decode kernel
+    const int rc = bf16b_make_plan(M, N, K, cfg, swiglu, &t->bf16b);
+    if (rc) return rc;
+    t->kind = 6;
+    t->rt = t->bf16b.rt;
+    t->upw = t->bf16b.upw;
+    t->nw = t->bf16b.nw_field;
+    t->ksplit = t->bf16b.ksplit;
+    t->tpw = t->bf16b.depth;
+    t->mt = 1;
+    t->R = (int)M;
+    t->ntiles = (int)(N / 16);
+    t->mblocks = 1;
+    t->groups = t->bf16b.groups;
+    t->lds = 0;
+    return ACORN_OK;
+  }
+  if (blocked && (swiglu || (cfg && cfg[0] > 0)))
+    return ACORN_ERR_UNSUPPORTED;  // bf16 blocks above 16 rows: the tiled or large-M kernel
   // the tiled kernel: the default for M > 16; for M <= 16 on request (rt 0
   // with an M tile of 32 or more in upw)
   if (!swiglu && ((M > 16 && (!cfg || cfg[0] <= 0)) || (cfg && cfg[0] == 0 && cfg[1] >= 32)))
@@ -1183,7 +1217,7 @@ int dispatch_tiled(const Tiling& t, const KArgs& a, hipStream_t st) {
 int plan_entry(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg, bool swiglu) {
   if (!cfg) return ACORN_ERR_VALUE;
   if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
-      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_W8B)
+      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_W8B && wfmt != ACORN_WFMT_BF16B)
     return ACORN_ERR_DTYPE;
   Tiling t;
   const int rc = make_plan(M, N, K, wfmt, cfg, &t, swiglu);
@@ -1200,7 +1234,8 @@ int plan_entry(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg, bool swiglu)
 int gemm_entry(const void* x, const void* w, const void* scale, const void* zero,
                void* out_bf16, float* part, int64_t M, int64_t N, int64_t K, int wfmt,
                const int* cfg, bool swiglu, hipStream_t st) {
-  if (!x || !w || (wfmt != ACORN_WFMT_BF16 && !scale)) return ACORN_ERR_VALUE;
+  if (!x || !w || (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_BF16B && !scale))
+    return ACORN_ERR_VALUE;
   if (!out_bf16 && !part) return ACORN_ERR_VALUE;
   if (M > 65535 * 64 || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return ACORN_ERR_SHAPE;
   Tiling t;
@@ -1225,9 +1260,10 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
   if (t.kind == 3) {
     // bf16 straight into out (one split), else fp32 split planes into part
     const bool direct = out_bf16 && t.ksplit == 1;
-    rc = t.swiglu ? dense_gemm_swiglu_launch(x, w, out_bf16, M, N, K, t.nw, t.upw, t.tpw, st)
+    const bool blk = wfmt == ACORN_WFMT_BF16B;
+    rc = t.swiglu ? dense_gemm_swiglu_launch(x, w, out_bf16, M, N, K, t.nw, t.upw, t.tpw, blk, st)
                   : dense_gemm_launch(x, w, direct ? out_bf16 : nullptr, direct ? nullptr : part,
-                                      M, N, K, t.nw, t.upw, t.tpw, t.ksplit, st);
+                                      M, N, K, t.nw, t.upw, t.tpw, t.ksplit, blk, st);
   } else if (t.kind == 2) {
     rc = w4b_launch(t.w4b, x, w, scale, zero, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K,
                     st);
@@ -1236,6 +1272,8 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
     rc = w4m_launch(t.w4m, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
   } else if (t.kind == 5) {
     rc = w8b_launch(t.w8b, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
+  } else if (t.kind == 6) {
+    rc = bf16b_launch(t.bf16b, x, w, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
   } else if (t.kind == 1) {
     switch (wfmt) {
       case ACORN_WFMT_BF16: rc = dispatch_tiled<ACORN_WFMT_BF16>(t, a, st); break;
@@ -1243,6 +1281,7 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
       case ACORN_WFMT_W4: rc = dispatch_tiled<ACORN_WFMT_W4>(t, a, st); break;
       case ACORN_WFMT_W4B: rc = dispatch_tiled<ACORN_WFMT_W4B>(t, a, st); break;
       case ACORN_WFMT_W8B: rc = dispatch_tiled<ACORN_WFMT_W8B>(t, a, st); break;
+      case ACORN_WFMT_BF16B: rc = dispatch_tiled<ACORN_WFMT_BF16B>(t, a, st); break;
     }
   } else {
     switch (wfmt) {
@@ -1281,7 +1320,8 @@ extern "C" int acorn_quant_gemm(const void* x, const void* w, const void* scale,
                                 const void* zero, void* out_bf16, float* part, int64_t M,
                                 int64_t N, int64_t K, int wfmt, const int* cfg, void* stream) {
   if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
-      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_W8B && wfmt != ACORN_WFMT_F32)
+      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_W8B && wfmt != ACORN_WFMT_BF16B &&
+      wfmt != ACORN_WFMT_F32)
     return ACORN_ERR_DTYPE;
   if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   if (M == 0) return ACORN_OK;
@@ -1305,7 +1345,7 @@ extern "C" int acorn_quant_gemm_swiglu(const void* x, const void* w, const void*
                                        const void* zero, void* act, int64_t M, int64_t N,
                                        int64_t K, int wfmt, const int* cfg, void* stream) {
   if (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_W8 && wfmt != ACORN_WFMT_W4 &&
-      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_W8B)
+      wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_W8B && wfmt != ACORN_WFMT_BF16B)
     return ACORN_ERR_DTYPE;
   if (M < 0 || N <= 0 || K <= 0) return ACORN_ERR_SHAPE;
   if (M == 0) return ACORN_OK;

@@ -185,7 +185,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
 }
 
 template <int RT, int UPW, int DEPTH, int RG, int KW>
-int launch(const W8bPlan& p, const W8dArgs& a, hipStream_t st) {
+int launch(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(RG * KW * kWave);
   if constexpr (RT >= 2) {
     if (p.swiglu) {
@@ -199,7 +199,7 @@ int launch(const W8bPlan& p, const W8dArgs& a, hipStream_t st) {
 }
 
 template <int RT, int UPW, int DEPTH>
-int by_layout(const W8bPlan& p, const W8dArgs& a, hipStream_t st) {
+int by_layout(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
   switch (p.nw_field) {
     case 1: return launch<RT, UPW, DEPTH, 1, 1>(p, a, st);
     case 4: return launch<RT, UPW, DEPTH, 4, 1>(p, a, st);
@@ -214,7 +214,7 @@ constexpr int stage_dwords(int rt, int upw) { return 4 * rt * upw + 8 * upw; }
 constexpr int kRingDwords = 160;   // the ring's budget (depth x stage)
 
 template <int RT, int UPW>
-int by_depth(const W8bPlan& p, const W8dArgs& a, hipStream_t st) {
+int by_depth(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
   switch (p.depth) {
     case 1: return by_layout<RT, UPW, 1>(p, a, st);
     case 2: return by_layout<RT, UPW, 2>(p, a, st);
@@ -226,7 +226,7 @@ int by_depth(const W8bPlan& p, const W8dArgs& a, hipStream_t st) {
 }
 
 template <int RT>
-int by_upw(const W8bPlan& p, const W8dArgs& a, hipStream_t st) {
+int by_upw(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
   switch (p.upw) {
     case 1: return by_depth<RT, 1>(p, a, st);
     case 2: return by_depth<RT, 2>(p, a, st);
@@ -250,7 +250,7 @@ namespace acorn {
 // number of depth rounds. With 0 the plan takes rt 2, upw 2, one wave per
 // workgroup, depth 4 (16 KB of weights in flight per wave), and the fewest
 // splits that launch at least three waves per CU.
-int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W8bPlan* p) {
+int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, DirectPlan* p) {
   if (M < 1 || M > 16) return ACORN_ERR_UNSUPPORTED;
   if (N % 16 || K % 64) return ACORN_ERR_SHAPE;
   if (swiglu && N % 32) return ACORN_ERR_SHAPE;
@@ -302,7 +302,7 @@ int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   return ACORN_OK;
 }
 
-int w8b_launch(const W8bPlan& p, const void* x, const void* w, const void* scale, void* out,
+int w8b_launch(const DirectPlan& p, const void* x, const void* w, const void* scale, void* out,
                float* part, int64_t M, int64_t N, int64_t K, hipStream_t st) {
   if (!x || !w || !scale) return ACORN_ERR_VALUE;
   if (M < 1 || M > 16) return ACORN_ERR_UNSUPPORTED;

@@ -32,18 +32,19 @@ import json
 import torch
 
 from acorninfer_amd.config import Qwen3Config
-from acorninfer_amd.models.qwen3 import (FORMATS, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B,
-                                         LayerWeights, QLinear, Qwen3DecodeModel)
+from acorninfer_amd.models.qwen3 import (FORMATS, WFMT_BF16, WFMT_BF16B, WFMT_W4, WFMT_W4B, WFMT_W8,
+                                         WFMT_W8B, LayerWeights, QLinear, Qwen3DecodeModel)
 from acorninfer_amd.ops.quant_gemm import deinterleave16
 
 FORMAT_NAMES = {v: k for k, v in FORMATS.items()}
-FORMAT_NAMES[WFMT_W4B] = "w4a16"      # the in-memory block layouts of int4 and int8
+FORMAT_NAMES[WFMT_W4B] = "w4a16"      # the in-memory block layouts of int4, int8 and bf16
 FORMAT_NAMES[WFMT_W8B] = "w8a16"
+FORMAT_NAMES[WFMT_BF16B] = "bf16"
 _NORMS = ("input_layernorm", "post_attention_layernorm", "self_attn.q_norm", "self_attn.k_norm")
 
 
 def _linear_tensors(name: str, lin: QLinear, out: dict) -> None:
-    lin = lin.natural()                   # files hold the reference's [N, K/2] packing
+    lin = lin.natural()                   # files hold the reference's layouts
     if lin.fmt == WFMT_BF16:
         out[f"{name}.weight"] = lin.w
     elif lin.fmt in (WFMT_W8, WFMT_W4):
@@ -150,7 +151,7 @@ def load_quantized(path: str, *, device="cuda") -> Qwen3DecodeModel:
         w = torch.cat([p[0] for p in parts], 0).contiguous()
         K = shapes[names[0].rsplit(".", 1)[-1]][1]
         if fmt == WFMT_BF16:
-            return QLinear(fmt, w, w.shape[0], K)
+            return QLinear(fmt, w, w.shape[0], K).blocked()
         s = torch.cat([p[1] for p in parts], 0).contiguous()
         z = None if parts[0][2] is None else torch.cat([p[2] for p in parts], 0).contiguous()
         return QLinear(fmt, w, w.shape[0], K, s, z).blocked()

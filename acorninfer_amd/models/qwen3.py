@@ -37,7 +37,8 @@ from dataclasses import dataclass, field
 import torch
 
 from acorninfer_amd import _lib
-from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B, check,
+from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_BF16B, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B,
+                                 check,
                                  dtype_code, lib, ptr, stream_ptr)
 from acorninfer_amd.config import Qwen3Config
 from acorninfer_amd.ops.paged_attention import prefill_supported
@@ -110,7 +111,9 @@ def dispatch_linear(mod, x: torch.Tensor) -> torch.Tensor:
 class QLinear:
     """One projection y = x @ W^T in a decode weight format.
 
-    bf16: w [N,K] bf16.  w8a16: w int8 [N,K], scale fp16 [N]; with N % 16
+    bf16: w [N,K] bf16; with N % 16 == 0 and K % 64 == 0 held in the bf16
+    decode kernel's 1 KB block layout (fmt WFMT_BF16B, quantize.to_bf16b:
+    the same shape). w8a16: w int8 [N,K], scale fp16 [N]; with N % 16
     == 0 and K % 64 == 0 held in the int8 decode kernel's 1 KB block layout
     (fmt WFMT_W8B, quantize.to_w8b: uint8 q + 128 of the same shape).
     w4a16: w uint8 [N,K/2] (low nibble = even k), scale fp16 [N,K/128], zero
@@ -130,7 +133,7 @@ class QLinear:
     def from_dense(cls, w: torch.Tensor, fmt: int) -> "QLinear":
         N, K = w.shape
         if fmt == WFMT_BF16:
-            return cls(fmt, w.to(torch.bfloat16).contiguous(), N, K)
+            return cls(fmt, w.to(torch.bfloat16).contiguous(), N, K).blocked()
         if fmt == WFMT_W8:
             q, s = Q.quantize_w8(w)
             return cls(fmt, q.contiguous(), N, K, s.contiguous()).blocked()
@@ -140,9 +143,11 @@ class QLinear:
         raise ValueError(f"unknown weight format {fmt}")
 
     def blocked(self) -> "QLinear":
-        """int8 in the W8B block layout (N % 16 == 0, K % 64 == 0) and
-        symmetric int4 in the W4B block layout (N % 16 == 0, K % 512 == 0)
-        where the shape allows it; any other weight unchanged."""
+        """bf16 in the BF16B block layout and int8 in the W8B one (N % 16 ==
+        0, K % 64 == 0), symmetric int4 in the W4B block layout (N % 16 == 0,
+        K % 512 == 0) where the shape allows it; any other weight unchanged."""
+        if self.fmt == WFMT_BF16 and not (self.N % 16 or self.K % 64):
+            return QLinear(WFMT_BF16B, Q.to_bf16b(self.w), self.N, self.K, il16=self.il16)
         if self.fmt == WFMT_W8 and not (self.N % 16 or self.K % 64):
             return QLinear(WFMT_W8B, Q.to_w8b(self.w), self.N, self.K, self.scale, None,
                            il16=self.il16)
@@ -152,8 +157,10 @@ class QLinear:
         return QLinear(WFMT_W4B, wb, self.N, self.K, sb, None, il16=self.il16)
 
     def natural(self) -> "QLinear":
-        """The same weight in the reference's layouts (int8 [N, K], int4
-        [N, K/2])."""
+        """The same weight in the reference's layouts (bf16 and int8 [N, K],
+        int4 [N, K/2])."""
+        if self.fmt == WFMT_BF16B:
+            return QLinear(WFMT_BF16, Q.from_bf16b(self.w), self.N, self.K, il16=self.il16)
         if self.fmt == WFMT_W8B:
             return QLinear(WFMT_W8, Q.from_w8b(self.w), self.N, self.K, self.scale, None,
                            il16=self.il16)
@@ -174,6 +181,8 @@ class QLinear:
         """fp32 dequantised weight [N, K] in [gate; up] row order (test helper)."""
         if self.fmt in (WFMT_BF16, _lib.WFMT_F32):
             d = self.w.float()
+        elif self.fmt == WFMT_BF16B:
+            d = self.natural().w.float()
         elif self.fmt in (WFMT_W8, WFMT_W8B):
             nat = self.natural()
             d = Q.dequant_w8(nat.w, nat.scale)
@@ -260,7 +269,7 @@ class QLinear:
         if tiling[0] == DEQUANT_RT:
             self._dequant(wtmp, M, stream)
             w, fmt, arr = wtmp, WFMT_BF16, (ctypes.c_int * 6)(DENSE_RT, *tiling[1:], 0)
-        scale = self.scale if fmt != WFMT_BF16 else None
+        scale = self.scale if fmt not in (WFMT_BF16, WFMT_BF16B) else None
         rc = lib().acorn_quant_gemm_swiglu(ptr(x), ptr(w), ptr(scale), ptr(self.zero), ptr(act),
                                            M, self.N, self.K, fmt, arr, stream)
         check(rc, "quant_gemm_swiglu")
@@ -584,7 +593,7 @@ class Qwen3DecodeModel:
         interleave."""
         gu = self.layers[0].gate_up
         return gu.il16 and rows >= PREFILL_SWIGLU_M and (
-            gu.fmt == WFMT_BF16 or (gu.fmt == WFMT_W4B and rows >= DEQUANT_M_MIN))
+            gu.fmt in (WFMT_BF16, WFMT_BF16B) or (gu.fmt == WFMT_W4B and rows >= DEQUANT_M_MIN))
 
     def fused_swiglu(self, batch: int) -> bool:
         """The gate|up launch carries the SwiGLU epilogue (decode sizes, and

@@ -21,7 +21,8 @@ from typing import NamedTuple
 
 import torch
 
-from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B, check, lib,
+from acorninfer_amd._lib import (BF16, WFMT_BF16, WFMT_BF16B, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B,
+                                 check, lib,
                                  ptr, require_gpu, stream_ptr)
 
 CLASSES = {
@@ -85,6 +86,10 @@ class Tiling(NamedTuple):
     int8 decode kernel (WFMT_W8B, M <= 16): rt row tiles per wave, upw 64-k
     blocks per stage, nw the wave layout (1, 4, 22, 44 as for int4), ksplit,
     tpw = stages in flight; above 16 rows W8B runs on the tiled kernel.
+    bf16 decode kernel (WFMT_BF16B, M <= 16): rt row tiles per wave, upw
+    32-k blocks per stage, nw the wave layout (1, 4, 22, 44), ksplit, tpw =
+    stages in flight; above 16 rows BF16B runs on the tiled kernel and from
+    256 rows on the large-M kernel (its direct-to-LDS and 64 / 128 forms).
     int4 mid-M kernel (WFMT_W4B, M > 16, rt == -3): upw row tiles per wave
     (1 / 2), nw waves (4 / 8), ksplit, tpw 128-k groups in flight (2 / 4);
     64 x rows per workgroup, streamed through LDS a group at a time.
@@ -303,8 +308,9 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
     planner = swiglu_plan if swiglu else plan
     base, _ = planner(M, N, K, wfmt)
     reqs = [Tiling()]
-    if wfmt in (WFMT_W4B, WFMT_W8B) and M <= DECODE_M_MAX:
-        reqs += _w4b_requests(swiglu) if wfmt == WFMT_W4B else _w8b_requests(swiglu)
+    if wfmt in (WFMT_W4B, WFMT_W8B, WFMT_BF16B) and M <= DECODE_M_MAX:
+        reqs += {WFMT_W4B: _w4b_requests, WFMT_W8B: _w8b_requests,
+                 WFMT_BF16B: _bf16b_requests}[wfmt](swiglu)
         if not swiglu:
             for bn in (64, 128):
                 for ks in (1, 2, 4, 8, 16):
@@ -372,6 +378,20 @@ def _w8b_requests(swiglu: bool) -> list[Tiling]:
         for upw, depth in ((1, 4), (2, 2), (2, 4)):
             for nw in (1, 4, 22, 44):
                 for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
+                    reqs.append(Tiling(rt, upw, nw, ks, depth))
+    return reqs
+
+
+def _bf16b_requests(swiglu: bool) -> list[Tiling]:
+    """Requests covering the bf16 direct kernel's knobs (M <= 16): 1, 2 or 4
+    row tiles per wave, 1 / 2 / 4 blocks of 32 k per stage with 2 to 8 stages
+    in flight, the wave layouts 1, 4, 22, 44, and split counts from one to
+    eight (the fused SwiGLU runs in one split)."""
+    reqs = []
+    for rt in ((2, 4) if swiglu else (1, 2, 4)):
+        for upw, depth in ((1, 8), (2, 4), (2, 8), (4, 2), (4, 4)):
+            for nw in (1, 4, 22, 44):
+                for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8)):
                     reqs.append(Tiling(rt, upw, nw, ks, depth))
     return reqs
 

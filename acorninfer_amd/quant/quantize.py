@@ -184,6 +184,31 @@ def from_w8b(wb: torch.Tensor) -> torch.Tensor:
     return (u.to(torch.int16) - 128).to(torch.int8).contiguous()
 
 
+def to_bf16b(w: torch.Tensor) -> torch.Tensor:
+    """bf16 [N, K] -> the bf16 decode kernel's 1 KB block layout
+    (ACORN_WFMT_BF16B) in a bf16 tensor of the same shape: the 8 values of row
+    n, k in [8c, 8c+8) moved to block (n // 16, c // 4), lane (c % 4) * 16 +
+    n % 16, so a block is the MFMA A operand of 16 rows x 32 k. Rows
+    16t..16t+15 hold row tile t, so 16-row block permutations (interleave16)
+    commute with the conversion. N % 16 == 0 and K % 64 == 0."""
+    n, k = w.shape
+    if w.dtype != torch.bfloat16 or n % 16 or k % 64:
+        raise ValueError(f"to_bf16b needs bf16 [N, K] with N % 16 == 0 and K % 64 == 0: "
+                         f"{w.dtype} {tuple(w.shape)}")
+    return (w.reshape(n // 16, 16, k // 32, 4, 8)          # tile, row, block, chunk, value
+            .permute(0, 2, 3, 1, 4).reshape(n, k).contiguous())
+
+
+def from_bf16b(wb: torch.Tensor) -> torch.Tensor:
+    """Inverse of to_bf16b."""
+    n, k = wb.shape
+    if wb.dtype != torch.bfloat16 or n % 16 or k % 64:
+        raise ValueError(f"from_bf16b needs bf16 [N, K] with N % 16 == 0 and K % 64 == 0: "
+                         f"{wb.dtype} {tuple(wb.shape)}")
+    return (wb.reshape(n // 16, k // 32, 4, 16, 8)          # tile, block, chunk, row, value
+            .permute(0, 3, 1, 2, 4).reshape(n, k).contiguous())
+
+
 def dequant_w8(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """fp32 [N,K] = q * scale[:, None]."""
     return q.float() * scale.float()[:, None]

@@ -545,14 +545,16 @@ def norm_benchmarks(seed: int) -> dict:
 
 def dense_gemm_benchmarks(seed: int) -> dict:
     """bf16 projections at prefill M (configuration 3's shapes): this
-    library's large-M kernel (its planner's tiling) against torch.mm
-    (hipBLASLt), fp32 output as the prefill step consumes it; TFLOP/s and the
-    fraction of the 2.5 PFLOP/s dense bf16 peak."""
+    library's large-M kernel (its planner's tiling) on the model's weight
+    layout (BF16B blocks) against torch.mm (hipBLASLt) on natural rows, fp32
+    output as the prefill step consumes it; TFLOP/s and the fraction of the
+    2.5 PFLOP/s dense bf16 peak."""
     import torch
 
     from acorninfer_amd import _lib
     from acorninfer_amd._lib import lib, ptr
     from acorninfer_amd.ops.quant_gemm import plan
+    from acorninfer_amd.quant.quantize import to_bf16b
 
     out = {}
     g = torch.Generator(device="cuda").manual_seed(seed + 21)
@@ -562,14 +564,15 @@ def dense_gemm_benchmarks(seed: int) -> dict:
         for name, (n, k) in shapes.items():
             x = torch.randn(M, k, device="cuda", generator=g).bfloat16()
             w = (0.02 * torch.randn(n, k, device="cuda", generator=g)).bfloat16()
-            t, _ = plan(M, n, k, _lib.WFMT_BF16)
+            wb = to_bf16b(w)
+            t, _ = plan(M, n, k, _lib.WFMT_BF16B)
             part = torch.empty(t.ksplit, M, n, device="cuda")
             arr = (ctypes.c_int * 6)(*t, 0)
 
             def own(st):
                 for _ in range(4):
-                    _lib.check(lib().acorn_quant_gemm(ptr(x), ptr(w), None, None, None,
-                                                      ptr(part), M, n, k, _lib.WFMT_BF16, arr,
+                    _lib.check(lib().acorn_quant_gemm(ptr(x), ptr(wb), None, None, None,
+                                                      ptr(part), M, n, k, _lib.WFMT_BF16B, arr,
                                                       st.cuda_stream), "dense GEMM")
 
             def library(st):
@@ -582,7 +585,7 @@ def dense_gemm_benchmarks(seed: int) -> dict:
                 "us": round(us, 1),
                 "frac_mfma": round(fl / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
                 "hipblaslt_us": round(us_lib, 1)}
-            del x, w, part
+            del x, w, wb, part
     torch.cuda.empty_cache()
     return out
 

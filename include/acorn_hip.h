@@ -51,6 +51,11 @@ extern "C" {
                              byte ((n/16)*(K/64) + c/4)*1024 + ((c%4)*16 + n%16)*16;
                              fp16 per-channel scale [N] as in W8. A block is
                              one wave's MFMA A operands for 16 rows x 64 k. */
+#define ACORN_WFMT_BF16B 6 /* ACORN_WFMT_BF16's values in 1 KB blocks (N % 16 == 0,
+                             K % 64 == 0): the 8 bf16 of row n, k in [8c, 8c+8)
+                             sit at element ((n/16)*(K/32) + c/4)*512 +
+                             ((c%4)*16 + n%16)*8. A block is one wave's MFMA A
+                             operand for 16 rows x 32 k. */
 
 /* error codes */
 #define ACORN_OK 0
@@ -244,6 +249,8 @@ int acorn_paged_attention_qkv_supported(int64_t H, int64_t KV, int64_t D, int64_
  *                         model's int4 weights)
  *   wfmt ACORN_WFMT_W8B : as W8, in the blocked layout above (the decode
  *                         model's int8 weights)
+ *   wfmt ACORN_WFMT_BF16B: as BF16, in the blocked layout above (the decode
+ *                         model's bf16 weights)
  *   wfmt ACORN_WFMT_F32 : w fp32 [N,K], x fp32 [M,K]; fp32 result in part
  * cfg: NULL or int[6] {rt, upw, nw, ksplit, tpw, -}; 0 entries are chosen by
  * the planner (acorn_gemm_plan). With the chosen ksplit:

@@ -159,3 +159,49 @@ def test_dense_gemm_split_planes_are_k_range_products(ks):
     for s in range(ks):
         ref = x[:, s * kr:(s + 1) * kr].double() @ w[:, s * kr:(s + 1) * kr].double().T
         torch.testing.assert_close(planes[s].double(), ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,K", [(513, 272, 256), (1000, 1040, 512), (777, 1536, 384),
+                                   (300, 4096, 1024)])
+@pytest.mark.parametrize("tiling", [(DENSE_RT, 256, 128, 1, 4), (DENSE_RT, 256, 128, 2, 4),
+                                    (DENSE_RT, 128, 64, 1, 2), (DENSE_RT, 128, 64, 2, 4),
+                                    (DENSE_RT, 64, 64, 1, 4), (DENSE_RT, 64, 128, 1, 2)])
+def test_dense_gemm_blocked_weights_bitwise(M, N, K, tiling):
+    """The decode model's bf16 weights in 1 KB blocks (BF16B) on every form of
+    the large-M kernel that reads them (direct-to-LDS 256 x 256; the
+    register-direct 64 / 128 forms): the same operands in the same order as
+    the natural rows, so the fp32 planes are bit for bit those of the natural
+    layout. Ragged N (272, 1040: a last 256-row tile cut inside) and M, K
+    splits, 6 and 12 k-pairs."""
+    from acorninfer_amd._lib import WFMT_BF16, WFMT_BF16B
+    from acorninfer_amd.ops.quant_gemm import Tiling, gemm_partials, plan
+    from acorninfer_amd.quant.quantize import to_bf16b
+    x, w = _operands(M, N, K, 29)
+    xd, wd = x.cuda(), w.cuda()
+    wb = to_bf16b(wd)
+    t = Tiling(*tiling)
+    try:
+        tb, _ = plan(M, N, K, WFMT_BF16B, t)
+    except NotImplementedError:
+        pytest.skip(f"{tiling} not built for K={K}")
+    assert tb == plan(M, N, K, WFMT_BF16, t)[0]
+    outs = []
+    for wf, ww in ((WFMT_BF16B, wb), (WFMT_BF16, wd)):
+        part = torch.full((tb.ksplit, M, N), float("nan"), device="cuda")
+        gemm_partials(xd, ww, None, None, wf, part, tb)
+        outs.append(part)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]), tiling
+    ref = xd.float() @ wd.float().T
+    rel = ((outs[0].sum(0) - ref).norm() / ref.norm()).item()
+    assert rel < 1e-5
+
+
+def test_planner_refuses_blocked_weights_on_the_staged_form():
+    """BF16B is read by the direct-to-LDS and register-direct forms only."""
+    from acorninfer_amd._lib import WFMT_BF16B
+    from acorninfer_amd.ops.quant_gemm import Tiling, plan
+    with pytest.raises(NotImplementedError):
+        plan(4096, 4096, 4096, WFMT_BF16B, Tiling(DENSE_RT, 256, 64, 1, 2))
+    assert plan(4096, 4096, 4096, WFMT_BF16B)[0] == Tiling(DENSE_RT, 256, 128, 1, 4)

@@ -8,9 +8,10 @@ sampler. As the reference's own Engine tests (tests/test_engine.py:152-230):
 - graph vs eager: the same submits through an Engine that replays captured
   decode steps and one that launches them uncaptured give bitwise the same
   token streams, greedy and sampled rows mixed in one batch;
-- EOS retirement shrinks the batch across buckets (8 -> 4 -> 2): the trap
-  ids come from a first run without traps, the graph and eager runs with
-  them agree bitwise and stop exactly where the traps say;
+- EOS retirement shrinks the batch across buckets (8 -> 4 -> 2): each trap
+  id comes from an earlier run with the same batch history up to it, the
+  graph and eager runs with them agree bitwise and stop exactly where the
+  traps say;
 - C=8 requests of 512-token prompts, greedy: the token streams against the
   oracle (oracle/qwen3_ref.py with bf16 activations; for W4A16 the
   dequantised weights kept exact in fp32) fed the same streams: wherever the
@@ -116,27 +117,38 @@ def test_engine_graph_equals_eager_mixed_sampling(models, fmt):
 @pytest.mark.gpu
 @pytest.mark.parametrize("fmt", ["bf16", "w4a16"])
 def test_engine_eos_shrinks_batch_across_buckets(models, fmt):
+    """The trap ids are each taken from a run with the same batch history as
+    the run they stop (the reference's two-phase traps,
+    tests/test_engine.py:185-226): a row's tokens are the same bits only
+    while the batch, and so the bucket's tilings and split-K summation
+    order, is the same."""
     model = models[fmt]
     prompts = [_ids(n, SEED + 40 + i) for i, n in enumerate([20, 41, 9, 63, 30, 52, 11, 77])]
-    full = _run(_engine(model, False), [(p, GREEDY, 10, NO_EOS) for p in prompts])
-    # requests 0-3 stop on their first decode token (batch 8 -> 4), 4-5 on
-    # their third (4 -> 2), 6-7 run to max_tokens
+
+    def reqs(traps):
+        return [(p, GREEDY, 10, frozenset({traps[i]}) if i in traps else NO_EOS)
+                for i, p in enumerate(prompts)]
+
+    # requests 0-3 stop on their first decode token (batch 8 -> 4), taken
+    # from the untrapped run (the first decode step runs all 8 rows in both)
+    full = _run(_engine(model, False), reqs({}))
     traps = {i: full[i][1] for i in range(4)}
-    traps.update({i: full[i][3] for i in (4, 5)})
-    want_len = [full[i].index(traps[i]) + 1 if i in traps else 10 for i in range(8)]
-    reqs = [(p, GREEDY, 10, frozenset({traps[i]}) if i in traps else NO_EOS)
-            for i, p in enumerate(prompts)]
+    # 4-5 on their third (4 -> 2), taken from a run with 0-3 trapped
+    mid = _run(_engine(model, False), reqs(traps))
+    assert [s[:2] for s in mid[:4]] == [s[:2] for s in full[:4]]
+    traps.update({i: mid[i][3] for i in (4, 5)})
+    want_len = [mid[i].index(traps[i]) + 1 if i in traps else 10 for i in range(8)]
     runs = {}
     for capture in (False, True):
         eng = _engine(model, capture)
-        runs[capture] = _run(eng, reqs)
+        runs[capture] = _run(eng, reqs(traps))
         if capture:
             used = sorted(eng.graph_runner.states)
             assert {8, 4, 2} <= set(used), used
             assert all(eng.graph_runner.states[b].graph is not None for b in (8, 4, 2))
     assert runs[True] == runs[False]
     assert [len(s) for s in runs[True]] == want_len
-    assert [s[:n] for s, n in zip(full, want_len)] == runs[True]
+    assert [s[:n] for s, n in zip(mid[:6], want_len[:6])] == runs[True][:6]
     print(f"\n[{fmt} engine EOS: lengths {want_len}, buckets 8 -> 4 -> 2]", flush=True)
 
 

@@ -203,7 +203,7 @@ def test_bucket_boundaries_and_classes():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["bf16", "w8", "w8b", "w4", "w4b"])
+@pytest.mark.parametrize("fmt", ["bf16", "bf16b", "w8", "w8b", "w4", "w4b"])
 @pytest.mark.parametrize("m", [1, 8, 16, 40, 256])
 def test_every_candidate_tiling_matches(fmt, m):
     """Every tiling the load-time sweep may pick (streaming kernel: row tiles
@@ -212,14 +212,17 @@ def test_every_candidate_tiling_matches(fmt, m):
     partial last M tile at M = 40) gives the oracle's result on the o shape
     (K=4096) and the down shape (K=12288); tilings differ only in fp32
     summation order."""
-    from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B
+    from acorninfer_amd._lib import WFMT_BF16, WFMT_BF16B, WFMT_W4, WFMT_W4B, WFMT_W8, WFMT_W8B
     from acorninfer_amd.ops.quant_gemm import _launch, candidates
-    from acorninfer_amd.quant.quantize import to_w4b, to_w8b
+    from acorninfer_amd.quant.quantize import to_bf16b, to_w4b, to_w8b
     for cls in ("o", "down"):
         n, k = SHAPES[cls]
         if fmt == "bf16":
             w, wref = _bf(cls)
             args, wf = (w, None, None), WFMT_BF16
+        elif fmt == "bf16b":
+            w, wref = _bf(cls)
+            args, wf = (to_bf16b(w), None, None), WFMT_BF16B
         elif fmt == "w8":
             q, s, wref = _w8(cls)
             args, wf = (q, s, None), WFMT_W8
@@ -270,6 +273,56 @@ def test_w8b_config3_matches_dequant_matmul(cls, m):
     print(f"\n[w8b {cls} M={m}: rel err {r:.3g}, vs natural layout {rn:.3g}]")
     assert r <= GEMM_REL and rn <= 1e-2
     torch.testing.assert_close(out.float(), ref, **TOL_W8[cls])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cls", list(SHAPES))
+@pytest.mark.parametrize("m", MS + [16])
+def test_bf16b_config3_matches_matmul(cls, m):
+    """The decode model's bf16 layout (BF16B blocks) at every configuration-3
+    shape and M with the planner's tiling (the bf16 decode kernel for
+    M <= 16, the tiled kernel above, the large-M kernel from 256 rows)
+    against the fp32 matmul, and equal to the natural-layout bf16 GEMM up to
+    fp32 summation order (bit for bit where both run the same kernel: the
+    tiled and large-M kernels)."""
+    from acorninfer_amd._lib import WFMT_BF16, WFMT_BF16B
+    from acorninfer_amd.ops.quant_gemm import _launch, plan
+    from acorninfer_amd.quant.quantize import from_bf16b, to_bf16b
+    w, wref = _bf(cls)
+    wb = to_bf16b(w)
+    assert torch.equal(from_bf16b(wb), w)
+    n, k = SHAPES[cls]
+    x = _x(m, k, 12)
+    out = _launch(x, wb, None, None, WFMT_BF16B, n, None, None)
+    r = rel_err(out, _ref(x, wref))
+    tb = plan(m, n, k, WFMT_BF16B)[0]
+    nat = _launch(x, w, None, None, WFMT_BF16, n, tb if m > 16 else None, None)
+    rn = rel_err(out, nat)
+    print(f"\n[bf16b {cls} M={m} {tuple(tb)}: rel err {r:.3g}, vs natural layout {rn:.3g}]")
+    assert r <= GEMM_REL and rn <= 1e-2
+    if m > 16:
+        assert torch.equal(out, nat)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [40, 200])
+def test_bf16b_tiled_equals_natural_bitwise(m):
+    """The tiled kernel does the same arithmetic on both bf16 layouts, only
+    its addressing differs: BF16B and natural bf16 give the same bits at
+    every tiled candidate."""
+    from acorninfer_amd._lib import WFMT_BF16, WFMT_BF16B
+    from acorninfer_amd.ops.quant_gemm import _launch, candidates
+    from acorninfer_amd.quant.quantize import to_bf16b
+    w, _ = _bf("qkv")
+    wb = to_bf16b(w)
+    n, k = SHAPES["qkv"]
+    x = _x(m, k, 13)
+    cands = [c for c in candidates(m, n, k, WFMT_BF16B) if c.rt == 0]
+    assert len(cands) >= 4
+    for c in cands:
+        a = _launch(x, wb, None, None, WFMT_BF16B, n, c, None)
+        b = _launch(x, w, None, None, WFMT_BF16, n, c, None)
+        assert torch.equal(a, b), tuple(c)
 
 
 @pytest.mark.gpu
@@ -483,14 +536,15 @@ def _swiglu_ref(x, wg, wu):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["bf16", "w8", "w8b", "w4"])
+@pytest.mark.parametrize("fmt", ["bf16", "bf16n", "w8", "w8b", "w4"])
 @pytest.mark.parametrize("m", [1, 8, 16])
 def test_fused_swiglu_every_tiling(fmt, m):
     """gate|up with the SwiGLU epilogue (interleaved 16-row gate/up blocks) vs
     the oracle's separate projections + activation; every candidate tiling;
     and the unfused path (partials + silu_mul on the interleaved layout).
-    w8 is int8 in the natural layout (the streaming kernel), w8b and w4 the
-    decode model's block layouts (the int8 / int4 direct kernels)."""
+    bf16n and w8 are bf16 and int8 in the natural layouts (the streaming
+    kernel), bf16, w8b and w4 the decode model's block layouts (the bf16 /
+    int8 / int4 direct kernels)."""
     import ctypes
     from acorninfer_amd import _lib
     from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, WFMT_W8, lib, ptr, stream_ptr
@@ -499,9 +553,9 @@ def test_fused_swiglu_every_tiling(fmt, m):
     inter, k = 1024, 4096
     g = torch.Generator().manual_seed(31)
     w = (0.02 * torch.randn(2 * inter, k, generator=g)).bfloat16().cuda()
-    wf = {"bf16": WFMT_BF16, "w8": WFMT_W8, "w8b": WFMT_W8, "w4": WFMT_W4}[fmt]
+    wf = {"bf16": WFMT_BF16, "bf16n": WFMT_BF16, "w8": WFMT_W8, "w8b": WFMT_W8, "w4": WFMT_W4}[fmt]
     lin = QLinear.from_dense(w, wf).interleaved()
-    if fmt == "w8":
+    if fmt in ("w8", "bf16n"):
         lin = lin.natural()
     deq = lin.dense()
     x = (torch.randn(m, k, generator=g)).bfloat16().cuda()
@@ -526,14 +580,15 @@ def test_fused_swiglu_every_tiling(fmt, m):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["bf16", "w4"])
+@pytest.mark.parametrize("fmt", ["bf16", "bf16n", "w4"])
 @pytest.mark.parametrize("m", [1100, 2048])
 def test_fused_swiglu_at_prefill_sizes(fmt, m):
     """gate|up + SwiGLU at prefill sizes (the large-M kernel's epilogue; int4
     dequantised onto it): bit for bit the one-split fp32 output of the same
     kernel through silu_mul, and within 1e-2 of the oracle's separate
-    projections + activation. inter = 1088: the last 256-row weight tile is
-    half full; 1100 rows leave a ragged last M tile."""
+    projections + activation; bf16 (blocks) bit for bit bf16n (natural rows).
+    inter = 1088: the last 256-row weight tile is half full; 1100 rows leave a
+    ragged last M tile."""
     from acorninfer_amd import _lib
     from acorninfer_amd._lib import WFMT_BF16, WFMT_W4, lib, ptr, stream_ptr
     from acorninfer_amd.models.qwen3 import DENSE_RT, DEQUANT_RT, QLinear
@@ -541,13 +596,16 @@ def test_fused_swiglu_at_prefill_sizes(fmt, m):
     inter, k = 1088, 1024
     g = torch.Generator().manual_seed(37)
     w = (0.02 * torch.randn(2 * inter, k, generator=g)).bfloat16().cuda()
-    lin = QLinear.from_dense(w, {"bf16": WFMT_BF16, "w4": WFMT_W4}[fmt]).interleaved()
+    lin = QLinear.from_dense(w, {"bf16": WFMT_BF16, "bf16n": WFMT_BF16,
+                                 "w4": WFMT_W4}[fmt]).interleaved()
+    if fmt == "bf16n":
+        lin = lin.natural()
     deq = lin.dense()
     x = torch.randn(m, k, generator=g).bfloat16().cuda()
     ref = _swiglu_ref(x, deq[:inter], deq[inter:])
     st = stream_ptr()
     t, _ = lin.swiglu_plan(m, workspace=True)
-    assert t.rt == (DENSE_RT if fmt == "bf16" else DEQUANT_RT) and t.ksplit == 1, t
+    assert t.rt == (DEQUANT_RT if fmt == "w4" else DENSE_RT) and t.ksplit == 1, t
     wtmp = torch.empty(2 * inter * k, dtype=torch.bfloat16, device="cuda")
     act = torch.full((m, inter), float("nan"), dtype=torch.bfloat16, device="cuda")
     lin.launch_swiglu(x, m, t, act, st, wtmp=wtmp)
@@ -560,6 +618,12 @@ def test_fused_swiglu_at_prefill_sizes(fmt, m):
                "silu_mul")
     torch.cuda.synchronize()
     assert torch.equal(act, act2)
+    if fmt == "bf16":
+        nat = lin.natural()
+        act3 = torch.full_like(act, float("nan"))
+        nat.launch_swiglu(x, m, nat.swiglu_plan(m, workspace=True)[0], act3, st)
+        torch.cuda.synchronize()
+        assert torch.equal(act, act3)
     r = rel_err(act, ref)
     print(f"\n[swiglu {fmt} M={m} at prefill size: rel err {r:.3g}]")
     assert r <= 1e-2
