@@ -548,7 +548,8 @@ struct EpiArgs {
 };
 constexpr int kQB = 4;    // EPI: split partials requested per element up front
 
-// EPI LDS after the slabs: q of the REP heads [REP][D], then the new k and v rows.
+// EPI LDS after the slabs, per wave: q of the REP heads [REP][D], then the
+// new k and v rows.
 __host__ __device__ constexpr size_t k3_epi_bytes(int rep, int d) {
   return (size_t)(rep + 2) * d * 2;
 }
@@ -559,7 +560,7 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
     const int32_t* __restrict__ tables, const int32_t* __restrict__ lens, T* __restrict__ out,
     float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l, int H,
     int KV, int P, int num_blocks, int table_stride, int S, float scale_log2, EpiArgs e) {
-  static_assert(!EPI || (NWV == 1 && PAGE16), "EPI is the one-wave, 16-token-page form");
+  static_assert(!EPI || PAGE16, "EPI is built for 16-token pages");
   constexpr int KB = D / 32;                   // q.k MFMA k-blocks
   constexpr int DPL = D / 16;                  // P V: dims per lane per token = MFMAs per chunk
   constexpr int VW = DPL / 2;                  // ... in 32-bit words
@@ -674,11 +675,17 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   // instruction, each line split over two instructions.
   constexpr int KPITCH = 2 * D + 16;           // bytes per slab row
   uint8_t* kslab = (uint8_t*)smem + k3_slab_offset(NWV, REP, D, pps) + (size_t)wid * CH * KPITCH;
-  // EPI: q of the REP heads, then the new token's k and v rows (activation dtype)
-  T* qs = (T*)((uint8_t*)smem + k3_slab_offset(NWV, REP, D, pps) + k3_slab_bytes(NWV, D));
+  // EPI: q of the REP heads, then the new token's k and v rows (activation
+  // dtype), one such region per wave
+  T* qs = (T*)((uint8_t*)smem + k3_slab_offset(NWV, REP, D, pps) + k3_slab_bytes(NWV, D) +
+               (size_t)wid * k3_epi_bytes(REP, D));
   T* kn = qs + REP * D;
   T* vn = kn + D;
-  const bool owner = EPI && sp == nsb - 1;
+  // the wave that holds the new token (the last page; page 0 of a sequence
+  // without tokens) writes its k and v: in the sequence's last split, the
+  // wave whose pages contain it
+  const int own_wid = NWV == 1 ? 0 : min(max(max(npages, 1) - 1 - wp0, 0) / ppv, NWV - 1);
+  const bool owner = EPI && sp == nsb - 1 && wid == own_wid;
   float m = -INFINITY, l = 0.f;
   f32x4_t acc[DPL];
 #pragma unroll
@@ -707,8 +714,12 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
     if constexpr (PAGE16) {
       // the whole chunk lies in one page: a uniform base, per-lane offsets
       const int pi = (t0 >> pshift) - vp0;
-      const int pg = reg_pages ? __builtin_amdgcn_readlane(pgr, pi)
-                               : __builtin_amdgcn_readfirstlane(tbl[pi + vp0 - wp0]);
+      // (a wave without pages, possible with NWV > 1, still issues the EPI
+      // form's first load: from the table slot after the split's last,
+      // clamped into the pool like every block id)
+      const int pgt = reg_pages ? __builtin_amdgcn_readlane(pgr, pi)
+                                : __builtin_amdgcn_readfirstlane(tbl[pi + vp0 - wp0]);
+      const int pg = (unsigned)pgt < (unsigned)num_blocks ? pgt : 0;
       const size_t base = ((size_t)pg * P + (t0 & (P - 1))) * tok_stride + (size_t)kvh * D;
       const T* kb = k_pages + base + (spare ? 0 : v_off);
       const T* vb = v_pages + base + (spare ? 0 : v_off);
@@ -1141,21 +1152,23 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
     const int64_t pps = (table_stride + S - 1) / S;
     const bool page16 = P % 16 == 0;
     const bool one = pps <= kOneWavePages;
-    if (epi && !(one && page16)) return ACORN_ERR_UNSUPPORTED;
+    if (epi && !page16) return ACORN_ERR_UNSUPPORTED;
     const int nwv = one ? 1 : kAttnWaves;
     const size_t lds = k3_slab_offset(nwv, REP, D, (int)pps) +
-                       (page16 ? k3_slab_bytes(nwv, D) : 0) + (epi ? k3_epi_bytes(REP, D) : 0);
+                       (page16 ? k3_slab_bytes(nwv, D) : 0) +
+                       (epi ? (size_t)nwv * k3_epi_bytes(REP, D) : 0);
     if (lds > 160 * 1024) return ACORN_ERR_UNSUPPORTED;
-    const int which = epi ? 4 : (one ? 2 : 0) + (page16 ? 1 : 0);
+    const int which = epi ? (one ? 4 : 5) : (one ? 2 : 0) + (page16 ? 1 : 0);
     using KFn = void (*)(const T*, const T*, const T*, const int32_t*, const int32_t*, T*, float*,
                          float*, float*, int, int, int, int, int, int, float, EpiArgs);
-    const KFn fns[5] = {paged_attn_mfma_kernel<T, D, REP, kAttnWaves, false>,
+    const KFn fns[6] = {paged_attn_mfma_kernel<T, D, REP, kAttnWaves, false>,
                         paged_attn_mfma_kernel<T, D, REP, kAttnWaves, true>,
                         paged_attn_mfma_kernel<T, D, REP, 1, false, kOneWaveDepth>,
                         paged_attn_mfma_kernel<T, D, REP, 1, true, kOneWaveDepth>,
-                        paged_attn_mfma_kernel<T, D, REP, 1, true, kOneWaveDepth, true>};
+                        paged_attn_mfma_kernel<T, D, REP, 1, true, kOneWaveDepth, true>,
+                        paged_attn_mfma_kernel<T, D, REP, kAttnWaves, true, 3, true>};
     const KFn kfn = fns[which];
-    static bool lds_raised[5] = {false, false, false, false, false};
+    static bool lds_raised[6] = {false, false, false, false, false, false};
     if (!lds_raised[which] && lds > 64 * 1024) {
       (void)hipFuncSetAttribute((const void*)kfn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 160 * 1024);
@@ -1672,8 +1685,14 @@ extern "C" int acorn_paged_attention_qkv_supported(int64_t H, int64_t KV, int64_
   if (!(dtype == ACORN_BF16 || dtype == ACORN_F16) || wdtype != dtype) return 0;
   if (!(D == 64 || D == 128) || P % 16 != 0 || (P & (P - 1)) != 0) return 0;
   if (!(rep == 1 || rep == 2 || rep == 4 || rep == 8)) return 0;
+  // one-wave splits, or workgroups of kAttnWaves waves whose LDS (block ids,
+  // wave partials, K slabs and the epilogue's rows) fits
   const int64_t pps = (table_stride + num_splits - 1) / num_splits;
-  return pps <= kOneWavePages ? 1 : 0;
+  if (pps <= kOneWavePages) return 1;
+  if (pps > (int64_t)1 << 20) return 0;
+  const size_t lds = k3_slab_offset(kAttnWaves, (int)rep, (int)D, (int)pps) +
+                     k3_slab_bytes(kAttnWaves, (int)D) + (size_t)kAttnWaves * k3_epi_bytes((int)rep, (int)D);
+  return lds <= 160 * 1024 ? 1 : 0;
 }
 
 extern "C" int acorn_paged_attention_qkv(const float* part, int64_t nsplit, void* k_pages,

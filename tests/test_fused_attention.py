@@ -23,7 +23,9 @@ def test_supported_predicate():
     assert f(32, 8, 128, 16, 48, 12, F32, F32) == 0     # fp32 has no MFMA K3
     assert f(32, 8, 128, 16, 48, 12, BF, F32) == 0      # norm weights of another dtype
     assert f(32, 8, 128, 8, 48, 12, BF, BF) == 0        # pages of 8 tokens
-    assert f(32, 8, 128, 16, 256, 8, BF, BF) == 0       # 32-page splits (multi-wave K3)
+    assert f(32, 8, 128, 16, 256, 8, BF, BF) == 1       # 32-page splits: 8-wave workgroups
+    assert f(32, 8, 128, 16, 640, 1, BF, BF) == 1       # one split of 640 pages
+    assert f(32, 8, 128, 16, 30000, 1, BF, BF) == 0     # block ids past the LDS budget
     assert f(32, 8, 256, 16, 48, 12, BF, BF) == 0
     assert f(48, 8, 128, 16, 48, 12, BF, BF) == 0       # 6 q heads per kv head
 
@@ -35,6 +37,12 @@ CASES = [
     (4, 16, 8, 128, 16, [33, 64, 65, 2], 6, 3, 6),       # ksplit 6: past the first batch
     (2, 8, 8, 64, 16, [31, 48], 4, 1, 3),                # D 64, one kv head per q head
     (2, 16, 2, 128, 32, [40, 95], 4, 2, 2),              # 32-token pages, 8 q heads per kv
+    # 8-wave workgroups (splits of more than 16 pages): the new token's wave
+    # writes it; waves past the sequence's pages only join the LDS merge
+    (2, 32, 8, 128, 16, [300, 513], 40, 1, 2),           # one split, owners waves 3 and 6
+    (3, 16, 8, 128, 16, [1, 64, 200], 20, 1, 1),         # a one-token sequence: wave 0
+    (2, 32, 8, 128, 16, [700, 1000], 80, 2, 3),          # 40-page splits, combine after
+    (2, 32, 8, 128, 16, [5000, 9000], 1100, 1, 2),       # 138 pages a wave: ids staged in LDS
 ]
 
 
