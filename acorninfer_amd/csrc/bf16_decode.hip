@@ -20,6 +20,11 @@
 //    results through LDS in fixed order at the end.
 //  * Split-K (ksplit > 1) writes fp32 partials [ksplit, M, N], summed in split
 //    order by the consumer (bitwise deterministic).
+//  * MODE 1 (NormIn): x is the residual; each lane computes its row's 1 / rms
+//    from the producer's per-16-column sums of squares (requested before the
+//    weights) and normalises every x operand on load. MODE 2 (ResidOut, one
+//    split, no SwiGLU): instead of y the epilogue stores the new residual
+//    bf16(res + bf16(y)) and each 16-row tile's sum of its squares per x row.
 #include "gemm_common.h"
 
 using namespace acorn;
@@ -33,21 +38,26 @@ struct BfdArgs {
   float* part;    // fp32 [ksplit, M, N] otherwise
   int M, N, K;
   int kr;         // K range of a split (a multiple of 32 * KW * UPW * DEPTH)
+  NormIn ni;      // MODE 1
+  ResidOut ro;    // MODE 2
 };
 
-template <int RT, int UPW>
+template <int RT, int UPW, bool NORM>
 struct BfdStage {
   u32x4 w[RT][UPW];          // block (tile rt, block u): this lane's 16 bytes
   u32x4 x[UPW];              // B operand of block u: x row lr, k 8 lg .. 8 lg + 7
+  u32x4 nw[NORM ? UPW : 1];  // MODE 1: the norm weights of those k
 };
 
 // Grid: x = tile groups of RG * RT 16-row tiles, y = ksplit; block RG * KW
 // waves. Row group r of workgroup b owns tiles (b RG + r) RT .. + RT - 1; its
 // KW waves split the split's K range. Lane (lr, lg) holds x row min(lr, M - 1)
 // (rows past M feed only columns that are never stored).
-template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU>
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU, int MODE>
 __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a) {
   constexpr int NW = RG * KW;
+  constexpr bool NORM = MODE == 1;
+  static_assert(MODE != 2 || !SWIGLU, "the residual epilogue replaces a plain output");
   const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lg = lane >> 4, lr = lane & 15;
   const int rg = wid / KW, kq = wid % KW;
@@ -60,9 +70,14 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
   const int ns = BW / UPW;                        // stages, a multiple of DEPTH
   const uint8_t* wb = a.w + ((size_t)tt * KB + kw0 / 32) * 1024 + lane * 16;
   const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 8 * lg;
-  auto load = [&](int s, BfdStage<RT, UPW>& r) {
+  const __bf16* nwb = NORM ? a.ni.w + kw0 + 8 * lg : nullptr;
+  auto load = [&](int s, BfdStage<RT, UPW, NORM>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) r.x[u] = *(const u32x4*)(xb + (s * UPW + u) * 32);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int u = 0; u < UPW; ++u) r.nw[u] = *(const u32x4*)(nwb + (s * UPW + u) * 32);
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -70,17 +85,24 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
         r.w[rt][u] = load_nt((const u32x4*)(wb + ((size_t)rt * KB + s * UPW + u) * 1024));
   };
 
-  BfdStage<RT, UPW> ring[DEPTH];
+  // MODE 1: this row's 1 / rms, its sums requested ahead of the weights
+  NormRegs nr;
+  if constexpr (NORM) norm_issue(a.ni, min(lr, a.M - 1), lg, nr);
+  BfdStage<RT, UPW, NORM> ring[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+  float inv = 1.f;
+  if constexpr (NORM) inv = norm_finish(a.ni, min(lr, a.M - 1), lg, a.K, nr);
   f32x4 acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](const BfdStage<RT, UPW>& r) {
+  auto compute = [&](const BfdStage<RT, UPW, NORM>& r) {
 #pragma unroll
-    for (int u = 0; u < UPW; ++u)
+    for (int u = 0; u < UPW; ++u) {
+      const u32x4 xu = NORM ? norm_x8(r.x[u], r.nw[u], inv) : r.x[u];
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) acc[rt] = mfma(r.w[rt][u], r.x[u], acc[rt]);
+      for (int rt = 0; rt < RT; ++rt) acc[rt] = mfma(r.w[rt][u], xu, acc[rt]);
+    }
   };
   int s0 = 0;
   for (; s0 + DEPTH < ns; s0 += DEPTH) {
@@ -126,6 +148,18 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
                          swiglu_bf16(acc[2 * p][3], acc[2 * p + 1][3]));
       __builtin_memcpy(a.out + (size_t)lr * NA + n, v, sizeof(v));
     }
+  } else if constexpr (MODE == 2) {
+    // the new residual, and per tile the sum of its squares over the 16 rows
+    // (lane groups 0..3 hold rows 4 lg .. 4 lg + 3: added pairwise, in order)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int n = (t0 + rt) * 16 + 4 * lg;
+      const float y[4] = {acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]};
+      float sq = resid_store4(a.ro, (size_t)lr * a.N + n, y);
+      sq = sq + __shfl_xor(sq, 16);
+      sq = sq + __shfl_xor(sq, 32);
+      if (lg == 0) a.ro.ss[(size_t)lr * (a.N / 16) + t0 + rt] = sq;
+    }
   } else if (a.out) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -145,12 +179,20 @@ int launch(const DirectPlan& p, const BfdArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(RG * KW * kWave);
   if constexpr (RT >= 2) {
     if (p.swiglu) {
-      bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, true><<<grid, block, 0, st>>>(a);
+      if (p.mode == 1)
+        bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 1><<<grid, block, 0, st>>>(a);
+      else
+        bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 0><<<grid, block, 0, st>>>(a);
       return ACORN_OK;
     }
   }
   if (p.swiglu) return ACORN_ERR_UNSUPPORTED;
-  bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false><<<grid, block, 0, st>>>(a);
+  switch (p.mode) {
+    case 0: bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 0><<<grid, block, 0, st>>>(a); break;
+    case 1: bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 1><<<grid, block, 0, st>>>(a); break;
+    case 2: bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 2><<<grid, block, 0, st>>>(a); break;
+    default: return ACORN_ERR_UNSUPPORTED;
+  }
   return ACORN_OK;
 }
 
@@ -261,17 +303,28 @@ int bf16b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu
   p->depth = depth;
   p->groups = (int)groups;
   p->swiglu = swiglu;
+  p->mode = 0;
   return ACORN_OK;
 }
 
 int bf16b_launch(const DirectPlan& p, const void* x, const void* w, void* out, float* part,
-                 int64_t M, int64_t N, int64_t K, hipStream_t st) {
+                 int64_t M, int64_t N, int64_t K, const NormIn* ni, const ResidOut* ro,
+                 hipStream_t st) {
   if (!x || !w) return ACORN_ERR_VALUE;
   if (M < 1 || M > 16) return ACORN_ERR_UNSUPPORTED;
   if (p.ksplit > 1) out = nullptr;
-  if (!out && (!part || p.swiglu)) return ACORN_ERR_VALUE;
-  const BfdArgs a{(const __bf16*)x, (const uint8_t*)w, (__bf16*)out, part, (int)M, (int)N,
-                  (int)K, (int)(K / p.ksplit)};
+  if (p.mode == 2) {
+    // the residual epilogue: one split, no SwiGLU, complete 16-row tiles
+    if (!ro || !ro->res || !ro->res_out || !ro->ss) return ACORN_ERR_VALUE;
+    if (p.ksplit != 1 || p.swiglu) return ACORN_ERR_UNSUPPORTED;
+  } else if (!out && (!part || p.swiglu)) {
+    return ACORN_ERR_VALUE;
+  }
+  if (p.mode == 1 && (!ni || !ni->w || !ni->ss || ni->nss * 16 != K)) return ACORN_ERR_VALUE;
+  BfdArgs a{(const __bf16*)x, (const uint8_t*)w, (__bf16*)out, part, (int)M, (int)N,
+            (int)K, (int)(K / p.ksplit), NormIn{}, ResidOut{}};
+  if (ni) a.ni = *ni;
+  if (ro) a.ro = *ro;
   int rc = ACORN_ERR_UNSUPPORTED;
   switch (p.rt) {
     case 1: rc = by_upw<1>(p, a, st); break;

@@ -93,6 +93,104 @@ __device__ __forceinline__ float swiglu_bf16(float g, float u) {
   return sg * u;
 }
 
+// ---- the RMSNorm folded into the decode GEMMs (direct kernels) ------------
+// A producer projection (o, down) that finishes its columns in one launch
+// (one split) writes the new residual v = bf16(res + bf16(y)) and, per 16
+// columns of v, the fp32 sum of v^2 (ss [M][N / 16]); the consumer projection
+// (gate|up, the next layer's qkv) reads v as its x and normalises it on load,
+// bf16((v * inv) * w) with inv = 1 / sqrt(sum ss / cols + eps): K1's arithmetic
+// (rmsnorm.hip), with the sum of squares added in another order.
+struct NormIn {
+  const __bf16* w;       // norm weight [K]
+  const float* ss;       // [M][nss] per-16-column sums of squares of x
+  int nss;               // K / 16
+  float eps;
+};
+struct ResidOut {
+  const __bf16* res;     // [M, N] residual in
+  __bf16* res_out;       // [M, N] residual out (may alias res: each element is read and
+                         // written by the same lane)
+  float* ss;             // [M][N / 16]
+};
+
+// Row m's 1 / rms from its nss partial sums, computed by the four lanes of lane
+// group q = 0..3 that hold row m (a quarter each, added in a fixed order), the
+// same value in every lane of every wave. In two halves, so that the sums are
+// requested before a kernel's first weights and added after them (loads
+// complete in order: waiting for the sums does not wait for the weights): up
+// to kNormRegs floats per lane go through registers, requested unconditionally
+// (past the quarter they re-read its last vector, unused); longer or unaligned
+// quarters are read at the finish.
+constexpr int kNormRegs = 64;
+struct NormRegs {
+  f32x4 v[kNormRegs / 4];
+};
+__device__ __forceinline__ void norm_issue(const NormIn& n, int m, int q, NormRegs& r) {
+  const int per = n.nss / 4;
+  if (per % 4 || per > kNormRegs) return;                 // uniform
+  const float* p = n.ss + (size_t)m * n.nss + q * per;
+#pragma unroll
+  for (int t = 0; t < kNormRegs / 4; ++t) r.v[t] = *(const f32x4*)(p + 4 * min(t, per / 4 - 1));
+}
+__device__ __forceinline__ float norm_finish(const NormIn& n, int m, int q, int cols,
+                                             const NormRegs& r) {
+#pragma clang fp contract(off)
+  const int per = n.nss / 4;
+  float s = 0.f;
+  if (per % 4 || per > kNormRegs) {
+    const float* p = n.ss + (size_t)m * n.nss + q * per;
+    for (int t = 0; t < per; ++t) s = s + p[t];
+  } else {
+#pragma unroll
+    for (int t = 0; t < kNormRegs / 4; ++t) {
+      if (4 * t < per) {
+        s = s + r.v[t][0];
+        s = s + r.v[t][1];
+        s = s + r.v[t][2];
+        s = s + r.v[t][3];
+      }
+    }
+  }
+  s = s + __shfl_xor(s, 16);
+  s = s + __shfl_xor(s, 32);
+  return 1.0f / sqrtf(s / (float)cols + n.eps);
+}
+
+// 8 bf16 of x (one MFMA operand) -> bf16((x * inv) * w), K1's rounding.
+__device__ __forceinline__ u32x4 norm_x8(u32x4 v, u32x4 w, float inv) {
+#pragma clang fp contract(off)
+  u32x4 r;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const float v0 = __uint_as_float(v[d] << 16), v1 = __uint_as_float(v[d] & 0xffff0000u);
+    const float w0 = __uint_as_float(w[d] << 16), w1 = __uint_as_float(w[d] & 0xffff0000u);
+    r[d] = pack_bf16x2((v0 * inv) * w0, (v1 * inv) * w1);
+  }
+  return r;
+}
+
+// The producer's epilogue for the 4 columns n .. n + 3 of row m held by one
+// lane (y fp32): v = bf16(res + bf16(y)) stored to res_out; returns their sum
+// of squares in column order.
+__device__ __forceinline__ float resid_store4(const ResidOut& r, size_t off, const float (&y)[4]) {
+#pragma clang fp contract(off)
+  uint32_t rin[2];
+  __builtin_memcpy(rin, r.res + off, sizeof(rin));
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float rv = __uint_as_float(i & 1 ? rin[i / 2] & 0xffff0000u : rin[i / 2] << 16);
+    const float yb = (float)(__bf16)y[i];
+    v[i] = (float)(__bf16)(rv + yb);
+  }
+  const uint32_t o[2] = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  __builtin_memcpy(r.res_out + off, o, sizeof(o));
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s = s + v[i] * v[i];
+  return s;
+}
+
 // ---- W4B: int4 weights in 1 KB blocks (ACORN_WFMT_W4B) -------------------
 // Block (n/16, g) holds rows 16*(n/16) .. +15 x the 128 k of group g as one
 // wave's MFMA A operand: lane (c%4)*16 + n%16 has the 16 bytes of row n,
@@ -139,13 +237,14 @@ struct W4bPlan {
   int groups;      // workgroups along N
   size_t lds;      // dynamic LDS bytes
   bool swiglu;
+  int mode;        // the direct kernel: 0 plain, 1 NormIn, 2 ResidOut (as DirectPlan)
 };
 int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4bPlan* p);
 // out (bf16 [M,N], or act [M,N/2] for swiglu) when given and ksplit == 1;
 // otherwise fp32 partials part[ksplit, M, N].
 int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale,
                const void* zero, void* out, float* part, int64_t M, int64_t N, int64_t K,
-               hipStream_t st);
+               const NormIn* ni, const ResidOut* ro, hipStream_t st);
 
 // ---- the int4 GEMM for 17..256 rows (w4_decode.hip) ----------------------------
 // cfg knobs (rt = kMidRT marks the request): upw = row tiles per wave (1, 2),
@@ -173,16 +272,19 @@ struct DirectPlan {
   int rt, upw, nw_field, rg, kw, ksplit, depth;
   int groups;      // workgroups along N
   bool swiglu;
+  int mode;        // 0 plain, 1 x normalised on load (NormIn), 2 residual epilogue (ResidOut)
 };
 int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, DirectPlan* p);
 // out (bf16 [M,N], or act [M,N/2] for swiglu) when given and ksplit == 1;
 // otherwise fp32 partials part[ksplit, M, N] (each already scaled).
 int w8b_launch(const DirectPlan& p, const void* x, const void* w, const void* scale, void* out,
-               float* part, int64_t M, int64_t N, int64_t K, hipStream_t st);
+               float* part, int64_t M, int64_t N, int64_t K, const NormIn* ni,
+               const ResidOut* ro, hipStream_t st);
 int bf16b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu,
                     DirectPlan* p);
 int bf16b_launch(const DirectPlan& p, const void* x, const void* w, void* out, float* part,
-                 int64_t M, int64_t N, int64_t K, hipStream_t st);
+                 int64_t M, int64_t N, int64_t K, const NormIn* ni, const ResidOut* ro,
+                 hipStream_t st);
 
 // ---- the large-M bf16 GEMM (dense_gemm.hip) ---------------------------------
 // out[M,N] = x[M,K] . w[N,K]^T, bf16 operands: (4 wn) x bm output tiles (wn

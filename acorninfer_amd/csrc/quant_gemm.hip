@@ -1233,14 +1233,22 @@ int plan_entry(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg, bool swiglu)
 
 int gemm_entry(const void* x, const void* w, const void* scale, const void* zero,
                void* out_bf16, float* part, int64_t M, int64_t N, int64_t K, int wfmt,
-               const int* cfg, bool swiglu, hipStream_t st) {
+               const int* cfg, bool swiglu, hipStream_t st, const NormIn* ni = nullptr,
+               const ResidOut* ro = nullptr) {
   if (!x || !w || (wfmt != ACORN_WFMT_BF16 && wfmt != ACORN_WFMT_BF16B && !scale))
     return ACORN_ERR_VALUE;
-  if (!out_bf16 && !part) return ACORN_ERR_VALUE;
+  if (!out_bf16 && !part && !ro) return ACORN_ERR_VALUE;
   if (M > 65535 * 64 || N > ((int64_t)1 << 30) || K > ((int64_t)1 << 30)) return ACORN_ERR_SHAPE;
   Tiling t;
   int rc = make_plan(M, N, K, wfmt, cfg, &t, swiglu);
   if (rc) return rc;
+  // the folded RMSNorm is built into the direct decode kernels only
+  const int mode = ni ? 1 : ro ? 2 : 0;
+  if (mode) {
+    if (!(t.kind == 6 || t.kind == 5 || (t.kind == 2 && t.w4b.direct)))
+      return ACORN_ERR_UNSUPPORTED;
+    t.bf16b.mode = t.w8b.mode = t.w4b.mode = mode;
+  }
   // ksplit > 1 with a bf16 output needs the partials workspace
   if (out_bf16 && t.ksplit > 1 && !part) return ACORN_ERR_VALUE;
   KArgs a;
@@ -1266,14 +1274,16 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
                                       M, N, K, t.nw, t.upw, t.tpw, t.ksplit, blk, st);
   } else if (t.kind == 2) {
     rc = w4b_launch(t.w4b, x, w, scale, zero, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K,
-                    st);
+                    ni, ro, st);
   } else if (t.kind == 4) {
     if (zero) return ACORN_ERR_UNSUPPORTED;  // the block layout is the symmetric format
     rc = w4m_launch(t.w4m, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
   } else if (t.kind == 5) {
-    rc = w8b_launch(t.w8b, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
+    rc = w8b_launch(t.w8b, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, ni,
+                    ro, st);
   } else if (t.kind == 6) {
-    rc = bf16b_launch(t.bf16b, x, w, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
+    rc = bf16b_launch(t.bf16b, x, w, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, ni, ro,
+                      st);
   } else if (t.kind == 1) {
     switch (wfmt) {
       case ACORN_WFMT_BF16: rc = dispatch_tiled<ACORN_WFMT_BF16>(t, a, st); break;
@@ -1352,6 +1362,28 @@ extern "C" int acorn_quant_gemm_swiglu(const void* x, const void* w, const void*
   if (!act) return ACORN_ERR_VALUE;
   return gemm_entry(x, w, scale, zero, act, nullptr, M, N, K, wfmt, cfg, true,
                     (hipStream_t)stream);
+}
+
+extern "C" int acorn_quant_gemm_norm(const void* x, const void* w, const void* scale,
+                                     void* out_bf16, float* part, int64_t M, int64_t N,
+                                     int64_t K, int wfmt, const int* cfg, int swiglu,
+                                     const void* norm_w, const float* ss_in, float eps,
+                                     const void* res, void* res_out, float* ss_out,
+                                     void* stream) {
+  if (wfmt != ACORN_WFMT_BF16B && wfmt != ACORN_WFMT_W8B && wfmt != ACORN_WFMT_W4B)
+    return ACORN_ERR_DTYPE;
+  if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 16) return ACORN_ERR_SHAPE;
+  if (M == 0) return ACORN_OK;
+  const bool norm = norm_w != nullptr, resid = res != nullptr;
+  if (norm == resid) return ACORN_ERR_VALUE;                 // exactly one of the two
+  if (resid && swiglu) return ACORN_ERR_UNSUPPORTED;
+  if (norm && !ss_in) return ACORN_ERR_VALUE;
+  if (resid && (!res_out || !ss_out)) return ACORN_ERR_VALUE;
+  if (swiglu && !out_bf16) return ACORN_ERR_VALUE;
+  const NormIn ni{(const __bf16*)norm_w, ss_in, (int)(K / 16), eps};
+  const ResidOut ro{(const __bf16*)res, (__bf16*)res_out, ss_out};
+  return gemm_entry(x, w, scale, nullptr, out_bf16, part, M, N, K, wfmt, cfg, swiglu != 0,
+                    (hipStream_t)stream, norm ? &ni : nullptr, resid ? &ro : nullptr);
 }
 
 extern "C" int acorn_dequant_w4b(const void* w, const void* scale, void* out_bf16, int64_t N,

@@ -47,13 +47,16 @@ struct W4dArgs {
   float* part;    // fp32 [ksplit, M, N] otherwise
   int M, N, K;
   int kr;         // K range of a split (a multiple of 128 * UPW * DEPTH)
+  NormIn ni;      // MODE 1: x is the residual, normalised on load (gemm_common.h)
+  ResidOut ro;    // MODE 2: the residual epilogue (gemm_common.h)
 };
 
-template <int RT, int UPW>
+template <int RT, int UPW, bool NORM>
 struct DStage {
   u32x4 w[RT][UPW];          // unit (rt, u): this lane's 16 bytes of block (tile, group)
   u32x4 x[UPW][4];           // B operand of MFMA j of group u: x row lr, k 32 lg + 8 j ..
   uint32_t s[RT][2 * UPW];   // fp16 scales: half 4u + i is row 4 lg + i of group u
+  u32x4 nw[NORM ? UPW : 1][4];   // MODE 1: the norm weights of those k
 };
 
 // bf16 -136 in every slot: an MFMA of it against x gives -136 X per column
@@ -66,9 +69,11 @@ constexpr uint32_t kNeg136x2 = 0xC308C308u;
 // order at the end). Each wave keeps DEPTH stages of UPW groups in flight.
 // Lane (lr, lg) holds x row min(lr, M - 1) (rows past M feed only columns
 // that are never stored).
-template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU>
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU, int MODE>
 __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) {
   constexpr int NW = RG * KW;
+  constexpr bool NORM = MODE == 1;
+  static_assert(MODE != 2 || !SWIGLU, "the residual epilogue replaces a plain output");
   const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lg = lane >> 4, lr = lane & 15;
   const int rg = wid / KW, kq = wid % KW;
@@ -83,11 +88,19 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
   const uint8_t* wb = a.w + ((size_t)tt * G + g0) * 1024 + lane * 16;
   const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 32 * lg;
   const _Float16* sb = a.scale + (size_t)tt * G4 * 64 + lg * 16;
-  auto load = [&](int s, DStage<RT, UPW>& r) {
+  const __bf16* nwb = NORM ? a.ni.w + kw0 + 32 * lg : nullptr;
+  auto load = [&](int s, DStage<RT, UPW, NORM>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u)
 #pragma unroll
       for (int j = 0; j < 4; ++j) r.x[u][j] = *(const u32x4*)(xb + (s * UPW + u) * 128 + 8 * j);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int u = 0; u < UPW; ++u)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          r.nw[u][j] = *(const u32x4*)(nwb + (s * UPW + u) * 128 + 8 * j);
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -99,24 +112,31 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
       load_dwords(sb + (size_t)rt * G4 * 64 + (g / 4) * 64 + (g % 4) * 4, r.s[rt]);
   };
 
-  DStage<RT, UPW> ring[DEPTH];
+  NormRegs nr;
+  if constexpr (NORM) norm_issue(a.ni, min(lr, a.M - 1), lg, nr);
+  DStage<RT, UPW, NORM> ring[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+  float inv = 1.f;
+  if constexpr (NORM) inv = norm_finish(a.ni, min(lr, a.M - 1), lg, a.K, nr);
   f32x4 acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const u32x4 neg136 = {kNeg136x2, kNeg136x2, kNeg136x2, kNeg136x2};
-  auto compute = [&](const DStage<RT, UPW>& r) {
+  auto compute = [&](const DStage<RT, UPW, NORM>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
+      u32x4 xu[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xu[j] = NORM ? norm_x8(r.x[u][j], r.nw[u][j], inv) : r.x[u][j];
       f32x4 xb136 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xb136 = mfma(neg136, r.x[u][j], xb136);
+      for (int j = 0; j < 4; ++j) xb136 = mfma(neg136, xu[j], xb136);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         f32x4 cc = xb136;                          // C - 136 X
 #pragma unroll
-        for (int j = 0; j < 4; ++j) cc = mfma(unpack_w4(r.w[rt][u][j]), r.x[u][j], cc);
+        for (int j = 0; j < 4; ++j) cc = mfma(unpack_w4(r.w[rt][u][j]), xu[j], cc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[rt][i] = fma_half(r.s[rt], 4 * u + i, cc[i], acc[rt][i]);
       }
@@ -168,6 +188,17 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
       v[1] = pack_bf16x2(swiglu_bf16(acc[2 * p][2], acc[2 * p + 1][2]),
                          swiglu_bf16(acc[2 * p][3], acc[2 * p + 1][3]));
       __builtin_memcpy(a.out + (size_t)lr * NA + n, v, sizeof(v));
+    }
+  } else if constexpr (MODE == 2) {
+    // the new residual, and per tile the sum of its squares over the 16 rows
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int n = (t0 + rt) * 16 + 4 * lg;
+      const float y[4] = {acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]};
+      float sq = resid_store4(a.ro, (size_t)lr * a.N + n, y);
+      sq = sq + __shfl_xor(sq, 16);
+      sq = sq + __shfl_xor(sq, 32);
+      if (lg == 0) a.ro.ss[(size_t)lr * (a.N / 16) + t0 + rt] = sq;
     }
   } else if (a.out) {
 #pragma unroll
@@ -570,12 +601,20 @@ int launch_direct(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(RG * KW * kWave);
   if constexpr (RT >= 2) {
     if (p.swiglu) {
-      w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, true><<<grid, block, 0, st>>>(a);
+      if (p.mode == 1)
+        w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 1><<<grid, block, 0, st>>>(a);
+      else
+        w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 0><<<grid, block, 0, st>>>(a);
       return ACORN_OK;
     }
   }
   if (p.swiglu) return ACORN_ERR_UNSUPPORTED;
-  w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false><<<grid, block, 0, st>>>(a);
+  switch (p.mode) {
+    case 0: w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 0><<<grid, block, 0, st>>>(a); break;
+    case 1: w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 1><<<grid, block, 0, st>>>(a); break;
+    case 2: w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 2><<<grid, block, 0, st>>>(a); break;
+    default: return ACORN_ERR_UNSUPPORTED;
+  }
   return ACORN_OK;
 }
 
@@ -742,6 +781,7 @@ int direct_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4
   p->groups = (int)groups;
   p->lds = 0;
   p->swiglu = swiglu;
+  p->mode = 0;
   return ACORN_OK;
 }
 
@@ -822,23 +862,33 @@ int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   p->groups = (int)groups;
   p->lds = lds(ks);
   p->swiglu = false;
+  p->mode = 0;
   if (groups > 0x7fffffff || ks > 65535) return ACORN_ERR_SHAPE;
   return ACORN_OK;
 }
 
 int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale,
                const void* zero, void* out, float* part, int64_t M, int64_t N, int64_t K,
-               hipStream_t st) {
+               const NormIn* ni, const ResidOut* ro, hipStream_t st) {
   if (zero) return ACORN_ERR_UNSUPPORTED;  // the block layout is the symmetric format
   if (!x || !w || !scale) return ACORN_ERR_VALUE;
   // bf16 (or SwiGLU act) output only with one split; else fp32 partials
   if (p.ksplit > 1) out = nullptr;
-  if (!out && (!part || p.swiglu)) return ACORN_ERR_VALUE;
+  if (p.mode != 0 && !p.direct) return ACORN_ERR_UNSUPPORTED;
+  if (p.mode == 2) {
+    if (!ro || !ro->res || !ro->res_out || !ro->ss) return ACORN_ERR_VALUE;
+    if (p.ksplit != 1 || p.swiglu) return ACORN_ERR_UNSUPPORTED;
+  } else if (!out && (!part || p.swiglu)) {
+    return ACORN_ERR_VALUE;
+  }
+  if (p.mode == 1 && (!ni || !ni->w || !ni->ss || ni->nss * 16 != K)) return ACORN_ERR_VALUE;
   int rc = ACORN_ERR_UNSUPPORTED;
   if (p.direct) {
     if (M > 16) return ACORN_ERR_UNSUPPORTED;
-    const W4dArgs a{(const __bf16*)x, (const uint8_t*)w, (const _Float16*)scale, (__bf16*)out,
-                    part, (int)M, (int)N, (int)K, (int)(K / p.ksplit)};
+    W4dArgs a{(const __bf16*)x, (const uint8_t*)w, (const _Float16*)scale, (__bf16*)out,
+              part, (int)M, (int)N, (int)K, (int)(K / p.ksplit), NormIn{}, ResidOut{}};
+    if (ni) a.ni = *ni;
+    if (ro) a.ro = *ro;
     switch (p.rt) {
       case 1: rc = direct_upw<1>(p, a, st); break;
       case 2: rc = direct_upw<2>(p, a, st); break;

@@ -22,6 +22,8 @@
 //    their results through LDS in fixed order at the end.
 //  * Split-K (ksplit > 1) writes scaled fp32 partials [ksplit, M, N], summed
 //    in split order by the consumer (bitwise deterministic).
+//  * MODE 1 / 2: the RMSNorm folded in as in bf16_decode.hip (x normalised on
+//    load; the residual epilogue with its sums of squares).
 #include "gemm_common.h"
 
 using namespace acorn;
@@ -36,12 +38,15 @@ struct W8dArgs {
   float* part;    // fp32 [ksplit, M, N] otherwise
   int M, N, K;
   int kr;         // K range of a split (a multiple of 64 * KW * UPW * DEPTH)
+  NormIn ni;      // MODE 1
+  ResidOut ro;    // MODE 2
 };
 
-template <int RT, int UPW>
+template <int RT, int UPW, bool NORM>
 struct W8Stage {
   u32x4 w[RT][UPW];          // block (tile rt, block u): this lane's 16 bytes
   u32x4 x[UPW][2];           // B operand of MFMA j of block u: x row lr, k 16 lg + 8 j ..
+  u32x4 nw[NORM ? UPW : 1][2];   // MODE 1: the norm weights of those k
 };
 
 // bf16 -128 in every slot: an MFMA of it against x gives -128 X per column
@@ -61,9 +66,11 @@ __device__ __forceinline__ u32x4 unpack_w8(uint32_t a, uint32_t b) {
 // waves. Row group r of workgroup b owns tiles (b RG + r) RT .. + RT - 1; its
 // KW waves split the split's K range. Lane (lr, lg) holds x row min(lr, M - 1)
 // (rows past M feed only columns that are never stored).
-template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU>
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU, int MODE>
 __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) {
   constexpr int NW = RG * KW;
+  constexpr bool NORM = MODE == 1;
+  static_assert(MODE != 2 || !SWIGLU, "the residual epilogue replaces a plain output");
   const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lg = lane >> 4, lr = lane & 15;
   const int rg = wid / KW, kq = wid % KW;
@@ -76,11 +83,19 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
   const int ns = BW / UPW;                        // stages, a multiple of DEPTH
   const uint8_t* wb = a.w + ((size_t)tt * KB + kw0 / 64) * 1024 + lane * 16;
   const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 16 * lg;
-  auto load = [&](int s, W8Stage<RT, UPW>& r) {
+  const __bf16* nwb = NORM ? a.ni.w + kw0 + 16 * lg : nullptr;
+  auto load = [&](int s, W8Stage<RT, UPW, NORM>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u)
 #pragma unroll
       for (int j = 0; j < 2; ++j) r.x[u][j] = *(const u32x4*)(xb + (s * UPW + u) * 64 + 8 * j);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int u = 0; u < UPW; ++u)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          r.nw[u][j] = *(const u32x4*)(nwb + (s * UPW + u) * 64 + 8 * j);
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -88,24 +103,31 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
         r.w[rt][u] = load_nt((const u32x4*)(wb + ((size_t)rt * KB + s * UPW + u) * 1024));
   };
 
-  W8Stage<RT, UPW> ring[DEPTH];
+  NormRegs nr;
+  if constexpr (NORM) norm_issue(a.ni, min(lr, a.M - 1), lg, nr);
+  W8Stage<RT, UPW, NORM> ring[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+  float inv = 1.f;
+  if constexpr (NORM) inv = norm_finish(a.ni, min(lr, a.M - 1), lg, a.K, nr);
   f32x4 acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
   f32x4 xacc = {0.f, 0.f, 0.f, 0.f};             // -128 X over the wave's K range
   const u32x4 neg128 = {kNeg128x2, kNeg128x2, kNeg128x2, kNeg128x2};
-  auto compute = [&](const W8Stage<RT, UPW>& r) {
+  auto compute = [&](const W8Stage<RT, UPW, NORM>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
+      u32x4 xu[2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) xacc = mfma(neg128, r.x[u][j], xacc);
+      for (int j = 0; j < 2; ++j) xu[j] = NORM ? norm_x8(r.x[u][j], r.nw[u][j], inv) : r.x[u][j];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) xacc = mfma(neg128, xu[j], xacc);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[rt] = mfma(unpack_w8(r.w[rt][u][2 * j], r.w[rt][u][2 * j + 1]), r.x[u][j], acc[rt]);
+          acc[rt] = mfma(unpack_w8(r.w[rt][u][2 * j], r.w[rt][u][2 * j + 1]), xu[j], acc[rt]);
       // one block at a time: keeps the unpacked operands of later blocks from
       // being hoisted past the register ring's budget
       __builtin_amdgcn_sched_barrier(0);
@@ -169,6 +191,16 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
                          swiglu_bf16(y[2 * p][3], y[2 * p + 1][3]));
       __builtin_memcpy(a.out + (size_t)lr * NA + n, v, sizeof(v));
     }
+  } else if constexpr (MODE == 2) {
+    // the new residual, and per tile the sum of its squares over the 16 rows
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int n = (t0 + rt) * 16 + 4 * lg;
+      float sq = resid_store4(a.ro, (size_t)lr * a.N + n, y[rt]);
+      sq = sq + __shfl_xor(sq, 16);
+      sq = sq + __shfl_xor(sq, 32);
+      if (lg == 0) a.ro.ss[(size_t)lr * (a.N / 16) + t0 + rt] = sq;
+    }
   } else if (a.out) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -189,12 +221,20 @@ int launch(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(RG * KW * kWave);
   if constexpr (RT >= 2) {
     if (p.swiglu) {
-      w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, true><<<grid, block, 0, st>>>(a);
+      if (p.mode == 1)
+        w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 1><<<grid, block, 0, st>>>(a);
+      else
+        w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 0><<<grid, block, 0, st>>>(a);
       return ACORN_OK;
     }
   }
   if (p.swiglu) return ACORN_ERR_UNSUPPORTED;
-  w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, false><<<grid, block, 0, st>>>(a);
+  switch (p.mode) {
+    case 0: w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 0><<<grid, block, 0, st>>>(a); break;
+    case 1: w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 1><<<grid, block, 0, st>>>(a); break;
+    case 2: w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 2><<<grid, block, 0, st>>>(a); break;
+    default: return ACORN_ERR_UNSUPPORTED;
+  }
   return ACORN_OK;
 }
 
@@ -299,17 +339,27 @@ int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   p->depth = depth;
   p->groups = (int)groups;
   p->swiglu = swiglu;
+  p->mode = 0;
   return ACORN_OK;
 }
 
 int w8b_launch(const DirectPlan& p, const void* x, const void* w, const void* scale, void* out,
-               float* part, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+               float* part, int64_t M, int64_t N, int64_t K, const NormIn* ni,
+               const ResidOut* ro, hipStream_t st) {
   if (!x || !w || !scale) return ACORN_ERR_VALUE;
   if (M < 1 || M > 16) return ACORN_ERR_UNSUPPORTED;
   if (p.ksplit > 1) out = nullptr;
-  if (!out && (!part || p.swiglu)) return ACORN_ERR_VALUE;
-  const W8dArgs a{(const __bf16*)x, (const uint8_t*)w, (const _Float16*)scale, (__bf16*)out,
-                  part, (int)M, (int)N, (int)K, (int)(K / p.ksplit)};
+  if (p.mode == 2) {
+    if (!ro || !ro->res || !ro->res_out || !ro->ss) return ACORN_ERR_VALUE;
+    if (p.ksplit != 1 || p.swiglu) return ACORN_ERR_UNSUPPORTED;
+  } else if (!out && (!part || p.swiglu)) {
+    return ACORN_ERR_VALUE;
+  }
+  if (p.mode == 1 && (!ni || !ni->w || !ni->ss || ni->nss * 16 != K)) return ACORN_ERR_VALUE;
+  W8dArgs a{(const __bf16*)x, (const uint8_t*)w, (const _Float16*)scale, (__bf16*)out,
+            part, (int)M, (int)N, (int)K, (int)(K / p.ksplit), NormIn{}, ResidOut{}};
+  if (ni) a.ni = *ni;
+  if (ro) a.ro = *ro;
   int rc = ACORN_ERR_UNSUPPORTED;
   switch (p.rt) {
     case 1: rc = by_upw<1>(p, a, st); break;

@@ -249,6 +249,38 @@ class QLinear:
                                     stream)
         check(rc, "quant_gemm")
 
+    def can_fold(self, M: int) -> bool:
+        """The RMSNorm can be folded into this projection's launch (the direct
+        decode kernels on the block layouts, M <= 16)."""
+        return self.fmt in (WFMT_BF16B, WFMT_W8B, WFMT_W4B) and M <= 16 and self.K % 16 == 0
+
+    def launch_norm(self, x: torch.Tensor, M: int, tiling, *, norm_w: torch.Tensor,
+                    ss: torch.Tensor, eps: float, stream: int, out: torch.Tensor | None = None,
+                    part: torch.Tensor | None = None, act: torch.Tensor | None = None) -> None:
+        """The projection of the normalised residual: x is the residual [M, K]
+        and each row is used as bf16((x * inv) * norm_w), inv from the
+        producer's per-16-column sums of squares ss [M, K/16] (K1's
+        arithmetic, acorninfer/ops/rmsnorm.py:39-82). Output as launch (act
+        given: the fused SwiGLU of launch_swiglu)."""
+        arr = (ctypes.c_int * 6)(*tiling, 0)
+        rc = lib().acorn_quant_gemm_norm(
+            ptr(x), ptr(self.w), ptr(self.scale), ptr(act if act is not None else out), ptr(part),
+            M, self.N, self.K, self.fmt, arr, int(act is not None), ptr(norm_w), ptr(ss),
+            float(eps), None, None, None, stream)
+        check(rc, "quant_gemm_norm")
+
+    def launch_resid(self, x: torch.Tensor, M: int, tiling, *, res: torch.Tensor,
+                     res_out: torch.Tensor, ss: torch.Tensor, stream: int) -> None:
+        """The projection whose output goes into the residual stream: stores
+        res_out = bf16(res + bf16(x @ W^T)) (res_out may be res) and the
+        per-16-column sums of squares ss [M, N/16] a launch_norm consumer
+        reads, in place of K1's residual add (one split only)."""
+        arr = (ctypes.c_int * 6)(*tiling, 0)
+        rc = lib().acorn_quant_gemm_norm(
+            ptr(x), ptr(self.w), ptr(self.scale), None, None, M, self.N, self.K, self.fmt, arr,
+            0, None, None, 0.0, ptr(res), ptr(res_out), ptr(ss), stream)
+        check(rc, "quant_gemm_resid")
+
     def swiglu_plan(self, M: int, tiling=None, workspace: bool = False):
         """As plan, for the fused gate|up + SwiGLU launch (int4 at prefill
         sizes: dequantised onto the bf16 kernel's SwiGLU form)."""
@@ -364,9 +396,15 @@ class Qwen3DecodeModel:
         # split take their output in the activation dtype (half the bytes of
         # an fp32 plane, the same bits after the consumer's rounding)
         self.prefill_direct = True
+        # decode steps fold the RMSNorms between projections into them (o and
+        # down store the residual and its sums of squares, qkv and gate|up
+        # normalise on load) where the kernels support it: no K1 launch
+        # between layers
+        self.fold_norm = True
         # batch -> {projection name -> Tiling}, filled by tune()
         self.tilings: dict[int, dict] = {}
         self.swiglu_choice: dict[int, bool] = {}
+        self.fold_choice: dict[int, bool] = {}
 
     # ---------------------------------------------------------------- building --
     @classmethod
@@ -508,14 +546,21 @@ class Qwen3DecodeModel:
         y_o = buf.y_o if buf.direct else None
         y_down = buf.y_down if buf.direct else None
         prev_ks = 0             # splits of the previous layer's down-projection partials
+        last = len(self.layers) - 1
         for li, lw in enumerate(self.layers):
-            # K1: input norm (layer 0 from the embedding; later layers reduce
-            # the previous down projection's output and add the residual)
-            k1(li == 0, y_down, buf.part_down, prev_ks, lw.input_norm)
-            # qkv projection -> fp32 partials (or its T output) -> K2 epilogue (+ KV scatter)
             cq = buf.cfgs["qkv"]
-            lw.qkv.launch(buf.normed, B, cq, out=y_qkv, part=buf.part_qkv, wtmp=buf.wtmp,
-                          stream=st)
+            if buf.fold and li > 0:
+                # the input norm folded into qkv: the previous down stored the
+                # residual and its sums of squares
+                lw.qkv.launch_norm(buf.res, B, cq, norm_w=lw.input_norm, ss=buf.ss_dn, eps=eps,
+                                   stream=st, out=y_qkv, part=buf.part_qkv)
+            else:
+                # K1: input norm (layer 0 from the embedding; later layers reduce
+                # the previous down projection's output and add the residual)
+                k1(li == 0, y_down, buf.part_down, prev_ks, lw.input_norm)
+                # qkv projection -> fp32 partials (or its T output) -> K2 epilogue (+ KV scatter)
+                lw.qkv.launch(buf.normed, B, cq, out=y_qkv, part=buf.part_qkv, wtmp=buf.wtmp,
+                              stream=st)
             kp = kbase + li * layer_elems * esz
             vp = vbase + li * layer_elems * esz
             if fused_attn:
@@ -545,22 +590,39 @@ class Qwen3DecodeModel:
                         ptr(buf.q), kp, vp, ptr(buf.tables), ptr(buf.lens), ptr(buf.attn),
                         ptr(buf.ws_acc), ptr(buf.ws_ml), B, nq, nkv, D, page_size, num_blocks,
                         buf.max_pages, buf.num_splits, float(self.scale), dt, st), "K3")
-            # o projection -> K1 (reduce + residual add + post-attention norm)
+            # o projection -> K1 (reduce + residual add + post-attention norm);
+            # folded: o adds itself to the residual, gate|up normalises on load
             co = buf.cfgs["o"]
-            lw.o.launch(buf.attn, B, co, out=y_o, part=buf.part_o, wtmp=buf.wtmp, stream=st)
-            k1(False, y_o, buf.part_o, co.ksplit, lw.post_norm)
-            # MLP: gate|up (+ fused SwiGLU) -> act -> down partials
             cg = buf.cfgs["gate_up"]
-            if buf.swiglu:
-                lw.gate_up.launch_swiglu(buf.normed, B, cg, buf.act, st, wtmp=buf.wtmp)
+            if buf.fold:
+                lw.o.launch_resid(buf.attn, B, co, res=buf.res, res_out=buf.res, ss=buf.ss_o,
+                                  stream=st)
+                if buf.swiglu:
+                    lw.gate_up.launch_norm(buf.res, B, cg, norm_w=lw.post_norm, ss=buf.ss_o,
+                                           eps=eps, stream=st, act=buf.act)
+                else:
+                    lw.gate_up.launch_norm(buf.res, B, cg, norm_w=lw.post_norm, ss=buf.ss_o,
+                                           eps=eps, stream=st, part=buf.part_gu)
             else:
-                lw.gate_up.launch(buf.normed, B, cg, part=buf.part_gu, wtmp=buf.wtmp,
-                                   stream=st)
+                lw.o.launch(buf.attn, B, co, out=y_o, part=buf.part_o, wtmp=buf.wtmp, stream=st)
+                k1(False, y_o, buf.part_o, co.ksplit, lw.post_norm)
+                # MLP: gate|up (+ fused SwiGLU) -> act -> down partials
+                if buf.swiglu:
+                    lw.gate_up.launch_swiglu(buf.normed, B, cg, buf.act, st, wtmp=buf.wtmp)
+                else:
+                    lw.gate_up.launch(buf.normed, B, cg, part=buf.part_gu, wtmp=buf.wtmp,
+                                      stream=st)
+            if not buf.swiglu:
                 check(L.acorn_silu_mul(ptr(buf.part_gu), cg.ksplit, None, ptr(buf.act), B, inter,
                                        int(lw.gate_up.il16), dt, st), "silu_mul")
             cd = buf.cfgs["down"]
-            lw.down.launch(buf.act, B, cd, out=y_down, part=buf.part_down, wtmp=buf.wtmp,
-                           stream=st)
+            if buf.fold and li < last:
+                # the next layer's input norm folded into its qkv
+                lw.down.launch_resid(buf.act, B, cd, res=buf.res, res_out=buf.res,
+                                     ss=buf.ss_dn, stream=st)
+            else:
+                lw.down.launch(buf.act, B, cd, out=y_down, part=buf.part_down, wtmp=buf.wtmp,
+                               stream=st)
             prev_ks = cd.ksplit
         # final norm (reduce + residual add) -> lm_head -> greedy
         k1(False, y_down, buf.part_down, prev_ks, self.norm)
@@ -595,11 +657,15 @@ class Qwen3DecodeModel:
         return gu.il16 and rows >= PREFILL_SWIGLU_M and (
             gu.fmt in (WFMT_BF16, WFMT_BF16B) or (gu.fmt == WFMT_W4B and rows >= DEQUANT_M_MIN))
 
+    def fused_swiglu_possible(self, batch: int) -> bool:
+        """The gate|up launch can carry the SwiGLU epilogue (decode sizes,
+        interleaved gate|up rows)."""
+        return batch <= 16 and self.layers[0].gate_up.il16
+
     def fused_swiglu(self, batch: int) -> bool:
-        """The gate|up launch carries the SwiGLU epilogue (decode sizes, and
+        """The gate|up launch carries the SwiGLU epilogue (where possible, and
         unless tune() found the split-K launch + silu_mul faster)."""
-        ok = batch <= 16 and self.layers[0].gate_up.il16
-        return ok and self.swiglu_choice.get(batch, True)
+        return self.fused_swiglu_possible(batch) and self.swiglu_choice.get(batch, True)
 
     def projections(self) -> dict[str, list[QLinear]]:
         """Each projection of the step with its per-layer weights."""
@@ -607,9 +673,20 @@ class Qwen3DecodeModel:
                 "gate_up": [L.gate_up for L in self.layers],
                 "down": [L.down for L in self.layers], "lm_head": [self.lm_head]}
 
+    def fold_possible(self, batch: int, *, tuned: bool = True) -> bool:
+        """Decode steps of `batch` rows fold the RMSNorms into the projections
+        (given one-split o and down tilings): the kernels support it, and
+        unless tune() found the plain launches with their K1s faster (tuned)."""
+        lw = self.layers[0]
+        ok = (self.fold_norm and self.dtype == torch.bfloat16 and
+              self.cfg.hidden_size % 16 == 0 and
+              all(lin.can_fold(batch) for lin in (lw.qkv, lw.o, lw.gate_up, lw.down)))
+        return ok and (not tuned or self.fold_choice.get(batch, True))
+
     def time_projection(self, lins: list[QLinear], M: int, tiling, reps: int = 3,
                         swiglu: bool = False, with_act: bool = False,
-                        with_reduce: bool = False, with_norm: bool = False) -> float:
+                        with_reduce: bool = False, with_norm: bool = False,
+                        norm_in: bool = False, resid: bool = False) -> float:
         """Average µs of one launch of `tiling`, measured as a hipGraph of one
         launch per weight in `lins` (distinct weights, so the 256 MB MALL does
         not hold them between launches) on a private stream with HIP events.
@@ -617,7 +694,8 @@ class Qwen3DecodeModel:
         grows with the split count: with_act adds the separate SwiGLU kernel
         the fused form saves; with_reduce a split-order reduction (the qkv
         epilogue's, spread over many workgroups); with_norm the step's own K1
-        (one workgroup per row), which reads the o and down partials."""
+        (one workgroup per row), which reads the o and down partials. norm_in /
+        resid time the folded forms instead (launch_norm / launch_resid)."""
         from acorninfer_amd.ops.quant_gemm import _native_cfg
         lin0 = lins[0]
         planner = lin0.swiglu_plan if swiglu else lin0.plan
@@ -628,19 +706,34 @@ class Qwen3DecodeModel:
                 if t.rt == DEQUANT_RT else None)
         act = torch.empty(M, lin0.N // 2, dtype=self.dtype, device=self.device)
         red = torch.empty(M, lin0.N, dtype=self.dtype, device=self.device) if with_reduce else None
-        if with_norm:
+        if with_norm or resid:
             res = torch.zeros(M, lin0.N, dtype=self.dtype, device=self.device)
             nrm = torch.empty(M, lin0.N, dtype=self.dtype, device=self.device)
             nw = torch.ones(lin0.N, dtype=self.norm.dtype, device=self.device)
+            ss_out = torch.empty(M, lin0.N // 16, dtype=torch.float32, device=self.device)
+        if norm_in:
+            nw_in = torch.ones(lin0.K, dtype=self.norm.dtype, device=self.device)
+            ss_in = torch.full((M, lin0.K // 16), 16.0, dtype=torch.float32, device=self.device)
+        eps = float(self.cfg.rms_norm_eps)
         s = torch.cuda.Stream(self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(s):
             def body():
                 for lin in lins:
-                    if swiglu:
+                    if resid:
+                        lin.launch_resid(x, M, t, res=res, res_out=res, ss=ss_out,
+                                         stream=s.cuda_stream)
+                    elif norm_in and swiglu:
+                        lin.launch_norm(x, M, t, norm_w=nw_in, ss=ss_in, eps=eps,
+                                        stream=s.cuda_stream, act=act)
+                    elif swiglu:
                         lin.launch_swiglu(x, M, t, act, s.cuda_stream, wtmp=wtmp)
                     else:
-                        lin.launch(x, M, t, part=part, wtmp=wtmp, stream=s.cuda_stream)
+                        if norm_in:
+                            lin.launch_norm(x, M, t, norm_w=nw_in, ss=ss_in, eps=eps,
+                                            stream=s.cuda_stream, part=part)
+                        else:
+                            lin.launch(x, M, t, part=part, wtmp=wtmp, stream=s.cuda_stream)
                         if with_act:   # the separate activation the fused form saves
                             check(lib().acorn_silu_mul(ptr(part), t.ksplit, None, ptr(act), M,
                                                        lin.N // 2, int(lin.il16),
@@ -670,60 +763,97 @@ class Qwen3DecodeModel:
         torch.cuda.current_stream(self.device).wait_stream(s)
         return e0.elapsed_time(e1) * 1e3 / (reps * len(lins))
 
-    def tune(self, batch: int, *, names=None, verbose: bool = False) -> dict:
+    def tune(self, batch: int, *, names=None, verbose: bool = False,
+             fold: bool | None = None) -> dict:
         """Load-time tiling choice for a decode bucket (the reference's
         quant_gemm.configure, acorninfer/ops/quant_gemm.py:449-492): every
         candidate tiling of each projection is timed in place, together with
         the work its split count puts on the consumer, the RETIME_TOP fastest
         are timed again with RETIME_REPS replays, and the fastest of those is
         kept in self.tilings[batch]; run before any graph capture."""
-        from acorninfer_amd.ops.quant_gemm import candidates
         if self.lm_head.fmt == _lib.WFMT_F32:
             return {}
         report = {}
         chosen = self.tilings.setdefault(batch, {})
+        # the folded norms (o and down in one split with the residual
+        # epilogue, qkv and gate|up normalising on load) are timed beside the
+        # plain launches with their K1s, and kept where the four together are
+        # faster (fold=True / False: only that form is timed, and kept)
+        fold_ok = self.fold_possible(batch, tuned=False)
+        if fold is not None:
+            self.fold_choice[batch] = fold
+        results = {}
         for name, lins in self.projections().items():
             if names is not None and name not in names:
                 continue
-            timed = []                             # (us, tiling, swiglu, consumer flags)
-            modes = [False]
             if name == "gate_up":
                 self.swiglu_choice.pop(batch, None)
-                modes = [True, False] if self.fused_swiglu(batch) else [False]
-            for sw in modes:
-                act = name == "gate_up" and not sw
-                red = name == "qkv"                   # the qkv epilogue reads its partials
-                nrm = name in ("o", "down")           # ... K1 those of o and down
-                cands = candidates(batch, lins[0].N, lins[0].K, lins[0].fmt, swiglu=sw)
-                if red:
-                    # the fused K3 requests QKV_SPLITS_UP_FRONT split partials
-                    # with its first loads; each further split costs it a
-                    # round trip, which the timed reduction does not show
-                    cands = [c for c in cands if c.ksplit <= QKV_SPLITS_UP_FRONT] or cands
-                for c in cands:
-                    us = self.time_projection(lins, batch, c, swiglu=sw, with_act=act,
-                                              with_reduce=red, with_norm=nrm)
-                    if verbose:
-                        print(f"TUNE {name} M={batch} swiglu={sw} {tuple(c)} {us:.2f} us",
-                              flush=True)
-                    timed.append((us, c, sw, (act, red, nrm)))
-            # the closest few are timed again with more replays: single
-            # timings of a few microseconds differ by more than the candidates do
-            timed.sort(key=lambda t: t[0])
-            best = None
-            for _us, c, sw, (act, red, nrm) in timed[:RETIME_TOP]:
-                us = self.time_projection(lins, batch, c, reps=RETIME_REPS, swiglu=sw,
-                                          with_act=act, with_reduce=red, with_norm=nrm)
-                if best is None or us < best[0]:
-                    best = (us, c, sw)
-            if name == "gate_up" and len(modes) == 2:
-                self.swiglu_choice[batch] = best[2]
-            chosen[name] = best[1]
-            report[name] = {"tiling": tuple(best[1]), "us": round(best[0], 3),
-                            "bytes": lins[0].nbytes()}
+            modes = ((False, True) if fold is None else (fold,)) if fold_ok and name in FOLDED \
+                else (False,)
+            results[name] = {f: self._tune_one(name, lins, batch, f, verbose) for f in modes}
+        if fold is None and fold_ok and all(n in results for n in FOLDED):
+            plain = sum(results[n][False][0] for n in FOLDED)
+            folded = sum(results[n][True][0] for n in FOLDED)
+            self.fold_choice[batch] = folded < plain
+            report["fold"] = {"chosen": folded < plain, "plain_us": round(plain, 3),
+                              "folded_us": round(folded, 3)}
+        fold = self.fold_possible(batch)
+        for name, res in results.items():
+            us, c, sw = res[fold] if fold in res else res[False]
+            if name == "gate_up" and self.fused_swiglu_possible(batch):
+                self.swiglu_choice[batch] = sw
+            chosen[name] = c
+            report[name] = {"tiling": tuple(c), "us": round(us, 3),
+                            "bytes": self.projections()[name][0].nbytes()}
             if name == "gate_up":
-                report[name]["fused_swiglu"] = best[2]
+                report[name]["fused_swiglu"] = sw
         return report
+
+    def _tune_one(self, name: str, lins: list, batch: int, fold: bool,
+                  verbose: bool) -> tuple:
+        """(µs, tiling, swiglu) of the fastest candidate of one projection,
+        each timed with the work its form puts on the step (see
+        time_projection); fold times the folded forms."""
+        from acorninfer_amd.ops.quant_gemm import candidates
+        timed = []                             # (us, tiling, swiglu, consumer flags)
+        modes = [False]
+        if name == "gate_up" and self.fused_swiglu_possible(batch):
+            modes = [True, False]
+        for sw in modes:
+            act = name == "gate_up" and not sw
+            red = name == "qkv"                   # the qkv epilogue reads its partials
+            nrm = name in ("o", "down") and not fold   # ... K1 those of o and down
+            nin = fold and name in ("qkv", "gate_up")
+            rsd = fold and name in ("o", "down")
+            cands = candidates(batch, lins[0].N, lins[0].K, lins[0].fmt, swiglu=sw)
+            if nin or rsd:
+                # the folded forms are the direct kernels' (rt > 0); the
+                # residual epilogue runs in one split
+                cands = [c for c in cands if c.rt > 0 and (nin or c.ksplit == 1)]
+            if red:
+                # the fused K3 requests QKV_SPLITS_UP_FRONT split partials
+                # with its first loads; each further split costs it a
+                # round trip, which the timed reduction does not show
+                cands = [c for c in cands if c.ksplit <= QKV_SPLITS_UP_FRONT] or cands
+            for c in cands:
+                us = self.time_projection(lins, batch, c, swiglu=sw, with_act=act,
+                                          with_reduce=red, with_norm=nrm, norm_in=nin,
+                                          resid=rsd)
+                if verbose:
+                    print(f"TUNE {name} M={batch} swiglu={sw} fold={fold} {tuple(c)} "
+                          f"{us:.2f} us", flush=True)
+                timed.append((us, c, sw, (act, red, nrm, nin, rsd)))
+        # the closest few are timed again with more replays: single
+        # timings of a few microseconds differ by more than the candidates do
+        timed.sort(key=lambda t: t[0])
+        best = None
+        for _us, c, sw, (act, red, nrm, nin, rsd) in timed[:RETIME_TOP]:
+            us = self.time_projection(lins, batch, c, reps=RETIME_REPS, swiglu=sw,
+                                      with_act=act, with_reduce=red, with_norm=nrm,
+                                      norm_in=nin, resid=rsd)
+            if best is None or us < best[0]:
+                best = (us, c, sw)
+        return best
 
     # Reference-shaped entry point (qwen3.py:520-595).
     def forward_decode(self, input_ids: torch.Tensor, views, *, prepared=None) -> torch.Tensor:
@@ -933,6 +1063,7 @@ WIDE_UNIT_PAGES = 16       # ... and splits of this many pages over wider ones
 QKV_SPLITS_UP_FRONT = 4   # qkv split partials the fused K3 loads up front (kQB)
 RETIME_TOP = 4      # tune(): candidates timed a second time ...
 RETIME_REPS = 12    # ... with this many graph replays
+FOLDED = ("qkv", "o", "gate_up", "down")   # the projections the RMSNorms fold into
 
 
 def attention_splits(batch: int, kv_heads: int, max_pages: int, *,
@@ -1063,6 +1194,13 @@ class StepBuffers:
         self.part_gu = (None if self.swiglu and self.prefill else
                         z(self.cfgs["gate_up"].ksplit, B, 2 * inter, dtype=f32))
         self.part_down = None if self.direct else z(self.cfgs["down"].ksplit, B, H, dtype=f32)
+        # the RMSNorms folded into the projections (decode, block layouts, o
+        # and down in one split): the sums of squares of the residual after o
+        # (read by gate|up) and after down (read by the next layer's qkv)
+        self.fold = (not self.prefill and m.fold_possible(B)
+                     and self.cfgs["o"].ksplit == 1 and self.cfgs["down"].ksplit == 1)
+        self.ss_o = z(B, H // 16, dtype=f32) if self.fold else None
+        self.ss_dn = z(B, H // 16, dtype=f32) if self.fold else None
         ks_lm = self.cfgs["lm_head"].ksplit
         S = self.num_splits
         self.ws_acc = z(B * nq * S * D, dtype=f32) if S > 1 else None

@@ -149,14 +149,17 @@ def build_workload(cfg, fmt: str, batch: int, prompt_len: int, total_steps: int,
     if tilings is not None:
         # a fixed choice (e.g. an unprofiled run's, for a profiled one)
         from acorninfer_amd.ops.quant_gemm import Tiling
-        model.tilings[batch] = {k: Tiling(*v) for k, v in tilings.items() if k != "swiglu"}
+        model.tilings[batch] = {k: Tiling(*v) for k, v in tilings.items()
+                                if k not in ("swiglu", "fold")}
         model.swiglu_choice[batch] = bool(tilings.get("swiglu", True))
+        model.fold_choice[batch] = bool(tilings.get("fold", True))
         report = {k: {"tiling": tuple(v), "us": float("nan"), "bytes": 1}
                   for k, v in model.tilings[batch].items()}
     elif tune:
         t0 = time.perf_counter()
         report = model.tune(batch)
-        _log(f"tuned {fmt} C={batch} in {time.perf_counter() - t0:.1f} s")
+        _log(f"tuned {fmt} C={batch} in {time.perf_counter() - t0:.1f} s "
+             f"(fold {report.get('fold')})")
     P = 16
     lens = prompt_lens if prompt_lens is not None else [prompt_len] * batch
     max_len = max(lens) + total_steps + 1
@@ -296,29 +299,43 @@ def gemm_step_bytes(model, batch: int) -> int:
 
 def gemm_roofline(model, runner, batch: int, reps: int = 5):
     """Time one step's GEMM launches (hipGraph on a private stream, HIP events
-    on that stream). Returns (achieved GB/s, per-step bytes, per-step µs,
-    launches per step)."""
+    on that stream): the forms the step runs, the folded ones (normalise on
+    load, residual epilogue) where it folds the RMSNorms, on copies of the
+    residual and its sums. Returns (achieved GB/s, per-step bytes, per-step
+    µs, launches per step)."""
     import torch
     st = runner._state(batch)
     buf = st.buf
     s = torch.cuda.Stream()
     launches = []
     for lw in model.layers:
-        launches += [("qkv", lw.qkv, buf.normed, buf.part_qkv), ("o", lw.o, buf.attn, buf.part_o),
-                     ("gate_up", lw.gate_up, buf.normed, "swiglu" if buf.swiglu else buf.part_gu),
-                     ("down", lw.down, buf.act, buf.part_down)]
-    launches.append(("lm_head", model.lm_head, buf.normed, None))
+        launches += [("qkv", lw.qkv, buf.normed, buf.part_qkv, lw.input_norm),
+                     ("o", lw.o, buf.attn, buf.part_o, None),
+                     ("gate_up", lw.gate_up, buf.normed,
+                      "swiglu" if buf.swiglu else buf.part_gu, lw.post_norm),
+                     ("down", lw.down, buf.act, buf.part_down, None)]
+    launches.append(("lm_head", model.lm_head, buf.normed, None, None))
     nbytes = sum(_gemm_bytes(lin, batch) for _, lin, *_ in launches)
+    eps = float(model.cfg.rms_norm_eps)
+    if buf.fold:
+        res = buf.res.clone()
+        ss = buf.ss_dn.clone()
 
     def body():
         sp = s.cuda_stream
-        for name, lin, x, part in launches:
+        for name, lin, x, part, nw in launches:
+            c = buf.cfgs[name]
             if part is None:
-                lin.launch(x, batch, buf.cfgs[name], out=buf.logits, part=buf.ws_lm, stream=sp)
+                lin.launch(x, batch, c, out=buf.logits, part=buf.ws_lm, stream=sp)
+            elif buf.fold and nw is not None:
+                kw = {"act": buf.act} if isinstance(part, str) else {"part": part}
+                lin.launch_norm(res, batch, c, norm_w=nw, ss=ss, eps=eps, stream=sp, **kw)
+            elif buf.fold:
+                lin.launch_resid(x, batch, c, res=res, res_out=res, ss=ss, stream=sp)
             elif isinstance(part, str):
-                lin.launch_swiglu(x, batch, buf.cfgs[name], buf.act, sp)
+                lin.launch_swiglu(x, batch, c, buf.act, sp)
             else:
-                lin.launch(x, batch, buf.cfgs[name], part=part, stream=sp)
+                lin.launch(x, batch, c, part=part, stream=sp)
 
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -997,7 +1014,8 @@ def main() -> None:
         tune=not args.no_tune,
         tilings=json.loads(args.tilings) if args.tilings else None)
     tilings_arg = json.dumps({**{k: list(v) for k, v in model.tilings.get(args.batch, {}).items()},
-                              "swiglu": model.fused_swiglu(args.batch)}, separators=(",", ":"))
+                              "swiglu": model.fused_swiglu(args.batch),
+                              "fold": model.fold_possible(args.batch)}, separators=(",", ":"))
     _log(f"tilings of this run (--tilings): {tilings_arg}")
     _log(f"graph captured for C={args.batch}; warmup {args.warmup}, timed {args.steps}")
     dt, log = time_decode(runner, views, first, args.steps, args.warmup)
@@ -1020,7 +1038,8 @@ def main() -> None:
              "tilings_arg": tilings_arg,
              "tuned": {k: {"tiling": v["tiling"], "us": v["us"],
                            "GBps": round(v["bytes"] / v["us"] / 1e3, 1)}
-                       for k, v in model.tune_report.items()}}
+                       for k, v in model.tune_report.items() if k != "fold"},
+             "fold": model.tune_report.get("fold")}
     if not args.no_extra:
         # configuration 4's prompts: prefill of C x 512 random ids (TTFT of a batch)
         for c in (1, args.batch):
@@ -1052,7 +1071,10 @@ def main() -> None:
             dt2, _ = time_decode(r2, v2, f2, args.steps, args.warmup)
             extra[f"{fmt}_C{c}_tok_s"] = round(c * args.steps / dt2, 2)
             extra[f"{fmt}_C{c}_ms_per_step"] = round(dt2 * 1e3 / args.steps, 4)
-            _log(f"{fmt} C={c}: {c * args.steps / dt2:.1f} tok/s")
+            if m2.tune_report.get("fold"):
+                extra[f"{fmt}_C{c}_fold"] = m2.tune_report["fold"]
+            _log(f"{fmt} C={c}: {c * args.steps / dt2:.1f} tok/s "
+                 f"(fold {m2.tune_report.get('fold')})")
             if c == 8 and fmt != "bf16":
                 # the quantised formats' own GEMM roofline (the line's is bf16's)
                 g2, nb2, us2, nl2 = gemm_roofline(m2, r2, c)
@@ -1062,7 +1084,8 @@ def main() -> None:
                     "traffic": measured_traffic(fmt, c), "in_step": in_step_gemm(fmt, c, nb2),
                     "tilings_arg": json.dumps(
                         {**{k: list(v) for k, v in m2.tilings.get(c, {}).items()},
-                         "swiglu": m2.fused_swiglu(c)}, separators=(",", ":"))}
+                         "swiglu": m2.fused_swiglu(c), "fold": m2.fold_possible(c)},
+                        separators=(",", ":"))}
                 _log(f"{fmt} C=8 GEMM: {nb2 / 1e9:.3f} GB in {us2:.1f} us -> {g2:.0f} GB/s")
             del m2, c2, r2
             torch.cuda.empty_cache()
