@@ -63,7 +63,7 @@ _SIGNATURES = {
     "acorn_quant_gemm_swiglu": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp],
     "acorn_gemm_swiglu_plan": [_i64, _i64, _i64, _i32, _vp],
     "acorn_quant_gemm_norm": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _i32, _vp,
-                              _vp, _f32, _vp, _vp, _vp, _vp],
+                              _f32, _vp, _vp, _vp, _vp, _vp, _vp],
     "acorn_embedding": [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "acorn_silu_mul": [_vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _vp],
     "acorn_argmax": [_vp, _i64, _i64, _vp, _i32, _vp],

@@ -20,11 +20,13 @@
 //    results through LDS in fixed order at the end.
 //  * Split-K (ksplit > 1) writes fp32 partials [ksplit, M, N], summed in split
 //    order by the consumer (bitwise deterministic).
-//  * MODE 1 (NormIn): x is the residual; each lane computes its row's 1 / rms
-//    from the producer's per-16-column sums of squares (requested before the
-//    weights) and normalises every x operand on load. MODE 2 (ResidOut, one
-//    split, no SwiGLU): instead of y the epilogue stores the new residual
-//    bf16(res + bf16(y)) and each 16-row tile's sum of its squares per x row.
+//  * MODE 1 (NormIn): x is the residual times the norm weight; each lane
+//    computes its row's 1 / rms from the producer's per-16-column sums of
+//    squares (requested before the weights) and multiplies its results by it
+//    before the epilogue. MODE 2 (ResidOut, one split, no SwiGLU): instead of
+//    y the epilogue stores the new residual bf16(res + bf16(y)), its rows
+//    times the next norm's weight, and each 16-row tile's sum of squares per
+//    x row (the RMSNorm folded into the GEMMs, gemm_common.h).
 #include "gemm_common.h"
 
 using namespace acorn;
@@ -42,11 +44,10 @@ struct BfdArgs {
   ResidOut ro;    // MODE 2
 };
 
-template <int RT, int UPW, bool NORM>
+template <int RT, int UPW>
 struct BfdStage {
   u32x4 w[RT][UPW];          // block (tile rt, block u): this lane's 16 bytes
   u32x4 x[UPW];              // B operand of block u: x row lr, k 8 lg .. 8 lg + 7
-  u32x4 nw[NORM ? UPW : 1];  // MODE 1: the norm weights of those k
 };
 
 // Grid: x = tile groups of RG * RT 16-row tiles, y = ksplit; block RG * KW
@@ -70,14 +71,9 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
   const int ns = BW / UPW;                        // stages, a multiple of DEPTH
   const uint8_t* wb = a.w + ((size_t)tt * KB + kw0 / 32) * 1024 + lane * 16;
   const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 8 * lg;
-  const __bf16* nwb = NORM ? a.ni.w + kw0 + 8 * lg : nullptr;
-  auto load = [&](int s, BfdStage<RT, UPW, NORM>& r) {
+  auto load = [&](int s, BfdStage<RT, UPW>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) r.x[u] = *(const u32x4*)(xb + (s * UPW + u) * 32);
-    if constexpr (NORM) {
-#pragma unroll
-      for (int u = 0; u < UPW; ++u) r.nw[u] = *(const u32x4*)(nwb + (s * UPW + u) * 32);
-    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -88,7 +84,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
   // MODE 1: this row's 1 / rms, its sums requested ahead of the weights
   NormRegs nr;
   if constexpr (NORM) norm_issue(a.ni, min(lr, a.M - 1), lg, nr);
-  BfdStage<RT, UPW, NORM> ring[DEPTH];
+  BfdStage<RT, UPW> ring[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
   float inv = 1.f;
@@ -96,13 +92,11 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
   f32x4 acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](const BfdStage<RT, UPW, NORM>& r) {
+  auto compute = [&](const BfdStage<RT, UPW>& r) {
 #pragma unroll
-    for (int u = 0; u < UPW; ++u) {
-      const u32x4 xu = NORM ? norm_x8(r.x[u], r.nw[u], inv) : r.x[u];
+    for (int u = 0; u < UPW; ++u)
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) acc[rt] = mfma(r.w[rt][u], xu, acc[rt]);
-    }
+      for (int rt = 0; rt < RT; ++rt) acc[rt] = mfma(r.w[rt][u], r.x[u], acc[rt]);
   };
   int s0 = 0;
   for (; s0 + DEPTH < ns; s0 += DEPTH) {
@@ -135,6 +129,12 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
   if (!active || lr >= a.M) return;
 
   // lane (lr, lg) holds rows 4 lg .. 4 lg + 3 of each tile, column (x row) lr
+  if constexpr (NORM) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[rt][i] = acc[rt][i] * inv;
+  }
   if constexpr (SWIGLU) {
     // tiles 2p (gate) and 2p + 1 (up) hold the 16 outputs of block t0 / 2 + p
     const int NA = a.N / 2;
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
     for (int rt = 0; rt < RT; ++rt) {
       const int n = (t0 + rt) * 16 + 4 * lg;
       const float y[4] = {acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]};
-      float sq = resid_store4(a.ro, (size_t)lr * a.N + n, y);
+      float sq = resid_store4(a.ro, (size_t)lr * a.N + n, n, y);
       sq = sq + __shfl_xor(sq, 16);
       sq = sq + __shfl_xor(sq, 32);
       if (lg == 0) a.ro.ss[(size_t)lr * (a.N / 16) + t0 + rt] = sq;
@@ -315,12 +315,12 @@ int bf16b_launch(const DirectPlan& p, const void* x, const void* w, void* out, f
   if (p.ksplit > 1) out = nullptr;
   if (p.mode == 2) {
     // the residual epilogue: one split, no SwiGLU, complete 16-row tiles
-    if (!ro || !ro->res || !ro->res_out || !ro->ss) return ACORN_ERR_VALUE;
+    if (!ro || !ro->res || !ro->res_out || !ro->ss || !ro->nw || !ro->xw) return ACORN_ERR_VALUE;
     if (p.ksplit != 1 || p.swiglu) return ACORN_ERR_UNSUPPORTED;
   } else if (!out && (!part || p.swiglu)) {
     return ACORN_ERR_VALUE;
   }
-  if (p.mode == 1 && (!ni || !ni->w || !ni->ss || ni->nss * 16 != K)) return ACORN_ERR_VALUE;
+  if (p.mode == 1 && (!ni || !ni->ss || ni->nss * 16 != K)) return ACORN_ERR_VALUE;
   BfdArgs a{(const __bf16*)x, (const uint8_t*)w, (__bf16*)out, part, (int)M, (int)N,
             (int)K, (int)(K / p.ksplit), NormIn{}, ResidOut{}};
   if (ni) a.ni = *ni;

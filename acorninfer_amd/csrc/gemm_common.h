@@ -94,15 +94,18 @@ __device__ __forceinline__ float swiglu_bf16(float g, float u) {
 }
 
 // ---- the RMSNorm folded into the decode GEMMs (direct kernels) ------------
-// A producer projection (o, down) that finishes its columns in one launch
-// (one split) writes the new residual v = bf16(res + bf16(y)) and, per 16
-// columns of v, the fp32 sum of v^2 (ss [M][N / 16]); the consumer projection
-// (gate|up, the next layer's qkv) reads v as its x and normalises it on load,
-// bf16((v * inv) * w) with inv = 1 / sqrt(sum ss / cols + eps): K1's arithmetic
-// (rmsnorm.hip), with the sum of squares added in another order.
+// RMSNorm(v) @ W^T = inv * (bf16(v * w) @ W^T) per row (inv = 1 / rms(v), w
+// the norm weight), so the norm splits between the two projections around
+// it. A producer projection (o, down) that finishes its columns in one
+// launch (one split) writes the new residual v = bf16(res + bf16(y)), the
+// weighted rows xw = bf16(v * w) of the next norm and, per 16 columns of v,
+// the fp32 sum of v^2 (ss [M][N / 16]). The consumer projection (gate|up, the
+// next layer's qkv) is the plain GEMM of xw whose rows are multiplied by inv
+// = 1 / sqrt(sum ss / cols + eps) before its epilogue (K1's inv, rmsnorm.hip,
+// with the sum of squares added in another order; the bf16 rounding falls on
+// v * w instead of (v * inv) * w).
 struct NormIn {
-  const __bf16* w;       // norm weight [K]
-  const float* ss;       // [M][nss] per-16-column sums of squares of x
+  const float* ss;       // [M][nss] per-16-column sums of squares of the residual
   int nss;               // K / 16
   float eps;
 };
@@ -111,6 +114,8 @@ struct ResidOut {
   __bf16* res_out;       // [M, N] residual out (may alias res: each element is read and
                          // written by the same lane)
   float* ss;             // [M][N / 16]
+  const __bf16* nw;      // [N] the next norm's weight
+  __bf16* xw;            // [M, N] bf16(res_out * nw)
 };
 
 // Row m's 1 / rms from its nss partial sums, computed by the four lanes of lane
@@ -156,35 +161,28 @@ __device__ __forceinline__ float norm_finish(const NormIn& n, int m, int q, int 
   return 1.0f / sqrtf(s / (float)cols + n.eps);
 }
 
-// 8 bf16 of x (one MFMA operand) -> bf16((x * inv) * w), K1's rounding.
-__device__ __forceinline__ u32x4 norm_x8(u32x4 v, u32x4 w, float inv) {
-#pragma clang fp contract(off)
-  u32x4 r;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const float v0 = __uint_as_float(v[d] << 16), v1 = __uint_as_float(v[d] & 0xffff0000u);
-    const float w0 = __uint_as_float(w[d] << 16), w1 = __uint_as_float(w[d] & 0xffff0000u);
-    r[d] = pack_bf16x2((v0 * inv) * w0, (v1 * inv) * w1);
-  }
-  return r;
-}
-
 // The producer's epilogue for the 4 columns n .. n + 3 of row m held by one
-// lane (y fp32): v = bf16(res + bf16(y)) stored to res_out; returns their sum
-// of squares in column order.
-__device__ __forceinline__ float resid_store4(const ResidOut& r, size_t off, const float (&y)[4]) {
+// lane (y fp32, off = m N + n): v = bf16(res + bf16(y)) stored to res_out and
+// bf16(v * w) to xw; returns their sum of squares in column order.
+__device__ __forceinline__ float resid_store4(const ResidOut& r, size_t off, int n,
+                                              const float (&y)[4]) {
 #pragma clang fp contract(off)
-  uint32_t rin[2];
+  uint32_t rin[2], win[2];
   __builtin_memcpy(rin, r.res + off, sizeof(rin));
-  float v[4];
+  __builtin_memcpy(win, r.nw + n, sizeof(win));
+  float v[4], vw[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float rv = __uint_as_float(i & 1 ? rin[i / 2] & 0xffff0000u : rin[i / 2] << 16);
+    const float wv = __uint_as_float(i & 1 ? win[i / 2] & 0xffff0000u : win[i / 2] << 16);
     const float yb = (float)(__bf16)y[i];
     v[i] = (float)(__bf16)(rv + yb);
+    vw[i] = v[i] * wv;
   }
   const uint32_t o[2] = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
   __builtin_memcpy(r.res_out + off, o, sizeof(o));
+  const uint32_t ow[2] = {pack_bf16x2(vw[0], vw[1]), pack_bf16x2(vw[2], vw[3])};
+  __builtin_memcpy(r.xw + off, ow, sizeof(ow));
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) s = s + v[i] * v[i];
@@ -272,7 +270,7 @@ struct DirectPlan {
   int rt, upw, nw_field, rg, kw, ksplit, depth;
   int groups;      // workgroups along N
   bool swiglu;
-  int mode;        // 0 plain, 1 x normalised on load (NormIn), 2 residual epilogue (ResidOut)
+  int mode;        // 0 plain, 1 rows scaled by 1 / rms (NormIn), 2 residual epilogue (ResidOut)
 };
 int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, DirectPlan* p);
 // out (bf16 [M,N], or act [M,N/2] for swiglu) when given and ksplit == 1;

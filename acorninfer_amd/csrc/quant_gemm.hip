@@ -1367,21 +1367,21 @@ extern "C" int acorn_quant_gemm_swiglu(const void* x, const void* w, const void*
 extern "C" int acorn_quant_gemm_norm(const void* x, const void* w, const void* scale,
                                      void* out_bf16, float* part, int64_t M, int64_t N,
                                      int64_t K, int wfmt, const int* cfg, int swiglu,
-                                     const void* norm_w, const float* ss_in, float eps,
-                                     const void* res, void* res_out, float* ss_out,
-                                     void* stream) {
+                                     const float* ss_in, float eps, const void* res,
+                                     void* res_out, float* ss_out, const void* norm_w,
+                                     void* xw_out, void* stream) {
   if (wfmt != ACORN_WFMT_BF16B && wfmt != ACORN_WFMT_W8B && wfmt != ACORN_WFMT_W4B)
     return ACORN_ERR_DTYPE;
   if (M < 0 || N <= 0 || K <= 0 || N % 16 || K % 16) return ACORN_ERR_SHAPE;
   if (M == 0) return ACORN_OK;
-  const bool norm = norm_w != nullptr, resid = res != nullptr;
+  const bool norm = ss_in != nullptr, resid = res != nullptr;
   if (norm == resid) return ACORN_ERR_VALUE;                 // exactly one of the two
   if (resid && swiglu) return ACORN_ERR_UNSUPPORTED;
-  if (norm && !ss_in) return ACORN_ERR_VALUE;
-  if (resid && (!res_out || !ss_out)) return ACORN_ERR_VALUE;
+  if (resid && (!res_out || !ss_out || !norm_w || !xw_out)) return ACORN_ERR_VALUE;
   if (swiglu && !out_bf16) return ACORN_ERR_VALUE;
-  const NormIn ni{(const __bf16*)norm_w, ss_in, (int)(K / 16), eps};
-  const ResidOut ro{(const __bf16*)res, (__bf16*)res_out, ss_out};
+  const NormIn ni{ss_in, (int)(K / 16), eps};
+  const ResidOut ro{(const __bf16*)res, (__bf16*)res_out, ss_out, (const __bf16*)norm_w,
+                    (__bf16*)xw_out};
   return gemm_entry(x, w, scale, nullptr, out_bf16, part, M, N, K, wfmt, cfg, swiglu != 0,
                     (hipStream_t)stream, norm ? &ni : nullptr, resid ? &ro : nullptr);
 }

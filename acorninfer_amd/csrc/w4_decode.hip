@@ -47,16 +47,15 @@ struct W4dArgs {
   float* part;    // fp32 [ksplit, M, N] otherwise
   int M, N, K;
   int kr;         // K range of a split (a multiple of 128 * UPW * DEPTH)
-  NormIn ni;      // MODE 1: x is the residual, normalised on load (gemm_common.h)
+  NormIn ni;      // MODE 1: results scaled by the rows' 1 / rms (gemm_common.h)
   ResidOut ro;    // MODE 2: the residual epilogue (gemm_common.h)
 };
 
-template <int RT, int UPW, bool NORM>
+template <int RT, int UPW>
 struct DStage {
   u32x4 w[RT][UPW];          // unit (rt, u): this lane's 16 bytes of block (tile, group)
   u32x4 x[UPW][4];           // B operand of MFMA j of group u: x row lr, k 32 lg + 8 j ..
   uint32_t s[RT][2 * UPW];   // fp16 scales: half 4u + i is row 4 lg + i of group u
-  u32x4 nw[NORM ? UPW : 1][4];   // MODE 1: the norm weights of those k
 };
 
 // bf16 -136 in every slot: an MFMA of it against x gives -136 X per column
@@ -88,19 +87,11 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
   const uint8_t* wb = a.w + ((size_t)tt * G + g0) * 1024 + lane * 16;
   const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 32 * lg;
   const _Float16* sb = a.scale + (size_t)tt * G4 * 64 + lg * 16;
-  const __bf16* nwb = NORM ? a.ni.w + kw0 + 32 * lg : nullptr;
-  auto load = [&](int s, DStage<RT, UPW, NORM>& r) {
+  auto load = [&](int s, DStage<RT, UPW>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u)
 #pragma unroll
       for (int j = 0; j < 4; ++j) r.x[u][j] = *(const u32x4*)(xb + (s * UPW + u) * 128 + 8 * j);
-    if constexpr (NORM) {
-#pragma unroll
-      for (int u = 0; u < UPW; ++u)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          r.nw[u][j] = *(const u32x4*)(nwb + (s * UPW + u) * 128 + 8 * j);
-    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -114,7 +105,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
 
   NormRegs nr;
   if constexpr (NORM) norm_issue(a.ni, min(lr, a.M - 1), lg, nr);
-  DStage<RT, UPW, NORM> ring[DEPTH];
+  DStage<RT, UPW> ring[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
   float inv = 1.f;
@@ -123,12 +114,10 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const u32x4 neg136 = {kNeg136x2, kNeg136x2, kNeg136x2, kNeg136x2};
-  auto compute = [&](const DStage<RT, UPW, NORM>& r) {
+  auto compute = [&](const DStage<RT, UPW>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
-      u32x4 xu[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xu[j] = NORM ? norm_x8(r.x[u][j], r.nw[u][j], inv) : r.x[u][j];
+      const u32x4 (&xu)[4] = r.x[u];
       f32x4 xb136 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < 4; ++j) xb136 = mfma(neg136, xu[j], xb136);
@@ -176,6 +165,12 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
   if (!active || lr >= a.M) return;
 
   // lane (lr, lg) holds rows 4 lg .. 4 lg + 3 of each tile, column (x row) lr
+  if constexpr (NORM) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[rt][i] = acc[rt][i] * inv;
+  }
   if constexpr (SWIGLU) {
     // tiles 2p (gate) and 2p + 1 (up) hold the 16 outputs of block t0 / 2 + p
     const int NA = a.N / 2;
@@ -195,7 +190,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
     for (int rt = 0; rt < RT; ++rt) {
       const int n = (t0 + rt) * 16 + 4 * lg;
       const float y[4] = {acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]};
-      float sq = resid_store4(a.ro, (size_t)lr * a.N + n, y);
+      float sq = resid_store4(a.ro, (size_t)lr * a.N + n, n, y);
       sq = sq + __shfl_xor(sq, 16);
       sq = sq + __shfl_xor(sq, 32);
       if (lg == 0) a.ro.ss[(size_t)lr * (a.N / 16) + t0 + rt] = sq;
@@ -876,12 +871,12 @@ int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale
   if (p.ksplit > 1) out = nullptr;
   if (p.mode != 0 && !p.direct) return ACORN_ERR_UNSUPPORTED;
   if (p.mode == 2) {
-    if (!ro || !ro->res || !ro->res_out || !ro->ss) return ACORN_ERR_VALUE;
+    if (!ro || !ro->res || !ro->res_out || !ro->ss || !ro->nw || !ro->xw) return ACORN_ERR_VALUE;
     if (p.ksplit != 1 || p.swiglu) return ACORN_ERR_UNSUPPORTED;
   } else if (!out && (!part || p.swiglu)) {
     return ACORN_ERR_VALUE;
   }
-  if (p.mode == 1 && (!ni || !ni->w || !ni->ss || ni->nss * 16 != K)) return ACORN_ERR_VALUE;
+  if (p.mode == 1 && (!ni || !ni->ss || ni->nss * 16 != K)) return ACORN_ERR_VALUE;
   int rc = ACORN_ERR_UNSUPPORTED;
   if (p.direct) {
     if (M > 16) return ACORN_ERR_UNSUPPORTED;

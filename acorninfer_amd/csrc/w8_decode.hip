@@ -22,8 +22,9 @@
 //    their results through LDS in fixed order at the end.
 //  * Split-K (ksplit > 1) writes scaled fp32 partials [ksplit, M, N], summed
 //    in split order by the consumer (bitwise deterministic).
-//  * MODE 1 / 2: the RMSNorm folded in as in bf16_decode.hip (x normalised on
-//    load; the residual epilogue with its sums of squares).
+//  * MODE 1 / 2: the RMSNorm folded in as in bf16_decode.hip (results scaled
+//    by the rows' 1 / rms, after the per-channel scale; the residual epilogue
+//    with the weighted rows and the sums of squares).
 #include "gemm_common.h"
 
 using namespace acorn;
@@ -42,11 +43,10 @@ struct W8dArgs {
   ResidOut ro;    // MODE 2
 };
 
-template <int RT, int UPW, bool NORM>
+template <int RT, int UPW>
 struct W8Stage {
   u32x4 w[RT][UPW];          // block (tile rt, block u): this lane's 16 bytes
   u32x4 x[UPW][2];           // B operand of MFMA j of block u: x row lr, k 16 lg + 8 j ..
-  u32x4 nw[NORM ? UPW : 1][2];   // MODE 1: the norm weights of those k
 };
 
 // bf16 -128 in every slot: an MFMA of it against x gives -128 X per column
@@ -83,19 +83,11 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
   const int ns = BW / UPW;                        // stages, a multiple of DEPTH
   const uint8_t* wb = a.w + ((size_t)tt * KB + kw0 / 64) * 1024 + lane * 16;
   const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 16 * lg;
-  const __bf16* nwb = NORM ? a.ni.w + kw0 + 16 * lg : nullptr;
-  auto load = [&](int s, W8Stage<RT, UPW, NORM>& r) {
+  auto load = [&](int s, W8Stage<RT, UPW>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u)
 #pragma unroll
       for (int j = 0; j < 2; ++j) r.x[u][j] = *(const u32x4*)(xb + (s * UPW + u) * 64 + 8 * j);
-    if constexpr (NORM) {
-#pragma unroll
-      for (int u = 0; u < UPW; ++u)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          r.nw[u][j] = *(const u32x4*)(nwb + (s * UPW + u) * 64 + 8 * j);
-    }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -105,7 +97,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
 
   NormRegs nr;
   if constexpr (NORM) norm_issue(a.ni, min(lr, a.M - 1), lg, nr);
-  W8Stage<RT, UPW, NORM> ring[DEPTH];
+  W8Stage<RT, UPW> ring[DEPTH];
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
   float inv = 1.f;
@@ -115,12 +107,10 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
   f32x4 xacc = {0.f, 0.f, 0.f, 0.f};             // -128 X over the wave's K range
   const u32x4 neg128 = {kNeg128x2, kNeg128x2, kNeg128x2, kNeg128x2};
-  auto compute = [&](const W8Stage<RT, UPW, NORM>& r) {
+  auto compute = [&](const W8Stage<RT, UPW>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
-      u32x4 xu[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) xu[j] = NORM ? norm_x8(r.x[u][j], r.nw[u][j], inv) : r.x[u][j];
+      const u32x4 (&xu)[2] = r.x[u];
 #pragma unroll
       for (int j = 0; j < 2; ++j) xacc = mfma(neg128, xu[j], xacc);
 #pragma unroll
@@ -178,6 +168,12 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
     for (int i = 0; i < 4; ++i)
       y[rt][i] = (float)__builtin_bit_cast(h16x2, sd[i / 2])[i & 1] * acc[rt][i];
   }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[rt][i] = y[rt][i] * inv;
+  }
   if constexpr (SWIGLU) {
     // tiles 2p (gate) and 2p + 1 (up) hold the 16 outputs of block t0 / 2 + p
     const int NA = a.N / 2;
@@ -196,7 +192,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int n = (t0 + rt) * 16 + 4 * lg;
-      float sq = resid_store4(a.ro, (size_t)lr * a.N + n, y[rt]);
+      float sq = resid_store4(a.ro, (size_t)lr * a.N + n, n, y[rt]);
       sq = sq + __shfl_xor(sq, 16);
       sq = sq + __shfl_xor(sq, 32);
       if (lg == 0) a.ro.ss[(size_t)lr * (a.N / 16) + t0 + rt] = sq;
@@ -350,12 +346,12 @@ int w8b_launch(const DirectPlan& p, const void* x, const void* w, const void* sc
   if (M < 1 || M > 16) return ACORN_ERR_UNSUPPORTED;
   if (p.ksplit > 1) out = nullptr;
   if (p.mode == 2) {
-    if (!ro || !ro->res || !ro->res_out || !ro->ss) return ACORN_ERR_VALUE;
+    if (!ro || !ro->res || !ro->res_out || !ro->ss || !ro->nw || !ro->xw) return ACORN_ERR_VALUE;
     if (p.ksplit != 1 || p.swiglu) return ACORN_ERR_UNSUPPORTED;
   } else if (!out && (!part || p.swiglu)) {
     return ACORN_ERR_VALUE;
   }
-  if (p.mode == 1 && (!ni || !ni->w || !ni->ss || ni->nss * 16 != K)) return ACORN_ERR_VALUE;
+  if (p.mode == 1 && (!ni || !ni->ss || ni->nss * 16 != K)) return ACORN_ERR_VALUE;
   W8dArgs a{(const __bf16*)x, (const uint8_t*)w, (const _Float16*)scale, (__bf16*)out,
             part, (int)M, (int)N, (int)K, (int)(K / p.ksplit), NormIn{}, ResidOut{}};
   if (ni) a.ni = *ni;

@@ -254,31 +254,35 @@ class QLinear:
         decode kernels on the block layouts, M <= 16)."""
         return self.fmt in (WFMT_BF16B, WFMT_W8B, WFMT_W4B) and M <= 16 and self.K % 16 == 0
 
-    def launch_norm(self, x: torch.Tensor, M: int, tiling, *, norm_w: torch.Tensor,
-                    ss: torch.Tensor, eps: float, stream: int, out: torch.Tensor | None = None,
+    def launch_norm(self, x: torch.Tensor, M: int, tiling, *, ss: torch.Tensor, eps: float,
+                    stream: int, out: torch.Tensor | None = None,
                     part: torch.Tensor | None = None, act: torch.Tensor | None = None) -> None:
-        """The projection of the normalised residual: x is the residual [M, K]
-        and each row is used as bf16((x * inv) * norm_w), inv from the
-        producer's per-16-column sums of squares ss [M, K/16] (K1's
-        arithmetic, acorninfer/ops/rmsnorm.py:39-82). Output as launch (act
-        given: the fused SwiGLU of launch_swiglu)."""
+        """The projection of the normalised residual: x is a launch_resid
+        producer's weighted rows bf16(v * norm_w) [M, K], and every result of
+        row m is multiplied by inv = 1 / rms(v) from the producer's
+        per-16-column sums of squares ss [M, K/16] before it is stored (the
+        RMSNorm of acorninfer/ops/rmsnorm.py:39-82 split around the GEMM).
+        Output as launch (act given: the fused SwiGLU of launch_swiglu)."""
         arr = (ctypes.c_int * 6)(*tiling, 0)
         rc = lib().acorn_quant_gemm_norm(
             ptr(x), ptr(self.w), ptr(self.scale), ptr(act if act is not None else out), ptr(part),
-            M, self.N, self.K, self.fmt, arr, int(act is not None), ptr(norm_w), ptr(ss),
-            float(eps), None, None, None, stream)
+            M, self.N, self.K, self.fmt, arr, int(act is not None), ptr(ss), float(eps),
+            None, None, None, None, None, stream)
         check(rc, "quant_gemm_norm")
 
     def launch_resid(self, x: torch.Tensor, M: int, tiling, *, res: torch.Tensor,
-                     res_out: torch.Tensor, ss: torch.Tensor, stream: int) -> None:
+                     res_out: torch.Tensor, ss: torch.Tensor, norm_w: torch.Tensor,
+                     xw: torch.Tensor, stream: int) -> None:
         """The projection whose output goes into the residual stream: stores
-        res_out = bf16(res + bf16(x @ W^T)) (res_out may be res) and the
-        per-16-column sums of squares ss [M, N/16] a launch_norm consumer
-        reads, in place of K1's residual add (one split only)."""
+        res_out = v = bf16(res + bf16(x @ W^T)) (res_out may be res), the rows
+        xw = bf16(v * norm_w) weighted by the next RMSNorm's weight, and the
+        per-16-column sums of squares ss [M, N/16] of v: what a launch_norm
+        consumer reads, in place of K1's residual add and norm (one split
+        only)."""
         arr = (ctypes.c_int * 6)(*tiling, 0)
         rc = lib().acorn_quant_gemm_norm(
             ptr(x), ptr(self.w), ptr(self.scale), None, None, M, self.N, self.K, self.fmt, arr,
-            0, None, None, 0.0, ptr(res), ptr(res_out), ptr(ss), stream)
+            0, None, 0.0, ptr(res), ptr(res_out), ptr(ss), ptr(norm_w), ptr(xw), stream)
         check(rc, "quant_gemm_resid")
 
     def swiglu_plan(self, M: int, tiling=None, workspace: bool = False):
@@ -551,9 +555,10 @@ class Qwen3DecodeModel:
             cq = buf.cfgs["qkv"]
             if buf.fold and li > 0:
                 # the input norm folded into qkv: the previous down stored the
-                # residual and its sums of squares
-                lw.qkv.launch_norm(buf.res, B, cq, norm_w=lw.input_norm, ss=buf.ss_dn, eps=eps,
-                                   stream=st, out=y_qkv, part=buf.part_qkv)
+                # residual, its rows times this norm's weight and its sums of
+                # squares
+                lw.qkv.launch_norm(buf.normed, B, cq, ss=buf.ss_dn, eps=eps, stream=st,
+                                   out=y_qkv, part=buf.part_qkv)
             else:
                 # K1: input norm (layer 0 from the embedding; later layers reduce
                 # the previous down projection's output and add the residual)
@@ -596,13 +601,13 @@ class Qwen3DecodeModel:
             cg = buf.cfgs["gate_up"]
             if buf.fold:
                 lw.o.launch_resid(buf.attn, B, co, res=buf.res, res_out=buf.res, ss=buf.ss_o,
-                                  stream=st)
+                                  norm_w=lw.post_norm, xw=buf.normed, stream=st)
                 if buf.swiglu:
-                    lw.gate_up.launch_norm(buf.res, B, cg, norm_w=lw.post_norm, ss=buf.ss_o,
-                                           eps=eps, stream=st, act=buf.act)
+                    lw.gate_up.launch_norm(buf.normed, B, cg, ss=buf.ss_o, eps=eps, stream=st,
+                                           act=buf.act)
                 else:
-                    lw.gate_up.launch_norm(buf.res, B, cg, norm_w=lw.post_norm, ss=buf.ss_o,
-                                           eps=eps, stream=st, part=buf.part_gu)
+                    lw.gate_up.launch_norm(buf.normed, B, cg, ss=buf.ss_o, eps=eps, stream=st,
+                                           part=buf.part_gu)
             else:
                 lw.o.launch(buf.attn, B, co, out=y_o, part=buf.part_o, wtmp=buf.wtmp, stream=st)
                 k1(False, y_o, buf.part_o, co.ksplit, lw.post_norm)
@@ -619,7 +624,8 @@ class Qwen3DecodeModel:
             if buf.fold and li < last:
                 # the next layer's input norm folded into its qkv
                 lw.down.launch_resid(buf.act, B, cd, res=buf.res, res_out=buf.res,
-                                     ss=buf.ss_dn, stream=st)
+                                     ss=buf.ss_dn, norm_w=self.layers[li + 1].input_norm,
+                                     xw=buf.normed, stream=st)
             else:
                 lw.down.launch(buf.act, B, cd, out=y_down, part=buf.part_down, wtmp=buf.wtmp,
                                stream=st)
@@ -712,8 +718,9 @@ class Qwen3DecodeModel:
             nw = torch.ones(lin0.N, dtype=self.norm.dtype, device=self.device)
             ss_out = torch.empty(M, lin0.N // 16, dtype=torch.float32, device=self.device)
         if norm_in:
-            nw_in = torch.ones(lin0.K, dtype=self.norm.dtype, device=self.device)
             ss_in = torch.full((M, lin0.K // 16), 16.0, dtype=torch.float32, device=self.device)
+        if resid:
+            xw = torch.empty(M, lin0.N, dtype=self.dtype, device=self.device)
         eps = float(self.cfg.rms_norm_eps)
         s = torch.cuda.Stream(self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
@@ -721,17 +728,17 @@ class Qwen3DecodeModel:
             def body():
                 for lin in lins:
                     if resid:
-                        lin.launch_resid(x, M, t, res=res, res_out=res, ss=ss_out,
-                                         stream=s.cuda_stream)
+                        lin.launch_resid(x, M, t, res=res, res_out=res, ss=ss_out, norm_w=nw,
+                                         xw=xw, stream=s.cuda_stream)
                     elif norm_in and swiglu:
-                        lin.launch_norm(x, M, t, norm_w=nw_in, ss=ss_in, eps=eps,
-                                        stream=s.cuda_stream, act=act)
+                        lin.launch_norm(x, M, t, ss=ss_in, eps=eps, stream=s.cuda_stream,
+                                        act=act)
                     elif swiglu:
                         lin.launch_swiglu(x, M, t, act, s.cuda_stream, wtmp=wtmp)
                     else:
                         if norm_in:
-                            lin.launch_norm(x, M, t, norm_w=nw_in, ss=ss_in, eps=eps,
-                                            stream=s.cuda_stream, part=part)
+                            lin.launch_norm(x, M, t, ss=ss_in, eps=eps, stream=s.cuda_stream,
+                                            part=part)
                         else:
                             lin.launch(x, M, t, part=part, wtmp=wtmp, stream=s.cuda_stream)
                         if with_act:   # the separate activation the fused form saves

@@ -319,6 +319,7 @@ def gemm_roofline(model, runner, batch: int, reps: int = 5):
     eps = float(model.cfg.rms_norm_eps)
     if buf.fold:
         res = buf.res.clone()
+        xw = buf.normed.clone()
         ss = buf.ss_dn.clone()
 
     def body():
@@ -329,9 +330,10 @@ def gemm_roofline(model, runner, batch: int, reps: int = 5):
                 lin.launch(x, batch, c, out=buf.logits, part=buf.ws_lm, stream=sp)
             elif buf.fold and nw is not None:
                 kw = {"act": buf.act} if isinstance(part, str) else {"part": part}
-                lin.launch_norm(res, batch, c, norm_w=nw, ss=ss, eps=eps, stream=sp, **kw)
+                lin.launch_norm(xw, batch, c, ss=ss, eps=eps, stream=sp, **kw)
             elif buf.fold:
-                lin.launch_resid(x, batch, c, res=res, res_out=res, ss=ss, stream=sp)
+                lin.launch_resid(x, batch, c, res=res, res_out=res, ss=ss,
+                                 norm_w=model.layers[0].input_norm, xw=xw, stream=sp)
             elif isinstance(part, str):
                 lin.launch_swiglu(x, batch, c, buf.act, sp)
             else:

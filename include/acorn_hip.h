@@ -289,26 +289,31 @@ int acorn_quant_gemm_swiglu(const void* x, const void* w, const void* scale, con
  * sits between two projections folded in, so that the step needs no K1
  * launch there. Replaces the pair acorn_quant_gemm + acorn_fused_add_rmsnorm
  * (acorninfer/ops/rmsnorm.py:39-82 after a projection, models/qwen3.py:
- * 412-439) split across the producer and the consumer projection:
+ * 412-439) split across the producer and the consumer projection, from
+ * RMSNorm(v) @ W^T = inv * (bf16(v * norm_w) @ W^T) per row:
  *   producer (res != NULL; ksplit 1, swiglu 0): instead of y the launch
  *       stores the new residual res_out[m, n] = bf16(res[m, n] + bf16(y[m, n]))
- *       (res_out may be res) and ss_out[m][n / 16] = the fp32 sum of
+ *       (res_out may be res), the weighted rows xw_out[m, n] =
+ *       bf16(res_out[m, n] * norm_w[n]) (norm_w [N]: the next RMSNorm's
+ *       weight) and ss_out[m][n / 16] = the fp32 sum of
  *       res_out[m, 16t .. 16t + 15]^2 per 16 columns t; out_bf16 and part are
  *       unused;
- *   consumer (norm_w != NULL): x is the residual [M, K]; each x row is used
- *       as bf16((x * inv) * norm_w) with inv = 1 / sqrt(sum_t ss_in[m][t] / K
- *       + eps), ss_in [M][K / 16] the producer's sums: K1's arithmetic, its sum
- *       of squares added in another order (so within rounding of K1, not
- *       bitwise). The output is as acorn_quant_gemm's (or the SwiGLU act with
- *       swiglu != 0).
- * Exactly one of norm_w, res is given. cfg as for acorn_quant_gemm (the
+ *   consumer (ss_in != NULL): x is the producer's xw_out [M, K]; every result
+ *       of row m (each split's partial, or the values the SwiGLU act is made
+ *       of) is multiplied by inv = 1 / sqrt(sum_t ss_in[m][t] / K + eps) before
+ *       it is stored, ss_in [M][K / 16] the producer's sums: K1's inv with its
+ *       sum of squares added in another order, and the bf16 rounding of the
+ *       normalised row on v * norm_w instead of (v * inv) * norm_w (so within
+ *       rounding of the K1 pair, not bitwise). The output is as
+ *       acorn_quant_gemm's (or the SwiGLU act with swiglu != 0).
+ * Exactly one of ss_in, res is given. cfg as for acorn_quant_gemm (the
  * direct kernels' tilings); other tilings return ACORN_ERR_UNSUPPORTED.
  */
 int acorn_quant_gemm_norm(const void* x, const void* w, const void* scale, void* out_bf16,
                           float* part, int64_t M, int64_t N, int64_t K, int wfmt,
-                          const int* cfg, int swiglu, const void* norm_w, const float* ss_in,
-                          float eps, const void* res, void* res_out, float* ss_out,
-                          void* stream);
+                          const int* cfg, int swiglu, const float* ss_in, float eps,
+                          const void* res, void* res_out, float* ss_out, const void* norm_w,
+                          void* xw_out, void* stream);
 
 /* Tiling of acorn_quant_gemm_swiglu, as acorn_gemm_plan. */
 int acorn_gemm_swiglu_plan(int64_t M, int64_t N, int64_t K, int wfmt, int* cfg);

@@ -1,17 +1,21 @@
-"""The RMSNorm folded into the decode GEMMs (acorn_quant_gemm_norm): the
-producer form against the plain launch followed by K1's residual add, the
-consumer form against the plain launch on rows normalised with K1's formula
-(rmsnorm.py:39-82, oracle/ops_ref.fused_add_rmsnorm_ref for the formula), and
-the decode step with the fold against the step with K1 launches.
+"""The RMSNorm folded into the decode GEMMs (acorn_quant_gemm_norm), from
+RMSNorm(v) @ W^T = inv * (bf16(v * w) @ W^T) per row: the producer form
+against the plain launch followed by K1's residual add, the consumer form
+against the plain launch on the weighted rows, and the decode step with the
+fold against the step with K1 launches (rmsnorm.py:39-82, and
+oracle/ops_ref.fused_add_rmsnorm_ref for the formula).
 
-- producer (o, down; one split): res_out must be bf16(res + bf16(y)) bit for bit,
-  y the plain launch's own output on the same tiling (the same accumulation
-  order), and ss_out the fp32 sums of squares of res_out per 16 columns;
-- consumer (qkv, gate|up): given the producer's sums, every row is used as
-  bf16((x * inv) * w); inv is restated here in the kernel's order of
-  additions (each quarter of a row's sums in order, then pairwise), so the
-  output must equal the plain launch on those normalised rows bit for bit;
-  inv itself is within 1e-6 of K1's float64 value;
+- producer (o, down; one split): res_out must be v = bf16(res + bf16(y)) bit
+  for bit, y the plain launch's own output on the same tiling (the same
+  accumulation order), xw = bf16(v * w_next) bit for bit, and ss_out the fp32
+  sums of squares of v per 16 columns;
+- consumer (qkv, gate|up): given xw and the producer's sums, every result of
+  row m is the plain launch's on xw times inv, inv restated here in the
+  kernel's order of additions (each quarter of a row's sums in order, then
+  pairwise): bitwise for the fp32 partials, within one bf16 ulp per rounding
+  for the fused SwiGLU (its silu goes through the device expf); inv itself is
+  within 1e-6 of K1's float64 value, and the result is within bf16 rounding
+  of the plain launch on K1's normalised rows bf16((v * inv) * w);
 - the step: the bf16 and W4A16 models tuned with the fold against the same
   models with it switched off (K1 launches), greedy tokens equal where the
   top-2 margin clears the gate, logits within the bf16 tolerance.
@@ -23,7 +27,7 @@ import pytest
 import torch
 
 from acorninfer_amd import _lib
-from tolerances import rel_err
+from tolerances import rel_err, ulp_distance
 
 SHAPES = {"o": (4096, 4096), "down": (4096, 12288), "qkv": (6144, 4096),
           "gate_up": (24576, 4096)}
@@ -72,6 +76,7 @@ def test_producer_residual_and_sums(fmt, m, cls):
     g = torch.Generator().manual_seed(11 + m)
     x = torch.randn(m, k, generator=g).bfloat16().cuda()
     res = torch.randn(m, n, generator=g).bfloat16().cuda()
+    nw = (1.0 + 0.1 * torch.randn(n, generator=g)).bfloat16().cuda()
     st = _lib.stream_ptr()
     tilings = _direct_tilings(lin, m, one_split=True)
     assert len(tilings) >= 4
@@ -79,17 +84,20 @@ def test_producer_residual_and_sums(fmt, m, cls):
         y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         lin.launch(x, m, t, out=y, part=torch.empty(1, m, n, device="cuda"), stream=st)
         res_out = torch.full_like(res, float("nan"))
+        xw = torch.full_like(res, float("nan"))
         ss = torch.full((m, n // 16), float("nan"), device="cuda")
-        lin.launch_resid(x, m, t, res=res, res_out=res_out, ss=ss, stream=st)
+        lin.launch_resid(x, m, t, res=res, res_out=res_out, ss=ss, norm_w=nw, xw=xw, stream=st)
         torch.cuda.synchronize()
         want = (res.float() + y.float()).bfloat16()
         assert torch.equal(res_out.view(torch.int16), want.view(torch.int16)), tuple(t)
+        want_xw = (want.float() * nw.float()).bfloat16()
+        assert torch.equal(xw.view(torch.int16), want_xw.view(torch.int16)), tuple(t)
         sq = want.float().view(m, n // 16, 16).pow(2).sum(-1)
         torch.testing.assert_close(ss, sq, rtol=1e-6, atol=0)
     # in place (res_out = res), as the step runs it
     t = tilings[0]
     r2 = res.clone()
-    lin.launch_resid(x, m, t, res=r2, res_out=r2, ss=ss, stream=st)
+    lin.launch_resid(x, m, t, res=r2, res_out=r2, ss=ss, norm_w=nw, xw=xw, stream=st)
     y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
     lin.launch(x, m, t, out=y, part=torch.empty(1, m, n, device="cuda"), stream=st)
     torch.cuda.synchronize()
@@ -97,60 +105,93 @@ def test_producer_residual_and_sums(fmt, m, cls):
     print(f"\n[fold producer {fmt} {cls} M={m}: {len(tilings)} tilings bitwise]")
 
 
+def _swiglu_ref(part: torch.Tensor, inv: torch.Tensor) -> torch.Tensor:
+    """The fused SwiGLU epilogue on one-split results [M, N] of interleaved
+    gate|up rows (16-row blocks: gate, up, gate, ...), each row scaled by inv
+    first: bf16(bf16(silu(bf16 g)) * bf16 u), the kernels' roundings."""
+    m, n = part.shape
+    v = (part * inv[:, None]).view(m, n // 32, 2, 16)
+    gb = v[:, :, 0].bfloat16().float()
+    ub = v[:, :, 1].bfloat16().float()
+    sg = (gb / (1.0 + torch.exp(-gb))).bfloat16().float()
+    return (sg * ub).bfloat16().reshape(m, n // 2)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("fmt", list(FMTS))
 @pytest.mark.parametrize("m", [1, 5, 8, 16])
 @pytest.mark.parametrize("cls", ["qkv", "gate_up"])
-def test_consumer_normalises_on_load(fmt, m, cls):
+def test_consumer_scales_rows_by_inv(fmt, m, cls):
     n, k = SHAPES[cls]
     lin = _lin(fmt, n, k, 5 + m)
     if cls == "gate_up":
         lin = lin.interleaved()
     g = torch.Generator().manual_seed(21 + m)
-    x = torch.randn(m, k, generator=g).bfloat16()              # the residual rows
+    v = torch.randn(m, k, generator=g).bfloat16()              # the residual rows
     nw = (1.0 + 0.1 * torch.randn(k, generator=g)).bfloat16()
     eps = 1e-6
-    ss = x.float().view(m, k // 16, 16).pow(2).sum(-1)         # a producer's sums
+    ss = v.float().view(m, k // 16, 16).pow(2).sum(-1)         # a producer's sums
+    xw = (v.float() * nw.float()).bfloat16()                   # ... and weighted rows
     inv = _inv_kernel_order(ss.numpy(), k, eps)
     # K1's value of inv (float64) is within 1e-6
-    ref = 1.0 / np.sqrt(x.double().pow(2).mean(-1).numpy() + eps)
+    ref = 1.0 / np.sqrt(v.double().pow(2).mean(-1).numpy() + eps)
     assert np.allclose(inv, ref, rtol=1e-6)
-    xn = ((x.float() * torch.from_numpy(inv)[:, None]) * nw.float()).bfloat16().cuda()
-    xd, nwd, ssd = x.cuda(), nw.cuda(), ss.cuda()
+    invd = torch.from_numpy(inv).cuda()
+    xn = ((v.float() * torch.from_numpy(inv)[:, None]) * nw.float()).bfloat16().cuda()
+    xwd, ssd = xw.cuda(), ss.cuda()
     st = _lib.stream_ptr()
     for swiglu in ((False, True) if cls == "gate_up" else (False,)):
         tilings = _direct_tilings(lin, m, swiglu=swiglu)
         assert len(tilings) >= 4
         for t in tilings:
             if swiglu:
-                a = torch.empty(m, n // 2, dtype=torch.bfloat16, device="cuda")
-                b = torch.empty_like(a)
-                lin.launch_swiglu(xn, m, t, a, st)
-                lin.launch_norm(xd, m, t, norm_w=nwd, ss=ssd, eps=eps, stream=st, act=b)
+                p1 = torch.empty(1, m, n, device="cuda")
+                lin.launch(xwd, m, t, part=p1, stream=st)
+                b = torch.empty(m, n // 2, dtype=torch.bfloat16, device="cuda")
+                lin.launch_norm(xwd, m, t, ss=ssd, eps=eps, stream=st, act=b)
+                torch.cuda.synchronize()
+                want = _swiglu_ref(p1[0], invd)
+                d = ulp_distance(b, want)
+                assert int(d.max()) <= 2 and float((d > 0).float().mean()) < 0.01, tuple(t)
+                k1 = torch.empty_like(b)
+                lin.launch_swiglu(xn, m, t, k1, st)
             else:
                 a = torch.empty(t.ksplit, m, n, device="cuda")
                 b = torch.full_like(a, float("nan"))
-                lin.launch(xn, m, t, part=a, stream=st)
-                lin.launch_norm(xd, m, t, norm_w=nwd, ss=ssd, eps=eps, stream=st, part=b)
+                lin.launch(xwd, m, t, part=a, stream=st)
+                lin.launch_norm(xwd, m, t, ss=ssd, eps=eps, stream=st, part=b)
+                torch.cuda.synchronize()
+                assert torch.equal(b, a * invd[None, :, None]), (tuple(t), swiglu)
+                k1 = torch.empty_like(a)
+                lin.launch(xn, m, t, part=k1, stream=st)
             torch.cuda.synchronize()
-            assert torch.equal(a, b), (tuple(t), swiglu)
-        print(f"\n[fold consumer {fmt} {cls} M={m} swiglu={swiglu}: {len(tilings)} tilings bitwise]")
+            # the K1 pair (norm, then the plain launch) within bf16 rounding
+            r = rel_err(b.float().sum(0) if b.dim() == 3 else b.float(),
+                        k1.float().sum(0) if k1.dim() == 3 else k1.float())
+            assert r < 1e-2, (tuple(t), swiglu, r)
+        print(f"\n[fold consumer {fmt} {cls} M={m} swiglu={swiglu}: {len(tilings)} tilings]")
 
 
 def test_fold_entry_rejects_bad_requests():
-    """Exactly one of the two forms; the residual form needs one split and no
-    SwiGLU; natural layouts are refused (the direct kernels read blocks)."""
+    """Exactly one of the two forms; the residual form needs its four outputs,
+    one split and no SwiGLU; natural layouts are refused (the direct kernels
+    read blocks)."""
     L = _lib.lib()
     arr = (ctypes.c_int * 6)()
-    rc = L.acorn_quant_gemm_norm(None, None, None, None, None, 8, 4096, 4096, _lib.WFMT_BF16B,
-                                 arr, 0, None, None, 1e-6, None, None, None, None)
-    assert rc == _lib.ERR_VALUE                       # neither form
-    rc = L.acorn_quant_gemm_norm(None, None, None, None, None, 8, 4096, 4096, _lib.WFMT_BF16,
-                                 arr, 0, 1, 1, 1e-6, None, None, None, None)
-    assert rc == _lib.ERR_DTYPE                       # natural rows
-    rc = L.acorn_quant_gemm_norm(None, None, None, None, None, 8, 4096, 4096, _lib.WFMT_W8B,
-                                 arr, 1, None, None, 1e-6, 1, 1, 1, None)
-    assert rc == _lib.ERR_UNSUPPORTED                 # residual form with SwiGLU
+    args = dict(x=None, w=None, scale=None, out=None, part=None, M=8, N=4096, K=4096,
+                wfmt=_lib.WFMT_BF16B, cfg=arr, swiglu=0, ss_in=None, eps=1e-6, res=None,
+                res_out=None, ss_out=None, norm_w=None, xw=None, stream=None)
+
+    def call(**kw):
+        return L.acorn_quant_gemm_norm(*{**args, **kw}.values())
+    assert call() == _lib.ERR_VALUE                                    # neither form
+    assert call(ss_in=1, res=1, res_out=1, ss_out=1, norm_w=1, xw=1) == _lib.ERR_VALUE  # both
+    assert call(wfmt=_lib.WFMT_BF16, ss_in=1) == _lib.ERR_DTYPE        # natural rows
+    assert call(wfmt=_lib.WFMT_W8B, swiglu=1, res=1, res_out=1, ss_out=1, norm_w=1,
+                xw=1) == _lib.ERR_UNSUPPORTED                          # residual with SwiGLU
+    assert call(res=1, res_out=1, ss_out=1, norm_w=1) == _lib.ERR_VALUE   # no xw
+    assert call(res=1, res_out=1, ss_out=1, xw=1) == _lib.ERR_VALUE       # no norm weight
+    assert call(M=8, N=4008, ss_in=1) == _lib.ERR_SHAPE
 
 
 @pytest.mark.gpu
