@@ -70,6 +70,11 @@ __device__ __forceinline__ void load_dwords(const void* p, uint32_t (&d)[NDW]) {
 // wait for that load there (and, as loads complete in order, for every load
 // before it): a register ring of weight and scale loads then never has more
 // than one stage in flight. h must fold to a constant.
+// The compiler inserts no wait states ahead of an asm statement: v must not be
+// an MFMA result read straight from its destination VGPRs. In the int4 direct
+// kernels the accumulators live in AGPRs, and the v_accvgpr_read that brings v
+// over carries the wait; a build that keeps them in VGPRs (a 512-thread launch
+// bound did) reads stale values here.
 template <int NDW>
 __device__ __forceinline__ float fma_half(const uint32_t (&d)[NDW], int h, float v, float acc) {
   float r;

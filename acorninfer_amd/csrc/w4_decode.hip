@@ -614,9 +614,10 @@ int launch_direct(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
 }
 
 // wave layouts (the nw field): 1 or 4 waves on their own rows, or 10 nw + kw
-// with kw waves splitting K over one row group (22, 44). Two row groups of
-// four K slices (84) gave wrong results in every instance on gfx950 while 44
-// was right; it is not built.
+// with kw waves splitting K over one row group (22, 44). No layout has eight
+// waves: under a 512-thread launch bound the compiler keeps the MFMA
+// accumulators in VGPRs, and fma_half's asm then reads them without the wait
+// states an MFMA result needs (gemm_common.h), so 84 and 88 computed garbage.
 template <int RT, int UPW, int DEPTH>
 int direct_nw(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
   switch (p.nw_field) {
