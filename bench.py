@@ -60,6 +60,18 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def _release() -> None:
+    """Drop the tensors nothing refers to any more, keeping their memory in
+    torch's cache rather than handing it back to the driver: memory a process
+    gets from the driver again after freeing it streamed ~5% slower in the
+    decode step on this part (bf16 C=8 3.28 against 3.13 ms, every model built
+    after the first) than its first allocations or blocks torch's cache hands
+    out again (3.13-3.14 ms), so every leg after the first reuses the cache.
+    torch still empties the cache itself when an allocation would fail."""
+    import gc
+    gc.collect()
+
+
 def _gemm_bytes(lin, M: int) -> int:
     """Algorithmic bytes of one projection launch: weights (+ scales) once,
     activations in and bf16 results out."""
@@ -502,7 +514,7 @@ def attention_benchmarks(seed: int, attn_splits: list[int] | None = None) -> dic
                                    "frac": round(nb / us5 / 1e3 / HBM_PEAK_GBS, 4), "splits": S5,
                                    "mean_ctx": round(float(clens.float().mean()), 1)}
         del kp5, vp5, acc5, ml5
-        torch.cuda.empty_cache()
+        _release()
     out.update(prefill_attention_benchmarks(seed))
     return out
 
@@ -558,7 +570,7 @@ def prefill_attention_benchmarks(seed: int) -> dict:
             "frac_mfma": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
             "k3_rows_us": round(us_rows, 1), "speedup_vs_k3_rows": round(us_rows / us, 2)}
         del kp, vp, acc, ml
-        torch.cuda.empty_cache()
+        _release()
     return out
 
 
@@ -642,7 +654,7 @@ def dense_gemm_benchmarks(seed: int) -> dict:
                 "frac_mfma": round(fl / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
                 "hipblaslt_us": round(us_lib, 1)}
             del x, w, wb, part
-    torch.cuda.empty_cache()
+    _release()
     return out
 
 
@@ -711,7 +723,7 @@ def gemm_benchmarks(seed: int, gemm_ms=(1, 8, 64, 256), fixed: dict | None = Non
                     "frac_mfma": round(flops / best[0] / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
                     "tiling": ",".join(map(str, t))}
             del lins
-            torch.cuda.empty_cache()
+            _release()
     return out
 
 
@@ -864,7 +876,7 @@ def gpu_config1(seed: int = 20261027, new_tokens: int = 32, prompt_len: int = 32
                 alloc.free(blk)
         out[f"config1_{tag}_tok_s"] = round(new_tokens / times[-1], 2)
         del model, runner, cache
-        torch.cuda.empty_cache()
+        _release()
     return out
 
 
@@ -1058,15 +1070,15 @@ def main() -> None:
         _log(f"bf16 prefill 1 x 8192: {ms_p:.2f} ms ({tps:.0f} tok/s)")
         model._extend_buf = None
         # configuration 4 end to end through the Engine (prefill + decode)
-        del cache, runner
-        torch.cuda.empty_cache()
+        del cache, runner, views
+        _release()
         e2e, ttft = engine_benchmark(model, cfg, args.batch, args.prompt_len, 256, args.seed + 9)
         extra[f"bf16_engine_C{args.batch}_tok_s"] = round(e2e, 1)
         extra[f"bf16_engine_C{args.batch}_ttft_ms"] = round(ttft, 2)
         _log(f"bf16 engine C={args.batch}, {args.prompt_len} + 256 tokens: {e2e:.1f} tok/s "
              f"end to end, TTFT {ttft:.1f} ms")
         del model
-        torch.cuda.empty_cache()
+        _release()
         for fmt, c in (("bf16", 1), ("w4a16", 8), ("w4a16", 1), ("w8a16", 8)):
             m2, c2, r2, v2, f2 = build_workload(cfg, fmt, c, args.prompt_len, total, args.seed,
                                                 tune=not args.no_tune)
@@ -1089,8 +1101,8 @@ def main() -> None:
                          "swiglu": m2.fused_swiglu(c), "fold": m2.fold_possible(c)},
                         separators=(",", ":"))}
                 _log(f"{fmt} C=8 GEMM: {nb2 / 1e9:.3f} GB in {us2:.1f} us -> {g2:.0f} GB/s")
-            del m2, c2, r2
-            torch.cuda.empty_cache()
+            del m2, c2, r2, v2, f2
+            _release()
         # configuration 4's largest concurrency: C=32, bf16, prompts of 512
         m2, c2, r2, v2, f2 = build_workload(cfg, "bf16", 32, args.prompt_len, total, args.seed,
                                             tune=not args.no_tune)
@@ -1098,8 +1110,8 @@ def main() -> None:
         extra["bf16_C32_tok_s"] = round(32 * args.steps / dt2, 2)
         extra["bf16_C32_ms_per_step"] = round(dt2 * 1e3 / args.steps, 4)
         _log(f"bf16 C=32: {32 * args.steps / dt2:.1f} tok/s")
-        del m2, c2, r2
-        torch.cuda.empty_cache()
+        del m2, c2, r2, v2, f2
+        _release()
         # configuration 5: W4A16, prompts U[1024, 8192], sampled, C=8 and C=64
         from acorninfer_amd.sampler import SamplingParams
         for c in (8, 64):
@@ -1117,8 +1129,8 @@ def main() -> None:
             if c == 64:
                 # configuration 5 end to end through the Engine: the same 64
                 # prompt lengths prefilled, then 128 sampled tokens each
-                del c2, r2
-                torch.cuda.empty_cache()
+                del c2, r2, v2, f2
+                _release()
                 e2e, ttft = engine_benchmark(m2, cfg, c, plens, 128, args.seed + 11,
                                              sampling=SamplingParams(temperature=0.6, top_p=0.95,
                                                                      top_k=20),
@@ -1128,14 +1140,14 @@ def main() -> None:
                 _log(f"w4a16 engine C=64, prompts U[1024, 8192] + 128 sampled tokens: "
                      f"{e2e:.1f} tok/s end to end, mean TTFT {ttft:.0f} ms")
                 del m2
-                torch.cuda.empty_cache()
+                _release()
                 continue
             if c == 8:
                 # configuration 5's longest prompt in W4A16: one 8192-token
                 # prefill, int4 projections dequantised onto the bf16 kernel
                 # ("own") and on the int4 kernels themselves
-                del c2, r2
-                torch.cuda.empty_cache()
+                del c2, r2, v2, f2
+                _release()
                 for how in ("own", "int4"):
                     m2.prefill_gemm = how
                     ms_p, tps = prefill_benchmark(m2, cfg, 1, 8192, args.seed + 8, reps=2)
@@ -1145,10 +1157,10 @@ def main() -> None:
                     _log(f"w4a16 prefill 1 x 8192 ({how}): {ms_p:.2f} ms ({tps:.0f} tok/s)")
                 m2._extend_buf = None
                 del m2
-                torch.cuda.empty_cache()
+                _release()
                 continue
-            del m2, c2, r2
-            torch.cuda.empty_cache()
+            del m2, c2, r2, v2, f2
+            _release()
     if not args.no_kernels:
         t0 = time.perf_counter()
         extra["kernels"] = kernel_benchmarks()
