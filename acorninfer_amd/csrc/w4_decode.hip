@@ -446,6 +446,7 @@ struct W4mArgs {
 
 constexpr int kMidBM = 64;                      // columns (x rows) per workgroup
 constexpr int kMidMB = kMidBM / 16;
+constexpr int kMidXP = kMidBM + 1;              // LDS pitch of one k piece (16-byte slots)
 
 template <int RT, int NW, int DEPTH>
 __global__ __launch_bounds__(NW * kWave, 1) void w4b_mid_kernel(W4mArgs a) {
@@ -453,8 +454,8 @@ __global__ __launch_bounds__(NW * kWave, 1) void w4b_mid_kernel(W4mArgs a) {
   constexpr int XPT = kMidBM * 16 / NT;          // x pieces per thread per group
   static_assert(XPT >= 1 && kMidBM * 16 % NT == 0, "whole x pieces per thread");
   extern __shared__ __align__(16) unsigned char smem[];
-  u32x4* xs = (u32x4*)smem;                      // [2][16 pieces][64 rows]
-  float* xsum = (float*)(smem + 2 * 16 * kMidBM * 16);   // [2][64]
+  u32x4* xs = (u32x4*)smem;                      // [2][16 pieces][kMidXP rows]
+  float* xsum = (float*)(smem + 2 * 16 * kMidXP * 16);   // [2][64]
   const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lg = lane >> 4, lr = lane & 15;
   int tile, split, mblk;
@@ -485,15 +486,18 @@ __global__ __launch_bounds__(NW * kWave, 1) void w4b_mid_kernel(W4mArgs a) {
     u32x4 w[RT];
     uint32_t s[RT][2];
   };
-  // piece p of a group: k piece p / 64 (8 k), x row p % 64 (rows past M
-  // re-read row M - 1; their columns are never stored)
+  // piece p of a group: x row p / 16, k piece p % 16 (8 k), so that a
+  // wave's load covers 4 rows x 256 contiguous bytes (rows past M re-read row
+  // M - 1; their columns are never stored); it goes to LDS slot
+  // piece * kMidXP + row, whose pad makes the stores and the MFMA operand
+  // reads (16 lanes: 16 consecutive rows of one piece) free of bank conflicts
   auto load = [&](int c, Slot& sl) {
     const int g = gbase + min(c, nch - 1);
 #pragma unroll
     for (int u = 0; u < XPT; ++u) {
       const int p = (int)threadIdx.x + NT * u;
-      const int m = min(m0 + p % kMidBM, a.M - 1);
-      sl.x[u] = *(const u32x4*)(a.x + (size_t)m * a.K + g * 128 + (p / kMidBM) * 8);
+      const int m = min(m0 + p / 16, a.M - 1);
+      sl.x[u] = *(const u32x4*)(a.x + (size_t)m * a.K + g * 128 + (p % 16) * 8);
     }
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -512,14 +516,17 @@ __global__ __launch_bounds__(NW * kWave, 1) void w4b_mid_kernel(W4mArgs a) {
 
   auto group = [&](int c, const Slot& sl) {
     const int b = c & 1;
-    u32x4* xb = xs + b * 16 * kMidBM;
+    u32x4* xb = xs + b * 16 * kMidXP;
 #pragma unroll
-    for (int u = 0; u < XPT; ++u) xb[threadIdx.x + NT * u] = sl.x[u];
+    for (int u = 0; u < XPT; ++u) {
+      const int p = (int)threadIdx.x + NT * u;
+      xb[(p % 16) * kMidXP + p / 16] = sl.x[u];
+    }
     __syncthreads();
     if (wid < kMidMB) {
       f32x4 xg = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xg = mfma(ones, xb[(4 * lg + j) * kMidBM + wid * 16 + lr], xg);
+      for (int j = 0; j < 4; ++j) xg = mfma(ones, xb[(4 * lg + j) * kMidXP + wid * 16 + lr], xg);
       if (lg == 0) xsum[b * kMidBM + wid * 16 + lr] = xg[0];
     }
     __syncthreads();
@@ -532,7 +539,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void w4b_mid_kernel(W4mArgs a) {
     for (int mb = 0; mb < kMidMB; ++mb) {
       u32x4 bx[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bx[j] = xb[(4 * lg + j) * kMidBM + mb * 16 + lr];
+      for (int j = 0; j < 4; ++j) bx[j] = xb[(4 * lg + j) * kMidXP + mb * 16 + lr];
       const float xg = xsum[b * kMidBM + mb * 16 + lr];
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
@@ -905,8 +912,8 @@ int w4b_launch(const W4bPlan& p, const void* x, const void* w, const void* scale
 }
 
 // Knobs: rt (16-row tiles per wave) 1 or 2, nw (waves) 4 or 8, ksplit, depth
-// (groups in flight) 2 or 4, except rt 2 with 8 waves and depth 4 (its
-// registers spill); N must be a whole number of NW * RT * 16 row
+// (groups in flight) 2 or 4, and 8 for rt 1 with 8 waves (rt 2 with 8 waves
+// and depth 8 spills its registers); N must be a whole number of NW * RT * 16 row
 // blocks, K of 128-k groups, and each split's group count of depth rounds. With
 // ksplit 0 the split grows from 1 while the launch has fewer workgroups than
 // 256 (two rounds of CUs at most) and each split keeps 4 depth rounds.
@@ -917,8 +924,8 @@ int w4m_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, W4mPlan* p) {
   const int nw = cfg && cfg[2] > 0 ? cfg[2] : 8;
   const int req_ks = cfg ? cfg[3] : 0;
   const int depth = cfg && cfg[4] > 0 ? cfg[4] : 2;
-  if ((rt != 1 && rt != 2) || (nw != 4 && nw != 8) || (depth != 2 && depth != 4) ||
-      (rt == 2 && nw == 8 && depth == 4))
+  if ((rt != 1 && rt != 2) || (nw != 4 && nw != 8) ||
+      (depth != 2 && depth != 4 && !(depth == 8 && rt == 1 && nw == 8)))
     return ACORN_ERR_UNSUPPORTED;
   const int64_t rows = (int64_t)nw * rt * 16;
   if (N % rows) return ACORN_ERR_UNSUPPORTED;
@@ -946,7 +953,7 @@ int w4m_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, W4mPlan* p) {
   p->depth = depth;
   p->groups = (int)groups;
   p->mblocks = (int)mblocks;
-  p->lds = (size_t)2 * 16 * kMidBM * 16 + (size_t)2 * kMidBM * 4;
+  p->lds = (size_t)2 * 16 * kMidXP * 16 + (size_t)2 * kMidBM * 4;
   return ACORN_OK;
 }
 
@@ -973,7 +980,9 @@ int w4m_launch(const W4mPlan& p, const void* x, const void* w, const void* scale
     case 184: rc = launch_mid<1, 8, 4>(p, a, st); break;
     case 242: rc = launch_mid<2, 4, 2>(p, a, st); break;
     case 244: rc = launch_mid<2, 4, 4>(p, a, st); break;
+    case 188: rc = launch_mid<1, 8, 8>(p, a, st); break;
     case 282: rc = launch_mid<2, 8, 2>(p, a, st); break;
+    case 284: rc = launch_mid<2, 8, 4>(p, a, st); break;
   }
   if (rc) return rc;
   ACORN_LAUNCH_CHECK();

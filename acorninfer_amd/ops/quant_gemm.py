@@ -339,7 +339,7 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
             reqs = _w4b_wide_requests()           # the int4 kernel with 2 or 4 x blocks
         if wfmt == WFMT_W4B:
             reqs += [Tiling(MID_RT, rt, nw, ks, depth)   # the mid-M int4 kernel
-                     for rt in (1, 2) for nw in (4, 8) for depth in (2, 4)
+                     for rt in (1, 2) for nw in (4, 8) for depth in (2, 4, 8)
                      for ks in (0, 1, 2, 4, 8, 16)]
         for bm in (32, 64, 128):
             for bn in (64, 128):
