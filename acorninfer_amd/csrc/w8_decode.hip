@@ -247,7 +247,7 @@ int by_layout(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
 
 // registers of one stage (dwords per lane): weights and x operands
 constexpr int stage_dwords(int rt, int upw) { return 4 * rt * upw + 8 * upw; }
-constexpr int kRingDwords = 160;   // the ring's budget (depth x stage)
+constexpr int kRingDwords = 192;   // the ring's budget (depth x stage)
 
 template <int RT, int UPW>
 int by_depth(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
@@ -256,6 +256,9 @@ int by_depth(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
     case 2: return by_layout<RT, UPW, 2>(p, a, st);
     case 4:
       if constexpr (4 * stage_dwords(RT, UPW) <= kRingDwords) return by_layout<RT, UPW, 4>(p, a, st);
+      break;
+    case 8:
+      if constexpr (8 * stage_dwords(RT, UPW) <= kRingDwords) return by_layout<RT, UPW, 8>(p, a, st);
       break;
   }
   return ACORN_ERR_UNSUPPORTED;
@@ -303,7 +306,7 @@ int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   if (upw != 1 && upw != 2) return ACORN_ERR_UNSUPPORTED;
   if (nwf != 1 && nwf != 4 && nwf != 22 && nwf != 44) return ACORN_ERR_UNSUPPORTED;
   const int nw = nwf < 10 ? nwf : nwf / 10, kw = nwf < 10 ? 1 : nwf % 10;
-  if (depth != 1 && depth != 2 && depth != 4) return ACORN_ERR_UNSUPPORTED;
+  if (depth != 1 && depth != 2 && depth != 4 && depth != 8) return ACORN_ERR_UNSUPPORTED;
   while (depth > 1 && (depth * stage_dwords(rt, upw) > kRingDwords || KB % (kw * upw * depth)))
     depth /= 2;
   if (KB % (kw * upw * depth)) return ACORN_ERR_SHAPE;

@@ -370,12 +370,12 @@ def _w4b_requests(swiglu: bool) -> list[Tiling]:
 
 def _w8b_requests(swiglu: bool) -> list[Tiling]:
     """Requests covering the int8 direct kernel's knobs (M <= 16): 1, 2 or 4
-    row tiles per wave, one or two 64-k blocks per stage with 2 or 4 stages in
+    row tiles per wave, one or two 64-k blocks per stage with 2 to 8 stages in
     flight, the same wave layouts as the int4 kernel (1, 4, 22, 44), and split
     counts from one to sixteen (the fused SwiGLU runs in one split)."""
     reqs = []
     for rt in ((2, 4) if swiglu else (1, 2, 4)):
-        for upw, depth in ((1, 4), (2, 2), (2, 4)):
+        for upw, depth in ((1, 4), (1, 8), (2, 2), (2, 4), (2, 8)):
             for nw in (1, 4, 22, 44):
                 for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
                     reqs.append(Tiling(rt, upw, nw, ks, depth))

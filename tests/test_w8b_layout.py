@@ -74,13 +74,13 @@ def test_planner_w8b_decode(M, N, K):
     """The default tiling, and every requested one the planner accepts, obey
     the int8 decode kernel's contract: rt in {1,2,4} dividing N/16, upw in
     {1,2}, a wave layout of 1 or 4 waves on their own rows or 10 nw + kw (22,
-    44), depth in {1,2,4} within the register ring's budget (stage = 4 rt
+    44), depth in {1,2,4,8} within the register ring's budget (stage = 4 rt
     upw + 8 upw dwords), and each wave's K range holding a whole number of
     depth-stage rounds of 64-k blocks."""
     lib = _lib.lib()
     reqs = [(0, 0, 0, 0, 0), (4, 1, 1, 0, 4), (1, 2, 4, 3, 2), (2, 2, 4, 5, 4), (2, 1, 1, 1, 4),
             (4, 2, 1, 2, 4), (1, 1, 4, 16, 1), (2, 1, 2, 0, 4), (1, 4, 1, 0, 2), (2, 1, 44, 1, 4),
-            (2, 2, 84, 2, 2), (4, 1, 22, 0, 4)]
+            (2, 2, 84, 2, 2), (4, 1, 22, 0, 4), (1, 2, 44, 1, 8), (2, 1, 1, 0, 8)]
     for r in reqs:
         cfg = (ctypes.c_int * 6)(*r, 0)
         rc = lib.acorn_gemm_plan(M, N, K, _lib.WFMT_W8B, cfg)
@@ -92,8 +92,8 @@ def test_planner_w8b_decode(M, N, K):
         kw = 1 if nwf < 10 else nwf % 10
         assert nwf in (1, 4, 22, 44)
         assert rt in (1, 2, 4) and (N // 16) % rt == 0
-        assert upw in (1, 2) and depth in (1, 2, 4)
-        assert depth * (4 * rt * upw + 8 * upw) <= 160
+        assert upw in (1, 2) and depth in (1, 2, 4, 8)
+        assert depth * (4 * rt * upw + 8 * upw) <= 192
         blocks = K // 64
         assert blocks % (ks * kw) == 0 and (blocks // ks // kw) % (upw * depth) == 0
         if r[3] == 0:
