@@ -263,6 +263,9 @@ class QLinear:
         per-16-column sums of squares ss [M, K/16] before it is stored (the
         RMSNorm of acorninfer/ops/rmsnorm.py:39-82 split around the GEMM).
         Output as launch (act given: the fused SwiGLU of launch_swiglu)."""
+        assert x.dtype == torch.bfloat16 and x.is_contiguous() and tuple(x.shape) == (M, self.K)
+        assert ss.dtype == torch.float32 and ss.is_contiguous() and \
+            tuple(ss.shape) == (M, self.K // 16), "sums of squares are [M, K/16] fp32"
         arr = (ctypes.c_int * 6)(*tiling, 0)
         rc = lib().acorn_quant_gemm_norm(
             ptr(x), ptr(self.w), ptr(self.scale), ptr(act if act is not None else out), ptr(part),
@@ -279,6 +282,12 @@ class QLinear:
         per-16-column sums of squares ss [M, N/16] of v: what a launch_norm
         consumer reads, in place of K1's residual add and norm (one split
         only)."""
+        for t in (res, res_out, xw):
+            assert t.dtype == torch.bfloat16 and t.is_contiguous() and \
+                tuple(t.shape) == (M, self.N), "res, res_out, xw are [M, N] bf16"
+        assert ss.dtype == torch.float32 and ss.is_contiguous() and \
+            tuple(ss.shape) == (M, self.N // 16), "sums of squares are [M, N/16] fp32"
+        assert norm_w.dtype == torch.bfloat16 and tuple(norm_w.shape) == (self.N,)
         arr = (ctypes.c_int * 6)(*tiling, 0)
         rc = lib().acorn_quant_gemm_norm(
             ptr(x), ptr(self.w), ptr(self.scale), None, None, M, self.N, self.K, self.fmt, arr,
