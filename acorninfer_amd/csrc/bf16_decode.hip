@@ -85,8 +85,13 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
   NormRegs nr;
   if constexpr (NORM) norm_issue(a.ni, min(lr, a.M - 1), lg, nr);
   BfdStage<RT, UPW> ring[DEPTH];
+  // in stage order, as the loop reissues them (the loop's static waits assume
+  // that order; left free, the scheduler reorders the first stages' loads)
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+  for (int d = 0; d < DEPTH; ++d) {
+    load(d, ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   float inv = 1.f;
   if constexpr (NORM) inv = norm_finish(a.ni, min(lr, a.M - 1), lg, a.K, nr);
   f32x4 acc[RT];

@@ -64,27 +64,17 @@ __device__ __forceinline__ void load_dwords(const void* p, uint32_t (&d)[NDW]) {
 }
 
 // s_h * v + acc in fp32, s_h the fp16 number h of a run of packed halves
-// (exactly converted): one v_fma_mix_f32 that selects the half of the packed
-// dword itself. It is asm because the compiler, left to convert the half,
-// shifts the high halves out right where their load is issued, which makes it
-// wait for that load there (and, as loads complete in order, for every load
-// before it): a register ring of weight and scale loads then never has more
-// than one stage in flight. h must fold to a constant.
-// The compiler inserts no wait states ahead of an asm statement: v must not be
-// an MFMA result read straight from its destination VGPRs. In the int4 direct
-// kernels the accumulators live in AGPRs, and the v_accvgpr_read that brings v
-// over carries the wait; a build that keeps them in VGPRs (a 512-thread launch
-// bound did) reads stale values here.
+// (exactly converted, one rounding): the compiler makes it one v_fma_mix_f32
+// that selects the half of the packed dword itself (op_sel), so no shift
+// touches a loaded scale before its use. h must fold to a constant. Plain
+// code rather than asm: the compiler then puts in the wait states an MFMA
+// result needs before a VALU reads it, wherever the accumulators live (VGPRs
+// under a 512-thread launch bound, AGPRs otherwise).
 template <int NDW>
 __device__ __forceinline__ float fma_half(const uint32_t (&d)[NDW], int h, float v, float acc) {
-  float r;
-  if (h & 1)
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-        : "=v"(r) : "v"(d[h / 2]), "v"(v), "v"(acc));
-  else
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]"
-        : "=v"(r) : "v"(d[h / 2]), "v"(v), "v"(acc));
-  return r;
+  const uint32_t w = d[h / 2];
+  const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)((h & 1) ? (w >> 16) : (w & 0xffffu)));
+  return __builtin_fmaf((float)s, v, acc);
 }
 
 // SwiGLU epilogue of the fused gate|up projection: g, u rounded to bf16,

@@ -106,8 +106,15 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
   NormRegs nr;
   if constexpr (NORM) norm_issue(a.ni, min(lr, a.M - 1), lg, nr);
   DStage<RT, UPW> ring[DEPTH];
+  // The first stages are issued in stage order, as the loop reissues them.
+  // Left free, the scheduler moves every stage's scale load after the last
+  // stage's weights; loads complete in order, so the loop's (static) wait
+  // for stage 0's scales would then wait for the whole ring, every round.
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+  for (int d = 0; d < DEPTH; ++d) {
+    load(d, ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   float inv = 1.f;
   if constexpr (NORM) inv = norm_finish(a.ni, min(lr, a.M - 1), lg, a.K, nr);
   f32x4 acc[RT];
@@ -294,7 +301,10 @@ __global__ __launch_bounds__(NW * kWave, 2) void w4b_decode_kernel(W4bArgs a) {
   for (int u = 0; u < XB; ++u) xv[u] = x_load((int)threadIdx.x + u * NT);
   Stage<RT, UPW> ring[DEPTH];
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+  for (int d = 0; d < DEPTH; ++d) {   // in stage order (see w4b_direct_kernel)
+    load(d, ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
   for (int u = 0; u < XB; ++u)
     if ((int)threadIdx.x + u * NT < xtotal) xs[threadIdx.x + u * NT] = xv[u];
@@ -555,8 +565,13 @@ __global__ __launch_bounds__(NW * kWave, 1) void w4b_mid_kernel(W4mArgs a) {
   };
 
   Slot ring[DEPTH];
+  // in slot order, as the loop reissues them: left free, the scheduler issued
+  // slot 0's x last, and the loop's static wait for it drained the whole ring
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) load(d, ring[d]);
+  for (int d = 0; d < DEPTH; ++d) {
+    load(d, ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   for (int c0 = 0; c0 < nch; c0 += DEPTH) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
@@ -621,10 +636,9 @@ int launch_direct(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
 }
 
 // wave layouts (the nw field): 1 or 4 waves on their own rows, or 10 nw + kw
-// with kw waves splitting K over one row group (22, 44). No layout has eight
-// waves: under a 512-thread launch bound the compiler keeps the MFMA
-// accumulators in VGPRs, and fma_half's asm then reads them without the wait
-// states an MFMA result needs (gemm_common.h), so 84 and 88 computed garbage.
+// with kw waves splitting K over nw / kw row groups (22, 44, 84, 88). The
+// eight-wave layouts give a projection that runs in one split (the residual
+// epilogue) twice the waves of 44.
 template <int RT, int UPW, int DEPTH>
 int direct_nw(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
   switch (p.nw_field) {
@@ -632,6 +646,8 @@ int direct_nw(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
     case 4: return launch_direct<RT, UPW, DEPTH, 4, 1>(p, a, st);
     case 22: return launch_direct<RT, UPW, DEPTH, 1, 2>(p, a, st);
     case 44: return launch_direct<RT, UPW, DEPTH, 1, 4>(p, a, st);
+    case 84: return launch_direct<RT, UPW, DEPTH, 2, 4>(p, a, st);
+    case 88: return launch_direct<RT, UPW, DEPTH, 1, 8>(p, a, st);
   }
   return ACORN_ERR_UNSUPPORTED;
 }
@@ -728,8 +744,8 @@ int divisor_at_least(int64_t n, int64_t v) {
 }
 
 // M <= 16: rt 1/2/4 (swiglu 2/4; N/16 divisible by rt), upw 1/2, the wave
-// layout in the nw field (1 or 4 waves on their own rows; 22, 44 = nw waves
-// in one row group of kw K slices), depth 1/2/4 within the ring's
+// layout in the nw field (1 or 4 waves on their own rows; 22, 44, 84, 88 = nw
+// waves in nw / kw row groups of kw K slices), depth 1/2/4 within the ring's
 // register budget, and split counts that give every wave a whole number of
 // depth rounds. With 0 the plan takes rt 2, upw 1, one wave per workgroup,
 // depth 4, and the fewest splits that launch at least three waves per CU.
@@ -745,13 +761,16 @@ int direct_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4
   while (rt > (swiglu ? 2 : 1) && ntiles % rt) rt /= 2;
   if (ntiles % rt) return ACORN_ERR_UNSUPPORTED;
   if (upw != 1 && upw != 2) return ACORN_ERR_UNSUPPORTED;
-  if (nwf != 1 && nwf != 4 && nwf != 22 && nwf != 44) return ACORN_ERR_UNSUPPORTED;
+  if (nwf != 1 && nwf != 4 && nwf != 22 && nwf != 44 && nwf != 84 && nwf != 88)
+    return ACORN_ERR_UNSUPPORTED;
   const int nw = nwf < 10 ? nwf : nwf / 10, kw = nwf < 10 ? 1 : nwf % 10;
   if (depth != 1 && depth != 2 && depth != 4) return ACORN_ERR_UNSUPPORTED;
   while (depth > 1 && (depth * direct_stage_dwords(rt, upw) > kDirectRingDwords ||
                        G % (kw * upw * depth)))
     depth /= 2;
-  if (G % (kw * upw * depth)) return ACORN_ERR_SHAPE;
+  // K % 512 == 0 makes the default (kw = upw = depth = 1) always fit: what
+  // does not is a request the shape cannot honour
+  if (G % (kw * upw * depth)) return ACORN_ERR_UNSUPPORTED;
   const int64_t q = G / (kw * upw * depth);     // ks must divide this
   const int64_t waves = ntiles / rt * kw;
   int ks;

@@ -81,10 +81,10 @@ class Tiling(NamedTuple):
     with rt >= 1 the one that stages x in LDS): rt row tiles per wave, upw
     128-k groups per pipeline stage, nw the wave layout (M <= 16: 1 or 4
     waves each on its own rows; above: 2 or 4; 10*nw + kw: kw waves share
-    rows and split K, 22 / 44 at M <= 16, 42 / 44 / 82 / 84 above),
-    ksplit, and tpw = stages in flight per wave.
+    rows and split K, 22 / 44 / 84 / 88 at M <= 16, 42 / 44 / 82 / 84
+    above), ksplit, and tpw = stages in flight per wave.
     int8 decode kernel (WFMT_W8B, M <= 16): rt row tiles per wave, upw 64-k
-    blocks per stage, nw the wave layout (1, 4, 22, 44 as for int4), ksplit,
+    blocks per stage, nw the wave layout (1, 4, 22, 44), ksplit,
     tpw = stages in flight; above 16 rows W8B runs on the tiled kernel.
     bf16 decode kernel (WFMT_BF16B, M <= 16): rt row tiles per wave, upw
     32-k blocks per stage, nw the wave layout (1, 4, 22, 44), ksplit, tpw =
@@ -356,13 +356,14 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
 def _w4b_requests(swiglu: bool) -> list[Tiling]:
     """Requests covering the int4 direct kernel's knobs (M <= 16): 1, 2 or 4
     row tiles per wave, one group per stage with 2 or 4 stages in flight or
-    two groups with 2, one or four waves per workgroup on their own rows or 2
-    or 4 K slices over shared rows (22, 44), and split counts from one to
-    sixteen (the fused SwiGLU runs in one split)."""
+    two groups with 2, one or four waves per workgroup on their own rows or 2,
+    4 or 8 K slices over shared rows (22, 44, 84 = two row groups of four
+    slices, 88), and split counts from one to sixteen (the fused SwiGLU runs
+    in one split)."""
     reqs = []
     for rt in ((2, 4) if swiglu else (1, 2, 4)):
         for upw, depth in ((1, 2), (1, 4), (2, 2)):
-            for nw in (1, 4, 22, 44):
+            for nw in (1, 4, 22, 44, 84, 88):
                 for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
                     reqs.append(Tiling(rt, upw, nw, ks, depth))
     return reqs

@@ -113,13 +113,14 @@ def test_planner_w4b_decode(M, N, K):
     """M <= 16 (the direct kernel): the default tiling, and every requested
     one the planner accepts, obey the kernel's contract: rt in {1,2,4}
     dividing N/16, upw in {1,2}, a wave layout of 1 or 4 waves on their own
-    rows or 10 nw + kw (22, 44; 84 is refused), depth in {1,2,4} within the register
+    rows or 10 nw + kw (22, 44, 84, 88), depth in {1,2,4} within the register
     ring's budget, and each wave's K range holding a whole number of
     depth-stage rounds."""
     lib = _lib.lib()
     reqs = [(0, 0, 0, 0, 0), (4, 1, 1, 0, 4), (1, 2, 4, 3, 2), (2, 2, 4, 5, 4), (2, 1, 1, 1, 4),
             (4, 2, 1, 2, 2), (1, 1, 4, 16, 1), (2, 1, 2, 0, 4), (1, 4, 1, 0, 2), (2, 1, 44, 1, 4),
-            (2, 2, 84, 2, 2), (4, 1, 22, 0, 4), (2, 1, 42, 1, 2)]
+            (2, 2, 84, 2, 2), (4, 1, 22, 0, 4), (2, 1, 42, 1, 2), (1, 1, 88, 1, 4),
+            (1, 2, 88, 1, 2), (2, 1, 84, 0, 4)]
     for r in reqs:
         cfg = (ctypes.c_int * 6)(*r, 0)
         rc = lib.acorn_gemm_plan(M, N, K, _lib.WFMT_W4B, cfg)
@@ -127,8 +128,8 @@ def test_planner_w4b_decode(M, N, K):
             continue                  # a request the shape cannot honour is refused
         assert rc == 0, (r, rc)
         rt, upw, nwf, ks, depth = cfg[:5]
-        assert r[2] in (0, 1, 4, 22, 44) and r[1] in (0, 1, 2), r   # refused knobs never plan
-        assert nwf in (1, 4, 22, 44)
+        assert r[2] in (0, 1, 4, 22, 44, 84, 88) and r[1] in (0, 1, 2), r   # refused knobs never plan
+        assert nwf in (1, 4, 22, 44, 84, 88)
         kw = 1 if nwf < 10 else nwf % 10
         assert rt in (1, 2, 4) and (N // 16) % rt == 0
         assert upw in (1, 2) and depth in (1, 2, 4)
