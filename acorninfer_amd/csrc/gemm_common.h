@@ -113,45 +113,92 @@ struct ResidOut {
   __bf16* xw;            // [M, N] bf16(res_out * nw)
 };
 
-// Row m's 1 / rms from its nss partial sums, computed by the four lanes of lane
-// group q = 0..3 that hold row m (a quarter each, added in a fixed order), the
-// same value in every lane of every wave. In two halves, so that the sums are
-// requested before a kernel's first weights and added after them (loads
-// complete in order: waiting for the sums does not wait for the weights): up
-// to kNormRegs floats per lane go through registers, requested unconditionally
-// (past the quarter they re-read its last vector, unused); longer or unaligned
-// quarters are read at the finish.
+// Row m's 1 / rms from its nss partial sums, the same value in every lane
+// that serves row m. With mp the power of two >= M (at most 16), lane l
+// serves row l % mp (rows past M re-read row M - 1) and adds part l / mp of
+// its sums, in order: 64 / mp parts of per = ceil(nss mp / 64) sums; the
+// parts are then added by an xor butterfly over lane strides mp, 2 mp .. 32.
+// Every lane loads, so a small batch reads each sum once instead of once per
+// lane group. In two halves, so that the sums are requested before a
+// kernel's first weights and added after them (loads complete in order:
+// waiting for the sums does not wait for the weights): parts of 4, 8, 16, 32
+// or 64 sums go through registers, others are read at the finish.
 constexpr int kNormRegs = 64;
 struct NormRegs {
   f32x4 v[kNormRegs / 4];
 };
-__device__ __forceinline__ void norm_issue(const NormIn& n, int m, int q, NormRegs& r) {
-  const int per = n.nss / 4;
-  if (per % 4 || per > kNormRegs) return;                 // uniform
-  const float* p = n.ss + (size_t)m * n.nss + q * per;
-#pragma unroll
-  for (int t = 0; t < kNormRegs / 4; ++t) r.v[t] = *(const f32x4*)(p + 4 * min(t, per / 4 - 1));
+// v of lane l ^ O (O < 32: a bitmask-mode ds_swizzle, no address register)
+template <int O>
+__device__ __forceinline__ float swizzle_xor(float v) {
+  static_assert(O > 0 && O < 32 && (O & (O - 1)) == 0, "a lane stride inside 32 lanes");
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (O << 10)));
 }
-__device__ __forceinline__ float norm_finish(const NormIn& n, int m, int q, int cols,
+__device__ __forceinline__ int norm_rows(int M) {
+  return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : 16;
+}
+// vectors per lane in registers: parts of 4, 8, 16, 32 or 64 sums; 0 = read
+// at the finish
+__device__ __forceinline__ int norm_vectors(int nss, int parts) {
+  const int per = nss / parts;
+  if (nss % parts || per % 4) return 0;
+  const int nv = per / 4;
+  return (nv & (nv - 1)) == 0 && nv <= kNormRegs / 4 ? nv : 0;
+}
+template <int NV>
+__device__ __forceinline__ void norm_load(const float* p, NormRegs& r) {
+#pragma unroll
+  for (int t = 0; t < NV; ++t) r.v[t] = *(const f32x4*)(p + 4 * t);
+}
+template <int NV>
+__device__ __forceinline__ float norm_add(const NormRegs& r) {
+#pragma clang fp contract(off)
+  float s = 0.f;
+#pragma unroll
+  for (int t = 0; t < NV; ++t) {
+    s = s + r.v[t][0];
+    s = s + r.v[t][1];
+    s = s + r.v[t][2];
+    s = s + r.v[t][3];
+  }
+  return s;
+}
+__device__ __forceinline__ void norm_issue(const NormIn& n, int M, int lane, NormRegs& r) {
+  const int mp = norm_rows(M), parts = kWave / mp;
+  const int nv = norm_vectors(n.nss, parts);
+  const float* p = n.ss + (size_t)min(lane % mp, M - 1) * n.nss + (lane / mp) * 4 * nv;
+  switch (nv) {                                            // uniform
+    case 1: norm_load<1>(p, r); break;
+    case 2: norm_load<2>(p, r); break;
+    case 4: norm_load<4>(p, r); break;
+    case 8: norm_load<8>(p, r); break;
+    case 16: norm_load<16>(p, r); break;
+    default: break;
+  }
+}
+__device__ __forceinline__ float norm_finish(const NormIn& n, int M, int lane, int cols,
                                              const NormRegs& r) {
 #pragma clang fp contract(off)
-  const int per = n.nss / 4;
+  const int mp = norm_rows(M), parts = kWave / mp;
   float s = 0.f;
-  if (per % 4 || per > kNormRegs) {
-    const float* p = n.ss + (size_t)m * n.nss + q * per;
-    for (int t = 0; t < per; ++t) s = s + p[t];
-  } else {
-#pragma unroll
-    for (int t = 0; t < kNormRegs / 4; ++t) {
-      if (4 * t < per) {
-        s = s + r.v[t][0];
-        s = s + r.v[t][1];
-        s = s + r.v[t][2];
-        s = s + r.v[t][3];
-      }
+  switch (norm_vectors(n.nss, parts)) {
+    case 1: s = norm_add<1>(r); break;
+    case 2: s = norm_add<2>(r); break;
+    case 4: s = norm_add<4>(r); break;
+    case 8: s = norm_add<8>(r); break;
+    case 16: s = norm_add<16>(r); break;
+    default: {
+      const int per = (n.nss + parts - 1) / parts;
+      const int t0 = (lane / mp) * per, t1 = min(t0 + per, n.nss);
+      const float* p = n.ss + (size_t)min(lane % mp, M - 1) * n.nss;
+      for (int t = t0; t < t1; ++t) s = s + p[t];
     }
   }
-  s = s + __shfl_xor(s, 16);
+  // strides below 32 by a swizzle (lane ^ O within 32 lanes), 32 by a permute
+  if (mp <= 1) s = s + swizzle_xor<1>(s);
+  if (mp <= 2) s = s + swizzle_xor<2>(s);
+  if (mp <= 4) s = s + swizzle_xor<4>(s);
+  if (mp <= 8) s = s + swizzle_xor<8>(s);
+  s = s + swizzle_xor<16>(s);
   s = s + __shfl_xor(s, 32);
   return 1.0f / sqrtf(s / (float)cols + n.eps);
 }

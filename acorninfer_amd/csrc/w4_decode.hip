@@ -104,7 +104,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
   };
 
   NormRegs nr;
-  if constexpr (NORM) norm_issue(a.ni, min(lr, a.M - 1), lg, nr);
+  if constexpr (NORM) norm_issue(a.ni, a.M, lane, nr);
   DStage<RT, UPW> ring[DEPTH];
   // The first stages are issued in stage order, as the loop reissues them.
   // Left free, the scheduler moves every stage's scale load after the last
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
     __builtin_amdgcn_sched_barrier(0);
   }
   float inv = 1.f;
-  if constexpr (NORM) inv = norm_finish(a.ni, min(lr, a.M - 1), lg, a.K, nr);
+  if constexpr (NORM) inv = norm_finish(a.ni, a.M, lane, a.K, nr);
   f32x4 acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};

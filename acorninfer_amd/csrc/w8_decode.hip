@@ -96,7 +96,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
   };
 
   NormRegs nr;
-  if constexpr (NORM) norm_issue(a.ni, min(lr, a.M - 1), lg, nr);
+  if constexpr (NORM) norm_issue(a.ni, a.M, lane, nr);
   W8Stage<RT, UPW> ring[DEPTH];
   // in stage order, as the loop reissues them (the loop's static waits assume
   // that order; left free, the scheduler reorders the first stages' loads)
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
     __builtin_amdgcn_sched_barrier(0);
   }
   float inv = 1.f;
-  if constexpr (NORM) inv = norm_finish(a.ni, min(lr, a.M - 1), lg, a.K, nr);
+  if constexpr (NORM) inv = norm_finish(a.ni, a.M, lane, a.K, nr);
   f32x4 acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};

@@ -50,20 +50,45 @@ def _direct_tilings(lin, m, swiglu=False, one_split=False):
 
 
 def _inv_kernel_order(ss: np.ndarray, cols: int, eps: float) -> np.ndarray:
-    """1/rms per row from [M, nss] fp32 sums, added as the kernels do."""
+    """1/rms per row from [M, nss] fp32 sums, added as the kernels do: mp =
+    the power of two >= M, 64 / mp parts of ceil(nss mp / 64) sums each added
+    in order, then the parts by an xor butterfly (neighbours first)."""
     m, nss = ss.shape
-    per = nss // 4
+    mp = 1 << max(m - 1, 0).bit_length()
+    parts = 64 // mp
+    per = -(-nss // parts)
     out = np.empty(m, dtype=np.float32)
     for r in range(m):
         q = []
-        for j in range(4):
+        for j in range(parts):
             s = np.float32(0)
-            for t in range(per):
-                s = np.float32(s + ss[r, j * per + t])
+            for t in range(j * per, min((j + 1) * per, nss)):
+                s = np.float32(s + ss[r, t])
             q.append(s)
-        tot = np.float32(np.float32(q[0] + q[1]) + np.float32(q[2] + q[3]))
-        out[r] = np.float32(1.0) / np.sqrt(np.float32(tot / np.float32(cols) + np.float32(eps)))
+        while len(q) > 1:
+            q = [np.float32(q[i] + q[i + 1]) for i in range(0, len(q), 2)]
+        out[r] = np.float32(1.0) / np.sqrt(np.float32(q[0] / np.float32(cols) + np.float32(eps)))
     return out
+
+
+def test_inv_order_restatement():
+    """The restated order on a known case: M = 16 is four parts per row added
+    as (q0 + q1) + (q2 + q3); M = 1 is 64 parts of one vector each; sums that
+    need every bit of the order (a large value cancelled later) pin it."""
+    nss = 256
+    ss = np.full((1, nss), 1.0, dtype=np.float32)
+    got = _inv_kernel_order(ss, 16 * nss, 0.0)
+    assert np.isclose(got[0], 1.0 / np.sqrt(nss / (16 * nss)))
+    # 2^24 + 1 is not an fp32: a part that adds 1.0 to 2^24 loses it, a part
+    # that adds the ones first keeps them
+    ss = np.zeros((16, nss), dtype=np.float32)
+    ss[:, 0] = 2.0 ** 24
+    ss[:, 1:64] = 1.0
+    tot16 = _inv_kernel_order(ss, 1, 0.0)        # part 0 holds 2^24 and the 63 ones
+    assert np.isclose(1.0 / tot16[0] ** 2, 2.0 ** 24, rtol=0, atol=0)
+    ss1 = ss[:1].copy()
+    tot1 = _inv_kernel_order(ss1, 1, 0.0)        # parts of 4: 2^24 + 3 ones, the rest exact
+    assert 1.0 / tot1[0] ** 2 > 2.0 ** 24
 
 
 @pytest.mark.gpu
