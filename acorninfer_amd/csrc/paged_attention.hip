@@ -35,6 +35,7 @@ constexpr int kChunk = 16;  // tokens per step
 constexpr int kLPT = 4;     // lanes per token in the q.k phase
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kAttnWaves = 8;  // waves per workgroup of the single-kernel form
+constexpr int64_t kCUs = 256;   // MI355X compute units (the head-group rule)
 constexpr int kOneWavePages = 16;  // MFMA form: splits of at most this many pages use one wave
 #ifndef ACORN_K3_ONE_WAVE_DEPTH
 #define ACORN_K3_ONE_WAVE_DEPTH 3
@@ -573,8 +574,15 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   int* tbl = (int*)(sl + NWV * REP);
 
   // kv head fastest in the grid: the KV workgroups of one split read the same
-  // pages (the heads of a token are adjacent in a page) at about the same time
-  const int kvh = blockIdx.x, sp = blockIdx.y, b = blockIdx.z;
+  // pages (the heads of a token are adjacent in a page) at about the same time.
+  // Head groups: gridDim.x = KV * G, G = (H / KV) / REP workgroups per kv
+  // head, group g = blockIdx.x / KV serving q heads qh0 .. qh0 + REP - 1 (G > 1
+  // gives a small batch's one split more workgroups than its (sequence, kv
+  // head) pairs, without a combine). Workgroups are dealt to the 8 XCDs round
+  // robin, so with KV a multiple of 8 a kv head's groups share one XCD and
+  // its pages are fetched once into that XCD's L2.
+  const int kvh = blockIdx.x % KV, sp = blockIdx.y, b = blockIdx.z;
+  const int qh0 = kvh * (H / KV) + (int)(blockIdx.x / KV) * REP;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x % kWave;
   const int r = lane >> 4, c = lane & 15;
@@ -604,7 +612,7 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   const int ic = min(lane, HALF - 1);                // this lane's pair
   const size_t width = (size_t)(H + 2 * KV) * D;
   const size_t qplane = (size_t)e.batch * width;
-  const float* qsrc = EPI ? e.part + (size_t)b * width + (size_t)kvh * REP * D + ic : nullptr;
+  const float* qsrc = EPI ? e.part + (size_t)b * width + (size_t)qh0 * D + ic : nullptr;
   float qpa[EPI ? REP : 1][kQB], qpc[EPI ? REP : 1][kQB], qw1 = 0.f, qw2 = 0.f, qfr = 0.f;
   float epos = 0.f;
   // ... and this kv head's k and v partials and k norm weights, for the wave
@@ -651,7 +659,7 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
   } else {
 #pragma unroll
     for (int j = 0; j < KB; ++j)
-      qb[j] = *(const u32x4_t*)(q + ((size_t)b * H + kvh * REP + min(c, REP - 1)) * D + 32 * j + 8 * r);
+      qb[j] = *(const u32x4_t*)(q + ((size_t)b * H + qh0 + min(c, REP - 1)) * D + 32 * j + 8 * r);
 #pragma unroll
     for (int j = 0; j < KB; ++j) asm volatile("" ::"v"(qb[j]));
   }
@@ -962,7 +970,7 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
     // a one-wave split writes its result straight from the accumulators:
     // lane (r, c < REP) holds dims DPL (4 r + i) + j of head c
     if (c < REP) {
-      const size_t orow = (size_t)b * H + kvh * REP + c;
+      const size_t orow = (size_t)b * H + qh0 + c;
       if (nsb == 1) {
         const float inv = 1.0f / l;
 #pragma unroll
@@ -1020,7 +1028,7 @@ __global__ __launch_bounds__(NWV * kWave, NWV == 1 ? (DEPTH <= 2 ? 4 : 3) : 2) v
         den += f * sl[w * REP + h];
       }
     }
-    const size_t orow = (size_t)b * H + kvh * REP + h;
+    const size_t orow = (size_t)b * H + qh0 + h;
     if (nsb == 1) {
       out[orow * D + d] = from_f32<T>(num / den);
     } else {
@@ -1137,11 +1145,26 @@ __global__ __launch_bounds__(kCombineWaves * kWave) void paged_attn_combine_kern
   }
 }
 
+// Head groups per kv head for the MFMA kernel: a single split over at most
+// kHeadGroupPages pages and fewer (sequence, kv head) pairs than half the CUs
+// gives each pair's q heads up to rep workgroups (halving the heads per
+// workgroup while the grid stays within the CU count), so a small batch fills
+// the chip without split partials and a combine launch.
+constexpr int64_t kHeadGroupPages = 64;
+int64_t k3_head_groups(int64_t B, int64_t KV, int64_t rep, int64_t S, int64_t ts) {
+  if (S != 1 || ts > kHeadGroupPages) return 1;
+  int64_t g = 1;
+  while (g < rep && B * KV * g * 2 <= kCUs) g *= 2;
+  return g;
+}
+
 template <typename T, int D, int REP>
 int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* tables,
                 const int32_t* lens, void* out, float* ws_acc, float* ws_ml, int64_t B,
                 int64_t H, int64_t KV, int64_t P, int64_t num_blocks, int64_t table_stride, int64_t S, float scale,
-                hipStream_t st, const EpiArgs* epi) {
+                hipStream_t st, const EpiArgs* epi, int64_t G) {
+  // G head groups per kv head (REP = H / KV / G q heads each): the MFMA kernel only
+  if (G != 1 && (D < 64 || std::is_same<T, float>::value)) return ACORN_ERR_UNSUPPORTED;
   dim3 grid((unsigned)S, (unsigned)KV, (unsigned)B);
   float* ws_m = ws_ml;
   float* ws_l = ws_ml ? ws_ml + B * H * S : nullptr;
@@ -1174,7 +1197,7 @@ int launch_attn(const void* q, const void* kp, const void* vp, const int32_t* ta
                                 160 * 1024);
       lds_raised[which] = true;
     }
-    kfn<<<dim3((unsigned)KV, (unsigned)S, (unsigned)B), dim3(nwv * kWave), lds, st>>>(
+    kfn<<<dim3((unsigned)(KV * G), (unsigned)S, (unsigned)B), dim3(nwv * kWave), lds, st>>>(
         (const T*)q, (const T*)kp, (const T*)vp, tables, lens, (T*)out, ws_acc, ws_m, ws_l,
         (int)H, (int)KV, (int)P, (int)num_blocks, (int)table_stride, (int)S, scale * kLog2e,
         epi ? *epi : EpiArgs{});
@@ -1215,12 +1238,12 @@ template <typename T, int D>
 int dispatch_rep(int64_t rep, const void* q, const void* kp, const void* vp,
                  const int32_t* tables, const int32_t* lens, void* out, float* ws_acc,
                  float* ws_ml, int64_t B, int64_t H, int64_t KV, int64_t P, int64_t num_blocks, int64_t ts,
-                 int64_t S, float scale, hipStream_t st, const EpiArgs* epi) {
-  switch (rep) {
-    case 1: return launch_attn<T, D, 1>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
-    case 2: return launch_attn<T, D, 2>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
-    case 4: return launch_attn<T, D, 4>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
-    case 8: return launch_attn<T, D, 8>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
+                 int64_t S, float scale, hipStream_t st, const EpiArgs* epi, int64_t G) {
+  switch (rep) {   // q heads per workgroup
+    case 1: return launch_attn<T, D, 1>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi, G);
+    case 2: return launch_attn<T, D, 2>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi, G);
+    case 4: return launch_attn<T, D, 4>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi, G);
+    case 8: return launch_attn<T, D, 8>(q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi, G);
   }
   return ACORN_ERR_UNSUPPORTED;
 }
@@ -1230,11 +1253,13 @@ int dispatch_d(int64_t D, int64_t rep, const void* q, const void* kp, const void
                const int32_t* tables, const int32_t* lens, void* out, float* ws_acc,
                float* ws_ml, int64_t B, int64_t H, int64_t KV, int64_t P, int64_t num_blocks, int64_t ts,
                int64_t S, float scale, hipStream_t st, const EpiArgs* epi = nullptr) {
+  const int64_t G = D >= 64 && !std::is_same<T, float>::value ? k3_head_groups(B, KV, rep, S, ts) : 1;
+  const int64_t r = rep / G;
   switch (D) {
-    case 16: return dispatch_rep<T, 16>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
-    case 32: return dispatch_rep<T, 32>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
-    case 64: return dispatch_rep<T, 64>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
-    case 128: return dispatch_rep<T, 128>(rep, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi);
+    case 16: return dispatch_rep<T, 16>(r, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi, G);
+    case 32: return dispatch_rep<T, 32>(r, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi, G);
+    case 64: return dispatch_rep<T, 64>(r, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi, G);
+    case 128: return dispatch_rep<T, 128>(r, q, kp, vp, tables, lens, out, ws_acc, ws_ml, B, H, KV, P, num_blocks, ts, S, scale, st, epi, G);
   }
   return ACORN_ERR_UNSUPPORTED;
 }

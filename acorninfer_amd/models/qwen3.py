@@ -1083,7 +1083,8 @@ FOLDED = ("qkv", "o", "gate_up", "down")   # the projections the RMSNorms fold i
 
 
 def attention_splits(batch: int, kv_heads: int, max_pages: int, *,
-                     unit_pages: int | None = None, max_splits: int = MAX_SPLITS) -> int:
+                     unit_pages: int | None = None, max_splits: int = MAX_SPLITS,
+                     q_per_kv: int = 1) -> int:
     """K3 split count S for block tables `max_pages` wide.
 
     K3 gives every split the same pps = ceil(max_pages / S) pages, so a
@@ -1103,10 +1104,15 @@ def attention_splits(batch: int, kv_heads: int, max_pages: int, *,
     such a grid takes WIDE_UNIT_PAGES-page splits, the longest that still run
     as one-wave workgroups: half the partials of 8-page splits for the
     combine (C = 64 over prompts U[1024, 8192], 512-page tables: K3 + combine
-    220 against 234 us per layer)."""
+    220 against 234 us per layer). With `q_per_kv` (q heads per kv head) the
+    one-split rule counts the q heads: K3 gives a single split's q heads
+    workgroups of their own while the pairs are fewer than the CUs (its head
+    groups), so C = 8 at 512 tokens runs as 256 workgroups with no combine
+    (bf16 step 3.11-3.13 against 3.14 ms)."""
+    if unit_pages is None and batch * kv_heads * q_per_kv >= WIDE_GRID \
+            and max_pages <= ONE_SPLIT_MAX_PAGES:
+        return 1
     if unit_pages is None and batch * kv_heads >= WIDE_GRID:
-        if max_pages <= ONE_SPLIT_MAX_PAGES:
-            return 1
         unit_pages = WIDE_UNIT_PAGES
     if unit_pages is None:
         unit_pages = 1 if batch * kv_heads * max_pages < SMALL_GRID_PAGES else UNIT_PAGES
@@ -1131,7 +1137,8 @@ class StepBuffers:
         H, D = cfg.hidden_size, cfg.head_dim
         nq, nkv, inter = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.intermediate_size
         if self.num_splits is None:
-            self.num_splits = attention_splits(B, nkv, self.max_pages)
+            self.num_splits = attention_splits(B, nkv, self.max_pages,
+                                               q_per_kv=1 if self.prefill else nq // nkv)
             if self.prefill:
                 # one row per prompt token: bound the split workspace
                 cap = PREFILL_WS_BYTES // max(1, B * nq * (D + 2) * 4)
