@@ -43,6 +43,11 @@ CASES = [
     (3, 16, 8, 128, 16, [1, 64, 200], 20, 1, 1),         # a one-token sequence: wave 0
     (2, 32, 8, 128, 16, [700, 1000], 80, 2, 3),          # 40-page splits, combine after
     (2, 32, 8, 128, 16, [5000, 9000], 1100, 1, 2),       # 138 pages a wave: ids staged in LDS
+    # head groups (one split over <= 64 pages, few (sequence, kv head) pairs): each kv
+    # head's q heads in G workgroups of their own
+    (1, 32, 4, 128, 16, [70], 6, 1, 2),                  # G = 8, one q head each, one wave
+    (1, 32, 4, 128, 16, [300], 20, 1, 2),                # G = 8, eight-wave workgroups
+    (2, 16, 4, 64, 32, [100, 300], 12, 1, 1),            # D 64, 32-token pages, G = 4
 ]
 
 
