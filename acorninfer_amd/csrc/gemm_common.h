@@ -299,6 +299,18 @@ struct W4mPlan {
 int w4m_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, W4mPlan* p);
 int w4m_launch(const W4mPlan& p, const void* x, const void* w, const void* scale, void* out,
                float* part, int64_t M, int64_t N, int64_t K, hipStream_t st);
+// ---- the int8 GEMM for 17..256 rows (w8_decode.hip) ----------------------------
+// The same knobs and request (rt = kMidRT) on W8B weights: upw = row tiles per
+// wave (1, 2), nw = waves (4, 8), ksplit, tpw = 128-k steps in flight (2, 4).
+struct W8mPlan {
+  int rt, nw, ksplit, depth;
+  int groups;      // row blocks of nw * rt * 16 rows
+  int mblocks;     // blocks of 64 x rows
+  size_t lds;
+};
+int w8m_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, W8mPlan* p);
+int w8m_launch(const W8mPlan& p, const void* x, const void* w, const void* scale, void* out,
+               float* part, int64_t M, int64_t N, int64_t K, hipStream_t st);
 // W4B weights -> bf16 [N, K] in row order (N % 16 == 0, K % 512 == 0).
 int w4b_dequant(const void* w, const void* scale, void* out, int64_t N, int64_t K,
                 hipStream_t st);

@@ -754,11 +754,13 @@ struct Tiling {
                                  // 4 = W4B mid-M kernel (rt == kMidRT, upw = row tiles
                                  //     per wave, nw = waves, tpw = groups in flight),
                                  // 5 = W8B decode kernel (tpw = its pipeline depth),
-                                 // 6 = BF16B decode kernel (tpw = its pipeline depth)
+                                 // 6 = BF16B decode kernel (tpw = its pipeline depth),
+                                 // 7 = W8B mid-M kernel (as 4, tpw = steps in flight)
   W4bPlan w4b;
   DirectPlan w8b;
   DirectPlan bf16b;
   W4mPlan w4m;
+  W8mPlan w8m;
 };
 
 int ilog2_ceil(int v) {
@@ -931,22 +933,24 @@ int make_plan(int64_t M, int64_t N, int64_t K, int wfmt, const int* cfg, Tiling*
   }
   if (cfg && cfg[0] == kDenseRT) return ACORN_ERR_UNSUPPORTED;
   if (cfg && cfg[0] == kMidRT) {
-    if (wfmt != ACORN_WFMT_W4B || swiglu || M <= 16) return ACORN_ERR_UNSUPPORTED;
-    const int rc = w4m_make_plan(M, N, K, cfg, &t->w4m);
+    if ((wfmt != ACORN_WFMT_W4B && wfmt != ACORN_WFMT_W8B) || swiglu || M <= 16)
+      return ACORN_ERR_UNSUPPORTED;
+    const bool w4 = wfmt == ACORN_WFMT_W4B;
+    const int rc = w4 ? w4m_make_plan(M, N, K, cfg, &t->w4m) : w8m_make_plan(M, N, K, cfg, &t->w8m);
     if (rc) return rc;
-    t->kind = 4;
+    t->kind = w4 ? 4 : 7;
     t->rt = kMidRT;
-    t->upw = t->w4m.rt;
-    t->nw = t->w4m.nw;
-    t->ksplit = t->w4m.ksplit;
-    t->tpw = t->w4m.depth;
+    t->upw = w4 ? t->w4m.rt : t->w8m.rt;
+    t->nw = w4 ? t->w4m.nw : t->w8m.nw;
+    t->ksplit = w4 ? t->w4m.ksplit : t->w8m.ksplit;
+    t->tpw = w4 ? t->w4m.depth : t->w8m.depth;
     t->mt = 1;
     t->R = 1;
     t->nk = 0;
-    t->ntiles = t->w4m.groups;
-    t->mblocks = t->w4m.mblocks;
-    t->groups = t->w4m.groups;
-    t->lds = t->w4m.lds;
+    t->ntiles = w4 ? t->w4m.groups : t->w8m.groups;
+    t->mblocks = w4 ? t->w4m.mblocks : t->w8m.mblocks;
+    t->groups = t->ntiles;
+    t->lds = w4 ? t->w4m.lds : t->w8m.lds;
     return ACORN_OK;
   }
   if (wfmt == ACORN_WFMT_W4B && ((M <= 16 && !(cfg && cfg[0] == 0 && cfg[1] >= 32)) ||
@@ -1278,6 +1282,8 @@ int gemm_entry(const void* x, const void* w, const void* scale, const void* zero
   } else if (t.kind == 4) {
     if (zero) return ACORN_ERR_UNSUPPORTED;  // the block layout is the symmetric format
     rc = w4m_launch(t.w4m, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
+  } else if (t.kind == 7) {
+    rc = w8m_launch(t.w8m, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, st);
   } else if (t.kind == 5) {
     rc = w8b_launch(t.w8b, x, w, scale, t.ksplit == 1 ? out_bf16 : nullptr, part, M, N, K, ni,
                     ro, st);

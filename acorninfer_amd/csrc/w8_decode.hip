@@ -283,6 +283,202 @@ int divisor_at_least(int64_t n, int64_t v) {
   return v <= n ? (int)v : 0;
 }
 
+
+// ---------------------------------------------------------------------------
+// int8 GEMM for batches of 17..256 rows (decode buckets 32 / 64, configuration
+// 3's M = 64 / 256), on the same W8B blocks, built as the int4 mid-M kernel
+// (w4_decode.hip): a workgroup of NW waves owns NW * RT 16-row tiles x 64
+// columns of x over a K range, and x moves through LDS 128 k (two blocks) at
+// a time:
+//  * every thread loads its share of the step's x (2 or 4 pieces of 16 bytes)
+//    and each wave its RT x 2 weight blocks, DEPTH steps ahead in a register
+//    ring (a step's loads are issued together, in step order);
+//  * per step: the x pieces go to LDS (two buffers), one barrier, four waves
+//    form the step's column sums of x (MFMAs against ones) for the -128 X
+//    correction, a second barrier, then each wave unpacks each weight block
+//    once (q + 128 -> bf16, exact) and runs RT x 2 x 2 x 4 MFMAs: every
+//    unpacked operand feeds the four column blocks, every x operand the RT
+//    tiles;
+//  * y = s[n] (C - 128 X) at the end, C the MFMA sum over the biased weights
+//    and X each column's sum of x over the K range, added up per step in
+//    fp32; split-K partials as everywhere else: fp32 [ksplit, M, N] of the
+//    scaled values, summed in split order by the consumer.
+struct W8mArgs {
+  const __bf16* x;
+  const uint8_t* w;
+  const _Float16* scale;
+  __bf16* out;    // bf16 [M, N] when ksplit == 1
+  float* part;    // fp32 [ksplit, M, N] otherwise
+  int M, N, K;
+  int kr;         // K range of a split (a multiple of 128 * DEPTH)
+};
+
+constexpr int kW8MidBM = 64;                    // columns (x rows) per workgroup
+constexpr int kW8MidMB = kW8MidBM / 16;
+constexpr int kW8MidXP = kW8MidBM + 1;          // LDS pitch of one k piece (16-byte slots)
+
+template <int RT, int NW, int DEPTH>
+__global__ __launch_bounds__(NW * kWave, 1) void w8b_mid_kernel(W8mArgs a) {
+  constexpr int NT = NW * kWave;
+  constexpr int XPT = kW8MidBM * 16 / NT;        // x pieces per thread per step
+  static_assert(XPT >= 1 && kW8MidBM * 16 % NT == 0, "whole x pieces per thread");
+  extern __shared__ __align__(16) unsigned char smem[];
+  u32x4* xs = (u32x4*)smem;                      // [2][16 pieces][kW8MidXP rows]
+  float* xsum = (float*)(smem + 2 * 16 * kW8MidXP * 16);   // [2][64]
+  const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lg = lane >> 4, lr = lane & 15;
+  int tile, split, mblk;
+  {
+    // the M blocks of one (row block, split) on one XCD (workgroups are dealt
+    // to the 8 XCDs round robin), so their weight re-reads come from its L2
+    const int ntl = gridDim.x, nks = gridDim.y, nmb = gridDim.z;
+    const int lin = blockIdx.x + ntl * (blockIdx.y + nks * blockIdx.z);
+    const int units = ntl * nks;
+    int unit;
+    if (nmb > 1 && units % 8 == 0) {
+      const int xcd = lin % 8, j = lin / 8;
+      unit = xcd * (units / 8) + j / nmb;
+      mblk = j % nmb;
+    } else {
+      unit = lin % units;
+      mblk = lin / units;
+    }
+    tile = unit % ntl;
+    split = unit / ntl;
+  }
+  const int KB = a.K / 64;                       // blocks per row
+  const int t0 = (tile * NW + wid) * RT;         // this wave's first 16-row tile
+  const int sbase = split * (a.kr / 128);        // first 128-k step of the split
+  const int nch = a.kr / 128;
+  const int m0 = mblk * kW8MidBM;
+
+  struct Slot {
+    u32x4 x[XPT];
+    u32x4 w[RT][2];
+  };
+  // piece p of a step: x row p / 16, k piece p % 16 (8 k), so that a wave's
+  // load covers 4 rows x 256 contiguous bytes (rows past M re-read row M - 1;
+  // their columns are never stored); it goes to LDS slot piece * kW8MidXP +
+  // row, whose pad keeps the stores and the operand reads free of bank
+  // conflicts
+  auto load = [&](int c, Slot& sl) {
+    const int st = sbase + min(c, nch - 1);
+#pragma unroll
+    for (int u = 0; u < XPT; ++u) {
+      const int p = (int)threadIdx.x + NT * u;
+      const int m = min(m0 + p / 16, a.M - 1);
+      sl.x[u] = *(const u32x4*)(a.x + (size_t)m * a.K + st * 128 + (p % 16) * 8);
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        sl.w[rt][u] = load_nt((const u32x4*)(a.w + ((size_t)(t0 + rt) * KB + 2 * st + u) * 1024 +
+                                             lane * 16));
+  };
+
+  f32x4 acc[RT][kW8MidMB];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mb = 0; mb < kW8MidMB; ++mb) acc[rt][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float xt[kW8MidMB];                            // column lr's sum of x so far, per block
+#pragma unroll
+  for (int mb = 0; mb < kW8MidMB; ++mb) xt[mb] = 0.f;
+  const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+
+  auto step = [&](int c, const Slot& sl) {
+    const int b = c & 1;
+    u32x4* xb = xs + b * 16 * kW8MidXP;
+#pragma unroll
+    for (int u = 0; u < XPT; ++u) {
+      const int p = (int)threadIdx.x + NT * u;
+      xb[(p % 16) * kW8MidXP + p / 16] = sl.x[u];
+    }
+    __syncthreads();
+    if (wid < kW8MidMB) {
+      f32x4 xg = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xg = mfma(ones, xb[(4 * lg + j) * kW8MidXP + wid * 16 + lr], xg);
+      if (lg == 0) xsum[b * kW8MidBM + wid * 16 + lr] = xg[0];
+    }
+    __syncthreads();
+    // block u, MFMA j: the lane's k slots stand for k 64 u + 16 lg + 8 j ..,
+    // i.e. x piece 8 u + 2 lg + j of the step
+    u32x4 aw[RT][2][2];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          aw[rt][u][j] = unpack_w8(sl.w[rt][u][2 * j], sl.w[rt][u][2 * j + 1]);
+#pragma unroll
+    for (int mb = 0; mb < kW8MidMB; ++mb) {
+      u32x4 bx[2][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          bx[u][j] = xb[(8 * u + 2 * lg + j) * kW8MidXP + mb * 16 + lr];
+      xt[mb] += xsum[b * kW8MidBM + mb * 16 + lr];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[rt][mb] = mfma(aw[rt][u][j], bx[u][j], acc[rt][mb]);
+    }
+  };
+
+  Slot ring[DEPTH];
+  // in slot order, as the loop reissues them (the loop's static waits assume it)
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    load(d, ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int c0 = 0; c0 < nch; c0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      step(c0 + d, ring[d]);
+      load(c0 + d + DEPTH, ring[d]);   // past the end: re-reads the last step
+    }
+  }
+
+  // lane (lr, lg) holds rows 4 lg .. 4 lg + 3 of tile t0 + rt, column 16 mb + lr
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    uint32_t sd[2];
+    load_dwords(a.scale + (t0 + rt) * 16 + 4 * lg, sd);
+#pragma unroll
+    for (int mb = 0; mb < kW8MidMB; ++mb) {
+      const int m = m0 + mb * 16 + lr;
+      if (m >= a.M) break;
+      const int n = (t0 + rt) * 16 + 4 * lg;
+      float y[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        y[i] = (float)__builtin_bit_cast(h16x2, sd[i / 2])[i & 1] *
+               __builtin_fmaf(xt[mb], -128.f, acc[rt][mb][i]);
+      if (a.out) {
+        uint32_t v[2] = {pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+        __builtin_memcpy(a.out + (size_t)m * a.N + n, v, sizeof(v));
+      } else {
+        *(f32x4*)(a.part + ((size_t)split * a.M + m) * a.N + n) = f32x4{y[0], y[1], y[2], y[3]};
+      }
+    }
+  }
+}
+
+template <int RT, int NW, int DEPTH>
+int launch_mid(const W8mPlan& p, const W8mArgs& a, hipStream_t st) {
+  w8b_mid_kernel<RT, NW, DEPTH><<<dim3((unsigned)p.groups, (unsigned)p.ksplit,
+                                       (unsigned)p.mblocks),
+                                  dim3(NW * kWave), p.lds, st>>>(a);
+  return ACORN_OK;
+}
+
 }  // namespace
 
 namespace acorn {
@@ -369,6 +565,73 @@ int w8b_launch(const DirectPlan& p, const void* x, const void* w, const void* sc
     case 1: rc = by_upw<1>(p, a, st); break;
     case 2: rc = by_upw<2>(p, a, st); break;
     case 4: rc = by_upw<4>(p, a, st); break;
+  }
+  if (rc) return rc;
+  ACORN_LAUNCH_CHECK();
+  return ACORN_OK;
+}
+
+// Knobs as the int4 mid-M kernel's: rt (16-row tiles per wave) 1 or 2, nw
+// (waves) 4 or 8, ksplit, depth (128-k steps in flight) 2 or 4; N a whole
+// number of NW * RT * 16 row blocks, K of 128-k steps, and each split's step
+// count of depth rounds. With ksplit 0 the split grows from 1 while the launch
+// has fewer workgroups than 256 and each split keeps 4 depth rounds.
+int w8m_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, W8mPlan* p) {
+  if (M < 1 || M > 65535 * (int64_t)kW8MidBM) return ACORN_ERR_SHAPE;
+  if (K % 128) return ACORN_ERR_SHAPE;
+  const int rt = cfg && cfg[1] > 0 ? cfg[1] : 2;
+  const int nw = cfg && cfg[2] > 0 ? cfg[2] : 8;
+  const int req_ks = cfg ? cfg[3] : 0;
+  const int depth = cfg && cfg[4] > 0 ? cfg[4] : 2;
+  if ((rt != 1 && rt != 2) || (nw != 4 && nw != 8) || (depth != 2 && depth != 4))
+    return ACORN_ERR_UNSUPPORTED;
+  const int64_t rows = (int64_t)nw * rt * 16;
+  if (N % rows) return ACORN_ERR_UNSUPPORTED;
+  const int64_t G = K / 128, groups = N / rows, mblocks = (M + kW8MidBM - 1) / kW8MidBM;
+  auto fits = [&](int64_t ks) { return ks >= 1 && G % ks == 0 && (G / ks) % depth == 0; };
+  int64_t ks;
+  if (req_ks > 0) {
+    ks = req_ks;
+    while (ks <= G && !fits(ks)) ++ks;
+    if (ks > G) return ACORN_ERR_UNSUPPORTED;
+  } else {
+    ks = 1;
+    if (!fits(1)) return ACORN_ERR_UNSUPPORTED;
+    while (groups * mblocks * ks < 256) {
+      int64_t nx = ks + 1;
+      while (nx <= G && !fits(nx)) ++nx;
+      if (nx > G || G / nx < 4 * depth) break;
+      ks = nx;
+    }
+  }
+  if (groups > 0x7fffffff || ks > 65535 || mblocks > 65535) return ACORN_ERR_SHAPE;
+  p->rt = rt;
+  p->nw = nw;
+  p->ksplit = (int)ks;
+  p->depth = depth;
+  p->groups = (int)groups;
+  p->mblocks = (int)mblocks;
+  p->lds = (size_t)2 * 16 * kW8MidXP * 16 + (size_t)2 * kW8MidBM * 4;
+  return ACORN_OK;
+}
+
+int w8m_launch(const W8mPlan& p, const void* x, const void* w, const void* scale, void* out,
+               float* part, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+  if (!x || !w || !scale) return ACORN_ERR_VALUE;
+  if (p.ksplit > 1) out = nullptr;
+  if (!out && !part) return ACORN_ERR_VALUE;
+  const W8mArgs a{(const __bf16*)x, (const uint8_t*)w, (const _Float16*)scale, (__bf16*)out,
+                  part, (int)M, (int)N, (int)K, (int)(K / p.ksplit)};
+  int rc = ACORN_ERR_UNSUPPORTED;
+  switch (p.rt * 100 + p.nw * 10 + p.depth) {
+    case 142: rc = launch_mid<1, 4, 2>(p, a, st); break;
+    case 144: rc = launch_mid<1, 4, 4>(p, a, st); break;
+    case 182: rc = launch_mid<1, 8, 2>(p, a, st); break;
+    case 184: rc = launch_mid<1, 8, 4>(p, a, st); break;
+    case 242: rc = launch_mid<2, 4, 2>(p, a, st); break;
+    case 244: rc = launch_mid<2, 4, 4>(p, a, st); break;
+    case 282: rc = launch_mid<2, 8, 2>(p, a, st); break;
+    case 284: rc = launch_mid<2, 8, 4>(p, a, st); break;
   }
   if (rc) return rc;
   ACORN_LAUNCH_CHECK();

@@ -42,7 +42,7 @@ _CLS_BY_SHAPE = {v: k for k, v in CLASSES.items()}
 
 DECODE_M_MAX = 16
 W4B_M_MAX = 64      # the int4 decode kernel takes up to this many rows on request
-MID_RT = -3         # Tiling.rt of the int4 mid-M kernel (W4B, M > 16)
+MID_RT = -3         # Tiling.rt of the mid-M kernels (W4B and W8B, M > 16)
 M_BUCKETS_LARGE = ("s", "m", "l")
 _M_REP_M = {"s": 64, "m": 256, "l": 1024}
 
@@ -85,14 +85,16 @@ class Tiling(NamedTuple):
     above), ksplit, and tpw = stages in flight per wave.
     int8 decode kernel (WFMT_W8B, M <= 16): rt row tiles per wave, upw 64-k
     blocks per stage, nw the wave layout (1, 4, 22, 44), ksplit,
-    tpw = stages in flight; above 16 rows W8B runs on the tiled kernel.
+    tpw = stages in flight; above 16 rows W8B runs on the tiled kernel or the
+    int8 mid-M kernel.
     bf16 decode kernel (WFMT_BF16B, M <= 16): rt row tiles per wave, upw
     32-k blocks per stage, nw the wave layout (1, 4, 22, 44), ksplit, tpw =
     stages in flight; above 16 rows BF16B runs on the tiled kernel and from
     256 rows on the large-M kernel (its direct-to-LDS and 64 / 128 forms).
-    int4 mid-M kernel (WFMT_W4B, M > 16, rt == -3): upw row tiles per wave
-    (1 / 2), nw waves (4 / 8), ksplit, tpw 128-k groups in flight (2 / 4);
-    64 x rows per workgroup, streamed through LDS a group at a time.
+    int4 / int8 mid-M kernels (WFMT_W4B / WFMT_W8B, M > 16, rt == -3): upw
+    row tiles per wave (1 / 2), nw waves (4 / 8), ksplit, tpw 128-k steps in
+    flight (2 / 4; 8 for the int4 one at one tile and 8 waves); 64 x rows per
+    workgroup, streamed through LDS 128 k at a time.
     Large-M bf16 kernel (the default for bf16 from 256 rows, or rt == -2):
     upw is the M tile. 64 / 128: nw the weight rows per wave (64 / 128; a
     workgroup's weight tile is 4 nw), tpw the weight prefetch depth in 64-k
@@ -337,8 +339,8 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
         reqs = [r for r in reqs if r.rt > 0]      # rt 0 means the tiled kernel here
         if wfmt == WFMT_W4B and M <= W4B_M_MAX:
             reqs = _w4b_wide_requests()           # the int4 kernel with 2 or 4 x blocks
-        if wfmt == WFMT_W4B:
-            reqs += [Tiling(MID_RT, rt, nw, ks, depth)   # the mid-M int4 kernel
+        if wfmt in (WFMT_W4B, WFMT_W8B):
+            reqs += [Tiling(MID_RT, rt, nw, ks, depth)   # the mid-M int4 / int8 kernels
                      for rt in (1, 2) for nw in (4, 8) for depth in (2, 4, 8)
                      for ks in (0, 1, 2, 4, 8, 16)]
         for bm in (32, 64, 128):

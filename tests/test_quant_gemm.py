@@ -431,6 +431,37 @@ def test_w4b_mid_kernel_matches(m):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m", [17, 64, 100, 256])
+def test_w8b_mid_kernel_matches(m):
+    """The int8 mid-M kernel (x through LDS 128 k at a time, 64 x rows per
+    workgroup, the -128 X correction from per-step column sums) at every
+    tiling the sweep offers it, on the qkv shape (N = 6144) and the down
+    shape (K = 12288), against the dequantised matmul (norm-wise GEMM_REL and
+    the reference's per-class elementwise TOL_W8); one split and four agree
+    up to fp32 summation order."""
+    from acorninfer_amd._lib import WFMT_W8B
+    from acorninfer_amd.ops.quant_gemm import MID_RT, Tiling, _launch, candidates
+    from acorninfer_amd.quant.quantize import to_w8b
+    for cls in ("qkv", "down"):
+        q, s, wref = _w8(cls)
+        wb = to_w8b(q)
+        n, k = SHAPES[cls]
+        x = _x(m, k, 14)
+        ref = _ref(x, wref)
+        cands = [c for c in candidates(m, n, k, WFMT_W8B) if c.rt == MID_RT]
+        assert len(cands) >= 8, len(cands)
+        for c in cands:
+            out = _launch(x, wb, s, None, WFMT_W8B, n, c, None)
+            r = rel_err(out, ref)
+            assert r <= GEMM_REL, f"{cls} M={m} {tuple(c)}: rel err {r:.3g}"
+            torch.testing.assert_close(out.float(), ref, **TOL_W8[cls])
+        one = _launch(x, wb, s, None, WFMT_W8B, n, Tiling(MID_RT, 2, 4, 1, 2), None)
+        four = _launch(x, wb, s, None, WFMT_W8B, n, Tiling(MID_RT, 2, 4, 4, 2), None)
+        assert rel_err(one, four) <= 1e-3      # bf16 outputs: a few one-ulp flips
+        print(f"\n[w8b mid M={m} {cls}: {len(cands)} tilings ok]")
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("cls", ["qkv", "down"])
 def test_dequant_w4b_bitwise(cls):
     """acorn_dequant_w4b writes the oracle's fp32 dequantised weight ((u - 8)
