@@ -293,12 +293,13 @@ int divisor_at_least(int64_t n, int64_t v) {
 //  * every thread loads its share of the step's x (2 or 4 pieces of 16 bytes)
 //    and each wave its RT x 2 weight blocks, DEPTH steps ahead in a register
 //    ring (a step's loads are issued together, in step order);
-//  * per step: the x pieces go to LDS (two buffers), one barrier, four waves
-//    form the step's column sums of x (MFMAs against ones) for the -128 X
-//    correction, a second barrier, then each wave unpacks each weight block
-//    once (q + 128 -> bf16, exact) and runs RT x 2 x 2 x 4 MFMAs: every
-//    unpacked operand feeds the four column blocks, every x operand the RT
-//    tiles;
+//  * per step: one barrier, then four waves form the step's column sums of x
+//    (MFMAs against ones) for the -128 X correction, each wave unpacks each
+//    weight block once (q + 128 -> bf16, exact) and runs RT x 2 x 2 x 4 MFMAs
+//    (every unpacked operand feeds the four column blocks, every x operand
+//    the RT tiles), and the next step's x pieces go to the other LDS buffer;
+//    the column sums are added to the running ones a step later, after the
+//    next barrier;
 //  * y = s[n] (C - 128 X) at the end, C the MFMA sum over the biased weights
 //    and X each column's sum of x over the K range, added up per step in
 //    fp32; split-K partials as everywhere else: fp32 [ksplit, M, N] of the
@@ -387,22 +388,31 @@ __global__ __launch_bounds__(NW * kWave, 1) void w8b_mid_kernel(W8mArgs a) {
   for (int mb = 0; mb < kW8MidMB; ++mb) xt[mb] = 0.f;
   const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
 
-  auto step = [&](int c, const Slot& sl) {
-    const int b = c & 1;
-    u32x4* xb = xs + b * 16 * kW8MidXP;
+  auto store_x = [&](int c, const Slot& sl) {
+    u32x4* xb = xs + (c & 1) * 16 * kW8MidXP;
 #pragma unroll
     for (int u = 0; u < XPT; ++u) {
       const int p = (int)threadIdx.x + NT * u;
       xb[(p % 16) * kW8MidXP + p / 16] = sl.x[u];
     }
+  };
+  // One barrier per step: x of step c was stored at the end of step c - 1
+  // (into the other buffer than the one step c - 1 read), and the column sums
+  // of step c are formed during step c and added during step c + 1.
+  auto step = [&](int c, const Slot& sl, const Slot& next) {
+    const int b = c & 1;
+    const u32x4* xb = xs + b * 16 * kW8MidXP;
     __syncthreads();
+    if (c > 0) {
+#pragma unroll
+      for (int mb = 0; mb < kW8MidMB; ++mb) xt[mb] += xsum[(b ^ 1) * kW8MidBM + mb * 16 + lr];
+    }
     if (wid < kW8MidMB) {
       f32x4 xg = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < 4; ++j) xg = mfma(ones, xb[(4 * lg + j) * kW8MidXP + wid * 16 + lr], xg);
       if (lg == 0) xsum[b * kW8MidBM + wid * 16 + lr] = xg[0];
     }
-    __syncthreads();
     // block u, MFMA j: the lane's k slots stand for k 64 u + 16 lg + 8 j ..,
     // i.e. x piece 8 u + 2 lg + j of the step
     u32x4 aw[RT][2][2];
@@ -421,7 +431,6 @@ __global__ __launch_bounds__(NW * kWave, 1) void w8b_mid_kernel(W8mArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
           bx[u][j] = xb[(8 * u + 2 * lg + j) * kW8MidXP + mb * 16 + lr];
-      xt[mb] += xsum[b * kW8MidBM + mb * 16 + lr];
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -429,6 +438,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void w8b_mid_kernel(W8mArgs a) {
 #pragma unroll
           for (int j = 0; j < 2; ++j) acc[rt][mb] = mfma(aw[rt][u][j], bx[u][j], acc[rt][mb]);
     }
+    if (c + 1 < nch) store_x(c + 1, next);
   };
 
   Slot ring[DEPTH];
@@ -438,13 +448,17 @@ __global__ __launch_bounds__(NW * kWave, 1) void w8b_mid_kernel(W8mArgs a) {
     load(d, ring[d]);
     __builtin_amdgcn_sched_barrier(0);
   }
+  store_x(0, ring[0]);
   for (int c0 = 0; c0 < nch; c0 += DEPTH) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      step(c0 + d, ring[d]);
+      step(c0 + d, ring[d], ring[(d + 1) % DEPTH]);
       load(c0 + d + DEPTH, ring[d]);   // past the end: re-reads the last step
     }
   }
+  __syncthreads();                     // the last step's column sums
+#pragma unroll
+  for (int mb = 0; mb < kW8MidMB; ++mb) xt[mb] += xsum[((nch - 1) & 1) * kW8MidBM + mb * 16 + lr];
 
   // lane (lr, lg) holds rows 4 lg .. 4 lg + 3 of tile t0 + rt, column 16 mb + lr
 #pragma unroll
