@@ -149,7 +149,10 @@ int acorn_qkv_epilogue(const float* part, int64_t nsplit, void* q_out, void* k_p
  * int32; seq_lens: [B] int32 (>= 1, includes the current token);
  * out: [B, H, D]. Token t of sequence b lives at (tables[b, t/P], t%P);
  * q head h reads kv head h / (H/KV). One workgroup serves all H/KV q heads of
- * a kv head (GQA reuse). Workspace: ws_acc [B*H*num_splits*D] fp32 and
+ * a kv head (GQA reuse); with bf16/fp16 activations, D >= 64, num_splits == 1
+ * over at most 64 pages and fewer (sequence, kv head) pairs than half the 256
+ * CUs, the launch gives the q heads of a kv head up to H/KV workgroups of their
+ * own instead (no partials, no combine). Workspace: ws_acc [B*H*num_splits*D] fp32 and
  * ws_ml [2*B*H*num_splits] fp32, caller-owned (bf16/fp16 activations with
  * D >= 64 keep each split's normalised output there in fp16, using half of it).
  */
@@ -190,7 +193,8 @@ int acorn_paged_attention_noalloc(const void* q, const void* k_pages, const void
  * acorn_qkv_epilogue does, and attends to them. Arguments are those of the
  * two entry points (tables/seq_lens/out/ws as in acorn_paged_attention,
  * part..inv_freq as in acorn_qkv_epilogue, positions int64); the results are
- * the same bits. No single reference function: qwen3.py:180-192, then
+ * the same bits (one split over a small batch: every q head group's
+ * workgroup stores the same new k, v). No single reference function: qwen3.py:180-192, then
  * cache/pager.py:87-113 (scatter_decode), then paged_attention.py:125-152.
  * Returns ACORN_ERR_UNSUPPORTED, launching nothing, unless
  * acorn_paged_attention_qkv_supported() holds for the shape.
