@@ -232,8 +232,11 @@ int acorn_paged_prefill_attention(const void* q, const void* k_pages, const void
 /*
  * 1 when acorn_paged_attention_qkv supports the shape: bf16 or fp16
  * activations with norm weights of the same dtype, D in {64, 128}, H/KV in
- * {1, 2, 4, 8}, pages of a multiple of 16 tokens and splits of at most 16
- * pages (ceil(table_stride / num_splits)); else 0. No reference counterpart.
+ * {1, 2, 4, 8}, pages of a power-of-two multiple of 16 tokens, and splits
+ * (ceil(table_stride / num_splits) pages) of at most 16 pages or of a size
+ * whose eight-wave workgroup fits the 160 KB of LDS (block ids, which grow
+ * with the split, wave partials, K slabs, the epilogue's rows); else 0. No
+ * reference counterpart.
  */
 int acorn_paged_attention_qkv_supported(int64_t H, int64_t KV, int64_t D, int64_t P,
                                         int64_t table_stride, int64_t num_splits, int dtype,
