@@ -278,6 +278,7 @@ struct W4bPlan {
   size_t lds;      // dynamic LDS bytes
   bool swiglu;
   int mode;        // the direct kernel: 0 plain, 1 NormIn, 2 ResidOut (as DirectPlan)
+  bool hx;         // the direct kernel's paired-x form (M <= 8, upw 2)
 };
 int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4bPlan* p);
 // out (bf16 [M,N], or act [M,N/2] for swiglu) when given and ksplit == 1;

@@ -51,12 +51,23 @@ struct W4dArgs {
   ResidOut ro;    // MODE 2: the residual epilogue (gemm_common.h)
 };
 
-template <int RT, int UPW>
+template <int RT, int UPW, bool HX>
 struct DStage {
   u32x4 w[RT][UPW];          // unit (rt, u): this lane's 16 bytes of block (tile, group)
-  u32x4 x[UPW][4];           // B operand of MFMA j of group u: x row lr, k 32 lg + 8 j ..
+  // B operand of MFMA j of group u: x row lr, k 32 lg + 8 j .. (HX: of group
+  // pair u / 2, lanes lr < 8 holding the even group and lr >= 8 the odd one)
+  u32x4 x[HX ? UPW / 2 : UPW][4];
   uint32_t s[RT][2 * UPW];   // fp16 scales: half 4u + i is row 4 lg + i of group u
 };
+
+// lane l gets lane (l + 8) mod 16 of its 16-lane row (DPP row rotate by 8)
+__device__ __forceinline__ u32x4 rot8(const u32x4& v) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v[i], 0x128, 0xF, 0xF, false);
+  return r;
+}
 
 // bf16 -136 in every slot: an MFMA of it against x gives -136 X per column
 constexpr uint32_t kNeg136x2 = 0xC308C308u;
@@ -67,12 +78,17 @@ constexpr uint32_t kNeg136x2 = 0xC308C308u;
 // without split-K partials: they add their results through LDS in fixed
 // order at the end). Each wave keeps DEPTH stages of UPW groups in flight.
 // Lane (lr, lg) holds x row min(lr, M - 1) (rows past M feed only columns
-// that are never stored).
-template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU, int MODE>
+// that are never stored). HX (M <= 8, UPW even): a wave's x loads carry two
+// groups at once, lanes lr < 8 the even group's rows and lr >= 8 the odd
+// one's; the odd group's operand is the same registers rotated by 8 lanes
+// (its columns 8..15 then hold the even group's x: never stored). Half the x
+// loads and x registers, four DPP moves per operand.
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU, int MODE, bool HX = false>
 __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) {
   constexpr int NW = RG * KW;
   constexpr bool NORM = MODE == 1;
   static_assert(MODE != 2 || !SWIGLU, "the residual epilogue replaces a plain output");
+  static_assert(!HX || UPW % 2 == 0, "x in group pairs");
   const int wid = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int lg = lane >> 4, lr = lane & 15;
   const int rg = wid / KW, kq = wid % KW;
@@ -85,13 +101,15 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
   const unsigned g0 = (unsigned)(kw0 / 128);
   const int ns = GW / UPW;                        // stages, a multiple of DEPTH
   const uint8_t* wb = a.w + ((size_t)tt * G + g0) * 1024 + lane * 16;
-  const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 32 * lg;
+  const __bf16* xb = HX ? a.x + (size_t)min(lr & 7, a.M - 1) * a.K + kw0 + 32 * lg + 128 * (lr >> 3)
+                        : a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 32 * lg;
   const _Float16* sb = a.scale + (size_t)tt * G4 * 64 + lg * 16;
-  auto load = [&](int s, DStage<RT, UPW>& r) {
+  auto load = [&](int s, DStage<RT, UPW, HX>& r) {
 #pragma unroll
-    for (int u = 0; u < UPW; ++u)
+    for (int u = 0; u < (HX ? UPW / 2 : UPW); ++u)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) r.x[u][j] = *(const u32x4*)(xb + (s * UPW + u) * 128 + 8 * j);
+      for (int j = 0; j < 4; ++j)
+        r.x[u][j] = *(const u32x4*)(xb + (s * UPW + (HX ? 2 * u : u)) * 128 + 8 * j);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -105,7 +123,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
 
   NormRegs nr;
   if constexpr (NORM) norm_issue(a.ni, a.M, lane, nr);
-  DStage<RT, UPW> ring[DEPTH];
+  DStage<RT, UPW, HX> ring[DEPTH];
   // The first stages are issued in stage order, as the loop reissues them.
   // Left free, the scheduler moves every stage's scale load after the last
   // stage's weights; loads complete in order, so the loop's (static) wait
@@ -121,10 +139,12 @@ __global__ __launch_bounds__(RG * KW * kWave) void w4b_direct_kernel(W4dArgs a) 
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const u32x4 neg136 = {kNeg136x2, kNeg136x2, kNeg136x2, kNeg136x2};
-  auto compute = [&](const DStage<RT, UPW>& r) {
+  auto compute = [&](const DStage<RT, UPW, HX>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
-      const u32x4 (&xu)[4] = r.x[u];
+      u32x4 xu[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xu[j] = HX && (u & 1) ? rot8(r.x[u / 2][j]) : r.x[HX ? u / 2 : u][j];
       f32x4 xb136 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < 4; ++j) xb136 = mfma(neg136, xu[j], xb136);
@@ -613,26 +633,46 @@ size_t w4b_lds(int R, int64_t kr, int nw, int kw, int rt, int mb) {
 }
 
 // ---- launchers: the direct kernel (M <= 16) ---------------------------------
-template <int RT, int UPW, int DEPTH, int RG, int KW>
-int launch_direct(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
+// registers of one stage (dwords per lane): weights, x operands (HX: half),
+// scales
+constexpr int direct_stage_dwords(int rt, int upw, bool hx = false) {
+  return 4 * rt * upw + 16 * (hx ? upw / 2 : upw) + 2 * rt * upw;
+}
+constexpr int kDirectRingDwords = 160;   // the ring's budget (depth x stage)
+
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool HX>
+int launch_direct_x(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(RG * KW * kWave);
   if constexpr (RT >= 2) {
     if (p.swiglu) {
       if (p.mode == 1)
-        w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 1><<<grid, block, 0, st>>>(a);
+        w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 1, HX><<<grid, block, 0, st>>>(a);
       else
-        w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 0><<<grid, block, 0, st>>>(a);
+        w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 0, HX><<<grid, block, 0, st>>>(a);
       return ACORN_OK;
     }
   }
   if (p.swiglu) return ACORN_ERR_UNSUPPORTED;
   switch (p.mode) {
-    case 0: w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 0><<<grid, block, 0, st>>>(a); break;
-    case 1: w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 1><<<grid, block, 0, st>>>(a); break;
-    case 2: w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 2><<<grid, block, 0, st>>>(a); break;
+    case 0: w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 0, HX><<<grid, block, 0, st>>>(a); break;
+    case 1: w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 1, HX><<<grid, block, 0, st>>>(a); break;
+    case 2: w4b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 2, HX><<<grid, block, 0, st>>>(a); break;
     default: return ACORN_ERR_UNSUPPORTED;
   }
   return ACORN_OK;
+}
+
+// the paired-x form where the plan asks for it (M <= 8, two groups per stage),
+// each form only within the ring's budget
+template <int RT, int UPW, int DEPTH, int RG, int KW>
+int launch_direct(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
+  if constexpr (UPW % 2 == 0 && DEPTH * direct_stage_dwords(RT, UPW, true) <= kDirectRingDwords) {
+    if (p.hx) return launch_direct_x<RT, UPW, DEPTH, RG, KW, true>(p, a, st);
+  }
+  if constexpr (DEPTH * direct_stage_dwords(RT, UPW) <= kDirectRingDwords) {
+    if (!p.hx) return launch_direct_x<RT, UPW, DEPTH, RG, KW, false>(p, a, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
 }
 
 // wave layouts (the nw field): 1 or 4 waves on their own rows, or 10 nw + kw
@@ -652,17 +692,13 @@ int direct_nw(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
   return ACORN_ERR_UNSUPPORTED;
 }
 
-// registers of one stage (dwords per lane): weights, x operands, scales
-constexpr int direct_stage_dwords(int rt, int upw) { return 4 * (rt + 4) * upw + 2 * rt * upw; }
-constexpr int kDirectRingDwords = 160;   // the ring's budget (depth x stage)
-
 template <int RT, int UPW>
 int direct_depth(const W4bPlan& p, const W4dArgs& a, hipStream_t st) {
   switch (p.depth) {
     case 1: return direct_nw<RT, UPW, 1>(p, a, st);
     case 2: return direct_nw<RT, UPW, 2>(p, a, st);
     case 4:
-      if constexpr (4 * direct_stage_dwords(RT, UPW) <= kDirectRingDwords)
+      if constexpr (4 * direct_stage_dwords(RT, UPW, UPW % 2 == 0) <= kDirectRingDwords)
         return direct_nw<RT, UPW, 4>(p, a, st);
       break;
   }
@@ -745,7 +781,8 @@ int divisor_at_least(int64_t n, int64_t v) {
 
 // M <= 16: rt 1/2/4 (swiglu 2/4; N/16 divisible by rt), upw 1/2, the wave
 // layout in the nw field (1 or 4 waves on their own rows; 22, 44, 84, 88 = nw
-// waves in nw / kw row groups of kw K slices), depth 1/2/4 within the ring's
+// waves in nw / kw row groups of kw K slices; at M <= 8 upw 2 takes the
+// paired-x form, whose smaller stages fit deeper rings), depth 1/2/4 within the ring's
 // register budget, and split counts that give every wave a whole number of
 // depth rounds. With 0 the plan takes rt 2, upw 1, one wave per workgroup,
 // depth 4, and the fewest splits that launch at least three waves per CU.
@@ -765,7 +802,9 @@ int direct_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4
     return ACORN_ERR_UNSUPPORTED;
   const int nw = nwf < 10 ? nwf : nwf / 10, kw = nwf < 10 ? 1 : nwf % 10;
   if (depth != 1 && depth != 2 && depth != 4) return ACORN_ERR_UNSUPPORTED;
-  while (depth > 1 && (depth * direct_stage_dwords(rt, upw) > kDirectRingDwords ||
+  // M <= 8 with two groups per stage: the paired-x form (half the x registers)
+  const bool hx = M <= 8 && upw == 2;
+  while (depth > 1 && (depth * direct_stage_dwords(rt, upw, hx) > kDirectRingDwords ||
                        G % (kw * upw * depth)))
     depth /= 2;
   // K % 512 == 0 makes the default (kw = upw = depth = 1) always fit: what
@@ -804,6 +843,7 @@ int direct_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, W4
   p->lds = 0;
   p->swiglu = swiglu;
   p->mode = 0;
+  p->hx = hx;
   return ACORN_OK;
 }
 
@@ -885,6 +925,7 @@ int w4b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   p->lds = lds(ks);
   p->swiglu = false;
   p->mode = 0;
+  p->hx = false;
   if (groups > 0x7fffffff || ks > 65535) return ACORN_ERR_SHAPE;
   return ACORN_OK;
 }

@@ -358,13 +358,14 @@ def candidates(M: int, N: int, K: int, wfmt: int, swiglu: bool = False) -> list[
 def _w4b_requests(swiglu: bool) -> list[Tiling]:
     """Requests covering the int4 direct kernel's knobs (M <= 16): 1, 2 or 4
     row tiles per wave, one group per stage with 2 or 4 stages in flight or
-    two groups with 2, one or four waves per workgroup on their own rows or 2,
+    two groups with 2 or 4 (4 where the paired-x form of M <= 8 fits it), one
+    or four waves per workgroup on their own rows or 2,
     4 or 8 K slices over shared rows (22, 44, 84 = two row groups of four
     slices, 88), and split counts from one to sixteen (the fused SwiGLU runs
     in one split)."""
     reqs = []
     for rt in ((2, 4) if swiglu else (1, 2, 4)):
-        for upw, depth in ((1, 2), (1, 4), (2, 2)):
+        for upw, depth in ((1, 2), (1, 4), (2, 2), (2, 4)):
             for nw in (1, 4, 22, 44, 84, 88):
                 for ks in ((1,) if swiglu else (0, 1, 2, 3, 4, 6, 8, 12, 16)):
                     reqs.append(Tiling(rt, upw, nw, ks, depth))

@@ -120,7 +120,7 @@ def test_planner_w4b_decode(M, N, K):
     reqs = [(0, 0, 0, 0, 0), (4, 1, 1, 0, 4), (1, 2, 4, 3, 2), (2, 2, 4, 5, 4), (2, 1, 1, 1, 4),
             (4, 2, 1, 2, 2), (1, 1, 4, 16, 1), (2, 1, 2, 0, 4), (1, 4, 1, 0, 2), (2, 1, 44, 1, 4),
             (2, 2, 84, 2, 2), (4, 1, 22, 0, 4), (2, 1, 42, 1, 2), (1, 1, 88, 1, 4),
-            (1, 2, 88, 1, 2), (2, 1, 84, 0, 4)]
+            (1, 2, 88, 1, 2), (2, 1, 84, 0, 4), (1, 2, 44, 1, 4), (2, 2, 1, 1, 4)]
     for r in reqs:
         cfg = (ctypes.c_int * 6)(*r, 0)
         rc = lib.acorn_gemm_plan(M, N, K, _lib.WFMT_W4B, cfg)
@@ -133,7 +133,9 @@ def test_planner_w4b_decode(M, N, K):
         kw = 1 if nwf < 10 else nwf % 10
         assert rt in (1, 2, 4) and (N // 16) % rt == 0
         assert upw in (1, 2) and depth in (1, 2, 4)
-        assert depth * (4 * (rt + 4) * upw + 2 * rt * upw) <= 160
+        # x registers per stage: 16 per group, half in the paired-x form (M <= 8, upw 2)
+        xd = 16 * (upw // 2 if M <= 8 and upw == 2 else upw)
+        assert depth * (4 * rt * upw + xd + 2 * rt * upw) <= 160
         groups = K // 128
         assert groups % (ks * kw) == 0 and (groups // ks // kw) % (upw * depth) == 0
         if r[3] == 0:
