@@ -309,6 +309,7 @@ int bf16b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu
   p->groups = (int)groups;
   p->swiglu = swiglu;
   p->mode = 0;
+  p->hx = false;
   return ACORN_OK;
 }
 

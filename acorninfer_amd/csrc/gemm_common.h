@@ -63,6 +63,19 @@ __device__ __forceinline__ void load_dwords(const void* p, uint32_t (&d)[NDW]) {
   }
 }
 
+// Lane l gets lane (l + 8) mod 16 of its 16-lane row (DPP row rotate by 8):
+// the paired-x form of the direct kernels (M <= 8) loads two k blocks of x
+// with one instruction, lanes 0..7 the first block's rows and 8..15 the
+// second's, and rotates the second into lanes 0..7 for its MFMAs (columns
+// 8..15 of an MFMA then hold the other block's x: outputs never stored).
+__device__ __forceinline__ u32x4 rot8(const u32x4& v) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v[i], 0x128, 0xF, 0xF, false);
+  return r;
+}
+
 // s_h * v + acc in fp32, s_h the fp16 number h of a run of packed halves
 // (exactly converted, one rounding): the compiler makes it one v_fma_mix_f32
 // that selects the half of the packed dword itself (op_sel), so no shift
@@ -326,6 +339,7 @@ struct DirectPlan {
   int groups;      // workgroups along N
   bool swiglu;
   int mode;        // 0 plain, 1 rows scaled by 1 / rms (NormIn), 2 residual epilogue (ResidOut)
+  bool hx;         // the paired-x form (M <= 8, upw 2; see rot8)
 };
 int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, DirectPlan* p);
 // out (bf16 [M,N], or act [M,N/2] for swiglu) when given and ksplit == 1;

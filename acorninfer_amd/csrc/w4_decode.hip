@@ -60,15 +60,6 @@ struct DStage {
   uint32_t s[RT][2 * UPW];   // fp16 scales: half 4u + i is row 4 lg + i of group u
 };
 
-// lane l gets lane (l + 8) mod 16 of its 16-lane row (DPP row rotate by 8)
-__device__ __forceinline__ u32x4 rot8(const u32x4& v) {
-  u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    r[i] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v[i], 0x128, 0xF, 0xF, false);
-  return r;
-}
-
 // bf16 -136 in every slot: an MFMA of it against x gives -136 X per column
 constexpr uint32_t kNeg136x2 = 0xC308C308u;
 

@@ -43,10 +43,12 @@ struct W8dArgs {
   ResidOut ro;    // MODE 2
 };
 
-template <int RT, int UPW>
+template <int RT, int UPW, bool HX>
 struct W8Stage {
   u32x4 w[RT][UPW];          // block (tile rt, block u): this lane's 16 bytes
-  u32x4 x[UPW][2];           // B operand of MFMA j of block u: x row lr, k 16 lg + 8 j ..
+  // B operand of MFMA j of block u: x row lr, k 16 lg + 8 j .. (HX: of block
+  // pair u / 2, lanes lr < 8 the even block's rows, lr >= 8 the odd one's)
+  u32x4 x[HX ? UPW / 2 : UPW][2];
 };
 
 // bf16 -128 in every slot: an MFMA of it against x gives -128 X per column
@@ -66,8 +68,10 @@ __device__ __forceinline__ u32x4 unpack_w8(uint32_t a, uint32_t b) {
 // waves. Row group r of workgroup b owns tiles (b RG + r) RT .. + RT - 1; its
 // KW waves split the split's K range. Lane (lr, lg) holds x row min(lr, M - 1)
 // (rows past M feed only columns that are never stored).
-template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU, int MODE>
+// HX (M <= 8, UPW even): the paired-x form (gemm_common.h, rot8).
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU, int MODE, bool HX = false>
 __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) {
+  static_assert(!HX || UPW % 2 == 0, "x in block pairs");
   constexpr int NW = RG * KW;
   constexpr bool NORM = MODE == 1;
   static_assert(MODE != 2 || !SWIGLU, "the residual epilogue replaces a plain output");
@@ -82,12 +86,14 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
   const int kw0 = blockIdx.y * a.kr + kq * BW * 64;
   const int ns = BW / UPW;                        // stages, a multiple of DEPTH
   const uint8_t* wb = a.w + ((size_t)tt * KB + kw0 / 64) * 1024 + lane * 16;
-  const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 16 * lg;
-  auto load = [&](int s, W8Stage<RT, UPW>& r) {
+  const __bf16* xb = HX ? a.x + (size_t)min(lr & 7, a.M - 1) * a.K + kw0 + 16 * lg + 64 * (lr >> 3)
+                        : a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 16 * lg;
+  auto load = [&](int s, W8Stage<RT, UPW, HX>& r) {
 #pragma unroll
-    for (int u = 0; u < UPW; ++u)
+    for (int u = 0; u < (HX ? UPW / 2 : UPW); ++u)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) r.x[u][j] = *(const u32x4*)(xb + (s * UPW + u) * 64 + 8 * j);
+      for (int j = 0; j < 2; ++j)
+        r.x[u][j] = *(const u32x4*)(xb + (s * UPW + (HX ? 2 * u : u)) * 64 + 8 * j);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -97,7 +103,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
 
   NormRegs nr;
   if constexpr (NORM) norm_issue(a.ni, a.M, lane, nr);
-  W8Stage<RT, UPW> ring[DEPTH];
+  W8Stage<RT, UPW, HX> ring[DEPTH];
   // in stage order, as the loop reissues them (the loop's static waits assume
   // that order; left free, the scheduler reorders the first stages' loads)
 #pragma unroll
@@ -112,10 +118,12 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
   f32x4 xacc = {0.f, 0.f, 0.f, 0.f};             // -128 X over the wave's K range
   const u32x4 neg128 = {kNeg128x2, kNeg128x2, kNeg128x2, kNeg128x2};
-  auto compute = [&](const W8Stage<RT, UPW>& r) {
+  auto compute = [&](const W8Stage<RT, UPW, HX>& r) {
 #pragma unroll
     for (int u = 0; u < UPW; ++u) {
-      const u32x4 (&xu)[2] = r.x[u];
+      u32x4 xu[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) xu[j] = HX && (u & 1) ? rot8(r.x[u / 2][j]) : r.x[HX ? u / 2 : u][j];
 #pragma unroll
       for (int j = 0; j < 2; ++j) xacc = mfma(neg128, xu[j], xacc);
 #pragma unroll
@@ -217,26 +225,45 @@ __global__ __launch_bounds__(RG * KW * kWave) void w8b_direct_kernel(W8dArgs a) 
   }
 }
 
-template <int RT, int UPW, int DEPTH, int RG, int KW>
-int launch(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
+// registers of one stage (dwords per lane): weights and x operands (HX: half)
+constexpr int stage_dwords(int rt, int upw, bool hx = false) {
+  return 4 * rt * upw + 8 * (hx ? upw / 2 : upw);
+}
+constexpr int kRingDwords = 192;   // the ring's budget (depth x stage)
+
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool HX>
+int launch_x(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(RG * KW * kWave);
   if constexpr (RT >= 2) {
     if (p.swiglu) {
       if (p.mode == 1)
-        w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 1><<<grid, block, 0, st>>>(a);
+        w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 1, HX><<<grid, block, 0, st>>>(a);
       else
-        w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 0><<<grid, block, 0, st>>>(a);
+        w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 0, HX><<<grid, block, 0, st>>>(a);
       return ACORN_OK;
     }
   }
   if (p.swiglu) return ACORN_ERR_UNSUPPORTED;
   switch (p.mode) {
-    case 0: w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 0><<<grid, block, 0, st>>>(a); break;
-    case 1: w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 1><<<grid, block, 0, st>>>(a); break;
-    case 2: w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 2><<<grid, block, 0, st>>>(a); break;
+    case 0: w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 0, HX><<<grid, block, 0, st>>>(a); break;
+    case 1: w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 1, HX><<<grid, block, 0, st>>>(a); break;
+    case 2: w8b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 2, HX><<<grid, block, 0, st>>>(a); break;
     default: return ACORN_ERR_UNSUPPORTED;
   }
   return ACORN_OK;
+}
+
+// the paired-x form where the plan asks for it, each form only within the
+// ring's budget
+template <int RT, int UPW, int DEPTH, int RG, int KW>
+int launch(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
+  if constexpr (UPW % 2 == 0 && DEPTH * stage_dwords(RT, UPW, true) <= kRingDwords) {
+    if (p.hx) return launch_x<RT, UPW, DEPTH, RG, KW, true>(p, a, st);
+  }
+  if constexpr (DEPTH * stage_dwords(RT, UPW) <= kRingDwords) {
+    if (!p.hx) return launch_x<RT, UPW, DEPTH, RG, KW, false>(p, a, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
 }
 
 template <int RT, int UPW, int DEPTH>
@@ -250,20 +277,19 @@ int by_layout(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
   return ACORN_ERR_UNSUPPORTED;
 }
 
-// registers of one stage (dwords per lane): weights and x operands
-constexpr int stage_dwords(int rt, int upw) { return 4 * rt * upw + 8 * upw; }
-constexpr int kRingDwords = 192;   // the ring's budget (depth x stage)
-
 template <int RT, int UPW>
 int by_depth(const DirectPlan& p, const W8dArgs& a, hipStream_t st) {
+  constexpr bool kPair = UPW % 2 == 0;
   switch (p.depth) {
     case 1: return by_layout<RT, UPW, 1>(p, a, st);
     case 2: return by_layout<RT, UPW, 2>(p, a, st);
     case 4:
-      if constexpr (4 * stage_dwords(RT, UPW) <= kRingDwords) return by_layout<RT, UPW, 4>(p, a, st);
+      if constexpr (4 * stage_dwords(RT, UPW, kPair) <= kRingDwords)
+        return by_layout<RT, UPW, 4>(p, a, st);
       break;
     case 8:
-      if constexpr (8 * stage_dwords(RT, UPW) <= kRingDwords) return by_layout<RT, UPW, 8>(p, a, st);
+      if constexpr (8 * stage_dwords(RT, UPW, kPair) <= kRingDwords)
+        return by_layout<RT, UPW, 8>(p, a, st);
       break;
   }
   return ACORN_ERR_UNSUPPORTED;
@@ -522,7 +548,9 @@ int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   if (nwf != 1 && nwf != 4 && nwf != 22 && nwf != 44) return ACORN_ERR_UNSUPPORTED;
   const int nw = nwf < 10 ? nwf : nwf / 10, kw = nwf < 10 ? 1 : nwf % 10;
   if (depth != 1 && depth != 2 && depth != 4 && depth != 8) return ACORN_ERR_UNSUPPORTED;
-  while (depth > 1 && (depth * stage_dwords(rt, upw) > kRingDwords || KB % (kw * upw * depth)))
+  // M <= 8 with two blocks per stage: the paired-x form (half the x registers)
+  const bool hx = M <= 8 && upw == 2;
+  while (depth > 1 && (depth * stage_dwords(rt, upw, hx) > kRingDwords || KB % (kw * upw * depth)))
     depth /= 2;
   if (KB % (kw * upw * depth)) return ACORN_ERR_SHAPE;
   const int64_t q = KB / (kw * upw * depth);    // ks must divide this
@@ -554,6 +582,7 @@ int w8b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu, 
   p->groups = (int)groups;
   p->swiglu = swiglu;
   p->mode = 0;
+  p->hx = hx;
   return ACORN_OK;
 }
 

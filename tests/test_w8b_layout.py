@@ -93,7 +93,9 @@ def test_planner_w8b_decode(M, N, K):
         assert nwf in (1, 4, 22, 44)
         assert rt in (1, 2, 4) and (N // 16) % rt == 0
         assert upw in (1, 2) and depth in (1, 2, 4, 8)
-        assert depth * (4 * rt * upw + 8 * upw) <= 192
+        # x registers per stage: 8 per block, half in the paired-x form (M <= 8, upw 2)
+        xd = 8 * (upw // 2 if M <= 8 and upw == 2 else upw)
+        assert depth * (4 * rt * upw + xd) <= 192
         blocks = K // 64
         assert blocks % (ks * kw) == 0 and (blocks // ks // kw) % (upw * depth) == 0
         if r[3] == 0:
