@@ -44,18 +44,22 @@ struct BfdArgs {
   ResidOut ro;    // MODE 2
 };
 
-template <int RT, int UPW>
+template <int RT, int UPW, bool HX>
 struct BfdStage {
   u32x4 w[RT][UPW];          // block (tile rt, block u): this lane's 16 bytes
-  u32x4 x[UPW];              // B operand of block u: x row lr, k 8 lg .. 8 lg + 7
+  // B operand of block u: x row lr, k 8 lg .. 8 lg + 7 (HX: of block pair
+  // u / 2, lanes lr < 8 the even block's rows, lr >= 8 the odd one's)
+  u32x4 x[HX ? UPW / 2 : UPW];
 };
 
 // Grid: x = tile groups of RG * RT 16-row tiles, y = ksplit; block RG * KW
 // waves. Row group r of workgroup b owns tiles (b RG + r) RT .. + RT - 1; its
 // KW waves split the split's K range. Lane (lr, lg) holds x row min(lr, M - 1)
 // (rows past M feed only columns that are never stored).
-template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU, int MODE>
+// HX (M <= 8, UPW even): the paired-x form (gemm_common.h, rot8).
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool SWIGLU, int MODE, bool HX = false>
 __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a) {
+  static_assert(!HX || UPW % 2 == 0, "x in block pairs");
   constexpr int NW = RG * KW;
   constexpr bool NORM = MODE == 1;
   static_assert(MODE != 2 || !SWIGLU, "the residual epilogue replaces a plain output");
@@ -70,10 +74,12 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
   const int kw0 = blockIdx.y * a.kr + kq * BW * 32;
   const int ns = BW / UPW;                        // stages, a multiple of DEPTH
   const uint8_t* wb = a.w + ((size_t)tt * KB + kw0 / 32) * 1024 + lane * 16;
-  const __bf16* xb = a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 8 * lg;
-  auto load = [&](int s, BfdStage<RT, UPW>& r) {
+  const __bf16* xb = HX ? a.x + (size_t)min(lr & 7, a.M - 1) * a.K + kw0 + 8 * lg + 32 * (lr >> 3)
+                        : a.x + (size_t)min(lr, a.M - 1) * a.K + kw0 + 8 * lg;
+  auto load = [&](int s, BfdStage<RT, UPW, HX>& r) {
 #pragma unroll
-    for (int u = 0; u < UPW; ++u) r.x[u] = *(const u32x4*)(xb + (s * UPW + u) * 32);
+    for (int u = 0; u < (HX ? UPW / 2 : UPW); ++u)
+      r.x[u] = *(const u32x4*)(xb + (s * UPW + (HX ? 2 * u : u)) * 32);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -84,7 +90,7 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
   // MODE 1: this row's 1 / rms, its sums requested ahead of the weights
   NormRegs nr;
   if constexpr (NORM) norm_issue(a.ni, a.M, lane, nr);
-  BfdStage<RT, UPW> ring[DEPTH];
+  BfdStage<RT, UPW, HX> ring[DEPTH];
   // in stage order, as the loop reissues them (the loop's static waits assume
   // that order; left free, the scheduler reorders the first stages' loads)
 #pragma unroll
@@ -97,11 +103,13 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
   f32x4 acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](const BfdStage<RT, UPW>& r) {
+  auto compute = [&](const BfdStage<RT, UPW, HX>& r) {
 #pragma unroll
-    for (int u = 0; u < UPW; ++u)
+    for (int u = 0; u < UPW; ++u) {
+      const u32x4 xu = HX && (u & 1) ? rot8(r.x[u / 2]) : r.x[HX ? u / 2 : u];
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) acc[rt] = mfma(r.w[rt][u], r.x[u], acc[rt]);
+      for (int rt = 0; rt < RT; ++rt) acc[rt] = mfma(r.w[rt][u], xu, acc[rt]);
+    }
   };
   int s0 = 0;
   for (; s0 + DEPTH < ns; s0 += DEPTH) {
@@ -179,26 +187,45 @@ __global__ __launch_bounds__(RG * KW * kWave) void bf16b_direct_kernel(BfdArgs a
   }
 }
 
-template <int RT, int UPW, int DEPTH, int RG, int KW>
-int launch(const DirectPlan& p, const BfdArgs& a, hipStream_t st) {
+// registers of one stage (dwords per lane): weights and x operands (HX: half)
+constexpr int stage_dwords(int rt, int upw, bool hx = false) {
+  return 4 * rt * upw + 4 * (hx ? upw / 2 : upw);
+}
+constexpr int kRingDwords = 192;   // the ring's budget (depth x stage)
+
+template <int RT, int UPW, int DEPTH, int RG, int KW, bool HX>
+int launch_x(const DirectPlan& p, const BfdArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)p.groups, (unsigned)p.ksplit), block(RG * KW * kWave);
   if constexpr (RT >= 2) {
     if (p.swiglu) {
       if (p.mode == 1)
-        bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 1><<<grid, block, 0, st>>>(a);
+        bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 1, HX><<<grid, block, 0, st>>>(a);
       else
-        bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 0><<<grid, block, 0, st>>>(a);
+        bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, true, 0, HX><<<grid, block, 0, st>>>(a);
       return ACORN_OK;
     }
   }
   if (p.swiglu) return ACORN_ERR_UNSUPPORTED;
   switch (p.mode) {
-    case 0: bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 0><<<grid, block, 0, st>>>(a); break;
-    case 1: bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 1><<<grid, block, 0, st>>>(a); break;
-    case 2: bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 2><<<grid, block, 0, st>>>(a); break;
+    case 0: bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 0, HX><<<grid, block, 0, st>>>(a); break;
+    case 1: bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 1, HX><<<grid, block, 0, st>>>(a); break;
+    case 2: bf16b_direct_kernel<RT, UPW, DEPTH, RG, KW, false, 2, HX><<<grid, block, 0, st>>>(a); break;
     default: return ACORN_ERR_UNSUPPORTED;
   }
   return ACORN_OK;
+}
+
+// the paired-x form where the plan asks for it, each form only within the
+// ring's budget
+template <int RT, int UPW, int DEPTH, int RG, int KW>
+int launch(const DirectPlan& p, const BfdArgs& a, hipStream_t st) {
+  if constexpr (UPW % 2 == 0 && DEPTH * stage_dwords(RT, UPW, true) <= kRingDwords) {
+    if (p.hx) return launch_x<RT, UPW, DEPTH, RG, KW, true>(p, a, st);
+  }
+  if constexpr (DEPTH * stage_dwords(RT, UPW) <= kRingDwords) {
+    if (!p.hx) return launch_x<RT, UPW, DEPTH, RG, KW, false>(p, a, st);
+  }
+  return ACORN_ERR_UNSUPPORTED;
 }
 
 template <int RT, int UPW, int DEPTH>
@@ -212,19 +239,18 @@ int by_layout(const DirectPlan& p, const BfdArgs& a, hipStream_t st) {
   return ACORN_ERR_UNSUPPORTED;
 }
 
-// registers of one stage (dwords per lane): weights and x operands
-constexpr int stage_dwords(int rt, int upw) { return 4 * rt * upw + 4 * upw; }
-constexpr int kRingDwords = 192;   // the ring's budget (depth x stage)
 
 template <int RT, int UPW>
 int by_depth(const DirectPlan& p, const BfdArgs& a, hipStream_t st) {
   switch (p.depth) {
     case 2: return by_layout<RT, UPW, 2>(p, a, st);
     case 4:
-      if constexpr (4 * stage_dwords(RT, UPW) <= kRingDwords) return by_layout<RT, UPW, 4>(p, a, st);
+      if constexpr (4 * stage_dwords(RT, UPW, UPW % 2 == 0) <= kRingDwords)
+        return by_layout<RT, UPW, 4>(p, a, st);
       break;
     case 8:
-      if constexpr (8 * stage_dwords(RT, UPW) <= kRingDwords) return by_layout<RT, UPW, 8>(p, a, st);
+      if constexpr (8 * stage_dwords(RT, UPW, UPW % 2 == 0) <= kRingDwords)
+        return by_layout<RT, UPW, 8>(p, a, st);
       break;
   }
   return ACORN_ERR_UNSUPPORTED;
@@ -275,10 +301,12 @@ int bf16b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu
   if (nwf != 1 && nwf != 4 && nwf != 22 && nwf != 44) return ACORN_ERR_UNSUPPORTED;
   const int nw = nwf < 10 ? nwf : nwf / 10, kw = nwf < 10 ? 1 : nwf % 10;
   if (depth != 2 && depth != 4 && depth != 8) return ACORN_ERR_UNSUPPORTED;
-  while (depth > 2 && (depth * stage_dwords(rt, upw) > kRingDwords || KB % (kw * upw * depth)))
+  // M <= 8 with an even number of blocks per stage: the paired-x form
+  const bool hx = M <= 8 && upw % 2 == 0;
+  while (depth > 2 && (depth * stage_dwords(rt, upw, hx) > kRingDwords || KB % (kw * upw * depth)))
     depth /= 2;
   while (upw > 1 && KB % (kw * upw * depth)) upw /= 2;   // short rows (K of 64 or 128)
-  if (depth * stage_dwords(rt, upw) > kRingDwords) return ACORN_ERR_UNSUPPORTED;
+  if (depth * stage_dwords(rt, upw, hx && upw % 2 == 0) > kRingDwords) return ACORN_ERR_UNSUPPORTED;
   if (KB % (kw * upw * depth)) return ACORN_ERR_SHAPE;
   const int64_t q = KB / (kw * upw * depth);    // ks must divide this
   const int64_t waves = ntiles / rt * kw;
@@ -309,7 +337,7 @@ int bf16b_make_plan(int64_t M, int64_t N, int64_t K, const int* cfg, bool swiglu
   p->groups = (int)groups;
   p->swiglu = swiglu;
   p->mode = 0;
-  p->hx = false;
+  p->hx = hx && upw % 2 == 0;
   return ACORN_OK;
 }
 

@@ -101,7 +101,9 @@ def test_planner_bf16b_decode(M, N, K):
         assert nwf in (1, 4, 22, 44)
         assert rt in (1, 2, 4) and (N // 16) % rt == 0
         assert upw in (1, 2, 4) and depth in (2, 4, 8)
-        assert depth * (4 * rt * upw + 4 * upw) <= 192
+        # x registers per stage: 4 per block, half in the paired-x form (M <= 8, even upw)
+        xd = 4 * (upw // 2 if M <= 8 and upw % 2 == 0 else upw)
+        assert depth * (4 * rt * upw + xd) <= 192
         blocks = K // 32
         assert blocks % (ks * kw) == 0 and (blocks // ks // kw) % (upw * depth) == 0
         if r[3] == 0:
