@@ -48,7 +48,10 @@ def test_w4_asym_bound():
 
 
 def test_symmetric_bridge_is_bitwise():
-    """dequant_w4(v+8, s, -8s) == v*s exactly in fp32 (SURVEY's proof)."""
+    """dequant_w4(v+8, s, -8s) == v*s exactly in fp32.
+
+    -8s is exact in fp16 (a power-of-two multiple), (v+8)*s needs at most
+    4 + 11 mantissa bits and fits fp32, and so does its difference with 8s."""
     rng = np.random.default_rng(3)
     v = rng.integers(-8, 8, (128, 512))
     s = (0.005 + 0.015 * rng.random((128, 4))).astype(np.float16)
